@@ -1,0 +1,103 @@
+/*
+ * odie_amd C-ABI: the MI355X (gfx950) implementation of ODIE's sparse grid-query hot path.
+ *
+ * Conventions (the reference's, odie/native/runtime.cu:318-331):
+ *  - every pointer argument named *_device / passed as a buffer is device memory owned by
+ *    the caller unless stated otherwise; host arrays are marked "host";
+ *  - streams are hipStream_t values passed as uint64_t (0 = the null stream);
+ *  - functions return 0 on success and -1 on failure, leaving a message that
+ *    odie_error() returns (thread-local, valid until the next failing call on the thread);
+ *  - arguments are validated before any device work is queued, so a call that fails has
+ *    queued nothing;
+ *  - fp16 data is IEEE binary16 (uint16_t bit patterns on the host side).
+ */
+#ifndef ODIE_AMD_H
+#define ODIE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread.  Replaces odie_error (odie/native/runtime.cu:320). */
+const char* odie_error(void);
+
+/* Device-to-device async copy.  Replaces odie_copy (odie/native/runtime.cu:329). */
+int odie_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Multiresolution hash grid encode (2D), the tiny-cuda-nn GridEncoding the reference's
+ * HashGrid wraps (odie/hash_grid.py:27,54; odie/native/runtime.cu:186,260,287).
+ * One level of the table: entries [offset, offset+size) of one expert's table, each of
+ * `features` values.  scale/resolution/size follow odie/config.py:83-94.
+ * --------------------------------------------------------------------------------------- */
+typedef struct odie_grid_level {
+    float scale;          /* fp32 grid scale 2^(l*log2 g)*base - 1 */
+    uint32_t resolution;  /* ceil(scale) + 1 vertices per side */
+    uint32_t size;        /* table entries of this level: min(align8(res^2), 2^log2T) */
+    uint32_t offset;      /* first entry of this level inside one expert's table */
+    uint32_t hashed;      /* 1 if res^2 > size (spatial hash), else dense x + y*res */
+} odie_grid_level;
+
+#define ODIE_MAX_LEVELS 32
+
+/* dtype codes */
+#define ODIE_F32 0
+#define ODIE_F16 1
+
+/* Forward encode of n coordinates in [0,1]^2 (coords fp32 [n,2]).
+ * Experts: coordinates [offsets[e], offsets[e+1]) read the table at params + e*expert_params
+ * (offsets: device int32 [experts+1], nondecreasing, offsets[0]=0, offsets[experts]=n);
+ * experts = 1 with offsets = NULL is a single grid.
+ * param_dtype ODIE_F16: fp16 table, fp16 fused multiply-add chain, fp16 output;
+ * ODIE_F32: fp32 table, fp32 chain, fp32 output.  levels: host array [n_levels].
+ * Output row i: level l feature c at column l*features + c of out_width >= n_levels*features
+ * columns; columns past n_levels*features are written as +0.
+ * Replaces tcnn.Encoding.forward (odie/hash_grid.py:54) / GridEncoding fwd
+ * (odie/native/runtime.cu:260). */
+int odie_grid_forward(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                      const void* params, int64_t expert_params, int param_dtype,
+                      const odie_grid_level* levels, int n_levels, int features,
+                      void* out, int out_width, uint64_t stream);
+
+/* Backward scatter: gradient[param] (fp32, experts*expert_params) receives
+ * sum over coordinates and corners of w_k * upstream, skipping zero upstream values
+ * (odie/packed_kernels.cu:66-88 semantics).  upstream: [n, up_width] of up_dtype.
+ * zero_first = 1 clears the gradient first (the reference returns a fresh zeroed tensor,
+ * odie/packed_kernels.cu:134); 0 accumulates.
+ * Replaces GridEncoding bwd (odie/native/runtime.cu:287). */
+int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                       const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                       const odie_grid_level* levels, int n_levels, int features,
+                       float* gradient, int zero_first, uint64_t stream);
+
+/* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
+ * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
+ * 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),
+ * "xcd_remap" (0/1: XCD-major block order).  Results do not depend on them beyond fp32
+ * summation order. */
+int odie_set_tuning(const char* key, int value);
+
+/* ---------------------------------------------------------------------------------------
+ * Packed xy planes (the on-demand representation), replacing the torch extension ops
+ * forward/backward (odie/packed_bindings.cpp:4-12, odie/packed_kernels.cu:107-145).
+ * descriptors: device int32 [levels, 8] = R, points, plane offset, node-word offset,
+ * cell-bitmap byte offset, F, output feature offset, direct (odie/model.py:100-101).
+ * grid: fp32 master [parameter_count]; every read is rounded to fp16.
+ * --------------------------------------------------------------------------------------- */
+int odie_packed_forward(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
+                        const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                        const int32_t* node_prefix, const uint8_t* bitmap, int width,
+                        uint16_t* features, uint8_t* visibility, uint64_t stream);
+
+int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
+                         const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                         const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
+                         int64_t parameter_count, uint64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ODIE_AMD_H */

@@ -1,0 +1,37 @@
+// Shared helpers for the gfx950 kernels and the C-ABI: error reporting, stream
+// handles, launch-shape helpers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+#include <string>
+
+#define ODIE_API extern "C" __attribute__((visibility("default")))
+
+namespace odie {
+
+// Last error of the calling thread; the C-ABI returns -1 and leaves the message here,
+// as the reference runtime does (odie/native/runtime.cu:318-331).
+std::string& error_slot();
+int fail(const std::string& message);
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(uint64_t bits) { return reinterpret_cast<hipStream_t>(bits); }
+
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin across them
+
+// Map a hardware block id onto a logical id so that consecutive logical ids run on the
+// same XCD (and share its L2).  `blocks` must be a multiple of kXcds.
+__device__ inline uint32_t xcd_major(uint32_t block, uint32_t blocks) {
+    return (block % kXcds) * (blocks / kXcds) + block / kXcds;
+}
+
+inline uint32_t round_up(uint32_t value, uint32_t multiple) {
+    return (value + multiple - 1) / multiple * multiple;
+}
+
+// fp16 <-> 16-bit patterns without relying on __half's class layout.
+__device__ inline __half bits_to_half(uint16_t bits) { return __ushort_as_half(bits); }
+__device__ inline uint16_t half_to_bits(__half value) { return __half_as_ushort(value); }
+
+}  // namespace odie

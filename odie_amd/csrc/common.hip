@@ -1,0 +1,34 @@
+// Thread-local error slot shared by every C-ABI entry point, plus odie_error/odie_copy.
+#include "common.h"
+#include "../../include/odie_amd.h"
+
+namespace odie {
+
+std::string& error_slot() {
+    static thread_local std::string slot;
+    return slot;
+}
+
+int fail(const std::string& message) {
+    error_slot() = message;
+    return -1;
+}
+
+int check_launch(const char* what) {
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess) return fail(std::string(what) + ": " + hipGetErrorString(status));
+    return 0;
+}
+
+}  // namespace odie
+
+ODIE_API const char* odie_error(void) { return odie::error_slot().c_str(); }
+
+ODIE_API int odie_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream) {
+    if (bytes == 0) return 0;
+    if (!dst || !src) return odie::fail("odie_copy: null pointer");
+    const hipError_t status = hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), bytes,
+                                             hipMemcpyDeviceToDevice, odie::as_stream(stream));
+    if (status != hipSuccess) return odie::fail(std::string("odie_copy: ") + hipGetErrorString(status));
+    return 0;
+}

@@ -1,0 +1,643 @@
+// Multiresolution grid encode for gfx950: hash grid (single grid or packed experts) and
+// packed xy planes, forward and gradient scatter.
+//
+// Work decomposition: one lane per coordinate, all levels in registers, so a row of
+// features is produced and stored with 16-byte stores and the upstream row is loaded the
+// same way.  Blocks own contiguous chunks of the (expert-compacted) coordinate array and
+// their block ids are remapped so consecutive chunks -- and therefore one expert's table
+// -- stay on one XCD and its L2.  The backward accumulates the coarse levels of the
+// chunk's expert in LDS (ds_add_f32) and flushes them once per chunk with global fp32
+// atomics; finer levels go straight to global_atomic_add_f32.
+#include <type_traits>
+
+#include "common.h"
+#include "../../include/odie_amd.h"
+
+namespace odie {
+namespace {
+
+constexpr int kBlock = 256;
+
+struct DevLevel {
+    float scale;
+    uint32_t res;
+    uint32_t size;
+    uint32_t mask;    // size - 1 when size is a power of two, else 0
+    uint32_t offset;  // first entry of the level
+    uint32_t hashed;
+};
+
+struct GridArgs {
+    const float* coords;
+    const int32_t* offsets;
+    const void* params;
+    void* out;
+    const void* upstream;
+    float* grad;
+    int64_t n;
+    int64_t expert_params;
+    int experts;
+    int n_levels;
+    int width;       // output (forward) or upstream (backward) row width in elements
+    int chunk;       // coordinates per block
+    int vec_rows;    // rows are 16-byte aligned and a multiple of 16 bytes
+    int lds_levels;  // backward: levels accumulated in LDS
+    int lds_floats;  // backward: LDS accumulator size in floats
+    int remap;       // 1: XCD-major block order
+    DevLevel level[ODIE_MAX_LEVELS];
+};
+
+// Tuning knobs (set through odie_set_tuning; defaults chosen by measurement).
+struct Tuning {
+    int forward_chunk = 1024;
+    int backward_chunk = 8192;
+    int lds_bytes = 65536;
+    int xcd_remap = 1;
+};
+Tuning& tuning() {
+    static Tuning t;
+    return t;
+}
+
+__device__ inline uint32_t wrap_index(uint32_t v, const DevLevel& lv) {
+    if (lv.mask) return v & lv.mask;
+    if (v < lv.size) return v;
+    v -= lv.size;
+    return v < lv.size ? v : v % lv.size;
+}
+
+// tiny-cuda-nn grid geometry: p = fma(scale, x, 0.5), corner = floor(p), fraction p - floor(p);
+// corners (0,0),(1,0),(0,1),(1,1); dense index x + y*res, hashed x ^ y*2654435761, mod size.
+__device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32_t idx[4], float w[4]) {
+    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
+    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
+    const float flx = floorf(px), fly = floorf(py);
+    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
+    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
+    const float fx = px - flx, fy = py - fly;
+    w[0] = (1.0f - fx) * (1.0f - fy);
+    w[1] = fx * (1.0f - fy);
+    w[2] = (1.0f - fx) * fy;
+    w[3] = fx * fy;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t cx = gx + static_cast<uint32_t>(k & 1), cy = gy + static_cast<uint32_t>(k >> 1);
+        const uint32_t raw = lv.hashed ? (cx ^ (cy * 2654435761u)) : (cx + cy * lv.res);
+        idx[k] = wrap_index(raw, lv);
+    }
+}
+
+// Largest expert e with offsets[e] <= i, clamped to a valid expert.
+__device__ inline int expert_at(const GridArgs& a, int64_t i) {
+    if (!a.offsets) return 0;
+    int lo = 0, hi = a.experts - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.offsets[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// End of the expert segment containing i, clipped to [i+1, end].
+__device__ inline int64_t segment_end(const GridArgs& a, int e, int64_t i, int64_t end) {
+    if (!a.offsets) return end;
+    int64_t stop = a.offsets[e + 1];
+    if (stop > end) stop = end;
+    if (stop <= i) stop = end;  // malformed offsets: finish the chunk as this expert
+    return stop;
+}
+
+template <bool HALF>
+using Elem = typename std::conditional<HALF, __half, float>::type;
+
+template <int F, bool HALF, int LMAX>
+__device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, int64_t i) {
+    using T = Elem<HALF>;
+    const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+    T vals[LMAX * F];
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+        if (l < a.n_levels) {
+            const DevLevel& lv = a.level[l];
+            uint32_t idx[4];
+            float w[4];
+            grid_corners(lv, p.x, p.y, idx, w);
+            const T* t = table + static_cast<size_t>(lv.offset) * F;
+            if constexpr (HALF && F % 2 == 0) {
+                __half2 acc[F / 2];
+#pragma unroll
+                for (int c = 0; c < F / 2; ++c) acc[c] = __half2(__float2half(0.0f), __float2half(0.0f));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const __half2* src = reinterpret_cast<const __half2*>(t + static_cast<size_t>(idx[k]) * F);
+                    const __half2 wk = __float2half2_rn(w[k]);
+#pragma unroll
+                    for (int c = 0; c < F / 2; ++c) acc[c] = __hfma2(wk, src[c], acc[c]);
+                }
+#pragma unroll
+                for (int c = 0; c < F / 2; ++c) {
+                    vals[l * F + 2 * c] = __low2half(acc[c]);
+                    vals[l * F + 2 * c + 1] = __high2half(acc[c]);
+                }
+            } else if constexpr (HALF) {
+                __half acc = __float2half(0.0f);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc = __hfma(__float2half_rn(w[k]), t[idx[k]], acc);
+                vals[l] = acc;
+            } else {
+                float acc[F];
+#pragma unroll
+                for (int c = 0; c < F; ++c) acc[c] = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float* src = t + static_cast<size_t>(idx[k]) * F;
+#pragma unroll
+                    for (int c = 0; c < F; ++c) acc[c] = __builtin_fmaf(w[k], src[c], acc[c]);
+                }
+#pragma unroll
+                for (int c = 0; c < F; ++c) vals[l * F + c] = acc[c];
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < F; ++c) vals[l * F + c] = T(0.0f);
+        }
+    }
+    T* row = reinterpret_cast<T*>(a.out) + static_cast<size_t>(i) * a.width;
+    const int used = a.n_levels * F;
+    if (a.vec_rows && (used * static_cast<int>(sizeof(T))) % 16 == 0) {
+        constexpr int kPer = 16 / sizeof(T);
+        constexpr int kChunks = (LMAX * F + kPer - 1) / kPer;
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            if (j * kPer < used) {
+                uint32_t words[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if constexpr (HALF) {
+                        const int e0 = j * kPer + 2 * q;
+                        const uint32_t lo = e0 < LMAX * F ? half_to_bits(vals[e0]) : 0u;
+                        const uint32_t hi = e0 + 1 < LMAX * F ? half_to_bits(vals[e0 + 1]) : 0u;
+                        words[q] = lo | (hi << 16);
+                    } else {
+                        const int e0 = j * kPer + q;
+                        words[q] = e0 < LMAX * F ? __float_as_uint(vals[e0]) : 0u;
+                    }
+                }
+                reinterpret_cast<uint4*>(row)[j] = make_uint4(words[0], words[1], words[2], words[3]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < LMAX * F; ++c)
+            if (c < used) row[c] = vals[c];
+    }
+    for (int c = used; c < a.width; ++c) row[c] = T(0.0f);
+}
+
+template <int F, bool HALF, int LMAX>
+__global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
+    const uint32_t block = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
+    int64_t begin = static_cast<int64_t>(block) * a.chunk;
+    if (begin >= a.n) return;
+    const int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
+    while (begin < end) {
+        const int e = expert_at(a, begin);
+        const int64_t stop = segment_end(a, e, begin, end);
+        const Elem<HALF>* table = reinterpret_cast<const Elem<HALF>*>(a.params) + static_cast<size_t>(e) * a.expert_params;
+        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) encode_row<F, HALF, LMAX>(a, table, i);
+        begin = stop;
+    }
+}
+
+template <int F, bool HALF_UP, int LMAX>
+__global__ __launch_bounds__(kBlock) void grid_backward_kernel(GridArgs a) {
+    extern __shared__ float lds[];
+    using U = Elem<HALF_UP>;
+    const uint32_t block = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
+    int64_t begin = static_cast<int64_t>(block) * a.chunk;
+    if (begin >= a.n) return;
+    const int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
+    const int used = a.n_levels * F;
+    while (begin < end) {
+        const int e = expert_at(a, begin);
+        const int64_t stop = segment_end(a, e, begin, end);
+        float* grad = a.grad + static_cast<size_t>(e) * a.expert_params;
+        if (a.lds_levels > 0) {
+            for (int j = threadIdx.x; j < a.lds_floats; j += kBlock) lds[j] = 0.0f;
+            __syncthreads();
+        }
+        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) {
+            const U* urow = reinterpret_cast<const U*>(a.upstream) + static_cast<size_t>(i) * a.width;
+            float up[LMAX * F];
+            if (a.vec_rows && (used * static_cast<int>(sizeof(U))) % 16 == 0) {
+                constexpr int kPer = 16 / sizeof(U);
+                constexpr int kChunks = (LMAX * F + kPer - 1) / kPer;
+#pragma unroll
+                for (int j = 0; j < kChunks; ++j) {
+                    if (j * kPer < used) {
+                        const uint4 v = reinterpret_cast<const uint4*>(urow)[j];
+                        const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            if constexpr (HALF_UP) {
+                                const int e0 = j * kPer + 2 * q;
+                                if (e0 < LMAX * F) up[e0] = __half2float(bits_to_half(static_cast<uint16_t>(words[q] & 0xffffu)));
+                                if (e0 + 1 < LMAX * F) up[e0 + 1] = __half2float(bits_to_half(static_cast<uint16_t>(words[q] >> 16)));
+                            } else {
+                                const int e0 = j * kPer + q;
+                                if (e0 < LMAX * F) up[e0] = __uint_as_float(words[q]);
+                            }
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < LMAX * F; ++c) up[c] = c < used ? static_cast<float>(urow[c]) : 0.0f;
+            }
+            const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+#pragma unroll
+            for (int l = 0; l < LMAX; ++l) {
+                if (l < a.n_levels) {
+                    const DevLevel& lv = a.level[l];
+                    uint32_t idx[4];
+                    float w[4];
+                    grid_corners(lv, p.x, p.y, idx, w);
+                    const bool local = l < a.lds_levels;
+                    float* base = local ? lds : grad;
+#pragma unroll
+                    for (int c = 0; c < F; ++c) {
+                        const float value = up[l * F + c];
+                        if (value == 0.0f) continue;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            float* target = base + (static_cast<size_t>(lv.offset) + idx[k]) * F + c;
+                            atomicAdd(target, w[k] * value);
+                        }
+                    }
+                }
+            }
+        }
+        if (a.lds_levels > 0) {
+            __syncthreads();
+            for (int j = threadIdx.x; j < a.lds_floats; j += kBlock) {
+                const float v = lds[j];
+                if (v != 0.0f) atomicAdd(grad + j, v);
+            }
+            __syncthreads();
+        }
+        begin = stop;
+    }
+}
+
+// Clears `count` floats (a fill kernel rather than hipMemsetAsync so that the backward can
+// be captured in a graph).
+__global__ __launch_bounds__(kBlock) void fill_zero_kernel(float* data, int64_t count) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * 4;
+    for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 4; i < count; i += stride) {
+        if (i + 4 <= count && (reinterpret_cast<uintptr_t>(data + i) & 15) == 0) {
+            *reinterpret_cast<float4*>(data + i) = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            for (int64_t j = i; j < i + 4 && j < count; ++j) data[j] = 0.0f;
+        }
+    }
+}
+
+int validate_grid(const char* what, const float* coords, int64_t n, const int32_t* offsets, int experts,
+                  int64_t expert_params, const odie_grid_level* levels, int n_levels, int features,
+                  GridArgs& a) {
+    const std::string w(what);
+    if (n < 0 || n > (int64_t{1} << 31) - 1) return fail(w + ": n must be within [0, 2^31-1]");
+    if (n > 0 && !coords) return fail(w + ": coords is null");
+    if (experts < 1) return fail(w + ": experts must be >= 1");
+    if (experts > 1 && !offsets) return fail(w + ": offsets are required when experts > 1");
+    if (!levels) return fail(w + ": levels is null");
+    if (n_levels < 1 || n_levels > ODIE_MAX_LEVELS) return fail(w + ": n_levels must be within 1..32");
+    if (features != 1 && features != 2 && features != 4 && features != 8)
+        return fail(w + ": features per level must be 1, 2, 4 or 8");
+    uint64_t entries = 0;
+    for (int l = 0; l < n_levels; ++l) {
+        const odie_grid_level& lv = levels[l];
+        if (lv.size == 0 || lv.resolution == 0) return fail(w + ": level size and resolution must be positive");
+        if (!(lv.scale == lv.scale)) return fail(w + ": level scale is NaN");
+        if (lv.offset != entries) return fail(w + ": level offsets must be contiguous from 0");
+        entries += lv.size;
+        DevLevel& d = a.level[l];
+        d.scale = lv.scale;
+        d.res = lv.resolution;
+        d.size = lv.size;
+        d.mask = (lv.size & (lv.size - 1)) == 0 ? lv.size - 1 : 0;
+        d.offset = lv.offset;
+        d.hashed = lv.hashed ? 1u : 0u;
+    }
+    if (expert_params < static_cast<int64_t>(entries) * features)
+        return fail(w + ": expert_params is smaller than the levels' table");
+    a.coords = coords;
+    a.offsets = experts > 1 ? offsets : nullptr;
+    a.n = n;
+    a.expert_params = expert_params;
+    a.experts = experts;
+    a.n_levels = n_levels;
+    return 0;
+}
+
+#define ODIE_GRID_DISPATCH(KERNEL, F, HALF, LMAX, GRID, SHMEM, STREAM, ARGS)                              \
+    do {                                                                                                  \
+        if (LMAX <= 16) {                                                                                 \
+            switch (F) {                                                                                  \
+                case 1: if (HALF) KERNEL<1, true, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);             \
+                        else KERNEL<1, false, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+                case 2: if (HALF) KERNEL<2, true, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);             \
+                        else KERNEL<2, false, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+                case 4: if (HALF) KERNEL<4, true, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);             \
+                        else KERNEL<4, false, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+                default: if (HALF) KERNEL<8, true, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);            \
+                        else KERNEL<8, false, 16><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+            }                                                                                             \
+        } else {                                                                                          \
+            switch (F) {                                                                                  \
+                case 1: if (HALF) KERNEL<1, true, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);             \
+                        else KERNEL<1, false, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+                case 2: if (HALF) KERNEL<2, true, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);             \
+                        else KERNEL<2, false, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+                case 4: if (HALF) KERNEL<4, true, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);             \
+                        else KERNEL<4, false, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+                default: if (HALF) KERNEL<8, true, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS);            \
+                        else KERNEL<8, false, 32><<<GRID, kBlock, SHMEM, STREAM>>>(ARGS); break;          \
+            }                                                                                             \
+        }                                                                                                 \
+    } while (0)
+
+uint32_t grid_blocks(int64_t n, int chunk) {
+    const uint64_t blocks = (static_cast<uint64_t>(n) + chunk - 1) / chunk;
+    return round_up(static_cast<uint32_t>(blocks), kXcds);
+}
+
+// ---------------------------------------------------------------------------------------
+// Packed xy planes (odie/packed_kernels.cu:12-88 semantics).
+// ---------------------------------------------------------------------------------------
+
+struct PackedArgs {
+    const float* coords;
+    const float* grid;
+    const int32_t* desc;
+    const uint64_t* node_bitmap;
+    const int32_t* prefix;
+    const uint8_t* bitmap;
+    const uint16_t* upstream;
+    uint16_t* features;
+    uint8_t* visibility;
+    float* gradient;
+    int64_t n;
+    int64_t params;
+    int levels;
+    int width;
+};
+
+// Geometry at integer resolution R: p = fma(R-1, x, 0.5), cell = floor(px) + floor(py)*R.
+// The cell's integer corner is clamped into the plane so that any input addresses memory
+// inside the layout; for x, y in [0,1] the clamp never changes the corner.
+__device__ inline void plane_geometry(float x, float y, int r, int& cell, float w[4]) {
+    const float px = __builtin_fmaf(static_cast<float>(r - 1), x, 0.5f);
+    const float py = __builtin_fmaf(static_cast<float>(r - 1), y, 0.5f);
+    int ix = static_cast<int>(floorf(px)), iy = static_cast<int>(floorf(py));
+    const float fx = px - static_cast<float>(ix), fy = py - static_cast<float>(iy);
+    ix = ix < 0 ? 0 : (ix > r - 1 ? r - 1 : ix);
+    iy = iy < 0 ? 0 : (iy > r - 1 ? r - 1 : iy);
+    cell = ix + iy * r;
+    w[0] = (1.0f - fx) * (1.0f - fy);
+    w[1] = fx * (1.0f - fy);
+    w[2] = (1.0f - fx) * fy;
+    w[3] = fx * fy;
+}
+
+__device__ inline int64_t plane_param(const PackedArgs& a, const int32_t* d, int cell, int k, int c) {
+    const int node = (cell + (k & 1) + (k >> 1) * d[0]) % d[1];
+    int row = node;
+    if (!d[7]) {
+        const int word = d[3] + (node >> 6), bit = node & 63;
+        const uint64_t mask = (uint64_t{1} << bit) - uint64_t{1};
+        row = a.prefix[word] + __popcll(a.node_bitmap[word] & mask);
+    }
+    int64_t p = static_cast<int64_t>(d[2]) + static_cast<int64_t>(row) * d[5] + c;
+    return p < 0 ? 0 : (p >= a.params ? a.params - 1 : p);
+}
+
+__global__ __launch_bounds__(kBlock) void packed_forward_kernel(PackedArgs a) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= a.n) return;
+    const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+    uint16_t* row = a.features + static_cast<size_t>(i) * a.width;
+    int written = 0;
+    uint32_t vis[ODIE_MAX_LEVELS / 4];
+#pragma unroll
+    for (int q = 0; q < ODIE_MAX_LEVELS / 4; ++q) vis[q] = 0;
+#pragma unroll
+    for (int l = 0; l < ODIE_MAX_LEVELS; ++l) {
+        if (l < a.levels) {
+            const int32_t* d = a.desc + 8 * l;
+            int cell;
+            float w[4];
+            plane_geometry(p.x, p.y, d[0], cell, w);
+            const bool on = (a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1;
+            vis[l / 4] |= static_cast<uint32_t>(on) << (8 * (l % 4));
+            for (int c = 0; c < d[5]; ++c) {
+                __half v = __float2half(0.0f);
+                if (on) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        v = __hfma(__float2half_rn(w[k]), __float2half_rn(a.grid[plane_param(a, d, cell, k, c)]), v);
+                }
+                row[d[6] + c] = half_to_bits(v);
+            }
+            const int top = d[6] + d[5];
+            written = top > written ? top : written;
+        }
+    }
+    for (int c = written; c < a.width; ++c) row[c] = 0;
+    uint8_t* vrow = a.visibility + static_cast<size_t>(i) * a.levels;
+#pragma unroll
+    for (int l = 0; l < ODIE_MAX_LEVELS; ++l)
+        if (l < a.levels) vrow[l] = static_cast<uint8_t>(vis[l / 4] >> (8 * (l % 4)));
+}
+
+__global__ __launch_bounds__(kBlock) void packed_backward_kernel(PackedArgs a) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= a.n) return;
+    const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+    const uint16_t* urow = a.upstream + static_cast<size_t>(i) * a.width;
+    for (int l = 0; l < a.levels; ++l) {
+        const int32_t* d = a.desc + 8 * l;
+        int cell;
+        float w[4];
+        plane_geometry(p.x, p.y, d[0], cell, w);
+        if (!((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1)) continue;
+        for (int c = 0; c < d[5]; ++c) {
+            const int col = d[6] + c;
+            if (col >= a.width) continue;
+            const float value = __half2float(bits_to_half(urow[col]));
+            if (value == 0.0f) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) atomicAdd(a.gradient + plane_param(a, d, cell, k, c), w[k] * value);
+        }
+    }
+}
+
+}  // namespace
+
+int launch_fill_zero(float* data, int64_t count, hipStream_t stream) {
+    if (count <= 0) return 0;
+    int64_t blocks = (count + 4 * kBlock - 1) / (4 * kBlock);
+    if (blocks > 8192) blocks = 8192;
+    fill_zero_kernel<<<static_cast<uint32_t>(blocks), kBlock, 0, stream>>>(data, count);
+    return check_launch("fill_zero");
+}
+
+int set_grid_tuning(const std::string& key, int value) {
+    Tuning& t = tuning();
+    if (key == "forward_chunk" && value >= kBlock && value % kBlock == 0) t.forward_chunk = value;
+    else if (key == "backward_chunk" && value >= kBlock && value % kBlock == 0) t.backward_chunk = value;
+    else if (key == "lds_bytes" && value >= 0 && value <= 160 * 1024) t.lds_bytes = value;
+    else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
+    else return fail("odie_set_tuning: unknown key or value out of range: " + key);
+    return 0;
+}
+
+}  // namespace odie
+
+using namespace odie;
+
+ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                               const void* params, int64_t expert_params, int param_dtype,
+                               const odie_grid_level* levels, int n_levels, int features,
+                               void* out, int out_width, uint64_t stream) {
+    GridArgs a{};
+    if (validate_grid("odie_grid_forward", coords, n, offsets, experts, expert_params, levels, n_levels, features, a))
+        return -1;
+    if (param_dtype != ODIE_F32 && param_dtype != ODIE_F16) return fail("odie_grid_forward: param_dtype must be 0 (fp32) or 1 (fp16)");
+    if (out_width < n_levels * features) return fail("odie_grid_forward: out_width is smaller than n_levels*features");
+    if (n == 0) return 0;
+    if (!params || !out) return fail("odie_grid_forward: params and out must be non-null");
+    const bool half = param_dtype == ODIE_F16;
+    const size_t elem = half ? 2 : 4;
+    a.params = params;
+    a.out = out;
+    a.width = out_width;
+    a.chunk = tuning().forward_chunk;
+    a.remap = tuning().xcd_remap;
+    a.vec_rows = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (out_width * elem) % 16 == 0;
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_forward: coords must be 8-byte aligned");
+    const uint32_t blocks = grid_blocks(n, a.chunk);
+    const hipStream_t s = as_stream(stream);
+    ODIE_GRID_DISPATCH(grid_forward_kernel, features, half, n_levels, blocks, 0, s, a);
+    return check_launch("odie_grid_forward");
+}
+
+ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                const odie_grid_level* levels, int n_levels, int features,
+                                float* gradient, int zero_first, uint64_t stream) {
+    GridArgs a{};
+    if (validate_grid("odie_grid_backward", coords, n, offsets, experts, expert_params, levels, n_levels, features, a))
+        return -1;
+    if (up_dtype != ODIE_F32 && up_dtype != ODIE_F16) return fail("odie_grid_backward: up_dtype must be 0 (fp32) or 1 (fp16)");
+    if (up_width < n_levels * features) return fail("odie_grid_backward: up_width is smaller than n_levels*features");
+    if (!gradient) return fail("odie_grid_backward: gradient is null");
+    if (n > 0 && !upstream) return fail("odie_grid_backward: upstream is null");
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_backward: coords must be 8-byte aligned");
+    const hipStream_t s = as_stream(stream);
+    const int64_t total = expert_params * experts;
+    if (zero_first && launch_fill_zero(gradient, total, s)) return -1;
+    if (n == 0) return 0;
+    const bool half = up_dtype == ODIE_F16;
+    const size_t elem = half ? 2 : 4;
+    const Tuning& t = tuning();
+    a.upstream = upstream;
+    a.grad = gradient;
+    a.width = up_width;
+    a.chunk = t.backward_chunk;
+    a.remap = t.xcd_remap;
+    a.vec_rows = (reinterpret_cast<uintptr_t>(upstream) % 16 == 0) && (up_width * elem) % 16 == 0;
+    // Coarse levels whose table is small next to the chunk's corner count are accumulated
+    // in LDS: the flush costs one atomic per entry instead of one per corner.
+    int lds_levels = 0;
+    int64_t lds_floats = 0;
+    for (int l = 0; l < n_levels; ++l) {
+        const int64_t floats = static_cast<int64_t>(levels[l].size) * features;
+        if ((lds_floats + floats) * 4 > t.lds_bytes) break;
+        if (static_cast<int64_t>(levels[l].size) > 2 * static_cast<int64_t>(a.chunk)) break;
+        lds_floats += floats;
+        lds_levels = l + 1;
+    }
+    a.lds_levels = lds_levels;
+    a.lds_floats = static_cast<int>(lds_floats);
+    const size_t shmem = static_cast<size_t>(lds_floats) * 4;
+    const uint32_t blocks = grid_blocks(n, a.chunk);
+    ODIE_GRID_DISPATCH(grid_backward_kernel, features, half, n_levels, blocks, shmem, s, a);
+    return check_launch("odie_grid_backward");
+}
+
+ODIE_API int odie_set_tuning(const char* key, int value) {
+    if (!key) return fail("odie_set_tuning: key is null");
+    return set_grid_tuning(key, value);
+}
+
+ODIE_API int odie_packed_forward(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
+                                 const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                                 const int32_t* node_prefix, const uint8_t* bitmap, int width,
+                                 uint16_t* features, uint8_t* visibility, uint64_t stream) {
+    if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_packed_forward: n must be within [0, 2^31-1]");
+    if (levels < 2 || levels > ODIE_MAX_LEVELS) return fail("odie_packed_forward: descriptor must have 2..32 levels");
+    if (width < 2 || width > 128) return fail("odie_packed_forward: feature width must be within 2..128");
+    if (parameter_count <= 0) return fail("odie_packed_forward: parameter_count must be positive");
+    if (n == 0) return 0;
+    if (!coords || !grid || !descriptors || !bitmap || !features || !visibility)
+        return fail("odie_packed_forward: null pointer");
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_packed_forward: coords must be 8-byte aligned");
+    PackedArgs a{};
+    a.coords = coords;
+    a.grid = grid;
+    a.desc = descriptors;
+    a.node_bitmap = node_bitmap;
+    a.prefix = node_prefix;
+    a.bitmap = bitmap;
+    a.features = features;
+    a.visibility = visibility;
+    a.n = n;
+    a.params = parameter_count;
+    a.levels = levels;
+    a.width = width;
+    const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
+    packed_forward_kernel<<<blocks, kBlock, 0, as_stream(stream)>>>(a);
+    return check_launch("odie_packed_forward");
+}
+
+ODIE_API int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
+                                  const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                                  const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
+                                  int64_t parameter_count, uint64_t stream) {
+    if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_packed_backward: n must be within [0, 2^31-1]");
+    if (levels < 2 || levels > ODIE_MAX_LEVELS) return fail("odie_packed_backward: descriptor must have 2..32 levels");
+    if (up_width < 2 || up_width > 128) return fail("odie_packed_backward: upstream width must be within 2..128");
+    if (parameter_count < 0) return fail("odie_packed_backward: parameter count must be nonnegative");
+    if (parameter_count > 0 && !gradient) return fail("odie_packed_backward: gradient is null");
+    const hipStream_t s = as_stream(stream);
+    if (launch_fill_zero(gradient, parameter_count, s)) return -1;
+    if (n == 0 || parameter_count == 0) return 0;
+    if (!coords || !upstream || !descriptors || !bitmap) return fail("odie_packed_backward: null pointer");
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_packed_backward: coords must be 8-byte aligned");
+    PackedArgs a{};
+    a.coords = coords;
+    a.desc = descriptors;
+    a.node_bitmap = node_bitmap;
+    a.prefix = node_prefix;
+    a.bitmap = bitmap;
+    a.upstream = upstream;
+    a.gradient = gradient;
+    a.n = n;
+    a.params = parameter_count;
+    a.levels = levels;
+    a.width = up_width;
+    const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
+    packed_backward_kernel<<<blocks, kBlock, 0, s>>>(a);
+    return check_launch("odie_packed_backward");
+}

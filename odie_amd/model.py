@@ -1,0 +1,180 @@
+"""Packed xy-plane layout and the PackedQuery op (odie/model.py).
+
+make_layout / plane_closure / make_node_index follow odie/model.py:33-118: each level's
+retained nodes are the closure {c, c+1, c+R, c+R+1} mod align8(R^2) of its support; a
+level whose closure is every node is addressed directly, otherwise through a bitmap of
+present nodes (64 per uint64 word, LSB first) and an int32 exclusive per-word prefix of
+present-node counts.  Descriptor row: R, points, plane offset, node-word offset (-1 when
+direct), cell-bitmap byte offset, F, output feature offset, direct.
+
+The layout is host bookkeeping done at initialization and at each plane activation;
+PackedQuery runs the encode on the GPU through libodie_amd.so.
+"""
+import numpy as np
+import torch
+
+from . import _lib
+
+COORDINATE_VERSION = 'unit-endpoints-native-fmaf-half-cell-align8-modulo-v1'
+LAYOUT_VERSION = 'packed-xy-only-native-closure-v1'
+ADDRESSING_VERSION = 'node-bitmap64-exclusive-prefix32-v1'
+INT32_MAX = 2 ** 31 - 1
+
+
+def align8(value):
+    return (int(value) + 7) // 8 * 8
+
+
+def router_weights(logits, activation):
+    if activation == 'sigmoid':
+        return torch.sigmoid(logits)
+    if activation == 'softplus':
+        return torch.nn.functional.softplus(logits, beta=1., threshold=20.)
+    raise ValueError('Unknown router activation: ' + activation)
+
+
+def gate_coarse_levels(config):
+    count = int(config.get('gate_coarse_levels_K', config['coarse_levels']))
+    if not 0 <= count <= int(config['n_levels']) or int(config['coarse_levels']) != count:
+        raise ValueError('Gate K must agree with coarse_levels and remain within declared level count')
+    return count
+
+
+def plane_closure(support, resolution):
+    """Sorted unique closure nodes of a flat bool support of R^2 cells (int64)."""
+    support = torch.as_tensor(support)
+    cells = support.nonzero(as_tuple=True)[0]
+    nodes = torch.cat([cells, cells + 1, cells + resolution, cells + resolution + 1])
+    return torch.unique(nodes.remainder(align8(resolution ** 2)), sorted=True)
+
+
+def make_node_index(nodes, points):
+    """(uint64 presence bitmap, int32 exclusive per-word prefix) of sorted unique nodes."""
+    if not isinstance(points, int) or points <= 0 or points > INT32_MAX:
+        raise ValueError('Native node universe must fit positive int32 addressing')
+    if nodes.device.type != 'cpu' or nodes.dtype != torch.int64 or nodes.ndim != 1:
+        raise ValueError('Nodes must be a flat CPU int64 tensor')
+    values = nodes.numpy()
+    if values.size and (values[0] < 0 or values[-1] >= points or bool((np.diff(values) <= 0).any())):
+        raise ValueError('Nodes must be sorted, unique and inside the native universe')
+    words = (points + 63) // 64
+    present = np.zeros(words * 64, dtype=np.uint8)
+    present[values] = 1
+    packed = np.packbits(present.reshape(words, 64), axis=1, bitorder='little')
+    bitmap = packed.view('<u8').reshape(words).copy()
+    counts = present.reshape(words, 64).sum(1, dtype=np.int64)
+    prefix = (np.cumsum(counts) - counts).astype(np.int32)
+    return torch.from_numpy(bitmap.view(np.int64)).view(torch.uint64), torch.from_numpy(prefix)
+
+
+def _cell_bitmap(support, points):
+    padded = np.zeros(points, dtype=np.uint8)
+    padded[:support.numel()] = support.numpy().astype(np.uint8)
+    return torch.from_numpy(np.packbits(padded.reshape(-1, 8), axis=1, bitorder='little').reshape(-1))
+
+
+def make_layout(config, supports, plane_dims, plane_node_caps):
+    resolutions = list(config['resolutions'])
+    if not (len(resolutions) == len(supports) == len(plane_dims) == len(plane_node_caps) == int(config['n_levels'])) \
+            or not all(f in (1, 2, 4) for f in plane_dims):
+        raise ValueError('Require aligned level descriptors and F1/F2/F4 features')
+    if config['representation'] != 'xy_planes':
+        raise ValueError('XY-only representation is required')
+    gate_coarse_levels(config)
+    if config['gate_topology'] != 'shared' or config['gate_position'] != 'feature':
+        raise ValueError('Preserve the shared feature gate')
+    node_bitmaps, prefixes, bitmaps, descriptors, levels, clean = [], [], [], [], [], []
+    params = feature_offset = node_word_offset = bitmap_offset = 0
+    for level, (resolution, support, dim, cap) in enumerate(zip(resolutions, supports, plane_dims, plane_node_caps)):
+        if support.device.type != 'cpu' or support.dtype != torch.bool or support.shape != (resolution ** 2,):
+            raise ValueError('Support must be a flat CPU bool R^2 tensor')
+        if level < int(config['initial_active_prefix']) and not bool(support.all()):
+            raise ValueError('Declared initial full-cover supports must remain full')
+        support = support.clone()
+        points = align8(resolution ** 2)
+        nodes = plane_closure(support, resolution)
+        if cap % 8 or not nodes.numel() <= cap <= points:
+            raise ValueError('Aligned node capacity must contain the complete interpolation closure')
+        if points > INT32_MAX or params + cap * dim > INT32_MAX:
+            raise ValueError('Native points and packed offsets must fit int32 addressing')
+        direct = nodes.numel() == points
+        if direct:
+            index_offset, words = -1, 0
+        else:
+            node_bitmap, prefix = make_node_index(nodes, points)
+            index_offset, words = node_word_offset, node_bitmap.numel()
+            node_bitmaps.append(node_bitmap)
+            prefixes.append(prefix)
+            node_word_offset += words
+        bitmap = _cell_bitmap(support, points)
+        descriptors.append([resolution, points, params, index_offset, bitmap_offset, dim, feature_offset, int(direct)])
+        levels.append({'level': level, 'resolution': resolution, 'plane_dim': dim,
+                       'allowed_cells': int(support.sum()), 'plane_retained_nodes': nodes.numel(),
+                       'plane_node_capacity': cap, 'plane_unused_slots': cap - nodes.numel(),
+                       'native_plane_points': points, 'plane_offset': params,
+                       'feature_offset': feature_offset, 'nodes': nodes,
+                       'node_index_words': words, 'direct_node_access': direct})
+        bitmaps.append(bitmap)
+        clean.append(support)
+        params += cap * dim
+        feature_offset += dim
+        bitmap_offset += bitmap.numel()
+    return {'descriptors': torch.tensor(descriptors, dtype=torch.int32),
+            'node_bitmap': torch.cat(node_bitmaps) if node_bitmaps else torch.empty(0, dtype=torch.uint64),
+            'node_prefix': torch.cat(prefixes) if prefixes else torch.empty(0, dtype=torch.int32),
+            'bitmap': torch.cat(bitmaps), 'levels': levels, 'supports': clean,
+            'params': params, 'input_width': feature_offset}
+
+
+def _device_layout(tensor):
+    return tensor if tensor.numel() else torch.zeros(1, dtype=tensor.dtype, device=tensor.device)
+
+
+def packed_forward(coordinates, grid, descriptors, node_bitmap, node_prefix, bitmap, width):
+    """(features fp16 [N, width], visibility bool [N, L]) -- odie/packed_kernels.cu:107-125."""
+    if coordinates.dtype != torch.float32 or coordinates.ndim != 2 or coordinates.shape[1] != 2:
+        raise ValueError('coordinates must be CUDA contiguous FP32 Nx2')
+    if grid.dtype != torch.float32 or grid.ndim != 1:
+        raise ValueError('grid must be flat CUDA FP32')
+    coordinates, grid = coordinates.contiguous(), grid.contiguous()
+    n, levels = coordinates.shape[0], descriptors.shape[0]
+    features = torch.empty((n, width), dtype=torch.float16, device=coordinates.device)
+    visibility = torch.empty((n, levels), dtype=torch.bool, device=coordinates.device)
+    _lib.check(_lib.library().odie_packed_forward(
+        coordinates.data_ptr(), n, grid.data_ptr(), grid.numel(), descriptors.data_ptr(), levels,
+        _device_layout(node_bitmap).data_ptr(), _device_layout(node_prefix).data_ptr(), bitmap.data_ptr(), width,
+        features.data_ptr(), visibility.data_ptr(), _lib.stream_of(coordinates)))
+    return features, visibility
+
+
+def packed_backward(coordinates, upstream, descriptors, node_bitmap, node_prefix, bitmap, parameter_count):
+    """fp32 gradient [parameter_count] -- odie/packed_kernels.cu:127-145."""
+    if upstream.dtype != torch.float16 or upstream.ndim != 2 or upstream.shape[0] != coordinates.shape[0]:
+        raise ValueError('upstream must be CUDA contiguous FP16 NxF')
+    upstream = upstream.contiguous()
+    gradient = torch.empty(parameter_count, dtype=torch.float32, device=coordinates.device)
+    _lib.check(_lib.library().odie_packed_backward(
+        coordinates.data_ptr(), coordinates.shape[0], upstream.data_ptr(), upstream.shape[1],
+        descriptors.data_ptr(), descriptors.shape[0], _device_layout(node_bitmap).data_ptr(),
+        _device_layout(node_prefix).data_ptr(), bitmap.data_ptr(), gradient.data_ptr(), parameter_count,
+        _lib.stream_of(coordinates)))
+    return gradient
+
+
+class PackedQuery(torch.autograd.Function):
+    """Same contract as odie/model.py:137-151."""
+
+    @staticmethod
+    def forward(ctx, coordinates, grid, descriptors, node_bitmap, node_prefix, bitmap, width):
+        features, visible = packed_forward(coordinates, grid, descriptors, node_bitmap, node_prefix, bitmap, width)
+        ctx.save_for_backward(coordinates, descriptors, node_bitmap, node_prefix, bitmap)
+        ctx.param_count = grid.numel()
+        ctx.mark_non_differentiable(visible)
+        return features, visible
+
+    @staticmethod
+    def backward(ctx, feature_gradient, visibility_gradient):
+        coordinates, descriptors, node_bitmap, node_prefix, bitmap = ctx.saved_tensors
+        gradient = packed_backward(coordinates, feature_gradient.contiguous(), descriptors, node_bitmap,
+                                   node_prefix, bitmap, ctx.param_count)
+        return None, gradient, None, None, None, None, None

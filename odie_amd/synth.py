@@ -1,0 +1,75 @@
+"""Deterministic synthetic inputs, identical on every machine.
+
+Random words come from a counter-based SplitMix64 (Steele, Lea & Flood 2014): word i of a
+named stream is mix(key + (i+1)*0x9E3779B97F4A7C15), where key = mix(seed*phi + fnv1a(name)).
+Each tensor draws from its own named stream, so adding a tensor never shifts another.
+Derived values:
+  uniform fp32 in [0,1): (word >> 40) * 2^-24
+  uniform integer in [0, m): (word >> 32) * m >> 32
+  normal: Box-Muller in fp64 on two words, u1 = ((w1>>11)+1)*2^-53, u2 = (w2>>11)*2^-53
+"""
+import numpy as np
+
+PHI = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+
+def _mix(z):
+    with np.errstate(over='ignore'):
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+    return z ^ (z >> np.uint64(31))
+
+
+def _fnv1a(name):
+    value = 14695981039346656037
+    for byte in name.encode():
+        value = ((value ^ byte) * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    return np.uint64(value)
+
+
+def stream_key(seed, name):
+    with np.errstate(over='ignore'):
+        return _mix(np.asarray(np.uint64(seed) * PHI + _fnv1a(name), dtype=np.uint64))
+
+
+def words(seed, name, count, start=0):
+    key = stream_key(seed, name)
+    counter = np.arange(start + 1, start + 1 + count, dtype=np.uint64)
+    with np.errstate(over='ignore'):
+        return _mix(key + counter * PHI)
+
+
+def uniform(seed, name, count):
+    """fp32 in [0, 1) with 24 random bits."""
+    return ((words(seed, name, count) >> np.uint64(40)).astype(np.float32) * np.float32(2.0 ** -24))
+
+
+def integers(seed, name, count, modulus):
+    """Uniform integers in [0, modulus) by 32-bit multiply-shift (modulus < 2^32)."""
+    high = (words(seed, name, count) >> np.uint64(32))
+    return ((high * np.uint64(modulus)) >> np.uint64(32)).astype(np.int64)
+
+
+def normal(seed, name, count):
+    w = words(seed, name, 2 * count)
+    u1 = ((w[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * 2.0 ** -53
+    u2 = (w[1::2] >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+    return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+
+
+def coordinates(seed, count, name='coords'):
+    """count x 2 fp32 coordinates uniform in [0, 1)^2."""
+    return uniform(seed, name, 2 * count).reshape(count, 2)
+
+
+def table(seed, count, low=-1e-4, high=1e-4, name='table'):
+    """fp32 table values uniform in [low, high), computed in fp64 then rounded."""
+    u = uniform(seed, name, count).astype(np.float64)
+    return (low + (high - low) * u).astype(np.float32)
+
+
+def upstream(seed, rows, columns, name='upstream'):
+    """fp16 [rows, columns] standard normal upstream gradients."""
+    return normal(seed, name, rows * columns).astype(np.float16).reshape(rows, columns)

@@ -1,0 +1,388 @@
+"""CPU oracle for the sparse grid-query hot path -- TEST INFRASTRUCTURE ONLY.
+
+Restates the reference's algorithms so the HIP kernels can be checked against them:
+the arithmetic-heavy parts in plain C (odie_oracle.c, built by oracle/Makefile into
+oracle/_build/libodie_oracle.so), the rest here in numpy / pure Python.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only
+as the checker or the timed CPU baseline; the odie_amd package never does.
+
+Pinning status of each function (what fixes it beyond this restatement) is listed in
+PINS below and checked by tests/test_oracle_pins.py.
+"""
+import ctypes as C
+import heapq
+import math
+from pathlib import Path
+import struct
+import subprocess
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / '_build' / 'libodie_oracle.so'
+
+PINS = {
+    'f2h/h2f/hfma': 'exhaustive fp16 round trips vs numpy; hfma vs exact rational arithmetic (fractions)',
+    'grid_levels': 'reference-held layouts in results/**/metrics.json (tests/golden/layout_goldens.json)',
+    'hash_forward': 'dense level == bilinear interpolation in exact arithmetic; hash index vs '
+                    'Instant-NGP Eq. 4 brute force; fp16 chain vs fractions on tiny inputs',
+    'hash_backward': 'adjoint identity <fwd(x,g),u> = <g,bwd(x,u)> in fp64; brute force on tiny inputs',
+    'packed_forward/backward': 'all-visible direct layout == hash grid dense level with integer scale; '
+                               'rank addressing vs brute force; adjoint identity',
+    'residual': 'numpy bincount restatement of odie/selection.py:58-73',
+    'native_thresholds': 'exact rational fma boundaries brute-forced over fp32 bit patterns',
+    'select_benefit_cost': 'O(n^2) brute-force greedy on tiny resolutions with planted ties',
+    'select_mean_rank': 'brute-force restatement on tiny resolutions',
+    'adam': 'torch.optim.Adam on the CPU (torch-style variant)',
+    'compaction/topk': 'numpy.argsort(kind="stable")',
+}
+
+
+def build():
+    subprocess.run(['make', '-s', '-C', str(HERE)], check=True)
+    return LIBRARY
+
+
+_lib = None
+
+
+class Level(C.Structure):
+    _fields_ = [('scale', C.c_float), ('res', C.c_uint32), ('size', C.c_uint32),
+                ('offset', C.c_uint32), ('hashed', C.c_uint32)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        handle = C.CDLL(str(LIBRARY))
+        P, I, I64 = C.c_void_p, C.c_int, C.c_int64
+        handle.ora_h2f.argtypes, handle.ora_h2f.restype = [C.c_uint16], C.c_float
+        handle.ora_d2h.argtypes, handle.ora_d2h.restype = [C.c_double], C.c_uint16
+        handle.ora_f2h.argtypes, handle.ora_f2h.restype = [C.c_float], C.c_uint16
+        handle.ora_hfma.argtypes, handle.ora_hfma.restype = [C.c_uint16] * 3, C.c_uint16
+        handle.ora_hash_forward.argtypes = [P, P, I, I64, P, I, P, I, I, I, P, I]
+        handle.ora_hash_backward.argtypes = [P, P, I, I64, P, I, P, I, I, I, P, P]
+        handle.ora_hash_backward_f32.argtypes = [P, P, I, I64, P, P, I, I, I, P, I]
+        handle.ora_packed_forward.argtypes = [P, I64, P, P, I, P, P, P, I, P, P, I]
+        handle.ora_packed_backward.argtypes = [P, I64, P, I, P, I, P, P, P, P, P]
+        handle.ora_residual.argtypes = [P, P, I, I64, I64, I, I, P, P, P]
+        handle.ora_adam.argtypes = [I, P, P, P, P, P, I64, I64, C.c_double, C.c_double, C.c_double,
+                                    C.c_double, C.c_double]
+        for name in ('ora_hash_forward', 'ora_hash_backward', 'ora_hash_backward_f32', 'ora_packed_forward',
+                     'ora_packed_backward', 'ora_residual', 'ora_adam'):
+            getattr(handle, name).restype = None
+        _lib = handle
+    return _lib
+
+
+def _p(array):
+    return None if array is None else array.ctypes.data
+
+
+# ---------------------------------------------------------------------------------------
+# fp16 scalars
+# ---------------------------------------------------------------------------------------
+
+def h2f(bits):
+    return lib().ora_h2f(int(bits))
+
+
+def f2h(value):
+    return lib().ora_f2h(float(value))
+
+
+def hfma(a, b, c):
+    return lib().ora_hfma(int(a), int(b), int(c))
+
+
+# ---------------------------------------------------------------------------------------
+# Hash grid geometry (odie/config.py:79-94, restated independently of odie_amd.config)
+# ---------------------------------------------------------------------------------------
+
+def _f32(value):
+    return struct.unpack('f', struct.pack('f', value))[0]
+
+
+def grid_levels(encoding):
+    """[(scale, res, size, offset, hashed)] and the entry total of one table."""
+    levels = int(encoding['n_levels'])
+    base = int(encoding['base_resolution'])
+    size_limit = 1 << int(encoding['log2_hashmap_size'])
+    growth = _f32(encoding['per_level_scale'])
+    log_growth = _f32(math.log2(growth))
+    rows, offset = [], 0
+    for i in range(levels):
+        scale = _f32(_f32(_f32(2 ** _f32(i * log_growth)) * base) - 1)
+        res = math.ceil(scale) + 1
+        size = min((res * res + 7) // 8 * 8, size_limit)
+        rows.append((scale, res, size, offset, int(res * res > size)))
+        offset += size
+    return rows, offset
+
+
+def _levels(rows):
+    array = (Level * len(rows))()
+    for i, row in enumerate(rows):
+        array[i] = Level(*row)
+    return array
+
+
+def _offsets(offsets, n):
+    if offsets is None:
+        return np.array([0, n], dtype=np.int64), 1
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    return offsets, len(offsets) - 1
+
+
+def hash_forward(xy, table, rows, features, *, offsets=None, expert_params=None, width=None, threads=1):
+    """fp16 table -> fp16 [N, width]; fp32 table -> fp32 [N, width]."""
+    xy = np.ascontiguousarray(xy, dtype=np.float32)
+    table = np.ascontiguousarray(table)
+    offsets, experts = _offsets(offsets, len(xy))
+    width = width or len(rows) * features
+    half = table.dtype == np.float16
+    out = np.zeros((len(xy), width), dtype=np.float16 if half else np.float32)
+    expert_params = expert_params or table.size // experts
+    lib().ora_hash_forward(_p(xy), _p(offsets), experts, expert_params, _p(table.view(np.uint16) if half else table),
+                           1 if half else 0, _levels(rows), len(rows), features, width,
+                           _p(out.view(np.uint16) if half else out), threads)
+    return out
+
+
+def hash_backward(xy, upstream, rows, features, total, *, offsets=None, expert_params=None):
+    """(gradient fp64 [total], magnitude fp64 [total]) -- exact-order-free checker."""
+    xy = np.ascontiguousarray(xy, dtype=np.float32)
+    upstream = np.ascontiguousarray(upstream)
+    offsets, experts = _offsets(offsets, len(xy))
+    expert_params = expert_params or total // experts
+    grad = np.zeros(total, dtype=np.float64)
+    magnitude = np.zeros(total, dtype=np.float64)
+    half = upstream.dtype == np.float16
+    values = upstream.view(np.uint16) if half else np.ascontiguousarray(upstream, dtype=np.float32)
+    lib().ora_hash_backward(_p(xy), _p(offsets), experts, expert_params, _p(values),
+                            1 if half else 0, _levels(rows), len(rows), features, upstream.shape[1],
+                            _p(grad), _p(magnitude))
+    return grad, magnitude
+
+
+def hash_backward_f32(xy, upstream, rows, features, total, *, offsets=None, expert_params=None, threads=1):
+    """The CPU-baseline form: fp32 accumulation with atomic adds across threads."""
+    xy = np.ascontiguousarray(xy, dtype=np.float32)
+    upstream = np.ascontiguousarray(upstream, dtype=np.float16)
+    offsets, experts = _offsets(offsets, len(xy))
+    expert_params = expert_params or total // experts
+    grad = np.zeros(total, dtype=np.float32)
+    lib().ora_hash_backward_f32(_p(xy), _p(offsets), experts, expert_params, _p(upstream.view(np.uint16)),
+                                _levels(rows), len(rows), features, upstream.shape[1], _p(grad), threads)
+    return grad
+
+
+# ---------------------------------------------------------------------------------------
+# Packed xy planes (odie/packed_kernels.cu)
+# ---------------------------------------------------------------------------------------
+
+def packed_forward(xy, grid, layout, width, threads=1):
+    xy = np.ascontiguousarray(xy, dtype=np.float32)
+    desc = np.ascontiguousarray(layout['descriptors'], dtype=np.int32)
+    node_bitmap = np.ascontiguousarray(layout['node_bitmap'], dtype=np.uint64)
+    prefix = np.ascontiguousarray(layout['node_prefix'], dtype=np.int32)
+    bitmap = np.ascontiguousarray(layout['bitmap'], dtype=np.uint8)
+    grid = np.ascontiguousarray(grid, dtype=np.float32)
+    out = np.zeros((len(xy), width), dtype=np.float16)
+    vis = np.zeros((len(xy), len(desc)), dtype=np.uint8)
+    lib().ora_packed_forward(_p(xy), len(xy), _p(grid), _p(desc), len(desc), _p(node_bitmap), _p(prefix),
+                             _p(bitmap), width, _p(out.view(np.uint16)), _p(vis), threads)
+    return out, vis.astype(bool)
+
+
+def packed_backward(xy, upstream, layout, total):
+    xy = np.ascontiguousarray(xy, dtype=np.float32)
+    upstream = np.ascontiguousarray(upstream, dtype=np.float16)
+    desc = np.ascontiguousarray(layout['descriptors'], dtype=np.int32)
+    node_bitmap = np.ascontiguousarray(layout['node_bitmap'], dtype=np.uint64)
+    prefix = np.ascontiguousarray(layout['node_prefix'], dtype=np.int32)
+    bitmap = np.ascontiguousarray(layout['bitmap'], dtype=np.uint8)
+    grad = np.zeros(total, dtype=np.float64)
+    magnitude = np.zeros(total, dtype=np.float64)
+    lib().ora_packed_backward(_p(xy), len(xy), _p(upstream.view(np.uint16)), upstream.shape[1], _p(desc),
+                              len(desc), _p(node_bitmap), _p(prefix), _p(bitmap), _p(grad), _p(magnitude))
+    return grad, magnitude
+
+
+# ---------------------------------------------------------------------------------------
+# Residual, thresholds, selection (odie/selection.py, odie/residual_cuda.cu)
+# ---------------------------------------------------------------------------------------
+
+def residual(prediction, target, width, resolution, xb, yb, begin=0, totals=None):
+    prediction = np.ascontiguousarray(prediction, dtype=np.float32)
+    target = np.ascontiguousarray(target)
+    rgb8 = target.dtype == np.uint8
+    if not rgb8:
+        target = target.astype(np.float32)
+    xb = np.ascontiguousarray(xb, dtype=np.int32)
+    yb = np.ascontiguousarray(yb, dtype=np.int32)
+    if totals is None:
+        totals = np.zeros(resolution * resolution, dtype=np.float64)
+    end = begin + prediction.reshape(-1, 3).shape[0]
+    lib().ora_residual(_p(prediction), _p(target), int(rgb8), begin, end, width, resolution, _p(xb), _p(yb),
+                       _p(totals))
+    return totals
+
+
+def align8(value):
+    return (int(value) + 7) // 8 * 8
+
+
+def _float_from_bits(bits):
+    return struct.unpack('<f', struct.pack('<I', bits))[0]
+
+
+def native_thresholds(resolution):
+    """Smallest fp32 x in [0,1] with floor(fma(R-1, x, 0.5)) >= region, per region 1..R-1
+    (odie/selection.py:16-42): binary search over fp32 bit patterns against the exact
+    rounding boundary of the fused result."""
+    scale = resolution - 1
+    thresholds = []
+    for region in range(1, resolution):
+        region_bits = struct.unpack('<I', struct.pack('<f', region))[0]
+        below_num, below_den = _float_from_bits(region_bits - 1).as_integer_ratio()
+        # fma(scale, x, 0.5) rounds up to `region` once scale*x + 0.5 passes the midpoint
+        # between `region` and its fp32 predecessor (ties go to the even neighbour).
+        boundary_num = (region - 1) * below_den + below_num
+        boundary_den = 2 * below_den
+        include_tie = region_bits % 2 == 0
+        lower, upper = 0, 0x3F800000
+        while lower < upper:
+            middle = (lower + upper) // 2
+            numerator, denominator = _float_from_bits(middle).as_integer_ratio()
+            left, right = scale * numerator * boundary_den, boundary_num * denominator
+            if left > right or (left == right and include_tie):
+                upper = middle
+            else:
+                lower = middle + 1
+        thresholds.append(_float_from_bits(lower))
+    return np.asarray(thresholds, dtype=np.float32)
+
+
+def pixel_cells(shape, resolution):
+    height, width = shape
+    thresholds = native_thresholds(resolution)
+    x = np.arange(width, dtype=np.float32) / np.float32(width - 1)
+    y = np.arange(height, dtype=np.float32) / np.float32(height - 1)
+    xb = np.searchsorted(thresholds, x, side='right')
+    yb = np.searchsorted(thresholds, y, side='right')
+    return (yb[:, None] * resolution + xb[None, :]).reshape(-1)
+
+
+def closure_nodes(cells, resolution):
+    cells = np.asarray(cells, dtype=np.int64)
+    return np.unique(np.concatenate([cells, cells + 1, cells + resolution, cells + resolution + 1])
+                     % align8(resolution ** 2))
+
+
+def select_mean_rank(scores, resolution, cap):
+    """B1 (odie/selection.py:108-126): stable descending ranking, admit a cell when its new
+    closure nodes fit under the cap."""
+    scores = np.asarray(scores, dtype=np.float64)
+    points = align8(resolution ** 2)
+    selected = np.zeros(resolution ** 2, dtype=bool)
+    nodes = np.zeros(points, dtype=bool)
+    used = 0
+    for cell in np.argsort(-scores, kind='stable'):
+        corners = (cell + np.array([0, 1, resolution, resolution + 1])) % points
+        added = corners[~nodes[corners]]
+        if used + len(added) <= cap:
+            selected[cell] = True
+            nodes[added] = True
+            used += len(added)
+    return selected, nodes
+
+
+def select_benefit_cost(scores, resolution, cap, normalize_by_cost=True, trace=None):
+    """B2 exact greedy (odie/selection.py:129-207): free cells (no new nodes) first in
+    ascending id; otherwise the best score/cost over cost 1..min(4, cap-used), compared by
+    cross-multiplication, ties to the lower id.  Returns (selected, nodes, iterations)."""
+    scores = np.asarray(scores, dtype=np.float64)
+    cells, points = resolution ** 2, align8(resolution ** 2)
+    selected = np.zeros(cells, dtype=bool)
+    nodes = np.zeros(points, dtype=bool)
+    missing = np.full(cells, 4, dtype=np.int64)
+    heaps = [[] for _ in range(5)]
+    heaps[4] = [(-float(value), cell) for cell, value in enumerate(scores)]
+    heapq.heapify(heaps[4])
+    used = iterations = 0
+    deltas = (0, 1, resolution, resolution + 1)
+
+    def top(cost):
+        heap = heaps[cost]
+        while heap and (selected[heap[0][1]] or missing[heap[0][1]] != cost):
+            heapq.heappop(heap)
+        return heap[0] if heap else None
+
+    while True:
+        free = top(0)
+        if free is not None:
+            cell, cost = free[1], 0
+        else:
+            best = None
+            for cost in range(1, min(4, cap - used) + 1):
+                candidate = top(cost)
+                if candidate is None:
+                    continue
+                score, cell = -candidate[0], candidate[1]
+                if best is None:
+                    best = (score, cost, cell)
+                    continue
+                left, right = ((score * best[1], best[0] * cost) if normalize_by_cost else (score, best[0]))
+                if left > right or (left == right and cell < best[2]):
+                    best = (score, cost, cell)
+            if best is None:
+                break
+            _, cost, cell = best
+        heapq.heappop(heaps[cost])
+        selected[cell] = True
+        corners = [(cell + d) % points for d in deltas]
+        added = [node for node in corners if not nodes[node]]
+        assert len(added) == cost, 'stale marginal cost'
+        nodes[added] = True
+        used += cost
+        iterations += 1
+        if trace is not None:
+            trace.append(cell)
+        changed = set()
+        for node in added:
+            for d in deltas:
+                incident = (node - d) % points
+                if incident < cells and not selected[incident]:
+                    missing[incident] -= 1
+                    changed.add(incident)
+        for incident in changed:
+            now = int(missing[incident])
+            heapq.heappush(heaps[now], (incident if now == 0 else -float(scores[incident]), incident))
+    return selected, nodes, iterations
+
+
+def topk_ids(scores, k):
+    """Top-k by (score descending, id ascending), returned sorted ascending by id."""
+    order = np.argsort(-np.asarray(scores, dtype=np.float64), kind='stable')[:k]
+    return np.sort(order)
+
+
+def compact(expert, experts):
+    """Stable counting sort by expert id: (perm, offsets)."""
+    expert = np.asarray(expert)
+    perm = np.argsort(expert, kind='stable')
+    counts = np.bincount(expert, minlength=experts)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    return perm.astype(np.int64), offsets.astype(np.int64)
+
+
+def adam(variant, param, grad, m, v, steps, step, lr, beta1=0.9, beta2=0.999, eps=1e-15, scale=1.0):
+    """In place on float64 arrays (steps: uint32 per-parameter ages for variant 1)."""
+    param = np.ascontiguousarray(param, dtype=np.float64)
+    grad = np.ascontiguousarray(grad, dtype=np.float64)
+    lib().ora_adam(int(variant), _p(param), _p(grad), _p(m), _p(v), _p(steps), param.size, int(step),
+                   lr, beta1, beta2, eps, scale)
+    return param

@@ -1,0 +1,77 @@
+"""The C-ABI library loads, exports every declared symbol, and rejects bad arguments
+before queuing any device work (these calls never reach the GPU)."""
+import ctypes as C
+import subprocess
+
+import pytest
+
+from odie_amd import _lib
+from odie_amd.config import grid_levels
+
+
+def test_every_declared_symbol_is_exported(native):
+    declared = _lib.declared_symbols()
+    assert 'odie_grid_forward' in declared and 'odie_error' in declared
+    exported = subprocess.run(['nm', '-D', '--defined-only', str(_lib.LIBRARY)], capture_output=True, text=True,
+                              check=True).stdout
+    names = {line.split()[-1] for line in exported.splitlines() if line.strip()}
+    missing = [name for name in declared if name not in names]
+    assert not missing, missing
+    for name in declared:
+        getattr(native, name)
+
+
+def test_bindings_cover_declarations():
+    assert set(_lib.declared_symbols()) <= set(_lib.SIGNATURES), \
+        set(_lib.declared_symbols()) - set(_lib.SIGNATURES)
+
+
+def _levels():
+    return grid_levels(dict(n_levels=4, base_resolution=4, log2_hashmap_size=8, per_level_scale=2.0))
+
+
+@pytest.mark.parametrize('change,message', [
+    (dict(n=-1), 'n must be'),
+    (dict(experts=0), 'experts must be'),
+    (dict(experts=2), 'offsets are required'),
+    (dict(n_levels=0), 'n_levels must be'),
+    (dict(n_levels=33), 'n_levels must be'),
+    (dict(features=3), 'features per level'),
+    (dict(dtype=7), 'param_dtype'),
+    (dict(width=3), 'out_width'),
+    (dict(expert_params=10), 'expert_params'),
+])
+def test_grid_forward_rejects_bad_arguments(native, change, message):
+    levels, entries = _levels()
+    args = dict(n=16, experts=1, n_levels=4, features=2, dtype=1, width=8, expert_params=entries * 2)
+    args.update(change)
+    code = native.odie_grid_forward(8, args['n'], None, args['experts'], 8, args['expert_params'], args['dtype'],
+                                    levels, args['n_levels'], args['features'], 16, args['width'], 0)
+    assert code == -1
+    assert message in native.odie_error().decode()
+
+
+def test_levels_must_be_contiguous(native):
+    levels, entries = _levels()
+    levels[2].offset += 8
+    assert native.odie_grid_backward(8, 16, None, 1, 8, 1, 8, entries * 2 + 64, levels, 4, 2, 16, 1, 0) == -1
+    assert 'contiguous' in native.odie_error().decode()
+
+
+def test_packed_rejects_bad_arguments(native):
+    assert native.odie_packed_forward(8, 4, 8, 100, 8, 1, 8, 8, 8, 4, 8, 8, 0) == -1
+    assert '2..32 levels' in native.odie_error().decode()
+    assert native.odie_packed_forward(8, 4, 8, 100, 8, 4, 8, 8, 8, 200, 8, 8, 0) == -1
+    assert 'width' in native.odie_error().decode()
+
+
+def test_tuning_rejects_unknown_keys(native):
+    assert native.odie_set_tuning(b'nonsense', 1) == -1
+    assert native.odie_set_tuning(b'lds_bytes', 10 ** 9) == -1
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, 'LIBRARY', tmp_path / 'libodie_amd.so')
+    monkeypatch.setattr(_lib, '_handle', None)
+    with pytest.raises(_lib.NativeError, match='no CPU fallback'):
+        _lib.library()

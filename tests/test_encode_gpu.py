@@ -1,0 +1,193 @@
+"""GPU parity of the grid encode (HIP via the C-ABI) against the CPU oracle.
+
+Forward: bit-exact (fp16 chain and fp32 chain).  Backward: each gradient entry within
+1e-4 of the sum of the absolute values of its contributions (the fp32 atomic summation
+order is free), plus 1e-30 absolute.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from odie_amd import _lib
+from odie_amd.config import grid_levels
+from odie_amd.encoding import grid_backward, grid_forward
+from odie_amd import synth
+
+pytestmark = pytest.mark.gpu
+GRAD_RTOL = 1e-4
+
+
+def rows_of(levels):
+    return [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
+
+
+def check_gradient(gpu, expected, magnitude, label=''):
+    gpu = gpu.detach().cpu().numpy().astype(np.float64)
+    bound = GRAD_RTOL * magnitude + 1e-30
+    bad = np.abs(gpu - expected) > bound
+    assert not bad.any(), '%s: %d/%d entries out of tolerance, first %s: gpu %r oracle %r' % (
+        label, bad.sum(), bad.size, np.flatnonzero(bad)[:5], gpu[bad][:5], expected[bad][:5])
+
+
+def encoding(levels=16, base=16, log2=19, scale=1.38, features=2):
+    return dict(n_levels=levels, base_resolution=base, log2_hashmap_size=log2, per_level_scale=scale,
+                n_features_per_level=features)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.float32])
+def test_single_grid_forward_bit_exact(dtype):
+    enc = encoding()
+    levels, entries = grid_levels(enc)
+    n = 1 << 16
+    xy = synth.coordinates(0, n)
+    values = synth.table(0, entries * 2)
+    table = values.astype(np.float16) if dtype == torch.float16 else values
+    out = grid_forward(torch.from_numpy(xy).cuda(), torch.from_numpy(table).cuda(), levels, 2)
+    expected = oracle.hash_forward(xy, table, rows_of(levels), 2, threads=0)
+    got = out.cpu().numpy()
+    view = np.uint16 if dtype == torch.float16 else np.uint32
+    mismatch = got.view(view) != expected.view(view)
+    assert not mismatch.any(), 'mismatches at %s' % (np.argwhere(mismatch)[:5],)
+
+
+@pytest.mark.parametrize('lds_bytes', [0, 65536])
+def test_single_grid_backward_tolerance(lds_bytes):
+    enc = encoding()
+    levels, entries = grid_levels(enc)
+    n = 1 << 16
+    xy = synth.coordinates(0, n)
+    up = synth.upstream(0, n, 32)
+    _lib.set_tuning('lds_bytes', lds_bytes)
+    try:
+        grad = grid_backward(torch.from_numpy(xy).cuda(), torch.from_numpy(up).cuda(), levels, 2,
+                             expert_params=entries * 2)
+    finally:
+        _lib.set_tuning('lds_bytes', 65536)
+    expected, magnitude = oracle.hash_backward(xy, up, rows_of(levels), 2, entries * 2)
+    check_gradient(grad, expected, magnitude, 'single grid lds=%d' % lds_bytes)
+
+
+def test_experts_forward_and_backward():
+    enc = encoding(log2=14)
+    levels, entries = grid_levels(enc)
+    experts, params = 16, entries * 2
+    n = 40000
+    rng = np.random.default_rng(1)
+    counts = rng.multinomial(n, np.r_[np.zeros(2), np.ones(experts - 3), [0.0]] / (experts - 3))
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)   # empty experts 0, 1, 15
+    xy = synth.coordinates(3, n)
+    table = synth.table(3, experts * params).astype(np.float16)
+    up = synth.upstream(3, n, 32)
+    d_xy, d_off = torch.from_numpy(xy).cuda(), torch.from_numpy(offsets).cuda()
+    out = grid_forward(d_xy, torch.from_numpy(table).cuda(), levels, 2, offsets=d_off, experts=experts,
+                       expert_params=params)
+    expected = oracle.hash_forward(xy, table, rows_of(levels), 2, offsets=offsets, expert_params=params, threads=0)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), expected.view(np.uint16))
+    grad = grid_backward(d_xy, torch.from_numpy(up).cuda(), levels, 2, offsets=d_off, experts=experts,
+                         expert_params=params)
+    exp_grad, magnitude = oracle.hash_backward(xy, up, rows_of(levels), 2, experts * params, offsets=offsets,
+                                               expert_params=params)
+    check_gradient(grad, exp_grad, magnitude, 'experts')
+
+
+@pytest.mark.parametrize('features,n_levels,width,n', [(1, 5, 5, 1000), (4, 3, 16, 777), (8, 2, 16, 513),
+                                                        (2, 20, 40, 3001), (2, 16, 36, 1029), (2, 1, 2, 1)])
+def test_shapes_and_padding(features, n_levels, width, n):
+    enc = encoding(levels=n_levels, base=3, log2=10, scale=1.7, features=features)
+    levels, entries = grid_levels(enc)
+    xy = synth.coordinates(5, n)
+    xy[0] = (0.0, 0.0)
+    if n > 1:
+        xy[1] = (1.0, 1.0)
+    table = synth.table(5, entries * features, -1.0, 1.0).astype(np.float16)
+    out = grid_forward(torch.from_numpy(xy).cuda(), torch.from_numpy(table).cuda(), levels, features, width=width)
+    expected = oracle.hash_forward(xy, table, rows_of(levels), features, width=width)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), expected.view(np.uint16))
+    up = synth.upstream(5, n, width)
+    up[:, ::3] = 0   # zero upstream values are skipped
+    grad = grid_backward(torch.from_numpy(xy).cuda(), torch.from_numpy(up).cuda(), levels, features,
+                         expert_params=entries * features)
+    exp_grad, magnitude = oracle.hash_backward(xy, up, rows_of(levels), features, entries * features)
+    check_gradient(grad, exp_grad, magnitude, 'F=%d L=%d' % (features, n_levels))
+
+
+def test_fp32_upstream_and_accumulate():
+    levels, entries = grid_levels(encoding(levels=8, log2=12))
+    n = 5000
+    xy = synth.coordinates(7, n)
+    up = synth.normal(7, 'up32', n * 16).astype(np.float32).reshape(n, 16)
+    d_xy = torch.from_numpy(xy).cuda()
+    grad = grid_backward(d_xy, torch.from_numpy(up).cuda(), levels, 2, expert_params=entries * 2)
+    grad = grid_backward(d_xy, torch.from_numpy(up).cuda(), levels, 2, expert_params=entries * 2, gradient=grad,
+                         accumulate=True)
+    expected, magnitude = oracle.hash_backward(xy, up, rows_of(levels), 2, entries * 2)
+    check_gradient(grad, 2 * expected, 2 * magnitude, 'fp32 upstream x2')
+
+
+def test_empty_input_and_xcd_order_invariance():
+    levels, entries = grid_levels(encoding(levels=4, log2=10))
+    empty = torch.zeros((0, 2), device='cuda')
+    assert grid_forward(empty, torch.zeros(entries * 2, dtype=torch.float16, device='cuda'), levels, 2).shape == (0, 8)
+    grad = grid_backward(empty, torch.zeros((0, 8), dtype=torch.float16, device='cuda'), levels, 2,
+                         expert_params=entries * 2)
+    assert not grad.any()
+    xy = torch.from_numpy(synth.coordinates(9, 3000)).cuda()
+    table = torch.from_numpy(synth.table(9, entries * 2).astype(np.float16)).cuda()
+    first = grid_forward(xy, table, levels, 2)
+    _lib.set_tuning('xcd_remap', 0)
+    try:
+        second = grid_forward(xy, table, levels, 2)
+    finally:
+        _lib.set_tuning('xcd_remap', 1)
+    assert torch.equal(first, second)
+
+
+def test_grid_encoding_module_autograd():
+    from odie_amd.encoding import GridEncoding
+    module = GridEncoding(encoding(levels=6, log2=12), dtype=torch.float16)
+    with torch.no_grad():
+        module.params.copy_(torch.from_numpy(synth.table(11, module.n_params, -1, 1)))
+    xy = torch.from_numpy(synth.coordinates(11, 2048)).cuda()
+    out = module(xy)
+    weight = torch.from_numpy(synth.upstream(11, 2048, 12)).cuda()
+    (out.float() * weight.float()).sum().backward()
+    expected, magnitude = oracle.hash_backward(xy.cpu().numpy(), weight.cpu().numpy(), rows_of(module.levels), 2,
+                                               module.n_params)
+    check_gradient(module.params.grad, expected, magnitude, 'autograd')
+
+
+def _packed_layout(seed):
+    from odie_amd.model import make_layout, plane_closure
+    rng = np.random.default_rng(seed)
+    resolutions = [8, 13, 20, 32, 51, 81]
+    supports, caps = [], []
+    for level, r in enumerate(resolutions):
+        support = np.ones(r * r, dtype=bool) if level < 3 else rng.random(r * r) < 0.3
+        nodes = plane_closure(torch.as_tensor(support), r)
+        supports.append(torch.as_tensor(support))
+        caps.append(min((r * r + 7) // 8 * 8, (nodes.numel() + 7) // 8 * 8 + 8 * level))
+    config = dict(resolutions=resolutions, n_levels=6, representation='xy_planes', coarse_levels=0,
+                  gate_topology='shared', gate_position='feature', initial_active_prefix=3)
+    return make_layout(config, supports, [2, 2, 2, 2, 1, 4], caps)
+
+
+def test_packed_planes_forward_backward():
+    from odie_amd.model import PackedQuery
+    layout = _packed_layout(2)
+    n, width = 20000, 13
+    xy = synth.coordinates(13, n)
+    xy[:4] = [(0, 0), (1, 1), (0, 1), (1, 0)]
+    grid = synth.table(13, layout['params'], -0.5, 0.5)
+    host = {k: layout[k].numpy() for k in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap')}
+    expected, vis = oracle.packed_forward(xy, grid, host, width)
+    dev = {k: layout[k].cuda() for k in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap')}
+    d_grid = torch.from_numpy(grid).cuda().requires_grad_(True)
+    features, visible = PackedQuery.apply(torch.from_numpy(xy).cuda(), d_grid, dev['descriptors'], dev['node_bitmap'],
+                                          dev['node_prefix'], dev['bitmap'], width)
+    assert np.array_equal(features.detach().cpu().numpy().view(np.uint16), expected.view(np.uint16))
+    assert np.array_equal(visible.cpu().numpy(), vis)
+    up = synth.upstream(13, n, width)
+    features.backward(torch.from_numpy(up).cuda())
+    exp_grad, magnitude = oracle.packed_backward(xy, up, host, layout['params'])
+    check_gradient(d_grid.grad, exp_grad, magnitude, 'packed')

@@ -1,0 +1,426 @@
+"""Pin the CPU oracle against what the mathematics, library routines and the reference's
+own recorded data fix -- never against a retyped copy of its own formula."""
+import ctypes
+from fractions import Fraction
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from exact import HALF, SINGLE, half_value, round_fraction, to_half_bits
+
+GOLDEN = Path(__file__).resolve().parent / 'golden'
+LIBM = ctypes.CDLL('libm.so.6')
+LIBM.fmaf.argtypes = [ctypes.c_float] * 3
+LIBM.fmaf.restype = ctypes.c_float
+
+
+# ---------------------------------------------------------------------------------------
+# fp16 conversions and the fused fp16 multiply-add
+# ---------------------------------------------------------------------------------------
+
+def test_half_to_float_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    expected = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.h2f(b) for b in bits], dtype=np.float32)
+    finite = np.isfinite(expected)
+    assert np.array_equal(got[finite].view(np.uint32), expected[finite].view(np.uint32))
+    assert np.isnan(got[~np.isfinite(expected) & np.isnan(expected)]).all()
+
+
+def test_float_to_half_matches_numpy_at_midpoints(oracle):
+    # every finite half, the exact midpoints between neighbours and one fp32 ulp either side
+    halves = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = (halves[:-1] + halves[1:]) / 2
+    candidates = np.concatenate([halves, mids]).astype(np.float32)
+    candidates = np.concatenate([candidates, np.nextafter(candidates, np.float32(np.inf)),
+                                 np.nextafter(candidates, np.float32(0))])
+    candidates = np.concatenate([candidates, -candidates, np.float32([65504, 65519.99, 65520, 1e6])])
+    expected = candidates.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f2h(v) for v in candidates], dtype=np.uint16)
+    assert np.array_equal(got, expected)
+
+
+def _exact_hfma(a, b, c):
+    value = half_value(a) * half_value(b) + half_value(c)
+    return round_fraction(value, HALF)
+
+
+def test_hfma_against_exact_rationals(oracle):
+    rng = np.random.default_rng(7)
+    finite = np.arange(0, 0x7c00, dtype=np.uint16)
+    finite = np.concatenate([finite, finite | 0x8000])
+    triples = rng.choice(finite, size=(4000, 3))
+    # products landing exactly on half midpoints, subnormal results, cancellation
+    special = [(0x3c00, 0x0001, 0x0000), (0x3800, 0x0001, 0x0000), (0x3800, 0x0003, 0x0000),
+               (0x3c01, 0x3c01, 0x0000), (0x3c00, 0x3c00, 0xbc00), (0x0400, 0x3800, 0x8001),
+               (0x3bff, 0x0001, 0x0001), (0x7bff, 0x3c00, 0x7bff)]
+    for a, b, c in list(map(tuple, triples)) + special:
+        got = oracle.hfma(a, b, c)
+        expected = _exact_hfma(a, b, c)
+        if isinstance(expected, float):
+            assert got in (0x7c00, 0xfc00) and (got == 0x7c00) == (expected > 0)
+        else:
+            assert half_value(got) == expected, (hex(a), hex(b), hex(c))
+
+
+# ---------------------------------------------------------------------------------------
+# Hash-grid geometry: reference-held layouts
+# ---------------------------------------------------------------------------------------
+
+def _goldens():
+    return json.loads((GOLDEN / 'layout_goldens.json').read_text())
+
+
+def test_grid_levels_match_reference_recorded_hashgrid_layout(oracle):
+    hash_runs = [v for v in _goldens().values() if v['config'].get('representation') == 'hash_grid']
+    assert hash_runs, 'expected HashGrid runs among the reference records'
+    for run in hash_runs:
+        config = run['config']
+        rows, _ = oracle.grid_levels(config['hash_encoding'])
+        assert [r[1] for r in rows] == config['resolutions']
+        assert [r[2] for r in rows] == config['cell_caps']
+        total = sum(r[2] for r in rows) * config['hash_encoding']['n_features_per_level']
+        assert total + config['gate_parameters'] + config['decoder_parameters'] == config['allocated_parameters']
+
+
+def test_grid_levels_single_expert_workload(oracle):
+    rows, entries = oracle.grid_levels(dict(n_levels=16, base_resolution=16, log2_hashmap_size=19,
+                                            per_level_scale=1.38))
+    assert [r[1] for r in rows] == [16, 23, 31, 43, 59, 81, 111, 153, 211, 291, 401, 554, 764, 1054, 1454, 2006]
+    assert [r[2] for r in rows][:12] == [256, 536, 968, 1856, 3488, 6568, 12328, 23416, 44528, 84688, 160808, 306920]
+    assert [r[4] for r in rows] == [0] * 12 + [1] * 4
+    assert entries == 2743512
+    rows, entries = oracle.grid_levels(dict(n_levels=16, base_resolution=16, log2_hashmap_size=16,
+                                            per_level_scale=1.38))
+    assert entries == 552696 and [r[4] for r in rows] == [0] * 9 + [1] * 7
+
+
+# ---------------------------------------------------------------------------------------
+# Hash-grid encode: bilinear interpolation and Instant-NGP Eq. 4 indices
+# ---------------------------------------------------------------------------------------
+
+def _exact_corner(scale, x):
+    """floor and fraction of fma(scale, x, 0.5) computed exactly (libm fmaf is correctly
+    rounded; cross-checked against rational rounding)."""
+    p = LIBM.fmaf(scale, x, 0.5)
+    exact = round_fraction(Fraction(float(np.float32(scale))) * Fraction(float(np.float32(x))) + Fraction(1, 2), SINGLE)
+    assert Fraction(float(np.float32(p))) == exact
+    g = math.floor(p)
+    return g, np.float32(p) - np.float32(g)
+
+
+def test_dense_level_reproduces_linear_function(oracle):
+    # table T[gx + gy*res] = gx + 1024*gy: bilinear interpolation returns px + 1024*py
+    scale = np.float32(21.08)
+    res, size = 23, 536
+    rows = [(float(scale), res, size, 0, 0)]
+    table = np.zeros(size, dtype=np.float32)
+    for gy in range(res):
+        for gx in range(res):
+            if gx + gy * res < size:
+                table[gx + gy * res] = gx + 1024 * gy
+    rng = np.random.default_rng(3)
+    xy = rng.uniform(0, (res - 2.0) / float(scale), size=(2000, 2)).astype(np.float32)
+    out = oracle.hash_forward(xy, table, rows, 1)
+    px = np.array([LIBM.fmaf(scale, x, 0.5) for x in xy[:, 0]], dtype=np.float64)
+    py = np.array([LIBM.fmaf(scale, y, 0.5) for y in xy[:, 1]], dtype=np.float64)
+    expected = px + 1024 * py
+    assert np.allclose(out[:, 0], expected, rtol=0, atol=1024 * res * 2.0 ** -21)
+    # swapping the axes must be visible
+    assert not np.allclose(out[:, 0], py + 1024 * px, atol=1.0)
+
+
+def test_hashed_level_indices_and_weights_brute_force(oracle):
+    scale = np.float32(2005.1)
+    res, size = 2007, 1 << 12
+    rows = [(float(scale), res, size, 0, 1)]
+    rng = np.random.default_rng(5)
+    xy = rng.random((64, 2), dtype=np.float32)
+    for i in range(len(xy)):
+        upstream = np.ones((1, 1), dtype=np.float16)
+        grad, _ = oracle.hash_backward(xy[i:i + 1], upstream, rows, 1, size)
+        gx, fx = _exact_corner(scale, xy[i, 0])
+        gy, fy = _exact_corner(scale, xy[i, 1])
+        expected = np.zeros(size)
+        weights = [(1 - fx) * (1 - fy), fx * (1 - fy), (1 - fx) * fy, fx * fy]
+        for k in range(4):
+            cx, cy = gx + (k & 1), gy + (k >> 1)
+            index = ((cx * 1) ^ ((cy * 2654435761) % 2 ** 32)) % size
+            expected[index] += float(np.float32(weights[k]))
+        assert np.array_equal(grad, expected)
+
+
+def test_fp16_chain_against_exact_rounding(oracle):
+    rows = [(15.0, 16, 256, 0, 0), (21.08, 23, 536, 256, 0)]
+    rng = np.random.default_rng(11)
+    table = rng.normal(0, 0.3, size=(792, 2)).astype(np.float16)
+    xy = rng.random((40, 2), dtype=np.float32)
+    out = oracle.hash_forward(xy, table, rows, 2)
+    for i in range(len(xy)):
+        for level, (scale, res, size, offset, _) in enumerate(rows):
+            gx, fx = _exact_corner(np.float32(scale), xy[i, 0])
+            gy, fy = _exact_corner(np.float32(scale), xy[i, 1])
+            weights = [np.float32((1 - fx) * (1 - fy)), np.float32(fx * (1 - fy)),
+                       np.float32((1 - fx) * fy), np.float32(fx * fy)]
+            for c in range(2):
+                value = Fraction(0)
+                for k in range(4):
+                    index = ((gx + (k & 1)) + (gy + (k >> 1)) * res) % size
+                    w16 = round_fraction(Fraction(float(weights[k])), HALF)
+                    g16 = Fraction(float(table[offset + index, c]))
+                    value = round_fraction(w16 * g16 + value, HALF)
+                assert Fraction(float(out[i, level * 2 + c])) == value
+
+
+def test_backward_is_adjoint_of_forward(oracle):
+    rows, entries = oracle.grid_levels(dict(n_levels=6, base_resolution=4, log2_hashmap_size=8,
+                                            per_level_scale=1.9))
+    rng = np.random.default_rng(13)
+    table = rng.normal(size=entries * 2).astype(np.float32)
+    xy = rng.random((300, 2), dtype=np.float32)
+    upstream = rng.normal(size=(300, 12)).astype(np.float32)
+    forward = oracle.hash_forward(xy, table, rows, 2).astype(np.float64)
+    grad, _ = oracle.hash_backward(xy, upstream, rows, 2, entries * 2)
+    left = float((forward * upstream).sum())
+    right = float((table.astype(np.float64) * grad).sum())
+    assert abs(left - right) <= 1e-5 * (np.abs(forward * upstream).sum())
+
+
+def test_expert_segments_equal_independent_grids(oracle):
+    rows, entries = oracle.grid_levels(dict(n_levels=4, base_resolution=4, log2_hashmap_size=6,
+                                            per_level_scale=2.0))
+    rng = np.random.default_rng(17)
+    experts, params = 3, entries * 2
+    table = rng.normal(size=experts * params).astype(np.float16)
+    offsets = np.array([0, 50, 50, 120])
+    xy = rng.random((120, 2), dtype=np.float32)
+    out = oracle.hash_forward(xy, table, rows, 2, offsets=offsets, expert_params=params)
+    for e in range(experts):
+        part = oracle.hash_forward(xy[offsets[e]:offsets[e + 1]], table[e * params:(e + 1) * params], rows, 2)
+        assert np.array_equal(out[offsets[e]:offsets[e + 1]].view(np.uint16), part.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------
+# Packed planes: direct layout == dense hash level at integer scale; rank addressing
+# ---------------------------------------------------------------------------------------
+
+def _layout(resolutions, supports, dims, caps):
+    import torch
+    from odie_amd.model import make_layout
+    config = dict(resolutions=resolutions, n_levels=len(resolutions), representation='xy_planes', coarse_levels=0,
+                  gate_topology='shared', gate_position='feature', initial_active_prefix=0)
+    return make_layout(config, [torch.as_tensor(s) for s in supports], dims, caps)
+
+
+def _numpy_layout(layout):
+    return {k: layout[k].numpy() if hasattr(layout[k], 'numpy') else layout[k]
+            for k in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap')}
+
+
+def test_packed_direct_equals_dense_hash_level(oracle):
+    import torch
+    resolutions = [5, 9]
+    supports = [np.ones(r * r, dtype=bool) for r in resolutions]
+    caps = [32, 88]
+    layout = _layout(resolutions, supports, [2, 2], caps)
+    rng = np.random.default_rng(19)
+    grid = rng.normal(0, 0.2, size=layout['params']).astype(np.float32)
+    xy = rng.random((500, 2), dtype=np.float32)
+    out, vis = oracle.packed_forward(xy, grid, _numpy_layout(layout), 4)
+    assert vis.all()
+    rows = [(float(r - 1), r, (r * r + 7) // 8 * 8, o, 0) for r, o in zip(resolutions, [0, 32])]
+    dense = oracle.hash_forward(xy, grid.astype(np.float16), rows, 2)
+    assert np.array_equal(out.view(np.uint16), dense.view(np.uint16))
+
+
+def test_packed_rank_addressing_brute_force(oracle):
+    import torch
+    rng = np.random.default_rng(23)
+    resolutions = [4, 12, 17]
+    supports = [np.ones(16, dtype=bool), rng.random(144) < 0.3, rng.random(289) < 0.15]
+    from odie_amd.model import plane_closure
+    closures = [plane_closure(torch.as_tensor(s), r).numpy() for s, r in zip(supports, resolutions)]
+    caps = [16, (len(closures[1]) + 7) // 8 * 8 + 8, (len(closures[2]) + 7) // 8 * 8]
+    layout = _layout(resolutions, supports, [2, 1, 4], caps)
+    grid = rng.normal(0, 0.2, size=layout['params']).astype(np.float32)
+    xy = rng.random((800, 2), dtype=np.float32)
+    out, vis = oracle.packed_forward(xy, grid, _numpy_layout(layout), 7)
+    # brute force: expand each plane to a dense node table by searchsorted rank
+    offset, dense_rows, dense_tables = 0, [], []
+    for level, (r, nodes, dim) in enumerate(zip(resolutions, closures, [2, 1, 4])):
+        points = (r * r + 7) // 8 * 8
+        plane = np.zeros((points, dim), dtype=np.float32)
+        base = layout['levels'][level]['plane_offset']
+        plane[nodes] = grid[base:base + len(nodes) * dim].reshape(-1, dim)
+        hashed = oracle.hash_forward(xy, plane.astype(np.float16).reshape(-1), [(float(r - 1), r, points, 0, 0)], dim)
+        column = layout['levels'][level]['feature_offset']
+        cells = oracle_cells(xy, r)
+        visible = supports[level][cells]
+        assert np.array_equal(vis[:, level], visible)
+        expected = np.where(visible[:, None], hashed, np.float16(0))
+        assert np.array_equal(out[:, column:column + dim].view(np.uint16), expected.view(np.uint16))
+
+
+def oracle_cells(xy, r):
+    px = np.array([LIBM.fmaf(np.float32(r - 1), x, 0.5) for x in xy[:, 0]])
+    py = np.array([LIBM.fmaf(np.float32(r - 1), y, 0.5) for y in xy[:, 1]])
+    return np.floor(px).astype(np.int64) + np.floor(py).astype(np.int64) * r
+
+
+def test_packed_backward_is_adjoint(oracle):
+    import torch
+    rng = np.random.default_rng(29)
+    resolutions = [6, 11]
+    supports = [np.ones(36, dtype=bool), rng.random(121) < 0.4]
+    from odie_amd.model import plane_closure
+    caps = [40, (len(plane_closure(torch.as_tensor(supports[1]), 11)) + 7) // 8 * 8]
+    layout = _layout(resolutions, supports, [2, 2], caps)
+    grid = rng.normal(size=layout['params']).astype(np.float32).astype(np.float16).astype(np.float32)
+    xy = rng.random((400, 2), dtype=np.float32)
+    upstream = rng.normal(size=(400, 4)).astype(np.float16)
+    grad, _ = oracle.packed_backward(xy, upstream, _numpy_layout(layout), layout['params'])
+    out, _ = oracle.packed_forward(xy, grid, _numpy_layout(layout), 4)
+    left = float((out.astype(np.float64) * upstream.astype(np.float64)).sum())
+    right = float((grid.astype(np.float64) * grad).sum())
+    scale = float(np.abs(out.astype(np.float64) * upstream.astype(np.float64)).sum())
+    assert abs(left - right) <= 2e-3 * scale     # fp16 forward chain rounding
+
+
+# ---------------------------------------------------------------------------------------
+# Residual, thresholds, selection, ranking, compaction, Adam
+# ---------------------------------------------------------------------------------------
+
+def test_native_thresholds_are_exact_boundaries(oracle):
+    for resolution in (2, 3, 8, 13, 128, 2048):
+        thresholds = oracle.native_thresholds(resolution)
+        for region, t in enumerate(thresholds, start=1):
+            below = np.nextafter(np.float32(t), np.float32(0))
+            assert math.floor(LIBM.fmaf(resolution - 1, t, 0.5)) >= region
+            assert math.floor(LIBM.fmaf(resolution - 1, below, 0.5)) < region
+
+
+def test_residual_matches_bincount_restatement(oracle):
+    rng = np.random.default_rng(31)
+    shape, resolution = (37, 53), 8
+    prediction = rng.random((shape[0] * shape[1], 3), dtype=np.float32)
+    target = rng.integers(0, 256, size=(shape[0] * shape[1], 3), dtype=np.uint8)
+    thresholds = oracle.native_thresholds(resolution)
+    xmap = np.searchsorted(thresholds, np.arange(shape[1], dtype=np.float32) / np.float32(shape[1] - 1), side='right')
+    ymap = np.searchsorted(thresholds, np.arange(shape[0], dtype=np.float32) / np.float32(shape[0] - 1), side='right')
+    xb = np.searchsorted(xmap, np.arange(resolution + 1)).astype(np.int32)
+    yb = np.searchsorted(ymap, np.arange(resolution + 1)).astype(np.int32)
+    totals = np.zeros(resolution ** 2)
+    # streamed in uneven chunks, as the reference's residual pass runs
+    for begin, end in ((0, 700), (700, 701), (701, shape[0] * shape[1])):
+        oracle.residual(prediction[begin:end], target[begin:end], shape[1], resolution, xb, yb, begin=begin,
+                        totals=totals)
+    truth = target.astype(np.float32) / np.float32(255.0)
+    squared = (prediction - truth) * (prediction - truth)
+    per_pixel = squared.sum(axis=1, dtype=np.float64) / 3.0
+    cells = oracle.pixel_cells(shape, resolution)
+    expected = np.bincount(cells, weights=per_pixel, minlength=resolution ** 2)
+    assert np.array_equal(totals, expected)
+
+
+def _brute_greedy(scores, resolution, cap):
+    cells, points = resolution ** 2, oracle_align8(resolution ** 2)
+    selected = np.zeros(cells, dtype=bool)
+    nodes = np.zeros(points, dtype=bool)
+    used = 0
+    order = []
+    while True:
+        cost = np.array([sum(not nodes[(c + d) % points] for d in (0, 1, resolution, resolution + 1))
+                         for c in range(cells)])
+        free = [c for c in range(cells) if not selected[c] and cost[c] == 0]
+        if free:
+            cell = min(free)
+        else:
+            best = None
+            for k in range(1, min(4, cap - used) + 1):
+                members = [c for c in range(cells) if not selected[c] and cost[c] == k]
+                if not members:
+                    continue
+                top = max(members, key=lambda c: (scores[c], -c))
+                if best is None:
+                    best = (scores[top], k, top)
+                    continue
+                left, right = scores[top] * best[1], best[0] * k
+                if left > right or (left == right and top < best[2]):
+                    best = (scores[top], k, top)
+            if best is None:
+                break
+            cell = best[2]
+        selected[cell] = True
+        for d in (0, 1, resolution, resolution + 1):
+            if not nodes[(cell + d) % points]:
+                nodes[(cell + d) % points] = True
+                used += 1
+        order.append(cell)
+    return selected, nodes, order
+
+
+def oracle_align8(value):
+    return (value + 7) // 8 * 8
+
+
+@pytest.mark.parametrize('resolution,cap,seed', [(3, 8, 0), (4, 16, 1), (5, 16, 2), (7, 32, 3), (9, 48, 4)])
+def test_b2_greedy_matches_brute_force(oracle, resolution, cap, seed):
+    rng = np.random.default_rng(seed)
+    scores = rng.choice([0.0, 0.25, 0.5, 0.5, 1.0, 3.0], size=resolution ** 2)   # planted ties
+    trace = []
+    selected, nodes, iterations = oracle.select_benefit_cost(scores, resolution, cap, trace=trace)
+    brute_selected, brute_nodes, order = _brute_greedy(scores, resolution, cap)
+    assert np.array_equal(selected, brute_selected) and np.array_equal(nodes, brute_nodes)
+    assert trace == order and iterations == len(order)
+    assert nodes.sum() <= cap
+
+
+def test_b1_mean_rank_respects_cap_and_order(oracle):
+    rng = np.random.default_rng(41)
+    scores = rng.choice([0.0, 1.0, 2.0], size=49)
+    selected, nodes = oracle.select_mean_rank(scores, 7, 24)
+    assert nodes.sum() <= 24
+    closure = oracle.closure_nodes(np.flatnonzero(selected), 7)
+    assert np.array_equal(closure, np.flatnonzero(nodes))
+
+
+def test_topk_and_compaction_against_python_sort(oracle):
+    rng = np.random.default_rng(43)
+    scores = rng.choice([0.5, 1.5, 2.5, 7.0], size=1000)
+    ids = oracle.topk_ids(scores, 37)
+    brute = sorted(sorted(range(1000), key=lambda i: (-scores[i], i))[:37])
+    assert list(ids) == brute
+    expert = rng.integers(0, 9, size=500)
+    perm, offsets = oracle.compact(expert, 9)
+    brute = sorted(range(500), key=lambda i: (expert[i], i))
+    assert list(perm) == brute and offsets[-1] == 500
+
+
+def test_adam_torch_variant_matches_torch(oracle):
+    import torch
+    rng = np.random.default_rng(47)
+    start = rng.normal(size=64)
+    grads = [rng.normal(size=64) * 128 for _ in range(5)]
+    param = torch.nn.Parameter(torch.tensor(start))
+    optimizer = torch.optim.Adam([param], lr=1e-2, betas=(.9, .999), eps=1e-15, foreach=False)
+    p, m, v = start.copy(), np.zeros(64), np.zeros(64)
+    steps = np.zeros(64, dtype=np.uint32)
+    for t, g in enumerate(grads, start=1):
+        param.grad = torch.tensor(g / 128.)
+        optimizer.step()
+        p = oracle.adam(0, p, g, m, v, steps, t, 1e-2, scale=128.)
+    assert np.allclose(p, param.detach().numpy(), rtol=1e-12, atol=1e-15)
+
+
+def test_adam_tcnn_variant_skips_zero_gradients(oracle):
+    p = np.array([1.0, 2.0])
+    m, v, steps = np.zeros(2), np.zeros(2), np.zeros(2, dtype=np.uint32)
+    p = oracle.adam(1, p, np.array([0.5, 0.0]), m, v, steps, 1, 0.1)
+    assert p[1] == 2.0 and steps.tolist() == [1, 0] and m[1] == 0 and v[1] == 0
+    # first step of Adam moves by lr * sign(g) (bias-corrected m/sqrt(v) = 1)
+    assert abs(p[0] - 0.9) < 1e-12
+    p = oracle.adam(1, p, np.array([0.0, 0.5]), m, v, steps, 2, 0.1)
+    assert abs(p[1] - 1.9) < 1e-12 and steps.tolist() == [1, 1]
