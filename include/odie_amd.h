@@ -96,6 +96,30 @@ int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstrea
                          const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
                          int64_t parameter_count, uint64_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Expert routing and compaction.  No counterpart in the reference (its "routing" is a soft
+ * per-level gate); built from its pieces: pixel id -> (id % W, id / W) in 32-bit
+ * arithmetic and the fp32 reciprocal-multiply coordinate convention of the batch kernel
+ * (odie/native/runtime.cu:30-38), and the stable ascending tie order of its rankings
+ * (odie/selection.py:116).
+ *
+ * The W x H image is cut into regions_x x regions_y tiles with bounds
+ * x0[r] = ceil(r*W/regions_x), y0[r] = ceil(r*H/regions_y); pixel (x, y) belongs to expert
+ * ry*regions_x + rx with x0[rx] <= x < x0[rx+1], y0[ry] <= y < y0[ry+1].  Its local
+ * coordinate is u = fp32(x - x0[rx]) * fp32(1/(tile_width-1)), v likewise.
+ * Outputs, in compacted order (grouped by expert, original order inside an expert):
+ *   perm[j]   index of the input id placed at slot j           (int32 [n])
+ *   coords[j] local (u, v) of that id                         (fp32 [n, 2])
+ *   offsets   first slot of every expert, offsets[E] = n       (int32 [E+1])
+ * expert (nullable) receives each input's expert id in input order (int32 [n]).
+ * workspace: caller-owned device scratch of odie_route_workspace(n, E) bytes.
+ * --------------------------------------------------------------------------------------- */
+int64_t odie_route_workspace(int64_t n, int experts);
+
+int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
+               int32_t* expert, int32_t* perm, float* coords, int32_t* offsets,
+               void* workspace, int64_t workspace_bytes, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

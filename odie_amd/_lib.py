@@ -30,6 +30,8 @@ SIGNATURES = {
     'odie_grid_backward': ([_P, _I64, _P, _I, _P, _I, _I, _I64, _P, _I, _I, _P, _I, _U64], _I),
     'odie_packed_forward': ([_P, _I64, _P, _I64, _P, _I, _P, _P, _P, _I, _P, _P, _U64], _I),
     'odie_packed_backward': ([_P, _I64, _P, _I, _P, _I, _P, _P, _P, _P, _I64, _U64], _I),
+    'odie_route_workspace': ([_I64, _I], _I64),
+    'odie_route': ([_P, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _U64], _I),
 }
 
 _handle = None

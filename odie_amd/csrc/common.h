@@ -15,6 +15,8 @@ namespace odie {
 std::string& error_slot();
 int fail(const std::string& message);
 int check_launch(const char* what);
+// Zero `count` floats (or any 4-byte words) with a fill kernel (graph-capturable).
+int launch_fill_zero(float* data, int64_t count, hipStream_t stream);
 
 inline hipStream_t as_stream(uint64_t bits) { return reinterpret_cast<hipStream_t>(bits); }
 
@@ -28,6 +30,15 @@ __device__ inline uint32_t xcd_major(uint32_t block, uint32_t blocks) {
 
 inline uint32_t round_up(uint32_t value, uint32_t multiple) {
     return (value + multiple - 1) / multiple * multiple;
+}
+
+// Materialize an fp32 value before it is converted to fp16.  Without this the compiler
+// folds fptrunc(a*b) into one v_fma_mixlo_f16, which rounds the exact product to fp16 once
+// instead of rounding it to fp32 first and then to fp16 as the reference's
+// __float2half_rn(weight) does (odie/packed_kernels.cu:58).
+__device__ inline float keep_fp32(float value) {
+    asm volatile("" : "+v"(value));
+    return value;
 }
 
 // fp16 <-> 16-bit patterns without relying on __half's class layout.

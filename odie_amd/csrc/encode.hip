@@ -130,7 +130,7 @@ __device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, in
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const __half2* src = reinterpret_cast<const __half2*>(t + static_cast<size_t>(idx[k]) * F);
-                    const __half2 wk = __float2half2_rn(w[k]);
+                    const __half2 wk = __float2half2_rn(keep_fp32(w[k]));
 #pragma unroll
                     for (int c = 0; c < F / 2; ++c) acc[c] = __hfma2(wk, src[c], acc[c]);
                 }
@@ -142,7 +142,7 @@ __device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, in
             } else if constexpr (HALF) {
                 __half acc = __float2half(0.0f);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) acc = __hfma(__float2half_rn(w[k]), t[idx[k]], acc);
+                for (int k = 0; k < 4; ++k) acc = __hfma(__float2half_rn(keep_fp32(w[k])), t[idx[k]], acc);
                 vals[l] = acc;
             } else {
                 float acc[F];
@@ -445,7 +445,8 @@ __global__ __launch_bounds__(kBlock) void packed_forward_kernel(PackedArgs a) {
                 if (on) {
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        v = __hfma(__float2half_rn(w[k]), __float2half_rn(a.grid[plane_param(a, d, cell, k, c)]), v);
+                        v = __hfma(__float2half_rn(keep_fp32(w[k])),
+                                   __float2half_rn(a.grid[plane_param(a, d, cell, k, c)]), v);
                 }
                 row[d[6] + c] = half_to_bits(v);
             }

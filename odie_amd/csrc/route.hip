@@ -1,0 +1,262 @@
+// Expert routing and compaction for gfx950.
+//
+// A pixel id is split into (x, y) = (id % W, id / W) with 32-bit arithmetic, as the
+// reference's batch kernel does (odie/native/runtime.cu:33-36).  The image is cut into a
+// regions_x x regions_y grid of tiles with integer bounds x0[r] = ceil(r*W/regions_x) (and
+// the same for y); expert = ry*regions_x + rx.  Each expert fits its tile as a sub-image,
+// so the coordinate it sees is the reference's pixel -> coordinate convention applied to
+// the tile: u = fp32(x - x0[rx]) * fp32(1/(tile_width-1)) (fp32 product of the fp32
+// reciprocal of the exact double quotient, runtime.cu:35-36), same for v.
+//
+// Compaction is a stable counting sort by expert: coordinates end up grouped by expert,
+// in their original order inside each expert (numpy argsort(kind='stable') order, the tie
+// rule the reference uses for rankings, odie/selection.py:116).
+//   pass 1  each wave counts the experts of its own sub-chunk (LDS histogram per wave)
+//   pass 2  one workgroup scans the counts, expert-major then sub-chunk order
+//   pass 3  each wave walks its sub-chunk 64 ids at a time; lanes sharing an expert get
+//           their order from a ballot over the wave (peel loop, one iteration per distinct
+//           expert in the group), and a per-wave running count in LDS carries the order
+//           across groups.  No global atomics, so the result is deterministic.
+#include "common.h"
+#include "../../include/odie_amd.h"
+
+namespace odie {
+namespace {
+
+constexpr int kRouteBlock = 256;
+constexpr int kWaves = kRouteBlock / 64;
+constexpr int kMaxRegions = 64;
+constexpr int kMaxExperts = kMaxRegions * kMaxRegions;
+constexpr int kScanBlock = 1024;
+
+struct RouteArgs {
+    const int64_t* ids;
+    int32_t* expert_out;
+    int32_t* perm;
+    float* coords;
+    int32_t* offsets;
+    int32_t* counts;   // [experts * parts]
+    int64_t n;
+    uint32_t width;
+    uint32_t height;
+    int regions_x;
+    int regions_y;
+    int experts;
+    int part;          // ids per wave sub-chunk (multiple of 64)
+    int parts;         // number of sub-chunks
+    int32_t x0[kMaxRegions + 1];
+    int32_t y0[kMaxRegions + 1];
+    float rx[kMaxRegions];   // fp32(1/(tile_width-1))
+    float ry[kMaxRegions];
+};
+
+struct Bounds {
+    int32_t x0[kMaxRegions + 1];
+    int32_t y0[kMaxRegions + 1];
+};
+
+__device__ inline int region_of(const int32_t* bounds, int regions, uint32_t v) {
+    // largest r with bounds[r] <= v
+    int lo = 0, hi = regions - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (static_cast<uint32_t>(bounds[mid]) <= v) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+__device__ inline void locate(const RouteArgs& a, const Bounds& b, int64_t i, int& expert, uint32_t& x, uint32_t& y,
+                              int& rx, int& ry) {
+    const uint32_t id = static_cast<uint32_t>(a.ids[i]);
+    x = id % a.width;
+    y = id / a.width;
+    if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
+    rx = region_of(b.x0, a.regions_x, x);
+    ry = region_of(b.y0, a.regions_y, y);
+    expert = ry * a.regions_x + rx;
+}
+
+__device__ inline void load_bounds(const RouteArgs& a, Bounds& b) {
+    for (int j = threadIdx.x; j <= kMaxRegions; j += blockDim.x) {
+        b.x0[j] = a.x0[j];
+        b.y0[j] = a.y0[j];
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
+    extern __shared__ int32_t hist[];  // [kWaves][experts]
+    __shared__ Bounds bounds;
+    load_bounds(a, bounds);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int part = blockIdx.x * kWaves + wave;
+    int32_t* mine = hist + wave * a.experts;
+    for (int e = lane; e < a.experts; e += 64) mine[e] = 0;
+    __syncthreads();
+    if (part < a.parts) {
+        const int64_t begin = static_cast<int64_t>(part) * a.part;
+        const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
+        for (int64_t i = begin + lane; i < end; i += 64) {
+            int expert, rx, ry;
+            uint32_t x, y;
+            locate(a, bounds, i, expert, x, y, rx, ry);
+            atomicAdd(mine + expert, 1);
+        }
+    }
+    __syncthreads();
+    if (part < a.parts)
+        for (int e = lane; e < a.experts; e += 64) a.counts[static_cast<int64_t>(e) * a.parts + part] = mine[e];
+}
+
+// Exclusive scan of counts (expert-major) in place; offsets[e] = first slot of expert e.
+__global__ __launch_bounds__(kScanBlock) void route_scan_kernel(RouteArgs a) {
+    __shared__ int64_t sums[kScanBlock];
+    const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
+    const int64_t per = (total + kScanBlock - 1) / kScanBlock;
+    const int64_t begin = threadIdx.x * per;
+    const int64_t end = begin + per < total ? begin + per : total;
+    int64_t local = 0;
+    for (int64_t j = begin; j < end; ++j) local += a.counts[j];
+    sums[threadIdx.x] = local;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over the 1024 partial sums
+    for (int stride = 1; stride < kScanBlock; stride <<= 1) {
+        const int64_t add = threadIdx.x >= stride ? sums[threadIdx.x - stride] : 0;
+        __syncthreads();
+        sums[threadIdx.x] += add;
+        __syncthreads();
+    }
+    int64_t running = sums[threadIdx.x] - local;
+    for (int64_t j = begin; j < end; ++j) {
+        const int32_t count = a.counts[j];
+        a.counts[j] = static_cast<int32_t>(running);
+        if (j % a.parts == 0) a.offsets[j / a.parts] = static_cast<int32_t>(running);
+        running += count;
+    }
+    if (threadIdx.x == 0) a.offsets[a.experts] = static_cast<int32_t>(a.n);
+}
+
+__global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a) {
+    extern __shared__ int32_t running[];  // [kWaves][experts]
+    __shared__ Bounds bounds;
+    load_bounds(a, bounds);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int part = blockIdx.x * kWaves + wave;
+    int32_t* mine = running + wave * a.experts;
+    for (int e = lane; e < a.experts; e += 64) mine[e] = 0;
+    __syncthreads();
+    if (part >= a.parts) return;
+    const int64_t begin = static_cast<int64_t>(part) * a.part;
+    const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    for (int64_t group = begin; group < end; group += 64) {
+        const int64_t i = group + lane;
+        const bool valid = i < end;
+        int expert = -1, rx = 0, ry = 0;
+        uint32_t x = 0, y = 0;
+        if (valid) locate(a, bounds, i, expert, x, y, rx, ry);
+        // Peel loop: one iteration per distinct expert among the valid lanes.
+        uint64_t pending = __ballot(valid);
+        int rank = 0;
+        int32_t base = 0;
+        while (pending) {
+            const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+            const int key = __shfl(expert, leader);
+            const uint64_t same = __ballot(valid && expert == key);
+            int32_t start = 0;
+            if (lane == leader) {
+                start = mine[key];
+                mine[key] = start + __popcll(same);
+            }
+            start = __shfl(start, leader);
+            if (valid && expert == key) {
+                rank = __popcll(same & below);
+                base = start;
+            }
+            pending &= ~same;
+        }
+        if (valid) {
+            const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.parts + part]) + base + rank;
+            a.perm[slot] = static_cast<int32_t>(i);
+            const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
+            const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
+            reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
+            if (a.expert_out) a.expert_out[i] = expert;
+        }
+    }
+}
+
+int route_plan(int64_t n, int experts, int& part, int& parts) {
+    // Sub-chunks of at least 1024 ids, few enough that experts*parts stays <= 2^20.
+    int64_t p = 1024;
+    while ((n + p - 1) / p * experts > (int64_t{1} << 20)) p *= 2;
+    part = static_cast<int>(p);
+    parts = static_cast<int>((n + p - 1) / p);
+    if (parts < 1) parts = 1;
+    return 0;
+}
+
+}  // namespace
+}  // namespace odie
+
+using namespace odie;
+
+ODIE_API int64_t odie_route_workspace(int64_t n, int experts) {
+    if (n < 0 || experts < 1) return -1;
+    int part, parts;
+    route_plan(n, experts, part, parts);
+    return static_cast<int64_t>(experts) * parts * 4;
+}
+
+ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
+                        int32_t* expert, int32_t* perm, float* coords, int32_t* offsets,
+                        void* workspace, int64_t workspace_bytes, uint64_t stream) {
+    if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_route: n must be within [0, 2^31-1]");
+    if (regions_x < 1 || regions_y < 1 || regions_x > kMaxRegions || regions_y > kMaxRegions)
+        return fail("odie_route: regions per axis must be within 1..64");
+    if (width < 2 * regions_x || height < 2 * regions_y)
+        return fail("odie_route: every tile needs at least two pixels per axis");
+    if (static_cast<uint64_t>(width) * static_cast<uint64_t>(height) > (uint64_t{1} << 32))
+        return fail("odie_route: images are limited to 2^32 pixels (32-bit pixel ids)");
+    const int experts = regions_x * regions_y;
+    if (!offsets) return fail("odie_route: offsets is null");
+    const int64_t need = odie_route_workspace(n, experts);
+    if (n > 0 && (!ids || !perm || !coords)) return fail("odie_route: ids, perm and coords must be non-null");
+    if (n > 0 && (!workspace || workspace_bytes < need))
+        return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_route: coords must be 8-byte aligned");
+    RouteArgs a{};
+    a.ids = ids;
+    a.expert_out = expert;
+    a.perm = perm;
+    a.coords = coords;
+    a.offsets = offsets;
+    a.counts = static_cast<int32_t*>(workspace);
+    a.n = n;
+    a.width = static_cast<uint32_t>(width);
+    a.height = static_cast<uint32_t>(height);
+    a.regions_x = regions_x;
+    a.regions_y = regions_y;
+    a.experts = experts;
+    route_plan(n, experts, a.part, a.parts);
+    for (int r = 0; r <= kMaxRegions; ++r) {
+        const int rxx = r < regions_x ? r : regions_x, ryy = r < regions_y ? r : regions_y;
+        a.x0[r] = static_cast<int32_t>((static_cast<int64_t>(rxx) * width + regions_x - 1) / regions_x);
+        a.y0[r] = static_cast<int32_t>((static_cast<int64_t>(ryy) * height + regions_y - 1) / regions_y);
+    }
+    for (int r = 0; r < kMaxRegions; ++r) {
+        const int tw = r < regions_x ? a.x0[r + 1] - a.x0[r] : 2;
+        const int th = r < regions_y ? a.y0[r + 1] - a.y0[r] : 2;
+        a.rx[r] = static_cast<float>(1.0 / static_cast<double>(tw - 1));
+        a.ry[r] = static_cast<float>(1.0 / static_cast<double>(th - 1));
+    }
+    const hipStream_t s = as_stream(stream);
+    const size_t shmem = static_cast<size_t>(kWaves) * experts * 4;
+    if (shmem + sizeof(Bounds) > 64 * 1024) return fail("odie_route: too many experts for the LDS histogram");
+    const uint32_t blocks = static_cast<uint32_t>((a.parts + kWaves - 1) / kWaves);
+    if (n == 0) return launch_fill_zero(reinterpret_cast<float*>(offsets), experts + 1, s);
+    route_count_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
+    route_scan_kernel<<<1, kScanBlock, 0, s>>>(a);
+    route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
+    return check_launch("odie_route");
+}

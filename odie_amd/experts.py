@@ -1,0 +1,71 @@
+"""Packed multi-expert hash grid: routing of pixel ids to tile experts, compaction, and
+the encode over every expert's table in one launch.
+
+Each expert owns a full multiresolution hash-grid table and fits one tile of the image as
+a sub-image; routing and compaction run on the GPU (odie_route), the encode reads the
+compacted coordinates with per-expert offsets (odie_grid_forward/backward).
+"""
+import torch
+
+from . import _lib
+from .config import grid_levels
+from .encoding import grid_backward, grid_forward
+
+
+def tile_bounds(size, regions):
+    """Integer tile starts ceil(r*size/regions), r = 0..regions."""
+    return [(r * size + regions - 1) // regions for r in range(regions + 1)]
+
+
+class Routing:
+    """Device buffers of one routed batch: perm, local coords, offsets (and optional
+    per-input expert ids)."""
+
+    def __init__(self, perm, coords, offsets, expert):
+        self.perm, self.coords, self.offsets, self.expert = perm, coords, offsets, expert
+
+
+def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None):
+    """Route int64 pixel ids [N] (CUDA) to regions_x*regions_y tile experts and compact."""
+    if ids.dtype != torch.int64 or ids.ndim != 1 or not ids.is_cuda:
+        raise ValueError('ids must be a CUDA int64 [N] tensor')
+    ids = ids.contiguous()
+    n, experts = ids.numel(), regions_x * regions_y
+    lib = _lib.library()
+    need = lib.odie_route_workspace(n, experts)
+    if need < 0:
+        raise ValueError('invalid routing size')
+    device = ids.device
+    if out is None:
+        out = Routing(torch.empty(n, dtype=torch.int32, device=device),
+                      torch.empty((n, 2), dtype=torch.float32, device=device),
+                      torch.empty(experts + 1, dtype=torch.int32, device=device),
+                      torch.empty(n, dtype=torch.int32, device=device) if with_expert else None)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
+    _lib.check(lib.odie_route(ids.data_ptr(), n, width, height, regions_x, regions_y, _lib.ptr(out.expert),
+                              out.perm.data_ptr(), out.coords.data_ptr(), out.offsets.data_ptr(),
+                              workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                              _lib.stream_of(ids)))
+    return out
+
+
+class ExpertGrid:
+    """experts independent hash grids packed in one table of experts*expert_params values."""
+
+    def __init__(self, encoding, experts, dtype=torch.float16, device='cuda'):
+        self.encoding = dict(encoding)
+        self.features = int(encoding['n_features_per_level'])
+        self.levels, entries = grid_levels(encoding)
+        self.experts = experts
+        self.expert_params = entries * self.features
+        self.width = len(self.levels) * self.features
+        self.table = torch.zeros(experts * self.expert_params, dtype=dtype, device=device)
+
+    def forward(self, coords, offsets, out=None):
+        return grid_forward(coords, self.table, self.levels, self.features, offsets=offsets,
+                            experts=self.experts, expert_params=self.expert_params, width=self.width, out=out)
+
+    def backward(self, coords, offsets, upstream, gradient=None, accumulate=False):
+        return grid_backward(coords, upstream, self.levels, self.features, offsets=offsets, experts=self.experts,
+                             expert_params=self.expert_params, gradient=gradient, accumulate=accumulate)

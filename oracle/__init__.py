@@ -386,3 +386,22 @@ def adam(variant, param, grad, m, v, steps, step, lr, beta1=0.9, beta2=0.999, ep
     lib().ora_adam(int(variant), _p(param), _p(grad), _p(m), _p(v), _p(steps), param.size, int(step),
                    lr, beta1, beta2, eps, scale)
     return param
+
+
+def route(ids, width, height, regions_x, regions_y):
+    """Routing spec restated with integer division: expert = (y*RY//H)*RX + x*RX//W, local
+    coordinate fp32(x - x0) * fp32(1/(tile-1)); returns (expert, perm, local_xy, offsets)
+    with perm the stable ascending-expert order."""
+    ids = np.asarray(ids, dtype=np.int64).astype(np.uint32).astype(np.int64)
+    x, y = ids % width, np.minimum(ids // width, height - 1)
+    rx, ry = x * regions_x // width, y * regions_y // height
+    expert = ry * regions_x + rx
+    x0 = -((-rx * width) // regions_x)
+    y0 = -((-ry * height) // regions_y)
+    x1 = -((-(rx + 1) * width) // regions_x)
+    y1 = -((-(ry + 1) * height) // regions_y)
+    u = (x - x0).astype(np.float32) * (1.0 / (x1 - x0 - 1).astype(np.float64)).astype(np.float32)
+    v = (y - y0).astype(np.float32) * (1.0 / (y1 - y0 - 1).astype(np.float64)).astype(np.float32)
+    perm, offsets = compact(expert, regions_x * regions_y)
+    local = np.stack([u, v], axis=1).astype(np.float32)[perm]
+    return expert.astype(np.int32), perm, local, offsets

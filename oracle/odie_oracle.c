@@ -98,6 +98,52 @@ API uint16_t ora_hfma(uint16_t a, uint16_t b, uint16_t c) {
     return sign | (uint16_t)(((E + 15) << 10) | ((int)q - 1024));
 }
 
+/* Fast forms used inside the encode loops.  h2f_fast/d2h_fast are bit-level conversions
+ * (same results as ora_h2f/ora_d2h); hfma_fast forms a*b + c in double, which is exact
+ * unless the TwoSum error term is nonzero, and falls back to the exact integer path
+ * otherwise -- so it returns ora_hfma's result for every input. */
+static inline float h2f_fast(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    if (e == 0) { const float v = (float)m * 0x1p-24f; return sign ? -v : v; }
+    uint32_t bits = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+    float v;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+
+static inline uint16_t d2h_fast(double d) {
+    uint64_t b;
+    memcpy(&b, &d, 8);
+    const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    const uint64_t a = b & 0x7fffffffffffffffull;
+    if (a >= 0x7ff0000000000000ull) return a > 0x7ff0000000000000ull ? 0x7e00u : (uint16_t)(sign | 0x7c00u);
+    int e = (int)(a >> 52) - 1023;
+    if (e >= 16) return sign | 0x7c00u;
+    if (e < -25) return sign;
+    const uint64_t m = (a & 0xfffffffffffffull) | (1ull << 52);
+    const int shift = (e >= -14 ? e - 10 : -24) - (e - 52);
+    uint64_t kept = m >> shift;
+    const uint64_t rem = m & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (kept & 1))) ++kept;
+    if (e >= -14) {
+        if (kept == 2048) { kept = 1024; ++e; }
+        if (e > 15) return sign | 0x7c00u;
+        return (uint16_t)(sign | ((e + 15) << 10) | (kept - 1024));
+    }
+    return (uint16_t)(sign | kept);
+}
+
+static inline uint16_t hfma_fast(uint16_t a, uint16_t b, uint16_t c) {
+    const double p = (double)h2f_fast(a) * (double)h2f_fast(b), q = (double)h2f_fast(c);
+    const double s = p + q, v = s - p;
+    const double err = (p - (s - v)) + (q - v);
+    if (err != 0.0 || s == 0.0 || !isfinite(s)) return ora_hfma(a, b, c);
+    return d2h_fast(s);
+}
+
+API uint16_t ora_hfma_fast(uint16_t a, uint16_t b, uint16_t c) { return hfma_fast(a, b, c); }
+API uint16_t ora_d2h_fast(double d) { return d2h_fast(d); }
+
 /* ------------------------------------------------------------------------------
  * Multiresolution hash grid (tiny-cuda-nn GridEncoding semantics, 2D).
  *
@@ -120,6 +166,10 @@ typedef struct {
 
 static inline uint32_t hash_index(const ora_level* lv, uint32_t gx, uint32_t gy) {
     uint32_t index = lv->hashed ? (gx ^ (gy * 2654435761u)) : (gx + gy * lv->res);
+    /* index mod size; the two shortcuts return the same value as the division */
+    if ((lv->size & (lv->size - 1)) == 0) return index & (lv->size - 1);
+    if (index < lv->size) return index;
+    if (index - lv->size < lv->size) return index - lv->size;
     return index % lv->size;
 }
 
@@ -176,7 +226,7 @@ API void ora_hash_forward(const float* xy, const int64_t* offsets, int experts, 
                     const uint16_t* t = (const uint16_t*)table;
                     uint16_t v = 0;
                     for (int k = 0; k < 4; ++k)
-                        v = ora_hfma(ora_f2h(w[k]), t[base + ((int64_t)lv->offset + idx[k]) * features + c], v);
+                        v = hfma_fast(d2h_fast((double)w[k]), t[base + ((int64_t)lv->offset + idx[k]) * features + c], v);
                     ((uint16_t*)out)[i * width + l * features + c] = v;
                 }
             }
@@ -202,7 +252,7 @@ API void ora_hash_backward(const float* xy, const int64_t* offsets, int experts,
             hash_geometry(lv, xy[2 * i], xy[2 * i + 1], idx, w);
             for (int c = 0; c < features; ++c) {
                 const int64_t col = i * width + l * features + c;
-                const float value = up_dtype ? ora_h2f(((const uint16_t*)upstream)[col]) : ((const float*)upstream)[col];
+                const float value = up_dtype ? h2f_fast(((const uint16_t*)upstream)[col]) : ((const float*)upstream)[col];
                 if (value == 0.0f) continue;
                 for (int k = 0; k < 4; ++k) {
                     const float add = w[k] * value;                     /* fp32 product */
@@ -233,7 +283,7 @@ API void ora_hash_backward_f32(const float* xy, const int64_t* offsets, int expe
             const ora_level* lv = levels + l;
             hash_geometry(lv, xy[2 * i], xy[2 * i + 1], idx, w);
             for (int c = 0; c < features; ++c) {
-                const float value = ora_h2f(upstream[i * width + l * features + c]);
+                const float value = h2f_fast(upstream[i * width + l * features + c]);
                 if (value == 0.0f) continue;
                 for (int k = 0; k < 4; ++k) {
                     const float add = w[k] * value;
@@ -299,7 +349,7 @@ API void ora_packed_forward(const float* xy, int64_t n, const float* grid, const
                     for (int k = 0; k < 4; ++k) {
                         const int node = (cell + (k & 1) + (k >> 1) * d[0]) % d[1];
                         const int row = plane_row(node_bitmap, prefix, d, node);
-                        v = ora_hfma(ora_f2h(w[k]), ora_f2h(grid[d[2] + (int64_t)row * d[5] + c]), v);
+                        v = hfma_fast(d2h_fast((double)w[k]), d2h_fast((double)grid[d[2] + (int64_t)row * d[5] + c]), v);
                     }
                 }
                 features[i * width + d[6] + c] = v;
@@ -319,7 +369,7 @@ API void ora_packed_backward(const float* xy, int64_t n, const uint16_t* upstrea
             plane_geometry(xy[2 * i], xy[2 * i + 1], d[0], &cell, w);
             if (!plane_visible(bitmap, d, cell)) continue;
             for (int c = 0; c < d[5]; ++c) {
-                const float value = ora_h2f(upstream[i * width + d[6] + c]);
+                const float value = h2f_fast(upstream[i * width + d[6] + c]);
                 if (value == 0.0f) continue;
                 for (int k = 0; k < 4; ++k) {
                     const int node = (cell + (k & 1) + (k >> 1) * d[0]) % d[1];

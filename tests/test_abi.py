@@ -75,3 +75,13 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, '_handle', None)
     with pytest.raises(_lib.NativeError, match='no CPU fallback'):
         _lib.library()
+
+
+def test_route_rejects_bad_arguments(native):
+    assert native.odie_route(8, 16, 2048, 1365, 65, 8, None, 8, 8, 8, 8, 1 << 20, 0) == -1
+    assert 'regions per axis' in native.odie_error().decode()
+    assert native.odie_route(8, 16, 10, 10, 8, 8, None, 8, 8, 8, 8, 1 << 20, 0) == -1
+    assert 'two pixels' in native.odie_error().decode()
+    assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, 8, 4, 0) == -1
+    assert 'workspace' in native.odie_error().decode()
+    assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4
