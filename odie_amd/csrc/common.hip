@@ -1,4 +1,7 @@
 // Thread-local error slot shared by every C-ABI entry point, plus odie_error/odie_copy.
+#include <map>
+#include <mutex>
+
 #include "common.h"
 #include "../../include/odie_amd.h"
 
@@ -18,6 +21,37 @@ int check_launch(const char* what) {
     const hipError_t status = hipGetLastError();
     if (status != hipSuccess) return fail(std::string(what) + ": " + hipGetErrorString(status));
     return 0;
+}
+
+void* workspace(size_t bytes, hipStream_t stream) {
+    static std::mutex lock;
+    static std::map<int, std::pair<void*, size_t>> buffers;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        fail("workspace: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(lock);
+    auto& slot = buffers[device];
+    if (slot.first && slot.second >= bytes) return slot.first;
+    if (slot.first) {
+        (void)stream;
+        if (hipDeviceSynchronize() != hipSuccess || hipFree(slot.first) != hipSuccess) {
+            fail("workspace: could not release the previous buffer");
+            return nullptr;
+        }
+        slot = {nullptr, 0};
+    }
+    size_t size = bytes + bytes / 4;
+    size = (size + (size_t{2} << 20) - 1) / (size_t{2} << 20) * (size_t{2} << 20);
+    void* pointer = nullptr;
+    const hipError_t status = hipMalloc(&pointer, size);
+    if (status != hipSuccess) {
+        fail(std::string("workspace: hipMalloc failed: ") + hipGetErrorString(status));
+        return nullptr;
+    }
+    slot = {pointer, size};
+    return pointer;
 }
 
 }  // namespace odie

@@ -8,24 +8,13 @@
 // -- stay on one XCD and its L2.  The backward accumulates the coarse levels of the
 // chunk's expert in LDS (ds_add_f32) and flushes them once per chunk with global fp32
 // atomics; finer levels go straight to global_atomic_add_f32.
-#include <type_traits>
-
-#include "common.h"
+#include "grid.h"
 #include "../../include/odie_amd.h"
 
 namespace odie {
 namespace {
 
 constexpr int kBlock = 256;
-
-struct DevLevel {
-    float scale;
-    uint32_t res;
-    uint32_t size;
-    uint32_t mask;    // size - 1 when size is a power of two, else 0
-    uint32_t offset;  // first entry of the level
-    uint32_t hashed;
-};
 
 struct GridArgs {
     const float* coords;
@@ -53,38 +42,12 @@ struct Tuning {
     int backward_chunk = 8192;
     int lds_bytes = 65536;
     int xcd_remap = 1;
+    int backward_mode = 1;          // 0: LDS + global fp32 atomics, 1: owner computes
+    int owner_lds_bytes = 162816;   // 160 KiB minus static LDS
 };
 Tuning& tuning() {
     static Tuning t;
     return t;
-}
-
-__device__ inline uint32_t wrap_index(uint32_t v, const DevLevel& lv) {
-    if (lv.mask) return v & lv.mask;
-    if (v < lv.size) return v;
-    v -= lv.size;
-    return v < lv.size ? v : v % lv.size;
-}
-
-// tiny-cuda-nn grid geometry: p = fma(scale, x, 0.5), corner = floor(p), fraction p - floor(p);
-// corners (0,0),(1,0),(0,1),(1,1); dense index x + y*res, hashed x ^ y*2654435761, mod size.
-__device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32_t idx[4], float w[4]) {
-    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
-    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
-    const float flx = floorf(px), fly = floorf(py);
-    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
-    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
-    const float fx = px - flx, fy = py - fly;
-    w[0] = (1.0f - fx) * (1.0f - fy);
-    w[1] = fx * (1.0f - fy);
-    w[2] = (1.0f - fx) * fy;
-    w[3] = fx * fy;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t cx = gx + static_cast<uint32_t>(k & 1), cy = gy + static_cast<uint32_t>(k >> 1);
-        const uint32_t raw = lv.hashed ? (cx ^ (cy * 2654435761u)) : (cx + cy * lv.res);
-        idx[k] = wrap_index(raw, lv);
-    }
 }
 
 // Largest expert e with offsets[e] <= i, clamped to a valid expert.
@@ -106,9 +69,6 @@ __device__ inline int64_t segment_end(const GridArgs& a, int e, int64_t i, int64
     if (stop <= i) stop = end;  // malformed offsets: finish the chunk as this expert
     return stop;
 }
-
-template <bool HALF>
-using Elem = typename std::conditional<HALF, __half, float>::type;
 
 template <int F, bool HALF, int LMAX>
 __device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, int64_t i) {
@@ -499,6 +459,8 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "backward_chunk" && value >= kBlock && value % kBlock == 0) t.backward_chunk = value;
     else if (key == "lds_bytes" && value >= 0 && value <= 160 * 1024) t.lds_bytes = value;
     else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
+    else if (key == "backward_mode" && (value == 0 || value == 1)) t.backward_mode = value;
+    else if (key == "owner_lds_bytes" && value >= 4096 && value <= 162816) t.owner_lds_bytes = value;
     else return fail("odie_set_tuning: unknown key or value out of range: " + key);
     return 0;
 }
@@ -547,11 +509,38 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_backward: coords must be 8-byte aligned");
     const hipStream_t s = as_stream(stream);
     const int64_t total = expert_params * experts;
+    const Tuning& t = tuning();
+    if (static_cast<int64_t>(a.level[n_levels - 1].offset + a.level[n_levels - 1].size) * features >= (int64_t{1} << 31))
+        return fail("odie_grid_backward: one table must hold fewer than 2^31 values");
+    if (n == 0) return zero_first ? launch_fill_zero(gradient, total, s) : 0;
+    if (t.backward_mode == 1) {
+        if (expert_params != static_cast<int64_t>(a.level[n_levels - 1].offset + a.level[n_levels - 1].size) * features) {
+            // values past the levels' tables are not owned by any slice: clear them up front
+            if (zero_first && launch_fill_zero(gradient, total, s)) return -1;
+            zero_first = 0;
+        }
+        OwnerLaunch o{};
+        o.coords = coords;
+        o.offsets = a.offsets;
+        o.upstream = upstream;
+        o.up_half = up_dtype == ODIE_F16;
+        o.up_width = up_width;
+        o.grad = gradient;
+        o.accumulate = zero_first ? 0 : 1;
+        o.n = n;
+        o.expert_params = expert_params;
+        o.experts = experts;
+        o.n_levels = n_levels;
+        o.features = features;
+        o.levels = a.level;
+        o.lds_bytes = t.owner_lds_bytes;
+        o.remap = t.xcd_remap;
+        o.stream = s;
+        return launch_owner_backward(o);
+    }
     if (zero_first && launch_fill_zero(gradient, total, s)) return -1;
-    if (n == 0) return 0;
     const bool half = up_dtype == ODIE_F16;
     const size_t elem = half ? 2 : 4;
-    const Tuning& t = tuning();
     a.upstream = upstream;
     a.grad = gradient;
     a.width = up_width;

@@ -1,0 +1,73 @@
+// Device helpers shared by the grid encode kernels: level descriptors and the
+// tiny-cuda-nn grid geometry (corner indices and bilinear weights).
+#pragma once
+#include <type_traits>
+
+#include "common.h"
+#include "../../include/odie_amd.h"
+
+namespace odie {
+
+struct DevLevel {
+    float scale;
+    uint32_t res;
+    uint32_t size;
+    uint32_t mask;    // size - 1 when size is a power of two, else 0
+    uint32_t offset;  // first entry of the level
+    uint32_t hashed;
+};
+
+__device__ inline uint32_t wrap_index(uint32_t v, const DevLevel& lv) {
+    if (lv.mask) return v & lv.mask;
+    if (v < lv.size) return v;
+    v -= lv.size;
+    return v < lv.size ? v : v % lv.size;
+}
+
+// tiny-cuda-nn grid geometry: p = fma(scale, x, 0.5), corner = floor(p), fraction p - floor(p);
+// corners (0,0),(1,0),(0,1),(1,1); dense index x + y*res, hashed x ^ y*2654435761, mod size.
+__device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32_t idx[4], float w[4]) {
+    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
+    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
+    const float flx = floorf(px), fly = floorf(py);
+    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
+    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
+    const float fx = px - flx, fy = py - fly;
+    w[0] = (1.0f - fx) * (1.0f - fy);
+    w[1] = fx * (1.0f - fy);
+    w[2] = (1.0f - fx) * fy;
+    w[3] = fx * fy;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t cx = gx + static_cast<uint32_t>(k & 1), cy = gy + static_cast<uint32_t>(k >> 1);
+        const uint32_t raw = lv.hashed ? (cx ^ (cy * 2654435761u)) : (cx + cy * lv.res);
+        idx[k] = wrap_index(raw, lv);
+    }
+}
+
+template <bool HALF>
+using Elem = typename std::conditional<HALF, __half, float>::type;
+
+// Host-side description of one owner-computes backward launch (backward.hip).
+struct OwnerLaunch {
+    const float* coords;
+    const int32_t* offsets;   // null for a single grid
+    const void* upstream;     // [n, up_width] row-major
+    int up_half;
+    int up_width;
+    float* grad;
+    int accumulate;
+    int64_t n;
+    int64_t expert_params;
+    int experts;
+    int n_levels;
+    int features;
+    const DevLevel* levels;   // host array [n_levels]
+    int64_t lds_bytes;
+    int remap;
+    hipStream_t stream;
+};
+int launch_owner_backward(const OwnerLaunch& launch);
+
+
+}  // namespace odie

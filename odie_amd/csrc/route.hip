@@ -27,7 +27,6 @@ constexpr int kRouteBlock = 256;
 constexpr int kWaves = kRouteBlock / 64;
 constexpr int kMaxRegions = 64;
 constexpr int kMaxExperts = kMaxRegions * kMaxRegions;
-constexpr int kScanBlock = 1024;
 
 struct RouteArgs {
     const int64_t* ids;
@@ -36,6 +35,7 @@ struct RouteArgs {
     float* coords;
     int32_t* offsets;
     int32_t* counts;   // [experts * parts]
+    int32_t* block_sums;  // [ceil(experts * parts / kScanSegment)]
     int64_t n;
     uint32_t width;
     uint32_t height;
@@ -108,32 +108,82 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
         for (int e = lane; e < a.experts; e += 64) a.counts[static_cast<int64_t>(e) * a.parts + part] = mine[e];
 }
 
-// Exclusive scan of counts (expert-major) in place; offsets[e] = first slot of expert e.
-__global__ __launch_bounds__(kScanBlock) void route_scan_kernel(RouteArgs a) {
-    __shared__ int64_t sums[kScanBlock];
-    const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
-    const int64_t per = (total + kScanBlock - 1) / kScanBlock;
-    const int64_t begin = threadIdx.x * per;
-    const int64_t end = begin + per < total ? begin + per : total;
-    int64_t local = 0;
-    for (int64_t j = begin; j < end; ++j) local += a.counts[j];
-    sums[threadIdx.x] = local;
+// Exclusive scan of counts (expert-major) in place, in three launches: every block sums a
+// segment of kScanSegment counts, one block scans those sums, every block rescans its
+// segment from its offset.  offsets[e] = first slot of expert e; offsets[E] = n.
+constexpr int kScanBlock = 256;
+constexpr int kScanSegment = 1024;  // counts per scan block (4 per thread)
+
+__device__ inline int32_t block_exclusive_scan(int32_t value, int32_t* shared, int32_t& total) {
+    // Inclusive scan of one value per thread over the block (kScanBlock threads) in LDS.
+    shared[threadIdx.x] = value;
     __syncthreads();
-    // Hillis-Steele inclusive scan over the 1024 partial sums
     for (int stride = 1; stride < kScanBlock; stride <<= 1) {
-        const int64_t add = threadIdx.x >= stride ? sums[threadIdx.x - stride] : 0;
+        const int32_t add = threadIdx.x >= stride ? shared[threadIdx.x - stride] : 0;
         __syncthreads();
-        sums[threadIdx.x] += add;
+        shared[threadIdx.x] += add;
         __syncthreads();
     }
-    int64_t running = sums[threadIdx.x] - local;
-    for (int64_t j = begin; j < end; ++j) {
-        const int32_t count = a.counts[j];
-        a.counts[j] = static_cast<int32_t>(running);
-        if (j % a.parts == 0) a.offsets[j / a.parts] = static_cast<int32_t>(running);
-        running += count;
+    total = shared[kScanBlock - 1];
+    const int32_t inclusive = shared[threadIdx.x];
+    __syncthreads();
+    return inclusive - value;
+}
+
+__global__ __launch_bounds__(kScanBlock) void route_scan_reduce_kernel(RouteArgs a) {
+    __shared__ int32_t shared[kScanBlock];
+    const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * kScanSegment + threadIdx.x * (kScanSegment / kScanBlock);
+    int32_t sum = 0;
+    for (int j = 0; j < kScanSegment / kScanBlock; ++j)
+        if (begin + j < total) sum += a.counts[begin + j];
+    int32_t block_total;
+    block_exclusive_scan(sum, shared, block_total);
+    if (threadIdx.x == 0) a.block_sums[blockIdx.x] = block_total;
+}
+
+__global__ __launch_bounds__(kScanBlock) void route_scan_top_kernel(RouteArgs a, int blocks) {
+    __shared__ int32_t shared[kScanBlock];
+    const int per = (blocks + kScanBlock - 1) / kScanBlock;
+    int32_t sum = 0;
+    for (int j = 0; j < per; ++j) {
+        const int b = threadIdx.x * per + j;
+        if (b < blocks) sum += a.block_sums[b];
+    }
+    int32_t total;
+    int32_t running = block_exclusive_scan(sum, shared, total);
+    for (int j = 0; j < per; ++j) {
+        const int b = threadIdx.x * per + j;
+        if (b < blocks) {
+            const int32_t value = a.block_sums[b];
+            a.block_sums[b] = running;
+            running += value;
+        }
     }
     if (threadIdx.x == 0) a.offsets[a.experts] = static_cast<int32_t>(a.n);
+}
+
+__global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs a) {
+    __shared__ int32_t shared[kScanBlock];
+    const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
+    constexpr int kPer = kScanSegment / kScanBlock;
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * kScanSegment + threadIdx.x * kPer;
+    int32_t values[kPer];
+    int32_t sum = 0;
+    for (int j = 0; j < kPer; ++j) {
+        values[j] = begin + j < total ? a.counts[begin + j] : 0;
+        sum += values[j];
+    }
+    int32_t block_total;
+    int32_t running = a.block_sums[blockIdx.x] + block_exclusive_scan(sum, shared, block_total);
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t k = begin + j;
+        if (k < total) {
+            a.counts[k] = running;
+            if (k % a.parts == 0) a.offsets[k / a.parts] = running;
+        }
+        running += values[j];
+    }
 }
 
 __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a) {
@@ -201,11 +251,18 @@ int route_plan(int64_t n, int experts, int& part, int& parts) {
 
 using namespace odie;
 
+int64_t scan_blocks(int64_t n, int experts) {
+    int part, parts;
+    route_plan(n, experts, part, parts);
+    return (static_cast<int64_t>(experts) * parts + kScanSegment - 1) / kScanSegment;
+}
+
 ODIE_API int64_t odie_route_workspace(int64_t n, int experts) {
     if (n < 0 || experts < 1) return -1;
     int part, parts;
     route_plan(n, experts, part, parts);
-    return static_cast<int64_t>(experts) * parts * 4;
+    const int64_t counts = (static_cast<int64_t>(experts) * parts * 4 + 255) / 256 * 256;
+    return counts + scan_blocks(n, experts) * 4;
 }
 
 ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
@@ -232,6 +289,12 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     a.coords = coords;
     a.offsets = offsets;
     a.counts = static_cast<int32_t*>(workspace);
+    {
+        int part, parts;
+        route_plan(n, regions_x * regions_y, part, parts);
+        const int64_t counts = (static_cast<int64_t>(regions_x) * regions_y * parts * 4 + 255) / 256 * 256;
+        a.block_sums = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + counts);
+    }
     a.n = n;
     a.width = static_cast<uint32_t>(width);
     a.height = static_cast<uint32_t>(height);
@@ -255,8 +318,12 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     if (shmem + sizeof(Bounds) > 64 * 1024) return fail("odie_route: too many experts for the LDS histogram");
     const uint32_t blocks = static_cast<uint32_t>((a.parts + kWaves - 1) / kWaves);
     if (n == 0) return launch_fill_zero(reinterpret_cast<float*>(offsets), experts + 1, s);
+    const int sblocks = static_cast<int>(scan_blocks(n, experts));
+    if (sblocks > kScanBlock * 64) return fail("odie_route: too many counts to scan");
     route_count_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
-    route_scan_kernel<<<1, kScanBlock, 0, s>>>(a);
+    route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
+    route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
+    route_scan_apply_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
     route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     return check_launch("odie_route");
 }

@@ -84,4 +84,4 @@ def test_route_rejects_bad_arguments(native):
     assert 'two pixels' in native.odie_error().decode()
     assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, 8, 4, 0) == -1
     assert 'workspace' in native.odie_error().decode()
-    assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4
+    assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4 + 256 * 4
