@@ -29,6 +29,8 @@ constexpr int kTransposeBlock = 256;
 constexpr int kTransposeRows = 1024;  // rows per transpose block (and per max-record)
 constexpr int kOwnerBlock = 1024;
 constexpr int kBatch = 4;             // coordinates per thread per owner-loop iteration
+constexpr int kRing = 128;            // per-wave LDS queue of candidate coordinates (power of two)
+constexpr int kRingBytes = kOwnerBlock / 64 * kRing * 4;
 
 struct TransposeArgs {
     const void* upstream;
@@ -116,6 +118,68 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArg
     }
 }
 
+// fp16 pairs (F = 2), levels a multiple of 4 and 16-byte rows: every thread loads its four
+// rows first (16-byte loads), then writes one dword per level and row; |u| maxima are kept as
+// packed 16-bit integer maxima of the magnitude bits (for fp16, |a| <= |b| iff the 15-bit
+// magnitudes compare the same way, with Inf and NaN above every finite value).
+template <int LMAX>
+__global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(TransposeArgs a) {
+    __shared__ uint32_t waves[kTransposeBlock / 64][LMAX];
+    constexpr int kRowsPerThread = kTransposeRows / kTransposeBlock;
+    constexpr int kChunks = LMAX / 4;  // 16-byte chunks per row (4 levels each)
+    uint32_t peak[LMAX];
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) peak[l] = 0;
+    uint4 rows[kRowsPerThread][kChunks];
+    const int chunks = a.n_levels / 4;
+#pragma unroll
+    for (int r = 0; r < kRowsPerThread; ++r) {
+        const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
+        const uint4* row = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.upstream) +
+                                                          static_cast<size_t>(i < a.n ? i : 0) * a.width);
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) rows[r][j] = j < chunks ? row[j] : make_uint4(0, 0, 0, 0);
+    }
+    uint32_t* planes = reinterpret_cast<uint32_t*>(a.planes);
+#pragma unroll
+    for (int r = 0; r < kRowsPerThread; ++r) {
+        const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
+        if (i >= a.n) continue;
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            if (j >= chunks) continue;
+            const uint32_t words[4] = {rows[r][j].x, rows[r][j].y, rows[r][j].z, rows[r][j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int l = 4 * j + q;
+                planes[static_cast<size_t>(l) * a.n + i] = words[q];
+                peak[l] = __builtin_elementwise_max(peak[l], words[q] & 0x7fff7fffu);
+            }
+        }
+    }
+    // Reduce the two 16-bit halves, then across the wave and the block.
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+        if (l < a.n_levels) {
+            uint32_t m = peak[l];
+            m = (m & 0xffffu) > (m >> 16) ? (m & 0xffffu) : (m >> 16);
+            for (int step = 32; step; step >>= 1) {
+                const uint32_t other = __shfl_xor(m, step);
+                m = other > m ? other : m;
+            }
+            if (lane == 0) waves[wave][l] = m;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < a.n_levels) {
+        uint32_t m = 0;
+        for (int w = 0; w < kTransposeBlock / 64; ++w) m = waves[w][threadIdx.x] > m ? waves[w][threadIdx.x] : m;
+        a.blockmax[static_cast<size_t>(blockIdx.x) * a.n_levels + threadIdx.x] =
+            __half2float(bits_to_half(static_cast<uint16_t>(m)));
+    }
+}
+
 struct OwnerArgs {
     const float* coords;
     const int32_t* offsets;
@@ -136,7 +200,171 @@ struct OwnerArgs {
     int first_pass[ODIE_MAX_LEVELS];
     int slices[ODIE_MAX_LEVELS];
     int slice_entries[ODIE_MAX_LEVELS];
+    int row_bits[ODIE_MAX_LEVELS];   // > 0: slices are aligned 2^row_bits blocks screened by row
+    int cap;                         // int64 accumulators in LDS; the candidate rings follow them
 };
+
+enum LevelKind { kDense = 0, kHashedPow2 = 1, kGeneric = 2, kHashed24 = 3 };
+
+// Nearest integer, halves rounded up (floor(x + 0.5)) in one instruction.  |x| < 2^31 here.
+// Any rounding to nearest keeps each fixed-point contribution within half a quantum.
+__device__ inline int32_t round_to_int(float x) {
+    int32_t r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+// Adds one coordinate's contributions at one level to the LDS slice [lo, lo+span).
+// us[c] = upstream feature c times the fixed-point scale 2^S ((w*u)*2^S == w*(u*2^S) exactly:
+// scaling by a power of two commutes with rounding).  Contributions are rounded to integers
+// before the (divergent) slice test so the masked part of the wave is only the LDS add.
+template <int F, int KIND>
+__device__ inline void contribute(float x, float y, const float* us, const DevLevel& lv, uint32_t lo, uint32_t span,
+                                  unsigned long long* acc) {
+    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
+    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
+    const float flx = floorf(px), fly = floorf(py);
+    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
+    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
+    const float fx = px - flx, fy = py - fly;
+    float w[4];
+    w[0] = (1.0f - fx) * (1.0f - fy);
+    w[1] = fx * (1.0f - fy);
+    w[2] = (1.0f - fx) * fy;
+    w[3] = fx * fy;
+    uint32_t idx[4];
+    if constexpr (KIND == kHashed24) {
+        // power-of-two table of at most 2^24 entries: 24-bit row multiply (see hash_row)
+        const uint32_t h0 = __umul24(gy, lv.prime), h1 = __umul24(gy + 1u, lv.prime);
+        idx[0] = (gx ^ h0) & lv.mask;
+        idx[1] = ((gx + 1u) ^ h0) & lv.mask;
+        idx[2] = (gx ^ h1) & lv.mask;
+        idx[3] = ((gx + 1u) ^ h1) & lv.mask;
+    } else if constexpr (KIND == kHashedPow2) {
+        const uint32_t h0 = gy * 2654435761u, h1 = (gy + 1u) * 2654435761u;
+        idx[0] = (gx ^ h0) & lv.mask;
+        idx[1] = ((gx + 1u) ^ h0) & lv.mask;
+        idx[2] = (gx ^ h1) & lv.mask;
+        idx[3] = ((gx + 1u) ^ h1) & lv.mask;
+    } else if constexpr (KIND == kDense) {
+        const uint32_t base = gx + gy * lv.res;
+        idx[0] = wrap_index(base, lv);
+        idx[1] = wrap_index(base + 1u, lv);
+        idx[2] = wrap_index(base + lv.res, lv);
+        idx[3] = wrap_index(base + lv.res + 1u, lv);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t cx = gx + static_cast<uint32_t>(k & 1), cy = gy + static_cast<uint32_t>(k >> 1);
+            idx[k] = wrap_index(cx ^ hash_row(cy, lv), lv);
+        }
+    }
+    int32_t q[4][F];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int c = 0; c < F; ++c) q[k][c] = round_to_int(w[k] * us[c]);
+    const uint32_t shift = lv.offset * F - lo;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t slot = idx[k] * F + shift;
+        if (slot >= span) continue;
+#pragma unroll
+        for (int c = 0; c < F; ++c)
+            atomicAdd(acc + slot + c, static_cast<unsigned long long>(static_cast<long long>(q[k][c])));
+    }
+}
+
+template <int F, bool HALF>
+__device__ inline void load_upstream(const Elem<HALF>* plane, int64_t at, float scale, bool valid, float* us) {
+    if constexpr (HALF && F == 2) {
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(plane + at * F);
+        us[0] = __half2float(bits_to_half(static_cast<uint16_t>(word & 0xffffu)));
+        us[1] = __half2float(bits_to_half(static_cast<uint16_t>(word >> 16)));
+    } else {
+#pragma unroll
+        for (int c = 0; c < F; ++c) us[c] = static_cast<float>(plane[at * F + c]);
+    }
+#pragma unroll
+    for (int c = 0; c < F; ++c) us[c] = valid ? us[c] * scale : 0.0f;
+}
+
+// Every coordinate of [b0, b1) against one level: each thread takes kBatch coordinates per
+// iteration, strided by the block so every load is coalesced; loads are issued
+// unconditionally (clamped index) before any arithmetic.
+template <int F, bool HALF, int KIND>
+__device__ inline void accumulate_level(const float* coords, const Elem<HALF>* plane, const DevLevel lv, int64_t b0,
+                                        int64_t b1, uint32_t lo, uint32_t span, float scale,
+                                        unsigned long long* acc) {
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBatch * kOwnerBlock) {
+        float2 xy[kBatch];
+        float us[kBatch][F];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int64_t ii = i + b * kOwnerBlock;
+            const int64_t at = ii < b1 ? ii : b0;
+            xy[b] = reinterpret_cast<const float2*>(coords)[at];
+            load_upstream<F, HALF>(plane, at, scale, ii < b1, us[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
+    }
+}
+
+// A hashed level whose table slice is the aligned block of 2^row_bits entries number `slice`,
+// with 2^row_bits above the level's resolution: corner (cx, cy) with cx <= res lands in slice
+// ((cy * 2654435761) & mask) >> row_bits whatever cx is, so a coordinate can only touch the
+// slice through its rows gy or gy+1.  Each wave screens its own contiguous share of the
+// coordinates with that y-only test, queues the candidates in its private LDS ring and runs
+// the full contribution only for them, 64 at a time.  Coordinates with x outside [0,1] are
+// always queued (their corner columns are not bounded by the resolution).
+template <int F, bool HALF>
+__device__ inline void accumulate_rows(const float* coords, const Elem<HALF>* plane, const DevLevel lv, int64_t b0,
+                                       int64_t b1, uint32_t lo, uint32_t span, float scale, unsigned long long* acc,
+                                       int32_t* ring, uint32_t row_bits, uint32_t slice) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kWaves = kOwnerBlock / 64;
+    const int64_t per = ((b1 - b0 + kWaves - 1) / kWaves + 63) / 64 * 64;
+    const int64_t w0 = b0 + wave * per < b1 ? b0 + wave * per : b1;
+    const int64_t w1 = w0 + per < b1 ? w0 + per : b1;
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    const uint32_t row_mask = lv.mask >> row_bits;
+    uint32_t head = 0, count = 0;
+    auto drain = [&](uint32_t take) {
+        const bool active = static_cast<uint32_t>(lane) < take;
+        const int64_t i = active ? ring[(head + lane) & (kRing - 1)] : b0;
+        const float2 xy = reinterpret_cast<const float2*>(coords)[i];
+        float us[F];
+        load_upstream<F, HALF>(plane, i, scale, active, us);
+        if (lv.mask < (1u << 24)) contribute<F, kHashed24>(xy.x, xy.y, us, lv, lo, span, acc);
+        else contribute<F, kHashedPow2>(xy.x, xy.y, us, lv, lo, span, acc);
+        head += take;
+        count -= take;
+    };
+    for (int64_t g = w0; g < w1; g += 64 * kBatch) {
+        float2 xy[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int64_t i = g + b * 64 + lane;
+            xy[b] = reinterpret_cast<const float2*>(coords)[i < w1 ? i : b0];
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int64_t i = g + b * 64 + lane;
+            const float py = __builtin_fmaf(lv.scale, xy[b].y, 0.5f);
+            const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(floorf(py)));
+            const uint32_t r0 = (hash_row(gy, lv) >> row_bits) & row_mask;
+            const uint32_t r1 = (hash_row(gy + 1u, lv) >> row_bits) & row_mask;
+            const bool inside = xy[b].x >= 0.0f && xy[b].x <= 1.0f;
+            const bool pick = i < w1 && (r0 == slice || r1 == slice || !inside);
+            const uint64_t picks = __ballot(pick);
+            if (pick) ring[(head + count + __popcll(picks & below)) & (kRing - 1)] = static_cast<int32_t>(i);
+            count += __popcll(picks);
+            if (count >= 64) drain(64);
+        }
+    }
+    while (count > 0) drain(count < 64 ? count : 64);
+}
 
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
@@ -217,62 +445,21 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     const float scale = ldexpf(1.0f, shift);
     const bool finite = !(peak != peak) && peak <= 3.0e38f;
 
-    // Each thread takes kBatch coordinates per iteration (strided by the block so every load
-    // stays coalesced) and issues all their loads before any arithmetic, keeping several
-    // L2/HBM requests in flight per lane.
-    const U* planes = reinterpret_cast<const U*>(a.planes);
-    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBatch * kOwnerBlock) {
-        float2 xy[kBatch];
-        bool valid[kBatch];
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int64_t ii = i + b * kOwnerBlock;
-            valid[b] = ii < b1;
-            xy[b] = valid[b] ? reinterpret_cast<const float2*>(a.coords)[ii] : make_float2(0.f, 0.f);
-        }
-        for (int l = l0; l < l1; ++l) {
-            float u[kBatch][F];
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b) {
-                const int64_t ii = i + b * kOwnerBlock;
-                const U* src = planes + (static_cast<size_t>(l) * a.n + (valid[b] ? ii : b0)) * F;
-                if constexpr (HALF && F == 2) {
-                    const uint32_t word = valid[b] ? *reinterpret_cast<const uint32_t*>(src) : 0u;
-                    u[b][0] = __half2float(bits_to_half(static_cast<uint16_t>(word & 0xffffu)));
-                    u[b][1] = __half2float(bits_to_half(static_cast<uint16_t>(word >> 16)));
-                } else {
-#pragma unroll
-                    for (int c = 0; c < F; ++c) u[b][c] = valid[b] ? static_cast<float>(src[c]) : 0.0f;
-                }
-            }
-            const DevLevel& lv = a.level[l];
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b) {
-                bool any = false;
-#pragma unroll
-                for (int c = 0; c < F; ++c) any |= u[b][c] != 0.0f;
-                if (!any) continue;
-                uint32_t idx[4];
-                float w[4];
-                grid_corners(lv, xy[b].x, xy[b].y, idx, w);
-                // Convert all contributions before the (divergent) slice test so that the
-                // masked part of the wave is only the LDS add itself.
-                int32_t q[4][F];
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-#pragma unroll
-                    for (int c = 0; c < F; ++c) q[k][c] = static_cast<int32_t>(rintf((w[k] * u[b][c]) * scale));
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t slot = (lv.offset + idx[k]) * F - lo;
-                    if (slot >= span) continue;
-#pragma unroll
-                    for (int c = 0; c < F; ++c)
-                        if (q[k][c] != 0)
-                            atomicAdd(acc + slot + c, static_cast<unsigned long long>(static_cast<long long>(q[k][c])));
-                }
-            }
-        }
+    int32_t* ring = reinterpret_cast<int32_t*>(acc + a.cap) + (threadIdx.x / 64) * kRing;
+    for (int l = l0; l < l1; ++l) {
+        const DevLevel lv = a.level[l];
+        const U* plane = reinterpret_cast<const U*>(a.planes) + static_cast<size_t>(l) * a.n * F;
+        if (a.row_bits[l] > 0 && !(a.group > 0 && p == 0))
+            accumulate_rows<F, HALF>(a.coords, plane, lv, b0, b1, lo, span, scale, acc, ring, a.row_bits[l],
+                                     static_cast<uint32_t>(p - a.first_pass[l]));
+        else if (lv.hashed && lv.mask && lv.mask < (1u << 24))
+            accumulate_level<F, HALF, kHashed24>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+        else if (lv.hashed && lv.mask)
+            accumulate_level<F, HALF, kHashedPow2>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+        else if (lv.hashed)
+            accumulate_level<F, HALF, kGeneric>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+        else
+            accumulate_level<F, HALF, kDense>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
     }
     __syncthreads();
     const double unscale = ldexp(1.0, -shift);
@@ -313,7 +500,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const bool half = in.up_half != 0;
     const size_t elem = half ? 2 : 4;
     const int64_t lds_bytes = in.lds_bytes;
-    const int64_t cap = lds_bytes / 8 - F;  // floats per slice (int64 accumulators), minus entry rounding
+    const int64_t cap = (lds_bytes - kRingBytes) / 8 - F;  // int64 accumulators per slice, minus entry rounding
     if (cap < 64) return fail("odie_grid_backward: LDS budget too small for the owner backward");
 
     OwnerArgs o{};
@@ -336,14 +523,24 @@ int launch_owner_backward(const OwnerLaunch& in) {
         o.level[l] = in.levels[l];
         if (l < group) continue;
         const int64_t floats = static_cast<int64_t>(in.levels[l].size) * F;
-        const int64_t slices = (floats + cap - 1) / cap;
+        int64_t slices = (floats + cap - 1) / cap;
+        int64_t entries = (in.levels[l].size + slices - 1) / slices;
+        int bits = 0;
+        while ((int64_t{2} << bits) * F <= cap) ++bits;   // 2^bits entries: largest block that fits
+        if (in.row_screen && in.levels[l].hashed && in.levels[l].mask && (int64_t{1} << bits) > in.levels[l].res &&
+            (int64_t{1} << bits) < in.levels[l].size) {
+            entries = int64_t{1} << bits;
+            slices = in.levels[l].size / entries;
+            o.row_bits[l] = bits;
+        }
         o.slices[l] = static_cast<int>(slices);
-        o.slice_entries[l] = static_cast<int>((in.levels[l].size + slices - 1) / slices);
+        o.slice_entries[l] = static_cast<int>(entries);
         o.first_pass[l] = passes;
         passes += static_cast<int>(slices);
     }
     o.group = group;
     o.passes = passes;
+    o.cap = static_cast<int>(cap + F);
     const int64_t per_pass = static_cast<int64_t>(in.experts) * passes;
     int splits = 1;
     if (per_pass < 512) {
@@ -376,14 +573,17 @@ int launch_owner_backward(const OwnerLaunch& in) {
     t.vec_rows = (reinterpret_cast<uintptr_t>(in.upstream) % 16 == 0) && (in.up_width * elem) % 16 == 0 &&
                  (L * F * elem) % 16 == 0;
     const uint32_t tblocks = static_cast<uint32_t>(row_blocks);
-    const size_t shmem = static_cast<size_t>(cap + F) * 8;
+    const size_t shmem = static_cast<size_t>(cap + F) * 8 + kRingBytes;
     const uint32_t total = static_cast<uint32_t>(per_pass * splits);
     const uint32_t oblocks = round_up(total, kXcds);
     hipStream_t s = in.stream;
 
 #define ODIE_TRANSPOSE(FF, HH)                                                                          \
     do {                                                                                                \
-        if (L <= 16) transpose_kernel<FF, HH, 16><<<tblocks, kTransposeBlock, 0, s>>>(t);               \
+        if (FF == 2 && HH && t.vec_rows && L % 4 == 0) {                                                \
+            if (L <= 16) transpose_half2_kernel<16><<<tblocks, kTransposeBlock, 0, s>>>(t);             \
+            else transpose_half2_kernel<32><<<tblocks, kTransposeBlock, 0, s>>>(t);                     \
+        } else if (L <= 16) transpose_kernel<FF, HH, 16><<<tblocks, kTransposeBlock, 0, s>>>(t);        \
         else transpose_kernel<FF, HH, 32><<<tblocks, kTransposeBlock, 0, s>>>(t);                       \
     } while (0)
 #define ODIE_OWNER(FF, HH)                                                                              \

@@ -33,16 +33,22 @@ struct GridArgs {
     int lds_levels;  // backward: levels accumulated in LDS
     int lds_floats;  // backward: LDS accumulator size in floats
     int remap;       // 1: XCD-major block order
+    int paired;      // forward, fp16 F=2: 16-byte group loads (table 16-byte aligned, entries % 4 == 0)
+    int stage_levels;   // forward, fp16 F=2: coarse levels read from an LDS copy of the expert's table
+    int stage_entries;  // entries staged (multiple of 4)
     DevLevel level[ODIE_MAX_LEVELS];
 };
 
 // Tuning knobs (set through odie_set_tuning; defaults chosen by measurement).
 struct Tuning {
-    int forward_chunk = 1024;
+    int forward_chunk = 256;
     int backward_chunk = 8192;
     int lds_bytes = 65536;
     int xcd_remap = 1;
     int backward_mode = 1;          // 0: LDS + global fp32 atomics, 1: owner computes
+    int row_screen = 0;             // owner: screen hashed slices by row (measured slower)
+    int paired_loads = 0;           // forward: 16-byte corner-pair loads (measured no gain)
+    int forward_lds_bytes = 28672;  // forward: LDS budget for staged coarse levels (0: off)
     int owner_lds_bytes = 162816;   // 160 KiB minus static LDS
 };
 Tuning& tuning() {
@@ -70,8 +76,14 @@ __device__ inline int64_t segment_end(const GridArgs& a, int e, int64_t i, int64
     return stop;
 }
 
+__device__ inline uint32_t pick4(const uint4& v, uint32_t j) {
+    const uint32_t low = (j & 1u) ? v.y : v.x;
+    const uint32_t high = (j & 1u) ? v.w : v.z;
+    return (j & 2u) ? high : low;
+}
+
 template <int F, bool HALF, int LMAX>
-__device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, int64_t i) {
+__device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, const uint32_t* staged, int64_t i) {
     using T = Elem<HALF>;
     const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
     T vals[LMAX * F];
@@ -83,7 +95,40 @@ __device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, in
             float w[4];
             grid_corners(lv, p.x, p.y, idx, w);
             const T* t = table + static_cast<size_t>(lv.offset) * F;
-            if constexpr (HALF && F % 2 == 0) {
+            if constexpr (HALF && F == 2) {
+                // Corners (0,1) and (2,3) usually sit in one aligned 16-byte group of four
+                // entries (x and x+1 differ only in their low bits, dense or hashed): fetch
+                // the group of the even corner and load the odd corner alone only when it
+                // falls outside.  Values and FMA order are unchanged.
+                uint32_t g[4];
+                if (l < a.stage_levels) {
+                    // coarse level staged in LDS by the block
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) g[k] = staged[lv.offset + idx[k]];
+                } else if (a.paired) {
+                    const uint32_t* entries = reinterpret_cast<const uint32_t*>(table);
+#pragma unroll
+                    for (int k = 0; k < 4; k += 2) {
+                        const uint32_t first = lv.offset + idx[k], second = lv.offset + idx[k + 1];
+                        const uint32_t base = first & ~3u;
+                        const uint4 group = *reinterpret_cast<const uint4*>(entries + base);
+                        g[k] = pick4(group, first & 3u);
+                        g[k + 1] = (second & ~3u) == base ? pick4(group, second & 3u) : entries[second];
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) g[k] = reinterpret_cast<const uint32_t*>(t)[idx[k]];
+                }
+                __half2 acc = __half2(__float2half(0.0f), __float2half(0.0f));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const __half2 value = __halves2half2(bits_to_half(static_cast<uint16_t>(g[k] & 0xffffu)),
+                                                         bits_to_half(static_cast<uint16_t>(g[k] >> 16)));
+                    acc = __hfma2(__float2half2_rn(keep_fp32(w[k])), value, acc);
+                }
+                vals[l * F] = __low2half(acc);
+                vals[l * F + 1] = __high2half(acc);
+            } else if constexpr (HALF && F % 2 == 0) {
                 __half2 acc[F / 2];
 #pragma unroll
                 for (int c = 0; c < F / 2; ++c) acc[c] = __half2(__float2half(0.0f), __float2half(0.0f));
@@ -160,11 +205,19 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
     int64_t begin = static_cast<int64_t>(block) * a.chunk;
     if (begin >= a.n) return;
     const int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
+    extern __shared__ uint32_t staged[];
     while (begin < end) {
         const int e = expert_at(a, begin);
         const int64_t stop = segment_end(a, e, begin, end);
         const Elem<HALF>* table = reinterpret_cast<const Elem<HALF>*>(a.params) + static_cast<size_t>(e) * a.expert_params;
-        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) encode_row<F, HALF, LMAX>(a, table, i);
+        if (a.stage_levels > 0) {
+            // Stage the expert's coarse levels (fp16 x2 entries as dwords) in LDS.
+            __syncthreads();
+            const uint4* src = reinterpret_cast<const uint4*>(table);
+            for (int j = threadIdx.x; j < a.stage_entries / 4; j += kBlock) reinterpret_cast<uint4*>(staged)[j] = src[j];
+            __syncthreads();
+        }
+        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) encode_row<F, HALF, LMAX>(a, table, staged, i);
         begin = stop;
     }
 }
@@ -288,6 +341,7 @@ int validate_grid(const char* what, const float* coords, int64_t n, const int32_
         d.mask = (lv.size & (lv.size - 1)) == 0 ? lv.size - 1 : 0;
         d.offset = lv.offset;
         d.hashed = lv.hashed ? 1u : 0u;
+        d.prime = (d.mask && d.mask < (1u << 24)) ? (2654435761u & d.mask) : 2654435761u;
     }
     if (expert_params < static_cast<int64_t>(entries) * features)
         return fail(w + ": expert_params is smaller than the levels' table");
@@ -460,6 +514,9 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "lds_bytes" && value >= 0 && value <= 160 * 1024) t.lds_bytes = value;
     else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
     else if (key == "backward_mode" && (value == 0 || value == 1)) t.backward_mode = value;
+    else if (key == "row_screen" && (value == 0 || value == 1)) t.row_screen = value;
+    else if (key == "paired_loads" && (value == 0 || value == 1)) t.paired_loads = value;
+    else if (key == "forward_lds_bytes" && value >= 0 && value <= 65536) t.forward_lds_bytes = value;
     else if (key == "owner_lds_bytes" && value >= 4096 && value <= 162816) t.owner_lds_bytes = value;
     else return fail("odie_set_tuning: unknown key or value out of range: " + key);
     return 0;
@@ -487,11 +544,28 @@ ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* of
     a.width = out_width;
     a.chunk = tuning().forward_chunk;
     a.remap = tuning().xcd_remap;
+    {
+        const uint64_t entries = static_cast<uint64_t>(levels[n_levels - 1].offset) + levels[n_levels - 1].size;
+        a.paired = tuning().paired_loads && half && features == 2 && reinterpret_cast<uintptr_t>(params) % 16 == 0 &&
+                   entries % 4 == 0 && (expert_params * 2) % 16 == 0;
+        // Stage the longest prefix of levels that fits the budget (entries of 4 bytes).
+        if (half && features == 2 && reinterpret_cast<uintptr_t>(params) % 16 == 0 && (expert_params * 2) % 16 == 0) {
+            int64_t staged = 0;
+            for (int l = 0; l < n_levels; ++l) {
+                const int64_t next = static_cast<int64_t>(levels[l].offset) + levels[l].size;
+                if (next * 4 > tuning().forward_lds_bytes || next % 4) break;
+                a.stage_levels = l + 1;
+                staged = next;
+            }
+            a.stage_entries = static_cast<int>(staged);
+        }
+    }
     a.vec_rows = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (out_width * elem) % 16 == 0;
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_forward: coords must be 8-byte aligned");
     const uint32_t blocks = grid_blocks(n, a.chunk);
     const hipStream_t s = as_stream(stream);
-    ODIE_GRID_DISPATCH(grid_forward_kernel, features, half, n_levels, blocks, 0, s, a);
+    ODIE_GRID_DISPATCH(grid_forward_kernel, features, half, n_levels, blocks,
+                       static_cast<size_t>(a.stage_entries) * 4, s, a);
     return check_launch("odie_grid_forward");
 }
 
@@ -535,6 +609,7 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
         o.levels = a.level;
         o.lds_bytes = t.owner_lds_bytes;
         o.remap = t.xcd_remap;
+        o.row_screen = t.row_screen;
         o.stream = s;
         return launch_owner_backward(o);
     }

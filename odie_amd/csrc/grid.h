@@ -15,7 +15,17 @@ struct DevLevel {
     uint32_t mask;    // size - 1 when size is a power of two, else 0
     uint32_t offset;  // first entry of the level
     uint32_t hashed;
+    uint32_t prime;   // hash multiplier: 2654435761 & mask when 0 < mask < 2^24, else 2654435761
 };
+
+// Row term of the spatial hash, y * 2654435761 reduced mod the (power-of-two) table size.
+// When the table has at most 2^24 entries only the low 24 bits of the product survive the
+// mask, and those depend only on the low 24 bits of both factors, so the full-rate 24-bit
+// multiply gives exactly the bits the 32-bit product would.
+__device__ inline uint32_t hash_row(uint32_t y, const DevLevel& lv) {
+    if (lv.mask && lv.mask < (1u << 24)) return __umul24(y, lv.prime);
+    return y * 2654435761u;
+}
 
 __device__ inline uint32_t wrap_index(uint32_t v, const DevLevel& lv) {
     if (lv.mask) return v & lv.mask;
@@ -40,7 +50,7 @@ __device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const uint32_t cx = gx + static_cast<uint32_t>(k & 1), cy = gy + static_cast<uint32_t>(k >> 1);
-        const uint32_t raw = lv.hashed ? (cx ^ (cy * 2654435761u)) : (cx + cy * lv.res);
+        const uint32_t raw = lv.hashed ? (cx ^ hash_row(cy, lv)) : (cx + cy * lv.res);
         idx[k] = wrap_index(raw, lv);
     }
 }
@@ -65,6 +75,7 @@ struct OwnerLaunch {
     const DevLevel* levels;   // host array [n_levels]
     int64_t lds_bytes;
     int remap;
+    int row_screen;
     hipStream_t stream;
 };
 int launch_owner_backward(const OwnerLaunch& launch);
