@@ -120,6 +120,37 @@ int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions
                int32_t* expert, int32_t* perm, float* coords, int32_t* offsets,
                void* workspace, int64_t workspace_bytes, uint64_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Residual pass.  Same name, signature and meaning as the reference's score_chunk
+ * (odie/residual_cuda.cu:45-52): pixels [begin, end) of a width-wide image in raster order;
+ * prediction fp32 [end-begin, 3], target uint8 (rgb8) or fp32 [end-begin, 3]; the cells of rows
+ * first_y.. (active_cells of them, row-major, `resolution` per row) with column/row bounds
+ * xb[resolution+1], yb[resolution+1] (device int32); totals fp64 [resolution^2] are read and
+ * updated: total += (fp64(d0^2) + fp64(d1^2) + fp64(d2^2)) / 3 per pixel, d = prediction - t,
+ * t = byte/255 in fp32, summed sequentially in raster order within each cell.
+ * --------------------------------------------------------------------------------------- */
+int score_chunk(const float* prediction, const void* target, int64_t begin, int64_t end, int width,
+                int resolution, int first_y, int active_cells, const int* xb, const int* yb,
+                double* totals, bool rgb8, uint64_t stream);
+
+/* Top-k cells by score: ids (device int32 [k]) of the k largest scores (fp64 [n], >= 0), ties to
+ * the lower id, written in ascending id order.  Ranking rule of select_mean_rank
+ * (odie/selection.py:103,116) with the sign-cleared FP64 key of the GPU selector
+ * (odie/native/selection_cuda.cu:14-17).  No counterpart entry point in the reference. */
+int odie_topk(const double* scores, int64_t n, int64_t k, int32_t* ids, uint64_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Fused Adam over n parameters: master fp32 (updated), half_copy fp16 (nullable; receives
+ * fp16(master) in the same pass), grad fp32 or fp16 carrying loss_scale, moments m, v fp32.
+ * variant 0: torch.optim.Adam with global step `step` (odie/optimizer.py:324,365).
+ * variant 1: per-parameter ages in steps (uint32 [n]); zero gradients skip the update and keep
+ * the age (the grid optimizer of odie/native/runtime.cu:212-215, odie/train.py:121-124).
+ * Replaces the TCNN optimizer step calls (odie/native/runtime.cu:304-310).
+ * --------------------------------------------------------------------------------------- */
+int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int grad_dtype, float* m, float* v,
+                   uint32_t* steps, int64_t n, int variant, int64_t step, float lr, float beta1, float beta2,
+                   float eps, float loss_scale, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,10 @@ SIGNATURES = {
     'odie_packed_backward': ([_P, _I64, _P, _I, _P, _I, _P, _P, _P, _P, _I64, _U64], _I),
     'odie_route_workspace': ([_I64, _I], _I64),
     'odie_route': ([_P, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _U64], _I),
+    'score_chunk': ([_P, _P, _I64, _I64, _I, _I, _I, _I, _P, _P, _P, C.c_bool, _U64], _I),
+    'odie_topk': ([_P, _I64, _I64, _P, _U64], _I),
+    'odie_adam_step': ([_P, _P, _P, _I, _P, _P, _P, _I64, _I, _I64, C.c_float, C.c_float, C.c_float,
+                        C.c_float, C.c_float, _U64], _I),
 }
 
 _handle = None

@@ -1,0 +1,97 @@
+// Residual pass: per-cell FP64 squared-error totals in raster order, bit-exact with the
+// reference's rule (odie/residual_cuda.cu:11-43, odie/selection.py:58-73).
+//
+// Per pixel: t = byte / 255 (correctly rounded fp32 division) or the fp32 target itself,
+// d = p - t in fp32, rgb = (double(d0*d0) + double(d1*d1)) + double(d2*d2) in fp64, and the
+// cell total grows by rgb / 3.0 in fp64 -- sequentially, in raster order within each cell,
+// continued across streamed chunks.  An FP64 sum is order dependent, so each cell is one
+// sequential chain; the parallelism is across cells.  To keep the chain's latency the only
+// serial part, every thread first computes the per-pixel terms of the next run of pixels of
+// its row (independent work the scheduler can overlap) and then folds them in order.
+#include "common.h"
+#include "../../include/odie_amd.h"
+
+namespace odie {
+namespace {
+
+constexpr int kResidualBlock = 128;
+constexpr int kRun = 8;   // pixel terms computed ahead of the sequential fold
+
+template <bool RGB8>
+__device__ inline double pixel_term(const float* prediction, const void* target, int64_t p) {
+    float t0, t1, t2;
+    if constexpr (RGB8) {
+        const uint8_t* bytes = static_cast<const uint8_t*>(target);
+        t0 = static_cast<float>(bytes[p]) / 255.0f;
+        t1 = static_cast<float>(bytes[p + 1]) / 255.0f;
+        t2 = static_cast<float>(bytes[p + 2]) / 255.0f;
+    } else {
+        const float* values = static_cast<const float*>(target);
+        t0 = values[p];
+        t1 = values[p + 1];
+        t2 = values[p + 2];
+    }
+    const float d0 = prediction[p] - t0, d1 = prediction[p + 1] - t1, d2 = prediction[p + 2] - t2;
+    double rgb = static_cast<double>(d0 * d0) + static_cast<double>(d1 * d1);
+    rgb = rgb + static_cast<double>(d2 * d2);
+    return rgb / 3.0;
+}
+
+template <bool RGB8>
+__global__ __launch_bounds__(kResidualBlock) void accumulate_kernel(const float* prediction, const void* target,
+                                                                    int64_t begin, int64_t end, int width,
+                                                                    int resolution, int first_y, int active_cells,
+                                                                    const int* xb, const int* yb, double* totals) {
+    const int t = blockIdx.x * kResidualBlock + threadIdx.x;
+    if (t >= active_cells) return;
+    const int cx = t % resolution, cy = first_y + t / resolution;
+    const int64_t cell = static_cast<int64_t>(cy) * resolution + cx;
+    const int64_t first_row = begin / width, last_row = (end - 1) / width + 1;
+    const int64_t y0 = yb[cy] > first_row ? yb[cy] : first_row;
+    const int64_t y1 = yb[cy + 1] < last_row ? yb[cy + 1] : last_row;
+    double sum = totals[cell];
+    for (int64_t y = y0; y < y1; ++y) {
+        const int64_t row = y * width;
+        const int64_t x0 = xb[cx] > begin - row ? xb[cx] : begin - row;
+        const int64_t x1 = xb[cx + 1] < end - row ? xb[cx + 1] : end - row;
+        int64_t x = x0;
+        for (; x + kRun <= x1; x += kRun) {
+            double terms[kRun];
+#pragma unroll
+            for (int j = 0; j < kRun; ++j) terms[j] = pixel_term<RGB8>(prediction, target, (row + x + j - begin) * 3);
+#pragma unroll
+            for (int j = 0; j < kRun; ++j) sum = sum + terms[j];
+        }
+        for (; x < x1; ++x) sum = sum + pixel_term<RGB8>(prediction, target, (row + x - begin) * 3);
+    }
+    totals[cell] = sum;
+}
+
+}  // namespace
+}  // namespace odie
+
+using namespace odie;
+
+// Same signature and meaning as score_chunk (odie/residual_cuda.cu:45-52): pixels [begin, end)
+// of a width-wide image, prediction fp32 [end-begin, 3], target uint8 or fp32 [end-begin, 3],
+// cells of rows first_y.. (active_cells of them) with column/row bounds xb[R+1], yb[R+1];
+// totals (fp64 [R*R]) are read and updated.  Returns 0 or -1 (see odie_error).
+ODIE_API int score_chunk(const float* prediction, const void* target, int64_t begin, int64_t end, int width,
+                         int resolution, int first_y, int active_cells, const int* xb, const int* yb, double* totals,
+                         bool rgb8, uint64_t stream) {
+    if (width < 1 || resolution < 1) return fail("score_chunk: width and resolution must be positive");
+    if (begin < 0 || end < begin) return fail("score_chunk: need 0 <= begin <= end");
+    if (first_y < 0 || active_cells < 0 || first_y + (active_cells + resolution - 1) / resolution > resolution)
+        return fail("score_chunk: cell rows out of range");
+    if (end == begin || active_cells == 0) return 0;
+    if (!prediction || !target || !xb || !yb || !totals) return fail("score_chunk: null pointer");
+    const uint32_t blocks = static_cast<uint32_t>((active_cells + kResidualBlock - 1) / kResidualBlock);
+    const hipStream_t s = as_stream(stream);
+    if (rgb8)
+        accumulate_kernel<true><<<blocks, kResidualBlock, 0, s>>>(prediction, target, begin, end, width, resolution,
+                                                                  first_y, active_cells, xb, yb, totals);
+    else
+        accumulate_kernel<false><<<blocks, kResidualBlock, 0, s>>>(prediction, target, begin, end, width, resolution,
+                                                                   first_y, active_cells, xb, yb, totals);
+    return check_launch("score_chunk");
+}

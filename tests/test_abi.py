@@ -85,3 +85,21 @@ def test_route_rejects_bad_arguments(native):
     assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, 8, 4, 0) == -1
     assert 'workspace' in native.odie_error().decode()
     assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4 + 256 * 4
+
+
+def test_selection_entry_points_reject_bad_arguments(native):
+    assert native.score_chunk(8, 8, 5, 3, 10, 4, 0, 4, 8, 8, 8, True, 0) == -1
+    assert 'begin' in native.odie_error().decode()
+    assert native.odie_topk(8, 10, 11, 8, 0) == -1
+    assert 'k must be' in native.odie_error().decode()
+    assert native.odie_adam_step(8, None, 8, 0, 8, 8, None, 10, 2, 1, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
+    assert 'variant' in native.odie_error().decode()
+    assert native.odie_adam_step(8, None, 8, 0, 8, 8, None, 10, 0, 0, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
+    assert 'step' in native.odie_error().decode()
+
+
+def test_product_thresholds_equal_oracle(oracle):
+    import numpy as np
+    from odie_amd.selection import native_thresholds
+    for r in (2, 8, 13, 128, 1290):
+        assert np.array_equal(np.asarray(native_thresholds(r), dtype=np.float32), oracle.native_thresholds(r))
