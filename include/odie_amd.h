@@ -140,6 +140,32 @@ int score_chunk(const float* prediction, const void* target, int64_t begin, int6
 int odie_topk(const double* scores, int64_t n, int64_t k, int32_t* ids, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
+ * B2 exact greedy support selection on the device (odie/selection.py:129-207): free cells
+ * (no new closure node) are taken first, in ascending id; otherwise the cell with the best
+ * score / new-node cost over costs 1..min(4, cap-used), ties to the lower id.
+ * Same names, signatures and state buffers as the reference's selector
+ * (odie/native/selection_cuda.cu:208-230, bound at odie/selection_cuda.py:46-49):
+ *   scores fp64 [n] (n = resolution^2, >= 0), missing int32 [n], chosen uint8 [n],
+ *   nodes uint8 [points] (points = align8(n)), tree int32 [odie_selection_tree_ints(n)],
+ *   stats int64 [4] = {used nodes, iterations, done, invariant error}, trace int32 [n] or null
+ *   (the chosen cells in order).
+ * selection_init resets the state and builds the tournament trees; host_offsets/host_sizes/
+ * levels may describe the caller's fan-32 tree allocation (then it is checked to be large
+ * enough) or be null/0.  selection_chunk runs up to `chunk` costly choices, each followed by
+ * the free cells it creates; call it until stats[2] (done) or stats[3] (error) is set.
+ * offsets/sizes/levels of selection_chunk are accepted and ignored.
+ * --------------------------------------------------------------------------------------- */
+int64_t odie_selection_tree_ints(int n);
+
+int selection_init(const double* scores, int n, int points, int* missing, uint8_t* chosen, uint8_t* nodes,
+                   int* tree, int64_t* stats, const int* host_offsets, const int* host_sizes, int levels,
+                   uint64_t stream);
+
+int selection_chunk(const double* scores, int n, int points, int resolution, int cap, bool normalized,
+                    int* missing, uint8_t* chosen, uint8_t* nodes, int* tree, const int* offsets,
+                    const int* sizes, int levels, int chunk, int64_t* stats, int* trace, uint64_t stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused Adam over n parameters: master fp32 (updated), half_copy fp16 (nullable; receives
  * fp16(master) in the same pass), grad fp32 or fp16 carrying loss_scale, moments m, v fp32.
  * variant 0: torch.optim.Adam with global step `step` (odie/optimizer.py:324,365).

@@ -73,3 +73,63 @@ def topk_tiles(scores, k):
     _lib.check(_lib.library().odie_topk(scores.data_ptr(), scores.numel(), k, ids.data_ptr(),
                                         _lib.stream_of(scores)))
     return ids
+
+
+class GreedySelection:
+    """Device state of the B2 exact greedy selector (odie/gpu_residual.py:75-128): scores stay
+    on the device, the host only polls the four stats words between bounded launches."""
+
+    def __init__(self, scores, resolution, cap, normalize_by_cost=True, trace=False, chunk=512):
+        if scores.dtype != torch.float64 or scores.ndim != 1 or not scores.is_cuda:
+            raise ValueError('scores must be a CUDA fp64 vector')
+        n = resolution * resolution
+        if scores.numel() != n:
+            raise ValueError('scores must hold resolution^2 cells')
+        if cap < 0 or cap % 8 or cap > align8(n):
+            raise ValueError('cap must be an 8-aligned node count within align8(resolution^2)')
+        device = scores.device
+        self.scores = scores.contiguous()
+        self.n, self.points, self.resolution, self.cap = n, align8(n), resolution, cap
+        self.normalize_by_cost, self.chunk = normalize_by_cost, chunk
+        lib = _lib.library()
+        self.missing = torch.empty(n, dtype=torch.int32, device=device)
+        self.chosen = torch.empty(n, dtype=torch.uint8, device=device)
+        self.nodes = torch.empty(self.points, dtype=torch.uint8, device=device)
+        self.tree = torch.empty(int(lib.odie_selection_tree_ints(n)), dtype=torch.int32, device=device)
+        self.stats = torch.empty(4, dtype=torch.int64, device=device)
+        self.trace = torch.full((n,), -1, dtype=torch.int32, device=device) if trace else None
+        self.launches = 0
+
+    def run(self):
+        """Select until done; returns (selected bool [n], nodes bool [points], iterations)."""
+        lib, stream = _lib.library(), _lib.stream_of(self.scores)
+        _lib.check(lib.selection_init(self.scores.data_ptr(), self.n, self.points, self.missing.data_ptr(),
+                                      self.chosen.data_ptr(), self.nodes.data_ptr(), self.tree.data_ptr(),
+                                      self.stats.data_ptr(), None, None, 0, stream))
+        trace = self.trace.data_ptr() if self.trace is not None else None
+        while True:
+            _lib.check(lib.selection_chunk(self.scores.data_ptr(), self.n, self.points, self.resolution, self.cap,
+                                           self.normalize_by_cost, self.missing.data_ptr(), self.chosen.data_ptr(),
+                                           self.nodes.data_ptr(), self.tree.data_ptr(), None, None, 0, self.chunk,
+                                           self.stats.data_ptr(), trace, stream))
+            self.launches += 1
+            stats = self.stats.cpu()
+            if stats[3]:
+                raise AssertionError('device greedy: exact marginal cost invariant failed')
+            if stats[2]:
+                break
+        used, iterations = int(stats[0]), int(stats[1])
+        selected, nodes = self.chosen.bool(), self.nodes.bool()
+        if int(nodes.sum()) != used:
+            raise AssertionError('device greedy: node count and stats disagree')
+        return selected, nodes, iterations
+
+
+def select_device(scores, resolution, cap, normalize_by_cost=True, trace=False, chunk=512):
+    """B2 exact greedy over device-resident fp64 scores (odie/gpu_residual.py:75).  Returns
+    (selected, nodes, iterations[, trace int32 [iterations]])."""
+    state = GreedySelection(scores, resolution, cap, normalize_by_cost, trace, chunk)
+    selected, nodes, iterations = state.run()
+    if trace:
+        return selected, nodes, iterations, state.trace[:iterations]
+    return selected, nodes, iterations

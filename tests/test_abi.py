@@ -96,6 +96,36 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert 'variant' in native.odie_error().decode()
     assert native.odie_adam_step(8, None, 8, 0, 8, 8, None, 10, 0, 0, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
     assert 'step' in native.odie_error().decode()
+    # greedy selector: n must be resolution^2, cap 8-aligned, chunk positive, tree large enough
+    args = [8, 4096, 4096, 63, 256, True, 8, 8, 8, 8, None, None, 0, 512, 8, None, 0]
+    assert native.selection_chunk(*args) == -1 and 'resolution^2' in native.odie_error().decode()
+    args[3], args[4] = 64, 100
+    assert native.selection_chunk(*args) == -1 and 'cap' in native.odie_error().decode()
+    args[4], args[13] = 256, 0
+    assert native.selection_chunk(*args) == -1 and 'chunk' in native.odie_error().decode()
+    offsets, sizes = (C.c_int * 1)(0), (C.c_int * 1)(10)
+    assert native.selection_init(8, 4096, 4096, 8, 8, 8, 8, 8, offsets, sizes, 1, 0) == -1
+    assert 'too small' in native.odie_error().decode()
+    assert native.selection_init(8, 4096, 4100, 8, 8, 8, 8, 8, None, None, 0, 0) == -1
+    assert 'points' in native.odie_error().decode()
+
+
+def test_selection_tree_fits_the_callers_fan32_allocation(native):
+    # the reference sizes the tree buffer as 5 ints per node of a fan-32 tree
+    # (odie/gpu_residual.py:77-88); the fan-64, 4-category tree must never need more
+    def fan32_ints(n):
+        total, children = 0, n
+        while True:
+            parents = (children + 31) // 32
+            total += parents * 5
+            if parents == 1:
+                return total
+            children = parents
+    assert native.odie_selection_tree_ints(4096) == (64 + 1) * 4
+    assert native.odie_selection_tree_ints(200704) == (3136 + 49 + 1) * 4
+    for n in (4, 9, 64, 65, 4096, 4097, 10 ** 6, 2 ** 24, 2 ** 31 - 1):
+        assert 0 < native.odie_selection_tree_ints(n) <= fan32_ints(n)
+    assert native.odie_selection_tree_ints(0) == -1
 
 
 def test_product_thresholds_equal_oracle(oracle):
