@@ -171,11 +171,37 @@ int selection_chunk(const double* scores, int n, int points, int resolution, int
  * variant 0: torch.optim.Adam with global step `step` (odie/optimizer.py:324,365).
  * variant 1: per-parameter ages in steps (uint32 [n]); zero gradients skip the update and keep
  * the age (the grid optimizer of odie/native/runtime.cu:212-215, odie/train.py:121-124).
+ * variant 2: per-parameter ages without the zero-gradient skip (the head optimizers of
+ * odie/native/runtime.cu:159-160, whose weights are matrix parameters).
  * Replaces the TCNN optimizer step calls (odie/native/runtime.cu:304-310).
  * --------------------------------------------------------------------------------------- */
 int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int grad_dtype, float* m, float* v,
                    uint32_t* steps, int64_t n, int variant, int64_t step, float lr, float beta1, float beta2,
                    float eps, float loss_scale, uint64_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Decoder MLP 32 -> 64 -> 64 -> 16 (ReLU hidden layers, no bias, no output activation), fp16
+ * weights and activations, fp32 accumulation: the decoder head of the reference (TCNN
+ * FullyFusedMLP, odie/hash_grid.py:32-34, forward/backward at odie/native/runtime.cu:270,273).
+ * weights fp16 [7168] = W1 [64][32] | W2 [64][64] | W3 [16][64], row-major [out][in].
+ *
+ * odie_mlp_forward: out fp16 [n][16] = decoder(x fp16 [n][32]).
+ *
+ * odie_mlp_train: forward, the step's loss (loss_grad, odie/native/runtime.cu:53-63) and
+ * backward in one pass.  Tile row j reads x[j]; its input row is i = rows[j] (rows null:
+ * i = j).  Target of input row i: rgb[3*ids[i] + c] * (1/255) (rgb non-null) or target[3*i + c].
+ * dy_c = fp16(fp16(2*d_c/(3*real)*128)*128) for c < 3 (zero for i >= real), d = y - t.
+ * Writes dz fp16 [n][32] = fp16(fp16(dL/dx * 16384) / 128) at row j (the grid's upstream,
+ * half_unscale at odie/native/runtime.cu:282), dweights fp32 [7168] = dL/dW * 16384
+ * (overwritten; deterministic), and, where non-null, out fp16 [.][16] and squares fp32 [.] at
+ * input row i (squares = sum_c d_c^2 / 3), hidden fp16 [n][128] = (h1 | h2) at row j.
+ * x must be 16-byte aligned, dz and out 8-byte aligned.
+ * --------------------------------------------------------------------------------------- */
+int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weights, uint16_t* out, uint64_t stream);
+
+int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights, const uint8_t* rgb,
+                   const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out, uint16_t* hidden,
+                   float* squares, uint16_t* dz, float* dweights, uint64_t stream);
 
 #ifdef __cplusplus
 }

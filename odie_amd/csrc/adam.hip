@@ -11,8 +11,11 @@
 //   parameter whose gradient is exactly zero is skipped and keeps its age; otherwise its own
 //   step counter t_i advances and
 //     p -= lr*sqrt(1-b2^t_i)/(1-b1^t_i) * m / (sqrt(v) + eps)
+// variant 2 (the tiny-cuda-nn Adam of the MLP heads, odie/native/runtime.cu:159-160, whose
+//   weights are matrix parameters and so never skipped): as variant 1, but every parameter's
+//   age advances on every step, zero gradient included.
 // Bias corrections are computed per call on the host in double (variant 0) or per parameter
-// on the device (variant 1, ages differ between parameters).
+// on the device (variants 1 and 2, ages may differ between parameters).
 #include <cmath>
 
 #include "common.h"
@@ -45,8 +48,8 @@ struct AdamArgs {
 __device__ inline void adam_one(const AdamArgs& a, int64_t i, float g, float& p, float& m, float& v, bool& touched) {
     g = g * a.inv_scale;
     touched = true;
-    if (a.variant == 1) {
-        if (g == 0.0f) {
+    if (a.variant != 0) {
+        if (a.variant == 1 && g == 0.0f) {
             touched = false;
             return;
         }
@@ -122,13 +125,14 @@ ODIE_API int odie_adam_step(float* master, uint16_t* half_copy, const void* grad
                             uint32_t* steps, int64_t n, int variant, int64_t step, float lr, float beta1, float beta2,
                             float eps, float loss_scale, uint64_t stream) {
     if (n < 0) return fail("odie_adam_step: n must be nonnegative");
-    if (variant != 0 && variant != 1) return fail("odie_adam_step: variant must be 0 (torch) or 1 (per-parameter age)");
+    if (variant < 0 || variant > 2)
+        return fail("odie_adam_step: variant must be 0 (torch), 1 (per-parameter age) or 2 (age, no skip)");
     if (grad_dtype != ODIE_F32 && grad_dtype != ODIE_F16) return fail("odie_adam_step: grad_dtype must be 0 or 1");
     if (variant == 0 && step < 1) return fail("odie_adam_step: step must be >= 1");
     if (!(loss_scale > 0.0f)) return fail("odie_adam_step: loss_scale must be positive");
     if (!(beta1 >= 0.0f && beta1 < 1.0f && beta2 >= 0.0f && beta2 < 1.0f)) return fail("odie_adam_step: betas must be in [0, 1)");
     if (n == 0) return 0;
-    if (!master || !grad || !m || !v || (variant == 1 && !steps)) return fail("odie_adam_step: null pointer");
+    if (!master || !grad || !m || !v || (variant != 0 && !steps)) return fail("odie_adam_step: null pointer");
     const bool aligned = reinterpret_cast<uintptr_t>(master) % 16 == 0 && reinterpret_cast<uintptr_t>(m) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(grad) % (grad_dtype == ODIE_F16 ? 8 : 16) == 0 &&

@@ -1,0 +1,71 @@
+"""The decoder head on the GPU: TCNN FullyFusedMLP 32 -> 64 -> 64 -> 16 (ReLU, no bias, no
+output activation, fp16), as configured at odie/hash_grid.py:32-34 and odie/model.py:186-195.
+
+Decoder keeps an fp32 master of the 7168 weights (W1 [64][32] | W2 [64][64] | W3 [16][64],
+row-major [out][in]) and their fp16 copy, which the kernels read.  `train` runs forward, the
+native step's loss (odie/native/runtime.cu:53-63) and backward in one launch.
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import _lib, synth
+
+INPUT, HIDDEN, OUTPUT = 32, 64, 16
+SHAPES = ((HIDDEN, INPUT), (HIDDEN, HIDDEN), (OUTPUT, HIDDEN))
+PARAMETERS = sum(rows * cols for rows, cols in SHAPES)   # 7168 (odie/config.py:176-177)
+
+
+def initial_weights(seed):
+    """fp32 [7168]: each layer uniform in +-sqrt(6 / (fan_in + fan_out)) from the counter PRNG."""
+    parts = []
+    for index, (rows, cols) in enumerate(SHAPES):
+        bound = math.sqrt(6.0 / (rows + cols))
+        u = synth.uniform(seed, 'decoder%d' % index, rows * cols).astype(np.float64)
+        parts.append(((2.0 * u - 1.0) * bound).astype(np.float32))
+    return np.concatenate(parts)
+
+
+class Decoder:
+    def __init__(self, weights=None, seed=0, device='cuda'):
+        values = initial_weights(seed) if weights is None else np.asarray(weights, dtype=np.float32)
+        if values.shape != (PARAMETERS,):
+            raise ValueError('decoder weights must be fp32 [%d]' % PARAMETERS)
+        self.params = torch.from_numpy(values.copy()).to(device)
+        self.half = self.params.half()
+        self.grad = torch.zeros(PARAMETERS, dtype=torch.float32, device=device)
+
+    def sync_weights(self):
+        """Refresh the fp16 copy from the fp32 master (odie_sync_weights)."""
+        self.half.copy_(self.params)
+
+    def forward(self, x):
+        x = _features(x)
+        out = torch.empty((x.shape[0], OUTPUT), dtype=torch.float16, device=x.device)
+        _lib.check(_lib.library().odie_mlp_forward(x.data_ptr(), x.shape[0], self.half.data_ptr(), out.data_ptr(),
+                                                   _lib.stream_of(x)))
+        return out
+
+    def train(self, x, real=None, *, rgb=None, ids=None, target=None, rows=None, out=None, hidden=None,
+              squares=None, dz=None):
+        """Forward + loss + backward.  Returns dz fp16 [n, 32] (the grid's upstream at loss
+        scale 128); self.grad receives dL/dW at loss scale 16384."""
+        x = _features(x)
+        n = x.shape[0]
+        real = n if real is None else int(real)
+        if (rgb is None) == (target is None) or (rgb is not None and ids is None):
+            raise ValueError('give rgb with ids, or target')
+        if dz is None:
+            dz = torch.empty((n, INPUT), dtype=torch.float16, device=x.device)
+        _lib.check(_lib.library().odie_mlp_train(
+            x.data_ptr(), n, real, self.half.data_ptr(), _lib.ptr(rgb), _lib.ptr(ids), _lib.ptr(target),
+            _lib.ptr(rows), _lib.ptr(out), _lib.ptr(hidden), _lib.ptr(squares), dz.data_ptr(), self.grad.data_ptr(),
+            _lib.stream_of(x)))
+        return dz
+
+
+def _features(x):
+    if x.dtype != torch.float16 or x.ndim != 2 or x.shape[1] != INPUT or not x.is_cuda:
+        raise ValueError('decoder input must be CUDA fp16 [n, %d]' % INPUT)
+    return x.contiguous()

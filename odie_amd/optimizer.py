@@ -3,13 +3,14 @@
 FusedAdam keeps the moments (and, for the per-parameter-age variant, the ages) next to one
 flat fp32 master buffer and updates it -- and an optional fp16 copy -- in one pass per step.
 variant 'torch' follows torch.optim.Adam (odie/optimizer.py:324); variant 'tcnn' skips zero
-gradients and keeps per-parameter ages (odie/native/runtime.cu:212-215).
+gradients and keeps per-parameter ages (the grid, odie/native/runtime.cu:212-215); variant
+'tcnn_dense' keeps per-parameter ages without the skip (the MLP heads, :159-160).
 """
 import torch
 
 from . import _lib
 
-_VARIANTS = {'torch': 0, 'tcnn': 1}
+_VARIANTS = {'torch': 0, 'tcnn': 1, 'tcnn_dense': 2}
 
 
 class FusedAdam:
@@ -17,13 +18,13 @@ class FusedAdam:
         if master.dtype != torch.float32 or not master.is_cuda or not master.is_contiguous():
             raise ValueError('master must be a contiguous CUDA fp32 tensor')
         if variant not in _VARIANTS:
-            raise ValueError('variant must be torch or tcnn')
+            raise ValueError('variant must be torch, tcnn or tcnn_dense')
         self.master, self.lr, self.betas, self.eps = master, float(lr), betas, float(eps)
         self.variant = variant
         self.half_copy = half_copy
         self.m = torch.zeros_like(master)
         self.v = torch.zeros_like(master)
-        self.steps = torch.zeros(master.numel(), dtype=torch.int32, device=master.device) if variant == 'tcnn' else None
+        self.steps = torch.zeros(master.numel(), dtype=torch.int32, device=master.device) if variant != 'torch' else None
         self.step_count = 0
 
     def step(self, grad, loss_scale=1.0):

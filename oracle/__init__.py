@@ -35,6 +35,10 @@ PINS = {
     'select_mean_rank': 'brute-force restatement on tiny resolutions',
     'adam': 'torch.optim.Adam on the CPU (torch-style variant)',
     'compaction/topk': 'numpy.argsort(kind="stable")',
+    'mlp': 'torch.nn.functional.linear/relu in float64 on the CPU (same fp16 weights and inputs); '
+           'layer outputs rounded once to fp16',
+    'mlp_loss': 'closed form of odie/native/runtime.cu:53-63 in IEEE float32/float16 numpy arithmetic; '
+                'hand-computed known answers',
 }
 
 
@@ -405,3 +409,89 @@ def route(ids, width, height, regions_x, regions_y):
     perm, offsets = compact(expert, regions_x * regions_y)
     local = np.stack([u, v], axis=1).astype(np.float32)[perm]
     return expert.astype(np.int32), perm, local, offsets
+
+
+# --------------------------------------------------------------------------------------------
+# Decoder MLP 32 -> 64 -> 64 -> 16 (the FullyFusedMLP head, odie/hash_grid.py:32-34) and the
+# step's loss (odie/native/runtime.cu:53-63).  Weights: fp16 [7168] = W1 [64][32] | W2 [64][64]
+# | W3 [16][64], row-major [out][in].  Layers are computed in float64 and rounded once to fp16;
+# TCNN's own accumulation order is not restated (parity tolerance covers fp32 accumulation).
+
+MLP_SHAPES = ((64, 32), (64, 64), (16, 64))
+
+
+def mlp_weights(flat16):
+    flat16 = np.asarray(flat16, dtype=np.float16)
+    out, start = [], 0
+    for rows, cols in MLP_SHAPES:
+        out.append(flat16[start:start + rows * cols].reshape(rows, cols))
+        start += rows * cols
+    return out
+
+
+def mlp_layer(inputs16, weight16, relu):
+    """fp16 [rows, in] x fp16 [out, in]^T in float64, ReLU, one rounding to fp16; also the
+    magnitude sum |inputs| |W|^T that bounds accumulation-order differences."""
+    x = np.asarray(inputs16, dtype=np.float64)
+    w = np.asarray(weight16, dtype=np.float64)
+    acc = x @ w.T
+    if relu:
+        acc = np.where(acc > 0, acc, 0.0)
+    return acc.astype(np.float16), np.abs(x) @ np.abs(w).T
+
+
+def mlp_forward(x16, flat16):
+    w1, w2, w3 = mlp_weights(flat16)
+    h1, _ = mlp_layer(x16, w1, True)
+    h2, _ = mlp_layer(h1, w2, True)
+    y, _ = mlp_layer(h2, w3, False)
+    return h1, h2, y
+
+
+def mlp_targets(rows, rgb=None, ids=None, target=None):
+    """fp32 targets [rows, 3]: byte * fp32(1/255) (odie/native/runtime.cu:37,56) or given fp32."""
+    if rgb is not None:
+        bytes_ = np.asarray(rgb, dtype=np.uint8).reshape(-1, 3)[np.asarray(ids)[rows]]
+        return bytes_.astype(np.float32) * (np.float32(1.0) / np.float32(255.0))
+    return np.asarray(target, dtype=np.float32).reshape(-1, 3)[rows]
+
+
+def mlp_loss(y16, targets, inputs, real):
+    """dy fp16 [rows, 16] and squares fp32 [rows] of odie/native/runtime.cu:53-63 for output
+    rows y16 whose input indices are `inputs`: d = y - t (fp32), dy = fp16(fp16(2d/(3 real) *
+    128) * 128) for c < 3, squares = fma(d2, d2, fma(d1, d1, d0*d0)) / 3; zero for inputs >= real."""
+    y = np.asarray(y16, dtype=np.float16)[:, :3].astype(np.float32)
+    d = (y - np.asarray(targets, dtype=np.float32)).astype(np.float32)
+    with np.errstate(over='ignore'):
+        scaled = ((np.float32(2.0) * d) / np.float32(3 * real) * np.float32(128.0)).astype(np.float16)
+        dy3 = (scaled.astype(np.float32) * np.float32(128.0)).astype(np.float16)
+    wide = d.astype(np.longdouble)
+    square = np.zeros(len(d), dtype=np.float32)
+    for c in range(3):   # fused multiply-add: one rounding of d^2 + s
+        square = (wide[:, c] * wide[:, c] + square.astype(np.longdouble)).astype(np.float32)
+    squares = (square / np.float32(3.0)).astype(np.float32)
+    real_rows = np.asarray(inputs) < real
+    dy = np.zeros((len(d), 16), dtype=np.float16)
+    dy[:, :3] = np.where(real_rows[:, None], dy3, np.float16(0))
+    return dy, np.where(real_rows, squares, np.float32(0))
+
+
+def mlp_backward(x16, h1, h2, dy16, flat16):
+    """Gradients of the decoder from the given activations: dz fp16 [rows, 32] =
+    fp16(fp16(dL/dx) / 128), dweights float64 [7168], and magnitude bounds of both."""
+    w1, w2, w3 = (w.astype(np.float64) for w in mlp_weights(flat16))
+    x, a1, a2, dy = (np.asarray(v, dtype=np.float16).astype(np.float64) for v in (x16, h1, h2, dy16))
+    pre2 = dy @ w3
+    dh2 = np.where(a2 > 0, pre2, 0.0).astype(np.float16).astype(np.float64)
+    m2 = np.where(a2 > 0, np.abs(dy) @ np.abs(w3), 0.0)
+    pre1 = dh2 @ w2
+    dh1 = np.where(a1 > 0, pre1, 0.0).astype(np.float16).astype(np.float64)
+    m1 = np.where(a1 > 0, (np.abs(dh2) + m2) @ np.abs(w2), 0.0)
+    dx = (dh1 @ w1).astype(np.float16)
+    dz = (dx.astype(np.float32) / np.float32(128.0)).astype(np.float16)
+    mx = (np.abs(dh1) + m1) @ np.abs(w1)
+    dweights = np.concatenate([(dh1.T @ x).ravel(), (dh2.T @ a1).ravel(), (dy.T @ a2).ravel()])
+    magnitude = np.concatenate([((np.abs(dh1) + m1).T @ np.abs(x)).ravel(),
+                                ((np.abs(dh2) + m2).T @ np.abs(a1)).ravel(),
+                                (np.abs(dy).T @ np.abs(a2)).ravel()])
+    return dz, mx / 128.0, dweights, magnitude

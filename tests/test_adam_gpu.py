@@ -11,7 +11,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize('variant,grad_dtype,n', [('torch', torch.float32, 1000003), ('tcnn', torch.float16, 4099),
-                                                  ('torch', torch.float16, 17), ('tcnn', torch.float32, 100000)])
+                                                  ('torch', torch.float16, 17), ('tcnn', torch.float32, 100000),
+                                                  ('tcnn_dense', torch.float32, 7168)])
 def test_adam_matches_oracle(variant, grad_dtype, n):
     start = synth.normal(5, 'params', n).astype(np.float32)
     master = torch.from_numpy(start).cuda()
@@ -25,12 +26,12 @@ def test_adam_matches_oracle(variant, grad_dtype, n):
         g[::5] = 0.0
         grad = torch.from_numpy(g).to(grad_dtype)
         opt.step(grad.cuda(), loss_scale=128.0)
-        p = oracle.adam(0 if variant == 'torch' else 1, p, grad.float().numpy().astype(np.float64), m, v, steps, t,
+        p = oracle.adam({'torch': 0, 'tcnn': 1, 'tcnn_dense': 2}[variant], p, grad.float().numpy().astype(np.float64), m, v, steps, t,
                         1e-2, scale=128.0)
     got = master.cpu().numpy().astype(np.float64)
     assert np.allclose(got, p, rtol=1e-5, atol=1e-6), np.abs(got - p).max()
     assert np.array_equal(half.cpu().numpy().view(np.uint16), master.cpu().numpy().astype(np.float16).view(np.uint16))
-    if variant == 'tcnn':
+    if variant != 'torch':
         assert np.array_equal(opt.steps.cpu().numpy().astype(np.uint32), steps)
 
 

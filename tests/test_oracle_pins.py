@@ -424,3 +424,117 @@ def test_adam_tcnn_variant_skips_zero_gradients(oracle):
     assert abs(p[0] - 0.9) < 1e-12
     p = oracle.adam(1, p, np.array([0.0, 0.5]), m, v, steps, 2, 0.1)
     assert abs(p[1] - 1.9) < 1e-12 and steps.tolist() == [1, 1]
+
+
+def test_adam_tcnn_dense_variant_never_skips(oracle):
+    p = np.array([1.0, 2.0])
+    m, v, steps = np.zeros(2), np.zeros(2), np.zeros(2, dtype=np.uint32)
+    p = oracle.adam(2, p, np.array([0.5, 0.0]), m, v, steps, 1, 0.1)
+    assert steps.tolist() == [1, 1] and p[1] == 2.0 and abs(p[0] - 0.9) < 1e-12
+    # a zero gradient after a nonzero one still moves the parameter by its momentum
+    p = oracle.adam(2, p, np.array([0.0, 0.0]), m, v, steps, 2, 0.1)
+    assert steps.tolist() == [2, 2] and p[0] < 0.9
+
+
+# Decoder MLP and loss ---------------------------------------------------------------------
+
+def _mlp_case(seed, rows):
+    rng = np.random.default_rng(seed)
+    x = (rng.normal(size=(rows, 32)) * 0.5).astype(np.float16)
+    flat = np.concatenate([(rng.uniform(-1, 1, size=r * c) * np.sqrt(6.0 / (r + c))) for r, c in
+                           ((64, 32), (64, 64), (16, 64))]).astype(np.float16)
+    return x, flat
+
+
+def test_mlp_forward_matches_torch_modules(oracle):
+    import torch
+    x, flat = _mlp_case(3, 200)
+    w1, w2, w3 = oracle.mlp_weights(flat)
+    net = torch.nn.Sequential(torch.nn.Linear(32, 64, bias=False), torch.nn.ReLU(),
+                              torch.nn.Linear(64, 64, bias=False), torch.nn.ReLU(),
+                              torch.nn.Linear(64, 16, bias=False)).double()
+    h1, h2, y = oracle.mlp_forward(x, flat)
+    with torch.no_grad():
+        for layer, weight in zip((net[0], net[2], net[4]), (w1, w2, w3)):
+            layer.weight.copy_(torch.from_numpy(weight.astype(np.float64)))
+        # the same network with fp16 rounding after each layer
+        a = torch.from_numpy(x.astype(np.float64))
+        a = net[1](net[0](a)).half().double()
+        assert np.array_equal(a.numpy().astype(np.float16), h1)
+        a = net[3](net[2](a)).half().double()
+        assert np.array_equal(a.numpy().astype(np.float16), h2)
+        a = net[4](a).half()
+        assert np.array_equal(a.numpy(), y)
+
+
+def test_mlp_backward_matches_autograd(oracle):
+    import torch
+    x, flat = _mlp_case(5, 96)
+    h1, h2, _ = oracle.mlp_forward(x, flat)
+    rng = np.random.default_rng(6)
+    dy = np.zeros((96, 16), dtype=np.float16)
+    dy[:, :3] = rng.normal(size=(96, 3)).astype(np.float16)
+    dz, dz_magnitude, dweights, magnitude = oracle.mlp_backward(x, h1, h2, dy, flat)
+    # float64 autograd through the same network without fp16 rounding, with the ReLU masks of
+    # the fp16 forward held fixed (a pre-activation that rounds to fp16 zero flips a mask); the
+    # oracle then differs only by fp16 rounding of activations and gradients
+    w = [torch.tensor(v.astype(np.float64), requires_grad=True) for v in oracle.mlp_weights(flat)]
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    m1, m2 = (torch.tensor((h > 0).astype(np.float64)) for h in (h1, h2))
+    out = (((xt @ w[0].T) * m1) @ w[1].T * m2) @ w[2].T
+    (out * torch.tensor(dy.astype(np.float64))).sum().backward()
+    expected = torch.cat([v.grad.reshape(-1) for v in w]).numpy()
+    assert np.all(np.abs(dweights - expected) <= 2e-2 * magnitude + 1e-12)
+    assert np.abs(dweights - expected).max() < 0.05 * np.abs(expected).max()
+    got = dz.astype(np.float64) * 128.0
+    assert np.all(np.abs(got - xt.grad.numpy()) <= 2e-2 * dz_magnitude * 128.0 + 1e-6)
+    # a transposed hidden weight is caught
+    wrong = flat.copy()
+    wrong[2048:2048 + 4096] = oracle.mlp_weights(flat)[1].T.ravel()
+    _, _, bad, _ = oracle.mlp_backward(x, h1, h2, dy, wrong)
+    assert not np.all(np.abs(bad - expected) <= 2e-2 * magnitude + 1e-12)
+
+
+def _round_f32(value):
+    """Correct rounding of a Fraction to fp32 (ties to even)."""
+    from fractions import Fraction
+    guess = np.float32(float(value))
+    best = None
+    for candidate in (np.nextafter(guess, np.float32(-np.inf)), guess, np.nextafter(guess, np.float32(np.inf))):
+        error = abs(Fraction(float(candidate)) - value)
+        key = (error, int(np.array(candidate).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, candidate)
+    return best[1]
+
+
+def test_mlp_loss_known_answers(oracle):
+    # y = 0.5, byte 255 -> t = 1, d = -0.5; real = 1: 2d/3 * 128 = -42.666.. -> fp16 -42.65625,
+    # times 128 = -5460 exactly; squares = 3 * 0.25 / 3 = 0.25
+    y = np.full((1, 16), 0.5, dtype=np.float16)
+    rgb = np.full((1, 3), 255, dtype=np.uint8)
+    t = oracle.mlp_targets(np.array([0]), rgb=rgb, ids=np.array([0]))
+    assert t.dtype == np.float32 and np.all(t == np.float32(1.0))
+    dy, squares = oracle.mlp_loss(y, t, np.array([0]), 1)
+    assert dy[0, :3].tolist() == [-5460.0] * 3 and not dy[0, 3:].any() and squares[0] == np.float32(0.25)
+    # padding rows: zero gradient and zero square
+    dy, squares = oracle.mlp_loss(y, t, np.array([5]), 5)
+    assert not dy.any() and squares[0] == 0
+    # the byte scaling multiplies by the fp32 reciprocal (not a division): 1/255 rounded first
+    byte = np.array([[7, 0, 0]], dtype=np.uint8)
+    t = oracle.mlp_targets(np.array([0]), rgb=byte, ids=np.array([0]))
+    assert t[0, 0] == np.float32(np.float32(7.0) * np.float32(1.0 / 255.0))
+
+
+def test_mlp_loss_squares_are_fused_sums(oracle):
+    from fractions import Fraction
+    rng = np.random.default_rng(9)
+    y = rng.uniform(-2, 2, size=(300, 16)).astype(np.float16)
+    t = rng.uniform(0, 1, size=(300, 3)).astype(np.float32)
+    _, squares = oracle.mlp_loss(y, t, np.arange(300), 300)
+    for row in range(300):
+        s = np.float32(0)
+        for c in range(3):
+            d = np.float32(np.float32(y[row, c]) - t[row, c])
+            s = _round_f32(Fraction(float(d)) ** 2 + Fraction(float(s)))
+        assert squares[row] == np.float32(s / np.float32(3))
