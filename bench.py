@@ -1,15 +1,18 @@
-"""Headline benchmark: packed 64-expert hash-grid encode forward+backward on 2^22 coords.
+"""Headline benchmark: one training step of the packed 64-expert hash-grid model on 2^22 coords.
 
-Workload: a 2048x1365 image cut into 8x8 tiles, one expert per tile; every expert is a
-16-level hash grid (2 fp16 features per level, 2^16-entry tables, base resolution 16,
-per-level scale 1.38), 70,745,088 parameters in one packed table.  2^22 pixel ids
-(uniform, seed 0) are routed to their tile experts and compacted on the GPU once during
-setup; the upstream gradient [2^22, 32] is fp16 N(0,1) (seed 0).
+Workload (the 64-expert configuration): a synthetic 2048x1365 RGB8 image (6 octaves of value
+noise plus random axis-aligned edges, seed 0) cut into 8x8 tiles, one expert per tile; every
+expert is a 16-level hash grid (2 fp16 features per level, 2^16-entry tables, base
+resolution 16, per-level scale 1.38): 70,745,088 parameters in one packed table, fp32 master
++ fp16 copy.  Decoder 32->64->64->16 fp16 MLP.  2^22 pixel ids uniform over the image (seed 0),
+resident in HBM.
 
-One step = encode forward (features [2^22,32] fp16) + encode backward (fp32 gradient of all
-70.7M parameters, every value written), all resident in HBM.  The CPU baseline runs
-the oracle's bit-exact port of the same fwd+bwd on the first coordinates of the same
-batch, on the host's cores.
+One step = route + compact the ids to their experts, encode forward [2^22, 32] fp16, decoder
+forward + loss + backward (MFMA), encode backward (fp32 gradient of all 70.7M parameters),
+Adam on the grid (per-parameter ages, zero gradients skipped, writes the fp16 copy) and on
+the decoder.  The metric counts the step's queries per second; the roofline line reports the
+dominant kernel.  The CPU baseline times the oracle's port of the same step on a bounded
+sample of the same ids, on the host's cores.
 
 Prints one JSON line.
 """
@@ -30,10 +33,19 @@ N_COORDS = 1 << 22
 WIDTH, HEIGHT, REGIONS = 2048, 1365, 8
 ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=16, base_resolution=16,
                 per_level_scale=1.38)
-# Algorithmic bytes per query (fp16 table, fp32 gradient accumulators):
-#   forward  8 (xy) + 16 levels*4 corners*2 feats*2 B (gathers) + 32*2 B (features)   = 328
-#   backward 8 (xy) + 32*2 B (upstream) + 16*4*2*(4 B read + 4 B write) (scatter)     = 1096
-FWD_BYTES, BWD_BYTES = 328, 1096
+# Algorithmic HBM bytes per query of each stage (element-level accesses, no cache reuse):
+#   route            read id 8, write perm 4 + local xy 8                                = 20
+#   encode_forward   xy 8 + 16 levels*4 corners*2 feats*2 B gathers + 32*2 B features    = 328
+#   decoder          features 64 + perm 4 + id 8 + rgb 3, write dz 64 + squared error 4  = 147
+#   encode_backward  xy 8 + upstream 64 + 16*4*2*(4 B read + 4 B write) scatter          = 1096
+# and per parameter per step:
+#   adam             read master, m, v, grad, age (20), write master, m, v, age (16), fp16 copy (2) = 38
+STAGE_BYTES = {'route': 20, 'encode_forward': 328, 'decoder': 147, 'encode_backward': 1096}
+ADAM_BYTES = 38
+KERNELS = {'route': 'route_count/scan/scatter kernels', 'encode_forward': 'grid_forward_kernel',
+           'decoder': 'mlp_train_kernel + mlp_reduce_kernel',
+           'encode_backward': 'transpose_half2_kernel + owner_kernel', 'grid_adam': 'adam_kernel',
+           'decoder_adam': 'adam_kernel'}
 
 
 def parse():
@@ -60,30 +72,58 @@ def copy_probe():
     print(json.dumps({'copy_probe_bytes_each_way': src.numel() * 4}))
 
 
-def cpu_baseline(xy, offsets, table, upstream, levels, expert_params, budget):
-    """Time the oracle's port of fwd+bwd on a bounded sample of the same routed batch."""
+def cpu_baseline(image, ids, table16, master, decoder16, levels, expert_params, budget):
+    """Time the oracle's port of the step on a bounded sample of the same ids: routing,
+    encode forward, decoder forward/loss/backward and encode backward per query; Adam over the
+    whole table once per batch, measured on a slice and scaled to the table."""
     import numpy as np
     import oracle
     rows = [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
     cores = len(os.sched_getaffinity(0))
-    experts = len(offsets) - 1
-    # probe the rate on a small prefix, then size the sample to the budget
-    def run(count):
-        cut = np.minimum(offsets, count)
+    experts = REGIONS * REGIONS
+    total = table16.size
+    rgb = image.reshape(-1, 3)
+
+    def per_query(count):
+        sample = ids[:count]
         started = time.perf_counter()
-        oracle.hash_forward(xy[:count], table, rows, 2, offsets=cut, expert_params=expert_params, threads=cores)
-        oracle.hash_backward_f32(xy[:count], upstream[:count], rows, 2, experts * expert_params, offsets=cut,
-                                 expert_params=expert_params, threads=cores)
+        _, perm, local, offsets = oracle.route(sample, WIDTH, HEIGHT, REGIONS, REGIONS)
+        raw = oracle.hash_forward(local, table16, rows, 2, offsets=offsets, expert_params=expert_params,
+                                  threads=cores)
+        dz, _ = oracle.mlp_step_f32(raw, decoder16, oracle.mlp_targets(perm, rgb=rgb, ids=sample), perm, count,
+                                    threads=cores)
+        oracle.hash_backward_f32(local, dz, rows, 2, total, offsets=offsets, expert_params=expert_params,
+                                 threads=cores)
         return time.perf_counter() - started
+
+    def adam(count):
+        p = master[:count].astype(np.float64)
+        g = np.where(np.arange(count) % 3 == 0, 0.0, 1e-3)
+        m, v = np.zeros(count), np.zeros(count)
+        steps = np.zeros(count, dtype=np.uint32)
+        started = time.perf_counter()
+        oracle.adam(1, p, g, m, v, steps, 1, 1e-2, scale=128.0)
+        return time.perf_counter() - started
+
+    # per-query rate from two sample sizes (the difference removes once-per-batch costs such
+    # as clearing the gradient), plus the once-per-batch part itself
     probe = 1 << 14
-    rate = probe / run(probe)
-    count = int(min(len(xy), max(probe, rate * budget / 3)))
-    times = [run(count) for _ in range(3)]
-    seconds = sorted(times)[1]
-    return dict(value=count / seconds, unit='queries/s', cores=cores, kind='port',
-                sample='first %d of the 2^22 routed coords (experts 0..%d), fwd+bwd, median of 3, '
-                       'oracle C port with exact fp16 FMA emulation, OpenMP %d threads' % (
-                           count, int(np.searchsorted(offsets, count, side='left')), cores),
+    rate = probe / per_query(probe)
+    small = int(min(len(ids) // 2, max(probe, rate * budget * 0.5 / 9)))
+    t_small = sorted(per_query(small) for _ in range(3))[1]
+    t_large = sorted(per_query(2 * small) for _ in range(3))[1]
+    marginal = max(t_large - t_small, 1e-9) / small
+    fixed = max(t_small - marginal * small, 0.0)
+    slice_ = 1 << 22
+    adam_seconds = sorted(adam(slice_) for _ in range(3))[1] * total / slice_
+    step_seconds = marginal * N_COORDS + fixed + adam_seconds
+    count = 2 * small
+    return dict(value=N_COORDS / step_seconds, unit='queries/s', cores=cores, kind='port',
+                sample='first %d and %d of the 2^22 ids through route+encode fwd+decoder+encode bwd (median '
+                       'of 3 each; per-query rate from the difference, OpenMP %d threads for encode and Adam, '
+                       'torch-CPU fp32 for the decoder), plus Adam over a 2^22-parameter slice scaled to the %d-parameter '
+                       'table, once per 2^22-query batch' % (count // 2, count, cores, total),
+                seconds_per_step=step_seconds,
                 cpu=platform.processor() or platform.machine())
 
 
@@ -99,84 +139,76 @@ def main():
     import numpy as np
     import torch
     from odie_amd import synth
-    from odie_amd.experts import ExpertGrid, route
+    from odie_amd.trainer import ExpertTrainer
 
     device = torch.device('cuda:0')
     torch.cuda.set_device(device)
-    experts = REGIONS * REGIONS
-    grid = ExpertGrid(ENCODING, experts, dtype=torch.float16, device=device)
-    grid.table.copy_(torch.from_numpy(synth.table(0, grid.table.numel()).astype(np.float16)))
-    ids = torch.from_numpy(synth.integers(0, 'ids', N_COORDS, WIDTH * HEIGHT)).to(device)
-    routed = route(ids, WIDTH, HEIGHT, REGIONS, REGIONS)
-    upstream = torch.from_numpy(synth.upstream(0, N_COORDS, grid.width)).to(device)
-    features = torch.empty((N_COORDS, grid.width), dtype=torch.float16, device=device)
-    gradient = torch.empty(grid.table.numel(), dtype=torch.float32, device=device)
+    image = synth.image(0, WIDTH, HEIGHT)
+    trainer = ExpertTrainer(image, ENCODING, REGIONS, REGIONS, N_COORDS, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
+                            device=device)
+    ids_host = synth.integers(0, 'ids', N_COORDS, WIDTH * HEIGHT)
+    ids = torch.from_numpy(ids_host).to(device)
     stream = torch.cuda.current_stream(device)
-
-    def step(events=None):
-        # The backward writes every gradient value (it clears as part of the scatter), so the
-        # step is exactly forward + backward.
-        if events:
-            events[0].record(stream)
-        grid.forward(routed.coords, routed.offsets, out=features)
-        if events:
-            events[1].record(stream)
-        grid.backward(routed.coords, routed.offsets, upstream, gradient=gradient, accumulate=False)
-        if events:
-            events[2].record(stream)
+    table16 = trainer.grid.table.cpu().numpy() if not args.no_cpu else None
+    master = trainer.master.cpu().numpy() if not args.no_cpu else None
+    decoder16 = trainer.decoder.half.cpu().numpy()
 
     for _ in range(args.warmup):
-        step()
+        trainer.step(ids)
     torch.cuda.synchronize(device)
-    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    names = ['start', 'route', 'encode_forward', 'decoder', 'encode_backward', 'grid_adam', 'decoder_adam']
+    marks = [{name: torch.cuda.Event(enable_timing=True) for name in names} for _ in range(args.steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(device)
     start.record(stream)
     for k in range(args.steps):
-        step(marks[k])
+        marks[k]['start'].record(stream)
+        trainer.step(ids, mark=lambda name, k=k: marks[k][name].record(stream))
     stop.record(stream)
     torch.cuda.synchronize(device)
     ms = start.elapsed_time(stop) / args.steps
-    fwd_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
-    bwd_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
+    stage_ms = {names[i]: sum(m[names[i - 1]].elapsed_time(m[names[i]]) for m in marks) / args.steps
+                for i in range(1, len(names))}
+    params = trainer.grid.table.numel()
+    stage_bytes = {name: per * N_COORDS for name, per in STAGE_BYTES.items()}
+    stage_bytes['grid_adam'] = ADAM_BYTES * params
+    stage_bytes['decoder_adam'] = ADAM_BYTES * trainer.decoder.params.numel()
+    stage_gbs = {name: stage_bytes[name] / (stage_ms[name] / 1e3) / 1e9 for name in stage_ms}
     qps = N_COORDS / (ms / 1e3)
-    step_gbs = N_COORDS * (FWD_BYTES + BWD_BYTES) / (ms / 1e3) / 1e9
-    fwd_gbs = N_COORDS * FWD_BYTES / (fwd_ms / 1e3) / 1e9
-    bwd_gbs = N_COORDS * BWD_BYTES / (bwd_ms / 1e3) / 1e9
-    # The dominant launch is the backward: odie_grid_backward runs transpose_half2_kernel then
-    # owner_kernel on the stream, timed together by the events around the call.
-    dominant = ('grid_backward', bwd_ms, bwd_gbs, BWD_BYTES) if bwd_ms >= fwd_ms else \
-        ('grid_forward', fwd_ms, fwd_gbs, FWD_BYTES)
-    kernels = {'grid_backward': 'transpose_half2_kernel + owner_kernel', 'grid_forward': 'grid_forward_kernel'}
+    step_gbs = sum(stage_bytes.values()) / (ms / 1e3) / 1e9
+    dominant = max(stage_ms, key=stage_ms.get)
     traffic_file = ROOT / 'profiles' / 'traffic.json'
     traffic = None
     if traffic_file.exists():
-        entry = json.loads(traffic_file.read_text()).get(dominant[0])
+        entry = json.loads(traffic_file.read_text()).get(dominant)
         traffic = entry['bytes'] if entry else None
+    encode_ms = stage_ms['encode_forward'] + stage_ms['encode_backward']
+    loss = float(trainer.squares.double().mean())
     result = {
         'metric': METRIC, 'value': qps, 'unit': 'queries/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': ms, 'higher_is_better': True, 'scaling': 'weak',
-        'vs_baseline': None, 'dtype': 'fp16 table/features, fp32 gradient', 'data': 'synthetic',
+        'vs_baseline': None, 'dtype': 'fp16 tables/features/MLP (fp32 accumulate), fp32 gradients and Adam',
+        'data': 'synthetic (procedural 2048x1365 RGB8 image, uniform pixel ids, seed 0)',
         'config': {'workload': '64-expert packed hash grid (8x8 tiles of a 2048x1365 image), 16 levels x 2 fp16 '
-                               'features, 2^16-entry tables, 2^22 routed coords, encode fwd+bwd',
-                   'experts': experts, 'coords': N_COORDS, 'params': grid.table.numel(),
+                               'features, 2^16-entry tables; 2^22 ids per step: route + encode fwd + decoder '
+                               '32-64-64-16 fwd/loss/bwd + encode bwd + Adam (grid and decoder)',
+                   'experts': REGIONS * REGIONS, 'coords': N_COORDS, 'params': params,
                    'parallelism': 'single GPU'},
         'achieved_GBps_step': step_gbs, 'pct_hbm_peak_step': 100 * step_gbs / HBM_PEAK_GBS,
-        'kernels_ms': {'forward': fwd_ms, 'backward': bwd_ms},
-        'roofline': {'bound': 'hbm', 'kernel': '%s (%s)' % (dominant[0], kernels[dominant[0]]),
-                     'achieved': dominant[2], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': dominant[2] / HBM_PEAK_GBS, 'traffic': traffic,
-                     'algorithmic_bytes_per_launch': dominant[3] * N_COORDS, 'avg_ms': dominant[1]},
-        'forward_GBps': fwd_gbs, 'backward_GBps': bwd_gbs,
+        'stage_ms': stage_ms, 'stage_GBps': stage_gbs,
+        'encode_fwd_bwd_queries_per_s': N_COORDS / (encode_ms / 1e3),
+        'encode_fwd_bwd_GBps': N_COORDS * (STAGE_BYTES['encode_forward'] + STAGE_BYTES['encode_backward'])
+        / (encode_ms / 1e3) / 1e9,
+        'roofline': {'bound': 'hbm', 'kernel': '%s (%s)' % (dominant, KERNELS[dominant]),
+                     'achieved': stage_gbs[dominant], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': stage_gbs[dominant] / HBM_PEAK_GBS, 'traffic': traffic,
+                     'algorithmic_bytes_per_launch': stage_bytes[dominant], 'avg_ms': stage_ms[dominant]},
+        'loss_after_timed_steps': loss,
     }
     if not args.no_cpu:
-        order = routed.perm.long()
-        xy = routed.coords.cpu().numpy()
-        offsets = routed.offsets.cpu().numpy().astype(np.int64)
-        result['cpu_baseline'] = cpu_baseline(xy, offsets, grid.table.cpu().numpy(), upstream.cpu().numpy(),
-                                              grid.levels, grid.expert_params, args.cpu_seconds)
+        result['cpu_baseline'] = cpu_baseline(image, ids_host, table16, master, decoder16, trainer.grid.levels,
+                                              trainer.grid.expert_params, args.cpu_seconds)
         result['gpu_over_cpu'] = qps / result['cpu_baseline']['value']
-        del order
     print(json.dumps(result))
 
 

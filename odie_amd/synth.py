@@ -73,3 +73,35 @@ def table(seed, count, low=-1e-4, high=1e-4, name='table'):
 def upstream(seed, rows, columns, name='upstream'):
     """fp16 [rows, columns] standard normal upstream gradients."""
     return normal(seed, name, rows * columns).astype(np.float16).reshape(rows, columns)
+
+
+def image(seed, width, height, octaves=6, edges=32):
+    """uint8 [height, width, 3]: a sum of `octaves` octaves of band-limited value noise (a
+    random lattice of 4*2^k cells per side, smoothstep-interpolated, amplitude 2^-k) plus
+    `edges` random axis-aligned rectangles that add a random colour step, normalized to
+    0..255."""
+    xs = np.arange(width, dtype=np.float64) / (width - 1)
+    ys = np.arange(height, dtype=np.float64) / (height - 1)
+    rgb = np.zeros((height, width, 3))
+    for k in range(octaves):
+        cells = 4 << k
+        lattice = uniform(seed, 'octave%d' % k, (cells + 1) * (cells + 1) * 3).astype(np.float64)
+        lattice = lattice.reshape(cells + 1, cells + 1, 3)
+
+        def axis(t):
+            g = t * cells
+            i = np.minimum(g.astype(np.int64), cells - 1)
+            f = g - i
+            return i, f * f * (3.0 - 2.0 * f)
+        ix, fx = axis(xs)
+        iy, fy = axis(ys)
+        rows = lattice[:, ix] * (1 - fx)[None, :, None] + lattice[:, ix + 1] * fx[None, :, None]  # along x
+        rgb += (rows[iy] * (1 - fy)[:, None, None] + rows[iy + 1] * fy[:, None, None]) * 0.5 ** k
+    corners = integers(seed, 'edge_corners', edges * 4, 1 << 30)
+    colours = uniform(seed, 'edge_colours', edges * 3).astype(np.float64).reshape(edges, 3) - 0.5
+    for e in range(edges):
+        x0, x1 = sorted(int(c) * width >> 30 for c in corners[4 * e:4 * e + 2])
+        y0, y1 = sorted(int(c) * height >> 30 for c in corners[4 * e + 2:4 * e + 4])
+        rgb[y0:y1 + 1, x0:x1 + 1] += colours[e]
+    low, high = rgb.min(), rgb.max()
+    return np.round((rgb - low) / (high - low) * 255.0).astype(np.uint8)

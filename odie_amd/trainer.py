@@ -1,0 +1,83 @@
+"""One training step of the packed multi-expert model on the GPU.
+
+This is the native step of the reference (Probe::step, odie/native/runtime.cu:246-312, for
+the hash-grid representation with the router disabled), with the single hash grid replaced
+by one hash grid per image tile:
+
+  ids --route--> (perm, local xy, offsets)            odie_route (no reference counterpart)
+      --encode forward--> raw fp16 [n, 32]            GridEncoding fwd       (:260)
+      --decoder + loss + backward--> dz, dW           decoder fwd/bwd, loss  (:270-273, :53-63)
+      --encode backward--> grid gradient (scale 128)  GridEncoding bwd       (:282-287)
+      --Adam--> grid master + fp16 copy (scale 128), decoder master + fp16 copy (scale 16384)
+
+Every buffer is allocated once, at construction, for `batch` ids; a step allocates nothing
+on the device beyond the library's grow-once workspace.
+"""
+import numpy as np
+import torch
+
+from . import _lib, synth
+from .decoder import Decoder
+from .experts import ExpertGrid, Routing, route
+from .optimizer import FusedAdam
+
+GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:59,305-308)
+
+
+class ExpertTrainer:
+    def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
+                 device='cuda'):
+        image = np.ascontiguousarray(image, dtype=np.uint8)
+        if image.ndim != 3 or image.shape[2] != 3:
+            raise ValueError('image must be uint8 [height, width, 3]')
+        self.height, self.width = image.shape[:2]
+        self.regions = (regions_x, regions_y)
+        self.batch = batch
+        experts = regions_x * regions_y
+        self.rgb = torch.from_numpy(image.reshape(-1)).to(device)
+        self.grid = ExpertGrid(encoding, experts, dtype=torch.float16, device=device)
+        total = self.grid.table.numel()
+        # fp32 master, uniform(-1e-4, 1e-4) as TCNN's HashGrid initializes its tables
+        self.master = torch.from_numpy(synth.table(seed, total)).to(device)
+        self.grid.table.copy_(self.master)
+        self.grid_optimizer = FusedAdam(self.master, grid_lr, variant='tcnn', half_copy=self.grid.table)
+        self.decoder = Decoder(seed=seed, device=device)
+        self.decoder_optimizer = FusedAdam(self.decoder.params, decoder_lr, variant='tcnn_dense',
+                                           half_copy=self.decoder.half)
+        self.routing = Routing(torch.empty(batch, dtype=torch.int32, device=device),
+                               torch.empty((batch, 2), dtype=torch.float32, device=device),
+                               torch.empty(experts + 1, dtype=torch.int32, device=device), None)
+        need = _lib.library().odie_route_workspace(batch, experts)
+        if need < 0:
+            raise ValueError('invalid batch size for routing')
+        self.workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
+        self.raw = torch.empty((batch, self.grid.width), dtype=torch.float16, device=device)
+        self.dz = torch.empty((batch, self.grid.width), dtype=torch.float16, device=device)
+        self.gradient = torch.empty(total, dtype=torch.float32, device=device)
+        self.squares = torch.empty(batch, dtype=torch.float32, device=device)
+        if self.grid.width != 32:
+            raise ValueError('the decoder takes 32 input features (16 levels x 2)')
+
+    def step(self, ids, update=True, mark=None):
+        """Train on int64 pixel ids [n] (n <= batch); returns per-id squared errors fp32 [n].
+        mark(name), if given, is called after each stage is queued (for stage timing)."""
+        n = ids.numel()
+        if not 1 <= n <= self.batch:
+            raise ValueError('batch size must be within 1..%d' % self.batch)
+        mark = mark or (lambda name: None)
+        r = self.routing
+        view = Routing(r.perm[:n], r.coords[:n], r.offsets, None)
+        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace)
+        mark('route')
+        raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
+        mark('encode_forward')
+        self.decoder.train(raw, n, rgb=self.rgb, ids=ids, rows=view.perm, squares=self.squares[:n], dz=self.dz[:n])
+        mark('decoder')
+        self.grid.backward(view.coords, view.offsets, self.dz[:n], gradient=self.gradient, accumulate=False)
+        mark('encode_backward')
+        if update:
+            self.grid_optimizer.step(self.gradient, loss_scale=GRID_SCALE)
+            mark('grid_adam')
+            self.decoder_optimizer.step(self.decoder.grad, loss_scale=HEAD_SCALE)
+            mark('decoder_adam')
+        return self.squares[:n]

@@ -495,3 +495,23 @@ def mlp_backward(x16, h1, h2, dy16, flat16):
                                 ((np.abs(dh2) + m2).T @ np.abs(a1)).ravel(),
                                 (np.abs(dy).T @ np.abs(a2)).ravel()])
     return dz, mx / 128.0, dweights, magnitude
+
+
+def mlp_step_f32(x16, flat16, targets, inputs, real, threads=1):
+    """The CPU-baseline form of the decoder stage (forward, loss, backward) in torch-CPU float32
+    with fp16 rounding of activations and gradients at the same points as mlp_forward /
+    mlp_loss / mlp_backward; returns (dz fp16 [rows, 32], dweights fp32 [7168])."""
+    import torch
+    torch.set_num_threads(max(1, threads))
+    w1, w2, w3 = (torch.from_numpy(w.astype(np.float32)) for w in mlp_weights(flat16))
+    x = torch.from_numpy(np.asarray(x16, dtype=np.float16)).float()
+    h1 = torch.relu(x @ w1.T).half().float()
+    h2 = torch.relu(h1 @ w2.T).half().float()
+    y = (h2 @ w3.T).half()
+    dy, _ = mlp_loss(y.numpy(), targets, inputs, real)
+    g = torch.from_numpy(dy).float()
+    dh2 = ((g @ w3) * (h2 > 0)).half().float()
+    dh1 = ((dh2 @ w2) * (h1 > 0)).half().float()
+    dz = ((dh1 @ w1).half().float() / 128.0).half()
+    dweights = torch.cat([(dh1.T @ x).reshape(-1), (dh2.T @ h1).reshape(-1), (g.T @ h2).reshape(-1)])
+    return dz.numpy(), dweights.numpy()

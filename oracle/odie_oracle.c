@@ -423,6 +423,8 @@ API void ora_residual(const float* prediction, const void* target, int rgb8, int
  * ---------------------------------------------------------------------------- */
 API void ora_adam(int variant, double* param, const double* grad, double* m, double* v, uint32_t* steps,
                   int64_t n, int64_t step, double lr, double beta1, double beta2, double eps, double scale) {
+    /* elementwise: the parallel loop gives the same result as a sequential one */
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
         const double g = grad[i] / scale;
         if (variant == 1 && g == 0.0) continue;

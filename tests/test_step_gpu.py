@@ -1,0 +1,104 @@
+"""One full training step of the packed multi-expert model (odie_amd.trainer.ExpertTrainer)
+against the oracle, stage by stage, each stage from the GPU's own output of the previous one:
+routing and the encode forward bit-exact; the decoder stage through a re-run with its
+hidden activations exported (bit-identical dz) checked as in the decoder tests; the grid
+gradient within the encode-backward tolerance; both Adam updates within the Adam tolerance."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from odie_amd import synth
+from odie_amd.trainer import ExpertTrainer
+
+pytestmark = pytest.mark.gpu
+
+ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=10, base_resolution=4, per_level_scale=1.3)
+
+
+def rows_of(levels):
+    return [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
+
+
+@pytest.mark.parametrize('regions,batch,n', [((2, 2), 4096, 3000), ((3, 2), 2048, 2048)])
+def test_training_step_matches_oracle(regions, batch, n):
+    width, height = 96, 70
+    image = synth.image(3, width, height)
+    trainer = ExpertTrainer(image, ENCODING, *regions, batch, seed=3)
+    ids_host = synth.integers(3, 'step_ids', n, width * height)
+    ids = torch.from_numpy(ids_host).cuda()
+    master0 = trainer.master.cpu().numpy().astype(np.float64)
+    table0 = trainer.grid.table.cpu().numpy()
+    decoder0 = trainer.decoder.params.cpu().numpy().astype(np.float64)
+    weights16 = trainer.decoder.half.cpu().numpy()
+    squares = trainer.step(ids).cpu().numpy()
+    torch.cuda.synchronize()
+
+    # routing and encode forward: bit-exact
+    _, perm, local, offsets = oracle.route(ids_host, width, height, *regions)
+    assert np.array_equal(trainer.routing.perm[:n].cpu().numpy(), perm)
+    assert np.array_equal(trainer.routing.coords[:n].cpu().numpy().view(np.uint32), local.view(np.uint32))
+    rows = rows_of(trainer.grid.levels)
+    raw = oracle.hash_forward(local, table0, rows, 2, offsets=offsets, expert_params=trainer.grid.expert_params)
+    assert np.array_equal(trainer.raw[:n].cpu().numpy().view(np.uint16), raw.view(np.uint16))
+
+    # decoder: the same launch with hidden activations and outputs exported gives the same dz
+    from odie_amd.decoder import Decoder
+    probe = Decoder(weights=decoder0.astype(np.float32))
+    out = torch.empty((n, 16), dtype=torch.float16, device='cuda')
+    hidden = torch.empty((n, 128), dtype=torch.float16, device='cuda')
+    again = torch.empty((n,), dtype=torch.float32, device='cuda')
+    dz = probe.train(trainer.raw[:n], n, rgb=trainer.rgb, ids=ids, rows=trainer.routing.perm[:n], out=out,
+                     hidden=hidden, squares=again).cpu().numpy()
+    assert np.array_equal(dz.view(np.uint16), trainer.dz[:n].cpu().numpy().view(np.uint16))
+    assert np.array_equal(again.cpu().numpy(), squares)
+    h = hidden.cpu().numpy()
+    y = out.cpu().numpy()[perm]
+    w1, w2, w3 = oracle.mlp_weights(weights16)
+    for got, (expected, magnitude) in ((h[:, :64], oracle.mlp_layer(raw, w1, True)),
+                                       (h[:, 64:], oracle.mlp_layer(h[:, :64], w2, True)),
+                                       (y, oracle.mlp_layer(h[:, 64:], w3, False))):
+        assert np.all(np.abs(got.astype(np.float64) - expected) <=
+                      2.0 ** -10 * np.abs(expected.astype(np.float64)) + 2.0 ** -16 * magnitude + 2.0 ** -24)
+    targets = oracle.mlp_targets(perm, rgb=image.reshape(-1, 3), ids=ids_host)
+    dy, ref_squares = oracle.mlp_loss(y, targets, perm, n)
+    assert np.array_equal(squares[perm], ref_squares)
+    ref_dz, dz_magnitude, ref_dw, dw_magnitude = oracle.mlp_backward(raw, h[:, :64], h[:, 64:], dy, weights16)
+    assert np.all(np.abs(dz.astype(np.float64) - ref_dz) <=
+                  2.0 ** -10 * np.abs(ref_dz.astype(np.float64)) + 2.0 ** -10 * dz_magnitude + 2.0 ** -24)
+    decoder_grad = probe.grad.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(decoder_grad - ref_dw) <= 2.0 ** -9 * dw_magnitude + 1e-6)
+
+    # grid gradient from the GPU's dz (loss scale 128)
+    total = trainer.grid.table.numel()
+    grad, magnitude = oracle.hash_backward(local, dz, rows, 2, total, offsets=offsets,
+                                           expert_params=trainer.grid.expert_params)
+    got = trainer.gradient.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - grad) <= 1e-4 * magnitude + 2.0 ** -32 * magnitude.max() + 1e-30)
+
+    # Adam: grid (per-parameter ages, zero gradients skipped, scale 128) and decoder
+    # (per-parameter ages, no skip, scale 16384), each from the GPU's gradient
+    m, v = np.zeros(total), np.zeros(total)
+    steps = np.zeros(total, dtype=np.uint32)
+    expected = oracle.adam(1, master0.copy(), got, m, v, steps, 1, 1e-2, scale=128.0)
+    master = trainer.master.cpu().numpy().astype(np.float64)
+    assert np.allclose(master, expected, rtol=1e-5, atol=1e-7)
+    assert np.array_equal(trainer.grid.table.cpu().numpy(), trainer.master.cpu().numpy().astype(np.float16))
+    assert np.array_equal(trainer.grid_optimizer.steps.cpu().numpy().astype(np.uint32), steps)
+    m, v = np.zeros(decoder0.size), np.zeros(decoder0.size)
+    steps = np.zeros(decoder0.size, dtype=np.uint32)
+    expected = oracle.adam(2, decoder0.copy(), decoder_grad, m, v, steps, 1, 1e-3, scale=16384.0)
+    assert np.allclose(trainer.decoder.params.cpu().numpy(), expected, rtol=1e-5, atol=1e-7)
+    assert np.array_equal(trainer.decoder.half.cpu().numpy(), trainer.decoder.params.cpu().numpy().astype(np.float16))
+
+
+def test_training_reduces_the_loss():
+    width, height = 64, 48
+    image = synth.image(4, width, height)
+    trainer = ExpertTrainer(image, ENCODING, 2, 2, 8192, grid_lr=1e-2, decoder_lr=1e-2, seed=4)
+    losses = []
+    for step in range(60):
+        ids = torch.from_numpy(synth.integers(step, 'train_ids', 8192, width * height)).cuda()
+        losses.append(float(trainer.step(ids).double().mean()))
+    assert np.isfinite(losses).all()
+    assert np.mean(losses[-5:]) < 0.5 * np.mean(losses[:5]), losses[::10]
