@@ -112,13 +112,16 @@ int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstrea
  *   coords[j] local (u, v) of that id                         (fp32 [n, 2])
  *   offsets   first slot of every expert, offsets[E] = n       (int32 [E+1])
  * expert (nullable) receives each input's expert id in input order (int32 [n]).
+ * rgb / colors (both null or both set): colors[j] = r | g << 8 | b << 16 of the pixel
+ *   (y*W + x, with y clamped as above) of slot j, read from the RGB8 image rgb [H*W][3] --
+ *   the training target of the slot, gathered where the id is already in a register.
  * workspace: caller-owned device scratch of odie_route_workspace(n, E) bytes.
  * --------------------------------------------------------------------------------------- */
 int64_t odie_route_workspace(int64_t n, int experts);
 
 int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
-               int32_t* expert, int32_t* perm, float* coords, int32_t* offsets,
-               void* workspace, int64_t workspace_bytes, uint64_t stream);
+               int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+               uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Residual pass.  Same name, signature and meaning as the reference's score_chunk
@@ -189,7 +192,9 @@ int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int gra
  *
  * odie_mlp_train: forward, the step's loss (loss_grad, odie/native/runtime.cu:53-63) and
  * backward in one pass.  Tile row j reads x[j]; its input row is i = rows[j] (rows null:
- * i = j).  Target of input row i: rgb[3*ids[i] + c] * (1/255) (rgb non-null) or target[3*i + c].
+ * i = j).  Target of tile row j, first given source wins: byte c of colors[j] * (1/255)
+ * (colors: uint32 [n] packed as odie_route writes them); rgb[3*ids[i] + c] * (1/255);
+ * target[3*i + c] (fp32).
  * dy_c = fp16(fp16(2*d_c/(3*real)*128)*128) for c < 3 (zero for i >= real), d = y - t.
  * Writes dz fp16 [n][32] = fp16(fp16(dL/dx * 16384) / 128) at row j (the grid's upstream,
  * half_unscale at odie/native/runtime.cu:282), dweights fp32 [7168] = dL/dW * 16384
@@ -199,9 +204,9 @@ int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int gra
  * --------------------------------------------------------------------------------------- */
 int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weights, uint16_t* out, uint64_t stream);
 
-int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights, const uint8_t* rgb,
-                   const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out, uint16_t* hidden,
-                   float* squares, uint16_t* dz, float* dweights, uint64_t stream);
+int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights, const uint32_t* colors,
+                   const uint8_t* rgb, const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out,
+                   uint16_t* hidden, float* squares, uint16_t* dz, float* dweights, uint64_t stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,11 @@ FLAGS = ['--offload-arch=' + ARCH, '-O3', '-std=c++17', '-fPIC', '-ffp-contract=
          '-I' + str(PACKAGE.parent / 'include')]
 
 
+# Per-source additions.  mlp.hip: MFMA results in VGPRs, so the layer outputs feed the fp16
+# conversions without an AGPR-to-VGPR copy per value.
+EXTRA = {'mlp.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+
+
 def hipcc():
     rocm = os.environ.get('ROCM_PATH', '/opt/rocm')
     return str(Path(rocm) / 'bin' / 'hipcc')
@@ -29,7 +34,7 @@ def hipcc():
 
 def _compile(source):
     target = BUILD / (source.stem + '.o')
-    command = [hipcc(), *FLAGS, '-c', str(source), '-o', str(target)]
+    command = [hipcc(), *FLAGS, *EXTRA.get(source.name, []), '-c', str(source), '-o', str(target)]
     result = subprocess.run(command, capture_output=True, text=True)
     if result.returncode:
         raise RuntimeError('hipcc failed for %s:\n%s' % (source.name, result.stderr[-6000:]))

@@ -12,9 +12,10 @@
 // one lane pair, and the accumulator layout of one layer (lane l: sample l%32, rows
 // 8*(v/4) + 4*(l/32) + v%4) is exactly the B operand of the next layer once the weights' K
 // columns are permuted the same way (slot_of below), so activations never leave registers.
-// Weight gradients contract over samples: the operands are transposed through a per-wave LDS
-// buffer and accumulated in registers across all tiles of a wave, then reduced across waves
-// (LDS, fixed order) and across workgroups (a second kernel, fixed order): deterministic.
+// Weight gradients contract over samples: each round of 4 tiles is transposed through a
+// workgroup LDS buffer and contracted by the waves, each owning a quarter of the gradient in
+// registers across all rounds; partials per workgroup are reduced by a second kernel in a
+// fixed order: deterministic.
 #include "common.h"
 #include "../../include/odie_amd.h"
 
@@ -24,6 +25,10 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef int16_t short8 __attribute__((ext_vector_type(8)));
+typedef uint16_t ushort8 __attribute__((ext_vector_type(8)));
 
 constexpr int kIn = 32, kHid = 64, kOut = 16;
 constexpr int kW1 = kHid * kIn, kW2 = kHid * kHid, kW3 = kOut * kHid;
@@ -40,9 +45,6 @@ constexpr int kW3t = kW3p + 16 * kS64;      // W3^T [64][slot(16)]    (dH2 = W3^
 constexpr int kW2t = kW3t + 64 * kS16;      // W2^T [64][slot(64)]    (dH1 = W2^T dH2)
 constexpr int kW1t = kW2t + 64 * kS64;      // W1^T [32][slot(64)]    (dX = W1^T dH1)
 constexpr int kWeightHalfs = kW1t + 32 * kS64;
-constexpr int kTStride = 40;                // transposition rows: 32 samples + pad
-constexpr int kTRows = 128;
-constexpr int kWaveHalfs = kTRows * kTStride;
 
 // K slot of feature k inside a 16-wide K step: the accumulator row order
 // 16t + 8*(e/4) + 4*g + e%4 (lane group g, element e) flattened to 16t + 8g + e.
@@ -59,14 +61,29 @@ __device__ inline f32x16 mfma(half8 a, half8 b, f32x16 c) {
 __device__ inline half8 lds8(const _Float16* p) { return *reinterpret_cast<const half8*>(p); }
 __device__ inline f32x16 zero16() { return f32x16{}; }
 
-// Make LDS writes of every lane of this wave visible to reads of other lanes of the wave.
-__device__ inline void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// fp16 of acc[base .. base+7], two values per conversion (v_cvt_pk_f16_f32, round to nearest even).
+__device__ inline half8 round8(const f32x16& acc, int base) {
+    const half2v p0 = __builtin_convertvector((float2v){acc[base + 0], acc[base + 1]}, half2v);
+    const half2v p1 = __builtin_convertvector((float2v){acc[base + 2], acc[base + 3]}, half2v);
+    const half2v p2 = __builtin_convertvector((float2v){acc[base + 4], acc[base + 5]}, half2v);
+    const half2v p3 = __builtin_convertvector((float2v){acc[base + 6], acc[base + 7]}, half2v);
+    return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-__device__ inline _Float16 relu_half(float x) { return static_cast<_Float16>(x > 0.0f ? x : 0.0f); }
+// ReLU of fp16 values on their bit patterns: a signed 16-bit max with 0 maps every negative
+// value and -0 to +0 and keeps positive values (v_pk_max_i16), so relu(fp16(x)) equals
+// fp16(x > 0 ? x : 0) bit for bit, and "h > 0" afterwards is "bits != 0".
+__device__ inline half8 relu8(half8 x) {
+    return __builtin_bit_cast(half8, __builtin_elementwise_max(__builtin_bit_cast(short8, x), short8{}));
+}
+
+// dh where the forward activation h is nonzero, +0 elsewhere: min(bits(h), 1) is 1 or 0 per
+// value and multiplies the bit pattern of dh (v_pk_min_u16, v_pk_mul_lo_u16).
+__device__ inline half8 mask8(half8 dh, half8 h) {
+    const ushort8 keep = __builtin_elementwise_min(__builtin_bit_cast(ushort8, h), (ushort8)(uint16_t{1}));
+    return __builtin_bit_cast(half8, __builtin_bit_cast(ushort8, dh) * keep);
+}
 
 // Weights into LDS in the six operand layouts (once per workgroup).
 __device__ void stage_weights(const uint16_t* weights, _Float16* w) {
@@ -93,6 +110,7 @@ struct MlpArgs {
     const uint16_t* weights;  // [7168] fp16
     int64_t n;
     int64_t real;             // rows whose input index is >= real are padding (dy = 0)
+    const uint32_t* colors;   // packed RGB8 target of tile row j, or null
     const uint8_t* rgb;       // image bytes [pixels][3] (target by pixel id), or null
     const int64_t* ids;       // pixel id per input row (with rgb)
     const float* target;      // fp32 [input rows][3] (without rgb)
@@ -113,22 +131,16 @@ __device__ inline void forward_tile(const _Float16* w, int g, int s, const half8
         f32x16 acc = zero16();
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) acc = mfma(lds8(w + kW1a + (mb * 32 + s) * kS32 + kt * 16 + 8 * g), xb[kt], acc);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            h1[2 * mb][e] = relu_half(acc[e]);
-            h1[2 * mb + 1][e] = relu_half(acc[8 + e]);
-        }
+        h1[2 * mb] = relu8(round8(acc, 0));
+        h1[2 * mb + 1] = relu8(round8(acc, 8));
     }
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
         f32x16 acc = zero16();
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW2p + (mb * 32 + s) * kS64 + 16 * t + 8 * g), h1[t], acc);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            h2[2 * mb][e] = relu_half(acc[e]);
-            h2[2 * mb + 1][e] = relu_half(acc[8 + e]);
-        }
+        h2[2 * mb] = relu8(round8(acc, 0));
+        h2[2 * mb + 1] = relu8(round8(acc, 8));
     }
     acc3 = zero16();
 #pragma unroll
@@ -167,43 +179,119 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_forward_kernel(const uint16_t* 
         f32x16 acc3;
         load_x(x, row, valid, g, xb);
         forward_tile(w, g, s, xb, h1, h2, acc3);
-        half8 y;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) y[v] = static_cast<_Float16>(acc3[v]);
+        const half8 y = round8(acc3, 0);
         if (valid) store_out(out, row, g, y);
     }
 }
 
+// Loads of one tile, issued a tile ahead of their use.
+struct TileInput {
+    half8 xb[2];
+    int32_t input;    // kept 32-bit: widening here would wait for the load right away
+    uint32_t color;
+};
+
+// The next tile's row of this lane, advanced by a fixed stride each round and kept in one
+// pinned 32-bit register: every prefetch load then addresses base (a kernel argument, in
+// scalar registers) + a 32-bit byte offset derived from it, with no temporary address
+// register whose reuse could force an early wait on the loads in flight.
+__device__ inline uint32_t pin(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+template <class T> __device__ inline T load_at(const T* base, uint32_t byte_offset) {
+    return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_offset);
+}
+
+// Loop-carried row and byte offsets of the next tile's loads (each advanced by a constant).
+struct TileCursor {
+    uint32_t row;       // row index
+    uint32_t off4;      // row * 4
+    uint32_t off64;     // row * 64 + 16 * g
+};
+
+__device__ inline void advance(TileCursor& c, uint32_t rows) {
+    c.row = pin(c.row + rows);
+    c.off4 = pin(c.off4 + rows * 4u);
+    c.off64 = pin(c.off64 + rows * 64u);
+}
+
+__device__ inline void fetch_tile(const MlpArgs& a, const TileCursor& c, TileInput& in) {
+    const bool valid = c.row < a.n;
+    // the small loads first: memory counters drain in issue order, so an early wait on them
+    // leaves the 64-byte x loads in flight
+    in.input = valid ? (a.rows ? load_at(a.rows, c.off4) : static_cast<int32_t>(c.row)) : 0;
+    in.color = valid && a.colors ? load_at(a.colors, c.off4) : 0u;
+    const half8* x = reinterpret_cast<const half8*>(a.x);
+    in.xb[0] = valid ? load_at(x, c.off64) : half8{};
+    in.xb[1] = valid ? load_at(x + 2, c.off64) : half8{};   // +32 bytes on the base, not the offset
+}
+
+// Shared transposition buffer of one round (4 tiles = 128 samples): feature-major rows of
+// 128 samples, padded so that 16-byte reads of 16 consecutive rows hit distinct banks.
+constexpr int kRoundSamples = 32 * kMlpWaves;
+constexpr int kRS = kRoundSamples + 8;
+// phase 1 rows: dy outputs 0..2, h2 (64), dh1 (64), x (32); phase 2 rows: dh2 (64), h1 (64)
+constexpr int kDyRow = 0, kH2Row = 3, kDh1Row = 67, kXRow = 131;
+constexpr int kRoundRows = 163;
+
+// Writes this wave's 32 samples of 32*blocks features held in accumulator-row order
+// (h[t][e] = feature feature_of(t, g, e)) into rows first.. of the round buffer.
+__device__ inline void put_features(_Float16* T, int first, int column, const half8* h, int blocks, int g) {
+    for (int t = 0; t < 2 * blocks; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) T[(first + feature_of(t, g, e)) * kRS + column] = h[t][e];
+}
+
+// One 32x32 block of a weight gradient: sum over the round's 128 samples of rows a0..
+// (M side, rows a0 + s for lanes s < a_rows) times rows b0.. (N side) of the round buffer,
+// alternating two accumulators so that consecutive MFMAs do not depend on each other.
+__device__ inline void round_block(const _Float16* T, int a0, int b0, int a_rows, int g, int s, f32x16& acc0,
+                                   f32x16& acc1) {
+#pragma unroll
+    for (int kt = 0; kt < kRoundSamples / 16; kt += 2) {
+        const half8 a0v = s < a_rows ? lds8(T + (a0 + s) * kRS + kt * 16 + 8 * g) : half8{};
+        const half8 a1v = s < a_rows ? lds8(T + (a0 + s) * kRS + kt * 16 + 16 + 8 * g) : half8{};
+        acc0 = mfma(a0v, lds8(T + (b0 + s) * kRS + kt * 16 + 8 * g), acc0);
+        acc1 = mfma(a1v, lds8(T + (b0 + s) * kRS + kt * 16 + 16 + 8 * g), acc1);
+    }
+}
+
+// Work split: each wave computes the forward, loss and input gradient of its own tile in
+// registers; the weight gradients are contracted per round of 4 tiles through the shared
+// buffer in two phases (1: dW3 = dy x h2 and dW1 = dh1 x x; 2: dW2 = dh2 x h1), each wave
+// owning two of the eight 32x32 gradient blocks (waves 0,1: dW3 column blocks; waves 2,3: dW1
+// row blocks; every wave one dW2 block), so no cross-wave reduction is needed.
 __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
     __shared__ _Float16 w[kWeightHalfs];
-    __shared__ __attribute__((aligned(16))) _Float16 transposed[kMlpWaves * kWaveHalfs];
+    __shared__ __attribute__((aligned(16))) _Float16 T[kRoundRows * kRS];
     stage_weights(a.weights, w);
     __syncthreads();
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
-    _Float16* T = transposed + wave * kWaveHalfs;
-    f32x16 gw3[2], gw2[2][2], gw1[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        gw3[i] = zero16();
-        gw1[i] = zero16();
-        gw2[i][0] = zero16();
-        gw2[i][1] = zero16();
-    }
+    const int column = 32 * wave + s;   // this lane's sample column in the round buffer
+    f32x16 gA = zero16(), gA1 = zero16(), gB = zero16(), gB1 = zero16();
     const int64_t tiles = (a.n + 31) / 32;
-    const int64_t waves = static_cast<int64_t>(gridDim.x) * kMlpWaves;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kMlpWaves;
     const float inv255 = 1.0f / 255.0f;
     const float denominator = static_cast<float>(3 * a.real);
-    for (int64_t tile = static_cast<int64_t>(blockIdx.x) * kMlpWaves + wave; tile < tiles; tile += waves) {
+    TileCursor cursor;
+    {
+        const uint32_t row0 = static_cast<uint32_t>((blockIdx.x * kMlpWaves + wave) * 32 + s);
+        cursor = {pin(row0), pin(row0 * 4u), pin(row0 * 64u + 16u * g)};
+    }
+    const uint32_t row_stride = static_cast<uint32_t>(stride * 32);
+    // One round on the tile whose inputs are in `current` (loaded a round earlier).
+    auto round = [&](int64_t base, const TileInput& current) {
+        const int64_t tile = base + wave;
         const int64_t row = tile * 32 + s;
-        const bool valid = row < a.n;
-        const int64_t input = valid ? (a.rows ? a.rows[row] : row) : 0;
-        half8 xb[2], h1[4], h2[4];
+        const bool valid = tile < tiles && row < a.n;
+        half8 xb[2] = {current.xb[0], current.xb[1]}, h1[4], h2[4];
         f32x16 acc3;
-        load_x(a.x, row, valid, g, xb);
         forward_tile(w, g, s, xb, h1, h2, acc3);
-        half8 y, dy{};
-#pragma unroll
-        for (int v = 0; v < 8; ++v) y[v] = static_cast<_Float16>(acc3[v]);
+        const int64_t input = current.input;
+        const half8 y = round8(acc3, 0);
+        half8 dy{};
         if (valid && a.out) store_out(a.out, input, g, y);
         // loss (odie/native/runtime.cu:53-63): outputs 0..2 live in lane group 0, v = 0..2
         if (valid && g == 0) {
@@ -211,7 +299,8 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
             if (input < a.real) {
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
-                    const float t = a.rgb ? __fmul_rn(static_cast<float>(a.rgb[3 * a.ids[input] + c]), inv255)
+                    const float t = a.colors ? __fmul_rn(static_cast<float>((current.color >> (8 * c)) & 0xffu), inv255)
+                                  : a.rgb ? __fmul_rn(static_cast<float>(a.rgb[3 * a.ids[input] + c]), inv255)
                                           : a.target[3 * input + c];
                     const float d = static_cast<float>(y[c]) - t;
                     square = fmaf(d, d, square);
@@ -233,142 +322,114 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                 *reinterpret_cast<uint2*>(hrow + 64 + feature_of(t, g, 4)) = make_uint2(b2.z, b2.w);
             }
         }
-        // dW3 = sum_samples dy (x) h2: T rows 0..15 = dy, 16..79 = h2 (feature-major, samples contiguous)
-#pragma unroll
-        for (int v = 0; v < 8; ++v) T[(8 * (v / 4) + 4 * g + v % 4) * kTStride + s] = dy[v];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) T[(16 + feature_of(t, g, e)) * kTStride + s] = h2[t][e];
-        wave_sync();
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const half8 ay = s < kOut ? lds8(T + s * kTStride + kt * 16 + 8 * g) : half8{};
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
-                gw3[nb] = mfma(ay, lds8(T + (16 + nb * 32 + s) * kTStride + kt * 16 + 8 * g), gw3[nb]);
-        }
-        // dH2 = relu'(h2) * (W3^T dy)
-        half8 dh2[4];
+        // input gradients: dH2 = relu'(h2) * (W3^T dy), dH1 = relu'(h1) * (W2^T dH2), dX = W1^T dH1
+        half8 dh2[4], dh1[4];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-            f32x16 acc = mfma(lds8(w + kW3t + (mb * 32 + s) * kS16 + 8 * g), dy, zero16());
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                dh2[2 * mb][e] = h2[2 * mb][e] > static_cast<_Float16>(0.0f) ? static_cast<_Float16>(acc[e]) : _Float16{};
-                dh2[2 * mb + 1][e] =
-                    h2[2 * mb + 1][e] > static_cast<_Float16>(0.0f) ? static_cast<_Float16>(acc[8 + e]) : _Float16{};
-            }
+            const f32x16 acc = mfma(lds8(w + kW3t + (mb * 32 + s) * kS16 + 8 * g), dy, zero16());
+            dh2[2 * mb] = mask8(round8(acc, 0), h2[2 * mb]);
+            dh2[2 * mb + 1] = mask8(round8(acc, 8), h2[2 * mb + 1]);
         }
-        wave_sync();
-        // dW2 = sum dh2 (x) h1: T rows 0..63 = dh2, 64..127 = h1
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                T[feature_of(t, g, e) * kTStride + s] = dh2[t][e];
-                T[(64 + feature_of(t, g, e)) * kTStride + s] = h1[t][e];
-            }
-        wave_sync();
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                const half8 ad = lds8(T + (mb * 32 + s) * kTStride + kt * 16 + 8 * g);
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb)
-                    gw2[mb][nb] = mfma(ad, lds8(T + (64 + nb * 32 + s) * kTStride + kt * 16 + 8 * g), gw2[mb][nb]);
-            }
-        // dH1 = relu'(h1) * (W2^T dH2)
-        half8 dh1[4];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
             f32x16 acc = zero16();
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW2t + (mb * 32 + s) * kS64 + 16 * t + 8 * g), dh2[t], acc);
+            dh1[2 * mb] = mask8(round8(acc, 0), h1[2 * mb]);
+            dh1[2 * mb + 1] = mask8(round8(acc, 8), h1[2 * mb + 1]);
+        }
+        {
+            f32x16 acc = zero16();
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                dh1[2 * mb][e] = h1[2 * mb][e] > static_cast<_Float16>(0.0f) ? static_cast<_Float16>(acc[e]) : _Float16{};
-                dh1[2 * mb + 1][e] =
-                    h1[2 * mb + 1][e] > static_cast<_Float16>(0.0f) ? static_cast<_Float16>(acc[8 + e]) : _Float16{};
+            for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW1t + s * kS64 + 16 * t + 8 * g), dh1[t], acc);
+            if (valid) {
+                uint16_t* p = a.dz + row * kIn;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value
+                    const half8 h = round8(acc, 8 * q) * (half8)(static_cast<_Float16>(0.0078125f));
+                    const u32x4 bits = __builtin_bit_cast(u32x4, h);
+                    *reinterpret_cast<uint2*>(p + 16 * q + 4 * g) = make_uint2(bits.x, bits.y);
+                    *reinterpret_cast<uint2*>(p + 16 * q + 8 + 4 * g) = make_uint2(bits.z, bits.w);
+                }
             }
         }
-        wave_sync();
-        // dW1 = sum dh1 (x) x: T rows 0..63 = dh1, 64..95 = x
+        // phase 1: dW3 = sum dy (x) h2 (waves 0, 1), dW1 = sum dh1 (x) x (waves 2, 3)
+        if (g == 0)
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) T[feature_of(t, g, e) * kTStride + s] = dh1[t][e];
+            for (int c = 0; c < 3; ++c) T[(kDyRow + c) * kRS + column] = dy[c];
+        put_features(T, kH2Row, column, h2, 2, g);
+        put_features(T, kDh1Row, column, dh1, 2, g);
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) T[(64 + kt * 16 + 8 * g + e) * kTStride + s] = xb[kt][e];
-        wave_sync();
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const half8 bx = lds8(T + (64 + s) * kTStride + kt * 16 + 8 * g);
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) gw1[mb] = mfma(lds8(T + (mb * 32 + s) * kTStride + kt * 16 + 8 * g), bx, gw1[mb]);
-        }
-        wave_sync();
-        // dX = W1^T dH1, then the grid's unscale: fp16(fp16(dx) / 128)
-        f32x16 acc = zero16();
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW1t + s * kS64 + 16 * t + 8 * g), dh1[t], acc);
-        if (valid) {
-            uint16_t* p = a.dz + row * kIn;
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                half8 h;
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    h[j] = static_cast<_Float16>(static_cast<float>(static_cast<_Float16>(acc[8 * q + j])) * (1.0f / 128.0f));
-                const u32x4 bits = __builtin_bit_cast(u32x4, h);
-                *reinterpret_cast<uint2*>(p + 16 * q + 4 * g) = make_uint2(bits.x, bits.y);
-                *reinterpret_cast<uint2*>(p + 16 * q + 8 + 4 * g) = make_uint2(bits.z, bits.w);
-            }
-        }
-    }
-    // Reduce the waves' weight gradients in a fixed order through LDS, then write this
-    // workgroup's partial.
-    __syncthreads();
-    float* sum = reinterpret_cast<float*>(transposed);   // 7168 floats fit in the transposition buffers
-    for (int turn = 0; turn < kMlpWaves; ++turn) {
-        if (wave == turn) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = 8 * (v / 4) + 4 * g + v % 4;
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    float* p1 = sum + (mb * 32 + r) * kIn + s;
-                    *p1 = turn ? *p1 + gw1[mb][v] : gw1[mb][v];
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb) {
-                        float* p2 = sum + kW1 + (mb * 32 + r) * kHid + nb * 32 + s;
-                        *p2 = turn ? *p2 + gw2[mb][nb][v] : gw2[mb][nb][v];
-                    }
-                }
-                if (v < 8) {
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb) {
-                        float* p3 = sum + kW1 + kW2 + r * kHid + nb * 32 + s;
-                        *p3 = turn ? *p3 + gw3[nb][v] : gw3[nb][v];
-                    }
-                }
-            }
-        }
+            for (int e = 0; e < 8; ++e) T[(kXRow + kt * 16 + 8 * g + e) * kRS + column] = xb[kt][e];
         __syncthreads();
+        if (wave < 2) round_block(T, kDyRow, kH2Row + 32 * wave, 3, g, s, gA, gA1);
+        else round_block(T, kDh1Row + 32 * (wave - 2), kXRow, 32, g, s, gA, gA1);
+        __syncthreads();
+        // phase 2: dW2 = sum dh2 (x) h1; rows 0..63 = dh2, 64..127 = h1
+        put_features(T, 0, column, dh2, 2, g);
+        put_features(T, 64, column, h1, 2, g);
+        __syncthreads();
+        round_block(T, 32 * (wave >> 1), 64 + 32 * (wave & 1), 32, g, s, gB, gB1);
+        __syncthreads();
+
+    };
+    // Unrolled by two with ping-pong input buffers, so that a round never copies the next
+    // round's prefetch (a copy would have to wait for it).
+    TileInput even, odd;
+    fetch_tile(a, cursor, even);
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * kMlpWaves; base < tiles; base += 2 * stride) {
+        advance(cursor, row_stride);
+        fetch_tile(a, cursor, odd);
+        round(base, even);
+        if (base + stride >= tiles) break;
+        advance(cursor, row_stride);
+        fetch_tile(a, cursor, even);
+        round(base + stride, odd);
     }
-    for (int i = threadIdx.x; i < kParams; i += kMlpBlock) a.partials[static_cast<int64_t>(blockIdx.x) * kParams + i] = sum[i];
+    // This workgroup's partial: each wave writes its own blocks (accumulator element v of
+    // lane (g, s) is row 8*(v/4) + 4g + v%4, column s of the block).
+    gA += gA1;
+    gB += gB1;
+    float* out = a.partials + static_cast<int64_t>(blockIdx.x) * kParams;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int r = 8 * (v / 4) + 4 * g + v % 4;
+        out[kW1 + (32 * (wave >> 1) + r) * kHid + 32 * (wave & 1) + s] = gB[v];
+        if (wave < 2) {
+            if (v < 8) out[kW1 + kW2 + r * kHid + 32 * wave + s] = gA[v];
+        } else {
+            out[(32 * (wave - 2) + r) * kIn + s] = gA[v];
+        }
+    }
 }
 
-// dweights[p] = sum over workgroups of partials[b][p], in workgroup order.
+// dweights[p] = sum over workgroups of partials[b][p] in a fixed order: four lane groups of a
+// 256-thread block take the workgroups b = q, q+4, q+8, ... (q = group), eight loads in flight
+// per step, and the four group sums are added in group order.
+constexpr int kReduceParams = 64;
 __global__ __launch_bounds__(256) void mlp_reduce_kernel(const float* partials, int blocks, float* dweights) {
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= kParams) return;
+    __shared__ float group_sum[4][kReduceParams];
+    const int local = threadIdx.x % kReduceParams, q = threadIdx.x / kReduceParams;
+    const int p = blockIdx.x * kReduceParams + local;
     float total = 0.0f;
-    for (int b = 0; b < blocks; ++b) total += partials[static_cast<int64_t>(b) * kParams + p];
-    dweights[p] = total;
+    if (p < kParams) {
+        int b = q;
+        for (; b + 28 < blocks; b += 32) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = partials[static_cast<int64_t>(b + 4 * j) * kParams + p];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) total += v[j];
+        }
+        for (; b < blocks; b += 4) total += partials[static_cast<int64_t>(b) * kParams + p];
+    }
+    group_sum[q][local] = total;
+    __syncthreads();
+    if (q == 0 && p < kParams)
+        dweights[p] = ((group_sum[0][local] + group_sum[1][local]) + group_sum[2][local]) + group_sum[3][local];
 }
 
 int mlp_blocks(int64_t n) {
@@ -392,12 +453,15 @@ ODIE_API int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weig
     return check_launch("odie_mlp_forward");
 }
 
-ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights, const uint8_t* rgb,
-                            const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out,
-                            uint16_t* hidden, float* squares, uint16_t* dz, float* dweights, uint64_t stream) {
+ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+                            const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
+                            const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz,
+                            float* dweights, uint64_t stream) {
     if (n < 0 || real < 1) return fail("odie_mlp_train: need n >= 0 and real >= 1");
+    if (n >= (int64_t{1} << 26)) return fail("odie_mlp_train: n must be below 2^26 (32-bit byte offsets)");
     if (!weights || !dweights || (n && (!x || !dz))) return fail("odie_mlp_train: null pointer");
-    if (n && !(rgb ? ids != nullptr : target != nullptr)) return fail("odie_mlp_train: need rgb with ids, or target");
+    if (n && !colors && !(rgb ? ids != nullptr : target != nullptr))
+        return fail("odie_mlp_train: need colors, rgb with ids, or target");
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(dz) % 8 ||
         (out && reinterpret_cast<uintptr_t>(out) % 8))
         return fail("odie_mlp_train: x must be 16-byte, dz and out 8-byte aligned");
@@ -406,9 +470,9 @@ ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const ui
     const int blocks = mlp_blocks(n);
     float* partials = static_cast<float*>(workspace(static_cast<size_t>(blocks) * kParams * sizeof(float), s));
     if (!partials) return -1;
-    MlpArgs a{x, weights, n, real, rgb, ids, target, rows, out, hidden, squares, dz, partials};
+    MlpArgs a{x, weights, n, real, colors, rgb, ids, target, rows, out, hidden, squares, dz, partials};
     mlp_train_kernel<<<blocks, kMlpBlock, 0, s>>>(a);
     if (check_launch("odie_mlp_train")) return -1;
-    mlp_reduce_kernel<<<(kParams + 255) / 256, 256, 0, s>>>(partials, blocks, dweights);
+    mlp_reduce_kernel<<<(kParams + kReduceParams - 1) / kReduceParams, 256, 0, s>>>(partials, blocks, dweights);
     return check_launch("odie_mlp_train reduce");
 }

@@ -34,6 +34,8 @@ struct RouteArgs {
     int32_t* perm;
     float* coords;
     int32_t* offsets;
+    const uint8_t* rgb;     // image bytes [height*width][3], or null
+    uint32_t* colors;       // packed r | g << 8 | b << 16 of each slot's pixel, or null
     int32_t* counts;   // [experts * parts]
     int32_t* block_sums;  // [ceil(experts * parts / kScanSegment)]
     int64_t n;
@@ -232,6 +234,10 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
             const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
             reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
             if (a.expert_out) a.expert_out[i] = expert;
+            if (a.colors) {
+                const uint8_t* pixel = a.rgb + 3 * (static_cast<uint64_t>(y) * a.width + x);
+                a.colors[slot] = pixel[0] | (uint32_t(pixel[1]) << 8) | (uint32_t(pixel[2]) << 16);
+            }
         }
     }
 }
@@ -266,8 +272,8 @@ ODIE_API int64_t odie_route_workspace(int64_t n, int experts) {
 }
 
 ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
-                        int32_t* expert, int32_t* perm, float* coords, int32_t* offsets,
-                        void* workspace, int64_t workspace_bytes, uint64_t stream) {
+                        int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+                        uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_route: n must be within [0, 2^31-1]");
     if (regions_x < 1 || regions_y < 1 || regions_x > kMaxRegions || regions_y > kMaxRegions)
         return fail("odie_route: regions per axis must be within 1..64");
@@ -279,6 +285,7 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     if (!offsets) return fail("odie_route: offsets is null");
     const int64_t need = odie_route_workspace(n, experts);
     if (n > 0 && (!ids || !perm || !coords)) return fail("odie_route: ids, perm and coords must be non-null");
+    if ((rgb == nullptr) != (colors == nullptr)) return fail("odie_route: rgb and colors go together");
     if (n > 0 && (!workspace || workspace_bytes < need))
         return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_route: coords must be 8-byte aligned");
@@ -288,6 +295,8 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     a.perm = perm;
     a.coords = coords;
     a.offsets = offsets;
+    a.rgb = rgb;
+    a.colors = colors;
     a.counts = static_cast<int32_t*>(workspace);
     {
         int part, parts;

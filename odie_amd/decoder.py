@@ -47,19 +47,19 @@ class Decoder:
                                                    _lib.stream_of(x)))
         return out
 
-    def train(self, x, real=None, *, rgb=None, ids=None, target=None, rows=None, out=None, hidden=None,
+    def train(self, x, real=None, *, colors=None, rgb=None, ids=None, target=None, rows=None, out=None, hidden=None,
               squares=None, dz=None):
         """Forward + loss + backward.  Returns dz fp16 [n, 32] (the grid's upstream at loss
         scale 128); self.grad receives dL/dW at loss scale 16384."""
         x = _features(x)
         n = x.shape[0]
         real = n if real is None else int(real)
-        if (rgb is None) == (target is None) or (rgb is not None and ids is None):
-            raise ValueError('give rgb with ids, or target')
+        if colors is None and ((rgb is None) == (target is None) or (rgb is not None and ids is None)):
+            raise ValueError('give colors, rgb with ids, or target')
         if dz is None:
             dz = torch.empty((n, INPUT), dtype=torch.float16, device=x.device)
         _lib.check(_lib.library().odie_mlp_train(
-            x.data_ptr(), n, real, self.half.data_ptr(), _lib.ptr(rgb), _lib.ptr(ids), _lib.ptr(target),
+            x.data_ptr(), n, real, self.half.data_ptr(), _lib.ptr(colors), _lib.ptr(rgb), _lib.ptr(ids), _lib.ptr(target),
             _lib.ptr(rows), _lib.ptr(out), _lib.ptr(hidden), _lib.ptr(squares), dz.data_ptr(), self.grad.data_ptr(),
             _lib.stream_of(x)))
         return dz

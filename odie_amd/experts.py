@@ -19,14 +19,16 @@ def tile_bounds(size, regions):
 
 class Routing:
     """Device buffers of one routed batch: perm, local coords, offsets (and optional
-    per-input expert ids)."""
+    per-input expert ids and per-slot packed RGB8 targets)."""
 
-    def __init__(self, perm, coords, offsets, expert):
+    def __init__(self, perm, coords, offsets, expert, colors=None):
         self.perm, self.coords, self.offsets, self.expert = perm, coords, offsets, expert
+        self.colors = colors
 
 
-def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None):
-    """Route int64 pixel ids [N] (CUDA) to regions_x*regions_y tile experts and compact."""
+def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None, rgb=None):
+    """Route int64 pixel ids [N] (CUDA) to regions_x*regions_y tile experts and compact.  With
+    rgb (CUDA uint8 [H*W*3]) each slot also receives its pixel's packed colour."""
     if ids.dtype != torch.int64 or ids.ndim != 1 or not ids.is_cuda:
         raise ValueError('ids must be a CUDA int64 [N] tensor')
     ids = ids.contiguous()
@@ -40,12 +42,13 @@ def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=No
         out = Routing(torch.empty(n, dtype=torch.int32, device=device),
                       torch.empty((n, 2), dtype=torch.float32, device=device),
                       torch.empty(experts + 1, dtype=torch.int32, device=device),
-                      torch.empty(n, dtype=torch.int32, device=device) if with_expert else None)
+                      torch.empty(n, dtype=torch.int32, device=device) if with_expert else None,
+                      torch.empty(n, dtype=torch.int32, device=device) if rgb is not None else None)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
     _lib.check(lib.odie_route(ids.data_ptr(), n, width, height, regions_x, regions_y, _lib.ptr(out.expert),
                               out.perm.data_ptr(), out.coords.data_ptr(), out.offsets.data_ptr(),
-                              workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                              _lib.ptr(rgb), _lib.ptr(out.colors if rgb is not None else None), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
                               _lib.stream_of(ids)))
     return out
 

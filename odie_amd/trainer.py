@@ -4,7 +4,7 @@ This is the native step of the reference (Probe::step, odie/native/runtime.cu:24
 the hash-grid representation with the router disabled), with the single hash grid replaced
 by one hash grid per image tile:
 
-  ids --route--> (perm, local xy, offsets)            odie_route (no reference counterpart)
+  ids --route--> (perm, local xy, offsets, targets)   odie_route (no reference counterpart)
       --encode forward--> raw fp16 [n, 32]            GridEncoding fwd       (:260)
       --decoder + loss + backward--> dz, dW           decoder fwd/bwd, loss  (:270-273, :53-63)
       --encode backward--> grid gradient (scale 128)  GridEncoding bwd       (:282-287)
@@ -46,7 +46,8 @@ class ExpertTrainer:
                                            half_copy=self.decoder.half)
         self.routing = Routing(torch.empty(batch, dtype=torch.int32, device=device),
                                torch.empty((batch, 2), dtype=torch.float32, device=device),
-                               torch.empty(experts + 1, dtype=torch.int32, device=device), None)
+                               torch.empty(experts + 1, dtype=torch.int32, device=device), None,
+                               torch.empty(batch, dtype=torch.int32, device=device))
         need = _lib.library().odie_route_workspace(batch, experts)
         if need < 0:
             raise ValueError('invalid batch size for routing')
@@ -66,12 +67,12 @@ class ExpertTrainer:
             raise ValueError('batch size must be within 1..%d' % self.batch)
         mark = mark or (lambda name: None)
         r = self.routing
-        view = Routing(r.perm[:n], r.coords[:n], r.offsets, None)
-        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace)
+        view = Routing(r.perm[:n], r.coords[:n], r.offsets, None, r.colors[:n])
+        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, rgb=self.rgb)
         mark('route')
         raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
         mark('encode_forward')
-        self.decoder.train(raw, n, rgb=self.rgb, ids=ids, rows=view.perm, squares=self.squares[:n], dz=self.dz[:n])
+        self.decoder.train(raw, n, colors=view.colors, rows=view.perm, squares=self.squares[:n], dz=self.dz[:n])
         mark('decoder')
         self.grid.backward(view.coords, view.offsets, self.dz[:n], gradient=self.gradient, accumulate=False)
         mark('encode_backward')

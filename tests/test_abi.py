@@ -78,11 +78,11 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
 
 
 def test_route_rejects_bad_arguments(native):
-    assert native.odie_route(8, 16, 2048, 1365, 65, 8, None, 8, 8, 8, 8, 1 << 20, 0) == -1
+    assert native.odie_route(8, 16, 2048, 1365, 65, 8, None, 8, 8, 8, None, None, 8, 1 << 20, 0) == -1
     assert 'regions per axis' in native.odie_error().decode()
-    assert native.odie_route(8, 16, 10, 10, 8, 8, None, 8, 8, 8, 8, 1 << 20, 0) == -1
+    assert native.odie_route(8, 16, 10, 10, 8, 8, None, 8, 8, 8, None, None, 8, 1 << 20, 0) == -1
     assert 'two pixels' in native.odie_error().decode()
-    assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, 8, 4, 0) == -1
+    assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, None, None, 8, 4, 0) == -1
     assert 'workspace' in native.odie_error().decode()
     assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4 + 256 * 4
 
@@ -98,9 +98,9 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert 'null' in native.odie_error().decode()     # variants 1 and 2 need the ages
     # decoder MLP: alignment, targets
     assert native.odie_mlp_forward(8, 10, 16, 16, 0) == -1 and 'aligned' in native.odie_error().decode()
-    assert native.odie_mlp_train(16, 10, 10, 16, None, None, None, None, None, None, None, 16, 16, 0) == -1
+    assert native.odie_mlp_train(16, 10, 10, 16, None, None, None, None, None, None, None, None, 16, 16, 0) == -1
     assert 'target' in native.odie_error().decode()
-    assert native.odie_mlp_train(16, 10, 0, 16, None, None, 16, None, None, None, None, 16, 16, 0) == -1
+    assert native.odie_mlp_train(16, 10, 0, 16, None, None, None, 16, None, None, None, None, 16, 16, 0) == -1
     assert 'real' in native.odie_error().decode()
     assert native.odie_adam_step(8, None, 8, 0, 8, 8, None, 10, 0, 0, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
     assert 'step' in native.odie_error().decode()

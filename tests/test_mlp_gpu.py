@@ -63,7 +63,11 @@ def _train_case(seed, n, *, rgb8=True, permute=True, real=None):
     hidden = torch.empty((n, 128), dtype=torch.float16, **device)
     squares = torch.full((n,), float('nan'), dtype=torch.float32, **device)
     kwargs = dict(rows=torch.from_numpy(rows).cuda(), out=out, hidden=hidden, squares=squares)
-    if rgb8:
+    if rgb8 == 'colors':
+        pixel = image.reshape(-1, 3)[ids[rows]].astype(np.uint32)
+        packed = (pixel[:, 0] | (pixel[:, 1] << 8) | (pixel[:, 2] << 16)).astype(np.uint32).view(np.int32)
+        kwargs.update(colors=torch.from_numpy(packed).cuda())
+    elif rgb8:
         kwargs.update(rgb=torch.from_numpy(image).cuda(), ids=torch.from_numpy(ids).cuda())
     else:
         kwargs.update(target=torch.from_numpy(target).cuda())
@@ -78,6 +82,7 @@ def _train_case(seed, n, *, rgb8=True, permute=True, real=None):
     (1000, False, False, None),     # ragged last tile, fp32 targets, identity rows
     (2048, True, True, 1500),       # inputs >= real are padding rows
     (1 << 17, True, True, None),    # every workgroup runs several tiles
+    (5000, 'colors', True, 4000),   # packed per-row targets (as odie_route writes them)
 ])
 def test_train_matches_oracle_stagewise(n, rgb8, permute, real):
     x, flat, rows, image, ids, target, real, got = _train_case(7, n, rgb8=rgb8, permute=permute, real=real)

@@ -28,6 +28,21 @@ def test_route_matches_oracle(width, height, rx, ry, n):
     assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
 
 
+@pytest.mark.parametrize('width,height,rx,ry,n', [(2048, 1365, 8, 8, 1 << 18), (100, 37, 3, 5, 4099)])
+def test_route_gathers_slot_colors(width, height, rx, ry, n):
+    ids = synth.integers(23, 'ids', n, width * height)
+    ids[:5] = width * height + np.arange(5)          # past the image: clamped to the last row
+    image = synth.integers(23, 'image', width * height * 3, 256).astype(np.uint8)
+    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, rgb=torch.from_numpy(image).cuda())
+    _, perm, _, _ = oracle.route(ids, width, height, rx, ry)
+    clamped = ids.astype(np.uint32).astype(np.int64)
+    x, y = clamped % width, np.minimum(clamped // width, height - 1)
+    pixel = image.reshape(-1, 3)[(y * width + x)[perm]].astype(np.uint32)
+    expected = pixel[:, 0] | (pixel[:, 1] << 8) | (pixel[:, 2] << 16)
+    assert np.array_equal(result.colors.cpu().numpy().view(np.uint32), expected)
+    assert np.array_equal(result.perm.cpu().numpy(), perm)
+
+
 def test_route_clustered_ids_and_empty_experts():
     # all ids inside one tile: every other expert is empty
     width, height = 2048, 1365
