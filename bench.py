@@ -40,11 +40,13 @@ ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=16, base_
 #   encode_backward  xy 8 + upstream 64 + 16*4*2*(4 B read + 4 B write) scatter          = 1096
 # and per parameter per step:
 #   adam             read master, m, v, grad, age (20), write master, m, v, age (16), fp16 copy (2) = 38
+#   fused into the encode backward (the gradient stays in LDS): 38 - 8                   = 30
 STAGE_BYTES = {'route': 20, 'encode_forward': 328, 'decoder': 147, 'encode_backward': 1096}
-ADAM_BYTES = 38
+ADAM_BYTES, FUSED_ADAM_BYTES = 38, 30
 KERNELS = {'route': 'route_count/scan/scatter kernels', 'encode_forward': 'grid_forward_kernel',
            'decoder': 'mlp_train_kernel + mlp_reduce_kernel',
-           'encode_backward': 'transpose_half2_kernel + owner_kernel', 'grid_adam': 'adam_kernel',
+           'encode_backward': 'transpose_half2_kernel + owner_kernel (grid Adam fused into its flush)',
+           'grid_adam': 'adam_kernel',
            'decoder_adam': 'adam_kernel'}
 
 
@@ -171,9 +173,12 @@ def main():
                 for i in range(1, len(names))}
     params = trainer.grid.table.numel()
     stage_bytes = {name: per * N_COORDS for name, per in STAGE_BYTES.items()}
-    stage_bytes['grid_adam'] = ADAM_BYTES * params
+    # the grid's Adam runs inside the encode backward (its flush); its stage mark is empty
+    stage_bytes['encode_backward'] += FUSED_ADAM_BYTES * params
+    stage_bytes['grid_adam'] = 0
     stage_bytes['decoder_adam'] = ADAM_BYTES * trainer.decoder.params.numel()
-    stage_gbs = {name: stage_bytes[name] / (stage_ms[name] / 1e3) / 1e9 for name in stage_ms}
+    stage_gbs = {name: stage_bytes[name] / (stage_ms[name] / 1e3) / 1e9 if stage_bytes[name] else None
+                 for name in stage_ms}
     qps = N_COORDS / (ms / 1e3)
     step_gbs = sum(stage_bytes.values()) / (ms / 1e3) / 1e9
     dominant = max(stage_ms, key=stage_ms.get)

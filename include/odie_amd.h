@@ -72,6 +72,19 @@ int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, i
                        const odie_grid_level* levels, int n_levels, int features,
                        float* gradient, int zero_first, uint64_t stream);
 
+/* Encode backward fused with the optimizer step: the gradient of every table value (as
+ * odie_grid_backward with zero_first = 1 computes it) is applied to master / m / v / steps /
+ * half_copy by the Adam update of odie_adam_step (variant, step, lr, betas, eps, loss_scale as
+ * there) where it is formed, without writing it to memory.  Bit-identical to
+ * odie_grid_backward followed by odie_adam_step.  expert_params must equal the levels' table
+ * size.  Replaces the grid's GridEncoding bwd + optimizer step pair of the native step
+ * (odie/native/runtime.cu:287,304-305). */
+int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                            const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                            const odie_grid_level* levels, int n_levels, int features, float* master,
+                            uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant, int64_t step,
+                            float lr, float beta1, float beta2, float eps, float loss_scale, uint64_t stream);
+
 /* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
  * 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),

@@ -21,6 +21,7 @@
 //                 slice (few experts, many coordinates): partial slices are summed.
 // Every gradient entry is written by exactly one workgroup, so no clearing pass is needed.
 #include "grid.h"
+#include "adam.h"
 
 namespace odie {
 namespace {
@@ -202,6 +203,8 @@ struct OwnerArgs {
     int slice_entries[ODIE_MAX_LEVELS];
     int row_bits[ODIE_MAX_LEVELS];   // > 0: slices are aligned 2^row_bits blocks screened by row
     int cap;                         // int64 accumulators in LDS; the candidate rings follow them
+    int fused;                       // 1: apply the optimizer step instead of writing the gradient
+    AdamStep adam;
 };
 
 enum LevelKind { kDense = 0, kHashedPow2 = 1, kGeneric = 2, kHashed24 = 3 };
@@ -463,6 +466,43 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     }
     __syncthreads();
     const double unscale = ldexp(1.0, -shift);
+    if (a.fused && a.splits == 1) {
+        // The final gradient of these parameters is in LDS: update them right here.  One
+        // workgroup holds the CU, so the loads of four elements per thread are issued before
+        // any of them is used, to keep memory latency off the critical path.
+        const AdamStep& o = a.adam;
+        const int64_t first = static_cast<int64_t>(e) * a.expert_params + lo;
+        constexpr int kBatch = 4;
+        for (uint32_t j0 = threadIdx.x; j0 < span; j0 += kBatch * kOwnerBlock) {
+            float g[kBatch], p[kBatch], m[kBatch], v[kBatch];
+            uint32_t age[kBatch];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const uint32_t j = j0 + k * kOwnerBlock;
+                const int64_t i = first + (j < span ? j : 0);
+                p[k] = o.master[i];
+                m[k] = o.m[i];
+                v[k] = o.v[i];
+                age[k] = o.variant != 0 ? o.steps[i] : 0u;
+                g[k] = static_cast<float>(static_cast<double>(static_cast<long long>(acc[j < span ? j : 0])) * unscale);
+                if (!finite) g[k] = __builtin_nanf("");
+            }
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const uint32_t j = j0 + k * kOwnerBlock;
+                if (j >= span) continue;
+                const int64_t i = first + j;
+                if (adam_math(o, g[k], p[k], m[k], v[k], age[k])) {
+                    o.master[i] = p[k];
+                    o.m[i] = m[k];
+                    o.v[i] = v[k];
+                    if (o.variant != 0) o.steps[i] = age[k];
+                }
+                if (o.half_copy) o.half_copy[i] = half_to_bits(__float2half_rn(p[k]));
+            }
+        }
+        return;
+    }
     float* out = a.splits == 1 ? a.grad + static_cast<size_t>(e) * a.expert_params + lo
                                : a.partial + static_cast<size_t>(s) * a.experts * a.expert_params +
                                      static_cast<size_t>(e) * a.expert_params + lo;
@@ -475,12 +515,15 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
 }
 
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial, float* grad, int64_t total, int splits,
-                                                           int accumulate) {
+                                                           int accumulate, int fused, AdamStep adam) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     for (int64_t x = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; x < total; x += stride) {
         float v = accumulate ? grad[x] : 0.0f;
         for (int s = 0; s < splits; ++s) v += partial[static_cast<size_t>(s) * total + x];
-        grad[x] = v;
+        if (fused)
+            adam_update(adam, x, v);
+        else
+            grad[x] = v;
     }
 }
 
@@ -511,6 +554,8 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.experts = in.experts;
     o.n_levels = L;
     o.accumulate = in.accumulate;
+    o.fused = in.adam != nullptr;
+    if (in.adam) o.adam = *in.adam;
     o.remap = in.remap;
     int group = 0;
     int64_t grouped = 0;
@@ -610,7 +655,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
         if (blocks > 16384) blocks = 16384;
         split_reduce_kernel<<<static_cast<uint32_t>(blocks), 256, 0, s>>>(o.partial, in.grad,
                                                                           static_cast<int64_t>(total_params), splits,
-                                                                          in.accumulate);
+                                                                          in.accumulate, o.fused, o.adam);
     }
     return check_launch("odie_grid_backward");
 }

@@ -9,6 +9,7 @@
 // chunk's expert in LDS (ds_add_f32) and flushes them once per chunk with global fp32
 // atomics; finer levels go straight to global_atomic_add_f32.
 #include "grid.h"
+#include "adam.h"
 #include "../../include/odie_amd.h"
 
 namespace odie {
@@ -639,6 +640,61 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
     const uint32_t blocks = grid_blocks(n, a.chunk);
     ODIE_GRID_DISPATCH(grid_backward_kernel, features, half, n_levels, blocks, shmem, s, a);
     return check_launch("odie_grid_backward");
+}
+
+// Encode backward fused with the optimizer step: every parameter's gradient is formed in
+// LDS by the owner-computes backward and the Adam update (adam.h) is applied where it is
+// flushed, so the gradient never reaches HBM.  Same result as odie_grid_backward followed
+// by odie_adam_step on the gradient, bit for bit.
+ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                     const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                     const odie_grid_level* levels, int n_levels, int features, float* master,
+                                     uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant, int64_t step,
+                                     float lr, float beta1, float beta2, float eps, float loss_scale, uint64_t stream) {
+    GridArgs a{};
+    if (validate_grid("odie_grid_backward_adam", coords, n, offsets, experts, expert_params, levels, n_levels,
+                      features, a))
+        return -1;
+    if (up_dtype != ODIE_F32 && up_dtype != ODIE_F16)
+        return fail("odie_grid_backward_adam: up_dtype must be 0 (fp32) or 1 (fp16)");
+    if (up_width < n_levels * features) return fail("odie_grid_backward_adam: up_width is smaller than n_levels*features");
+    if (n > 0 && !upstream) return fail("odie_grid_backward_adam: upstream is null");
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_backward_adam: coords must be 8-byte aligned");
+    const int64_t table = static_cast<int64_t>(a.level[n_levels - 1].offset + a.level[n_levels - 1].size) * features;
+    if (table >= (int64_t{1} << 31)) return fail("odie_grid_backward_adam: one table must hold fewer than 2^31 values");
+    if (expert_params != table) return fail("odie_grid_backward_adam: expert_params must equal the levels' table size");
+    AdamStep adam;
+    if (make_adam_step("odie_grid_backward_adam", master, half_copy, m, v, steps, variant, step, lr, beta1, beta2, eps,
+                       loss_scale, true, adam))
+        return -1;
+    const hipStream_t s = as_stream(stream);
+    const int64_t total = expert_params * experts;
+    if (n == 0) {   // every gradient is zero
+        float* zero = static_cast<float*>(workspace(static_cast<size_t>(total) * 4, s));
+        if (!zero || launch_fill_zero(zero, total, s)) return -1;
+        return launch_adam(adam, zero, 0, total, s);
+    }
+    const Tuning& t = tuning();
+    OwnerLaunch o{};
+    o.coords = coords;
+    o.offsets = a.offsets;
+    o.upstream = upstream;
+    o.up_half = up_dtype == ODIE_F16;
+    o.up_width = up_width;
+    o.grad = nullptr;
+    o.accumulate = 0;
+    o.n = n;
+    o.expert_params = expert_params;
+    o.experts = experts;
+    o.n_levels = n_levels;
+    o.features = features;
+    o.levels = a.level;
+    o.lds_bytes = t.owner_lds_bytes;
+    o.remap = t.xcd_remap;
+    o.row_screen = t.row_screen;
+    o.stream = s;
+    o.adam = &adam;
+    return launch_owner_backward(o);
 }
 
 ODIE_API int odie_set_tuning(const char* key, int value) {

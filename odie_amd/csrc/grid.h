@@ -59,6 +59,8 @@ template <bool HALF>
 using Elem = typename std::conditional<HALF, __half, float>::type;
 
 // Host-side description of one owner-computes backward launch (backward.hip).
+struct AdamStep;
+
 struct OwnerLaunch {
     const float* coords;
     const int32_t* offsets;   // null for a single grid
@@ -77,6 +79,7 @@ struct OwnerLaunch {
     int remap;
     int row_screen;
     hipStream_t stream;
+    const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad
 };
 int launch_owner_backward(const OwnerLaunch& launch);
 

@@ -72,3 +72,24 @@ class ExpertGrid:
     def backward(self, coords, offsets, upstream, gradient=None, accumulate=False):
         return grid_backward(coords, upstream, self.levels, self.features, offsets=offsets, experts=self.experts,
                              expert_params=self.expert_params, gradient=gradient, accumulate=accumulate)
+
+    def backward_adam(self, coords, offsets, upstream, optimizer, loss_scale=1.0):
+        """Encode backward fused with optimizer.step (a FusedAdam over this table's fp32 master,
+        typically with half_copy = self.table): the same parameters, moments and ages as
+        backward() followed by optimizer.step(gradient, loss_scale), without the gradient."""
+        from .encoding import _DTYPES, _check_coords, _offsets_arg
+        _check_coords(coords)
+        if upstream.dtype not in _DTYPES or upstream.ndim != 2 or upstream.shape[0] != coords.shape[0]:
+            raise ValueError('upstream must be fp32 or fp16 [N, width]')
+        if optimizer.master.numel() != self.experts * self.expert_params:
+            raise ValueError('the optimizer must own this table\'s fp32 master')
+        upstream = upstream.contiguous()
+        offsets = _offsets_arg(offsets, self.experts, coords.shape[0])
+        optimizer.step_count += 1
+        _lib.check(_lib.library().odie_grid_backward_adam(
+            coords.data_ptr(), coords.shape[0], _lib.ptr(offsets), self.experts, upstream.data_ptr(),
+            _DTYPES[upstream.dtype], upstream.shape[1], self.expert_params, self.levels, len(self.levels),
+            self.features, optimizer.master.data_ptr(), _lib.ptr(optimizer.half_copy), optimizer.m.data_ptr(),
+            optimizer.v.data_ptr(), _lib.ptr(optimizer.steps), optimizer.variant_code, optimizer.step_count,
+            optimizer.lr, optimizer.betas[0], optimizer.betas[1], optimizer.eps, float(loss_scale),
+            _lib.stream_of(coords)))

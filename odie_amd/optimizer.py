@@ -21,6 +21,7 @@ class FusedAdam:
             raise ValueError('variant must be torch, tcnn or tcnn_dense')
         self.master, self.lr, self.betas, self.eps = master, float(lr), betas, float(eps)
         self.variant = variant
+        self.variant_code = _VARIANTS[variant]
         self.half_copy = half_copy
         self.m = torch.zeros_like(master)
         self.v = torch.zeros_like(master)

@@ -10,6 +10,9 @@ by one hash grid per image tile:
       --encode backward--> grid gradient (scale 128)  GridEncoding bwd       (:282-287)
       --Adam--> grid master + fp16 copy (scale 128), decoder master + fp16 copy (scale 16384)
 
+With fused=True (the default) the grid's Adam step runs inside the encode backward
+(odie_grid_backward_adam): the gradient never reaches memory, and self.gradient is unused.
+
 Every buffer is allocated once, at construction, for `batch` ids; a step allocates nothing
 on the device beyond the library's grow-once workspace.
 """
@@ -26,13 +29,14 @@ GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:
 
 class ExpertTrainer:
     def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
-                 device='cuda'):
+                 device='cuda', fused=True):
         image = np.ascontiguousarray(image, dtype=np.uint8)
         if image.ndim != 3 or image.shape[2] != 3:
             raise ValueError('image must be uint8 [height, width, 3]')
         self.height, self.width = image.shape[:2]
         self.regions = (regions_x, regions_y)
         self.batch = batch
+        self.fused = fused          # grid Adam applied inside the encode backward
         experts = regions_x * regions_y
         self.rgb = torch.from_numpy(image.reshape(-1)).to(device)
         self.grid = ExpertGrid(encoding, experts, dtype=torch.float16, device=device)
@@ -54,7 +58,7 @@ class ExpertTrainer:
         self.workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
         self.raw = torch.empty((batch, self.grid.width), dtype=torch.float16, device=device)
         self.dz = torch.empty((batch, self.grid.width), dtype=torch.float16, device=device)
-        self.gradient = torch.empty(total, dtype=torch.float32, device=device)
+        self.gradient = None if fused else torch.empty(total, dtype=torch.float32, device=device)
         self.squares = torch.empty(batch, dtype=torch.float32, device=device)
         if self.grid.width != 32:
             raise ValueError('the decoder takes 32 input features (16 levels x 2)')
@@ -74,11 +78,17 @@ class ExpertTrainer:
         mark('encode_forward')
         self.decoder.train(raw, n, colors=view.colors, rows=view.perm, squares=self.squares[:n], dz=self.dz[:n])
         mark('decoder')
-        self.grid.backward(view.coords, view.offsets, self.dz[:n], gradient=self.gradient, accumulate=False)
-        mark('encode_backward')
-        if update:
-            self.grid_optimizer.step(self.gradient, loss_scale=GRID_SCALE)
+        if update and self.fused:
+            self.grid.backward_adam(view.coords, view.offsets, self.dz[:n], self.grid_optimizer, loss_scale=GRID_SCALE)
+            mark('encode_backward')
             mark('grid_adam')
+        else:
+            self.grid.backward(view.coords, view.offsets, self.dz[:n], gradient=self.gradient, accumulate=False)
+            mark('encode_backward')
+        if update:
+            if not self.fused:
+                self.grid_optimizer.step(self.gradient, loss_scale=GRID_SCALE)
+                mark('grid_adam')
             self.decoder_optimizer.step(self.decoder.grad, loss_scale=HEAD_SCALE)
             mark('decoder_adam')
         return self.squares[:n]

@@ -48,3 +48,38 @@ def test_adam_matches_torch_optimizer():
         torch_opt.step()
         opt.step((g).cuda(), loss_scale=128.0)
     assert torch.allclose(master.cpu(), reference.detach(), rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize('experts,n,variant,up16', [
+    (4, 20000, 'tcnn', True),
+    (4, 20000, 'torch', True),
+    (3, 9000, 'tcnn_dense', False),   # fp32 upstream
+    (1, 200000, 'tcnn', True),        # one expert, many coords: the backward splits and reduces
+    (2, 0, 'tcnn_dense', True),       # empty batch: every gradient is zero
+])
+def test_grid_backward_adam_equals_backward_then_adam(experts, n, variant, up16):
+    from odie_amd.experts import ExpertGrid
+    encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=8, per_level_scale=1.4)
+    grids, optimizers = [], []
+    for _ in range(2):
+        grid = ExpertGrid(encoding, experts, dtype=torch.float16)
+        master = torch.from_numpy(synth.table(8, grid.table.numel())).cuda()
+        grid.table.copy_(master)
+        grids.append(grid)
+        optimizers.append(FusedAdam(master, lr=1e-2, variant=variant, half_copy=grid.table))
+    coords = torch.from_numpy(synth.coordinates(9, n)).cuda()
+    counts = np.diff(np.linspace(0, n, experts + 1).astype(np.int64))
+    offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).cuda()
+    for step in range(2):
+        upstream = torch.from_numpy(synth.upstream(10 + step, n, 32)).cuda()
+        if not up16:
+            upstream = upstream.float()
+        grids[0].backward_adam(coords, offsets, upstream, optimizers[0], loss_scale=128.0)
+        gradient = grids[1].backward(coords, offsets, upstream)
+        optimizers[1].step(gradient, loss_scale=128.0)
+    for name in ('master', 'm', 'v'):
+        x, y = (getattr(o, name).cpu().numpy() for o in optimizers)
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+    assert np.array_equal(grids[0].table.cpu().numpy().view(np.uint16), grids[1].table.cpu().numpy().view(np.uint16))
+    if variant != 'torch':
+        assert np.array_equal(optimizers[0].steps.cpu().numpy(), optimizers[1].steps.cpu().numpy())

@@ -24,7 +24,7 @@ def rows_of(levels):
 def test_training_step_matches_oracle(regions, batch, n):
     width, height = 96, 70
     image = synth.image(3, width, height)
-    trainer = ExpertTrainer(image, ENCODING, *regions, batch, seed=3)
+    trainer = ExpertTrainer(image, ENCODING, *regions, batch, seed=3, fused=False)
     ids_host = synth.integers(3, 'step_ids', n, width * height)
     ids = torch.from_numpy(ids_host).cuda()
     master0 = trainer.master.cpu().numpy().astype(np.float64)
@@ -102,3 +102,22 @@ def test_training_reduces_the_loss():
         losses.append(float(trainer.step(ids).double().mean()))
     assert np.isfinite(losses).all()
     assert np.mean(losses[-5:]) < 0.5 * np.mean(losses[:5]), losses[::10]
+
+
+def test_fused_grid_adam_step_is_bit_identical():
+    width, height = 80, 60
+    image = synth.image(6, width, height)
+    fused = ExpertTrainer(image, ENCODING, 2, 3, 4096, seed=6, fused=True)
+    plain = ExpertTrainer(image, ENCODING, 2, 3, 4096, seed=6, fused=False)
+    for step in range(3):
+        ids = torch.from_numpy(synth.integers(step, 'fused_ids', 4096 - 7 * step, width * height)).cuda()
+        a = fused.step(ids).cpu().numpy()
+        b = plain.step(ids).cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for name in ('master', 'm', 'v'):
+        x = getattr(fused.grid_optimizer, name).cpu().numpy()
+        y = getattr(plain.grid_optimizer, name).cpu().numpy()
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+    assert np.array_equal(fused.grid_optimizer.steps.cpu().numpy(), plain.grid_optimizer.steps.cpu().numpy())
+    assert np.array_equal(fused.grid.table.cpu().numpy().view(np.uint16), plain.grid.table.cpu().numpy().view(np.uint16))
+    assert np.array_equal(fused.decoder.params.cpu().numpy(), plain.decoder.params.cpu().numpy())
