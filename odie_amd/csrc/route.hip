@@ -44,6 +44,7 @@ struct RouteArgs {
     int regions_x;
     int regions_y;
     int experts;
+    int expert_bits;   // bits of the largest expert id
     int part;          // ids per wave sub-chunk (multiple of 64)
     int parts;         // number of sub-chunks
     int32_t x0[kMaxRegions + 1];
@@ -207,26 +208,24 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
         int expert = -1, rx = 0, ry = 0;
         uint32_t x = 0, y = 0;
         if (valid) locate(a, bounds, i, expert, x, y, rx, ry);
-        // Peel loop: one iteration per distinct expert among the valid lanes.
-        uint64_t pending = __ballot(valid);
-        int rank = 0;
-        int32_t base = 0;
-        while (pending) {
-            const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
-            const int key = __shfl(expert, leader);
-            const uint64_t same = __ballot(valid && expert == key);
-            int32_t start = 0;
-            if (lane == leader) {
-                start = mine[key];
-                mine[key] = start + __popcll(same);
-            }
-            start = __shfl(start, leader);
-            if (valid && expert == key) {
-                rank = __popcll(same & below);
-                base = start;
-            }
-            pending &= ~same;
+        // Lanes holding the same expert: the AND over the id's bits of ballot(bit) or its
+        // complement (one ballot per bit, whatever the number of distinct experts).  Every
+        // lane reads the running count of its expert, then the lowest lane of each expert
+        // advances it; the LDS reads of one instruction precede its writes in the wave.
+        uint64_t same = __ballot(valid);
+        for (int bit = 0; bit < a.expert_bits; ++bit) {
+            const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
+            same &= ((expert >> bit) & 1) ? ones : ~ones;
         }
+        int32_t base = 0, rank = 0;
+        if (valid) {
+            rank = __popcll(same & below);
+            base = mine[expert];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank == 0) mine[expert] = base + __popcll(same);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (valid) {
             const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.parts + part]) + base + rank;
             a.perm[slot] = static_cast<int32_t>(i);
@@ -310,6 +309,8 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     a.regions_x = regions_x;
     a.regions_y = regions_y;
     a.experts = experts;
+    a.expert_bits = 0;
+    while ((1 << a.expert_bits) < experts) ++a.expert_bits;
     route_plan(n, experts, a.part, a.parts);
     for (int r = 0; r <= kMaxRegions; ++r) {
         const int rxx = r < regions_x ? r : regions_x, ryy = r < regions_y ? r : regions_y;

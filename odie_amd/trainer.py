@@ -64,7 +64,8 @@ class ExpertTrainer:
             raise ValueError('the decoder takes 32 input features (16 levels x 2)')
 
     def step(self, ids, update=True, mark=None):
-        """Train on int64 pixel ids [n] (n <= batch); returns per-id squared errors fp32 [n].
+        """Train on int64 pixel ids [n] (n <= batch); returns the squared errors fp32 [n] in
+        routed order (entry j belongs to ids[self.routing.perm[j]]).
         mark(name), if given, is called after each stage is queued (for stage timing)."""
         n = ids.numel()
         if not 1 <= n <= self.batch:
@@ -76,7 +77,8 @@ class ExpertTrainer:
         mark('route')
         raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
         mark('encode_forward')
-        self.decoder.train(raw, n, colors=view.colors, rows=view.perm, squares=self.squares[:n], dz=self.dz[:n])
+        # squared errors stay in routed order (slot j is id perm[j]); their mean is the loss
+        self.decoder.train(raw, n, colors=view.colors, squares=self.squares[:n], dz=self.dz[:n])
         mark('decoder')
         if update and self.fused:
             self.grid.backward_adam(view.coords, view.offsets, self.dz[:n], self.grid_optimizer, loss_scale=GRID_SCALE)
