@@ -221,6 +221,27 @@ int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* w
                    const uint8_t* rgb, const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out,
                    uint16_t* hidden, float* squares, uint16_t* dz, float* dweights, uint64_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Router gate (router_enabled) of the hash-grid model: gate MLP 32 -> 32 -> 16 (ReLU hidden
+ * layer, no bias, fp16; weights fp16 [1536] = Wg1 [32][32] | Wg2 [16][32], row-major
+ * [out][in]) on the raw features [n][32] (16 levels x 2), then parallel_gate / parallel_gate_back
+ * and hash_router_gradient of the native step (odie/native/runtime.cu:64-92,99-103).
+ * visible: uint8 [n][16] or null (all visible).  Levels below `coarse` have s = 1 and no gate
+ * gradient; softplus selects softplus (threshold 20) instead of the sigmoid.
+ *
+ * odie_gate_forward: weighted [n][32] = raw * fp16(s * visible) per level, s fp32 [n][16].
+ * odie_gate_backward: value = the decoder's input gradient / 128 ([n][32] fp16, as
+ *   odie_mlp_train's dz); writes the grid's upstream [n][32] = fp16(direct + fp16(d_raw / 128))
+ *   and the gate's weight gradient fp32 [1536] (overwritten, deterministic; loss scale 16384).
+ * Rows are 16-byte aligned.
+ * --------------------------------------------------------------------------------------- */
+int odie_gate_forward(const uint16_t* raw, int64_t n, const uint16_t* weights, const uint8_t* visible,
+                      int coarse, int softplus, uint16_t* weighted, float* sigmoid, uint64_t stream);
+
+int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int64_t n, const uint16_t* weights,
+                       const uint8_t* visible, const float* sigmoid, int coarse, int softplus,
+                       uint16_t* upstream, float* dweights, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

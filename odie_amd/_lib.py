@@ -41,6 +41,8 @@ SIGNATURES = {
     'selection_chunk': ([_P, _I, _I, _I, _I, C.c_bool, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
     'odie_mlp_forward': ([_P, _I64, _P, _P, _U64], _I),
     'odie_mlp_train': ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U64], _I),
+    'odie_gate_forward': ([_P, _I64, _P, _P, _I, _I, _P, _P, _U64], _I),
+    'odie_gate_backward': ([_P, _P, _I64, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
     'odie_adam_step': ([_P, _P, _P, _I, _P, _P, _P, _I64, _I, _I64, C.c_float, C.c_float, C.c_float,
                         C.c_float, C.c_float, _U64], _I),
 }

@@ -10,6 +10,9 @@ by one hash grid per image tile:
       --encode backward--> grid gradient (scale 128)  GridEncoding bwd       (:282-287)
       --Adam--> grid master + fp16 copy (scale 128), decoder master + fp16 copy (scale 16384)
 
+With router=True the gate (odie_gate_forward / odie_gate_backward) scales each level's features
+before the decoder and turns the decoder's input gradient into the grid's upstream.
+
 With fused=True (the default) the grid's Adam step runs inside the encode backward
 (odie_grid_backward_adam): the gradient never reaches memory, and self.gradient is unused.
 
@@ -22,6 +25,7 @@ import torch
 from . import _lib, synth
 from .decoder import Decoder
 from .experts import ExpertGrid, Routing, route
+from .gate import Gate
 from .optimizer import FusedAdam
 
 GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:59,305-308)
@@ -29,7 +33,7 @@ GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:
 
 class ExpertTrainer:
     def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
-                 device='cuda', fused=True):
+                 device='cuda', fused=True, router=False, gate_lr=1e-3, coarse_levels=0, activation='sigmoid'):
         image = np.ascontiguousarray(image, dtype=np.uint8)
         if image.ndim != 3 or image.shape[2] != 3:
             raise ValueError('image must be uint8 [height, width, 3]')
@@ -46,6 +50,13 @@ class ExpertTrainer:
         self.grid.table.copy_(self.master)
         self.grid_optimizer = FusedAdam(self.master, grid_lr, variant='tcnn', half_copy=self.grid.table)
         self.decoder = Decoder(seed=seed, device=device)
+        # router (odie/native/runtime.cu:266-269,276-282): the gate scales each level's features
+        self.gate = Gate(seed=seed, coarse=coarse_levels, activation=activation, device=device) if router else None
+        if router:
+            self.gate_optimizer = FusedAdam(self.gate.params, gate_lr, variant='tcnn_dense', half_copy=self.gate.half)
+            self.weighted = torch.empty((batch, 32), dtype=torch.float16, device=device)
+            self.sigmoid = torch.empty((batch, 16), dtype=torch.float32, device=device)
+            self.upstream = torch.empty((batch, 32), dtype=torch.float16, device=device)
         self.decoder_optimizer = FusedAdam(self.decoder.params, decoder_lr, variant='tcnn_dense',
                                            half_copy=self.decoder.half)
         self.routing = Routing(torch.empty(batch, dtype=torch.int32, device=device),
@@ -77,20 +88,28 @@ class ExpertTrainer:
         mark('route')
         raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
         mark('encode_forward')
+        features = raw
+        if self.gate is not None:
+            features, sigmoid = self.gate.forward(raw, weighted=self.weighted[:n], sigmoid=self.sigmoid[:n])
         # squared errors stay in routed order (slot j is id perm[j]); their mean is the loss
-        self.decoder.train(raw, n, colors=view.colors, squares=self.squares[:n], dz=self.dz[:n])
+        self.decoder.train(features, n, colors=view.colors, squares=self.squares[:n], dz=self.dz[:n])
+        upstream = self.dz[:n]
+        if self.gate is not None:
+            upstream = self.gate.backward(raw, self.dz[:n], sigmoid, upstream=self.upstream[:n])
         mark('decoder')
         if update and self.fused:
-            self.grid.backward_adam(view.coords, view.offsets, self.dz[:n], self.grid_optimizer, loss_scale=GRID_SCALE)
+            self.grid.backward_adam(view.coords, view.offsets, upstream, self.grid_optimizer, loss_scale=GRID_SCALE)
             mark('encode_backward')
             mark('grid_adam')
         else:
-            self.grid.backward(view.coords, view.offsets, self.dz[:n], gradient=self.gradient, accumulate=False)
+            self.grid.backward(view.coords, view.offsets, upstream, gradient=self.gradient, accumulate=False)
             mark('encode_backward')
         if update:
             if not self.fused:
                 self.grid_optimizer.step(self.gradient, loss_scale=GRID_SCALE)
                 mark('grid_adam')
             self.decoder_optimizer.step(self.decoder.grad, loss_scale=HEAD_SCALE)
+            if self.gate is not None:
+                self.gate_optimizer.step(self.gate.grad, loss_scale=HEAD_SCALE)
             mark('decoder_adam')
         return self.squares[:n]

@@ -39,6 +39,9 @@ PINS = {
            'layer outputs rounded once to fp16',
     'mlp_loss': 'closed form of odie/native/runtime.cu:53-63 in IEEE float32/float16 numpy arithmetic; '
                 'hand-computed known answers',
+    'gate': 'recorded gates of the reference (tests/golden/gate_support_sample.npz: effective = fp16(s*visible)); '
+            'torch.sigmoid / softplus; exact fp16 arithmetic of parallel_gate_back checked by fractions; autograd '
+            'of the gate MLP',
 }
 
 
@@ -515,3 +518,88 @@ def mlp_step_f32(x16, flat16, targets, inputs, real, threads=1):
     dz = ((dh1 @ w1).half().float() / 128.0).half()
     dweights = torch.cat([(dh1.T @ x).reshape(-1), (dh2.T @ h1).reshape(-1), (g.T @ h2).reshape(-1)])
     return dz.numpy(), dweights.numpy()
+
+
+# --------------------------------------------------------------------------------------------
+# Router gate (odie/native/runtime.cu:64-92,99-103; odie/model.py:17-22): gate MLP 32 -> 32 -> 16
+# (ReLU, no bias), s = 1 below `coarse`, else sigmoid / softplus of the fp16 logit; features of
+# level l scaled by fp16(s * visible).  Weights fp16 [1536] = Wg1 [32][32] | Wg2 [16][32].
+
+GATE_SHAPES = ((32, 32), (16, 32))
+
+
+def gate_weights(flat16):
+    flat16 = np.asarray(flat16, dtype=np.float16)
+    return flat16[:1024].reshape(32, 32), flat16[1024:1536].reshape(16, 32)
+
+
+def gate_logits(x16, flat16):
+    """(hidden fp16 [n, 32], logits fp16 [n, 16], magnitude bound of the logits)."""
+    w1, w2 = gate_weights(flat16)
+    h, _ = mlp_layer(x16, w1, True)
+    z, magnitude = mlp_layer(h, w2, False)
+    return h, z, magnitude
+
+
+def gate_values(z16, coarse, softplus=False):
+    """s fp32 [n, 16] from fp16 logits (odie/native/runtime.cu:72); libm exp in float64, rounded."""
+    z = np.asarray(z16, dtype=np.float16).astype(np.float64)
+    if softplus:
+        s = np.where(z > 20.0, z, np.log1p(np.exp(z)))
+    else:
+        s = 1.0 / (1.0 + np.exp(-z))
+    s = s.astype(np.float32)
+    s[:, :coarse] = np.float32(1.0)
+    return s
+
+
+def gate_apply(x16, s, visible=None):
+    """weighted fp16 [n, 32]: feature 2l + c times fp16(s_l * visible_l) (one fp16 rounding)."""
+    s = np.asarray(s, dtype=np.float32)
+    vis = np.ones_like(s) if visible is None else np.asarray(visible, dtype=np.float32)
+    weight = (s * vis).astype(np.float16)
+    per_feature = np.repeat(weight, 2, axis=1).astype(np.float64)
+    return (np.asarray(x16, dtype=np.float16).astype(np.float64) * per_feature).astype(np.float16)
+
+
+def gate_back(x16, value16, s, coarse, softplus=False, visible=None):
+    """parallel_gate_back (odie/native/runtime.cu:77-91): direct fp16 [n, 32] and da fp16 [n, 16]
+    (loss scale 128 x value's scale), every fp16 operation one rounding of the exact result."""
+    x = np.asarray(x16, dtype=np.float16).astype(np.float64)
+    value = np.asarray(value16, dtype=np.float16).astype(np.float64)
+    s = np.asarray(s, dtype=np.float32)
+    vis = np.ones_like(s) if visible is None else np.asarray(visible, dtype=np.float32)
+    weight = (s * vis).astype(np.float16).astype(np.float64)
+    direct = (value * np.repeat(weight, 2, axis=1)).astype(np.float16)
+    products = (value * x).astype(np.float16).astype(np.float64)
+    reduced = (products[:, 0::2] + 0.0).astype(np.float16).astype(np.float64)   # 0 + first product
+    reduced = (reduced + products[:, 1::2]).astype(np.float16)
+    incoming = reduced.astype(np.float32) * vis
+    if softplus:
+        derivative = incoming * (-np.expm1(-s.astype(np.float64))).astype(np.float32)
+    else:
+        derivative = (incoming * (np.float32(1.0) - s)).astype(np.float32) * s
+    derivative = derivative.astype(np.float32)
+    derivative[:, :coarse] = np.float32(0.0)
+    da = (derivative.astype(np.float16).astype(np.float32) * np.float32(128.0)).astype(np.float16)
+    return direct, da
+
+
+def gate_mlp_backward(x16, h16, da16, flat16):
+    """Gate MLP backward from the given hidden activations: d(raw) fp16 [n, 32] with its
+    magnitude bound, weight gradients float64 [1536] with theirs."""
+    w1, w2 = (w.astype(np.float64) for w in gate_weights(flat16))
+    x, h, da = (np.asarray(v, dtype=np.float16).astype(np.float64) for v in (x16, h16, da16))
+    dh = np.where(h > 0, da @ w2, 0.0).astype(np.float16).astype(np.float64)
+    m1 = np.where(h > 0, np.abs(da) @ np.abs(w2), 0.0)
+    dr = (dh @ w1).astype(np.float16)
+    dr_magnitude = (np.abs(dh) + m1) @ np.abs(w1)
+    dweights = np.concatenate([(dh.T @ x).ravel(), (da.T @ h).ravel()])
+    magnitude = np.concatenate([((np.abs(dh) + m1).T @ np.abs(x)).ravel(), (np.abs(da).T @ np.abs(h)).ravel()])
+    return dr, dr_magnitude, dweights, magnitude
+
+
+def gate_upstream(direct16, dr16):
+    """hash_router_gradient (odie/native/runtime.cu:99-103): fp16(direct + fp16(dr / 128))."""
+    unscaled = (np.asarray(dr16, dtype=np.float16).astype(np.float32) / np.float32(128.0)).astype(np.float16)
+    return (np.asarray(direct16, dtype=np.float16).astype(np.float64) + unscaled.astype(np.float64)).astype(np.float16)

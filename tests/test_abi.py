@@ -102,6 +102,11 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert 'target' in native.odie_error().decode()
     assert native.odie_mlp_train(16, 10, 0, 16, None, None, None, 16, None, None, None, None, 16, 16, 0) == -1
     assert 'real' in native.odie_error().decode()
+    # router gate: coarse range, alignment
+    assert native.odie_gate_forward(16, 10, 16, None, 17, 0, 16, 16, 0) == -1 and 'coarse' in native.odie_error().decode()
+    assert native.odie_gate_forward(8, 10, 16, None, 0, 0, 16, 16, 0) == -1 and 'aligned' in native.odie_error().decode()
+    assert native.odie_gate_backward(16, 16, 10, 16, None, 16, 0, 0, 16, None, 0) == -1
+    assert 'null' in native.odie_error().decode()
     assert native.odie_adam_step(8, None, 8, 0, 8, 8, None, 10, 0, 0, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
     assert 'step' in native.odie_error().decode()
     # greedy selector: n must be resolution^2, cap 8-aligned, chunk positive, tree large enough

@@ -538,3 +538,81 @@ def test_mlp_loss_squares_are_fused_sums(oracle):
             d = np.float32(np.float32(y[row, c]) - t[row, c])
             s = _round_f32(Fraction(float(d)) ** 2 + Fraction(float(s)))
         assert squares[row] == np.float32(s / np.float32(3))
+
+
+# Router gate ---------------------------------------------------------------------------------
+
+def test_gate_weight_rule_matches_recorded_gates(oracle):
+    from pathlib import Path
+    data = np.load(Path(__file__).parent / 'golden' / 'gate_support_sample.npz', allow_pickle=False)
+    gate, visible, effective = data['gate'], data['visible'], data['effective']
+    weighted = oracle.gate_apply(np.ones((len(gate), 32), dtype=np.float16), gate.astype(np.float32), visible)
+    assert np.array_equal(weighted[:, 0::2].view(np.uint16), effective.view(np.uint16))
+    assert np.array_equal(weighted[:, 1::2].view(np.uint16), effective.view(np.uint16))
+    # invisible cells contribute nothing, visible ones their gate
+    assert not effective[~visible].any() and np.array_equal(effective[visible], gate[visible])
+
+
+def test_gate_values_match_torch(oracle):
+    import torch
+    z = np.concatenate([np.linspace(-30, 30, 4001), [-0.0, 0.0, 19.99, 20.0, 20.01]]).astype(np.float16)
+    z = np.tile(z[:, None], (1, 16))
+    s = oracle.gate_values(z, 0)
+    expected = torch.sigmoid(torch.from_numpy(z.astype(np.float64))).float().numpy()
+    assert np.allclose(s, expected, rtol=2.0 ** -23, atol=0)
+    soft = oracle.gate_values(z, 0, softplus=True)
+    expected = torch.nn.functional.softplus(torch.from_numpy(z.astype(np.float64)), threshold=20).float().numpy()
+    assert np.allclose(soft, expected, rtol=2.0 ** -23, atol=0)
+    assert (oracle.gate_values(z, 5)[:, :5] == 1).all()
+
+
+def test_gate_back_matches_exact_rational_arithmetic(oracle):
+    from fractions import Fraction
+    rng = np.random.default_rng(12)
+    x = rng.normal(size=(40, 32)).astype(np.float16)
+    value = (rng.normal(size=(40, 32)) * 3).astype(np.float16)
+    s = rng.uniform(0, 1, size=(40, 16)).astype(np.float32)
+    visible = rng.integers(0, 2, size=(40, 16)).astype(bool)
+    direct, da = oracle.gate_back(x, value, s, 3, visible=visible)
+
+    def exact16(q):   # correct rounding of a rational to fp16 (ties to even)
+        guess = np.float16(float(q))
+        best = None
+        for c in (np.nextafter(guess, np.float16(-np.inf)), guess, np.nextafter(guess, np.float16(np.inf))):
+            key = (abs(Fraction(float(c)) - q), int(np.array(c).view(np.uint16)) & 1)
+            if best is None or key < best[0]:
+                best = (key, c)
+        return best[1]
+    for i in range(40):
+        for l in range(16):
+            w = exact16(Fraction(float(s[i, l])) * int(visible[i, l]))
+            for c in range(2):
+                assert direct[i, 2 * l + c] == exact16(Fraction(float(value[i, 2 * l + c])) * Fraction(float(w)))
+            p0 = exact16(Fraction(float(value[i, 2 * l])) * Fraction(float(x[i, 2 * l])))
+            p1 = exact16(Fraction(float(value[i, 2 * l + 1])) * Fraction(float(x[i, 2 * l + 1])))
+            reduced = exact16(Fraction(float(exact16(Fraction(0) + Fraction(float(p0))))) + Fraction(float(p1)))
+            if l < 3:
+                assert da[i, l] == 0
+            else:
+                incoming = np.float32(np.float32(reduced) * np.float32(int(visible[i, l])))
+                derivative = np.float32(np.float32(incoming * np.float32(np.float32(1) - s[i, l])) * s[i, l])
+                assert da[i, l] == exact16(Fraction(float(np.float16(derivative))) * 128)
+
+
+def test_gate_mlp_backward_matches_autograd(oracle):
+    import torch
+    rng = np.random.default_rng(13)
+    x = (rng.normal(size=(64, 32)) * 0.5).astype(np.float16)
+    flat = np.concatenate([rng.uniform(-1, 1, 1024) * np.sqrt(6 / 64), rng.uniform(-1, 1, 512) * np.sqrt(6 / 48)])
+    flat = flat.astype(np.float16)
+    h, z, _ = oracle.gate_logits(x, flat)
+    da = (rng.normal(size=(64, 16)) * 100).astype(np.float16)
+    dr, dr_magnitude, dweights, magnitude = oracle.gate_mlp_backward(x, h, da, flat)
+    w = [torch.tensor(v.astype(np.float64), requires_grad=True) for v in oracle.gate_weights(flat)]
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    mask = torch.tensor((h > 0).astype(np.float64))
+    logits = ((xt @ w[0].T) * mask) @ w[1].T
+    (logits * torch.tensor(da.astype(np.float64))).sum().backward()
+    expected = torch.cat([v.grad.reshape(-1) for v in w]).numpy()
+    assert np.all(np.abs(dweights - expected) <= 2e-2 * magnitude + 1e-9)
+    assert np.all(np.abs(dr.astype(np.float64) - xt.grad.numpy()) <= 2e-2 * dr_magnitude + 1e-6)

@@ -121,3 +121,28 @@ def test_fused_grid_adam_step_is_bit_identical():
     assert np.array_equal(fused.grid_optimizer.steps.cpu().numpy(), plain.grid_optimizer.steps.cpu().numpy())
     assert np.array_equal(fused.grid.table.cpu().numpy().view(np.uint16), plain.grid.table.cpu().numpy().view(np.uint16))
     assert np.array_equal(fused.decoder.params.cpu().numpy(), plain.decoder.params.cpu().numpy())
+
+
+def test_router_step_composes_the_tested_stages():
+    from odie_amd.decoder import Decoder
+    from odie_amd.gate import Gate
+    width, height = 72, 56
+    image = synth.image(8, width, height)
+    trainer = ExpertTrainer(image, ENCODING, 2, 2, 3000, seed=8, fused=False, router=True, coarse_levels=2)
+    gate0 = trainer.gate.params.cpu().numpy()
+    decoder0 = trainer.decoder.params.cpu().numpy()
+    ids = torch.from_numpy(synth.integers(8, 'router_ids', 3000, width * height)).cuda()
+    trainer.step(ids)
+    torch.cuda.synchronize()
+    gate, decoder = Gate(weights=gate0, coarse=2), Decoder(weights=decoder0)
+    raw = trainer.raw[:3000]
+    weighted, sigmoid = gate.forward(raw)
+    assert np.array_equal(weighted.cpu().numpy().view(np.uint16), trainer.weighted[:3000].cpu().numpy().view(np.uint16))
+    dz = decoder.train(weighted, 3000, colors=trainer.routing.colors[:3000])
+    upstream = gate.backward(raw, dz, sigmoid)
+    assert np.array_equal(upstream.cpu().numpy().view(np.uint16), trainer.upstream[:3000].cpu().numpy().view(np.uint16))
+    gradient = trainer.grid.backward(trainer.routing.coords[:3000], trainer.routing.offsets, upstream)
+    assert np.array_equal(gradient.cpu().numpy().view(np.uint32), trainer.gradient.cpu().numpy().view(np.uint32))
+    assert np.array_equal(gate.grad.cpu().numpy().view(np.uint32), trainer.gate.grad.cpu().numpy().view(np.uint32))
+    # the gate's optimizer ran (per-parameter ages, no skip, scale 16384)
+    assert (trainer.gate_optimizer.steps.cpu().numpy() == 1).all()
