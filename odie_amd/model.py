@@ -178,3 +178,93 @@ class PackedQuery(torch.autograd.Function):
         gradient = packed_backward(coordinates, feature_gradient.contiguous(), descriptors, node_bitmap,
                                    node_prefix, bitmap, ctx.param_count)
         return None, gradient, None, None, None, None, None
+
+
+class PackedPlanes:
+    """The packed xy-plane grid of PackedXYPlanes (odie/model.py:154-262) without its TCNN heads:
+    fp32 master `grid` in packed storage, the layout's addressing buffers on the device, the
+    active prefix, and the activation of the next plane's support.
+
+    Plane values are inputs of the path (odie/model.py:208-224 draws them from a CUDA generator
+    stream); here a plane's native nodes draw N(0, feature_init_std) from the counter PRNG of
+    odie_amd.synth under the same per-level seed, so a plane is initialized exactly once and
+    identically on every machine.
+    """
+
+    def __init__(self, config, supports, plane_dims, plane_node_caps, device='cuda'):
+        self.config = dict(config)
+        self.layout = make_layout(self.config, supports, plane_dims, plane_node_caps)
+        self.supports = self.layout['supports']
+        self.plane_dims, self.plane_node_caps = list(plane_dims), list(plane_node_caps)
+        self.n_levels = int(self.config['n_levels'])
+        self.input_width = self.layout['input_width']
+        self.device = torch.device(device)
+        self.grid = torch.zeros(self.layout['params'], dtype=torch.float32, device=self.device)
+        self.initialized_planes = [False] * self.n_levels
+        for level, item in enumerate(self.layout['levels']):
+            if item['nodes'].numel():
+                self._initialize_plane(level)
+        self._upload(self.layout)
+        self.active_prefix = int(self.config.get('initial_active_prefix', self.n_levels))
+
+    def _upload(self, layout):
+        for name in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap'):
+            setattr(self, name, _device_layout(layout[name]).to(self.device))
+
+    @torch.no_grad()
+    def _initialize_plane(self, level):
+        from . import synth
+        if self.initialized_planes[level]:
+            raise RuntimeError('Each plane must be initialized exactly once')
+        item = self.layout['levels'][level]
+        level_seed = (self.config['seed'] + 1000003 * (level + 1)) % (2 ** 31)
+        branch_seed = (level_seed + 104729 * 3) % (2 ** 31)
+        width = max(2, item['plane_dim'])
+        draws = synth.normal(branch_seed, 'plane', item['native_plane_points'] * width).reshape(-1, width)
+        nodes = item['nodes'].numpy()
+        values = (draws[nodes, :item['plane_dim']] * float(self.config['feature_init_std'])).astype(np.float32)
+        offset = item['plane_offset']
+        self.grid[offset:offset + values.size].copy_(torch.from_numpy(values.reshape(-1)))
+        self.initialized_planes[level] = True
+
+    @torch.no_grad()
+    def activate_support(self, level, support):
+        """Add only the next unopened plane, retaining packed storage and offsets
+        (odie/model.py:226-257): same checks, same record."""
+        if level != self.active_prefix or not 2 <= level < self.n_levels:
+            raise ValueError('Select the next unopened plane before advancing the prefix')
+        if self.initialized_planes[level] or bool(self.supports[level].any()):
+            raise RuntimeError('An opened support cannot be replaced or initialized again')
+        resolution = self.config['resolutions'][level]
+        if support.device.type != 'cpu' or support.dtype != torch.bool or support.shape != (resolution ** 2,):
+            raise ValueError('New support must be a flat CPU bool R^2 tensor')
+        nodes = plane_closure(support, resolution)
+        cap = self.plane_node_caps[level]
+        if not 0 < nodes.numel() <= cap:
+            raise ValueError('New support requires a nonempty complete closure within its cap')
+        storage_pointer = self.grid.data_ptr()
+        updated = list(self.supports)
+        updated[level] = support.clone()
+        layout = make_layout(self.config, updated, self.plane_dims, self.plane_node_caps)
+        self._upload(layout)
+        self.layout, self.supports = layout, layout['supports']
+        points = layout['levels'][level]['native_plane_points']
+        self._initialize_plane(level)
+        if self.grid.data_ptr() != storage_pointer:
+            raise AssertionError('Packed storage changed during plane activation')
+        return {'level': level, 'initialized_once': True, 'grid_storage_unchanged': True,
+                'original_dense_f2_seed': (self.config['seed'] + 1000003 * (level + 1) + 104729 * 3) % (2 ** 31),
+                'native_dense_draw_shape': [points, max(2, self.plane_dims[level])], 'selected_nodes': nodes.numel()}
+
+    def set_active_prefix(self, prefix):
+        if not isinstance(prefix, int) or not 2 <= prefix <= self.n_levels:
+            raise ValueError('Active prefix must be an integer between 2 and declared level count')
+        self.active_prefix = prefix
+
+    def query_features(self, coordinates):
+        """(features fp16 [N, input_width], visibility bool [N, L]) through PackedQuery."""
+        if coordinates.dtype != torch.float32 or coordinates.ndim != 2 or coordinates.shape[1] != 2 \
+                or coordinates.requires_grad:
+            raise ValueError('Coordinates must be FP32 Nx2, without coordinate gradients')
+        return PackedQuery.apply(coordinates.contiguous(), self.grid, self.descriptors, self.node_bitmap,
+                                 self.node_prefix, self.bitmap, self.input_width)

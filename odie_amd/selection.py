@@ -59,6 +59,34 @@ def cell_bounds(shape, resolution):
     return (np.searchsorted(xmap, bounds).astype(np.int32), np.searchsorted(ymap, bounds).astype(np.int32), ymap)
 
 
+def closure_nodes(cells, resolution):
+    """Sorted unique closure nodes {c, c+1, c+R, c+R+1} mod align8(R^2) (odie/selection.py:76-79)."""
+    cells = np.asarray(cells, dtype=np.int64)
+    return np.unique(np.concatenate([cells, cells + 1, cells + resolution, cells + resolution + 1])
+                     % align8(resolution ** 2))
+
+
+def selection_record(selected, nodes, resolution, cap, policy, iterations):
+    """The closure check and record of odie/selection.py:90-105: raises unless nodes is exactly
+    the closure of the selected cells and fits the cap."""
+    selected, nodes = np.asarray(selected, dtype=bool), np.asarray(nodes, dtype=bool)
+    closure = closure_nodes(np.flatnonzero(selected), resolution)
+    if not np.array_equal(closure, np.flatnonzero(nodes)) or len(closure) > cap:
+        raise AssertionError('Selection must preserve its complete node closure')
+    used = int(nodes.sum())
+    return {
+        'policy': policy, 'selected_cells': int(selected.sum()),
+        'closure_nodes': used, 'node_capacity': cap,
+        'unused_allocated_node_slots': int(cap - used),
+        'aligned_used_node_slots': align8(used),
+        'node_capacity_utilization': float(used / cap) if cap else 0.,
+        'aligned_capacity_utilization': float(align8(used) / cap) if cap else 0.,
+        'complete_interpolation_closure': True,
+        'tie_order': 'descending score, ascending native cell ID',
+        'iterations': iterations,
+    }
+
+
 def uniform_bounds(size, tile):
     """Bounds of equal tiles of `tile` pixels (the last one shorter if size % tile)."""
     return np.array(list(range(0, size, tile)) + [size], dtype=np.int32)
