@@ -242,6 +242,51 @@ int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int64_t n, co
                        const uint8_t* visible, const float* sigmoid, int coarse, int softplus,
                        uint16_t* upstream, float* dweights, uint64_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * The native training step: the reference's Probe handle (odie/native/runtime.cu:163-331),
+ * bound by NativeOptimizer (odie/native_backend.py:32-44).  Same entry points, arguments and
+ * 0 / -1 + odie_error convention; one step is ids -> xy and targets, the grid query (packed
+ * planes with the active prefix, or the hash grid), the router gate when "gate" is given, the
+ * decoder with the loss, the gate backward, the grid backward and the three Adam updates
+ * (grid: per-parameter ages, zero gradients skipped, fp16 gradients at loss scale 128; heads:
+ * fp16 gradients halved to 128 as the reference's half_unscale does unless mode bit 1).
+ *
+ * Settings (JSON object): the reference's keys stream, total, width, height, mode (bit 4: fp16
+ * grid gradients, required for the hash grid; bit 16: parallel gate, required with a gate;
+ * bit 8 accepted, no effect on results), rgb, grid, decoder, gate (optional), descriptors,
+ * node_bitmap, node_prefix, bitmap (packed planes), hash_encoding (optional object),
+ * active, grid_lr, gate_lr, decoder_lr; and, for what the reference fixes at compile time
+ * (odie/build.py:26-30): levels (16), raw_width (32), rgb8 (1: uint8 image, 0: fp32 image),
+ * gate_coarse_levels (K, default 0), router_activation ("sigmoid" | "softplus").
+ * Built for 16 levels x 2 features in level order; other layouts are rejected at create.
+ * Every buffer is allocated at create for batches of up to 65536 ids: odie_step allocates
+ * nothing and only queues work on the settings' stream (graph-capturable).
+ * --------------------------------------------------------------------------------------- */
+
+/* Replaces odie_create (odie/native/runtime.cu:321); null on failure. */
+void* odie_create(const char* settings);
+/* Replaces odie_step (:322): ids device int64 [n], 1 <= n <= 65536; update = 0 computes the
+ * gradients without the optimizer steps. */
+int odie_step(void* handle, uint64_t ids, int n, int update);
+/* Replaces odie_configure (:325): active, learning rates and (packed planes) the four pointers. */
+int odie_configure(void* handle, const char* settings);
+/* Replaces odie_pointers (:323): JSON of the handle's buffers (squares fp32 [65536] is the one
+ * NativeOptimizer reads; grid_grad holds the fp32 grid gradient x128 of the last packed step or
+ * hash step without update; half_grad and dirty_count are 0: no such buffers exist here). */
+const char* odie_pointers(void* handle);
+/* Replaces odie_state (:324): begin >= 0: {"pristine": bool} over grid parameters [begin, end);
+ * begin < 0: {"hash_fnv1a64": "...", "bytes": N}, an FNV-1a digest of every Adam state array
+ * (its value is this library's own; compare digests only with digests from this library). */
+const char* odie_state(void* handle, int begin, int end);
+/* Replaces odie_sync_weights (:327): fp16 copies of the fp32 master weights. */
+int odie_sync_weights(void* handle);
+/* Replace odie_pin_contexts / odie_release_contexts (:328,326): no per-step context objects
+ * exist here (every buffer belongs to the handle), so both do nothing. */
+void odie_pin_contexts(void* handle);
+void odie_release_contexts(void* handle);
+/* Replaces odie_destroy (:330): waits for the stream, frees the handle's buffers. */
+void odie_destroy(void* handle);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,10 @@
 // variant 2 (the tiny-cuda-nn Adam of the MLP heads, odie/native/runtime.cu:159-160, whose
 //   weights are matrix parameters and so never skipped): as variant 1, but every parameter's
 //   age advances on every step, zero gradient included.
+// half_divisor > 0 first stores the gradient as a half-precision gradient buffer would:
+//   g = fp16(fp16(g) / half_divisor) (the tiny-cuda-nn optimizers of the native step take fp16
+//   gradients, odie/native/runtime.cu:212-215,301-309; half_divisor 1 is the plain fp16 store,
+//   128 the heads' half_unscale, odie/native/kernels.cuh:140-143).
 #pragma once
 #include "common.h"
 
@@ -36,11 +40,14 @@ struct AdamStep {
     float inv_bc2_sqrt;     // variant 0: 1 / sqrt(1 - b2^t)
     float log_beta1;        // variants 1, 2: ln b1, ln b2
     float log_beta2;
+    float half_divisor;     // > 0: gradient rounded through fp16 first (see above); 0: as given
 };
 
 // Updates p, m, v (and the age) from gradient g (still carrying the loss scale); returns
 // false when the parameter is skipped (variant 1, zero gradient).
 __device__ inline bool adam_math(const AdamStep& a, float g, float& p, float& m, float& v, uint32_t& age) {
+    if (a.half_divisor > 0.0f)
+        g = __half2float(__float2half_rn(__half2float(__float2half_rn(g)) / a.half_divisor));
     g = g * a.inv_scale;
     if (a.variant != 0) {
         if (a.variant == 1 && g == 0.0f) return false;

@@ -15,9 +15,10 @@ namespace odie {
 std::string& error_slot();
 int fail(const std::string& message);
 int check_launch(const char* what);
-// Library-owned device scratch of at least `bytes`, one buffer per device, grown on demand
-// (a growth synchronizes the device and reallocates; steady-state calls allocate nothing).
-// Calls that use it must not overlap on one device.  Returns null and sets the error on failure.
+// Library-owned device scratch of at least `bytes`, one buffer per device, grown on demand (at
+// least doubling; an outgrown buffer is kept until the process ends, so work already queued or
+// captured in a graph keeps a valid address; steady-state calls allocate nothing).  Calls that
+// use it must not overlap on one device.  Returns null and sets the error on failure.
 void* workspace(size_t bytes, hipStream_t stream);
 // Zero `count` floats (or any 4-byte words) with a fill kernel (graph-capturable).
 int launch_fill_zero(float* data, int64_t count, hipStream_t stream);

@@ -1,6 +1,7 @@
 // Thread-local error slot shared by every C-ABI entry point, plus odie_error/odie_copy.
 #include <map>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 #include "../../include/odie_amd.h"
@@ -26,6 +27,9 @@ int check_launch(const char* what) {
 void* workspace(size_t bytes, hipStream_t stream) {
     static std::mutex lock;
     static std::map<int, std::pair<void*, size_t>> buffers;
+    // Outgrown buffers stay allocated until the process ends: queued kernels and captured
+    // graphs may still hold their addresses.
+    static std::vector<void*> retired;
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) {
         fail("workspace: no current device");
@@ -34,15 +38,8 @@ void* workspace(size_t bytes, hipStream_t stream) {
     std::lock_guard<std::mutex> guard(lock);
     auto& slot = buffers[device];
     if (slot.first && slot.second >= bytes) return slot.first;
-    if (slot.first) {
-        (void)stream;
-        if (hipDeviceSynchronize() != hipSuccess || hipFree(slot.first) != hipSuccess) {
-            fail("workspace: could not release the previous buffer");
-            return nullptr;
-        }
-        slot = {nullptr, 0};
-    }
-    size_t size = bytes + bytes / 4;
+    (void)stream;
+    size_t size = slot.first ? (bytes > 2 * slot.second ? bytes : 2 * slot.second) : bytes + bytes / 4;
     size = (size + (size_t{2} << 20) - 1) / (size_t{2} << 20) * (size_t{2} << 20);
     void* pointer = nullptr;
     const hipError_t status = hipMalloc(&pointer, size);
@@ -50,6 +47,7 @@ void* workspace(size_t bytes, hipStream_t stream) {
         fail(std::string("workspace: hipMalloc failed: ") + hipGetErrorString(status));
         return nullptr;
     }
+    if (slot.first) retired.push_back(slot.first);
     slot = {pointer, size};
     return pointer;
 }

@@ -406,6 +406,8 @@ struct PackedArgs {
     int64_t params;
     int levels;
     int width;
+    int active;          // levels >= active are off (the native step's active prefix)
+    uint16_t pad;        // fp16 bits written to columns past the last level
 };
 
 // Geometry at integer resolution R: p = fma(R-1, x, 0.5), cell = floor(px) + floor(py)*R.
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(kBlock) void packed_forward_kernel(PackedArgs a) {
             int cell;
             float w[4];
             plane_geometry(p.x, p.y, d[0], cell, w);
-            const bool on = (a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1;
+            const bool on = l < a.active && ((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1);
             vis[l / 4] |= static_cast<uint32_t>(on) << (8 * (l % 4));
             for (int c = 0; c < d[5]; ++c) {
                 __half v = __float2half(0.0f);
@@ -469,7 +471,7 @@ __global__ __launch_bounds__(kBlock) void packed_forward_kernel(PackedArgs a) {
             written = top > written ? top : written;
         }
     }
-    for (int c = written; c < a.width; ++c) row[c] = 0;
+    for (int c = written; c < a.width; ++c) row[c] = a.pad;
     uint8_t* vrow = a.visibility + static_cast<size_t>(i) * a.levels;
 #pragma unroll
     for (int l = 0; l < ODIE_MAX_LEVELS; ++l)
@@ -646,11 +648,12 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
 // LDS by the owner-computes backward and the Adam update (adam.h) is applied where it is
 // flushed, so the gradient never reaches HBM.  Same result as odie_grid_backward followed
 // by odie_adam_step on the gradient, bit for bit.
-ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                                     const void* upstream, int up_dtype, int up_width, int64_t expert_params,
-                                     const odie_grid_level* levels, int n_levels, int features, float* master,
-                                     uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant, int64_t step,
-                                     float lr, float beta1, float beta2, float eps, float loss_scale, uint64_t stream) {
+namespace odie {
+
+int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                const odie_grid_level* levels, int n_levels, int features, const AdamStep& adam,
+                                hipStream_t s) {
     GridArgs a{};
     if (validate_grid("odie_grid_backward_adam", coords, n, offsets, experts, expert_params, levels, n_levels,
                       features, a))
@@ -663,11 +666,6 @@ ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32
     const int64_t table = static_cast<int64_t>(a.level[n_levels - 1].offset + a.level[n_levels - 1].size) * features;
     if (table >= (int64_t{1} << 31)) return fail("odie_grid_backward_adam: one table must hold fewer than 2^31 values");
     if (expert_params != table) return fail("odie_grid_backward_adam: expert_params must equal the levels' table size");
-    AdamStep adam;
-    if (make_adam_step("odie_grid_backward_adam", master, half_copy, m, v, steps, variant, step, lr, beta1, beta2, eps,
-                       loss_scale, true, adam))
-        return -1;
-    const hipStream_t s = as_stream(stream);
     const int64_t total = expert_params * experts;
     if (n == 0) {   // every gradient is zero
         float* zero = static_cast<float*>(workspace(static_cast<size_t>(total) * 4, s));
@@ -697,15 +695,32 @@ ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32
     return launch_owner_backward(o);
 }
 
+}  // namespace odie
+
+ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                     const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                     const odie_grid_level* levels, int n_levels, int features, float* master,
+                                     uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant, int64_t step,
+                                     float lr, float beta1, float beta2, float eps, float loss_scale, uint64_t stream) {
+    AdamStep adam;
+    if (make_adam_step("odie_grid_backward_adam", master, half_copy, m, v, steps, variant, step, lr, beta1, beta2, eps,
+                       loss_scale, true, adam))
+        return -1;
+    return grid_backward_adam_internal(coords, n, offsets, experts, upstream, up_dtype, up_width, expert_params, levels,
+                                       n_levels, features, adam, as_stream(stream));
+}
+
 ODIE_API int odie_set_tuning(const char* key, int value) {
     if (!key) return fail("odie_set_tuning: key is null");
     return set_grid_tuning(key, value);
 }
 
-ODIE_API int odie_packed_forward(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
-                                 const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
-                                 const int32_t* node_prefix, const uint8_t* bitmap, int width,
-                                 uint16_t* features, uint8_t* visibility, uint64_t stream) {
+namespace odie {
+
+int packed_forward_internal(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
+                            const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                            const int32_t* node_prefix, const uint8_t* bitmap, int width, int active, uint16_t pad,
+                            uint16_t* features, uint8_t* visibility, hipStream_t stream) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_packed_forward: n must be within [0, 2^31-1]");
     if (levels < 2 || levels > ODIE_MAX_LEVELS) return fail("odie_packed_forward: descriptor must have 2..32 levels");
     if (width < 2 || width > 128) return fail("odie_packed_forward: feature width must be within 2..128");
@@ -727,9 +742,23 @@ ODIE_API int odie_packed_forward(const float* coords, int64_t n, const float* gr
     a.params = parameter_count;
     a.levels = levels;
     a.width = width;
+    a.active = active;
+    a.pad = pad;
     const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
-    packed_forward_kernel<<<blocks, kBlock, 0, as_stream(stream)>>>(a);
+    packed_forward_kernel<<<blocks, kBlock, 0, stream>>>(a);
     return check_launch("odie_packed_forward");
+}
+
+}  // namespace odie
+
+using namespace odie;
+
+ODIE_API int odie_packed_forward(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
+                                 const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                                 const int32_t* node_prefix, const uint8_t* bitmap, int width,
+                                 uint16_t* features, uint8_t* visibility, uint64_t stream) {
+    return packed_forward_internal(coords, n, grid, parameter_count, descriptors, levels, node_bitmap, node_prefix,
+                                   bitmap, width, levels, 0, features, visibility, as_stream(stream));
 }
 
 ODIE_API int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstream, int up_width,

@@ -83,5 +83,19 @@ struct OwnerLaunch {
 };
 int launch_owner_backward(const OwnerLaunch& launch);
 
+// odie_grid_backward_adam with the optimizer step already formed (adam.h), so that callers
+// can set fields the C ABI does not expose (the fp16 gradient store).
+int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                const odie_grid_level* levels, int n_levels, int features, const AdamStep& adam,
+                                hipStream_t stream);
+
+// The packed-plane forward with the native step's active prefix (levels >= active are off)
+// and the fp16 bits written past the last level (the runtime pads with 1.0).
+int packed_forward_internal(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
+                            const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                            const int32_t* node_prefix, const uint8_t* bitmap, int width, int active, uint16_t pad,
+                            uint16_t* features, uint8_t* visibility, hipStream_t stream);
+
 
 }  // namespace odie

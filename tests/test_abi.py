@@ -1,6 +1,7 @@
 """The C-ABI library loads, exports every declared symbol, and rejects bad arguments
 before queuing any device work (these calls never reach the GPU)."""
 import ctypes as C
+import json
 import subprocess
 
 import pytest
@@ -146,3 +147,49 @@ def test_product_thresholds_equal_oracle(oracle):
     from odie_amd.selection import native_thresholds
     for r in (2, 8, 13, 128, 1290):
         assert np.array_equal(np.asarray(native_thresholds(r), dtype=np.float32), oracle.native_thresholds(r))
+
+
+def _settings(**change):
+    settings = dict(stream=0, total=1024, width=64, height=64, mode=20, rgb=4096, grid=4096, decoder=4096,
+                    descriptors=4096, node_bitmap=4096, node_prefix=4096, bitmap=4096, active=16, grid_lr=1e-2,
+                    decoder_lr=1e-3)
+    settings.update(change)
+    return json.dumps({k: v for k, v in settings.items() if v is not None}).encode()
+
+
+@pytest.mark.parametrize('settings,message', [
+    (b'not json', 'settings JSON'),
+    (b'[1, 2]', 'expected an object'),
+    (b'{"stream": 0} trailing', 'trailing'),
+    (_settings(total=None), 'missing setting: total'),
+    (_settings(total=0), 'invalid total'),
+    (_settings(grid=0), 'null rgb or grid'),
+    (_settings(grid=4100), '16-byte aligned'),
+    (_settings(levels=12), '16 levels'),
+    (_settings(raw_width=48), '32-wide'),
+    (_settings(router_activation='tanh'), 'router_activation'),
+    (_settings(gate_coarse_levels=17), 'gate_coarse_levels'),
+    (_settings(gate=4096, mode=4), 'parallel gate'),
+    (_settings(gate=4096, mode=21), 'mode bit 1'),
+    (_settings(hash_encoding=dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
+                                  per_level_scale=1.5), mode=16), 'half gradients'),
+    (_settings(hash_encoding=dict(n_levels=8, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
+                                  per_level_scale=1.5)), '16 levels x 2 features'),
+    (_settings(hash_encoding=dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
+                                  per_level_scale=1.5)), 'allocation differs'),
+])
+def test_runtime_rejects_settings_before_touching_the_device(native, settings, message):
+    assert native.odie_create(settings) is None
+    assert message in native.odie_error().decode()
+
+
+def test_runtime_entry_points_reject_a_null_handle(native):
+    assert native.odie_step(None, 8, 16, 1) == -1
+    assert 'null handle' in native.odie_error().decode()
+    assert native.odie_configure(None, b'{}') == -1
+    assert native.odie_sync_weights(None) == -1
+    assert native.odie_pointers(None) is None
+    assert native.odie_state(None, -1, -1) is None
+    native.odie_pin_contexts(None)
+    native.odie_release_contexts(None)
+    native.odie_destroy(None)
