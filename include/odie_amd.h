@@ -243,6 +243,23 @@ int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int64_t n, co
                        uint16_t* upstream, float* dweights, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Fused reconstruction: the streamed full-image inference of the residual pass
+ * (odie/evaluation.py:12-36, odie/gpu_residual.py:130-179, scripts/reconstruct.py:9-48), for
+ * the multi-expert hash-grid model.  Pixels [begin, begin+n) in raster order (id = y*W + x,
+ * 32-bit); the pixel's tile and tile coordinate follow odie_route; the tile's table slot is
+ * slots[tile] (device int32 [regions_x*regions_y]; < 0 or >= experts: no expert, features 0;
+ * slots null: slot = tile); the 16-level x 2-feature fp16 encode of that slot's table
+ * (table + slot*expert_params, the odie_grid_forward layout) feeds the decoder (weights as in
+ * odie_mlp_forward) without leaving registers.  Writes, where non-null, prediction fp32 [n][3]
+ * (the decoder's first three outputs), features fp16 [n][32] and output fp16 [n][16] at row
+ * id - begin: the same bits as odie_route + odie_grid_forward + odie_mlp_forward.
+ * --------------------------------------------------------------------------------------- */
+int odie_reconstruct(int64_t begin, int64_t n, int width, int height, int regions_x, int regions_y,
+                     const int32_t* slots, int experts, const uint16_t* table, int64_t expert_params,
+                     const odie_grid_level* levels, int n_levels, const uint16_t* weights, float* prediction,
+                     uint16_t* features, uint16_t* output, uint64_t stream);
+
+/* ---------------------------------------------------------------------------------------
  * The native training step: the reference's Probe handle (odie/native/runtime.cu:163-331),
  * bound by NativeOptimizer (odie/native_backend.py:32-44).  Same entry points, arguments and
  * 0 / -1 + odie_error convention; one step is ids -> xy and targets, the grid query (packed

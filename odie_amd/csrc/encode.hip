@@ -120,15 +120,9 @@ __device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, co
 #pragma unroll
                     for (int k = 0; k < 4; ++k) g[k] = reinterpret_cast<const uint32_t*>(t)[idx[k]];
                 }
-                __half2 acc = __half2(__float2half(0.0f), __float2half(0.0f));
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const __half2 value = __halves2half2(bits_to_half(static_cast<uint16_t>(g[k] & 0xffffu)),
-                                                         bits_to_half(static_cast<uint16_t>(g[k] >> 16)));
-                    acc = __hfma2(__float2half2_rn(keep_fp32(w[k])), value, acc);
-                }
-                vals[l * F] = __low2half(acc);
-                vals[l * F + 1] = __high2half(acc);
+                const uint32_t pair = half2_level(g, w);
+                vals[l * F] = bits_to_half(static_cast<uint16_t>(pair & 0xffffu));
+                vals[l * F + 1] = bits_to_half(static_cast<uint16_t>(pair >> 16));
             } else if constexpr (HALF && F % 2 == 0) {
                 __half2 acc[F / 2];
 #pragma unroll
@@ -329,21 +323,7 @@ int validate_grid(const char* what, const float* coords, int64_t n, const int32_
     if (features != 1 && features != 2 && features != 4 && features != 8)
         return fail(w + ": features per level must be 1, 2, 4 or 8");
     uint64_t entries = 0;
-    for (int l = 0; l < n_levels; ++l) {
-        const odie_grid_level& lv = levels[l];
-        if (lv.size == 0 || lv.resolution == 0) return fail(w + ": level size and resolution must be positive");
-        if (!(lv.scale == lv.scale)) return fail(w + ": level scale is NaN");
-        if (lv.offset != entries) return fail(w + ": level offsets must be contiguous from 0");
-        entries += lv.size;
-        DevLevel& d = a.level[l];
-        d.scale = lv.scale;
-        d.res = lv.resolution;
-        d.size = lv.size;
-        d.mask = (lv.size & (lv.size - 1)) == 0 ? lv.size - 1 : 0;
-        d.offset = lv.offset;
-        d.hashed = lv.hashed ? 1u : 0u;
-        d.prime = (d.mask && d.mask < (1u << 24)) ? (2654435761u & d.mask) : 2654435761u;
-    }
+    if (make_dev_levels(what, levels, n_levels, a.level, entries)) return -1;
     if (expert_params < static_cast<int64_t>(entries) * features)
         return fail(w + ": expert_params is smaller than the levels' table");
     a.coords = coords;

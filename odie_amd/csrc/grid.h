@@ -55,8 +55,47 @@ __device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32
     }
 }
 
+// One fp16 level of 2 features: acc = fma(fp16(w_k), entry_k, acc) over the corners in order,
+// from +0, on both features at once (v_pk_fma_f16); entries and the result are fp16 pairs
+// (feature 0 in the low half).  The forward's arithmetic (odie/packed_kernels.cu:52-62).
+__device__ inline uint32_t half2_level(const uint32_t g[4], const float w[4]) {
+    __half2 acc = __half2(__float2half(0.0f), __float2half(0.0f));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const __half2 value = __halves2half2(bits_to_half(static_cast<uint16_t>(g[k] & 0xffffu)),
+                                             bits_to_half(static_cast<uint16_t>(g[k] >> 16)));
+        acc = __hfma2(__float2half2_rn(keep_fp32(w[k])), value, acc);
+    }
+    return static_cast<uint32_t>(half_to_bits(__low2half(acc))) |
+           (static_cast<uint32_t>(half_to_bits(__high2half(acc))) << 16);
+}
+
 template <bool HALF>
 using Elem = typename std::conditional<HALF, __half, float>::type;
+
+// Host: device rows of an odie_grid_level table (levels contiguous from entry 0); entries
+// receives the table's entry count.  Returns 0, or -1 with the error set.
+inline int make_dev_levels(const char* what, const odie_grid_level* levels, int n_levels, DevLevel* out,
+                           uint64_t& entries) {
+    const std::string w(what);
+    entries = 0;
+    for (int l = 0; l < n_levels; ++l) {
+        const odie_grid_level& lv = levels[l];
+        if (lv.size == 0 || lv.resolution == 0) return fail(w + ": level size and resolution must be positive");
+        if (!(lv.scale == lv.scale)) return fail(w + ": level scale is NaN");
+        if (lv.offset != entries) return fail(w + ": level offsets must be contiguous from 0");
+        entries += lv.size;
+        DevLevel& d = out[l];
+        d.scale = lv.scale;
+        d.res = lv.resolution;
+        d.size = lv.size;
+        d.mask = (lv.size & (lv.size - 1)) == 0 ? lv.size - 1 : 0;
+        d.offset = lv.offset;
+        d.hashed = lv.hashed ? 1u : 0u;
+        d.prime = (d.mask && d.mask < (1u << 24)) ? (2654435761u & d.mask) : 2654435761u;
+    }
+    return 0;
+}
 
 // Host-side description of one owner-computes backward launch (backward.hip).
 struct AdamStep;

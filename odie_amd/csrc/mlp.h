@@ -1,0 +1,162 @@
+// MFMA building blocks of the decoder MLP 32 -> 64 -> 64 -> 16 (ReLU hidden layers, no bias,
+// fp16 weights and activations, fp32 accumulation), shared by the training kernel (mlp.hip) and
+// the fused reconstruction (reconstruct.hip) so that both compute the same bits.
+//
+// One wave per tile of 32 samples; every product is a v_mfma_f32_32x32x16_f16 with the samples
+// as the 32 columns.  Lane (g, s) = (lane / 32, lane % 32) holds, for sample s, input features
+// 16*kt + 8*g + e (kt = 0, 1; e = 0..7) as the B operand of layer 1; the accumulator layout of
+// one layer (rows 8*(v/4) + 4*g + v%4 of sample s) is the B operand of the next once the
+// weights' K columns are permuted the same way (slot_of).
+#pragma once
+#include "common.h"
+
+namespace odie {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef int16_t short8 __attribute__((ext_vector_type(8)));
+typedef uint16_t ushort8 __attribute__((ext_vector_type(8)));
+
+constexpr int kIn = 32, kHid = 64, kOut = 16;
+constexpr int kW1 = kHid * kIn, kW2 = kHid * kHid, kW3 = kOut * kHid;
+constexpr int kParams = kW1 + kW2 + kW3;
+constexpr int kMlpBlock = 256;
+constexpr int kMlpWaves = kMlpBlock / 64;
+
+// LDS rows are padded so that 16-byte reads of 16 consecutive lanes hit distinct banks.
+constexpr int kS32 = 40, kS64 = 72, kS16 = 24;
+constexpr int kW1a = 0;                     // W1 [64][32]            (layer 1, A operand)
+constexpr int kW2p = kW1a + 64 * kS32;      // W2 [64][slot(64)]      (layer 2)
+constexpr int kW3p = kW2p + 64 * kS64;      // W3 [16][slot(64)]      (layer 3)
+constexpr int kW3t = kW3p + 16 * kS64;      // W3^T [64][slot(16)]    (dH2 = W3^T dY)
+constexpr int kW2t = kW3t + 64 * kS16;      // W2^T [64][slot(64)]    (dH1 = W2^T dH2)
+constexpr int kW1t = kW2t + 64 * kS64;      // W1^T [32][slot(64)]    (dX = W1^T dH1)
+constexpr int kWeightHalfs = kW1t + 32 * kS64;
+
+// K slot of feature k inside a 16-wide K step: the accumulator row order
+// 16t + 8*(e/4) + 4*g + e%4 (lane group g, element e) flattened to 16t + 8g + e.
+__device__ inline int slot_of(int k) {
+    const int t = k >> 4, w = k & 15;
+    return 16 * t + 8 * ((w >> 2) & 1) + 4 * (w >> 3) + (w & 3);
+}
+// Feature held by lane group g, element e of K step t (inverse of slot_of).
+__device__ inline int feature_of(int t, int g, int e) { return 16 * t + 8 * (e >> 2) + 4 * g + (e & 3); }
+
+__device__ inline f32x16 mfma(half8 a, half8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ inline half8 lds8(const _Float16* p) { return *reinterpret_cast<const half8*>(p); }
+__device__ inline f32x16 zero16() { return f32x16{}; }
+
+// fp16 of acc[base .. base+7], two values per conversion (v_cvt_pk_f16_f32, round to nearest even).
+__device__ inline half8 round8(const f32x16& acc, int base) {
+    const half2v p0 = __builtin_convertvector((float2v){acc[base + 0], acc[base + 1]}, half2v);
+    const half2v p1 = __builtin_convertvector((float2v){acc[base + 2], acc[base + 3]}, half2v);
+    const half2v p2 = __builtin_convertvector((float2v){acc[base + 4], acc[base + 5]}, half2v);
+    const half2v p3 = __builtin_convertvector((float2v){acc[base + 6], acc[base + 7]}, half2v);
+    return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// ReLU of fp16 values on their bit patterns: a signed 16-bit max with 0 maps every negative
+// value and -0 to +0 and keeps positive values (v_pk_max_i16), so relu(fp16(x)) equals
+// fp16(x > 0 ? x : 0) bit for bit, and "h > 0" afterwards is "bits != 0".
+__device__ inline half8 relu8(half8 x) {
+    return __builtin_bit_cast(half8, __builtin_elementwise_max(__builtin_bit_cast(short8, x), short8{}));
+}
+
+// dh where the forward activation h is nonzero, +0 elsewhere: min(bits(h), 1) is 1 or 0 per
+// value and multiplies the bit pattern of dh (v_pk_min_u16, v_pk_mul_lo_u16).
+__device__ inline half8 mask8(half8 dh, half8 h) {
+    const ushort8 keep = __builtin_elementwise_min(__builtin_bit_cast(ushort8, h), (ushort8)(uint16_t{1}));
+    return __builtin_bit_cast(half8, __builtin_bit_cast(ushort8, dh) * keep);
+}
+
+// Weights into LDS in the six operand layouts (once per workgroup).
+__device__ inline void stage_weights(const uint16_t* weights, _Float16* w) {
+    for (int i = threadIdx.x; i < kParams; i += kMlpBlock) {
+        const _Float16 v = __builtin_bit_cast(_Float16, weights[i]);
+        if (i < kW1) {
+            const int r = i / kIn, c = i % kIn;
+            w[kW1a + r * kS32 + c] = v;
+            w[kW1t + c * kS64 + slot_of(r)] = v;
+        } else if (i < kW1 + kW2) {
+            const int j = i - kW1, r = j / kHid, c = j % kHid;
+            w[kW2p + r * kS64 + slot_of(c)] = v;
+            w[kW2t + c * kS64 + slot_of(r)] = v;
+        } else {
+            const int j = i - kW1 - kW2, o = j / kHid, c = j % kHid;
+            w[kW3p + o * kS64 + slot_of(c)] = v;
+            w[kW3t + c * kS16 + slot_of(o)] = v;
+        }
+    }
+}
+
+struct MlpArgs {
+    const uint16_t* x;        // [n][32] fp16
+    const uint16_t* weights;  // [7168] fp16
+    int64_t n;
+    int64_t real;             // rows whose input index is >= real are padding (dy = 0)
+    const uint32_t* colors;   // packed RGB8 target of tile row j, or null
+    const uint8_t* rgb;       // image bytes [pixels][3] (target by pixel id), or null
+    const int64_t* ids;       // pixel id per input row (with rgb)
+    const float* target;      // fp32 [input rows][3] (without rgb)
+    const int32_t* rows;      // input row of tile row j (null: identity)
+    uint16_t* out;            // fp16 [input rows][16], or null
+    uint16_t* hidden;         // fp16 [n][128] = h1 | h2 of tile row j, or null
+    float* squares;           // fp32 [input rows], or null
+    uint16_t* dz;             // fp16 [n][32] = fp16(fp16(dL/dx) / 128)
+    float* partials;          // fp32 [blocks][7168]
+};
+
+// Forward of one tile: x (B operand of layer 1) -> h1, h2 (B operands of the next layers),
+// y accumulator (rows 0..15 valid).
+__device__ inline void forward_tile(const _Float16* w, int g, int s, const half8 xb[2], half8 h1[4], half8 h2[4],
+                                    f32x16& acc3) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) acc = mfma(lds8(w + kW1a + (mb * 32 + s) * kS32 + kt * 16 + 8 * g), xb[kt], acc);
+        h1[2 * mb] = relu8(round8(acc, 0));
+        h1[2 * mb + 1] = relu8(round8(acc, 8));
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW2p + (mb * 32 + s) * kS64 + 16 * t + 8 * g), h1[t], acc);
+        h2[2 * mb] = relu8(round8(acc, 0));
+        h2[2 * mb + 1] = relu8(round8(acc, 8));
+    }
+    acc3 = zero16();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const half8 a = s < kOut ? lds8(w + kW3p + s * kS64 + 16 * t + 8 * g) : half8{};
+        acc3 = mfma(a, h2[t], acc3);
+    }
+}
+
+// Forward-only copy of the weights: the three A-operand layouts forward_tile reads.
+constexpr int kForwardHalfs = kW3t;
+__device__ inline void stage_forward_weights(const uint16_t* weights, _Float16* w) {
+    for (int i = threadIdx.x; i < kParams; i += kMlpBlock) {
+        const _Float16 v = __builtin_bit_cast(_Float16, weights[i]);
+        if (i < kW1) {
+            w[kW1a + (i / kIn) * kS32 + i % kIn] = v;
+        } else if (i < kW1 + kW2) {
+            const int j = i - kW1;
+            w[kW2p + (j / kHid) * kS64 + slot_of(j % kHid)] = v;
+        } else {
+            const int j = i - kW1 - kW2;
+            w[kW3p + (j / kHid) * kS64 + slot_of(j % kHid)] = v;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace odie

@@ -1,0 +1,187 @@
+// Fused reconstruction of an image through the multi-expert hash-grid model: for every pixel
+// of a raster range, its expert tile and tile coordinate (the router's convention), the 16-level
+// fp16 encode from that expert's table and the decoder MLP, in one kernel, so the features never
+// reach memory.  The streamed full-image inference the residual pass scores
+// (odie/evaluation.py:12-36, odie/gpu_residual.py:130-179: prediction = model(coordinates(ids))
+// for ids in raster order).
+//
+// One wave per tile of 32 consecutive pixels.  Lane (g, s) encodes pixel s's levels
+// 8*kt + 4*g + j (kt = 0, 1; j = 0..3): exactly the features 16*kt + 8*g + e that the decoder's
+// first MFMA takes from that lane as its B operand, so the encode feeds the MLP in registers.
+// Every value is computed with the arithmetic of odie_grid_forward (fp16 table, fp16 FMA chain,
+// half2_level) and odie_mlp_forward (forward_tile): the same bits as those two entry points on
+// the routed coordinates.
+#include "grid.h"
+#include "mlp.h"
+#include "tiles.h"
+#include "../../include/odie_amd.h"
+
+namespace odie {
+namespace {
+
+constexpr int kLevels = 16;
+constexpr int kReconBlock = kMlpBlock;
+constexpr int kReconWaves = kReconBlock / 64;
+
+struct ReconArgs {
+    int64_t begin;
+    int64_t n;
+    uint32_t width;
+    uint32_t height;
+    int regions_x;
+    int regions_y;
+    int experts;
+    const int32_t* slots;      // table slot of each tile, < 0: no expert (null: slot = tile)
+    const uint32_t* table;     // fp16 pairs
+    int64_t expert_pairs;      // pairs per expert
+    const uint16_t* weights;
+    float* prediction;         // [n][3] or null
+    uint16_t* features;        // [n][32] or null
+    uint16_t* output;          // [n][16] or null
+    DevLevel level[kLevels];
+};
+
+__device__ inline DevLevel pick(const DevLevel& first, const DevLevel& second, bool take_second) {
+    DevLevel d;
+    d.scale = take_second ? second.scale : first.scale;
+    d.res = take_second ? second.res : first.res;
+    d.size = take_second ? second.size : first.size;
+    d.mask = take_second ? second.mask : first.mask;
+    d.offset = take_second ? second.offset : first.offset;
+    d.hashed = take_second ? second.hashed : first.hashed;
+    d.prime = take_second ? second.prime : first.prime;
+    return d;
+}
+
+__global__ __launch_bounds__(kReconBlock) void reconstruct_kernel(ReconArgs a, TileBounds bounds) {
+    __shared__ _Float16 w[kForwardHalfs];
+    __shared__ TileBounds tb;
+    stage_forward_weights(a.weights, w);
+    for (int j = threadIdx.x; j <= kMaxTiles; j += kReconBlock) {
+        tb.x0[j] = bounds.x0[j];
+        tb.y0[j] = bounds.y0[j];
+        if (j < kMaxTiles) {
+            tb.rx[j] = bounds.rx[j];
+            tb.ry[j] = bounds.ry[j];
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x % 64, g = lane / 32, s = lane % 32;
+    const int64_t tiles = (a.n + 31) / 32;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kReconWaves;
+    for (int64_t tile = static_cast<int64_t>(blockIdx.x) * kReconWaves + threadIdx.x / 64; tile < tiles;
+         tile += waves) {
+        const int64_t row = tile * 32 + s;
+        const bool valid = row < a.n;
+        const uint32_t id = static_cast<uint32_t>(a.begin + (valid ? row : 0));
+        const uint32_t x = id % a.width;
+        uint32_t y = id / a.width;
+        if (y >= a.height) y = a.height - 1;
+        const int tx = tile_of(tb.x0, a.regions_x, x), ty = tile_of(tb.y0, a.regions_y, y);
+        const int t = ty * a.regions_x + tx;
+        int slot = a.slots ? a.slots[t] : t;
+        if (slot >= a.experts || !valid) slot = -1;
+        const float u = static_cast<float>(x - static_cast<uint32_t>(tb.x0[tx])) * tb.rx[tx];
+        const float v = static_cast<float>(y - static_cast<uint32_t>(tb.y0[ty])) * tb.ry[ty];
+        const uint32_t* table = a.table + (slot >= 0 ? static_cast<int64_t>(slot) * a.expert_pairs : 0);
+        uint32_t pairs[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                // both half-waves' levels are read with uniform indices, then selected per lane
+                const DevLevel lv = pick(a.level[8 * kt + j], a.level[8 * kt + 4 + j], g != 0);
+                uint32_t idx[4];
+                float wk[4];
+                grid_corners(lv, u, v, idx, wk);
+                uint32_t e[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) e[k] = slot >= 0 ? table[lv.offset + idx[k]] : 0u;
+                pairs[kt][j] = slot >= 0 ? half2_level(e, wk) : 0u;
+            }
+        }
+        half8 xb[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+            xb[kt] = __builtin_bit_cast(half8, u32x4{pairs[kt][0], pairs[kt][1], pairs[kt][2], pairs[kt][3]});
+        half8 h1[4], h2[4];
+        f32x16 acc3;
+        forward_tile(w, g, s, xb, h1, h2, acc3);
+        const half8 out = round8(acc3, 0);
+        if (!valid) continue;
+        if (a.features) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                *reinterpret_cast<uint4*>(a.features + row * 32 + 16 * kt + 8 * g) =
+                    make_uint4(pairs[kt][0], pairs[kt][1], pairs[kt][2], pairs[kt][3]);
+        }
+        if (a.output) {
+            const u32x4 bits = __builtin_bit_cast(u32x4, out);
+            uint16_t* p = a.output + row * 16;
+            *reinterpret_cast<uint2*>(p + 4 * g) = make_uint2(bits.x, bits.y);
+            *reinterpret_cast<uint2*>(p + 8 + 4 * g) = make_uint2(bits.z, bits.w);
+        }
+        // output rows 0..2 (the RGB prediction) are elements 0..2 of lane group 0
+        if (a.prediction && g == 0) {
+            const u32x4 bits = __builtin_bit_cast(u32x4, out);   // element 2i in the low half of dword i
+            float* p = a.prediction + row * 3;
+            p[0] = __half2float(bits_to_half(static_cast<uint16_t>(bits.x & 0xffffu)));
+            p[1] = __half2float(bits_to_half(static_cast<uint16_t>(bits.x >> 16)));
+            p[2] = __half2float(bits_to_half(static_cast<uint16_t>(bits.y & 0xffffu)));
+        }
+    }
+}
+
+}  // namespace
+}  // namespace odie
+
+using namespace odie;
+
+ODIE_API int odie_reconstruct(int64_t begin, int64_t n, int width, int height, int regions_x, int regions_y,
+                              const int32_t* slots, int experts, const uint16_t* table, int64_t expert_params,
+                              const odie_grid_level* levels, int n_levels, const uint16_t* weights, float* prediction,
+                              uint16_t* features, uint16_t* output, uint64_t stream) {
+    if (n < 0 || begin < 0) return fail("odie_reconstruct: begin and n must be nonnegative");
+    if (regions_x < 1 || regions_y < 1 || regions_x > kMaxTiles || regions_y > kMaxTiles)
+        return fail("odie_reconstruct: regions per axis must be within 1..64");
+    if (width < 2 * regions_x || height < 2 * regions_y)
+        return fail("odie_reconstruct: every tile needs at least two pixels per axis");
+    const uint64_t pixels = static_cast<uint64_t>(width) * static_cast<uint64_t>(height);
+    if (pixels > (uint64_t{1} << 32)) return fail("odie_reconstruct: images are limited to 2^32 pixels");
+    if (static_cast<uint64_t>(begin) + static_cast<uint64_t>(n) > pixels)
+        return fail("odie_reconstruct: the pixel range runs past the image");
+    if (n_levels != kLevels) return fail("odie_reconstruct: the fused decoder takes 16 levels x 2 features");
+    if (experts < 1) return fail("odie_reconstruct: experts must be >= 1");
+    if (!levels) return fail("odie_reconstruct: levels is null");
+    ReconArgs a{};
+    uint64_t entries = 0;
+    if (make_dev_levels("odie_reconstruct", levels, n_levels, a.level, entries)) return -1;
+    if (expert_params < static_cast<int64_t>(entries) * 2 || expert_params % 2)
+        return fail("odie_reconstruct: expert_params must be even and hold the levels' table");
+    if (n == 0) return 0;
+    if (!table || !weights || (!prediction && !features && !output)) return fail("odie_reconstruct: null pointer");
+    if (reinterpret_cast<uintptr_t>(table) % 4 || (features && reinterpret_cast<uintptr_t>(features) % 16) ||
+        (output && reinterpret_cast<uintptr_t>(output) % 8))
+        return fail("odie_reconstruct: table must be 4-byte, features 16-byte and output 8-byte aligned");
+    a.begin = begin;
+    a.n = n;
+    a.width = static_cast<uint32_t>(width);
+    a.height = static_cast<uint32_t>(height);
+    a.regions_x = regions_x;
+    a.regions_y = regions_y;
+    a.experts = experts;
+    a.slots = slots;
+    a.table = reinterpret_cast<const uint32_t*>(table);
+    a.expert_pairs = expert_params / 2;
+    a.weights = weights;
+    a.prediction = prediction;
+    a.features = features;
+    a.output = output;
+    TileBounds bounds;
+    make_tile_bounds(width, height, regions_x, regions_y, bounds);
+    const int64_t tiles = (n + 31) / 32;
+    int64_t blocks = (tiles + kReconWaves - 1) / kReconWaves;
+    if (blocks > 4096) blocks = 4096;
+    reconstruct_kernel<<<static_cast<uint32_t>(blocks), kReconBlock, 0, as_stream(stream)>>>(a, bounds);
+    return check_launch("odie_reconstruct");
+}

@@ -18,6 +18,7 @@
 //           expert in the group), and a per-wave running count in LDS carries the order
 //           across groups.  No global atomics, so the result is deterministic.
 #include "common.h"
+#include "tiles.h"
 #include "../../include/odie_amd.h"
 
 namespace odie {
@@ -25,7 +26,7 @@ namespace {
 
 constexpr int kRouteBlock = 256;
 constexpr int kWaves = kRouteBlock / 64;
-constexpr int kMaxRegions = 64;
+constexpr int kMaxRegions = kMaxTiles;
 constexpr int kMaxExperts = kMaxRegions * kMaxRegions;
 
 struct RouteArgs {
@@ -58,24 +59,14 @@ struct Bounds {
     int32_t y0[kMaxRegions + 1];
 };
 
-__device__ inline int region_of(const int32_t* bounds, int regions, uint32_t v) {
-    // largest r with bounds[r] <= v
-    int lo = 0, hi = regions - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (static_cast<uint32_t>(bounds[mid]) <= v) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-}
-
 __device__ inline void locate(const RouteArgs& a, const Bounds& b, int64_t i, int& expert, uint32_t& x, uint32_t& y,
                               int& rx, int& ry) {
     const uint32_t id = static_cast<uint32_t>(a.ids[i]);
     x = id % a.width;
     y = id / a.width;
     if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
-    rx = region_of(b.x0, a.regions_x, x);
-    ry = region_of(b.y0, a.regions_y, y);
+    rx = tile_of(b.x0, a.regions_x, x);
+    ry = tile_of(b.y0, a.regions_y, y);
     expert = ry * a.regions_x + rx;
 }
 
@@ -312,16 +303,17 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     a.expert_bits = 0;
     while ((1 << a.expert_bits) < experts) ++a.expert_bits;
     route_plan(n, experts, a.part, a.parts);
-    for (int r = 0; r <= kMaxRegions; ++r) {
-        const int rxx = r < regions_x ? r : regions_x, ryy = r < regions_y ? r : regions_y;
-        a.x0[r] = static_cast<int32_t>((static_cast<int64_t>(rxx) * width + regions_x - 1) / regions_x);
-        a.y0[r] = static_cast<int32_t>((static_cast<int64_t>(ryy) * height + regions_y - 1) / regions_y);
-    }
-    for (int r = 0; r < kMaxRegions; ++r) {
-        const int tw = r < regions_x ? a.x0[r + 1] - a.x0[r] : 2;
-        const int th = r < regions_y ? a.y0[r + 1] - a.y0[r] : 2;
-        a.rx[r] = static_cast<float>(1.0 / static_cast<double>(tw - 1));
-        a.ry[r] = static_cast<float>(1.0 / static_cast<double>(th - 1));
+    {
+        TileBounds tb;
+        make_tile_bounds(width, height, regions_x, regions_y, tb);
+        for (int r = 0; r <= kMaxRegions; ++r) {
+            a.x0[r] = tb.x0[r];
+            a.y0[r] = tb.y0[r];
+        }
+        for (int r = 0; r < kMaxRegions; ++r) {
+            a.rx[r] = tb.rx[r];
+            a.ry[r] = tb.ry[r];
+        }
     }
     const hipStream_t s = as_stream(stream);
     const size_t shmem = static_cast<size_t>(kWaves) * experts * 4;

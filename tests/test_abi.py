@@ -193,3 +193,19 @@ def test_runtime_entry_points_reject_a_null_handle(native):
     native.odie_pin_contexts(None)
     native.odie_release_contexts(None)
     native.odie_destroy(None)
+
+
+def test_reconstruct_rejects_bad_arguments(native):
+    levels, entries = grid_levels(dict(n_levels=16, base_resolution=4, log2_hashmap_size=8, per_level_scale=1.3))
+    params = entries * 2
+    call = lambda **k: native.odie_reconstruct(
+        k.get('begin', 0), k.get('n', 64), k.get('width', 64), k.get('height', 64), k.get('rx', 2), k.get('ry', 2),
+        None, k.get('experts', 4), 4096, k.get('params', params), levels, k.get('levels', 16), 4096, 4096, None,
+        None, 0)
+    for change, message in [(dict(n=-1), 'nonnegative'), (dict(rx=65), 'regions per axis'),
+                            (dict(width=3), 'two pixels'), (dict(begin=64 * 64 - 10, n=11), 'past the image'),
+                            (dict(levels=8), '16 levels'), (dict(experts=0), 'experts'),
+                            (dict(params=params - 1), 'expert_params')]:
+        assert call(**change) == -1, change
+        assert message in native.odie_error().decode(), (change, native.odie_error())
+    assert call(n=0) == 0
