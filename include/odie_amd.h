@@ -259,6 +259,19 @@ int odie_reconstruct(int64_t begin, int64_t n, int width, int height, int region
                      const odie_grid_level* levels, int n_levels, const uint16_t* weights, float* prediction,
                      uint16_t* features, uint16_t* output, uint64_t stream);
 
+/* Fused reconstruction + residual: every pixel of the image predicted as odie_reconstruct does,
+ * scored into per-cell fp64 totals with score_chunk's rule and order (one cell at a time, its
+ * pixels in raster order), with no prediction in memory.  target: RGB8 [H*W][3]; cells are
+ * [xb[cx], xb[cx+1]) x [yb[cy], yb[cy+1]) for cx, cy < resolution (device int32 [R+1]);
+ * totals fp64 [R*R] are read and updated (as successive score_chunk calls over the whole image
+ * leave them); squares (fp64 [R*R], nullable) receive each cell's sum of (p - byte*(1/255))^2
+ * over its pixels and channels in fp64 (the mse numerator of odie/evaluation.py:25, in a
+ * different summation order); prediction (fp32 [H*W][3], nullable) receives the image. */
+int odie_reconstruct_scores(int width, int height, int regions_x, int regions_y, const int32_t* slots, int experts,
+                            const uint16_t* table, int64_t expert_params, const odie_grid_level* levels, int n_levels,
+                            const uint16_t* weights, const uint8_t* target, int resolution, const int32_t* xb,
+                            const int32_t* yb, double* totals, double* squares, float* prediction, uint64_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * The native training step: the reference's Probe handle (odie/native/runtime.cu:163-331),
  * bound by NativeOptimizer (odie/native_backend.py:32-44).  Same entry points, arguments and

@@ -8,7 +8,7 @@
 // sequential chain; the parallelism is across cells.  To keep the chain's latency the only
 // serial part, every thread first computes the per-pixel terms of the next run of pixels of
 // its row (independent work the scheduler can overlap) and then folds them in order.
-#include "common.h"
+#include "residual.h"
 #include "../../include/odie_amd.h"
 
 namespace odie {
@@ -22,19 +22,16 @@ __device__ inline double pixel_term(const float* prediction, const void* target,
     float t0, t1, t2;
     if constexpr (RGB8) {
         const uint8_t* bytes = static_cast<const uint8_t*>(target);
-        t0 = static_cast<float>(bytes[p]) / 255.0f;
-        t1 = static_cast<float>(bytes[p + 1]) / 255.0f;
-        t2 = static_cast<float>(bytes[p + 2]) / 255.0f;
+        t0 = byte_target(bytes[p]);
+        t1 = byte_target(bytes[p + 1]);
+        t2 = byte_target(bytes[p + 2]);
     } else {
         const float* values = static_cast<const float*>(target);
         t0 = values[p];
         t1 = values[p + 1];
         t2 = values[p + 2];
     }
-    const float d0 = prediction[p] - t0, d1 = prediction[p + 1] - t1, d2 = prediction[p + 2] - t2;
-    double rgb = static_cast<double>(d0 * d0) + static_cast<double>(d1 * d1);
-    rgb = rgb + static_cast<double>(d2 * d2);
-    return rgb / 3.0;
+    return residual_term(prediction[p], prediction[p + 1], prediction[p + 2], t0, t1, t2);
 }
 
 template <bool RGB8>

@@ -44,24 +44,41 @@ def reconstruct(grid, decoder_half, shape, regions, begin, n, *, slots=None, pre
 
 @torch.no_grad()
 def score_image(grid, decoder_half, target, shape, regions, *, resolution=None, tile=None, batch=1 << 24,
-                slots=None):
-    """Reconstruct the whole image batch by batch and score it: returns ({'mse', 'psnr_db'},
-    DeviceScores).  target: CUDA uint8 [H*W, 3].  Cells are the native geometry cells at
-    `resolution`, or uniform tiles of `tile` pixels (DeviceScores)."""
+                slots=None, fused=True, prediction=None):
+    """Reconstruct the whole image and score it: returns ({'mse', 'psnr_db'}, DeviceScores).
+    target: CUDA uint8 [H*W, 3].  Cells are the native geometry cells at `resolution`, or
+    uniform tiles of `tile` pixels (DeviceScores).  fused: one odie_reconstruct_scores launch
+    (a wave per cell, no prediction in memory unless `prediction` [H*W, 3] is given); otherwise
+    batches of `batch` pixels through odie_reconstruct and score_chunk with the reference's torch
+    mse."""
     height, width = shape
     pixels = height * width
     if target.dtype != torch.uint8 or tuple(target.shape) != (pixels, 3):
         raise ValueError('target must be uint8 [H*W, 3]')
     scores = DeviceScores(shape, resolution=resolution, tile=tile, device=target.device)
-    total = torch.zeros((), dtype=torch.float64, device=target.device)
-    buffer = torch.empty((min(batch, pixels), 3), dtype=torch.float32, device=target.device)
-    for begin in range(0, pixels, batch):
-        n = min(batch, pixels - begin)
-        prediction = reconstruct(grid, decoder_half, shape, regions, begin, n, slots=slots, prediction=buffer[:n])
-        truth = target[begin:begin + n]
-        # the mse of odie/evaluation.py:25 (ByteTarget: bytes / 255. on the device)
-        total += (prediction - truth.float() / 255.).square().double().sum()
-        scores.add(prediction, truth, begin)
+    if fused:
+        if grid.table.dtype != torch.float16 or grid.features != 2:
+            raise ValueError('the fused reconstruction reads fp16 tables of 2 features per level')
+        if prediction is not None and (tuple(prediction.shape) != (pixels, 3) or prediction.dtype != torch.float32):
+            raise ValueError('prediction must be fp32 [H*W, 3]')
+        squares = torch.zeros(scores.resolution ** 2, dtype=torch.float64, device=target.device)
+        xb, yb = scores.xb.to(torch.int32).contiguous(), scores.yb.to(torch.int32).contiguous()
+        _lib.check(_lib.library().odie_reconstruct_scores(
+            width, height, regions[0], regions[1], _lib.ptr(slots), grid.experts, grid.table.data_ptr(),
+            grid.expert_params, grid.levels, len(grid.levels), decoder_half.data_ptr(), target.data_ptr(),
+            scores.resolution, xb.data_ptr(), yb.data_ptr(), scores.totals.data_ptr(), squares.data_ptr(),
+            _lib.ptr(prediction), _lib.stream_of(target)))
+        total = squares.sum()
+    else:
+        total = torch.zeros((), dtype=torch.float64, device=target.device)
+        buffer = torch.empty((min(batch, pixels), 3), dtype=torch.float32, device=target.device)
+        for begin in range(0, pixels, batch):
+            n = min(batch, pixels - begin)
+            chunk = reconstruct(grid, decoder_half, shape, regions, begin, n, slots=slots, prediction=buffer[:n])
+            truth = target[begin:begin + n]
+            # the mse of odie/evaluation.py:25 (ByteTarget: bytes / 255. on the device)
+            total += (chunk - truth.float() / 255.).square().double().sum()
+            scores.add(chunk, truth, begin)
     mse = float(total.item() / target.numel())
     if not math.isfinite(mse) or not bool(torch.isfinite(scores.totals).all()):
         raise FloatingPointError('GPU live RGB residual is nonfinite')

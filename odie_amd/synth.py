@@ -105,3 +105,59 @@ def image(seed, width, height, octaves=6, edges=32):
         rgb[y0:y1 + 1, x0:x1 + 1] += colours[e]
     low, high = rgb.min(), rgb.max()
     return np.round((rgb - low) / (high - low) * 255.0).astype(np.uint8)
+
+
+def image_device(seed, width, height, octaves=6, edges=32, device='cuda', rows=2048):
+    """image() computed with torch on `device`, `rows` image rows at a time (for gigapixel
+    sizes): the same fp64 operations in the same order, so the same bytes; uint8 [height,
+    width, 3].  Divisions are tensor by tensor (torch turns division by a Python scalar into a
+    reciprocal multiply)."""
+    import torch
+
+    def axis(size, cells):
+        t = np.arange(size, dtype=np.float64) / (size - 1)
+        g = t * cells
+        i = np.minimum(g.astype(np.int64), cells - 1)
+        f = g - i
+        return torch.from_numpy(i).to(device), torch.from_numpy(f * f * (3.0 - 2.0 * f)).to(device)
+
+    octave_rows, octave_y = [], []
+    for k in range(octaves):
+        cells = 4 << k
+        lattice = torch.from_numpy(uniform(seed, 'octave%d' % k, (cells + 1) * (cells + 1) * 3).astype(np.float64)
+                                   .reshape(cells + 1, cells + 1, 3)).to(device)
+        ix, fx = axis(width, cells)
+        octave_rows.append(lattice[:, ix] * (1 - fx)[None, :, None] + lattice[:, ix + 1] * fx[None, :, None])
+        octave_y.append(axis(height, cells))
+    corners = integers(seed, 'edge_corners', edges * 4, 1 << 30)
+    colours = torch.from_numpy(uniform(seed, 'edge_colours', edges * 3).astype(np.float64).reshape(edges, 3) - 0.5)
+    boxes = []
+    for e in range(edges):
+        x0, x1 = sorted(int(c) * width >> 30 for c in corners[4 * e:4 * e + 2])
+        y0, y1 = sorted(int(c) * height >> 30 for c in corners[4 * e + 2:4 * e + 4])
+        boxes.append((x0, x1, y0, y1, colours[e].to(device)))
+
+    def block(r0, r1):
+        rgb = torch.zeros((r1 - r0, width, 3), dtype=torch.float64, device=device)
+        for k in range(octaves):
+            iy, fy = octave_y[k]
+            iy, fy = iy[r0:r1], fy[r0:r1]
+            rows_ = octave_rows[k]
+            rgb += (rows_[iy] * (1 - fy)[:, None, None] + rows_[iy + 1] * fy[:, None, None]) * 0.5 ** k
+        for x0, x1, y0, y1, colour in boxes:
+            a, b = max(y0, r0), min(y1 + 1, r1)
+            if a < b:
+                rgb[a - r0:b - r0, x0:x1 + 1] += colour
+        return rgb
+
+    low = high = None
+    for r0 in range(0, height, rows):
+        rgb = block(r0, min(r0 + rows, height))
+        low = rgb.min() if low is None else torch.minimum(low, rgb.min())
+        high = rgb.max() if high is None else torch.maximum(high, rgb.max())
+    out = torch.empty((height, width, 3), dtype=torch.uint8, device=device)
+    span = high - low
+    for r0 in range(0, height, rows):
+        r1 = min(r0 + rows, height)
+        out[r0:r1] = torch.round((block(r0, r1) - low) / span * 255.0).to(torch.uint8)
+    return out

@@ -209,3 +209,14 @@ def test_reconstruct_rejects_bad_arguments(native):
         assert call(**change) == -1, change
         assert message in native.odie_error().decode(), (change, native.odie_error())
     assert call(n=0) == 0
+
+
+def test_reconstruct_scores_rejects_bad_arguments(native):
+    levels, entries = grid_levels(dict(n_levels=16, base_resolution=4, log2_hashmap_size=8, per_level_scale=1.3))
+    call = lambda resolution=8, experts=4, target=4096: native.odie_reconstruct_scores(
+        64, 64, 2, 2, None, experts, 4096, entries * 2, levels, 16, 4096, target, resolution, 4096, 4096, 4096, None,
+        None, 0)
+    for kwargs, message in [(dict(resolution=0), 'resolution'), (dict(experts=0), 'experts'),
+                            (dict(target=None), 'null pointer')]:
+        assert call(**kwargs) == -1
+        assert message in native.odie_error().decode()

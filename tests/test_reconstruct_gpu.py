@@ -3,7 +3,9 @@ route the raster ids, encode the compacted coordinates (odie_grid_forward), run 
 (odie_mlp_forward) and put the rows back in raster order -- features, decoder outputs and
 predictions bit for bit, over ragged ranges and with tiles that have no expert.  Then the
 scoring pipeline (score_image): per-cell totals bit-exact against the oracle's residual of the
-fused predictions, the top tiles against the oracle's ranking, the mse against float64."""
+fused predictions, the top tiles against the oracle's ranking, the mse against torch's expression;
+both the streamed form (odie_reconstruct + score_chunk) and the fused one (odie_reconstruct_scores,
+a wave per cell)."""
 import numpy as np
 import pytest
 import torch
@@ -83,22 +85,27 @@ def test_tiles_without_an_expert_predict_zero():
     assert bool(empty.any()) and bool((output[empty] == 0).all())
 
 
-@pytest.mark.parametrize('shape,resolution,tile,batch', [((128, 160), 8, None, 4096), ((128, 128), None, 32, 10000)])
-def test_scoring_pipeline_matches_the_oracle(shape, resolution, tile, batch):
-    regions = (4, 4)
-    grid, decoder = _model(4, 16)
+@pytest.mark.parametrize('fused', [True, False])
+@pytest.mark.parametrize('shape,resolution,tile,batch', [((128, 160), 8, None, 4096), ((128, 128), None, 32, 10000),
+                                                         ((90, 77), 5, None, 1000)])
+def test_scoring_pipeline_matches_the_oracle(shape, resolution, tile, batch, fused):
+    regions = (4, 4) if shape[0] >= 128 else (3, 2)
+    grid, decoder = _model(4, regions[0] * regions[1])
     image = synth.image(5, shape[1], shape[0]).reshape(-1, 3)
     target = torch.from_numpy(image).cuda()
-    metrics, scores = score_image(grid, decoder.half, target, shape, regions, resolution=resolution, tile=tile,
-                                  batch=batch)
     n = shape[0] * shape[1]
+    image_out = torch.full((n, 3), float('nan'), dtype=torch.float32, device='cuda') if fused else None
+    metrics, scores = score_image(grid, decoder.half, target, shape, regions, resolution=resolution, tile=tile,
+                                  batch=batch, fused=fused, prediction=image_out)
     prediction = reconstruct(grid, decoder.half, shape, regions, 0, n).cpu().numpy()
+    if fused:
+        assert np.array_equal(image_out.cpu().numpy().view(np.uint32), prediction.view(np.uint32))
     expected = oracle.residual(prediction, image, shape[1], scores.resolution, scores.xb.cpu().numpy(),
                                scores.yb.cpu().numpy())
     assert np.array_equal(scores.totals.cpu().numpy().view(np.uint64), expected.view(np.uint64))
     truth = torch.from_numpy(image).cuda().float() / 255.
     reference = ((torch.from_numpy(prediction).cuda() - truth).square().double().sum() / image.size).item()
-    assert metrics['mse'] == pytest.approx(reference, rel=1e-12)
+    assert metrics['mse'] == pytest.approx(reference, rel=1e-12)   # summation order only
     k = scores.resolution ** 2 // 4
     ids = topk_tiles(scores.totals / torch.from_numpy(scores.counts).cuda(), k).cpu().numpy()
     means = expected / scores.counts
