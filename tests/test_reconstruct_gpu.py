@@ -110,3 +110,9 @@ def test_scoring_pipeline_matches_the_oracle(shape, resolution, tile, batch, fus
     ids = topk_tiles(scores.totals / torch.from_numpy(scores.counts).cuda(), k).cpu().numpy()
     means = expected / scores.counts
     assert np.array_equal(ids, oracle.topk_ids(means, k))
+
+
+def test_device_image_on_the_gpu_equals_numpy():
+    expected = synth.image(7, 300, 170)
+    got = synth.image_device(7, 300, 170, device='cuda', rows=64).cpu().numpy()
+    assert np.array_equal(got, expected)
