@@ -243,6 +243,15 @@ int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int64_t n, co
                        uint16_t* upstream, float* dweights, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Stratified sampling, the device part of stratified_batches (odie/data.py:63-80): batch (a
+ * square power of two, side = sqrt(batch)) slots, slot j in stratum (j % side, j / side);
+ * uniforms fp32 [batch][2] (torch.rand's draws); ids int64 [batch] =
+ * clamp(trunc((u/side + stratum/side) * W)) + W * clamp(trunc((v/side + stratum_y/side) * H)),
+ * fp32 arithmetic as the reference's torch expression.
+ * --------------------------------------------------------------------------------------- */
+int odie_stratified_ids(const float* uniforms, int batch, int width, int height, int64_t* ids, uint64_t stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused reconstruction: the streamed full-image inference of the residual pass
  * (odie/evaluation.py:12-36, odie/gpu_residual.py:130-179, scripts/reconstruct.py:9-48), for
  * the multi-expert hash-grid model.  Pixels [begin, begin+n) in raster order (id = y*W + x,

@@ -48,6 +48,7 @@ SIGNATURES = {
     'odie_reconstruct': ([_I64, _I64, _I, _I, _I, _I, _P, _I, _P, _I64, _P, _I, _P, _P, _P, _P, _U64], _I),
     'odie_reconstruct_scores': ([_I, _I, _I, _I, _P, _I, _P, _I64, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _U64],
                                 _I),
+    'odie_stratified_ids': ([_P, _I, _I, _I, _P, _U64], _I),
     'odie_create': ([C.c_char_p], _P),
     'odie_step': ([_P, _U64, _I, _I], _I),
     'odie_configure': ([_P, C.c_char_p], _I),

@@ -42,6 +42,9 @@ PINS = {
     'gate': 'recorded gates of the reference (tests/golden/gate_support_sample.npz: effective = fp16(s*visible)); '
             'torch.sigmoid / softplus; exact fp16 arithmetic of parallel_gate_back checked by fractions; autograd '
             'of the gate MLP',
+    'stratified_ids': 'exact rational arithmetic: each pixel lies in its stratum\'s pixel interval, u = 0 gives '
+                      'floor(stratum * size / side), u -> 1 stays below the next stratum; axes distinguished on '
+                      'non-square images',
 }
 
 
@@ -603,3 +606,17 @@ def gate_upstream(direct16, dr16):
     """hash_router_gradient (odie/native/runtime.cu:99-103): fp16(direct + fp16(dr / 128))."""
     unscaled = (np.asarray(dr16, dtype=np.float16).astype(np.float32) / np.float32(128.0)).astype(np.float16)
     return (np.asarray(direct16, dtype=np.float16).astype(np.float64) + unscaled.astype(np.float64)).astype(np.float16)
+
+
+def stratified_ids(uniforms, width, height):
+    """ids of one stratified batch from fp32 uniforms [batch, 2], the expression of
+    odie/data.py:73-80 in numpy fp32: uv = u / side + stratum / side, pixel = trunc(uv * (W, H))
+    clamped, id = y * W + x."""
+    u = np.asarray(uniforms, dtype=np.float32).reshape(-1, 2)
+    batch = u.shape[0]
+    side = int(round(batch ** 0.5))
+    slots = np.arange(batch)
+    strata = np.stack((slots % side, slots // side), axis=1).astype(np.float32) / np.float32(side)
+    uv = u / np.float32(side) + strata
+    xy = (uv * np.array([width, height], dtype=np.float32)).astype(np.int64)
+    return np.clip(xy[:, 1], 0, height - 1) * width + np.clip(xy[:, 0], 0, width - 1)

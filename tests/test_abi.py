@@ -220,3 +220,10 @@ def test_reconstruct_scores_rejects_bad_arguments(native):
                             (dict(target=None), 'null pointer')]:
         assert call(**kwargs) == -1
         assert message in native.odie_error().decode()
+
+
+def test_stratified_ids_reject_bad_arguments(native):
+    assert native.odie_stratified_ids(8, 8, 10, 10, 8, 0) == -1
+    assert 'square power-of-two' in native.odie_error().decode()
+    assert native.odie_stratified_ids(8, 12, 10, 10, 8, 0) == -1
+    assert native.odie_stratified_ids(None, 16, 10, 10, 8, 0) == -1

@@ -616,3 +616,30 @@ def test_gate_mlp_backward_matches_autograd(oracle):
     expected = torch.cat([v.grad.reshape(-1) for v in w]).numpy()
     assert np.all(np.abs(dweights - expected) <= 2e-2 * magnitude + 1e-9)
     assert np.all(np.abs(dr.astype(np.float64) - xt.grad.numpy()) <= 2e-2 * dr_magnitude + 1e-6)
+
+
+# Stratified sampling ---------------------------------------------------------------------------
+
+def test_stratified_ids_follow_the_strata(oracle):
+    """The oracle's ids against exact rational arithmetic: with u in [0, 1) the pixel of slot j
+    lies in [floor(s * W / side), ceil((s + 1) * W / side)] of its stratum column s (rows alike;
+    the upper end is reachable only through fp32 rounding of u/side + s/side), u = 0 gives
+    floor(s * W / side) exactly (truncation, not rounding), and the axes are not swapped
+    (W != H)."""
+    from fractions import Fraction
+    import math
+    for width, height, batch in ((97, 61, 16), (1536, 2040, 64), (33, 5, 4), (2048, 1365, 1024)):
+        side = int(round(batch ** 0.5))
+        rng = np.random.default_rng(width)
+        u = rng.random((batch, 2), dtype=np.float32)
+        u[1] = np.nextafter(np.float32(1.0), np.float32(0.0))
+        ids = oracle.stratified_ids(u, width, height)
+        zero = oracle.stratified_ids(np.zeros((batch, 2), dtype=np.float32), width, height)
+        for j in range(batch):
+            sx, sy = j % side, j // side
+            assert zero[j] == math.floor(Fraction(sy * height, side)) * width + math.floor(Fraction(sx * width, side))
+            x, y = ids[j] % width, ids[j] // width
+            for value, s, size in ((x, sx, width), (y, sy, height)):
+                low = math.floor(Fraction(s * size, side))
+                high = min(math.ceil(Fraction((s + 1) * size, side)), size - 1)
+                assert low <= value <= high, (width, height, batch, j)
