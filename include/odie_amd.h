@@ -88,8 +88,10 @@ int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offse
 /* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
  * 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),
- * "xcd_remap" (0/1: XCD-major block order).  Results do not depend on them beyond fp32
- * summation order. */
+ * "xcd_remap" (0/1: XCD-major block order), "backward_mode" (1: owner computes, 0: atomics),
+ * "bucketed" (0/1: the owner's fine passes walk per-slice coordinate buckets), "owner_lds_bytes",
+ * "row_screen", "paired_loads", "forward_lds_bytes".  Results do not depend on them beyond fp32
+ * summation order and the owner's fixed-point scale. */
 int odie_set_tuning(const char* key, int value);
 
 /* ---------------------------------------------------------------------------------------

@@ -205,6 +205,15 @@ struct OwnerArgs {
     int cap;                         // int64 accumulators in LDS; the candidate rings follow them
     int fused;                       // 1: apply the optimizer step instead of writing the gradient
     AdamStep adam;
+    // Bucketed fine passes: pass p >= fine_first of expert e walks only the coordinates listed
+    // in its bucket, list + start_e * fine_passes + (p - fine_first) * n_e, of length
+    // bucket_count[e * fine_passes + p - fine_first] (start_e, n_e: the expert's coordinates).
+    int bucketed;
+    int fine_first;
+    int fine_passes;
+    const int32_t* bucket_count;
+    const int32_t* bucket_list;
+    int slice_bits[ODIE_MAX_LEVELS]; // bucketed: slice of entry j is j >> slice_bits
 };
 
 enum LevelKind { kDense = 0, kHashedPow2 = 1, kGeneric = 2, kHashed24 = 3 };
@@ -217,25 +226,9 @@ __device__ inline int32_t round_to_int(float x) {
     return r;
 }
 
-// Adds one coordinate's contributions at one level to the LDS slice [lo, lo+span).
-// us[c] = upstream feature c times the fixed-point scale 2^S ((w*u)*2^S == w*(u*2^S) exactly:
-// scaling by a power of two commutes with rounding).  Contributions are rounded to integers
-// before the (divergent) slice test so the masked part of the wave is only the LDS add.
-template <int F, int KIND>
-__device__ inline void contribute(float x, float y, const float* us, const DevLevel& lv, uint32_t lo, uint32_t span,
-                                  unsigned long long* acc) {
-    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
-    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
-    const float flx = floorf(px), fly = floorf(py);
-    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
-    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
-    const float fx = px - flx, fy = py - fly;
-    float w[4];
-    w[0] = (1.0f - fx) * (1.0f - fy);
-    w[1] = fx * (1.0f - fy);
-    w[2] = (1.0f - fx) * fy;
-    w[3] = fx * fy;
-    uint32_t idx[4];
+// Table entries of the four corners of grid cell (gx, gy) (grid_corners' indices, per level kind).
+template <int KIND>
+__device__ inline void corner_index(uint32_t gx, uint32_t gy, const DevLevel& lv, uint32_t idx[4]) {
     if constexpr (KIND == kHashed24) {
         // power-of-two table of at most 2^24 entries: 24-bit row multiply (see hash_row)
         const uint32_t h0 = __umul24(gy, lv.prime), h1 = __umul24(gy + 1u, lv.prime);
@@ -262,6 +255,34 @@ __device__ inline void contribute(float x, float y, const float* us, const DevLe
             idx[k] = wrap_index(cx ^ hash_row(cy, lv), lv);
         }
     }
+}
+
+__device__ inline int level_kind(const DevLevel& lv) {
+    if (lv.hashed && lv.mask && lv.mask < (1u << 24)) return kHashed24;
+    if (lv.hashed && lv.mask) return kHashedPow2;
+    return lv.hashed ? kGeneric : kDense;
+}
+
+// Adds one coordinate's contributions at one level to the LDS slice [lo, lo+span).
+// us[c] = upstream feature c times the fixed-point scale 2^S ((w*u)*2^S == w*(u*2^S) exactly:
+// scaling by a power of two commutes with rounding).  Contributions are rounded to integers
+// before the (divergent) slice test so the masked part of the wave is only the LDS add.
+template <int F, int KIND>
+__device__ inline void contribute(float x, float y, const float* us, const DevLevel& lv, uint32_t lo, uint32_t span,
+                                  unsigned long long* acc) {
+    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
+    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
+    const float flx = floorf(px), fly = floorf(py);
+    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
+    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
+    const float fx = px - flx, fy = py - fly;
+    float w[4];
+    w[0] = (1.0f - fx) * (1.0f - fy);
+    w[1] = fx * (1.0f - fy);
+    w[2] = (1.0f - fx) * fy;
+    w[3] = fx * fy;
+    uint32_t idx[4];
+    corner_index<KIND>(gx, gy, lv, idx);
     int32_t q[4][F];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -308,6 +329,30 @@ __device__ inline void accumulate_level(const float* coords, const Elem<HALF>* p
             const int64_t at = ii < b1 ? ii : b0;
             xy[b] = reinterpret_cast<const float2*>(coords)[at];
             load_upstream<F, HALF>(plane, at, scale, ii < b1, us[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
+    }
+}
+
+// The coordinates listed in list[k0, k1) against one level (a bucket of one slice).
+template <int F, bool HALF, int KIND>
+__device__ inline void accumulate_bucket(const float* coords, const Elem<HALF>* plane, const DevLevel lv,
+                                         const int32_t* list, int64_t k0, int64_t k1, uint32_t lo, uint32_t span,
+                                         float scale, unsigned long long* acc) {
+    for (int64_t k = k0 + threadIdx.x; k < k1; k += kBatch * kOwnerBlock) {
+        int32_t at[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int64_t kk = k + b * kOwnerBlock;
+            at[b] = list[kk < k1 ? kk : k0];
+        }
+        float2 xy[kBatch];
+        float us[kBatch][F];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            xy[b] = reinterpret_cast<const float2*>(coords)[at[b]];
+            load_upstream<F, HALF>(plane, at[b], scale, k + b * kOwnerBlock < k1, us[b]);
         }
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
@@ -369,17 +414,108 @@ __device__ inline void accumulate_rows(const float* coords, const Elem<HALF>* pl
     while (count > 0) drain(count < 64 ? count : 64);
 }
 
+// Bucketing of the fine passes: for every coordinate of an expert and every fine level, the
+// distinct slices its four corners fall in; each (expert, slice) bucket receives the
+// coordinate's index once.  A workgroup counts its share of one expert's coordinates per bucket
+// in LDS, reserves its run of every bucket with one global atomic, then writes the indices.
+// The order inside a bucket does not matter: the owner's integer sums are order free.
+constexpr int kBucketBlock = 256;
+
+template <int KIND>
+__device__ inline int slices_of(float x, float y, const DevLevel& lv, int bits, int slices[4]) {
+    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
+    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
+    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(floorf(px)));
+    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(floorf(py)));
+    uint32_t idx[4];
+    corner_index<KIND>(gx, gy, lv, idx);
+    int count = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int slice = static_cast<int>(idx[k] >> bits);
+        bool seen = false;
+#pragma unroll
+        for (int j = 0; j < k; ++j) seen |= j < count && slices[j] == slice;
+        if (!seen) slices[count++] = slice;
+    }
+    return count;
+}
+
+template <bool PLACE>
+__device__ inline void bucket_coordinate(const OwnerArgs& a, float x, float y, int32_t* bins, int32_t* list,
+                                         int64_t list_base, int64_t stride, int32_t index) {
+    for (int l = a.group; l < a.n_levels; ++l) {
+        const DevLevel& lv = a.level[l];
+        int slices[4];
+        int count;
+        switch (level_kind(lv)) {
+            case kHashed24: count = slices_of<kHashed24>(x, y, lv, a.slice_bits[l], slices); break;
+            case kHashedPow2: count = slices_of<kHashedPow2>(x, y, lv, a.slice_bits[l], slices); break;
+            case kGeneric: count = slices_of<kGeneric>(x, y, lv, a.slice_bits[l], slices); break;
+            default: count = slices_of<kDense>(x, y, lv, a.slice_bits[l], slices); break;
+        }
+        for (int j = 0; j < count; ++j) {
+            const int q = a.first_pass[l] - a.fine_first + (slices[j] < a.slices[l] ? slices[j] : a.slices[l] - 1);
+            const int32_t at = atomicAdd(bins + q, 1);
+            if constexpr (PLACE) list[list_base + static_cast<int64_t>(q) * stride + bins[a.fine_passes + q] + at] = index;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBucketBlock) void bucket_kernel(OwnerArgs a, int bsplits, int32_t* counts,
+                                                              int32_t* list) {
+    extern __shared__ int32_t bins[];   // [fine_passes] counts / cursors, then [fine_passes] run starts
+    const int e = blockIdx.x / bsplits, s = blockIdx.x % bsplits;
+    int64_t base = 0, stop = a.n;
+    if (a.offsets) {
+        base = a.offsets[e];
+        stop = a.offsets[e + 1];
+        if (stop < base) stop = base;
+        if (stop > a.n) stop = a.n;
+        if (base > stop) base = stop;
+    }
+    const int64_t share = (stop - base + bsplits - 1) / bsplits;
+    const int64_t b0 = base + share * s < stop ? base + share * s : stop;
+    const int64_t b1 = b0 + share < stop ? b0 + share : stop;
+    for (int q = threadIdx.x; q < a.fine_passes; q += kBucketBlock) bins[q] = 0;
+    __syncthreads();
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBucketBlock) {
+        const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
+        bucket_coordinate<false>(a, xy.x, xy.y, bins, nullptr, 0, 0, 0);
+    }
+    __syncthreads();
+    int32_t* row = counts + static_cast<int64_t>(e) * a.fine_passes;
+    for (int q = threadIdx.x; q < a.fine_passes; q += kBucketBlock) {
+        const int32_t c = bins[q];
+        bins[a.fine_passes + q] = c ? atomicAdd(row + q, c) : 0;
+        bins[q] = 0;
+    }
+    __syncthreads();
+    const int64_t list_base = base * a.fine_passes;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBucketBlock) {
+        const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
+        bucket_coordinate<true>(a, xy.x, xy.y, bins, list, list_base, stop - base, static_cast<int32_t>(i));
+    }
+}
+
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
     __shared__ float reduce[kOwnerBlock / 64];
     using U = Elem<HALF>;
-    const uint32_t total = static_cast<uint32_t>(a.experts) * a.passes * a.splits;
+    // Work items per expert: every pass split `splits` ways, or, with buckets, only the coarse
+    // group pass split and each bucketed pass whole (its bucket order is not deterministic, so
+    // only a whole bucket gives a deterministic sum).
+    const int split_passes = a.bucketed ? a.fine_first : a.passes;
+    const uint32_t per_expert = static_cast<uint32_t>(split_passes * a.splits + (a.passes - split_passes));
+    const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
     const uint32_t work = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
     if (work >= total) return;
-    const int e = work / (a.passes * a.splits);
-    const int p = (work / a.splits) % a.passes;
-    const int s = work % a.splits;
+    const int e = work / per_expert;
+    const int r = work % per_expert;
+    const int p = r < split_passes * a.splits ? r / a.splits : split_passes + (r - split_passes * a.splits);
+    const int s = r < split_passes * a.splits ? r % a.splits : 0;
+    const int splits = p < split_passes ? a.splits : 1;   // ways this pass is split
 
     // Pass -> levels [l0, l1) and the slice [lo, hi) of the expert's gradient (in floats).
     int l0, l1;
@@ -412,14 +548,18 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         if (stop > a.n) stop = a.n;
         if (base > stop) base = stop;
     }
-    const int64_t share = (stop - base + a.splits - 1) / a.splits;
+    const int64_t share = (stop - base + splits - 1) / splits;
     const int64_t b0 = base + share * s < stop ? base + share * s : stop;
     const int64_t b1 = b0 + share < stop ? b0 + share : stop;
+    const bool bucket = a.bucketed && p >= a.fine_first;
+    // a bucketed pass bounds its scale over all of the expert's coordinates (every split of the
+    // pass then shares one scale); otherwise over this split's range
+    const int64_t m0 = bucket ? base : b0, m1 = bucket ? stop : b1;
 
     // Fixed-point scale from the bound 4 * count * max|upstream| over this range and levels.
     float bound = 0.0f;
-    if (b1 > b0) {
-        const int64_t r0 = b0 / kTransposeRows, r1 = (b1 - 1) / kTransposeRows;
+    if (m1 > m0) {
+        const int64_t r0 = m0 / kTransposeRows, r1 = (m1 - 1) / kTransposeRows;
         const int levels = l1 - l0;
         for (int64_t t = threadIdx.x; t < (r1 - r0 + 1) * levels; t += kOwnerBlock) {
             const float v = a.blockmax[(r0 + t / levels) * a.n_levels + l0 + t % levels];
@@ -437,7 +577,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     for (int w = 0; w < kOwnerBlock / 64; ++w) peak = (reduce[w] > peak || reduce[w] != reduce[w]) ? reduce[w] : peak;
     // Scale 2^shift: every contribution |w*u| <= peak maps below 2^31 (so it converts with one
     // rint + cvt_i32), and 4*count contributions of that size stay below 2^62 in the int64 sum.
-    const double limit = 4.0 * static_cast<double>(b1 - b0) * static_cast<double>(peak);
+    const double limit = 4.0 * static_cast<double>(m1 - m0) * static_cast<double>(peak);
     int shift = 60;
     if (peak > 0.0f && limit <= 1.0e300) {
         const int by_value = 30 - ilogb(peak);
@@ -452,7 +592,18 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     for (int l = l0; l < l1; ++l) {
         const DevLevel lv = a.level[l];
         const U* plane = reinterpret_cast<const U*>(a.planes) + static_cast<size_t>(l) * a.n * F;
-        if (a.row_bits[l] > 0 && !(a.group > 0 && p == 0))
+        if (bucket) {
+            const int q = p - a.fine_first;
+            const int64_t count = a.bucket_count[static_cast<int64_t>(e) * a.fine_passes + q];
+            const int32_t* list = a.bucket_list + base * a.fine_passes + static_cast<int64_t>(q) * (stop - base);
+            const int64_t k0 = 0, k1 = count;
+            switch (level_kind(lv)) {
+                case kHashed24: accumulate_bucket<F, HALF, kHashed24>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
+                case kHashedPow2: accumulate_bucket<F, HALF, kHashedPow2>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
+                case kGeneric: accumulate_bucket<F, HALF, kGeneric>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
+                default: accumulate_bucket<F, HALF, kDense>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
+            }
+        } else if (a.row_bits[l] > 0 && !(a.group > 0 && p == 0))
             accumulate_rows<F, HALF>(a.coords, plane, lv, b0, b1, lo, span, scale, acc, ring, a.row_bits[l],
                                      static_cast<uint32_t>(p - a.first_pass[l]));
         else if (lv.hashed && lv.mask && lv.mask < (1u << 24))
@@ -466,7 +617,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     }
     __syncthreads();
     const double unscale = ldexp(1.0, -shift);
-    if (a.fused && a.splits == 1) {
+    if (a.fused && splits == 1) {
         // The final gradient of these parameters is in LDS: update them right here.  One
         // workgroup holds the CU, so the loads of four elements per thread are issued before
         // any of them is used, to keep memory latency off the critical path.
@@ -503,21 +654,26 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         }
         return;
     }
-    float* out = a.splits == 1 ? a.grad + static_cast<size_t>(e) * a.expert_params + lo
+    float* out = splits == 1 ? a.grad + static_cast<size_t>(e) * a.expert_params + lo
                                : a.partial + static_cast<size_t>(s) * a.experts * a.expert_params +
                                      static_cast<size_t>(e) * a.expert_params + lo;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) {
         float v = static_cast<float>(static_cast<double>(static_cast<long long>(acc[j])) * unscale);
         if (!finite) v = __builtin_nanf("");
-        if (a.splits == 1 && a.accumulate) v += out[j];
+        if (splits == 1 && a.accumulate) v += out[j];
         out[j] = v;
     }
 }
 
+// Sums the split partials of the first `prefix` values of every expert (prefix = expert_params:
+// all of them) and writes the gradient or applies the optimizer step.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial, float* grad, int64_t total, int splits,
-                                                           int accumulate, int fused, AdamStep adam) {
+                                                           int accumulate, int fused, AdamStep adam,
+                                                           int64_t expert_params, int64_t prefix) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t x = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; x < total; x += stride) {
+    const int64_t count = total / expert_params * prefix;
+    for (int64_t y = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; y < count; y += stride) {
+        const int64_t x = y / prefix * expert_params + y % prefix;
         float v = accumulate ? grad[x] : 0.0f;
         for (int s = 0; s < splits; ++s) v += partial[static_cast<size_t>(s) * total + x];
         if (fused)
@@ -533,6 +689,19 @@ int allow_lds(Kernel kernel, size_t bytes) {
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     if (status != hipSuccess) return fail(std::string("LDS attribute: ") + hipGetErrorString(status));
     return 0;
+}
+
+// Clears the bucket counts and fills the buckets of every fine pass.
+int launch_buckets(const OwnerArgs& o, int32_t* counts, int32_t* list, hipStream_t s) {
+    if (launch_fill_zero(reinterpret_cast<float*>(counts), static_cast<int64_t>(o.experts) * o.fine_passes, s))
+        return -1;
+    int64_t bsplits = (2048 + o.experts - 1) / o.experts;
+    const int64_t most = o.n / (static_cast<int64_t>(o.experts) * kBucketBlock);
+    if (bsplits > most) bsplits = most > 1 ? most : 1;
+    const size_t shmem = static_cast<size_t>(o.fine_passes) * 2 * sizeof(int32_t);
+    bucket_kernel<<<static_cast<uint32_t>(o.experts * bsplits), kBucketBlock, shmem, s>>>(o, static_cast<int>(bsplits),
+                                                                                           counts, list);
+    return check_launch("owner buckets");
 }
 
 }  // namespace
@@ -572,8 +741,13 @@ int launch_owner_backward(const OwnerLaunch& in) {
         int64_t entries = (in.levels[l].size + slices - 1) / slices;
         int bits = 0;
         while ((int64_t{2} << bits) * F <= cap) ++bits;   // 2^bits entries: largest block that fits
-        if (in.row_screen && in.levels[l].hashed && in.levels[l].mask && (int64_t{1} << bits) > in.levels[l].res &&
-            (int64_t{1} << bits) < in.levels[l].size) {
+        if (in.bucketed) {
+            // aligned power-of-two slices: the bucketing pass finds a corner's slice by a shift
+            entries = int64_t{1} << bits;
+            slices = (in.levels[l].size + entries - 1) / entries;
+            o.slice_bits[l] = bits;
+        } else if (in.row_screen && in.levels[l].hashed && in.levels[l].mask &&
+                   (int64_t{1} << bits) > in.levels[l].res && (int64_t{1} << bits) < in.levels[l].size) {
             entries = int64_t{1} << bits;
             slices = in.levels[l].size / entries;
             o.row_bits[l] = bits;
@@ -586,6 +760,10 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.group = group;
     o.passes = passes;
     o.cap = static_cast<int>(cap + F);
+    o.fine_first = group > 0 ? 1 : 0;
+    o.fine_passes = passes - o.fine_first;
+    o.bucketed = in.bucketed && o.fine_passes > 0 && static_cast<int64_t>(o.fine_passes) * 8 <= 64 * 1024 &&
+                 static_cast<int64_t>(o.fine_passes) * in.n < (int64_t{1} << 31);
     const int64_t per_pass = static_cast<int64_t>(in.experts) * passes;
     int splits = 1;
     if (per_pass < 512) {
@@ -600,12 +778,20 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t planes_bytes = (static_cast<size_t>(in.n) * L * F * elem + 255) / 256 * 256;
     const size_t max_bytes = (static_cast<size_t>(row_blocks) * L * 4 + 255) / 256 * 256;
     const size_t total_params = static_cast<size_t>(in.experts) * in.expert_params;
-    const size_t partial_bytes = splits > 1 ? static_cast<size_t>(splits) * total_params * 4 : 0;
-    char* space = static_cast<char*>(workspace(planes_bytes + max_bytes + partial_bytes, in.stream));
+    const size_t partial_bytes = (splits > 1 ? static_cast<size_t>(splits) * total_params * 4 + 255 : 0) / 256 * 256;
+    const size_t count_bytes =
+        o.bucketed ? (static_cast<size_t>(in.experts) * o.fine_passes * 4 + 255) / 256 * 256 : 0;
+    const size_t list_bytes = o.bucketed ? static_cast<size_t>(in.n) * o.fine_passes * 4 : 0;
+    char* space = static_cast<char*>(
+        workspace(planes_bytes + max_bytes + partial_bytes + count_bytes + list_bytes, in.stream));
     if (!space) return -1;
     o.planes = space;
     o.blockmax = reinterpret_cast<float*>(space + planes_bytes);
     o.partial = reinterpret_cast<float*>(space + planes_bytes + max_bytes);
+    int32_t* bucket_count = reinterpret_cast<int32_t*>(space + planes_bytes + max_bytes + partial_bytes);
+    int32_t* bucket_list = reinterpret_cast<int32_t*>(space + planes_bytes + max_bytes + partial_bytes + count_bytes);
+    o.bucket_count = bucket_count;
+    o.bucket_list = bucket_list;
     o.grad = in.grad;
 
     TransposeArgs t{};
@@ -619,7 +805,9 @@ int launch_owner_backward(const OwnerLaunch& in) {
                  (L * F * elem) % 16 == 0;
     const uint32_t tblocks = static_cast<uint32_t>(row_blocks);
     const size_t shmem = static_cast<size_t>(cap + F) * 8 + kRingBytes;
-    const uint32_t total = static_cast<uint32_t>(per_pass * splits);
+    const int split_passes = o.bucketed ? o.fine_first : passes;
+    const uint32_t total =
+        static_cast<uint32_t>(in.experts * (static_cast<int64_t>(split_passes) * splits + (passes - split_passes)));
     const uint32_t oblocks = round_up(total, kXcds);
     hipStream_t s = in.stream;
 
@@ -633,6 +821,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     } while (0)
 #define ODIE_OWNER(FF, HH)                                                                              \
     do {                                                                                                \
+        if (o.bucketed && launch_buckets(o, bucket_count, bucket_list, s)) return -1;                  \
         if (allow_lds(owner_kernel<FF, HH>, shmem)) return -1;                                          \
         owner_kernel<FF, HH><<<oblocks, kOwnerBlock, shmem, s>>>(o);                                    \
     } while (0)
@@ -650,12 +839,17 @@ int launch_owner_backward(const OwnerLaunch& in) {
 #undef ODIE_BOTH
 #undef ODIE_OWNER
 #undef ODIE_TRANSPOSE
-    if (splits > 1) {
-        int64_t blocks = (static_cast<int64_t>(total_params) + 255) / 256;
+    if (splits > 1 && split_passes > 0) {
+        // with buckets only the coarse group pass (the expert's first values) is split
+        const int64_t prefix = o.bucketed
+            ? static_cast<int64_t>(in.levels[group - 1].offset + in.levels[group - 1].size) * F
+            : in.expert_params;
+        int64_t blocks = (static_cast<int64_t>(in.experts) * prefix + 255) / 256;
         if (blocks > 16384) blocks = 16384;
         split_reduce_kernel<<<static_cast<uint32_t>(blocks), 256, 0, s>>>(o.partial, in.grad,
                                                                           static_cast<int64_t>(total_params), splits,
-                                                                          in.accumulate, o.fused, o.adam);
+                                                                          in.accumulate, o.fused, o.adam,
+                                                                          in.expert_params, prefix);
     }
     return check_launch("odie_grid_backward");
 }

@@ -48,6 +48,7 @@ struct Tuning {
     int xcd_remap = 1;
     int backward_mode = 1;          // 0: LDS + global fp32 atomics, 1: owner computes
     int row_screen = 0;             // owner: screen hashed slices by row (measured slower)
+    int bucketed = 0;               // owner: fine passes walk per-slice coordinate buckets (measured slower)
     int paired_loads = 0;           // forward: 16-byte corner-pair loads (measured no gain)
     int forward_lds_bytes = 28672;  // forward: LDS budget for staged coarse levels (0: off)
     int owner_lds_bytes = 162816;   // 160 KiB minus static LDS
@@ -498,6 +499,7 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
     else if (key == "backward_mode" && (value == 0 || value == 1)) t.backward_mode = value;
     else if (key == "row_screen" && (value == 0 || value == 1)) t.row_screen = value;
+    else if (key == "bucketed" && (value == 0 || value == 1)) t.bucketed = value;
     else if (key == "paired_loads" && (value == 0 || value == 1)) t.paired_loads = value;
     else if (key == "forward_lds_bytes" && value >= 0 && value <= 65536) t.forward_lds_bytes = value;
     else if (key == "owner_lds_bytes" && value >= 4096 && value <= 162816) t.owner_lds_bytes = value;
@@ -593,6 +595,7 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
         o.lds_bytes = t.owner_lds_bytes;
         o.remap = t.xcd_remap;
         o.row_screen = t.row_screen;
+        o.bucketed = t.bucketed;
         o.stream = s;
         return launch_owner_backward(o);
     }
@@ -670,6 +673,7 @@ int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* o
     o.lds_bytes = t.owner_lds_bytes;
     o.remap = t.xcd_remap;
     o.row_screen = t.row_screen;
+    o.bucketed = t.bucketed;
     o.stream = s;
     o.adam = &adam;
     return launch_owner_backward(o);

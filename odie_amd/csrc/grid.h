@@ -117,6 +117,7 @@ struct OwnerLaunch {
     int64_t lds_bytes;
     int remap;
     int row_screen;
+    int bucketed;             // fine passes walk per-slice coordinate buckets
     hipStream_t stream;
     const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad
 };

@@ -53,11 +53,14 @@ def test_single_grid_forward_bit_exact(dtype):
     assert not mismatch.any(), 'mismatches at %s' % (np.argwhere(mismatch)[:5],)
 
 
-@pytest.fixture(params=[1, 0], ids=['owner', 'atomics'])
+@pytest.fixture(params=[(1, 1), (1, 0), (0, 0)], ids=['owner-buckets', 'owner', 'atomics'])
 def backward_mode(request):
-    _lib.set_tuning('backward_mode', request.param)
-    yield request.param
+    mode, bucketed = request.param
+    _lib.set_tuning('backward_mode', mode)
+    _lib.set_tuning('bucketed', bucketed)
+    yield mode
     _lib.set_tuning('backward_mode', 1)
+    _lib.set_tuning('bucketed', 0)
 
 
 @pytest.mark.parametrize('lds_bytes', [0, 65536])
@@ -87,6 +90,30 @@ def test_owner_backward_is_deterministic():
     first = grid_backward(xy, up, levels, 2, expert_params=entries * 2)
     second = grid_backward(xy, up, levels, 2, expert_params=entries * 2)
     assert torch.equal(first, second)
+
+
+@pytest.mark.parametrize('log2,experts,n', [(16, 64, 1 << 20), (14, 16, 300000), (12, 3, 5000)])
+def test_bucketed_owner_is_bit_identical(log2, experts, n):
+    """The bucketed fine passes only skip coordinates whose corners miss the slice: with one
+    workgroup per (expert, pass) the gradient is the same integer sum, bit for bit."""
+    levels, entries = grid_levels(encoding(log2=log2))
+    params = entries * 2
+    counts = np.random.default_rng(log2).multinomial(n, np.ones(experts) / experts)
+    offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).cuda()
+    xy = torch.from_numpy(synth.coordinates(log2, n)).cuda()
+    up = torch.from_numpy(synth.upstream(log2, n, 32)).cuda().half()
+    results = []
+    for bucketed in (1, 0):
+        _lib.set_tuning('bucketed', bucketed)
+        try:
+            results.append(grid_backward(xy, up, levels, 2, offsets=offsets, experts=experts, expert_params=params))
+        finally:
+            _lib.set_tuning('bucketed', 0)
+    got, want = results[0].cpu().numpy(), results[1].cpu().numpy()
+    if experts >= 16:     # no coordinate splits: the same fixed-point scale per workgroup
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
 
 
 def test_experts_forward_and_backward(backward_mode):
