@@ -62,6 +62,8 @@ def parse():
     parser.add_argument('--native-steps', type=int, default=200)
     parser.add_argument('--no-reconstruction', action='store_true', help='skip the 32768^2 residual pass')
     parser.add_argument('--reconstruction-batch', type=int, default=1 << 26)
+    parser.add_argument('--no-gigapixel', action='store_true', help='skip the 1024-expert 2^24-id step')
+    parser.add_argument('--gigapixel-steps', type=int, default=5)
     parser.add_argument('--copy-probe', action='store_true',
                         help='only run a plain 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE)')
     return parser.parse_args()
@@ -252,6 +254,32 @@ def reconstruction_pass(batch, fused=True):
                     'full-image inference + residual scoring on an RTX 3060'}
 
 
+def gigapixel_steps(steps):
+    """The gigapixel training step: the 32768x32768 synthetic image (seed 1), 1024 experts on
+    its 32x32 tiles of 1024^2 (16 levels x 2 fp16 features, 2^9-entry tables: 16.25 M grid
+    parameters + 7168 decoder parameters, 31 MiB in fp16, under the 50 MiB budget), 2^24 pixel
+    ids per step; the same step as the headline.  Reported beside the headline, not as it."""
+    import torch
+    from odie_amd import synth
+    from odie_amd.trainer import ExpertTrainer
+    side, n = C5_SIDE, 1 << 24
+    image = synth.image_device(1, side, side)
+    trainer = ExpertTrainer(image, C5_ENCODING, C5_TILES, C5_TILES, n, grid_lr=1e-2, decoder_lr=1e-3, seed=1)
+    batches = [torch.from_numpy(synth.integers(k, 'gigapixel_ids', n, side * side)).cuda() for k in range(2)]
+    trainer.step(batches[0])
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for k in range(steps):
+        trainer.step(batches[k % 2])
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    return {'coords': n, 'experts': trainer.grid.experts, 'params': trainer.grid.table.numel(),
+            'ms_per_step': ms, 'queries_per_s': n / (ms / 1e3),
+            'loss': float(trainer.squares.double().mean()), 'steps': steps}
+
+
 def main():
     args = parse()
     if args.copy_probe:
@@ -337,6 +365,8 @@ def main():
         result['native_step'] = native_steps(image, args.native_steps)
     if not args.no_reconstruction:
         result['reconstruction'] = reconstruction_pass(args.reconstruction_batch)
+    if not args.no_gigapixel:
+        result['gigapixel_step'] = gigapixel_steps(args.gigapixel_steps)
     if not args.no_cpu:
         result['cpu_baseline'] = cpu_baseline(image, ids_host, table16, master, decoder16, trainer.grid.levels,
                                               trainer.grid.expert_params, args.cpu_seconds)

@@ -34,15 +34,21 @@ GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:
 class ExpertTrainer:
     def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
                  device='cuda', fused=True, router=False, gate_lr=1e-3, coarse_levels=0, activation='sigmoid'):
-        image = np.ascontiguousarray(image, dtype=np.uint8)
-        if image.ndim != 3 or image.shape[2] != 3:
-            raise ValueError('image must be uint8 [height, width, 3]')
+        if isinstance(image, torch.Tensor):    # already on the device (gigapixel images)
+            if image.dtype != torch.uint8 or image.ndim != 3 or image.shape[2] != 3:
+                raise ValueError('image must be uint8 [height, width, 3]')
+            rgb = image.contiguous().reshape(-1).to(device)
+        else:
+            image = np.ascontiguousarray(image, dtype=np.uint8)
+            if image.ndim != 3 or image.shape[2] != 3:
+                raise ValueError('image must be uint8 [height, width, 3]')
+            rgb = torch.from_numpy(image.reshape(-1)).to(device)
         self.height, self.width = image.shape[:2]
         self.regions = (regions_x, regions_y)
         self.batch = batch
         self.fused = fused          # grid Adam applied inside the encode backward
         experts = regions_x * regions_y
-        self.rgb = torch.from_numpy(image.reshape(-1)).to(device)
+        self.rgb = rgb
         self.grid = ExpertGrid(encoding, experts, dtype=torch.float16, device=device)
         total = self.grid.table.numel()
         # fp32 master, uniform(-1e-4, 1e-4) as TCNN's HashGrid initializes its tables

@@ -146,3 +146,23 @@ def test_router_step_composes_the_tested_stages():
     assert np.array_equal(gate.grad.cpu().numpy().view(np.uint32), trainer.gate.grad.cpu().numpy().view(np.uint32))
     # the gate's optimizer ran (per-parameter ages, no skip, scale 16384)
     assert (trainer.gate_optimizer.steps.cpu().numpy() == 1).all()
+
+
+def test_gigapixel_step_is_deterministic_and_fused_equals_unfused():
+    """The 1024-expert configuration at its real size (32x32 tiles of a 32768^2 image, 2^9-entry
+    tables, 2^24 ids): two steps of the fused trainer equal two steps of the unfused one bit for
+    bit (size-independent property; the oracle covers the same step at small sizes)."""
+    from odie_amd import synth as s
+    enc = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=9, base_resolution=16, per_level_scale=1.38)
+    side, n = 32768, 1 << 24
+    image = s.image_device(1, side, side)
+    fused = ExpertTrainer(image, enc, 32, 32, n, seed=1, fused=True)
+    plain = ExpertTrainer(image, enc, 32, 32, n, seed=1, fused=False)
+    for k in range(2):
+        ids = torch.from_numpy(s.integers(k, 'gigapixel_ids', n, side * side)).cuda()
+        a = fused.step(ids)
+        b = plain.step(ids)
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), k
+        assert bool(torch.isfinite(a).all())
+    assert torch.equal(fused.master.view(torch.int32), plain.master.view(torch.int32))
+    assert torch.equal(fused.decoder.params, plain.decoder.params)
