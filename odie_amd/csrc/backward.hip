@@ -121,16 +121,17 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArg
 
 // fp16 pairs (F = 2), levels a multiple of 4 and 16-byte rows: every thread loads its four
 // rows first (16-byte loads), then writes one dword per level and row; |u| maxima are kept as
-// packed 16-bit integer maxima of the magnitude bits (for fp16, |a| <= |b| iff the 15-bit
-// magnitudes compare the same way, with Inf and NaN above every finite value).
+// packed 16-bit integer maxima of the magnitude bits, one per half (for fp16, |a| <= |b| iff
+// the 15-bit magnitudes compare the same way, with Inf and NaN above every finite value).
+typedef uint16_t magnitude2 __attribute__((ext_vector_type(2)));
 template <int LMAX>
 __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(TransposeArgs a) {
     __shared__ uint32_t waves[kTransposeBlock / 64][LMAX];
     constexpr int kRowsPerThread = kTransposeRows / kTransposeBlock;
     constexpr int kChunks = LMAX / 4;  // 16-byte chunks per row (4 levels each)
-    uint32_t peak[LMAX];
+    magnitude2 peak[LMAX];
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l) peak[l] = 0;
+    for (int l = 0; l < LMAX; ++l) peak[l] = magnitude2{0, 0};
     uint4 rows[kRowsPerThread][kChunks];
     const int chunks = a.n_levels / 4;
 #pragma unroll
@@ -154,7 +155,8 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
             for (int q = 0; q < 4; ++q) {
                 const int l = 4 * j + q;
                 planes[static_cast<size_t>(l) * a.n + i] = words[q];
-                peak[l] = __builtin_elementwise_max(peak[l], words[q] & 0x7fff7fffu);
+                // per-half maximum (v_pk_max_u16): a 32-bit maximum would follow the high half only
+                peak[l] = __builtin_elementwise_max(peak[l], __builtin_bit_cast(magnitude2, words[q] & 0x7fff7fffu));
             }
         }
     }
@@ -163,8 +165,7 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) {
         if (l < a.n_levels) {
-            uint32_t m = peak[l];
-            m = (m & 0xffffu) > (m >> 16) ? (m & 0xffffu) : (m >> 16);
+            uint32_t m = peak[l].x > peak[l].y ? peak[l].x : peak[l].y;
             for (int step = 32; step; step >>= 1) {
                 const uint32_t other = __shfl_xor(m, step);
                 m = other > m ? other : m;

@@ -239,3 +239,23 @@ def test_packed_planes_forward_backward():
     features.backward(torch.from_numpy(up).cuda())
     exp_grad, magnitude = oracle.packed_backward(xy, up, host, layout['params'])
     check_gradient(d_grid.grad, exp_grad, magnitude, 'packed')
+
+
+def test_owner_scale_sees_both_features():
+    """Regression: the largest |upstream| of a row block must cover both features of a level.
+    Feature 0 carries values ~1e3 while feature 1 is ~1e-3 and largest in a row whose feature 0
+    is tiny; a maximum taken over packed 32-bit words follows feature 1 only, picks a scale
+    2^40 too fine and saturates the fixed-point contributions of feature 0."""
+    levels, entries = grid_levels(encoding(log2=12))
+    n = 4096
+    xy = synth.coordinates(31, n)
+    up = np.empty((n, 32), dtype=np.float32)
+    up[:, 0::2] = np.where(synth.uniform(31, 'sign', n * 16).reshape(n, 16) < 0.5, -1000.0, 1000.0)
+    up[:, 1::2] = 0.001
+    up[7, 1::2] = 0.002
+    up[7, 0::2] = 0.0001
+    up = up.astype(np.float16)
+    grad = grid_backward(torch.from_numpy(xy).cuda(), torch.from_numpy(up).cuda(), levels, 2,
+                         expert_params=entries * 2)
+    expected, magnitude = oracle.hash_backward(xy, up, rows_of(levels), 2, entries * 2)
+    check_gradient(grad, expected, magnitude, 'two-scale upstream')
