@@ -50,11 +50,6 @@ __global__ __launch_bounds__(kAdamBlock) void adam_kernel(AdamStep a, const void
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kAdamBlock * 4;
     for (int64_t base = (static_cast<int64_t>(blockIdx.x) * kAdamBlock + threadIdx.x) * 4; base < n; base += stride) {
         if (base + 4 <= n) {
-            const float4 p = *reinterpret_cast<float4*>(a.master + base);
-            const float4 m = *reinterpret_cast<float4*>(a.m + base);
-            const float4 v = *reinterpret_cast<float4*>(a.v + base);
-            uint4 age = make_uint4(0, 0, 0, 0);
-            if (a.variant != 0) age = *reinterpret_cast<const uint4*>(a.steps + base);
             float g[4];
             if (grad_half) {
                 const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(grad) + base);
@@ -66,6 +61,15 @@ __global__ __launch_bounds__(kAdamBlock) void adam_kernel(AdamStep a, const void
                 const float4 raw = *reinterpret_cast<const float4*>(static_cast<const float*>(grad) + base);
                 g[0] = raw.x; g[1] = raw.y; g[2] = raw.z; g[3] = raw.w;
             }
+            // variant 1 leaves parameters with a zero gradient untouched: with no fp16 copy to
+            // refresh, four of them need no further memory traffic (sparse updates stay cheap)
+            if (a.variant == 1 && !a.half_copy && g[0] == 0.0f && g[1] == 0.0f && g[2] == 0.0f && g[3] == 0.0f)
+                continue;
+            const float4 p = *reinterpret_cast<float4*>(a.master + base);
+            const float4 m = *reinterpret_cast<float4*>(a.m + base);
+            const float4 v = *reinterpret_cast<float4*>(a.v + base);
+            uint4 age = make_uint4(0, 0, 0, 0);
+            if (a.variant != 0) age = *reinterpret_cast<const uint4*>(a.steps + base);
             float ps[4] = {p.x, p.y, p.z, p.w}, ms[4] = {m.x, m.y, m.z, m.w}, vs[4] = {v.x, v.y, v.z, v.w};
             uint32_t ts[4] = {age.x, age.y, age.z, age.w};
 #pragma unroll

@@ -49,6 +49,8 @@ struct Tuning {
     int backward_mode = 1;          // 0: LDS + global fp32 atomics, 1: owner computes
     int row_screen = 0;             // owner: screen hashed slices by row (measured slower)
     int bucketed = 0;               // owner: fine passes walk per-slice coordinate buckets (measured slower)
+    int packed_lds = 1;             // packed backward: coarse levels accumulated in LDS
+    int packed_blocks = 256;        // packed backward with LDS: most blocks (each flushes its partials once)
     int paired_loads = 0;           // forward: 16-byte corner-pair loads (measured no gain)
     int forward_lds_bytes = 28672;  // forward: LDS budget for staged coarse levels (0: off)
     int owner_lds_bytes = 162816;   // 160 KiB minus static LDS
@@ -481,6 +483,52 @@ __global__ __launch_bounds__(kBlock) void packed_backward_kernel(PackedArgs a) {
     }
 }
 
+// Packed backward with the coarse levels accumulated in LDS: the levels whose parameters lie in
+// the first lds_floats values (found from the descriptors' plane offsets) take LDS atomics, and
+// the block adds its partial sums to the gradient once at the end; the finer, sparsely updated
+// levels take global atomics directly.  A block walks a contiguous chunk of coordinates.
+constexpr int kPackedLdsFloats = 16384;
+
+__global__ __launch_bounds__(kBlock) void packed_backward_lds_kernel(PackedArgs a, int64_t chunk) {
+    __shared__ float lds[kPackedLdsFloats];
+    // coarse levels: the longest prefix of levels that ends within the LDS budget
+    int lds_levels = 0;
+    while (lds_levels + 1 < a.levels && a.desc[8 * (lds_levels + 1) + 2] <= kPackedLdsFloats &&
+           a.desc[8 * (lds_levels + 1) + 2] >= 0)
+        ++lds_levels;
+    const int lds_floats = lds_levels > 0 ? a.desc[8 * lds_levels + 2] : 0;
+    for (int j = threadIdx.x; j < lds_floats; j += kBlock) lds[j] = 0.0f;
+    __syncthreads();
+    const int64_t b0 = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int64_t b1 = b0 + chunk < a.n ? b0 + chunk : a.n;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBlock) {
+        const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+        const uint16_t* urow = a.upstream + static_cast<size_t>(i) * a.width;
+        for (int l = 0; l < a.levels; ++l) {
+            const int32_t* d = a.desc + 8 * l;
+            int cell;
+            float w[4];
+            plane_geometry(p.x, p.y, d[0], cell, w);
+            if (!((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1)) continue;
+            for (int c = 0; c < d[5]; ++c) {
+                const int col = d[6] + c;
+                if (col >= a.width) continue;
+                const float value = __half2float(bits_to_half(urow[col]));
+                if (value == 0.0f) continue;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int64_t param = plane_param(a, d, cell, k, c);
+                    if (l < lds_levels && param < lds_floats) atomicAdd(lds + param, w[k] * value);
+                    else atomicAdd(a.gradient + param, w[k] * value);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < lds_floats; j += kBlock)
+        if (lds[j] != 0.0f) atomicAdd(a.gradient + j, lds[j]);
+}
+
 }  // namespace
 
 int launch_fill_zero(float* data, int64_t count, hipStream_t stream) {
@@ -500,6 +548,8 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "backward_mode" && (value == 0 || value == 1)) t.backward_mode = value;
     else if (key == "row_screen" && (value == 0 || value == 1)) t.row_screen = value;
     else if (key == "bucketed" && (value == 0 || value == 1)) t.bucketed = value;
+    else if (key == "packed_lds" && (value == 0 || value == 1)) t.packed_lds = value;
+    else if (key == "packed_blocks" && value >= 1 && value <= 65536) t.packed_blocks = value;
     else if (key == "paired_loads" && (value == 0 || value == 1)) t.paired_loads = value;
     else if (key == "forward_lds_bytes" && value >= 0 && value <= 65536) t.forward_lds_bytes = value;
     else if (key == "owner_lds_bytes" && value >= 4096 && value <= 162816) t.owner_lds_bytes = value;
@@ -771,7 +821,15 @@ ODIE_API int odie_packed_backward(const float* coords, int64_t n, const uint16_t
     a.params = parameter_count;
     a.levels = levels;
     a.width = up_width;
-    const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
-    packed_backward_kernel<<<blocks, kBlock, 0, s>>>(a);
+    if (tuning().packed_lds) {
+        // few large chunks: each block flushes its coarse partials once
+        int64_t blocks = (n + 255) / 256;
+        if (blocks > tuning().packed_blocks) blocks = tuning().packed_blocks;
+        const int64_t chunk = (n + blocks - 1) / blocks;
+        packed_backward_lds_kernel<<<static_cast<uint32_t>(blocks), kBlock, 0, s>>>(a, chunk);
+    } else {
+        const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
+        packed_backward_kernel<<<blocks, kBlock, 0, s>>>(a);
+    }
     return check_launch("odie_packed_backward");
 }

@@ -279,12 +279,30 @@ __global__ __launch_bounds__(kGateBlock) void gate_backward_kernel(GateArgs a) {
         a.partials[static_cast<int64_t>(blockIdx.x) * kGateParams + i] = sum[i];
 }
 
+// dweights[p] = sum over workgroups of partials[b][p] in a fixed order: four lane groups of a
+// 256-thread block take the workgroups b = q, q+4, q+8, ... (q = group), eight loads in flight
+// per step, and the four group sums are added in group order.
+constexpr int kReduceParams = 64;
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* partials, int blocks, float* dweights) {
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= kGateParams) return;
+    __shared__ float group_sum[4][kReduceParams];
+    const int local = threadIdx.x % kReduceParams, q = threadIdx.x / kReduceParams;
+    const int p = blockIdx.x * kReduceParams + local;
     float total = 0.0f;
-    for (int b = 0; b < blocks; ++b) total += partials[static_cast<int64_t>(b) * kGateParams + p];
-    dweights[p] = total;
+    if (p < kGateParams) {
+        int b = q;
+        for (; b + 28 < blocks; b += 32) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = partials[static_cast<int64_t>(b + 4 * j) * kGateParams + p];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) total += v[j];
+        }
+        for (; b < blocks; b += 4) total += partials[static_cast<int64_t>(b) * kGateParams + p];
+    }
+    group_sum[q][local] = total;
+    __syncthreads();
+    if (q == 0 && p < kGateParams)
+        dweights[p] = ((group_sum[0][local] + group_sum[1][local]) + group_sum[2][local]) + group_sum[3][local];
 }
 
 int gate_blocks(int64_t n) {
@@ -335,6 +353,6 @@ ODIE_API int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int6
                softplus ? 1 : 0};
     gate_backward_kernel<<<blocks, kGateBlock, 0, s>>>(a);
     if (check_launch("odie_gate_backward")) return -1;
-    gate_reduce_kernel<<<(kGateParams + 255) / 256, 256, 0, s>>>(partials, blocks, dweights);
+    gate_reduce_kernel<<<(kGateParams + kReduceParams - 1) / kReduceParams, 256, 0, s>>>(partials, blocks, dweights);
     return check_launch("odie_gate_backward reduce");
 }
