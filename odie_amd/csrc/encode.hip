@@ -461,6 +461,46 @@ __global__ __launch_bounds__(kBlock) void packed_forward_kernel(PackedArgs a) {
         if (l < a.levels) vrow[l] = static_cast<uint8_t>(vis[l / 4] >> (8 * (l % 4)));
 }
 
+// packed_forward_kernel for 16 levels of 2 features in level order (width 32): both features of
+// a corner in one 8-byte load, the row kept in registers and written with 16-byte stores, the
+// visibility bytes with one.  Same arithmetic, same bits.
+__global__ __launch_bounds__(kBlock) void packed_forward16x2_kernel(PackedArgs a) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= a.n) return;
+    const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+    uint32_t pairs[16];
+    uint32_t vis[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+        const int32_t* d = a.desc + 8 * l;
+        int cell;
+        float w[4];
+        plane_geometry(p.x, p.y, d[0], cell, w);
+        const bool on = l < a.active && ((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1);
+        vis[l / 4] |= static_cast<uint32_t>(on) << (8 * (l % 4));
+        __half v0 = __float2half(0.0f), v1 = __float2half(0.0f);
+        if (on) {
+            float2 g[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int64_t at = plane_param(a, d, cell, k, 0);   // even: both features are inside
+                g[k] = *reinterpret_cast<const float2*>(a.grid + (at < a.params - 1 ? at : a.params - 2));
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const __half wk = __float2half_rn(keep_fp32(w[k]));
+                v0 = __hfma(wk, __float2half_rn(g[k].x), v0);
+                v1 = __hfma(wk, __float2half_rn(g[k].y), v1);
+            }
+        }
+        pairs[l] = static_cast<uint32_t>(half_to_bits(v0)) | (static_cast<uint32_t>(half_to_bits(v1)) << 16);
+    }
+    uint4* row = reinterpret_cast<uint4*>(a.features + static_cast<size_t>(i) * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) row[j] = make_uint4(pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2], pairs[4 * j + 3]);
+    reinterpret_cast<uint4*>(a.visibility)[i] = make_uint4(vis[0], vis[1], vis[2], vis[3]);
+}
+
 __global__ __launch_bounds__(kBlock) void packed_backward_kernel(PackedArgs a) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= a.n) return;
@@ -754,7 +794,7 @@ namespace odie {
 int packed_forward_internal(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
                             const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
                             const int32_t* node_prefix, const uint8_t* bitmap, int width, int active, uint16_t pad,
-                            uint16_t* features, uint8_t* visibility, hipStream_t stream) {
+                            uint16_t* features, uint8_t* visibility, hipStream_t stream, bool levels16x2) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_packed_forward: n must be within [0, 2^31-1]");
     if (levels < 2 || levels > ODIE_MAX_LEVELS) return fail("odie_packed_forward: descriptor must have 2..32 levels");
     if (width < 2 || width > 128) return fail("odie_packed_forward: feature width must be within 2..128");
@@ -779,7 +819,11 @@ int packed_forward_internal(const float* coords, int64_t n, const float* grid, i
     a.active = active;
     a.pad = pad;
     const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
-    packed_forward_kernel<<<blocks, kBlock, 0, stream>>>(a);
+    if (levels16x2 && levels == 16 && width == 32 && reinterpret_cast<uintptr_t>(features) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(visibility) % 16 == 0 && reinterpret_cast<uintptr_t>(grid) % 8 == 0)
+        packed_forward16x2_kernel<<<blocks, kBlock, 0, stream>>>(a);
+    else
+        packed_forward_kernel<<<blocks, kBlock, 0, stream>>>(a);
     return check_launch("odie_packed_forward");
 }
 

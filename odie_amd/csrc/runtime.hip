@@ -440,7 +440,7 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
                                raw.data, kWidth, s));
     else
         call(packed_forward_internal(xy.data, n, grid, total, desc, kLevels, bits, prefix, cells, kWidth, active,
-                                     0x3C00, raw.data, vis.data, stream));
+                                     0x3C00, raw.data, vis.data, stream, true));
     const uint16_t* features = raw.data;
     if (gate) {
         call(odie_gate_forward(raw.data, n, gate->half.data, vis.data, coarse, softplus, weighted.data, sigmoid.data, s));
