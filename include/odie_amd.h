@@ -129,7 +129,8 @@ int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstrea
  * expert (nullable) receives each input's expert id in input order (int32 [n]).
  * rgb / colors (both null or both set): colors[j] = r | g << 8 | b << 16 of the pixel
  *   (y*W + x, with y clamped as above) of slot j, read from the RGB8 image rgb [H*W][3] --
- *   the training target of the slot, gathered where the id is already in a register.
+ *   the training target of the slot, gathered in slot order so each tile's bytes are read
+ *   through one L2.
  * workspace: caller-owned device scratch of odie_route_workspace(n, E) bytes.
  * --------------------------------------------------------------------------------------- */
 int64_t odie_route_workspace(int64_t n, int experts);

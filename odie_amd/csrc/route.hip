@@ -224,18 +224,47 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
             const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
             reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
             if (a.expert_out) a.expert_out[i] = expert;
-            if (a.colors) {
-                const uint8_t* pixel = a.rgb + 3 * (static_cast<uint64_t>(y) * a.width + x);
-                a.colors[slot] = pixel[0] | (uint32_t(pixel[1]) << 8) | (uint32_t(pixel[2]) << 16);
-            }
+            // the pixel's index for route_colors_kernel (below 2^32: the image size is bounded)
+            if (a.colors) a.colors[slot] = y * a.width + x;
         }
     }
 }
 
+// Target colors in slot order.  route_scatter leaves each slot's pixel index in colors; the
+// slots of one expert are contiguous and lie in one tile of the image, and consecutive chunks
+// of slots run on one XCD (xcd_major), so each XCD gathers the bytes of its own run of tiles
+// through its L2 instead of fetching a line of the image for every id.
+constexpr int kColorsPer = 8;
+constexpr int kColorsChunk = kRouteBlock * kColorsPer;
+
+__global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t* rgb, uint32_t* colors, int64_t n) {
+    const int64_t begin = static_cast<int64_t>(xcd_major(blockIdx.x, gridDim.x)) * kColorsChunk + threadIdx.x;
+    uint32_t pixel[kColorsPer];
+#pragma unroll
+    for (int k = 0; k < kColorsPer; ++k) {
+        const int64_t i = begin + k * kRouteBlock;
+        pixel[k] = i < n ? colors[i] : 0u;
+    }
+    uint32_t r[kColorsPer], g[kColorsPer], b[kColorsPer];
+#pragma unroll
+    for (int k = 0; k < kColorsPer; ++k) {
+        const uint8_t* at = rgb + 3 * static_cast<uint64_t>(pixel[k]);
+        r[k] = at[0];
+        g[k] = at[1];
+        b[k] = at[2];
+    }
+#pragma unroll
+    for (int k = 0; k < kColorsPer; ++k) {
+        const int64_t i = begin + k * kRouteBlock;
+        if (i < n) colors[i] = r[k] | (g[k] << 8) | (b[k] << 16);
+    }
+}
+
 int route_plan(int64_t n, int experts, int& part, int& parts) {
-    // Sub-chunks of at least 1024 ids, few enough that experts*parts stays <= 2^20.
+    // Sub-chunks of at least 1024 ids, few enough that experts*parts stays <= 2^22 (16 MiB of
+    // counts): with many experts a sub-chunk stays short enough to keep every CU busy.
     int64_t p = 1024;
-    while ((n + p - 1) / p * experts > (int64_t{1} << 20)) p *= 2;
+    while ((n + p - 1) / p * experts > (int64_t{1} << 22)) p *= 2;
     part = static_cast<int>(p);
     parts = static_cast<int>((n + p - 1) / p);
     if (parts < 1) parts = 1;
@@ -327,5 +356,9 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
     route_scan_apply_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
     route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
+    if (colors) {
+        const uint32_t chunks = round_up(static_cast<uint32_t>((n + kColorsChunk - 1) / kColorsChunk), kXcds);
+        route_colors_kernel<<<chunks, kRouteBlock, 0, s>>>(rgb, colors, n);
+    }
     return check_launch("odie_route");
 }
