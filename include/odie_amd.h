@@ -85,6 +85,17 @@ int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offse
                             uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant, int64_t step,
                             float lr, float beta1, float beta2, float eps, float loss_scale, uint64_t stream);
 
+/* odie_grid_backward_adam for features = 2 with the fp16 upstream given as odie_mlp_train_planes
+ * writes it (planes uint32 [n_levels][n], blockmax fp32 [ceil(n/128)][n_levels]) instead of rows
+ * [n, up_width]: the same update, bit for bit, without transposing the upstream.  No counterpart
+ * in the reference (see odie_mlp_train_planes). */
+int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                   const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                   const odie_grid_level* levels, int n_levels, int features, float* master,
+                                   uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant,
+                                   int64_t step, float lr, float beta1, float beta2, float eps, float loss_scale,
+                                   uint64_t stream);
+
 /* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
  * 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),
@@ -223,6 +234,17 @@ int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weights, uint
 int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights, const uint32_t* colors,
                    const uint8_t* rgb, const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out,
                    uint16_t* hidden, float* squares, uint16_t* dz, float* dweights, uint64_t stream);
+
+/* odie_mlp_train with dz written in the layout odie_grid_backward_adam_planes reads instead of
+ * rows: planes uint32 [16][n] (plane l, row j = the fp16 pair of columns 2l, 2l+1 of dz row j)
+ * and blockmax fp32 [ceil(n/128)][16] (record r, level l = max |dz| over rows 128r..128r+127
+ * and both features of level l; NaN if any of them is NaN).  Same values as odie_mlp_train's
+ * dz, bit for bit.  No counterpart in the reference: it saves the encode backward's transposition
+ * of dz, a layout change of this implementation. */
+int odie_mlp_train_planes(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+                          const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
+                          const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares, uint32_t* planes,
+                          float* blockmax, float* dweights, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Router gate (router_enabled) of the hash-grid model: gate MLP 32 -> 32 -> 16 (ReLU hidden

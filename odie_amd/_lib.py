@@ -27,6 +27,8 @@ SIGNATURES = {
     'odie_copy': ([_U64, _U64, _U64, _U64], _I),
     'odie_grid_backward_adam': ([_P, _I64, _P, _I, _P, _I, _I, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I64,
                                  C.c_float, C.c_float, C.c_float, C.c_float, C.c_float, _U64], _I),
+    'odie_grid_backward_adam_planes': ([_P, _I64, _P, _I, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I64,
+                                        C.c_float, C.c_float, C.c_float, C.c_float, C.c_float, _U64], _I),
     'odie_set_tuning': ([C.c_char_p, _I], _I),
     'odie_grid_forward': ([_P, _I64, _P, _I, _P, _I64, _I, _P, _I, _I, _P, _I, _U64], _I),
     'odie_grid_backward': ([_P, _I64, _P, _I, _P, _I, _I, _I64, _P, _I, _I, _P, _I, _U64], _I),
@@ -41,6 +43,7 @@ SIGNATURES = {
     'selection_chunk': ([_P, _I, _I, _I, _I, C.c_bool, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
     'odie_mlp_forward': ([_P, _I64, _P, _P, _U64], _I),
     'odie_mlp_train': ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U64], _I),
+    'odie_mlp_train_planes': ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U64], _I),
     'odie_gate_forward': ([_P, _I64, _P, _P, _I, _I, _P, _P, _U64], _I),
     'odie_gate_backward': ([_P, _P, _I64, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
     'odie_adam_step': ([_P, _P, _P, _I, _P, _P, _P, _I64, _I, _I64, C.c_float, C.c_float, C.c_float,

@@ -27,7 +27,8 @@ namespace odie {
 namespace {
 
 constexpr int kTransposeBlock = 256;
-constexpr int kTransposeRows = 1024;  // rows per transpose block (and per max-record)
+constexpr int kTransposeRows = 1024;  // rows per transpose block
+constexpr int kMaxRows = 128;         // rows per |upstream| maximum record (two waves of a pass)
 constexpr int kOwnerBlock = 1024;
 constexpr int kBatch = 4;             // coordinates per thread per owner-loop iteration
 constexpr int kRing = 128;            // per-wave LDS queue of candidate coordinates (power of two)
@@ -43,99 +44,100 @@ struct TransposeArgs {
     int vec_rows;
 };
 
-template <int F, bool HALF, int LMAX>
-__global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArgs a) {
-    using U = Elem<HALF>;
-    __shared__ float waves[kTransposeBlock / 64][LMAX];
-    float peak[LMAX];
-#pragma unroll
-    for (int l = 0; l < LMAX; ++l) peak[l] = 0.0f;
-    const int used = a.n_levels * F;
-    for (int r = 0; r < kTransposeRows / kTransposeBlock; ++r) {
-        const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
-        if (i >= a.n) break;
-        const U* row = reinterpret_cast<const U*>(a.upstream) + static_cast<size_t>(i) * a.width;
-        U vals[LMAX * F];
-        if (a.vec_rows) {
-            constexpr int kPer = 16 / sizeof(U);
-            constexpr int kChunks = (LMAX * F + kPer - 1) / kPer;
-#pragma unroll
-            for (int j = 0; j < kChunks; ++j) {
-                if (j * kPer < used) {
-                    const uint4 v = reinterpret_cast<const uint4*>(row)[j];
-                    const U* parts = reinterpret_cast<const U*>(&v);
-#pragma unroll
-                    for (int q = 0; q < kPer; ++q)
-                        if (j * kPer + q < LMAX * F) vals[j * kPer + q] = parts[q];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < LMAX * F; ++c)
-                if (c < used) vals[c] = row[c];
-        }
-        U* planes = reinterpret_cast<U*>(a.planes);
-#pragma unroll
-        for (int l = 0; l < LMAX; ++l) {
-            if (l < a.n_levels) {
-                U* dst = planes + (static_cast<size_t>(l) * a.n + i) * F;
-                if constexpr (HALF && F == 2) {
-                    const uint32_t word = static_cast<uint32_t>(half_to_bits(vals[l * F])) |
-                                          (static_cast<uint32_t>(half_to_bits(vals[l * F + 1])) << 16);
-                    *reinterpret_cast<uint32_t*>(dst) = word;
-                } else {
-#pragma unroll
-                    for (int c = 0; c < F; ++c) dst[c] = vals[l * F + c];
-                }
-#pragma unroll
-                for (int c = 0; c < F; ++c) {
-                    const float v = fabsf(static_cast<float>(vals[l * F + c]));
-                    peak[l] = (v > peak[l] || v != v) ? v : peak[l];
-                }
-            }
-        }
-    }
-    // NaN is kept by the comparisons below (not fmaxf) so the owner pass sees a non-finite bound.
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-#pragma unroll
-    for (int l = 0; l < LMAX; ++l) {
-        if (l < a.n_levels) {
-            float m = peak[l];
-            for (int step = 32; step; step >>= 1) {
-                const float other = __shfl_xor(m, step);
-                m = (other > m || other != other) ? other : m;
-            }
-            if (lane == 0) waves[wave][l] = m;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < a.n_levels) {
-        float m = 0.0f;
-        for (int w = 0; w < kTransposeBlock / 64; ++w) {
-            const float other = waves[w][threadIdx.x];
-            m = (other > m || other != other) ? other : m;
-        }
-        a.blockmax[static_cast<size_t>(blockIdx.x) * a.n_levels + threadIdx.x] = m;
+// Maximum of two |upstream| records; NaN wins, so the owner pass sees a non-finite bound.
+__device__ inline float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
+
+// Record q of the block (rows q*128.. of its 1024) is waves 2*(q%2) and 2*(q%2)+1 of pass q/2.
+__device__ inline void write_records(const TransposeArgs& a, const float* waves, int lmax) {
+    constexpr int kRecords = kTransposeRows / kMaxRows;
+    for (int t = threadIdx.x; t < kRecords * a.n_levels; t += kTransposeBlock) {
+        const int q = t / a.n_levels, l = t % a.n_levels;
+        const int64_t record = static_cast<int64_t>(blockIdx.x) * kRecords + q;
+        if (record * kMaxRows >= a.n) continue;
+        const float* pass = waves + (q / 2) * (kTransposeBlock / 64) * lmax;
+        const int w = 2 * (q % 2);
+        a.blockmax[record * a.n_levels + l] = nan_max(pass[w * lmax + l], pass[(w + 1) * lmax + l]);
     }
 }
 
+template <int F, bool HALF, int LMAX>
+__global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArgs a) {
+    using U = Elem<HALF>;
+    constexpr int kPasses = kTransposeRows / kTransposeBlock;
+    __shared__ float waves[kPasses][kTransposeBlock / 64][LMAX];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int used = a.n_levels * F;
+    for (int r = 0; r < kPasses; ++r) {
+        const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
+        float peak[LMAX];
+#pragma unroll
+        for (int l = 0; l < LMAX; ++l) peak[l] = 0.0f;
+        if (i < a.n) {
+            const U* row = reinterpret_cast<const U*>(a.upstream) + static_cast<size_t>(i) * a.width;
+            U vals[LMAX * F];
+            if (a.vec_rows) {
+                constexpr int kPer = 16 / sizeof(U);
+                constexpr int kChunks = (LMAX * F + kPer - 1) / kPer;
+#pragma unroll
+                for (int j = 0; j < kChunks; ++j) {
+                    if (j * kPer < used) {
+                        const uint4 v = reinterpret_cast<const uint4*>(row)[j];
+                        const U* parts = reinterpret_cast<const U*>(&v);
+#pragma unroll
+                        for (int q = 0; q < kPer; ++q)
+                            if (j * kPer + q < LMAX * F) vals[j * kPer + q] = parts[q];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < LMAX * F; ++c)
+                    if (c < used) vals[c] = row[c];
+            }
+            U* planes = reinterpret_cast<U*>(a.planes);
+#pragma unroll
+            for (int l = 0; l < LMAX; ++l) {
+                if (l < a.n_levels) {
+                    U* dst = planes + (static_cast<size_t>(l) * a.n + i) * F;
+                    if constexpr (HALF && F == 2) {
+                        const uint32_t word = static_cast<uint32_t>(half_to_bits(vals[l * F])) |
+                                              (static_cast<uint32_t>(half_to_bits(vals[l * F + 1])) << 16);
+                        *reinterpret_cast<uint32_t*>(dst) = word;
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < F; ++c) dst[c] = vals[l * F + c];
+                    }
+#pragma unroll
+                    for (int c = 0; c < F; ++c) peak[l] = nan_max(peak[l], fabsf(static_cast<float>(vals[l * F + c])));
+                }
+            }
+        }
+        // the wave's 64 rows lie in one record of kMaxRows = 128 rows
+#pragma unroll
+        for (int l = 0; l < LMAX; ++l) {
+            if (l < a.n_levels) {
+                float m = peak[l];
+                for (int step = 32; step; step >>= 1) m = nan_max(m, __shfl_xor(m, step));
+                if (lane == 0) waves[r][wave][l] = m;
+            }
+        }
+    }
+    __syncthreads();
+    write_records(a, &waves[0][0][0], LMAX);
+}
+
 // fp16 pairs (F = 2), levels a multiple of 4 and 16-byte rows: every thread loads its four
-// rows first (16-byte loads), then writes one dword per level and row; |u| maxima are kept as
-// packed 16-bit integer maxima of the magnitude bits, one per half (for fp16, |a| <= |b| iff
-// the 15-bit magnitudes compare the same way, with Inf and NaN above every finite value).
-typedef uint16_t magnitude2 __attribute__((ext_vector_type(2)));
+// rows first (16-byte loads), then writes one dword per level and row; |u| maxima are packed
+// 16-bit magnitude maxima, two levels per dword, reduced over the wave's 64 rows (one half of
+// a 128-row record).
 template <int LMAX>
 __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(TransposeArgs a) {
-    __shared__ uint32_t waves[kTransposeBlock / 64][LMAX];
-    constexpr int kRowsPerThread = kTransposeRows / kTransposeBlock;
+    constexpr int kPasses = kTransposeRows / kTransposeBlock;
     constexpr int kChunks = LMAX / 4;  // 16-byte chunks per row (4 levels each)
-    magnitude2 peak[LMAX];
-#pragma unroll
-    for (int l = 0; l < LMAX; ++l) peak[l] = magnitude2{0, 0};
-    uint4 rows[kRowsPerThread][kChunks];
+    __shared__ uint32_t waves[kPasses][kTransposeBlock / 64][LMAX / 2];   // level pairs
+    uint4 rows[kPasses][kChunks];
     const int chunks = a.n_levels / 4;
 #pragma unroll
-    for (int r = 0; r < kRowsPerThread; ++r) {
+    for (int r = 0; r < kPasses; ++r) {
         const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
         const uint4* row = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.upstream) +
                                                           static_cast<size_t>(i < a.n ? i : 0) * a.width);
@@ -143,42 +145,39 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
         for (int j = 0; j < kChunks; ++j) rows[r][j] = j < chunks ? row[j] : make_uint4(0, 0, 0, 0);
     }
     uint32_t* planes = reinterpret_cast<uint32_t*>(a.planes);
-#pragma unroll
-    for (int r = 0; r < kRowsPerThread; ++r) {
-        const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
-        if (i >= a.n) continue;
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            if (j >= chunks) continue;
-            const uint32_t words[4] = {rows[r][j].x, rows[r][j].y, rows[r][j].z, rows[r][j].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int l = 4 * j + q;
-                planes[static_cast<size_t>(l) * a.n + i] = words[q];
-                // per-half maximum (v_pk_max_u16): a 32-bit maximum would follow the high half only
-                peak[l] = __builtin_elementwise_max(peak[l], __builtin_bit_cast(magnitude2, words[q] & 0x7fff7fffu));
-            }
-        }
-    }
-    // Reduce the two 16-bit halves, then across the wave and the block.
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l) {
-        if (l < a.n_levels) {
-            uint32_t m = peak[l].x > peak[l].y ? peak[l].x : peak[l].y;
-            for (int step = 32; step; step >>= 1) {
-                const uint32_t other = __shfl_xor(m, step);
-                m = other > m ? other : m;
+    for (int r = 0; r < kPasses; ++r) {
+        const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
+        const bool valid = i < a.n;
+        uint32_t peak[LMAX / 2];
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const uint32_t words[4] = {rows[r][j].x, rows[r][j].y, rows[r][j].z, rows[r][j].w};
+            if (valid && j < chunks) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) planes[static_cast<size_t>(4 * j + q) * a.n + i] = words[q];
             }
-            if (lane == 0) waves[wave][l] = m;
+            peak[2 * j] = valid ? pair_peak(words[0], words[1]) : 0u;
+            peak[2 * j + 1] = valid ? pair_peak(words[2], words[3]) : 0u;
+        }
+#pragma unroll
+        for (int p = 0; p < LMAX / 2; ++p) {
+            if (2 * p < a.n_levels) {
+                uint32_t m = peak[p];
+                for (int step = 32; step; step >>= 1) m = pair_max(m, __shfl_xor(m, step));
+                if (lane == 0) waves[r][wave][p] = m;
+            }
         }
     }
     __syncthreads();
-    if (threadIdx.x < a.n_levels) {
-        uint32_t m = 0;
-        for (int w = 0; w < kTransposeBlock / 64; ++w) m = waves[w][threadIdx.x] > m ? waves[w][threadIdx.x] : m;
-        a.blockmax[static_cast<size_t>(blockIdx.x) * a.n_levels + threadIdx.x] =
-            __half2float(bits_to_half(static_cast<uint16_t>(m)));
+    constexpr int kRecords = kTransposeRows / kMaxRows;
+    for (int t = threadIdx.x; t < kRecords * a.n_levels; t += kTransposeBlock) {
+        const int q = t / a.n_levels, l = t % a.n_levels;
+        const int64_t record = static_cast<int64_t>(blockIdx.x) * kRecords + q;
+        if (record * kMaxRows >= a.n) continue;
+        const uint32_t both = pair_max(waves[q / 2][2 * (q % 2)][l / 2], waves[q / 2][2 * (q % 2) + 1][l / 2]);
+        a.blockmax[record * a.n_levels + l] = __half2float(bits_to_half(static_cast<uint16_t>(both >> (16 * (l % 2)))));
     }
 }
 
@@ -560,7 +559,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     // Fixed-point scale from the bound 4 * count * max|upstream| over this range and levels.
     float bound = 0.0f;
     if (m1 > m0) {
-        const int64_t r0 = m0 / kTransposeRows, r1 = (m1 - 1) / kTransposeRows;
+        const int64_t r0 = m0 / kMaxRows, r1 = (m1 - 1) / kMaxRows;
         const int levels = l1 - l0;
         for (int64_t t = threadIdx.x; t < (r1 - r0 + 1) * levels; t += kOwnerBlock) {
             const float v = a.blockmax[(r0 + t / levels) * a.n_levels + l0 + t % levels];
@@ -776,8 +775,9 @@ int launch_owner_backward(const OwnerLaunch& in) {
 
     // Workspace: level-major planes, block maxima, split partials.
     const int64_t row_blocks = (in.n + kTransposeRows - 1) / kTransposeRows;
-    const size_t planes_bytes = (static_cast<size_t>(in.n) * L * F * elem + 255) / 256 * 256;
-    const size_t max_bytes = (static_cast<size_t>(row_blocks) * L * 4 + 255) / 256 * 256;
+    const int64_t records = (in.n + kMaxRows - 1) / kMaxRows;
+    const size_t planes_bytes = in.planes ? 0 : (static_cast<size_t>(in.n) * L * F * elem + 255) / 256 * 256;
+    const size_t max_bytes = in.planes ? 0 : (static_cast<size_t>(records) * L * 4 + 255) / 256 * 256;
     const size_t total_params = static_cast<size_t>(in.experts) * in.expert_params;
     const size_t partial_bytes = (splits > 1 ? static_cast<size_t>(splits) * total_params * 4 + 255 : 0) / 256 * 256;
     const size_t count_bytes =
@@ -786,8 +786,10 @@ int launch_owner_backward(const OwnerLaunch& in) {
     char* space = static_cast<char*>(
         workspace(planes_bytes + max_bytes + partial_bytes + count_bytes + list_bytes, in.stream));
     if (!space) return -1;
-    o.planes = space;
-    o.blockmax = reinterpret_cast<float*>(space + planes_bytes);
+    // upstream already level-major with its maxima (the caller wrote them): no transpose
+    const bool given = in.planes != nullptr;
+    o.planes = given ? in.planes : space;
+    o.blockmax = given ? in.blockmax : reinterpret_cast<float*>(space + planes_bytes);
     o.partial = reinterpret_cast<float*>(space + planes_bytes + max_bytes);
     int32_t* bucket_count = reinterpret_cast<int32_t*>(space + planes_bytes + max_bytes + partial_bytes);
     int32_t* bucket_list = reinterpret_cast<int32_t*>(space + planes_bytes + max_bytes + partial_bytes + count_bytes);
@@ -828,8 +830,8 @@ int launch_owner_backward(const OwnerLaunch& in) {
     } while (0)
 #define ODIE_BOTH(FF)                                                                                   \
     do {                                                                                                \
-        if (half) { ODIE_TRANSPOSE(FF, true); ODIE_OWNER(FF, true); }                                   \
-        else { ODIE_TRANSPOSE(FF, false); ODIE_OWNER(FF, false); }                                      \
+        if (half) { if (!given) ODIE_TRANSPOSE(FF, true); ODIE_OWNER(FF, true); }                      \
+        else { if (!given) ODIE_TRANSPOSE(FF, false); ODIE_OWNER(FF, false); }                         \
     } while (0)
     switch (F) {
         case 1: ODIE_BOTH(1); break;

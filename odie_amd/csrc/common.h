@@ -48,6 +48,24 @@ __device__ inline float keep_fp32(float value) {
 
 // fp16 <-> 16-bit patterns without relying on __half's class layout.
 __device__ inline __half bits_to_half(uint16_t bits) { return __ushort_as_half(bits); }
+
+// Maxima of fp16 magnitudes on their bit patterns (|a| <= |b| iff the 15-bit magnitudes compare
+// the same way, with Inf and NaN above every finite value), two 16-bit maxima per dword.
+typedef uint16_t magnitude2 __attribute__((ext_vector_type(2)));
+
+// {max |feature| of level A, max |feature| of level B} from the fp16 feature pairs of two levels.
+__device__ inline uint32_t pair_peak(uint32_t level_a, uint32_t level_b) {
+    const magnitude2 x = __builtin_bit_cast(magnitude2, level_a & 0x7fff7fffu);
+    const magnitude2 y = __builtin_bit_cast(magnitude2, level_b & 0x7fff7fffu);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_shufflevector(x, y, 0, 2),
+                                                                  __builtin_shufflevector(x, y, 1, 3)));
+}
+
+// Per-half maximum of two such dwords (v_pk_max_u16).
+__device__ inline uint32_t pair_max(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(magnitude2, a),
+                                                                  __builtin_bit_cast(magnitude2, b)));
+}
 __device__ inline uint16_t half_to_bits(__half value) { return __half_as_ushort(value); }
 
 }  // namespace odie

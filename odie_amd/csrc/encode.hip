@@ -723,22 +723,30 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
 // by odie_adam_step on the gradient, bit for bit.
 namespace odie {
 
-int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
-                                const odie_grid_level* levels, int n_levels, int features, const AdamStep& adam,
-                                hipStream_t s) {
+namespace {
+
+// Shared body of the two fused entry points: upstream rows (transposed by the owner launch)
+// or, with planes set, the level-major fp16 planes and their 128-row maxima.
+int backward_adam(const char* name, const float* coords, int64_t n, const int32_t* offsets, int experts,
+                  const void* upstream, int up_dtype, int up_width, const uint32_t* planes, const float* blockmax,
+                  int64_t expert_params, const odie_grid_level* levels, int n_levels, int features,
+                  const AdamStep& adam, hipStream_t s) {
     GridArgs a{};
-    if (validate_grid("odie_grid_backward_adam", coords, n, offsets, experts, expert_params, levels, n_levels,
-                      features, a))
-        return -1;
-    if (up_dtype != ODIE_F32 && up_dtype != ODIE_F16)
-        return fail("odie_grid_backward_adam: up_dtype must be 0 (fp32) or 1 (fp16)");
-    if (up_width < n_levels * features) return fail("odie_grid_backward_adam: up_width is smaller than n_levels*features");
-    if (n > 0 && !upstream) return fail("odie_grid_backward_adam: upstream is null");
-    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_backward_adam: coords must be 8-byte aligned");
+    if (validate_grid(name, coords, n, offsets, experts, expert_params, levels, n_levels, features, a)) return -1;
+    if (planes || blockmax) {
+        if (features != 2) return fail(std::string(name) + ": planes carry 2 fp16 features per level");
+        if (n > 0 && (!planes || !blockmax)) return fail(std::string(name) + ": planes and blockmax must be non-null");
+        if (reinterpret_cast<uintptr_t>(planes) % 4) return fail(std::string(name) + ": planes must be 4-byte aligned");
+    } else {
+        if (up_dtype != ODIE_F32 && up_dtype != ODIE_F16)
+            return fail(std::string(name) + ": up_dtype must be 0 (fp32) or 1 (fp16)");
+        if (up_width < n_levels * features) return fail(std::string(name) + ": up_width is smaller than n_levels*features");
+        if (n > 0 && !upstream) return fail(std::string(name) + ": upstream is null");
+    }
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail(std::string(name) + ": coords must be 8-byte aligned");
     const int64_t table = static_cast<int64_t>(a.level[n_levels - 1].offset + a.level[n_levels - 1].size) * features;
-    if (table >= (int64_t{1} << 31)) return fail("odie_grid_backward_adam: one table must hold fewer than 2^31 values");
-    if (expert_params != table) return fail("odie_grid_backward_adam: expert_params must equal the levels' table size");
+    if (table >= (int64_t{1} << 31)) return fail(std::string(name) + ": one table must hold fewer than 2^31 values");
+    if (expert_params != table) return fail(std::string(name) + ": expert_params must equal the levels' table size");
     const int64_t total = expert_params * experts;
     if (n == 0) {   // every gradient is zero
         float* zero = static_cast<float*>(workspace(static_cast<size_t>(total) * 4, s));
@@ -749,9 +757,11 @@ int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* o
     OwnerLaunch o{};
     o.coords = coords;
     o.offsets = a.offsets;
-    o.upstream = upstream;
-    o.up_half = up_dtype == ODIE_F16;
-    o.up_width = up_width;
+    o.upstream = planes ? nullptr : upstream;
+    o.up_half = planes ? 1 : up_dtype == ODIE_F16;
+    o.up_width = planes ? n_levels * features : up_width;
+    o.planes = planes;
+    o.blockmax = blockmax;
     o.grad = nullptr;
     o.accumulate = 0;
     o.n = n;
@@ -769,6 +779,24 @@ int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* o
     return launch_owner_backward(o);
 }
 
+}  // namespace
+
+int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                const odie_grid_level* levels, int n_levels, int features, const AdamStep& adam,
+                                hipStream_t s) {
+    return backward_adam("odie_grid_backward_adam", coords, n, offsets, experts, upstream, up_dtype, up_width, nullptr,
+                         nullptr, expert_params, levels, n_levels, features, adam, s);
+}
+
+int grid_backward_adam_planes_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                       const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                       const odie_grid_level* levels, int n_levels, int features,
+                                       const AdamStep& adam, hipStream_t s) {
+    return backward_adam("odie_grid_backward_adam_planes", coords, n, offsets, experts, nullptr, ODIE_F16, 0, planes,
+                         blockmax, expert_params, levels, n_levels, features, adam, s);
+}
+
 }  // namespace odie
 
 ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offsets, int experts,
@@ -782,6 +810,20 @@ ODIE_API int odie_grid_backward_adam(const float* coords, int64_t n, const int32
         return -1;
     return grid_backward_adam_internal(coords, n, offsets, experts, upstream, up_dtype, up_width, expert_params, levels,
                                        n_levels, features, adam, as_stream(stream));
+}
+
+ODIE_API int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                            const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                            const odie_grid_level* levels, int n_levels, int features, float* master,
+                                            uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant,
+                                            int64_t step, float lr, float beta1, float beta2, float eps,
+                                            float loss_scale, uint64_t stream) {
+    AdamStep adam;
+    if (make_adam_step("odie_grid_backward_adam_planes", master, half_copy, m, v, steps, variant, step, lr, beta1,
+                       beta2, eps, loss_scale, true, adam))
+        return -1;
+    return grid_backward_adam_planes_internal(coords, n, offsets, experts, planes, blockmax, expert_params, levels,
+                                              n_levels, features, adam, as_stream(stream));
 }
 
 ODIE_API int odie_set_tuning(const char* key, int value) {

@@ -120,6 +120,8 @@ struct OwnerLaunch {
     int bucketed;             // fine passes walk per-slice coordinate buckets
     hipStream_t stream;
     const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad
+    const void* planes;       // non-null: upstream already level-major [n_levels][n][features]
+    const float* blockmax;    // with planes: max |upstream| per 128-row record and level
 };
 int launch_owner_backward(const OwnerLaunch& launch);
 
@@ -129,6 +131,13 @@ int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* o
                                 const void* upstream, int up_dtype, int up_width, int64_t expert_params,
                                 const odie_grid_level* levels, int n_levels, int features, const AdamStep& adam,
                                 hipStream_t stream);
+
+// grid_backward_adam_internal on an upstream already in the owner's layout (fp16 level-major
+// planes and their 128-row maxima, as the decoder's training kernel can write them).
+int grid_backward_adam_planes_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                       const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                       const odie_grid_level* levels, int n_levels, int features,
+                                       const AdamStep& adam, hipStream_t stream);
 
 // The packed-plane forward with the native step's active prefix (levels >= active are off)
 // and the fp16 bits written past the last level (the runtime pads with 1.0).  levels16x2: the

@@ -109,8 +109,10 @@ struct MlpArgs {
     uint16_t* out;            // fp16 [input rows][16], or null
     uint16_t* hidden;         // fp16 [n][128] = h1 | h2 of tile row j, or null
     float* squares;           // fp32 [input rows], or null
-    uint16_t* dz;             // fp16 [n][32] = fp16(fp16(dL/dx) / 128)
+    uint16_t* dz;             // fp16 [n][32] = fp16(fp16(dL/dx) / 128), or null with planes
     float* partials;          // fp32 [blocks][7168]
+    uint32_t* planes;         // dz as level-major fp16 pairs [16][n], or null
+    float* blockmax;          // with planes: max |dz| per 128-row record and level [n/128][16]
 };
 
 // Forward of one tile: x (B operand of layer 1) -> h1, h2 (B operands of the next layers),

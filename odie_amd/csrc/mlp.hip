@@ -22,6 +22,20 @@
 namespace odie {
 namespace {
 
+// Per-half maximum of a level-pair dword over the 32 lanes of a lane group (the whole wave
+// active): DPP within rows of 16 lanes (the two quad swaps, half-row mirror, row mirror), then a
+// swizzle that pairs lane i with lane i ^ 16.
+template <int kControl> __device__ inline uint32_t dpp(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kControl, 0xF, 0xF, false));
+}
+__device__ inline uint32_t group_max(uint32_t v) {
+    v = pair_max(v, dpp<0xB1>(v));    // quad_perm [1, 0, 3, 2]
+    v = pair_max(v, dpp<0x4E>(v));    // quad_perm [2, 3, 0, 1]
+    v = pair_max(v, dpp<0x141>(v));   // row_half_mirror
+    v = pair_max(v, dpp<0x140>(v));   // row_mirror
+    return pair_max(v, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F)));  // xor 16
+}
+
 __device__ inline void load_x(const uint16_t* x, int64_t row, bool valid, int g, half8 xb[2]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -135,9 +149,11 @@ __device__ inline void round_block(const _Float16* T, int a0, int b0, int a_rows
 // buffer in two phases (1: dW3 = dy x h2 and dW1 = dh1 x x; 2: dW2 = dh2 x h1), each wave
 // owning two of the eight 32x32 gradient blocks (waves 0,1: dW3 column blocks; waves 2,3: dW1
 // row blocks; every wave one dW2 block), so no cross-wave reduction is needed.
+template <bool PLANES>
 __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
     __shared__ _Float16 w[kWeightHalfs];
     __shared__ __attribute__((aligned(16))) _Float16 T[kRoundRows * kRS];
+    __shared__ uint32_t records[kMlpWaves][2][4];   // per wave and lane group: level-pair |dz| maxima
     stage_weights(a.weights, w);
     __syncthreads();
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
@@ -214,15 +230,42 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
             f32x16 acc = zero16();
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW1t + s * kS64 + 16 * t + 8 * g), dh1[t], acc);
-            if (valid) {
+            // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value.  Word
+            // .x/.y/.z/.w of bits[q] holds the feature pair of level 8q+2g, 8q+2g+1, 8q+4+2g,
+            // 8q+5+2g (columns 16q+4g.. and 16q+8+4g.. of the row).
+            u32x4 bits[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                bits[q] = __builtin_bit_cast(u32x4, round8(acc, 8 * q) * (half8)(static_cast<_Float16>(0.0078125f)));
+            if constexpr (PLANES) {
+                if (valid) {
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        a.planes[(8 * q + 2 * g) * a.n + row] = bits[q].x;
+                        a.planes[(8 * q + 2 * g + 1) * a.n + row] = bits[q].y;
+                        a.planes[(8 * q + 4 + 2 * g) * a.n + row] = bits[q].z;
+                        a.planes[(8 * q + 5 + 2 * g) * a.n + row] = bits[q].w;
+                    }
+                }
+                // this round's 128 rows are one record: level-pair maxima over the 32 lanes of
+                // this lane group, then over the four waves (after the barrier below)
+                uint32_t peak[4];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    peak[2 * q] = valid ? pair_peak(bits[q].x, bits[q].y) : 0u;
+                    peak[2 * q + 1] = valid ? pair_peak(bits[q].z, bits[q].w) : 0u;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    peak[j] = group_max(peak[j]);
+                    if (s == 0) records[wave][g][j] = peak[j];
+                }
+            } else if (valid) {
                 uint16_t* p = a.dz + row * kIn;
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
-                    // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value
-                    const half8 h = round8(acc, 8 * q) * (half8)(static_cast<_Float16>(0.0078125f));
-                    const u32x4 bits = __builtin_bit_cast(u32x4, h);
-                    *reinterpret_cast<uint2*>(p + 16 * q + 4 * g) = make_uint2(bits.x, bits.y);
-                    *reinterpret_cast<uint2*>(p + 16 * q + 8 + 4 * g) = make_uint2(bits.z, bits.w);
+                    *reinterpret_cast<uint2*>(p + 16 * q + 4 * g) = make_uint2(bits[q].x, bits[q].y);
+                    *reinterpret_cast<uint2*>(p + 16 * q + 8 + 4 * g) = make_uint2(bits[q].z, bits[q].w);
                 }
             }
         }
@@ -237,6 +280,14 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) T[(kXRow + kt * 16 + 8 * g + e) * kRS + column] = xb[kt][e];
         __syncthreads();
+        if (PLANES && threadIdx.x < 16) {
+            // level L = 8q + 4h + 2g + b sits in word 2q + h of lane group g, half b
+            const int level = threadIdx.x, q = level / 8, h = (level / 4) % 2, lg = (level / 2) % 2, b = level % 2;
+            uint32_t m = 0;
+#pragma unroll
+            for (int v = 0; v < kMlpWaves; ++v) m = pair_max(m, records[v][lg][2 * q + h]);
+            a.blockmax[(base / kMlpWaves) * 16 + level] = __half2float(bits_to_half(static_cast<uint16_t>(m >> (16 * b))));
+        }
         if (wave < 2) round_block(T, kDyRow, kH2Row + 32 * wave, 3, g, s, gA, gA1);
         else round_block(T, kDh1Row + 32 * (wave - 2), kXRow, 32, g, s, gA, gA1);
         __syncthreads();
@@ -325,26 +376,51 @@ ODIE_API int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weig
     return check_launch("odie_mlp_forward");
 }
 
-ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
-                            const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
-                            const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz,
-                            float* dweights, uint64_t stream) {
-    if (n < 0 || real < 1) return fail("odie_mlp_train: need n >= 0 and real >= 1");
-    if (n >= (int64_t{1} << 26)) return fail("odie_mlp_train: n must be below 2^26 (32-bit byte offsets)");
-    if (!weights || !dweights || (n && (!x || !dz))) return fail("odie_mlp_train: null pointer");
+namespace {
+
+int mlp_train(const char* name, const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+              const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target, const int32_t* rows,
+              uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz, uint32_t* planes, float* blockmax,
+              float* dweights, uint64_t stream) {
+    const std::string who(name);
+    if (n < 0 || real < 1) return fail(who + ": need n >= 0 and real >= 1");
+    if (n >= (int64_t{1} << 26)) return fail(who + ": n must be below 2^26 (32-bit byte offsets)");
+    if (!weights || !dweights || (n && !x)) return fail(who + ": null pointer");
+    if (n && (planes ? !blockmax : !dz)) return fail(who + ": null pointer");
     if (n && !colors && !(rgb ? ids != nullptr : target != nullptr))
-        return fail("odie_mlp_train: need colors, rgb with ids, or target");
+        return fail(who + ": need colors, rgb with ids, or target");
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(dz) % 8 ||
-        (out && reinterpret_cast<uintptr_t>(out) % 8))
-        return fail("odie_mlp_train: x must be 16-byte, dz and out 8-byte aligned");
+        reinterpret_cast<uintptr_t>(planes) % 4 || (out && reinterpret_cast<uintptr_t>(out) % 8))
+        return fail(who + ": x must be 16-byte, dz and out 8-byte, planes 4-byte aligned");
     const hipStream_t s = as_stream(stream);
     if (n == 0) return launch_fill_zero(dweights, kParams, s);
     const int blocks = mlp_blocks(n);
     float* partials = static_cast<float*>(workspace(static_cast<size_t>(blocks) * kParams * sizeof(float), s));
     if (!partials) return -1;
-    MlpArgs a{x, weights, n, real, colors, rgb, ids, target, rows, out, hidden, squares, dz, partials};
-    mlp_train_kernel<<<blocks, kMlpBlock, 0, s>>>(a);
-    if (check_launch("odie_mlp_train")) return -1;
+    MlpArgs a{x, weights, n, real, colors, rgb, ids, target, rows, out, hidden, squares, planes ? nullptr : dz, partials,
+              planes, planes ? blockmax : nullptr};
+    if (planes) mlp_train_kernel<true><<<blocks, kMlpBlock, 0, s>>>(a);
+    else mlp_train_kernel<false><<<blocks, kMlpBlock, 0, s>>>(a);
+    if (check_launch(name)) return -1;
     mlp_reduce_kernel<<<(kParams + kReduceParams - 1) / kReduceParams, 256, 0, s>>>(partials, blocks, dweights);
-    return check_launch("odie_mlp_train reduce");
+    return check_launch((who + " reduce").c_str());
+}
+
+}  // namespace
+
+ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+                            const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
+                            const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz,
+                            float* dweights, uint64_t stream) {
+    return mlp_train("odie_mlp_train", x, n, real, weights, colors, rgb, ids, target, rows, out, hidden, squares, dz,
+                     nullptr, nullptr, dweights, stream);
+}
+
+ODIE_API int odie_mlp_train_planes(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+                                   const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
+                                   const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares,
+                                   uint32_t* planes, float* blockmax, float* dweights, uint64_t stream) {
+    if (n > 0 && !planes) return fail("odie_mlp_train_planes: planes is null");
+    return mlp_train("odie_mlp_train_planes", x, n, real, weights, colors, rgb, ids, target, rows, out, hidden,
+                     squares, nullptr, planes, blockmax, dweights, stream);
 }

@@ -13,6 +13,7 @@ import torch
 from . import _lib, synth
 
 INPUT, HIDDEN, OUTPUT = 32, 64, 16
+LEVELS = INPUT // 2   # grid levels of 2 features in the input
 SHAPES = ((HIDDEN, INPUT), (HIDDEN, HIDDEN), (OUTPUT, HIDDEN))
 PARAMETERS = sum(rows * cols for rows, cols in SHAPES)   # 7168 (odie/config.py:176-177)
 
@@ -63,6 +64,31 @@ class Decoder:
             _lib.ptr(rows), _lib.ptr(out), _lib.ptr(hidden), _lib.ptr(squares), dz.data_ptr(), self.grad.data_ptr(),
             _lib.stream_of(x)))
         return dz
+
+    def train_planes(self, x, real=None, *, colors=None, rgb=None, ids=None, target=None, rows=None, out=None,
+                     hidden=None, squares=None, planes=None, blockmax=None):
+        """train() with dz written for ExpertGrid.backward_adam_planes: planes int32 [16, n] (the
+        fp16 feature pair of each level and row) and blockmax fp32 [ceil(n/128), 16] (max |dz|
+        per 128-row record and level).  Returns (planes, blockmax)."""
+        x = _features(x)
+        n = x.shape[0]
+        real = n if real is None else int(real)
+        if colors is None and ((rgb is None) == (target is None) or (rgb is not None and ids is None)):
+            raise ValueError('give colors, rgb with ids, or target')
+        records = (n + 127) // 128
+        if planes is None:
+            planes = torch.empty((LEVELS, n), dtype=torch.int32, device=x.device)
+        if blockmax is None:
+            blockmax = torch.empty((records, LEVELS), dtype=torch.float32, device=x.device)
+        if tuple(planes.shape) != (LEVELS, n) or planes.dtype != torch.int32 or not planes.is_contiguous():
+            raise ValueError('planes must be a contiguous int32 [16, n] tensor')
+        if tuple(blockmax.shape) != (records, LEVELS) or blockmax.dtype != torch.float32 or not blockmax.is_contiguous():
+            raise ValueError('blockmax must be a contiguous fp32 [ceil(n/128), 16] tensor')
+        _lib.check(_lib.library().odie_mlp_train_planes(
+            x.data_ptr(), n, real, self.half.data_ptr(), _lib.ptr(colors), _lib.ptr(rgb), _lib.ptr(ids),
+            _lib.ptr(target), _lib.ptr(rows), _lib.ptr(out), _lib.ptr(hidden), _lib.ptr(squares), planes.data_ptr(),
+            blockmax.data_ptr(), self.grad.data_ptr(), _lib.stream_of(x)))
+        return planes, blockmax
 
 
 def _features(x):

@@ -93,3 +93,26 @@ class ExpertGrid:
             optimizer.v.data_ptr(), _lib.ptr(optimizer.steps), optimizer.variant_code, optimizer.step_count,
             optimizer.lr, optimizer.betas[0], optimizer.betas[1], optimizer.eps, float(loss_scale),
             _lib.stream_of(coords)))
+
+    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0):
+        """backward_adam with the fp16 upstream given as Decoder.train_planes writes it (planes
+        int32 [levels, N], blockmax fp32 [ceil(N/128), levels]): the same update, bit for bit."""
+        from .encoding import _check_coords, _offsets_arg
+        _check_coords(coords)
+        n = coords.shape[0]
+        levels = len(self.levels)
+        if tuple(planes.shape) != (levels, n) or planes.dtype != torch.int32 or not planes.is_contiguous():
+            raise ValueError('planes must be a contiguous int32 [levels, N] tensor')
+        if (tuple(blockmax.shape) != ((n + 127) // 128, levels) or blockmax.dtype != torch.float32
+                or not blockmax.is_contiguous()):
+            raise ValueError('blockmax must be a contiguous fp32 [ceil(N/128), levels] tensor')
+        if optimizer.master.numel() != self.experts * self.expert_params:
+            raise ValueError('the optimizer must own this table\'s fp32 master')
+        offsets = _offsets_arg(offsets, self.experts, n)
+        optimizer.step_count += 1
+        _lib.check(_lib.library().odie_grid_backward_adam_planes(
+            coords.data_ptr(), n, _lib.ptr(offsets), self.experts, planes.data_ptr(), blockmax.data_ptr(),
+            self.expert_params, self.levels, levels, self.features, optimizer.master.data_ptr(),
+            _lib.ptr(optimizer.half_copy), optimizer.m.data_ptr(), optimizer.v.data_ptr(), _lib.ptr(optimizer.steps),
+            optimizer.variant_code, optimizer.step_count, optimizer.lr, optimizer.betas[0], optimizer.betas[1],
+            optimizer.eps, float(loss_scale), _lib.stream_of(coords)))

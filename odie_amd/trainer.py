@@ -15,6 +15,10 @@ before the decoder and turns the decoder's input gradient into the grid's upstre
 
 With fused=True (the default) the grid's Adam step runs inside the encode backward
 (odie_grid_backward_adam): the gradient never reaches memory, and self.gradient is unused.
+Without the router, planes=True (the default) has the decoder write the grid's upstream in the
+encode backward's own level-major layout with its 128-row maxima (odie_mlp_train_planes,
+odie_grid_backward_adam_planes), so the backward does not transpose it; the result is the same,
+bit for bit.
 
 Every buffer is allocated once, at construction, for `batch` ids; a step allocates nothing
 on the device beyond the library's grow-once workspace.
@@ -33,7 +37,8 @@ GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:
 
 class ExpertTrainer:
     def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
-                 device='cuda', fused=True, router=False, gate_lr=1e-3, coarse_levels=0, activation='sigmoid'):
+                 device='cuda', fused=True, router=False, gate_lr=1e-3, coarse_levels=0, activation='sigmoid',
+                 planes=True):
         if isinstance(image, torch.Tensor):    # already on the device (gigapixel images)
             if image.dtype != torch.uint8 or image.ndim != 3 or image.shape[2] != 3:
                 raise ValueError('image must be uint8 [height, width, 3]')
@@ -77,6 +82,10 @@ class ExpertTrainer:
         self.dz = torch.empty((batch, self.grid.width), dtype=torch.float16, device=device)
         self.gradient = None if fused else torch.empty(total, dtype=torch.float32, device=device)
         self.squares = torch.empty(batch, dtype=torch.float32, device=device)
+        self.planes = planes and fused and not router
+        if self.planes:
+            self.plane_buffer = torch.empty(16 * batch, dtype=torch.int32, device=device)
+            self.max_buffer = torch.empty(16 * ((batch + 127) // 128), dtype=torch.float32, device=device)
         if self.grid.width != 32:
             raise ValueError('the decoder takes 32 input features (16 levels x 2)')
 
@@ -98,6 +107,18 @@ class ExpertTrainer:
         if self.gate is not None:
             features, sigmoid = self.gate.forward(raw, weighted=self.weighted[:n], sigmoid=self.sigmoid[:n])
         # squared errors stay in routed order (slot j is id perm[j]); their mean is the loss
+        if self.planes and update:
+            planes, blockmax = self.decoder.train_planes(
+                features, n, colors=view.colors, squares=self.squares[:n], planes=self.plane_buffer[:16 * n].view(16, n),
+                blockmax=self.max_buffer[:16 * ((n + 127) // 128)].view(-1, 16))
+            mark('decoder')
+            self.grid.backward_adam_planes(view.coords, view.offsets, planes, blockmax, self.grid_optimizer,
+                                           loss_scale=GRID_SCALE)
+            mark('encode_backward')
+            mark('grid_adam')
+            self.decoder_optimizer.step(self.decoder.grad, loss_scale=HEAD_SCALE)
+            mark('decoder_adam')
+            return self.squares[:n]
         self.decoder.train(features, n, colors=view.colors, squares=self.squares[:n], dz=self.dz[:n])
         upstream = self.dz[:n]
         if self.gate is not None:

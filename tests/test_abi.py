@@ -103,6 +103,23 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert 'target' in native.odie_error().decode()
     assert native.odie_mlp_train(16, 10, 0, 16, None, None, None, 16, None, None, None, None, 16, 16, 0) == -1
     assert 'real' in native.odie_error().decode()
+    assert native.odie_mlp_train_planes(16, 10, 10, 16, 16, None, None, None, None, None, None, None, None, 16, 16,
+                                        0) == -1
+    assert 'planes is null' in native.odie_error().decode()
+    assert native.odie_mlp_train_planes(16, 10, 10, 16, 16, None, None, None, None, None, None, None, 16, None, 16,
+                                        0) == -1
+    assert 'null' in native.odie_error().decode()
+    assert native.odie_mlp_train_planes(16, 10, 10, 16, 16, None, None, None, None, None, None, None, 18, 16, 16,
+                                        0) == -1
+    assert 'aligned' in native.odie_error().decode()
+    # encode backward on planes: two features per level, both buffers
+    from odie_amd.config import grid_levels
+    levels, entries = grid_levels(dict(n_levels=16, base_resolution=8, log2_hashmap_size=10, per_level_scale=1.4))
+    adam = [16, None, 16, 16, 16, 1, 1, 0.01, 0.9, 0.99, 1e-15, 128.0, 0]
+    assert native.odie_grid_backward_adam_planes(16, 10, None, 1, 16, None, entries * 2, levels, 16, 2, *adam) == -1
+    assert 'planes and blockmax must be' in native.odie_error().decode()
+    assert native.odie_grid_backward_adam_planes(16, 10, None, 1, 16, 16, entries, levels, 16, 1, *adam) == -1
+    assert '2 fp16 features' in native.odie_error().decode()
     # router gate: coarse range, alignment
     assert native.odie_gate_forward(16, 10, 16, None, 17, 0, 16, 16, 0) == -1 and 'coarse' in native.odie_error().decode()
     assert native.odie_gate_forward(8, 10, 16, None, 0, 0, 16, 16, 0) == -1 and 'aligned' in native.odie_error().decode()

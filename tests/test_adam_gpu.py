@@ -83,3 +83,38 @@ def test_grid_backward_adam_equals_backward_then_adam(experts, n, variant, up16)
     assert np.array_equal(grids[0].table.cpu().numpy().view(np.uint16), grids[1].table.cpu().numpy().view(np.uint16))
     if variant != 'torch':
         assert np.array_equal(optimizers[0].steps.cpu().numpy(), optimizers[1].steps.cpu().numpy())
+
+
+@pytest.mark.parametrize('experts,n,variant', [
+    (4, 20000, 'tcnn'),
+    (1, 200000, 'tcnn'),        # one expert, many coords: split passes and their reduction
+    (3, 1000 + 17, 'torch'),    # ragged last 128-row record
+])
+def test_grid_backward_adam_planes_equals_rows(experts, n, variant):
+    """odie_grid_backward_adam_planes on the upstream's level-major planes and 128-row maxima
+    (built here with torch) gives the row-major entry point's update bit for bit."""
+    from odie_amd.experts import ExpertGrid
+    encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=8, per_level_scale=1.4)
+    grids, optimizers = [], []
+    for _ in range(2):
+        grid = ExpertGrid(encoding, experts, dtype=torch.float16)
+        master = torch.from_numpy(synth.table(8, grid.table.numel())).cuda()
+        grid.table.copy_(master)
+        grids.append(grid)
+        optimizers.append(FusedAdam(master, lr=1e-2, variant=variant, half_copy=grid.table))
+    coords = torch.from_numpy(synth.coordinates(9, n)).cuda()
+    counts = np.diff(np.linspace(0, n, experts + 1).astype(np.int64))
+    offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).cuda()
+    records = (n + 127) // 128
+    for step in range(2):
+        upstream = torch.from_numpy(synth.upstream(10 + step, n, 32)).cuda()
+        planes = upstream.view(torch.int32).t().contiguous()
+        level = torch.zeros((records * 128, 16), dtype=torch.float32, device='cuda')
+        level[:n] = upstream.abs().view(n, 16, 2).amax(dim=2).float()
+        blockmax = level.view(records, 128, 16).amax(dim=1).contiguous()
+        grids[0].backward_adam_planes(coords, offsets, planes, blockmax, optimizers[0], loss_scale=128.0)
+        grids[1].backward_adam(coords, offsets, upstream, optimizers[1], loss_scale=128.0)
+    for name in ('master', 'm', 'v'):
+        x, y = (getattr(o, name).cpu().numpy() for o in optimizers)
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+    assert np.array_equal(grids[0].table.cpu().numpy().view(np.uint16), grids[1].table.cpu().numpy().view(np.uint16))

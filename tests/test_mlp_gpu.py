@@ -125,3 +125,41 @@ def test_empty_batch_zeroes_weight_gradient():
                   target=torch.zeros((0, 3), device='cuda'))
     torch.cuda.synchronize()
     assert decoder.grad.shape == (PARAMETERS,) and not decoder.grad.any()
+
+
+def _record_maxima(dz):
+    """max |dz| per 128-row record and level (torch's amax keeps NaN), fp32 [ceil(n/128), 16]."""
+    n = dz.shape[0]
+    records = (n + 127) // 128
+    level = dz.abs().view(n, 16, 2).amax(dim=2).float()
+    padded = torch.zeros((records * 128, 16), dtype=torch.float32, device=dz.device)
+    padded[:n] = level
+    return padded.view(records, 128, 16).amax(dim=1)
+
+
+@pytest.mark.parametrize('n,poison', [(1, False), (1000, False), (4096 + 37, False), (1 << 17, False), (3000, True)])
+def test_train_planes_equals_rows(n, poison):
+    """odie_mlp_train_planes writes odie_mlp_train's dz, bit for bit, as level-major planes with
+    exact 128-row maxima (NaN where a row of the record is NaN); outputs and gradients agree."""
+    x, decoder = _inputs(13, n)
+    xd = torch.from_numpy(x).cuda()
+    if poison:
+        # a NaN target makes its row's dz NaN (a NaN input would not: the ReLU on bit patterns
+        # turns a negative-signed NaN into +0)
+        target = torch.from_numpy(synth.normal(13, 'target', n * 3).reshape(n, 3).astype(np.float32)).cuda()
+        target[1234, 1] = float('nan')
+        source = dict(target=target)
+    else:
+        image = synth.image(13, 64, 48)
+        source = dict(rgb=torch.from_numpy(image).cuda(), ids=torch.from_numpy(synth.integers(13, 'ids', n, 64 * 48)).cuda())
+    squares = [torch.full((n,), float('nan'), device='cuda') for _ in range(2)]
+    dz = decoder.train(xd, squares=squares[0], **source)
+    rows_grad = decoder.grad.clone()
+    planes, blockmax = decoder.train_planes(xd, squares=squares[1], **source)
+    want = dz.view(torch.int32).view(n, 16).t().contiguous()
+    assert torch.equal(planes, want)
+    expected = _record_maxima(dz)
+    assert np.array_equal(blockmax.cpu().numpy(), expected.cpu().numpy(), equal_nan=True)
+    assert bool(blockmax.isnan().any()) == poison
+    assert torch.equal(squares[0].view(torch.int32), squares[1].view(torch.int32))
+    assert torch.equal(decoder.grad.view(torch.int32), rows_grad.view(torch.int32))

@@ -123,6 +123,26 @@ def test_fused_grid_adam_step_is_bit_identical():
     assert np.array_equal(fused.decoder.params.cpu().numpy(), plain.decoder.params.cpu().numpy())
 
 
+def test_planes_layout_step_is_bit_identical():
+    """The decoder writing the grid's upstream as level-major planes (the default without the
+    router) trains exactly as the row-major upstream does."""
+    width, height = 96, 70
+    image = synth.image(9, width, height)
+    planes = ExpertTrainer(image, ENCODING, 3, 2, 5000, seed=9)
+    rows = ExpertTrainer(image, ENCODING, 3, 2, 5000, seed=9, planes=False)
+    assert planes.planes and not rows.planes
+    for step in range(3):
+        ids = torch.from_numpy(synth.integers(step, 'planes_ids', 5000 - 11 * step, width * height)).cuda()
+        a = planes.step(ids).cpu().numpy()
+        b = rows.step(ids).cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for name in ('master', 'm', 'v'):
+        x = getattr(planes.grid_optimizer, name).cpu().numpy()
+        y = getattr(rows.grid_optimizer, name).cpu().numpy()
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+    assert np.array_equal(planes.decoder.params.cpu().numpy(), rows.decoder.params.cpu().numpy())
+
+
 def test_router_step_composes_the_tested_stages():
     from odie_amd.decoder import Decoder
     from odie_amd.gate import Gate
