@@ -498,6 +498,34 @@ __global__ __launch_bounds__(kBucketBlock) void bucket_kernel(OwnerArgs a, int b
     }
 }
 
+// Block -> work item.  Remapped, each XCD takes a contiguous chunk of the items (an expert's
+// slices share its coordinates in that XCD's L2).  Inside a chunk the heavy items -- the
+// splits of every expert's coarse-group pass, `heavy` per expert, which walk all coordinates
+// through several fully landing levels and take about six times as long as a fine slice --
+// come first, so that they start at once instead of finishing after everything else.  A
+// permutation of [0, blocks) that keeps every item in its chunk.
+__device__ inline uint32_t work_of(uint32_t block, uint32_t blocks, int remap, uint32_t per_expert,
+                                   uint32_t heavy) {
+    uint32_t chunk = blocks, q = block, o = 0;
+    if (remap) {
+        chunk = blocks / kXcds;
+        o = (block % kXcds) * chunk;
+        q = block / kXcds;
+    }
+    if (heavy == 0 || heavy >= per_expert) return o + q;
+    const auto heavy_before = [&](uint32_t w) {
+        const uint32_t r = w % per_expert;
+        return (w / per_expert) * heavy + (r < heavy ? r : heavy);
+    };
+    const uint32_t f0 = heavy_before(o), count = heavy_before(o + chunk) - f0;
+    if (q < count) {
+        const uint32_t k = f0 + q;
+        return (k / heavy) * per_expert + k % heavy;
+    }
+    const uint32_t light = per_expert - heavy, m = (o - f0) + (q - count);
+    return (m / light) * per_expert + heavy + m % light;
+}
+
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
@@ -509,7 +537,8 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     const int split_passes = a.bucketed ? a.fine_first : a.passes;
     const uint32_t per_expert = static_cast<uint32_t>(split_passes * a.splits + (a.passes - split_passes));
     const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
-    const uint32_t work = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
+    const uint32_t heavy = a.group > 0 && split_passes > 0 ? static_cast<uint32_t>(a.splits) : 0u;
+    const uint32_t work = work_of(blockIdx.x, gridDim.x, a.remap, per_expert, heavy);
     if (work >= total) return;
     const int e = work / per_expert;
     const int r = work % per_expert;
