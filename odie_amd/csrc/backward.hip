@@ -20,6 +20,8 @@
 //   3. reduce     only when one expert's coordinates are split over several workgroups per
 //                 slice (few experts, many coordinates): partial slices are summed.
 // Every gradient entry is written by exactly one workgroup, so no clearing pass is needed.
+#include <cmath>
+
 #include "grid.h"
 #include "adam.h"
 
@@ -197,6 +199,7 @@ struct OwnerArgs {
     int splits;       // coordinate splits per pass
     int accumulate;   // 1: grad += slice
     int remap;
+    int split_passes; // passes 0 .. split_passes-1 are split `splits` ways
     DevLevel level[ODIE_MAX_LEVELS];
     int first_pass[ODIE_MAX_LEVELS];
     int slices[ODIE_MAX_LEVELS];
@@ -531,10 +534,9 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
     __shared__ float reduce[kOwnerBlock / 64];
     using U = Elem<HALF>;
-    // Work items per expert: every pass split `splits` ways, or, with buckets, only the coarse
-    // group pass split and each bucketed pass whole (its bucket order is not deterministic, so
-    // only a whole bucket gives a deterministic sum).
-    const int split_passes = a.bucketed ? a.fine_first : a.passes;
+    // Work items per expert: the first split_passes passes split `splits` ways (all of them, or
+    // only the coarse group pass), the others whole.
+    const int split_passes = a.split_passes;
     const uint32_t per_expert = static_cast<uint32_t>(split_passes * a.splits + (a.passes - split_passes));
     const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
     const uint32_t heavy = a.group > 0 && split_passes > 0 ? static_cast<uint32_t>(a.splits) : 0u;
@@ -793,14 +795,32 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.fine_passes = passes - o.fine_first;
     o.bucketed = in.bucketed && o.fine_passes > 0 && static_cast<int64_t>(o.fine_passes) * 8 <= 64 * 1024 &&
                  static_cast<int64_t>(o.fine_passes) * in.n < (int64_t{1} << 31);
+    // Splits.  Too few work items to fill the GPU: every pass is split over the coordinates (and
+    // the partials summed by split_reduce_kernel).  Otherwise only the coarse-group pass may be:
+    // it walks every coordinate through `group` fully landing levels, about group + 1 times the
+    // work of a fine slice (measured: ~6x with 5 levels), and when that alone exceeds one CU's
+    // share of the whole pass it would set the kernel's length (the native step's single-expert
+    // batch), so it is cut into pieces of about that share.
     const int64_t per_pass = static_cast<int64_t>(in.experts) * passes;
     int splits = 1;
-    if (per_pass < 512) {
+    int split_passes = passes;
+    if (per_pass < 128) {
         const int64_t want = (512 + per_pass - 1) / per_pass;
         const int64_t most = in.n / (static_cast<int64_t>(in.experts) * 16384);
         splits = static_cast<int>(want < most ? want : (most > 1 ? most : 1));
+    } else if (group > 0) {
+        const double share = static_cast<double>(in.experts) * (passes + group) / kCus;   // fine-slice units
+        if (group + 1 > share) {
+            const int64_t want = static_cast<int64_t>(std::ceil((group + 1) / (share > 1.0 ? share : 1.0)));
+            const int64_t most = in.n / (static_cast<int64_t>(in.experts) * 4096);
+            splits = static_cast<int>(want < most ? want : (most > 1 ? most : 1));
+        }
+        split_passes = 1;
     }
+    if (o.bucketed) split_passes = o.fine_first;   // a bucket is summed whole (its order varies)
+    if (splits == 1) split_passes = passes;
     o.splits = splits;
+    o.split_passes = split_passes;
 
     // Workspace: level-major planes, block maxima, split partials.
     const int64_t row_blocks = (in.n + kTransposeRows - 1) / kTransposeRows;
@@ -837,7 +857,6 @@ int launch_owner_backward(const OwnerLaunch& in) {
                  (L * F * elem) % 16 == 0;
     const uint32_t tblocks = static_cast<uint32_t>(row_blocks);
     const size_t shmem = static_cast<size_t>(cap + F) * 8 + kRingBytes;
-    const int split_passes = o.bucketed ? o.fine_first : passes;
     const uint32_t total =
         static_cast<uint32_t>(in.experts * (static_cast<int64_t>(split_passes) * splits + (passes - split_passes)));
     const uint32_t oblocks = round_up(total, kXcds);
@@ -872,8 +891,8 @@ int launch_owner_backward(const OwnerLaunch& in) {
 #undef ODIE_OWNER
 #undef ODIE_TRANSPOSE
     if (splits > 1 && split_passes > 0) {
-        // with buckets only the coarse group pass (the expert's first values) is split
-        const int64_t prefix = o.bucketed
+        // only the coarse group pass split: the expert's first values
+        const int64_t prefix = split_passes < passes
             ? static_cast<int64_t>(in.levels[group - 1].offset + in.levels[group - 1].size) * F
             : in.expert_params;
         int64_t blocks = (static_cast<int64_t>(in.experts) * prefix + 255) / 256;

@@ -26,6 +26,7 @@ int launch_fill_zero(float* data, int64_t count, hipStream_t stream);
 inline hipStream_t as_stream(uint64_t bits) { return reinterpret_cast<hipStream_t>(bits); }
 
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin across them
+constexpr int kCus = 256; // MI355X: compute units (32 per XCD)
 
 // Map a hardware block id onto a logical id so that consecutive logical ids run on the
 // same XCD (and share its L2).  `blocks` must be a multiple of kXcds.

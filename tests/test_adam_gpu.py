@@ -118,3 +118,31 @@ def test_grid_backward_adam_planes_equals_rows(experts, n, variant):
         x, y = (getattr(o, name).cpu().numpy() for o in optimizers)
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
     assert np.array_equal(grids[0].table.cpu().numpy().view(np.uint16), grids[1].table.cpu().numpy().view(np.uint16))
+
+
+def test_fused_backward_with_split_group_pass():
+    """One expert with 2^19-entry tables and 65536 coordinates (the native step's batch): only
+    the coarse-group pass is split over the coordinates and summed, with the optimizer applied in
+    that sum; the rest flush straight into the optimizer.  Same update as backward + adam."""
+    from odie_amd.experts import ExpertGrid
+    encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=19, base_resolution=16,
+                    per_level_scale=1.38)
+    n = 65536
+    grids, optimizers = [], []
+    for _ in range(2):
+        grid = ExpertGrid(encoding, 1, dtype=torch.float16)
+        master = torch.from_numpy(synth.table(12, grid.table.numel())).cuda()
+        grid.table.copy_(master)
+        grids.append(grid)
+        optimizers.append(FusedAdam(master, lr=1e-2, variant='tcnn', half_copy=grid.table))
+    coords = torch.from_numpy(synth.coordinates(13, n)).cuda()
+    offsets = torch.tensor([0, n], dtype=torch.int32, device='cuda')
+    for step in range(2):
+        upstream = torch.from_numpy(synth.upstream(14 + step, n, 32)).cuda()
+        grids[0].backward_adam(coords, offsets, upstream, optimizers[0], loss_scale=128.0)
+        gradient = grids[1].backward(coords, offsets, upstream)
+        optimizers[1].step(gradient, loss_scale=128.0)
+    for name in ('master', 'm', 'v'):
+        x, y = (getattr(o, name).cpu().numpy() for o in optimizers)
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+    assert np.array_equal(optimizers[0].steps.cpu().numpy(), optimizers[1].steps.cpu().numpy())
