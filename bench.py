@@ -43,9 +43,9 @@ ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=16, base_
 #   fused into the encode backward (the gradient stays in LDS): 38 - 8                   = 30
 STAGE_BYTES = {'route': 20, 'encode_forward': 328, 'decoder': 147, 'encode_backward': 1096}
 ADAM_BYTES, FUSED_ADAM_BYTES = 38, 30
-KERNELS = {'route': 'route_count/scan/scatter kernels', 'encode_forward': 'grid_forward_kernel',
-           'decoder': 'mlp_train_kernel + mlp_reduce_kernel',
-           'encode_backward': 'transpose_half2_kernel + owner_kernel (grid Adam fused into its flush)',
+KERNELS = {'route': 'route_count/scan/scatter/colors kernels', 'encode_forward': 'grid_forward_kernel',
+           'decoder': 'mlp_train_kernel<true> (dz as level-major planes + 128-row maxima) + mlp_reduce_kernel',
+           'encode_backward': 'owner_kernel (grid Adam fused into its flush; upstream planes from the decoder)',
            'grid_adam': 'adam_kernel',
            'decoder_adam': 'adam_kernel'}
 
