@@ -260,6 +260,110 @@ __global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t
     }
 }
 
+// The scatter with one wave per block staging its sub-chunk in LDS: the wave first places
+// every id of its sub-chunk at its position inside the sub-chunk's expert-ordered output
+// (the run of expert e starts at the sum of the sub-chunk's counts of the experts before e),
+// then writes the runs out in order, so consecutive lanes store consecutive slots.  Same slots
+// as route_scatter_kernel; the stores are whole runs instead of one id per expert per group.
+struct Staging {
+    int32_t* running;  // [experts] ids of each expert placed so far
+    int32_t* start;    // [experts] first local position of each expert's run
+    int32_t* slot;     // [part] global slot of local position j
+    int32_t* index;    // [part] input index
+    float* u;
+    float* v;
+    uint32_t* pixel;
+};
+
+__device__ inline Staging staging(int32_t* lds, int experts, int part) {
+    Staging t;
+    t.running = lds;
+    t.start = lds + experts;
+    t.slot = lds + 2 * experts;
+    t.index = t.slot + part;
+    t.u = reinterpret_cast<float*>(t.index + part);
+    t.v = t.u + part;
+    t.pixel = reinterpret_cast<uint32_t*>(t.v + part);
+    return t;
+}
+
+inline size_t staging_bytes(int experts, int part) { return (static_cast<size_t>(2) * experts + 5 * part) * 4; }
+
+__global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
+    extern __shared__ int32_t lds[];
+    __shared__ Bounds bounds;
+    load_bounds(a, bounds);
+    const int lane = threadIdx.x;
+    const int part = blockIdx.x;
+    if (part >= a.parts) return;
+    const Staging t = staging(lds, a.experts, a.part);
+    // local run starts: exclusive scan over the experts of this sub-chunk's counts (count(e, part)
+    // is the difference of consecutive scanned offsets in expert-major order)
+    const int64_t last = static_cast<int64_t>(a.experts) * a.parts - 1;
+    int32_t carry = 0;
+    for (int e0 = 0; e0 < a.experts; e0 += 64) {
+        const int e = e0 + lane;
+        int32_t c = 0;
+        if (e < a.experts) {
+            const int64_t k = static_cast<int64_t>(e) * a.parts + part;
+            const int32_t next = k < last ? a.counts[k + 1] : static_cast<int32_t>(a.n);
+            c = next - a.counts[k];
+        }
+        int32_t inclusive = c;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int32_t other = __shfl_up(inclusive, d);
+            if (lane >= d) inclusive += other;
+        }
+        if (e < a.experts) {
+            t.start[e] = carry + inclusive - c;
+            t.running[e] = 0;
+        }
+        carry += __shfl(inclusive, 63);
+    }
+    __syncthreads();
+    const int64_t begin = static_cast<int64_t>(part) * a.part;
+    const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    for (int64_t group = begin; group < end; group += 64) {
+        const int64_t i = group + lane;
+        const bool valid = i < end;
+        int expert = -1, rx = 0, ry = 0;
+        uint32_t x = 0, y = 0;
+        if (valid) locate(a, bounds, i, expert, x, y, rx, ry);
+        uint64_t same = __ballot(valid);
+        for (int bit = 0; bit < a.expert_bits; ++bit) {
+            const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
+            same &= ((expert >> bit) & 1) ? ones : ~ones;
+        }
+        int32_t base = 0, rank = 0;
+        if (valid) {
+            rank = __popcll(same & below);
+            base = t.running[expert];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank == 0) t.running[expert] = base + __popcll(same);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (valid) {
+            const int32_t local = t.start[expert] + base + rank;
+            t.slot[local] = a.counts[static_cast<int64_t>(expert) * a.parts + part] + base + rank;
+            t.index[local] = static_cast<int32_t>(i);
+            t.u[local] = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
+            t.v[local] = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
+            t.pixel[local] = y * a.width + x;
+            if (a.expert_out) a.expert_out[i] = expert;
+        }
+    }
+    __syncthreads();
+    const int32_t count = static_cast<int32_t>(end - begin);
+    for (int32_t j = lane; j < count; j += 64) {
+        const int32_t slot = t.slot[j];
+        a.perm[slot] = t.index[j];
+        reinterpret_cast<float2*>(a.coords)[slot] = make_float2(t.u[j], t.v[j]);
+        if (a.colors) a.colors[slot] = t.pixel[j];
+    }
+}
+
 int route_plan(int64_t n, int experts, int& part, int& parts) {
     // Sub-chunks of at least 1024 ids, few enough that experts*parts stays <= 2^22 (16 MiB of
     // counts): with many experts a sub-chunk stays short enough to keep every CU busy.
@@ -355,7 +459,12 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
     route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
     route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
     route_scan_apply_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
-    route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
+    // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU)
+    const size_t staged = staging_bytes(experts, a.part);
+    if (staged + sizeof(Bounds) <= 40 * 1024)
+        route_scatter_staged_kernel<<<static_cast<uint32_t>(a.parts), 64, staged, s>>>(a);
+    else
+        route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     if (colors) {
         const uint32_t chunks = round_up(static_cast<uint32_t>((n + kColorsChunk - 1) / kColorsChunk), kXcds);
         route_colors_kernel<<<chunks, kRouteBlock, 0, s>>>(rgb, colors, n);
