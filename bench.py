@@ -153,6 +153,7 @@ def native_steps(image, steps):
     from odie_amd.gate import Gate
     from odie_amd.model import PackedPlanes
     from odie_amd.native_backend import NativeModel, NativeOptimizer, make_native_optimizer
+    from odie_amd.sampling import stratified_batches
 
     target = torch.from_numpy(image).cuda().contiguous()
     shape = image.shape[:2]
@@ -179,27 +180,33 @@ def native_steps(image, steps):
                 model = NativeModel(Decoder(seed=0), Gate(seed=1), grid=grid)
                 optimizer = NativeOptimizer(model, target, shape, config, [grid])
             optimizer.prepare_epoch()
-            batches = [torch.from_numpy(synth.integers(k, 'native_ids', 65536, shape[0] * shape[1])).cuda()
-                       for k in range(4)]
-            for k in range(5):
-                optimizer.train_batch(batches[k % 4])
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            start.record(stream)
-            for k in range(steps):
-                optimizer.fixed.copy_(batches[k % 4])
-                optimizer.graph.replay()
-            stop.record(stream)
-            torch.cuda.synchronize()
-            ms = start.elapsed_time(stop) / steps
-            loss = float(optimizer.squares.double().mean())
-            out[kind] = {'ms_per_step': ms, 'pixels_per_s': 65536 / (ms / 1e3), 'params': model.grid.numel(),
-                         'loss': loss}
+            draw = stratified_batches(shape, 65536, torch.Generator(device='cuda').manual_seed(0))
+            samplings = {'': [next(draw) for _ in range(4)],
+                         '_uniform_ids': [torch.from_numpy(synth.integers(k, 'native_ids', 65536,
+                                                                          shape[0] * shape[1])).cuda()
+                                          for k in range(4)]}
+            for suffix, batches in samplings.items():
+                for k in range(5):
+                    optimizer.train_batch(batches[k % 4])
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                start.record(stream)
+                for k in range(steps):
+                    optimizer.fixed.copy_(batches[k % 4])
+                    optimizer.graph.replay()
+                stop.record(stream)
+                torch.cuda.synchronize()
+                ms = start.elapsed_time(stop) / steps
+                loss = float(optimizer.squares.double().mean())
+                out[kind + suffix] = {'ms_per_step': ms, 'pixels_per_s': 65536 / (ms / 1e3),
+                                      'params': model.grid.numel(), 'loss': loss}
             optimizer.close()
     out['batch'] = 65536
     out['steps'] = steps
-    out['note'] = ('graph replays of odie_step (router on), ids resident; the reference records 34.8 M px/s '
-                   '(packed planes) and 19.0 M px/s (hash grid) for this step on an RTX 3060')
+    out['note'] = ('graph replays of odie_step (router on), ids resident, stratified batches as the '
+                   "reference's configurations draw them (the *_uniform_ids lines: ids uniform over the "
+                   'image); the reference records 34.8 M px/s (packed planes) and 19.0 M px/s (hash grid) '
+                   'for this step on an RTX 3060')
     return out
 
 

@@ -316,14 +316,35 @@ __device__ inline void load_upstream(const Elem<HALF>* plane, int64_t at, float 
     for (int c = 0; c < F; ++c) us[c] = valid ? us[c] * scale : 0.0f;
 }
 
+// Offset of this thread's coordinate within each run of kOwnerBlock.  Hashed levels take the
+// thread index: one wave reads 64 consecutive coordinates, fully coalesced.  Dense levels have
+// few, large cells, and a spatially ordered batch (the stratified draw lists its strata row by
+// row) would put a whole wave on two or three of them, where its 64-bit LDS adds to one
+// address serialize.  There a wave takes 16 runs of 4 consecutive coordinates, 16 coordinates
+// apart, from a quarter of the block:
+//   offset = (wave / 4) * 256 + (wave % 4 + 4 * (lane / 4)) * 4 + lane % 4,
+// a permutation of [0, 1024) whose loads still come in 32-byte runs.  A 65536-id stratified
+// batch has 256 strata per row, so the wave's runs land 16 strata apart along a row.
+template <int KIND>
+__device__ inline int64_t lane_offset() {
+    static_assert(kOwnerBlock == 1024, "the spread order covers 16 waves");
+    if constexpr (KIND != kDense) {
+        return threadIdx.x;
+    } else {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        return (wave >> 2) * 256 + ((wave & 3) + 4 * (lane >> 2)) * 4 + (lane & 3);
+    }
+}
+
 // Every coordinate of [b0, b1) against one level: each thread takes kBatch coordinates per
-// iteration, strided by the block so every load is coalesced; loads are issued
-// unconditionally (clamped index) before any arithmetic.
+// iteration, kOwnerBlock apart, at lane_offset<KIND>() within each run; loads are issued
+// unconditionally (clamped index) before any arithmetic.  A thread stops once its first
+// coordinate is past b1: its later ones are too.
 template <int F, bool HALF, int KIND>
 __device__ inline void accumulate_level(const float* coords, const Elem<HALF>* plane, const DevLevel lv, int64_t b0,
                                         int64_t b1, uint32_t lo, uint32_t span, float scale,
                                         unsigned long long* acc) {
-    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBatch * kOwnerBlock) {
+    for (int64_t i = b0 + lane_offset<KIND>(); i < b1; i += kBatch * kOwnerBlock) {
         float2 xy[kBatch];
         float us[kBatch][F];
 #pragma unroll

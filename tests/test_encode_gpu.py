@@ -92,6 +92,39 @@ def test_owner_backward_is_deterministic():
     assert torch.equal(first, second)
 
 
+def test_owner_backward_is_order_independent():
+    """Coordinates in row bands, x ascending within a band (the order of a stratified draw), and
+    the same rows shuffled within each expert give the same fixed-point sums bit for bit: every
+    coordinate is added once whichever lane takes it (dense levels spread a wave over its block,
+    hashed levels take consecutive coordinates).  The upstream has one magnitude per level and
+    random signs, so every range (an expert's, or a split of one) bounds the same fixed-point
+    scale in both orders.  The banded order is also checked against the oracle."""
+    levels, entries = grid_levels(encoding(log2=14))
+    params, experts, per = entries * 2, 64, 4096
+    n = experts * per
+    xy = synth.coordinates(31, n)
+    rng = np.random.default_rng(31)
+    magnitude = 2.0 ** -(np.arange(32) // 2 % 4)
+    up = (np.where(rng.random((n, 32)) < 0.5, -1.0, 1.0) * magnitude).astype(np.float16)
+    banded, shuffled = [], []
+    for e in range(experts):
+        rows = np.arange(e * per, (e + 1) * per)
+        bands = np.floor(xy[rows, 1] * 64).astype(np.int64)
+        banded.append(rows[np.lexsort((xy[rows, 0], bands))])
+        shuffled.append(rng.permutation(rows))
+    offsets = np.arange(0, n + 1, per, dtype=np.int32)
+    d_off = torch.from_numpy(offsets).cuda()
+    grads = []
+    for order in (np.concatenate(banded), np.concatenate(shuffled)):
+        grads.append(grid_backward(torch.from_numpy(xy[order]).cuda(), torch.from_numpy(up[order]).cuda(), levels, 2,
+                                   offsets=d_off, experts=experts, expert_params=params))
+    assert torch.equal(grads[0], grads[1])
+    order = np.concatenate(banded)
+    expected, magnitude = oracle.hash_backward(xy[order], up[order], rows_of(levels), 2, experts * params,
+                                               offsets=offsets, expert_params=params)
+    check_gradient(grads[0], expected, magnitude, 'banded')
+
+
 @pytest.mark.parametrize('log2,experts,n', [(16, 64, 1 << 20), (14, 16, 300000), (12, 3, 5000)])
 def test_bucketed_owner_is_bit_identical(log2, experts, n):
     """The bucketed fine passes only skip coordinates whose corners miss the slice: with one
