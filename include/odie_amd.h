@@ -9,7 +9,13 @@
  *    odie_error() returns (thread-local, valid until the next failing call on the thread);
  *  - arguments are validated before any device work is queued, so a call that fails has
  *    queued nothing;
- *  - fp16 data is IEEE binary16 (uint16_t bit patterns on the host side).
+ *  - fp16 data is IEEE binary16 (uint16_t bit patterns on the host side);
+ *  - odie_grid_backward, odie_grid_backward_adam(_planes), odie_mlp_train(_planes),
+ *    odie_gate_backward and odie_step use one library-owned scratch buffer per device.  It
+ *    grows (hipMalloc) the first time a call needs more, and outgrown buffers are kept until
+ *    the process ends, so queued work and captured graphs keep valid addresses.  These calls
+ *    must not run concurrently on one device (queue them on one stream, or order the
+ *    streams), and a call at a new, larger size should run once before a graph captures it.
  */
 #ifndef ODIE_AMD_H
 #define ODIE_AMD_H
