@@ -148,7 +148,8 @@ int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstrea
  *   (y*W + x, with y clamped as above) of slot j, read from the RGB8 image rgb [H*W][3] --
  *   the training target of the slot, gathered in slot order so each tile's bytes are read
  *   through one L2.
- * workspace: caller-owned device scratch of odie_route_workspace(n, E) bytes.
+ * workspace: caller-owned device scratch of odie_route_workspace(n, E) bytes (-1 for n outside
+ *   [0, 2^31-1] or E outside [1, 4096]).
  * --------------------------------------------------------------------------------------- */
 int64_t odie_route_workspace(int64_t n, int experts);
 

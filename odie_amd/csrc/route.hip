@@ -387,7 +387,7 @@ int64_t scan_blocks(int64_t n, int experts) {
 }
 
 ODIE_API int64_t odie_route_workspace(int64_t n, int experts) {
-    if (n < 0 || experts < 1) return -1;
+    if (n < 0 || n > (int64_t{1} << 31) - 1 || experts < 1 || experts > kMaxExperts) return -1;
     int part, parts;
     route_plan(n, experts, part, parts);
     const int64_t counts = (static_cast<int64_t>(experts) * parts * 4 + 255) / 256 * 256;

@@ -86,6 +86,9 @@ def test_route_rejects_bad_arguments(native):
     assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, None, None, 8, 4, 0) == -1
     assert 'workspace' in native.odie_error().decode()
     assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4 + 256 * 4
+    assert native.odie_route_workspace(1 << 24, 4096) > 0
+    for n, experts in ((5, 4097), (5, 0), (-1, 4), (1 << 31, 4)):   # outside [0, 2^31-1] x [1, 64*64]
+        assert native.odie_route_workspace(n, experts) == -1
 
 
 def test_selection_entry_points_reject_bad_arguments(native):
