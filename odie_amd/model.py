@@ -268,3 +268,91 @@ class PackedPlanes:
             raise ValueError('Coordinates must be FP32 Nx2, without coordinate gradients')
         return PackedQuery.apply(coordinates.contiguous(), self.grid, self.descriptors, self.node_bitmap,
                                  self.node_prefix, self.bitmap, self.input_width)
+
+
+# tiny-cuda-nn's seeds for the two heads (odie/model.py:191-193)
+GATE_SEED, DECODER_SEED = 2000003, 4000037
+
+
+class PackedXYPlanes(PackedPlanes):
+    """The on-demand model (odie/model.py:154-262): the packed planes with the router gate and the
+    decoder (Gate / Decoder, fp32 masters in `params`), 2 features per level (the width this
+    library's heads and runtime are built for).  forward(coordinates) is the reference's
+    evaluation path (odie/model.py:266-279): query, mask the levels past the active prefix, gate
+    by level with visibility, decode, first 3 outputs as fp32; it runs without autograd, training
+    goes through NativeOptimizer."""
+
+    def __init__(self, config, supports, plane_dims, plane_node_caps, axis_mode='none', kernel_a=0.,
+                 kernel_omega=1.5 * np.pi, device='cuda'):
+        if axis_mode != 'none' or kernel_a != 0.:
+            raise ValueError('No axis branches or non-linear interpolation kernel in this ablation')
+        if any(int(dim) != 2 for dim in plane_dims):
+            raise ValueError('PackedXYPlanes runs 2 features per level')
+        super().__init__(config, supports, plane_dims, plane_node_caps, device=device)
+        from .decoder import Decoder, PARAMETERS as DECODER_PARAMETERS
+        from .gate import Gate, PARAMETERS as GATE_PARAMETERS
+        self.router_enabled = bool(config.get('router_enabled', True))
+        self.gate_coarse_levels_K = gate_coarse_levels(config)
+        seed = int(config['seed'])
+        if ((GATE_PARAMETERS if self.router_enabled else 0) != config['gate_parameters'] or
+                DECODER_PARAMETERS != config['decoder_parameters']):
+            raise RuntimeError('Unexpected TCNN head allocation for the configured input width')
+        self.gate = (Gate(seed=(seed + GATE_SEED) % 2 ** 31, coarse=self.gate_coarse_levels_K,
+                          activation=config.get('router_output_activation', 'sigmoid'), device=device)
+                     if self.router_enabled else None)
+        self.decoder = Decoder(seed=(seed + DECODER_SEED) % 2 ** 31, device=device)
+
+    def forward(self, coordinates):
+        with torch.no_grad():
+            raw, visible = self.query_features(coordinates)
+            level = torch.arange(self.n_levels, device=raw.device)
+            active = level < self.active_prefix
+            raw = raw * active.repeat_interleave(2).to(raw.dtype)
+            self.decoder.sync_weights()
+            if self.gate is None:
+                return self.decoder.forward(raw).float()[:, :3]
+            self.gate.sync_weights()
+            # levels at or below K keep a gate of one; a prefix within them gates nothing else
+            weighted, _ = self.gate.forward(raw, visible=(visible & active).to(torch.uint8).contiguous())
+            return self.decoder.forward(weighted).float()[:, :3]
+
+    __call__ = forward
+
+    def storage_stats(self):
+        grid = self.grid.numel()
+        gate = self.gate.params.numel() if self.gate is not None else 0
+        heads = gate + self.decoder.params.numel()
+        size = lambda t: t.numel() * t.element_size()
+        node_bitmaps, prefixes, bitmaps = size(self.node_bitmap), size(self.node_prefix), size(self.bitmap)
+        descriptors = size(self.descriptors)
+        gate_index = self.input_width * 8                     # the int64 feature -> level index
+        active_flags = self.n_levels + 2 * self.input_width   # bool per level, fp16 per feature
+        return {'actual_params': grid + heads, 'grid_params': grid, 'head_params': heads,
+                'gate_params': gate, 'decoder_params': self.decoder.params.numel(),
+                'router_enabled': self.router_enabled, 'axis_params': 0, 'plane_params': grid,
+                'plane_caps': self.plane_node_caps, 'fp16_parameter_payload_bytes': 2 * (grid + heads),
+                'fp32_master_bytes': 4 * (grid + heads), 'adam_moment_bytes': 8 * (grid + heads),
+                'full_gradient_bytes': 4 * (grid + heads), 'index_bytes': node_bitmaps + prefixes,
+                'node_bitmap_bytes': node_bitmaps, 'node_prefix_bytes': prefixes, 'bitmap_bytes': bitmaps,
+                'descriptor_bytes': descriptors,
+                'runtime_index_bytes': node_bitmaps + prefixes + bitmaps + descriptors + gate_index + active_flags,
+                'active_flag_bytes': active_flags, 'input_width': self.input_width,
+                'native_input_padding': (self.input_width + 15) // 16 * 16, 'axis_mode': 'none',
+                'active_layers_from_update1': int(self.config.get('initial_active_prefix', 2)),
+                'active_prefix': self.active_prefix, 'gate_coarse_levels_K': self.gate_coarse_levels_K,
+                'full_cover_coarse_layers': self.config.get('full_cover_coarse_layers', [0, 1]),
+                'plane_dims': self.plane_dims,
+                'coordinate_version': COORDINATE_VERSION, 'layout_version': LAYOUT_VERSION,
+                'addressing_version': ADDRESSING_VERSION, 'query_cuda_launches': 1, 'backward_cuda_launches': 1,
+                'forward_precision': 'P01 FP32 geometry and FP16 interpolation chain',
+                'gradient_precision': 'FP16 feature gradient, FP32 interpolation weights and atomicAdd',
+                'levels': [{key: value for key, value in level.items() if key != 'nodes'}
+                           for level in self.layout['levels']]}
+
+
+def build_model(config, supports, plane_dims, plane_node_caps, **kwargs):
+    """The model of config['representation'] (odie/model.py:318-321)."""
+    if config['representation'] == 'hash_grid':
+        from .hash_grid import HashGrid
+        return HashGrid(config, supports, plane_dims, plane_node_caps)
+    return PackedXYPlanes(config, supports, plane_dims, plane_node_caps, **kwargs)
