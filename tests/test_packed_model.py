@@ -90,3 +90,29 @@ def test_packed_model_forward_follows_the_reference_gating(router, coarse, prefi
         full = PackedXYPlanes(_config(router, coarse), supports, dims, caps)
         full.set_active_prefix(16)
         assert not torch.equal(rgb, full.forward(xy))
+
+
+@pytest.mark.gpu
+def test_native_optimizer_trains_a_packed_model():
+    """NativeOptimizer takes PackedXYPlanes itself (its grid, addressing buffers, layout, prefix
+    and heads): steps move the grid and both heads, and forward sees the new weights."""
+    from odie_amd.native_backend import make_native_optimizer
+    width, height = 97, 61
+    supports, dims, caps = _inputs(4)
+    config = dict(_config(router=True), target_storage='uint8', plane_feature_dimensions=dims, grid_lr=1e-2,
+                  gate_lr=1e-3, decoder_lr=1e-3)
+    model = PackedXYPlanes(config, supports, dims, caps)
+    model.set_active_prefix(16)
+    image = torch.from_numpy(synth.image(8, width, height)).cuda().contiguous()
+    xy = torch.from_numpy(synth.coordinates(8, 777)).cuda()
+    before = model.forward(xy)
+    grid, decoder, gate = model.grid.clone(), model.decoder.params.clone(), model.gate.params.clone()
+    opt, _ = make_native_optimizer(model, image, (height, width), config)
+    for step in range(3):
+        opt.step_raw(torch.from_numpy(synth.integers(step, 'packed_model_ids', 4096, width * height)).cuda())
+    torch.cuda.synchronize()
+    opt.close()
+    assert not torch.equal(model.grid, grid)
+    assert not torch.equal(model.decoder.params, decoder)
+    assert not torch.equal(model.gate.params, gate)
+    assert not torch.equal(model.forward(xy), before)
