@@ -16,7 +16,7 @@ import torch
 
 from . import synth
 from .config import grid_levels
-from .decoder import Decoder, PARAMETERS as DECODER_PARAMETERS
+from .decoder import Decoder, LEVELS, PARAMETERS as DECODER_PARAMETERS
 from .encoding import grid_forward
 from .gate import Gate, PARAMETERS as GATE_PARAMETERS
 
@@ -36,8 +36,9 @@ class HashGrid:
         self.plane_dims, self.plane_node_caps = list(plane_dims), list(plane_node_caps)
         self.supports = []
         encoding = config['hash_encoding']
-        if int(encoding.get('n_features_per_level', 2)) != 2 or self.input_width != 2 * self.n_levels:
-            raise ValueError('HashGrid runs 2 features per level')
+        if (int(encoding.get('n_features_per_level', 2)) != 2 or self.n_levels != LEVELS or
+                list(plane_dims) != [2] * LEVELS):
+            raise ValueError('HashGrid runs %d levels of 2 features (the width of the heads)' % LEVELS)
         self.levels, entries = grid_levels(encoding)
         offset, levels = 0, []
         for dim, cap in zip(plane_dims, plane_node_caps):
@@ -88,6 +89,7 @@ class HashGrid:
                     active_layers_from_update1=self.n_levels, active_prefix=self.n_levels,
                     full_cover_coarse_layers=list(range(self.n_levels)), plane_dims=self.plane_dims,
                     coordinate_version='unit-endpoints-v1', layout_version='official-tcnn-hash-grid-v1',
-                    addressing_version='official-tcnn-hash-grid', initialization='official TCNN',
+                    addressing_version='official-tcnn-hash-grid',
+                    initialization='TCNN distributions from a counter PRNG (grid uniform +-1e-4)',
                     levels=[dict(level=i, resolution=r, **item) for i, (r, item) in
                             enumerate(zip(self.config['resolutions'], self.layout['levels']))])

@@ -276,7 +276,7 @@ GATE_SEED, DECODER_SEED = 2000003, 4000037
 
 class PackedXYPlanes(PackedPlanes):
     """The on-demand model (odie/model.py:154-262): the packed planes with the router gate and the
-    decoder (Gate / Decoder, fp32 masters in `params`), 2 features per level (the width this
+    decoder (Gate / Decoder, fp32 masters in `params`), 16 levels of 2 features (the width this
     library's heads and runtime are built for).  forward(coordinates) is the reference's
     evaluation path (odie/model.py:266-279): query, mask the levels past the active prefix, gate
     by level with visibility, decode, first 3 outputs as fp32; it runs without autograd, training
@@ -286,10 +286,10 @@ class PackedXYPlanes(PackedPlanes):
                  kernel_omega=1.5 * np.pi, device='cuda'):
         if axis_mode != 'none' or kernel_a != 0.:
             raise ValueError('No axis branches or non-linear interpolation kernel in this ablation')
-        if any(int(dim) != 2 for dim in plane_dims):
-            raise ValueError('PackedXYPlanes runs 2 features per level')
+        from .decoder import Decoder, LEVELS, PARAMETERS as DECODER_PARAMETERS
+        if list(plane_dims) != [2] * LEVELS or int(config['n_levels']) != LEVELS:
+            raise ValueError('PackedXYPlanes runs %d levels of 2 features (the width of the heads)' % LEVELS)
         super().__init__(config, supports, plane_dims, plane_node_caps, device=device)
-        from .decoder import Decoder, PARAMETERS as DECODER_PARAMETERS
         from .gate import Gate, PARAMETERS as GATE_PARAMETERS
         self.router_enabled = bool(config.get('router_enabled', True))
         self.gate_coarse_levels_K = gate_coarse_levels(config)

@@ -39,6 +39,11 @@ def test_hash_grid_refuses_what_the_reference_refuses(changes, supports, error, 
         HashGrid(_config(**changes), supports, [2] * 16, _caps(), device='cpu')
 
 
+def test_hash_grid_refuses_other_widths():
+    with pytest.raises(ValueError, match='levels of 2 features'):
+        HashGrid(_config(), [], [2] * 15 + [1], _caps(), device='cpu')
+
+
 def test_hash_grid_refuses_a_table_that_differs_from_the_caps():
     caps = _caps()
     caps[-1] += 8

@@ -46,7 +46,7 @@ def test_packed_model_refuses_what_the_reference_refuses(changes, kwargs, error,
 
 def test_packed_model_refuses_other_feature_widths():
     supports, dims, caps = _inputs(1)
-    with pytest.raises(ValueError, match='2 features'):
+    with pytest.raises(ValueError, match='levels of 2 features'):
         PackedXYPlanes(_config(), supports, [1] + dims[1:], caps, device='cpu')
 
 
