@@ -205,7 +205,7 @@ int selection_chunk(const double* scores, int n, int points, int resolution, int
 /* ---------------------------------------------------------------------------------------
  * Fused Adam over n parameters: master fp32 (updated), half_copy fp16 (nullable; receives
  * fp16(master) in the same pass), grad fp32 or fp16 carrying loss_scale, moments m, v fp32.
- * variant 0: torch.optim.Adam with global step `step` (odie/optimizer.py:324,365).
+ * variant 0: torch.optim.Adam with global step `step` (odie/optimizer.py:33-44,77-84).
  * variant 1: per-parameter ages in steps (uint32 [n]); zero gradients skip the update and keep
  * the age (the grid optimizer of odie/native/runtime.cu:212-215, odie/train.py:121-124).
  * variant 2: per-parameter ages without the zero-gradient skip (the head optimizers of

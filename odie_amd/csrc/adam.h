@@ -1,8 +1,8 @@
 // Adam update of one parameter, shared by the standalone optimizer kernel and the encode
 // backward's fused flush so that both give the same bits for the same gradient.
 //
-// variant 0 (torch.optim.Adam as configured at odie/optimizer.py:324, gradients divided by
-//   the loss scale first, odie/optimizer.py:365), with t the global step:
+// variant 0 (torch.optim.Adam as configured at odie/optimizer.py:33-44, gradients divided by
+//   the loss scale first, odie/optimizer.py:77-84), with t the global step:
 //     m = b1*m + (1-b1)*g;  v = b2*v + (1-b2)*g^2;
 //     p -= lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps)
 // variant 1 (the tiny-cuda-nn Adam the reference's native runtime uses for the grid,

@@ -2,7 +2,7 @@
 
 FusedAdam keeps the moments (and, for the per-parameter-age variant, the ages) next to one
 flat fp32 master buffer and updates it -- and an optional fp16 copy -- in one pass per step.
-variant 'torch' follows torch.optim.Adam (odie/optimizer.py:324); variant 'tcnn' skips zero
+variant 'torch' follows torch.optim.Adam (odie/optimizer.py:33-44); variant 'tcnn' skips zero
 gradients and keeps per-parameter ages (the grid, odie/native/runtime.cu:212-215); variant
 'tcnn_dense' keeps per-parameter ages without the skip (the MLP heads, :159-160).
 """

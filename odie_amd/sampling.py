@@ -1,4 +1,4 @@
-"""Pixel sampling for the training step (odie/data.py:47-107): the same batch generators, with
+"""Pixel sampling for the training step (odie/data.py:47-106): the same batch generators, with
 the stratified draw's id arithmetic on the GPU (odie_stratified_ids).
 
 The uniforms come from torch.rand on the caller's generator, as in the reference; the ids of a
@@ -45,7 +45,7 @@ def full_batches(pixels, batch, generator, device='cuda'):
 
 
 def shuffled_batches(pixels, batch, generator, mode='global', chunk=4194304, device='cuda', shape=None):
-    """The reference's sampling modes (odie/data.py:83-107)."""
+    """The reference's sampling modes (odie/data.py:83-106)."""
     if mode == 'global_full':
         yield from full_batches(pixels, batch, generator, device)
     elif mode == 'stratified':

@@ -413,7 +413,7 @@ API void ora_residual(const float* prediction, const void* target, int rgb8, int
 /* ------------------------------------------------------------------------------
  * Adam, in double (the HIP update runs in fp32 and is compared with a tolerance).
  * variant 0, torch-style: torch.optim.Adam(betas, eps, weight_decay=0) as configured at
- *   odie/optimizer.py:324, gradient divided by the loss scale first (:365):
+ *   odie/optimizer.py:33-44, gradient divided by the loss scale first (:77-84):
  *   m = b1*m + (1-b1)*g; v = b2*v + (1-b2)*g^2;
  *   p -= lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps), t = the global step.
  * variant 1, tiny-cuda-nn style (odie/native/runtime.cu:212-215, documented at

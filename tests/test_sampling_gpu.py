@@ -1,6 +1,6 @@
 """Stratified sampling on the GPU (odie_stratified_ids) against the oracle's restatement of
 odie/data.py:73-80, bit for bit, on torch.rand draws and on edge draws; the batch generators'
-contracts (odie/data.py:47-107)."""
+contracts (odie/data.py:47-106)."""
 import numpy as np
 import pytest
 import torch
