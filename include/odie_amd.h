@@ -157,6 +157,21 @@ int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions
                int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
                uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream);
 
+/* odie_route without the workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  It allocates nothing: its scratch is a static device array of
+ * ODIE_ROUTE_NOALLOC_BYTES (4 MiB + 64 KiB) that every GPU the library runs on holds until the
+ * process ends, resolved once per device.  Calls whose odie_route_workspace(n, E) exceeds it
+ * fail (-1, nothing queued): up to 2^24 ids over 64 experts, 2^22 over 256 and 2^18 over
+ * 4096 fit.  Every call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (different streams without ordering, or several host threads) race and give wrong results.
+ * Same outputs as odie_route, bit for bit. */
+#define ODIE_ROUTE_NOALLOC_BYTES ((int64_t)((4 << 20) + (64 << 10)))
+
+int odie_route_noalloc(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
+                       int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+                       uint32_t* colors, uint64_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * Residual pass.  Same name, signature and meaning as the reference's score_chunk
  * (odie/residual_cuda.cu:45-52): pixels [begin, end) of a width-wide image in raster order;

@@ -17,6 +17,10 @@
 //           their order from a ballot over the wave (peel loop, one iteration per distinct
 //           expert in the group), and a per-wave running count in LDS carries the order
 //           across groups.  No global atomics, so the result is deterministic.
+#include <map>
+#include <mutex>
+#include <string>
+
 #include "common.h"
 #include "tiles.h"
 #include "../../include/odie_amd.h"
@@ -394,9 +398,12 @@ ODIE_API int64_t odie_route_workspace(int64_t n, int experts) {
     return counts + scan_blocks(n, experts) * 4;
 }
 
-ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
-                        int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
-                        uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream) {
+namespace odie {
+namespace {
+
+// Checks the arguments common to odie_route and odie_route_noalloc (nothing is queued).
+int route_check(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y, int32_t* perm,
+                float* coords, int32_t* offsets, const uint8_t* rgb, uint32_t* colors) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_route: n must be within [0, 2^31-1]");
     if (regions_x < 1 || regions_y < 1 || regions_x > kMaxRegions || regions_y > kMaxRegions)
         return fail("odie_route: regions per axis must be within 1..64");
@@ -404,14 +411,19 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
         return fail("odie_route: every tile needs at least two pixels per axis");
     if (static_cast<uint64_t>(width) * static_cast<uint64_t>(height) > (uint64_t{1} << 32))
         return fail("odie_route: images are limited to 2^32 pixels (32-bit pixel ids)");
-    const int experts = regions_x * regions_y;
     if (!offsets) return fail("odie_route: offsets is null");
-    const int64_t need = odie_route_workspace(n, experts);
     if (n > 0 && (!ids || !perm || !coords)) return fail("odie_route: ids, perm and coords must be non-null");
     if ((rgb == nullptr) != (colors == nullptr)) return fail("odie_route: rgb and colors go together");
-    if (n > 0 && (!workspace || workspace_bytes < need))
-        return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_route: coords must be 8-byte aligned");
+    return 0;
+}
+
+// Queues the route on `stream` with `workspace` (odie_route_workspace(n, E) bytes, checked by
+// the caller) as its scratch.
+int route_launch(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
+                 int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+                 uint32_t* colors, void* workspace, uint64_t stream) {
+    const int experts = regions_x * regions_y;
     RouteArgs a{};
     a.ids = ids;
     a.expert_out = expert;
@@ -470,4 +482,59 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
         route_colors_kernel<<<chunks, kRouteBlock, 0, s>>>(rgb, colors, n);
     }
     return check_launch("odie_route");
+}
+
+// Scratch of odie_route_noalloc: one copy per device, held until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in for the device
+// variable); it uses the per-device address from hipGetSymbolAddress.
+constexpr int64_t kRouteScratchBytes = ODIE_ROUTE_NOALLOC_BYTES;
+static __device__ __align__(256) uint8_t scratch[kRouteScratchBytes];
+
+void* scratch_address() {
+    static std::mutex lock;
+    static std::map<int, void*> addresses;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        fail("odie_route_noalloc: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(lock);
+    auto found = addresses.find(device);
+    if (found != addresses.end()) return found->second;
+    void* address = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (status != hipSuccess || !address) {
+        fail(std::string("odie_route_noalloc: hipGetSymbolAddress failed: ") + hipGetErrorString(status));
+        return nullptr;
+    }
+    addresses[device] = address;
+    return address;
+}
+
+}  // namespace
+}  // namespace odie
+
+ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
+                        int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+                        uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream) {
+    if (route_check(ids, n, width, height, regions_x, regions_y, perm, coords, offsets, rgb, colors)) return -1;
+    if (n > 0 && (!workspace || workspace_bytes < odie_route_workspace(n, regions_x * regions_y)))
+        return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
+    return route_launch(ids, n, width, height, regions_x, regions_y, expert, perm, coords, offsets, rgb, colors,
+                        workspace, stream);
+}
+
+ODIE_API int odie_route_noalloc(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
+                                int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+                                uint32_t* colors, uint64_t stream) {
+    if (route_check(ids, n, width, height, regions_x, regions_y, perm, coords, offsets, rgb, colors)) return -1;
+    const int64_t need = odie_route_workspace(n, regions_x * regions_y);
+    if (need > kRouteScratchBytes)
+        return fail("odie_route_noalloc: " + std::to_string(n) + " ids over " + std::to_string(regions_x * regions_y) +
+                    " experts need " + std::to_string(need) + " bytes of scratch, more than its " +
+                    std::to_string(kRouteScratchBytes) + "; use odie_route with a workspace");
+    void* space = scratch_address();
+    if (!space) return -1;
+    return route_launch(ids, n, width, height, regions_x, regions_y, expert, perm, coords, offsets, rgb, colors, space,
+                        stream);
 }
