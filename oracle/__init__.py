@@ -42,6 +42,11 @@ PINS = {
     'gate': 'recorded gates of the reference (tests/golden/gate_support_sample.npz: effective = fp16(s*visible)); '
             'torch.sigmoid / softplus; exact fp16 arithmetic of parallel_gate_back checked by fractions; autograd '
             'of the gate MLP',
+    'route': 'per-pixel brute force over whole small non-square images: tile found by searching the integer '
+             'bounds ceil(r*size/regions), local coordinate as the exactly rounded fp32 product (fractions), '
+             'stable order of a Python sort, clamped and wrapped ids',
+    'gate_upstream': 'exact rational arithmetic (fractions) with planted subnormal quotients, ties, overflow and '
+                     'signed zeros',
     'stratified_ids': 'exact rational arithmetic: each pixel lies in its stratum\'s pixel interval, u = 0 gives '
                       'floor(stratum * size / side), u -> 1 stays below the next stratum; axes distinguished on '
                       'non-square images',

@@ -644,3 +644,104 @@ def test_stratified_ids_follow_the_strata(oracle):
                 low = math.floor(Fraction(s * size, side))
                 high = min(math.ceil(Fraction((s + 1) * size, side)), size - 1)
                 assert low <= value <= high, (width, height, batch, j)
+
+
+# Routing of pixel ids to tile experts --------------------------------------------------------
+
+def _exact_f32(value):
+    """Correctly rounded fp32 of a Fraction (ties to even), as a numpy float32."""
+    return np.float32(float(round_fraction(value, SINGLE)))
+
+
+@pytest.mark.parametrize('width,height,regions_x,regions_y', [
+    (23, 17, 3, 5),        # non-square image, different tile counts per axis, ragged tiles
+    (64, 9, 8, 2),         # tiles of exactly 8 x 4.5 pixels
+    (41 * 2 + 2, 13, 2, 1),  # tile width 42: (w-1) * fp32(1/(w-1)) rounds below 1 in fp32
+    (7, 5, 2, 2),
+])
+def test_route_against_per_pixel_brute_force(oracle, width, height, regions_x, regions_y):
+    """oracle.route against a brute force over every pixel of the image (and ids past it):
+    the tile of a pixel is found by searching the integer bounds ceil(r * size / regions)
+    (exact rationals), not by the oracle's floor(x * regions / size); every pixel lies in
+    exactly one tile; the local coordinate is the exactly rounded fp32 product
+    fp32(x - x0) * fp32(1 / (tile - 1)) of the reference's pixel -> coordinate convention
+    (odie/native/runtime.cu:34-36), so 0 at a tile's first pixel, monotone across the tile, and
+    within one ulp below 1 at its last (exactly 1 where fp32 allows); x and y are not swapped;
+    ids past the image clamp to its last row, ids beyond 2^32 wrap as the 32-bit id does; the
+    order is the stable ascending-expert order of a Python sort."""
+    def bounds(size, regions):
+        return [math.ceil(Fraction(r * size, regions)) for r in range(regions + 1)]
+    xb, yb = bounds(width, regions_x), bounds(height, regions_y)
+    pixels = width * height
+    ids = np.concatenate([np.arange(pixels), pixels + np.arange(3 * width),
+                          (1 << 32) + np.arange(5), np.arange(pixels)[::-7]]).astype(np.int64)
+    expert, perm, local, offsets = oracle.route(ids, width, height, regions_x, regions_y)
+    expected_expert, expected_uv = [], []
+    for raw in ids.tolist():
+        pixel = raw % (1 << 32)
+        x, y = pixel % width, min(pixel // width, height - 1)
+        rx = [r for r in range(regions_x) if xb[r] <= x < xb[r + 1]]
+        ry = [r for r in range(regions_y) if yb[r] <= y < yb[r + 1]]
+        assert len(rx) == 1 and len(ry) == 1
+        rx, ry = rx[0], ry[0]
+        expected_expert.append(ry * regions_x + rx)
+        u = _exact_f32(Fraction(x - xb[rx]) * Fraction(float(_exact_f32(Fraction(1, xb[rx + 1] - xb[rx] - 1)))))
+        v = _exact_f32(Fraction(y - yb[ry]) * Fraction(float(_exact_f32(Fraction(1, yb[ry + 1] - yb[ry] - 1)))))
+        expected_uv.append((u, v))
+    assert expert.tolist() == expected_expert
+    order = sorted(range(len(ids)), key=lambda i: expected_expert[i])
+    assert list(perm) == order
+    uv = np.array(expected_uv, dtype=np.float32)[order]
+    assert np.array_equal(local.view(np.uint32), uv.view(np.uint32))
+    counts = [expected_expert.count(e) for e in range(regions_x * regions_y)]
+    assert list(offsets) == [sum(counts[:e]) for e in range(regions_x * regions_y + 1)]
+    # the geometry of each tile: first pixel 0, last pixel 1 or one ulp below, increasing
+    slot_of = {int(ids[j]): k for k, j in enumerate(perm) if ids[j] < pixels}
+    for ry in range(regions_y):
+        for rx in range(regions_x):
+            row = [local[slot_of[yb[ry] * width + x]][0] for x in range(xb[rx], xb[rx + 1])]
+            column = [local[slot_of[y * width + xb[rx]]][1] for y in range(yb[ry], yb[ry + 1])]
+            for values in (row, column):
+                assert values[0] == 0.0
+                assert 1.0 - 2.0 ** -24 <= values[-1] <= 1.0
+                assert all(a < b for a, b in zip(values, values[1:]))
+    last = np.float32(41.0) * np.float32(1.0 / 41.0)
+    assert last == np.float32(1.0) - np.float32(2.0 ** -24)   # the rounding the third case exercises
+
+
+def test_gate_upstream_matches_exact_rational_arithmetic(oracle):
+    """hash_router_gradient (odie/native/runtime.cu:99-103) in exact arithmetic: the router's input
+    gradient is divided by 128 in fp32 (exact: a power of two inside the fp32 range), rounded once
+    to fp16 (which loses bits only where the quotient falls below fp16's normal range), then added
+    to the direct gradient with one fp16 rounding.  The planted values hit fp16 subnormal
+    quotients, ties to even in the sum, overflow to infinity and signed zeros, so dropping the
+    intermediate rounding, scaling by another power of two or adding before the division fails."""
+    rng = np.random.default_rng(77)
+    direct = (rng.normal(size=4000) * rng.choice([1e-6, 1e-3, 1.0, 300.0], size=4000)).astype(np.float16)
+    dr = np.clip(rng.normal(size=4000) * rng.choice([1e-3, 1.0, 1e3, 6e4], size=4000), -65504, 65504)
+    dr = dr.astype(np.float16)
+    planted_direct = np.array([0.0, -0.0, -0.0, 65504.0, 2.0 ** -14, 1.0, 2.0 ** -24, 0.0], dtype=np.float16)
+    planted_dr = np.array([-0.0, -0.0, 0.0, 60000.0, 3 * 2.0 ** -17, 2.0 ** -4, 1.5 * 2.0 ** -17, 2.0 ** -10],
+                          dtype=np.float16)
+    direct = np.concatenate([direct, planted_direct])
+    dr = np.concatenate([dr, planted_dr])
+    with np.errstate(over='ignore'):
+        out = oracle.gate_upstream(direct, dr)
+    for a, b, got in zip(direct.tolist(), dr.tolist(), out):
+        unscaled = round_fraction(Fraction(b) / 128, HALF)
+        if unscaled == 0 and (b < 0 or (b == 0 and math.copysign(1.0, b) < 0)):
+            unscaled_sign = -1.0
+        else:
+            unscaled_sign = 1.0 if unscaled >= 0 else -1.0
+        total = Fraction(a) + Fraction(unscaled)
+        expected = round_fraction(total, HALF)
+        bits = int(np.array([got], dtype=np.float16).view(np.uint16)[0])
+        if isinstance(expected, float):                       # overflow
+            assert bits == to_half_bits(expected)
+        elif expected == 0:
+            # IEEE: the sum of two zeros of the same sign keeps it, otherwise +0
+            negative = math.copysign(1.0, a) < 0 and unscaled_sign < 0 and Fraction(a) == 0
+            assert bits == (0x8000 if negative else 0x0000), (a, b)
+        else:
+            assert Fraction(float(np.float16(got))) == expected, (a, b)
+    assert np.isinf(out[-5]) and out[-5] > 0            # 65504 + 468.75 overflows
