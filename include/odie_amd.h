@@ -185,6 +185,13 @@ int score_chunk(const float* prediction, const void* target, int64_t begin, int6
                 int resolution, int first_y, int active_cells, const int* xb, const int* yb,
                 double* totals, bool rgb8, uint64_t stream);
 
+/* Bounds of the residual's native geometry cells (the pixel -> cell map of odie/selection.py:44-55,
+ * odie/gpu_residual.py:49-62): pixel column p has x = fp32(p) / fp32(width - 1) and the cell column
+ * floor(fmaf(R - 1, x, 0.5)); xb[c] (device int32 [R+1]) is the first column of cell column c and
+ * xb[R] = width; yb likewise over rows.  No counterpart entry point in the reference (its host
+ * computes the fp32 thresholds of the same map). */
+int odie_cell_bounds(int width, int height, int resolution, int32_t* xb, int32_t* yb, uint64_t stream);
+
 /* Top-k cells by score: ids (device int32 [k]) of the k largest scores (fp64 [n], >= 0), ties to
  * the lower id, written in ascending id order.  Ranking rule of select_mean_rank
  * (odie/selection.py:103,116) with the sign-cleared FP64 key of the GPU selector
@@ -232,12 +239,14 @@ int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int gra
                    float eps, float loss_scale, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
- * Decoder MLP 32 -> 64 -> 64 -> 16 (ReLU hidden layers, no bias, no output activation), fp16
+ * Decoder MLP width -> 64 -> 64 -> 16 (ReLU hidden layers, no bias, no output activation), fp16
  * weights and activations, fp32 accumulation: the decoder head of the reference (TCNN
- * FullyFusedMLP, odie/hash_grid.py:32-34, forward/backward at odie/native/runtime.cu:270,273).
- * weights fp16 [7168] = W1 [64][32] | W2 [64][64] | W3 [16][64], row-major [out][in].
+ * FullyFusedMLP with n_input_dims W = align16(sum of the grid's features), odie/hash_grid.py:32-34,
+ * odie/native/runtime.cu:17,151-162,190; forward/backward at odie/native/runtime.cu:270,273).
+ * width: 16, 32, 48, 64 or 80.  weights fp16 [64*width + 5120] = W1 [64][width] | W2 [64][64] |
+ * W3 [16][64], row-major [out][in] (7168 at width 32).
  *
- * odie_mlp_forward: out fp16 [n][16] = decoder(x fp16 [n][32]).
+ * odie_mlp_forward: out fp16 [n][16] = decoder(x fp16 [n][width]).
  *
  * odie_mlp_train: forward, the step's loss (loss_grad, odie/native/runtime.cu:53-63) and
  * backward in one pass.  Tile row j reads x[j]; its input row is i = rows[j] (rows null:
@@ -245,20 +254,22 @@ int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int gra
  * (colors: uint32 [n] packed as odie_route writes them); rgb[3*ids[i] + c] * (1/255);
  * target[3*i + c] (fp32).
  * dy_c = fp16(fp16(2*d_c/(3*real)*128)*128) for c < 3 (zero for i >= real), d = y - t.
- * Writes dz fp16 [n][32] = fp16(fp16(dL/dx * 16384) / 128) at row j (the grid's upstream,
- * half_unscale at odie/native/runtime.cu:282), dweights fp32 [7168] = dL/dW * 16384
+ * Writes dz fp16 [n][width] = fp16(fp16(dL/dx * 16384) / 128) at row j (the grid's upstream,
+ * half_unscale at odie/native/runtime.cu:282), dweights fp32 [64*width + 5120] = dL/dW * 16384
  * (overwritten; deterministic), and, where non-null, out fp16 [.][16] and squares fp32 [.] at
  * input row i (squares = sum_c d_c^2 / 3), hidden fp16 [n][128] = (h1 | h2) at row j.
- * x must be 16-byte aligned, dz and out 8-byte aligned.
+ * x must be 16-byte aligned, dz and out 8-byte aligned; n * width < 2^31.
  * --------------------------------------------------------------------------------------- */
-int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weights, uint16_t* out, uint64_t stream);
+int odie_mlp_forward(const uint16_t* x, int64_t n, int width, const uint16_t* weights, uint16_t* out,
+                     uint64_t stream);
 
-int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights, const uint32_t* colors,
-                   const uint8_t* rgb, const int64_t* ids, const float* target, const int32_t* rows, uint16_t* out,
-                   uint16_t* hidden, float* squares, uint16_t* dz, float* dweights, uint64_t stream);
+int odie_mlp_train(const uint16_t* x, int64_t n, int width, int64_t real, const uint16_t* weights,
+                   const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
+                   const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz,
+                   float* dweights, uint64_t stream);
 
-/* odie_mlp_train with dz written in the layout odie_grid_backward_adam_planes reads instead of
- * rows: planes uint32 [16][n] (plane l, row j = the fp16 pair of columns 2l, 2l+1 of dz row j)
+/* odie_mlp_train at width 32 (16 levels x 2 features) with dz written in the layout
+ * odie_grid_backward_adam_planes reads instead of rows: planes uint32 [16][n] (plane l, row j = the fp16 pair of columns 2l, 2l+1 of dz row j)
  * and blockmax fp32 [ceil(n/128)][16] (record r, level l = max |dz| over rows 128r..128r+127
  * and both features of level l; NaN if any of them is NaN).  Same values as odie_mlp_train's
  * dz, bit for bit.  No counterpart in the reference: it saves the encode backward's transposition
@@ -269,25 +280,31 @@ int odie_mlp_train_planes(const uint16_t* x, int64_t n, int64_t real, const uint
                           float* blockmax, float* dweights, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
- * Router gate (router_enabled) of the hash-grid model: gate MLP 32 -> 32 -> 16 (ReLU hidden
- * layer, no bias, fp16; weights fp16 [1536] = Wg1 [32][32] | Wg2 [16][32], row-major
- * [out][in]) on the raw features [n][32] (16 levels x 2), then parallel_gate / parallel_gate_back
- * and hash_router_gradient of the native step (odie/native/runtime.cu:64-92,99-103).
- * visible: uint8 [n][16] or null (all visible).  Levels below `coarse` have s = 1 and no gate
- * gradient; softplus selects softplus (threshold 20) instead of the sigmoid.
+ * Router gate (router_enabled): gate MLP width -> 32 -> G (ReLU hidden layer, no bias, fp16;
+ * G = align16(levels); weights fp16 [32*width + 32*G] = Wg1 [32][width] | Wg2 [G][32], row-major
+ * [out][in], odie/config.py:176) on the raw features [n][width], then parallel_gate /
+ * parallel_gate_back and hash_router_gradient of the native step (odie/native/runtime.cu:64-92,
+ * 99-103).  Level l owns columns [o_l, o_l + F_l) of a row: features (host int32 [levels], each
+ * 1, 2 or 4; null = 2 for every level) with o_l the running sum in level order, and
+ * width = align16(sum F) (16..80); levels 1..32.
+ * visible: uint8 [n][levels] or null (all visible).  Levels below `coarse` have s = 1 and no
+ * gate gradient; softplus selects softplus (threshold 20) instead of the sigmoid.
  *
- * odie_gate_forward: weighted [n][32] = raw * fp16(s * visible) per level, s fp32 [n][16].
- * odie_gate_backward: value = the decoder's input gradient / 128 ([n][32] fp16, as
- *   odie_mlp_train's dz); writes the grid's upstream [n][32] = fp16(direct + fp16(d_raw / 128))
- *   and the gate's weight gradient fp32 [1536] (overwritten, deterministic; loss scale 16384).
+ * odie_gate_forward: weighted [n][width] = raw * fp16(s * visible) per level (columns past the
+ *   levels' features: 1), s fp32 [n][levels].
+ * odie_gate_backward: value = the decoder's input gradient / 128 ([n][width] fp16, as
+ *   odie_mlp_train's dz); writes the grid's upstream [n][width] = fp16(direct + fp16(d_raw / 128))
+ *   (direct = 0 in columns past the levels' features) and the gate's weight gradient fp32
+ *   [32*width + 32*G] (overwritten, deterministic; loss scale 16384).
  * Rows are 16-byte aligned.
  * --------------------------------------------------------------------------------------- */
-int odie_gate_forward(const uint16_t* raw, int64_t n, const uint16_t* weights, const uint8_t* visible,
-                      int coarse, int softplus, uint16_t* weighted, float* sigmoid, uint64_t stream);
+int odie_gate_forward(const uint16_t* raw, int64_t n, int width, int levels, const int32_t* features,
+                      const uint16_t* weights, const uint8_t* visible, int coarse, int softplus, uint16_t* weighted,
+                      float* sigmoid, uint64_t stream);
 
-int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int64_t n, const uint16_t* weights,
-                       const uint8_t* visible, const float* sigmoid, int coarse, int softplus,
-                       uint16_t* upstream, float* dweights, uint64_t stream);
+int odie_gate_backward(const uint16_t* raw, const uint16_t* value, int64_t n, int width, int levels,
+                       const int32_t* features, const uint16_t* weights, const uint8_t* visible, const float* sigmoid,
+                       int coarse, int softplus, uint16_t* upstream, float* dweights, uint64_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Stratified sampling, the device part of stratified_batches (odie/data.py:63-80): batch (a
@@ -342,9 +359,14 @@ int odie_reconstruct_scores(int width, int height, int regions_x, int regions_y,
  * bit 8 accepted, no effect on results), rgb, grid, decoder, gate (optional), descriptors,
  * node_bitmap, node_prefix, bitmap (packed planes), hash_encoding (optional object),
  * active, grid_lr, gate_lr, decoder_lr; and, for what the reference fixes at compile time
- * (odie/build.py:26-30): levels (16), raw_width (32), rgb8 (1: uint8 image, 0: fp32 image),
- * gate_coarse_levels (K, default 0), router_activation ("sigmoid" | "softplus").
- * Built for 16 levels x 2 features in level order; other layouts are rejected at create.
+ * (odie/build.py:26-30): levels (L, 2..20; required with packed planes, checked against
+ * hash_encoding's n_levels), raw_width (RAW = the levels' features, checked), rgb8 (1: uint8
+ * image, 0: fp32 image), gate_coarse_levels (K, default 0), router_activation ("sigmoid" |
+ * "softplus").  Packed planes take each level's features (1, 2 or 4, columns in level order) from
+ * the descriptors; the hash grid has n_features_per_level (1, 2 or 4) per level.  The decoder
+ * reads rows of W = align16(RAW) <= 80 columns (columns past RAW are 1), its weights fp32
+ * [64*W + 5120]; the gate's are fp32 [32*W + 32*align16(L)] (odie/native/runtime.cu:17-18,
+ * odie/config.py:175-177).
  * Every buffer is allocated at create for batches of up to 65536 ids: odie_step allocates
  * nothing and only queues work on the settings' stream (graph-capturable).
  * --------------------------------------------------------------------------------------- */

@@ -39,14 +39,15 @@ SIGNATURES = {
     'odie_route_noalloc': ([_P, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _U64], _I),
     'score_chunk': ([_P, _P, _I64, _I64, _I, _I, _I, _I, _P, _P, _P, C.c_bool, _U64], _I),
     'odie_topk': ([_P, _I64, _I64, _P, _U64], _I),
+    'odie_cell_bounds': ([_I, _I, _I, _P, _P, _U64], _I),
     'odie_selection_tree_ints': ([_I], _I64),
     'selection_init': ([_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _U64], _I),
     'selection_chunk': ([_P, _I, _I, _I, _I, C.c_bool, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
-    'odie_mlp_forward': ([_P, _I64, _P, _P, _U64], _I),
-    'odie_mlp_train': ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U64], _I),
+    'odie_mlp_forward': ([_P, _I64, _I, _P, _P, _U64], _I),
+    'odie_mlp_train': ([_P, _I64, _I, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U64], _I),
     'odie_mlp_train_planes': ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U64], _I),
-    'odie_gate_forward': ([_P, _I64, _P, _P, _I, _I, _P, _P, _U64], _I),
-    'odie_gate_backward': ([_P, _P, _I64, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
+    'odie_gate_forward': ([_P, _I64, _I, _I, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
+    'odie_gate_backward': ([_P, _P, _I64, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _U64], _I),
     'odie_adam_step': ([_P, _P, _P, _I, _P, _P, _P, _I64, _I, _I64, C.c_float, C.c_float, C.c_float,
                         C.c_float, C.c_float, _U64], _I),
     'odie_reconstruct': ([_I64, _I64, _I, _I, _I, _I, _P, _I, _P, _I64, _P, _I, _P, _P, _P, _P, _U64], _I),

@@ -1,11 +1,13 @@
-// Decoder MLP on MFMA: 32 -> 64 -> 64 -> 16, ReLU on the hidden layers, no bias, no output
-// activation, fp16 weights and activations, fp32 accumulation -- the decoder head of the
-// reference (FullyFusedMLP config at odie/hash_grid.py:32-34, odie/model.py:186-195; used by
-// the native step at odie/native/runtime.cu:270,273), fused with the step's loss
-// (loss_grad, odie/native/runtime.cu:53-63) and the grid-gradient unscale
-// (half_unscale by 128, odie/native/runtime.cu:282).
+// Decoder MLP on MFMA: in -> 64 -> 64 -> 16 (in = align16 of the grid's feature count, 16..80),
+// ReLU on the hidden layers, no bias, no output activation, fp16 weights and activations, fp32
+// accumulation -- the decoder head of the reference (FullyFusedMLP with n_input_dims W,
+// odie/native/runtime.cu:17,151-162,190; odie/hash_grid.py:32-34, odie/model.py:186-195; used
+// by the native step at odie/native/runtime.cu:270,273), fused with the step's loss (loss_grad,
+// odie/native/runtime.cu:53-63) and the grid-gradient unscale (half_unscale by 128,
+// odie/native/runtime.cu:282).
 //
-// Weights: fp16 [7168] = W1 [64][32] | W2 [64][64] | W3 [16][64], each row-major [out][in].
+// Weights: fp16 [64*in + 5120] = W1 [64][in] | W2 [64][64] | W3 [16][64], each row-major
+// [out][in] (7168 at in = 32).
 //
 // Work split: one wave per tile of 32 samples; every product is a v_mfma_f32_32x32x16_f16
 // with the samples as the 32 columns.  The transposed form H^T = W * X^T keeps each sample in
@@ -36,10 +38,10 @@ __device__ inline uint32_t group_max(uint32_t v) {
     return pair_max(v, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F)));  // xor 16
 }
 
-__device__ inline void load_x(const uint16_t* x, int64_t row, bool valid, int g, half8 xb[2]) {
+template <int KT> __device__ inline void load_x(const uint16_t* x, int64_t row, bool valid, int g, half8 xb[KT]) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-        xb[kt] = valid ? *reinterpret_cast<const half8*>(x + row * kIn + kt * 16 + 8 * g) : half8{};
+    for (int kt = 0; kt < KT; ++kt)
+        xb[kt] = valid ? *reinterpret_cast<const half8*>(x + row * (16 * KT) + kt * 16 + 8 * g) : half8{};
 }
 
 // Output row o of accumulator element v (v < 8): 8*(v/4) + 4*g + v%4.
@@ -50,10 +52,11 @@ __device__ inline void store_out(uint16_t* out, int64_t row, int g, const half8&
     *reinterpret_cast<uint2*>(p + 8 + 4 * g) = make_uint2(bits.z, bits.w);
 }
 
+template <int KT>
 __global__ __launch_bounds__(kMlpBlock) void mlp_forward_kernel(const uint16_t* x, int64_t n, const uint16_t* weights,
                                                                 uint16_t* out) {
-    __shared__ _Float16 w[kWeightHalfs];
-    stage_weights(weights, w);
+    __shared__ _Float16 w[Shape<KT>::kWeightHalfs];
+    stage_weights<KT>(weights, w);
     __syncthreads();
     const int lane = threadIdx.x % 64, g = lane / 32, s = lane % 32;
     const int64_t tiles = (n + 31) / 32;
@@ -61,18 +64,18 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_forward_kernel(const uint16_t* 
     for (int64_t tile = static_cast<int64_t>(blockIdx.x) * kMlpWaves + threadIdx.x / 64; tile < tiles; tile += waves) {
         const int64_t row = tile * 32 + s;
         const bool valid = row < n;
-        half8 xb[2], h1[4], h2[4];
+        half8 xb[KT], h1[4], h2[4];
         f32x16 acc3;
-        load_x(x, row, valid, g, xb);
-        forward_tile(w, g, s, xb, h1, h2, acc3);
+        load_x<KT>(x, row, valid, g, xb);
+        forward_tile<KT>(w, g, s, xb, h1, h2, acc3);
         const half8 y = round8(acc3, 0);
         if (valid) store_out(out, row, g, y);
     }
 }
 
 // Loads of one tile, issued a tile ahead of their use.
-struct TileInput {
-    half8 xb[2];
+template <int KT> struct TileInput {
+    half8 xb[KT];
     int32_t input;    // kept 32-bit: widening here would wait for the load right away
     uint32_t color;
 };
@@ -94,33 +97,34 @@ template <class T> __device__ inline T load_at(const T* base, uint32_t byte_offs
 struct TileCursor {
     uint32_t row;       // row index
     uint32_t off4;      // row * 4
-    uint32_t off64;     // row * 64 + 16 * g
+    uint32_t offx;      // row * 2 * in + 16 * g
 };
 
-__device__ inline void advance(TileCursor& c, uint32_t rows) {
+template <int KT> __device__ inline void advance(TileCursor& c, uint32_t rows) {
     c.row = pin(c.row + rows);
     c.off4 = pin(c.off4 + rows * 4u);
-    c.off64 = pin(c.off64 + rows * 64u);
+    c.offx = pin(c.offx + rows * (32u * KT));
 }
 
-__device__ inline void fetch_tile(const MlpArgs& a, const TileCursor& c, TileInput& in) {
+template <int KT> __device__ inline void fetch_tile(const MlpArgs& a, const TileCursor& c, TileInput<KT>& in) {
     const bool valid = c.row < a.n;
     // the small loads first: memory counters drain in issue order, so an early wait on them
     // leaves the 64-byte x loads in flight
     in.input = valid ? (a.rows ? load_at(a.rows, c.off4) : static_cast<int32_t>(c.row)) : 0;
     in.color = valid && a.colors ? load_at(a.colors, c.off4) : 0u;
     const half8* x = reinterpret_cast<const half8*>(a.x);
-    in.xb[0] = valid ? load_at(x, c.off64) : half8{};
-    in.xb[1] = valid ? load_at(x + 2, c.off64) : half8{};   // +32 bytes on the base, not the offset
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)   // + 32 kt bytes on the base, not the offset
+        in.xb[kt] = valid ? load_at(x + 2 * kt, c.offx) : half8{};
 }
 
 // Shared transposition buffer of one round (4 tiles = 128 samples): feature-major rows of
 // 128 samples, padded so that 16-byte reads of 16 consecutive rows hit distinct banks.
 constexpr int kRoundSamples = 32 * kMlpWaves;
 constexpr int kRS = kRoundSamples + 8;
-// phase 1 rows: dy outputs 0..2, h2 (64), dh1 (64), x (32); phase 2 rows: dh2 (64), h1 (64)
+// phase 1 rows: dy outputs 0..2, h2 (64), dh1 (64), x (in); phase 2 rows: dh2 (64), h1 (64)
 constexpr int kDyRow = 0, kH2Row = 3, kDh1Row = 67, kXRow = 131;
-constexpr int kRoundRows = 163;
+template <int KT> constexpr int round_rows() { return kXRow + 16 * KT; }
 
 // Writes this wave's 32 samples of 32*blocks features held in accumulator-row order
 // (h[t][e] = feature feature_of(t, g, e)) into rows first.. of the round buffer.
@@ -131,34 +135,64 @@ __device__ inline void put_features(_Float16* T, int first, int column, const ha
 }
 
 // One 32x32 block of a weight gradient: sum over the round's 128 samples of rows a0..
-// (M side, rows a0 + s for lanes s < a_rows) times rows b0.. (N side) of the round buffer,
-// alternating two accumulators so that consecutive MFMAs do not depend on each other.
-__device__ inline void round_block(const _Float16* T, int a0, int b0, int a_rows, int g, int s, f32x16& acc0,
-                                   f32x16& acc1) {
+// (M side, rows a0 + s for lanes s < a_rows) times rows b0.. (N side, lanes s < b_rows) of the
+// round buffer; DUAL alternates two accumulators so that consecutive MFMAs do not depend on
+// each other (their sum is the block).
+template <bool DUAL>
+__device__ inline void round_block(const _Float16* T, int a0, int b0, int a_rows, int b_rows, int g, int s,
+                                   f32x16& acc0, f32x16& acc1) {
 #pragma unroll
     for (int kt = 0; kt < kRoundSamples / 16; kt += 2) {
         const half8 a0v = s < a_rows ? lds8(T + (a0 + s) * kRS + kt * 16 + 8 * g) : half8{};
         const half8 a1v = s < a_rows ? lds8(T + (a0 + s) * kRS + kt * 16 + 16 + 8 * g) : half8{};
-        acc0 = mfma(a0v, lds8(T + (b0 + s) * kRS + kt * 16 + 8 * g), acc0);
-        acc1 = mfma(a1v, lds8(T + (b0 + s) * kRS + kt * 16 + 16 + 8 * g), acc1);
+        const half8 b0v = s < b_rows ? lds8(T + (b0 + s) * kRS + kt * 16 + 8 * g) : half8{};
+        const half8 b1v = s < b_rows ? lds8(T + (b0 + s) * kRS + kt * 16 + 16 + 8 * g) : half8{};
+        acc0 = mfma(a0v, b0v, acc0);
+        if constexpr (DUAL) acc1 = mfma(a1v, b1v, acc1);
+        else acc0 = mfma(a1v, b1v, acc0);
+    }
+}
+
+// Phase-1 gradient blocks of the round: dW3 (dy x h2, two 32-column blocks) then dW1 (dh1 x x,
+// two 32-row blocks times ceil(in/32) column blocks); wave w owns blocks w, w + 4, ...
+template <int KT> struct Phase1 {
+    static constexpr int kColumnBlocks = (KT + 1) / 2;
+    static constexpr int kBlocks = 2 + 2 * kColumnBlocks;
+    static constexpr int kSlots = (kBlocks + kMlpWaves - 1) / kMlpWaves;   // 1 (in <= 32) or 2
+};
+
+// Block b of phase 1: A rows, B rows and their counts; dW1 block (mb, nb) = b - 2 = mb * NB + nb.
+template <int KT> __device__ inline void phase1_block(int b, int& a0, int& b0, int& a_rows, int& b_rows) {
+    if (b < 2) {
+        a0 = kDyRow, a_rows = 3, b0 = kH2Row + 32 * b, b_rows = 32;
+    } else {
+        const int mb = (b - 2) / Phase1<KT>::kColumnBlocks, nb = (b - 2) % Phase1<KT>::kColumnBlocks;
+        a0 = kDh1Row + 32 * mb, a_rows = 32, b0 = kXRow + 32 * nb;
+        b_rows = 16 * KT - 32 * nb < 32 ? 16 * KT - 32 * nb : 32;
     }
 }
 
 // Work split: each wave computes the forward, loss and input gradient of its own tile in
 // registers; the weight gradients are contracted per round of 4 tiles through the shared
 // buffer in two phases (1: dW3 = dy x h2 and dW1 = dh1 x x; 2: dW2 = dh2 x h1), each wave
-// owning two of the eight 32x32 gradient blocks (waves 0,1: dW3 column blocks; waves 2,3: dW1
-// row blocks; every wave one dW2 block), so no cross-wave reduction is needed.
-template <bool PLANES>
+// owning its own 32x32 gradient blocks (Phase1 above; phase 2: one dW2 block per wave), so no
+// cross-wave reduction is needed.  PLANES (in = 32 only) writes dz as level-major planes.
+template <int KT, bool PLANES>
 __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
-    __shared__ _Float16 w[kWeightHalfs];
-    __shared__ __attribute__((aligned(16))) _Float16 T[kRoundRows * kRS];
+    using S = Shape<KT>;
+    using P1 = Phase1<KT>;
+    static_assert(!PLANES || KT == 2, "the planes layout is built for 16 levels x 2 features");
+    constexpr int kNB = P1::kColumnBlocks;   // 32-row blocks of dX
+    __shared__ _Float16 w[S::kWeightHalfs];
+    __shared__ __attribute__((aligned(16))) _Float16 T[round_rows<KT>() * kRS];
     __shared__ uint32_t records[kMlpWaves][2][4];   // per wave and lane group: level-pair |dz| maxima
-    stage_weights(a.weights, w);
+    stage_weights<KT>(a.weights, w);
     __syncthreads();
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
     const int column = 32 * wave + s;   // this lane's sample column in the round buffer
-    f32x16 gA = zero16(), gA1 = zero16(), gB = zero16(), gB1 = zero16();
+    f32x16 gA[P1::kSlots], gA1 = zero16(), gB = zero16(), gB1 = zero16();
+#pragma unroll
+    for (int k = 0; k < P1::kSlots; ++k) gA[k] = zero16();
     const int64_t tiles = (a.n + 31) / 32;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kMlpWaves;
     const float inv255 = 1.0f / 255.0f;
@@ -166,17 +200,19 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
     TileCursor cursor;
     {
         const uint32_t row0 = static_cast<uint32_t>((blockIdx.x * kMlpWaves + wave) * 32 + s);
-        cursor = {pin(row0), pin(row0 * 4u), pin(row0 * 64u + 16u * g)};
+        cursor = {pin(row0), pin(row0 * 4u), pin(row0 * (32u * KT) + 16u * g)};
     }
     const uint32_t row_stride = static_cast<uint32_t>(stride * 32);
     // One round on the tile whose inputs are in `current` (loaded a round earlier).
-    auto round = [&](int64_t base, const TileInput& current) {
+    auto round = [&](int64_t base, const TileInput<KT>& current) {
         const int64_t tile = base + wave;
         const int64_t row = tile * 32 + s;
         const bool valid = tile < tiles && row < a.n;
-        half8 xb[2] = {current.xb[0], current.xb[1]}, h1[4], h2[4];
+        half8 xb[KT], h1[4], h2[4];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) xb[kt] = current.xb[kt];
         f32x16 acc3;
-        forward_tile(w, g, s, xb, h1, h2, acc3);
+        forward_tile<KT>(w, g, s, xb, h1, h2, acc3);
         const int64_t input = current.input;
         const half8 y = round8(acc3, 0);
         half8 dy{};
@@ -214,7 +250,7 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
         half8 dh2[4], dh1[4];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-            const f32x16 acc = mfma(lds8(w + kW3t + (mb * 32 + s) * kS16 + 8 * g), dy, zero16());
+            const f32x16 acc = mfma(lds8(w + S::kW3t + (mb * 32 + s) * kS16 + 8 * g), dy, zero16());
             dh2[2 * mb] = mask8(round8(acc, 0), h2[2 * mb]);
             dh2[2 * mb + 1] = mask8(round8(acc, 8), h2[2 * mb + 1]);
         }
@@ -222,21 +258,32 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
         for (int mb = 0; mb < 2; ++mb) {
             f32x16 acc = zero16();
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW2t + (mb * 32 + s) * kS64 + 16 * t + 8 * g), dh2[t], acc);
+            for (int t = 0; t < 4; ++t)
+                acc = mfma(lds8(w + S::kW2t + (mb * 32 + s) * kS64 + 16 * t + 8 * g), dh2[t], acc);
             dh1[2 * mb] = mask8(round8(acc, 0), h1[2 * mb]);
             dh1[2 * mb + 1] = mask8(round8(acc, 8), h1[2 * mb + 1]);
         }
         {
-            f32x16 acc = zero16();
+            // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value.  K step
+            // ks = 2b + q of dX is half q of block b; word .x/.y/.z/.w of bits[ks] holds columns
+            // 16ks + 4g + 0..1, + 2..3, 16ks + 8 + 4g + 0..1, + 2..3 of the row (for in = 32: the
+            // feature pairs of levels 8ks + 2g, 8ks + 2g + 1, 8ks + 4 + 2g, 8ks + 5 + 2g).
+            u32x4 bits[KT];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc = mfma(lds8(w + kW1t + s * kS64 + 16 * t + 8 * g), dh1[t], acc);
-            // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value.  Word
-            // .x/.y/.z/.w of bits[q] holds the feature pair of level 8q+2g, 8q+2g+1, 8q+4+2g,
-            // 8q+5+2g (columns 16q+4g.. and 16q+8+4g.. of the row).
-            u32x4 bits[2];
+            for (int b = 0; b < kNB; ++b) {
+                f32x16 acc = zero16();
+                const bool row_ok = 32 * b + s < S::kIn;
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
-                bits[q] = __builtin_bit_cast(u32x4, round8(acc, 8 * q) * (half8)(static_cast<_Float16>(0.0078125f)));
+                for (int t = 0; t < 4; ++t) {
+                    const half8 at = row_ok ? lds8(w + S::kW1t + (32 * b + s) * kS64 + 16 * t + 8 * g) : half8{};
+                    acc = mfma(at, dh1[t], acc);
+                }
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    if (2 * b + q < KT)
+                        bits[2 * b + q] =
+                            __builtin_bit_cast(u32x4, round8(acc, 8 * q) * (half8)(static_cast<_Float16>(0.0078125f)));
+            }
             if constexpr (PLANES) {
                 if (valid) {
 #pragma unroll
@@ -261,22 +308,22 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                     if (s == 0) records[wave][g][j] = peak[j];
                 }
             } else if (valid) {
-                uint16_t* p = a.dz + row * kIn;
+                uint16_t* p = a.dz + row * S::kIn;
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    *reinterpret_cast<uint2*>(p + 16 * q + 4 * g) = make_uint2(bits[q].x, bits[q].y);
-                    *reinterpret_cast<uint2*>(p + 16 * q + 8 + 4 * g) = make_uint2(bits[q].z, bits[q].w);
+                for (int ks = 0; ks < KT; ++ks) {
+                    *reinterpret_cast<uint2*>(p + 16 * ks + 4 * g) = make_uint2(bits[ks].x, bits[ks].y);
+                    *reinterpret_cast<uint2*>(p + 16 * ks + 8 + 4 * g) = make_uint2(bits[ks].z, bits[ks].w);
                 }
             }
         }
-        // phase 1: dW3 = sum dy (x) h2 (waves 0, 1), dW1 = sum dh1 (x) x (waves 2, 3)
+        // phase 1: dW3 = sum dy (x) h2, dW1 = sum dh1 (x) x
         if (g == 0)
 #pragma unroll
             for (int c = 0; c < 3; ++c) T[(kDyRow + c) * kRS + column] = dy[c];
         put_features(T, kH2Row, column, h2, 2, g);
         put_features(T, kDh1Row, column, dh1, 2, g);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int e = 0; e < 8; ++e) T[(kXRow + kt * 16 + 8 * g + e) * kRS + column] = xb[kt][e];
         __syncthreads();
@@ -288,43 +335,61 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
             for (int v = 0; v < kMlpWaves; ++v) m = pair_max(m, records[v][lg][2 * q + h]);
             a.blockmax[(base / kMlpWaves) * 16 + level] = __half2float(bits_to_half(static_cast<uint16_t>(m >> (16 * b))));
         }
-        if (wave < 2) round_block(T, kDyRow, kH2Row + 32 * wave, 3, g, s, gA, gA1);
-        else round_block(T, kDh1Row + 32 * (wave - 2), kXRow, 32, g, s, gA, gA1);
+#pragma unroll
+        for (int k = 0; k < P1::kSlots; ++k) {
+            const int block = wave + kMlpWaves * k;
+            if (block < P1::kBlocks) {
+                int a0, b0, a_rows, b_rows;
+                phase1_block<KT>(block, a0, b0, a_rows, b_rows);
+                if constexpr (P1::kSlots == 1) round_block<true>(T, a0, b0, a_rows, b_rows, g, s, gA[k], gA1);
+                else round_block<false>(T, a0, b0, a_rows, b_rows, g, s, gA[k], gA1);
+            }
+        }
         __syncthreads();
         // phase 2: dW2 = sum dh2 (x) h1; rows 0..63 = dh2, 64..127 = h1
         put_features(T, 0, column, dh2, 2, g);
         put_features(T, 64, column, h1, 2, g);
         __syncthreads();
-        round_block(T, 32 * (wave >> 1), 64 + 32 * (wave & 1), 32, g, s, gB, gB1);
+        round_block<true>(T, 32 * (wave >> 1), 64 + 32 * (wave & 1), 32, 32, g, s, gB, gB1);
         __syncthreads();
 
     };
     // Unrolled by two with ping-pong input buffers, so that a round never copies the next
     // round's prefetch (a copy would have to wait for it).
-    TileInput even, odd;
-    fetch_tile(a, cursor, even);
+    TileInput<KT> even, odd;
+    fetch_tile<KT>(a, cursor, even);
     for (int64_t base = static_cast<int64_t>(blockIdx.x) * kMlpWaves; base < tiles; base += 2 * stride) {
-        advance(cursor, row_stride);
-        fetch_tile(a, cursor, odd);
+        advance<KT>(cursor, row_stride);
+        fetch_tile<KT>(a, cursor, odd);
         round(base, even);
         if (base + stride >= tiles) break;
-        advance(cursor, row_stride);
-        fetch_tile(a, cursor, even);
+        advance<KT>(cursor, row_stride);
+        fetch_tile<KT>(a, cursor, even);
         round(base + stride, odd);
     }
     // This workgroup's partial: each wave writes its own blocks (accumulator element v of
     // lane (g, s) is row 8*(v/4) + 4g + v%4, column s of the block).
-    gA += gA1;
+    if constexpr (P1::kSlots == 1) gA[0] += gA1;
     gB += gB1;
-    float* out = a.partials + static_cast<int64_t>(blockIdx.x) * kParams;
+    float* out = a.partials + static_cast<int64_t>(blockIdx.x) * S::kParams;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int r = 8 * (v / 4) + 4 * g + v % 4;
-        out[kW1 + (32 * (wave >> 1) + r) * kHid + 32 * (wave & 1) + s] = gB[v];
-        if (wave < 2) {
-            if (v < 8) out[kW1 + kW2 + r * kHid + 32 * wave + s] = gA[v];
-        } else {
-            out[(32 * (wave - 2) + r) * kIn + s] = gA[v];
+        out[S::kW1 + (32 * (wave >> 1) + r) * kHid + 32 * (wave & 1) + s] = gB[v];
+    }
+#pragma unroll
+    for (int k = 0; k < P1::kSlots; ++k) {
+        const int block = wave + kMlpWaves * k;
+        if (block >= P1::kBlocks) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = 8 * (v / 4) + 4 * g + v % 4;
+            if (block < 2) {
+                if (v < 8) out[S::kW1 + kW2 + r * kHid + 32 * block + s] = gA[k][v];
+            } else {
+                const int mb = (block - 2) / P1::kColumnBlocks, nb = (block - 2) % P1::kColumnBlocks;
+                if (32 * nb + s < S::kIn) out[(32 * mb + r) * S::kIn + 32 * nb + s] = gA[k][v];
+            }
         }
     }
 }
@@ -333,25 +398,26 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
 // 256-thread block take the workgroups b = q, q+4, q+8, ... (q = group), eight loads in flight
 // per step, and the four group sums are added in group order.
 constexpr int kReduceParams = 64;
-__global__ __launch_bounds__(256) void mlp_reduce_kernel(const float* partials, int blocks, float* dweights) {
+__global__ __launch_bounds__(256) void mlp_reduce_kernel(const float* partials, int blocks, int params,
+                                                         float* dweights) {
     __shared__ float group_sum[4][kReduceParams];
     const int local = threadIdx.x % kReduceParams, q = threadIdx.x / kReduceParams;
     const int p = blockIdx.x * kReduceParams + local;
     float total = 0.0f;
-    if (p < kParams) {
+    if (p < params) {
         int b = q;
         for (; b + 28 < blocks; b += 32) {
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = partials[static_cast<int64_t>(b + 4 * j) * kParams + p];
+            for (int j = 0; j < 8; ++j) v[j] = partials[static_cast<int64_t>(b + 4 * j) * params + p];
 #pragma unroll
             for (int j = 0; j < 8; ++j) total += v[j];
         }
-        for (; b < blocks; b += 4) total += partials[static_cast<int64_t>(b) * kParams + p];
+        for (; b < blocks; b += 4) total += partials[static_cast<int64_t>(b) * params + p];
     }
     group_sum[q][local] = total;
     __syncthreads();
-    if (q == 0 && p < kParams)
+    if (q == 0 && p < params)
         dweights[p] = ((group_sum[0][local] + group_sum[1][local]) + group_sum[2][local]) + group_sum[3][local];
 }
 
@@ -361,30 +427,48 @@ int mlp_blocks(int64_t n) {
     return static_cast<int>(blocks < 512 ? (blocks < 1 ? 1 : blocks) : 512);
 }
 
+// Input widths the decoder is built for: 16, 32, 48, 64, 80 (align16 of 2..80 grid features).
+int input_steps(int width) { return width >= 16 && width <= 16 * kMaxInputSteps && width % 16 == 0 ? width / 16 : 0; }
+int64_t decoder_params(int width) { return int64_t{64} * width + kW2 + kW3; }
+
 }  // namespace
 }  // namespace odie
 
 using namespace odie;
 
-ODIE_API int odie_mlp_forward(const uint16_t* x, int64_t n, const uint16_t* weights, uint16_t* out, uint64_t stream) {
+ODIE_API int odie_mlp_forward(const uint16_t* x, int64_t n, int width, const uint16_t* weights, uint16_t* out,
+                              uint64_t stream) {
+    const int kt = input_steps(width);
+    if (!kt) return fail("odie_mlp_forward: width must be 16, 32, 48, 64 or 80");
     if (n < 0) return fail("odie_mlp_forward: n must be nonnegative");
     if (n == 0) return 0;
     if (!x || !weights || !out) return fail("odie_mlp_forward: null pointer");
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(out) % 8)
         return fail("odie_mlp_forward: x must be 16-byte and out 8-byte aligned");
-    mlp_forward_kernel<<<mlp_blocks(n), kMlpBlock, 0, as_stream(stream)>>>(x, n, weights, out);
+    const hipStream_t s = as_stream(stream);
+    const int blocks = mlp_blocks(n);
+    switch (kt) {
+        case 1: mlp_forward_kernel<1><<<blocks, kMlpBlock, 0, s>>>(x, n, weights, out); break;
+        case 2: mlp_forward_kernel<2><<<blocks, kMlpBlock, 0, s>>>(x, n, weights, out); break;
+        case 3: mlp_forward_kernel<3><<<blocks, kMlpBlock, 0, s>>>(x, n, weights, out); break;
+        case 4: mlp_forward_kernel<4><<<blocks, kMlpBlock, 0, s>>>(x, n, weights, out); break;
+        default: mlp_forward_kernel<5><<<blocks, kMlpBlock, 0, s>>>(x, n, weights, out); break;
+    }
     return check_launch("odie_mlp_forward");
 }
 
 namespace {
 
-int mlp_train(const char* name, const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+int mlp_train(const char* name, const uint16_t* x, int64_t n, int width, int64_t real, const uint16_t* weights,
               const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target, const int32_t* rows,
               uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz, uint32_t* planes, float* blockmax,
               float* dweights, uint64_t stream) {
     const std::string who(name);
+    const int kt = input_steps(width);
+    if (!kt) return fail(who + ": width must be 16, 32, 48, 64 or 80");
+    if (planes && kt != 2) return fail(who + ": the planes layout is built for width 32");
     if (n < 0 || real < 1) return fail(who + ": need n >= 0 and real >= 1");
-    if (n >= (int64_t{1} << 26)) return fail(who + ": n must be below 2^26 (32-bit byte offsets)");
+    if (n * 2 * width >= (int64_t{1} << 32)) return fail(who + ": n * width must stay below 2^31 (32-bit byte offsets)");
     if (!weights || !dweights || (n && !x)) return fail(who + ": null pointer");
     if (n && (planes ? !blockmax : !dz)) return fail(who + ": null pointer");
     if (n && !colors && !(rgb ? ids != nullptr : target != nullptr))
@@ -393,27 +477,38 @@ int mlp_train(const char* name, const uint16_t* x, int64_t n, int64_t real, cons
         reinterpret_cast<uintptr_t>(planes) % 4 || (out && reinterpret_cast<uintptr_t>(out) % 8))
         return fail(who + ": x must be 16-byte, dz and out 8-byte, planes 4-byte aligned");
     const hipStream_t s = as_stream(stream);
-    if (n == 0) return launch_fill_zero(dweights, kParams, s);
+    const int64_t params = decoder_params(width);
+    if (n == 0) return launch_fill_zero(dweights, params, s);
     const int blocks = mlp_blocks(n);
-    float* partials = static_cast<float*>(workspace(static_cast<size_t>(blocks) * kParams * sizeof(float), s));
+    float* partials = static_cast<float*>(workspace(static_cast<size_t>(blocks) * params * sizeof(float), s));
     if (!partials) return -1;
     MlpArgs a{x, weights, n, real, colors, rgb, ids, target, rows, out, hidden, squares, planes ? nullptr : dz, partials,
               planes, planes ? blockmax : nullptr};
-    if (planes) mlp_train_kernel<true><<<blocks, kMlpBlock, 0, s>>>(a);
-    else mlp_train_kernel<false><<<blocks, kMlpBlock, 0, s>>>(a);
+    if (planes) {
+        mlp_train_kernel<2, true><<<blocks, kMlpBlock, 0, s>>>(a);
+    } else {
+        switch (kt) {
+            case 1: mlp_train_kernel<1, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
+            case 2: mlp_train_kernel<2, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
+            case 3: mlp_train_kernel<3, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
+            case 4: mlp_train_kernel<4, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
+            default: mlp_train_kernel<5, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
+        }
+    }
     if (check_launch(name)) return -1;
-    mlp_reduce_kernel<<<(kParams + kReduceParams - 1) / kReduceParams, 256, 0, s>>>(partials, blocks, dweights);
+    mlp_reduce_kernel<<<static_cast<uint32_t>((params + kReduceParams - 1) / kReduceParams), 256, 0, s>>>(
+        partials, blocks, static_cast<int>(params), dweights);
     return check_launch((who + " reduce").c_str());
 }
 
 }  // namespace
 
-ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
+ODIE_API int odie_mlp_train(const uint16_t* x, int64_t n, int width, int64_t real, const uint16_t* weights,
                             const uint32_t* colors, const uint8_t* rgb, const int64_t* ids, const float* target,
                             const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares, uint16_t* dz,
                             float* dweights, uint64_t stream) {
-    return mlp_train("odie_mlp_train", x, n, real, weights, colors, rgb, ids, target, rows, out, hidden, squares, dz,
-                     nullptr, nullptr, dweights, stream);
+    return mlp_train("odie_mlp_train", x, n, width, real, weights, colors, rgb, ids, target, rows, out, hidden, squares,
+                     dz, nullptr, nullptr, dweights, stream);
 }
 
 ODIE_API int odie_mlp_train_planes(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,
@@ -421,6 +516,6 @@ ODIE_API int odie_mlp_train_planes(const uint16_t* x, int64_t n, int64_t real, c
                                    const int32_t* rows, uint16_t* out, uint16_t* hidden, float* squares,
                                    uint32_t* planes, float* blockmax, float* dweights, uint64_t stream) {
     if (n > 0 && !planes) return fail("odie_mlp_train_planes: planes is null");
-    return mlp_train("odie_mlp_train_planes", x, n, real, weights, colors, rgb, ids, target, rows, out, hidden,
+    return mlp_train("odie_mlp_train_planes", x, n, kIn, real, weights, colors, rgb, ids, target, rows, out, hidden,
                      squares, nullptr, planes, blockmax, dweights, stream);
 }

@@ -56,7 +56,7 @@ __device__ inline DevLevel pick(const DevLevel& first, const DevLevel& second, b
 
 // Per-block copies of the decoder's forward weights and the tile bounds.
 __device__ inline void stage_model(const ReconArgs& a, const TileBounds& bounds, _Float16* w, TileBounds& tb) {
-    stage_forward_weights(a.weights, w);
+    stage_forward_weights<2>(a.weights, w);
     for (int j = threadIdx.x; j <= kMaxTiles; j += kReconBlock) {
         tb.x0[j] = bounds.x0[j];
         tb.y0[j] = bounds.y0[j];
@@ -103,7 +103,7 @@ __device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const _
         xb[kt] = __builtin_bit_cast(half8, u32x4{pairs[kt][0], pairs[kt][1], pairs[kt][2], pairs[kt][3]});
     half8 h1[4], h2[4];
     f32x16 acc3;
-    forward_tile(w, g, s, xb, h1, h2, acc3);
+    forward_tile<2>(w, g, s, xb, h1, h2, acc3);
     out = round8(acc3, 0);
 }
 

@@ -64,10 +64,41 @@ __global__ __launch_bounds__(kResidualBlock) void accumulate_kernel(const float*
     totals[cell] = sum;
 }
 
+// Cell bounds of the native geometry cells along one axis of `size` pixels (the pixel -> cell map of
+// odie/selection.py:44-55 and odie/gpu_residual.py:49-62): pixel p has the coordinate
+// x = fp32(p) / fp32(size - 1) (correctly rounded division) and the cell floor(fmaf(R - 1, x, 0.5))
+// -- the encode's own geometry -- so bounds[c] is the first pixel whose cell is >= c and
+// bounds[R] = size.  Cells grow with p, so each thread writes the bounds of the cells its pixel
+// opens.
+__device__ inline int native_cell(int p, int size, int resolution) {
+    const float x = __fdiv_rn(static_cast<float>(p), static_cast<float>(size - 1));
+    const int cell = static_cast<int>(floorf(__builtin_fmaf(static_cast<float>(resolution - 1), x, 0.5f)));
+    return cell < resolution - 1 ? cell : resolution - 1;
+}
+
+__global__ __launch_bounds__(256) void cell_bounds_kernel(int size, int resolution, int32_t* bounds) {
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= size) return;
+    const int cell = native_cell(p, size, resolution);
+    const int before = p ? native_cell(p - 1, size, resolution) : -1;
+    for (int c = before + 1; c <= cell; ++c) bounds[c] = p;
+    if (p == size - 1) bounds[resolution] = size;
+}
+
 }  // namespace
 }  // namespace odie
 
 using namespace odie;
+
+ODIE_API int odie_cell_bounds(int width, int height, int resolution, int32_t* xb, int32_t* yb, uint64_t stream) {
+    if (width < 2 || height < 2) return fail("odie_cell_bounds: width and height must be at least 2");
+    if (resolution < 2 || resolution > (1 << 23)) return fail("odie_cell_bounds: resolution must be within [2, 2^23]");
+    if (!xb || !yb) return fail("odie_cell_bounds: null pointer");
+    const hipStream_t s = as_stream(stream);
+    cell_bounds_kernel<<<static_cast<uint32_t>((width + 255) / 256), 256, 0, s>>>(width, resolution, xb);
+    cell_bounds_kernel<<<static_cast<uint32_t>((height + 255) / 256), 256, 0, s>>>(height, resolution, yb);
+    return check_launch("odie_cell_bounds");
+}
 
 // Same signature and meaning as score_chunk (odie/residual_cuda.cu:45-52): pixels [begin, end)
 // of a width-wide image, prediction fp32 [end-begin, 3], target uint8 or fp32 [end-begin, 3],

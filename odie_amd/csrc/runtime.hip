@@ -5,7 +5,12 @@
 // allocates nothing and only launches work on the handle's stream, so it can be captured in a
 // graph once a few eager steps have sized the library's workspace.
 //
-// Step (odie/native/runtime.cu:246-312), for 16 levels x 2 features (input width 32):
+// The reference fixes the level count L (2..20), the row of raw features (RAW = sum of the
+// levels' feature counts, padded to W = align16(RAW) with columns of 1) and G = align16(L) gate
+// outputs at compile time (odie/native/runtime.cu:17-18, odie/build.py:26-30); here they come
+// from the settings and the descriptors, and every buffer is sized from them at create.
+//
+// Step (odie/native/runtime.cu:246-312):
 //   ids -> xy and packed RGB8 targets                       input_batch          (:30-38)
 //   packed planes (active prefix, visibility) or hash grid  query / GridEncoding (:39-52,260)
 //   router gate (when a gate is given)                      parallel_gate        (:64-76)
@@ -27,10 +32,12 @@ namespace odie {
 namespace {
 
 constexpr int kBatch = 65536;
-constexpr int kLevels = 16;
-constexpr int kWidth = 32;
-constexpr int kDecoderParams = 7168;
-constexpr int kGateParams = 1536;
+constexpr int kMinLevels = 2, kMaxLevels = 20;   // odie/native/runtime.cu:18
+constexpr int kMaxRow = 80;                       // align16(20 levels x 4 features)
+
+int align16(int value) { return (value + 15) / 16 * 16; }
+int64_t decoder_params(int row) { return int64_t{64} * row + 64 * 64 + 64 * 16; }      // odie/config.py:176
+int64_t gate_params(int row, int levels) { return int64_t{32} * row + int64_t{32} * align16(levels); }
 
 // ---------------------------------------------------------------------------------------------
 // Settings: the flat JSON objects the reference's NativeOptimizer writes (numbers, booleans,
@@ -195,6 +202,14 @@ __global__ __launch_bounds__(256) void cast_half_kernel(const float* in, uint16_
     if (i < n) out[i] = half_to_bits(__float2half_rn(in[i]));
 }
 
+// Columns [from, row) of every row of raw features set to fp16 1.0, the padding the decoder and
+// gate read past the levels' features (odie/native/runtime.cu:51).
+__global__ __launch_bounds__(256) void pad_columns_kernel(uint16_t* rows, int n, int row, int from) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int per = row - from;
+    if (i < static_cast<int64_t>(n) * per) rows[(i / per) * row + from + i % per] = 0x3C00;
+}
+
 // Sets *flag when any word of [begin, end) of the three state arrays is nonzero.
 __global__ __launch_bounds__(256) void any_state_kernel(const float* m, const float* v, const uint32_t* steps,
                                                         int64_t begin, int64_t end, int* flag) {
@@ -259,7 +274,11 @@ struct Runtime {
     bool hash, rgb8 = true, half_grads, fused;
     const void* rgb;
     float* grid;                      // caller-owned fp32 master
-    int active = kLevels, coarse = 0, softplus = 0;
+    int levels = 0;                   // L
+    int raw_width = 0, row = 0;       // RAW = sum of the levels' features, W = align16(RAW)
+    std::vector<int32_t> features;    // F of each level (the descriptors' column 5)
+    bool levels16x2 = false;          // 16 levels x 2 features in level order (the forward's fast path)
+    int active = 0, coarse = 0, softplus = 0;
     float grid_lr = 0.0f;
     // packed planes (odie/model.py:100-101)
     const int32_t* desc = nullptr;
@@ -280,6 +299,7 @@ struct Runtime {
 
     explicit Runtime(const Json& j);
     void configure(const Json& j);
+    void read_shape(const int32_t* descriptors);
     void sync_weights();
     void step(const int64_t* ids, int n, bool update);
     std::string pointers() const;
@@ -293,7 +313,8 @@ std::vector<odie_grid_level> hash_grid_levels(const Json& e, int64_t& entries) {
     const int log2t = static_cast<int>(e.at("log2_hashmap_size").i64());
     const int base = static_cast<int>(e.at("base_resolution").i64());
     const float growth = static_cast<float>(e.at("per_level_scale").number());
-    if (levels != kLevels || features != 2) throw std::runtime_error("this runtime builds 16 levels x 2 features");
+    if (levels < kMinLevels || levels > kMaxLevels) throw std::runtime_error("HashGrid levels must be within 2..20");
+    if (features != 1 && features != 2 && features != 4) throw std::runtime_error("HashGrid features per level must be 1, 2 or 4");
     if (log2t < 3 || log2t > 30 || base < 2 || !(growth > 1.0f) || !std::isfinite(growth))
         throw std::runtime_error("invalid hash_encoding");
     const float log_growth = static_cast<float>(std::log2(static_cast<double>(growth)));
@@ -330,10 +351,9 @@ Runtime::Runtime(const Json& j)
         throw std::runtime_error("invalid total, width or height");
     if (!rgb || !grid) throw std::runtime_error("null rgb or grid");
     if (reinterpret_cast<uintptr_t>(grid) % 16) throw std::runtime_error("grid must be 16-byte aligned");
-    // compile-time specializations of the reference library (odie/build.py:26-30), here settings
-    if (const Json* k = j.find("levels"); k && k->i64() != kLevels) throw std::runtime_error("this runtime builds 16 levels");
-    if (const Json* k = j.find("raw_width"); k && k->i64() != kWidth)
-        throw std::runtime_error("this runtime builds a 32-wide feature row");
+    // compile-time specializations of the reference library (odie/build.py:26-30), here settings:
+    // levels (ODIE_LEVELS), raw_width (ODIE_RAW_WIDTH, checked against the levels' features),
+    // rgb8, gate_coarse_levels, router_activation
     if (const Json* k = j.find("rgb8")) rgb8 = k->number() != 0.0;
     if (const Json* k = j.find("gate_coarse_levels")) coarse = static_cast<int>(k->i64());
     if (const Json* a = j.find("router_activation")) {
@@ -341,36 +361,57 @@ Runtime::Runtime(const Json& j)
             throw std::runtime_error("router_activation must be sigmoid or softplus");
         softplus = a->text == "softplus";
     }
-    if (coarse < 0 || coarse > kLevels) throw std::runtime_error("gate_coarse_levels must be within 0..16");
     const bool router = j.find("gate") != nullptr;
     if (router && !(mode & 16)) throw std::runtime_error("the router gate is built as the parallel gate (mode bit 16)");
     if (router && fused && !hash)
         throw std::runtime_error("mode bit 1 with the router on packed planes is not built (NativeOptimizer uses 16 and 20)");
     if (hash) {
         if (!(mode & 4)) throw std::runtime_error("HashGrid requires native half gradients");
+        const Json& e = j.at("hash_encoding");
         int64_t entries = 0;
-        hash_levels = hash_grid_levels(j.at("hash_encoding"), entries);
-        if (entries * 2 != total) throw std::runtime_error("HashGrid allocation differs from resolved layout");
+        hash_levels = hash_grid_levels(e, entries);
+        levels = static_cast<int>(hash_levels.size());
+        if (const Json* k = j.find("levels"); k && k->i64() != levels)
+            throw std::runtime_error("levels differs from the grid's level count");
+        features.assign(levels, static_cast<int32_t>(e.at("n_features_per_level").i64()));
+        if (entries * features[0] != total) throw std::runtime_error("HashGrid allocation differs from resolved layout");
         grid_half.allocate(total);
+    } else {
+        const Json* k = j.find("levels");
+        if (!k) throw std::runtime_error("levels is required with packed planes (the reference fixes it at build time)");
+        levels = static_cast<int>(k->i64());
+        if (levels < kMinLevels || levels > kMaxLevels) throw std::runtime_error("levels must be within 2..20");
     }
+    if (coarse < 0 || coarse > levels) throw std::runtime_error("gate_coarse_levels must be within 0..levels");
+    if (const Json* k = j.find("raw_width"); k && (k->i64() < levels || k->i64() > kMaxRow))
+        throw std::runtime_error("raw_width must be within levels..80");
+    // settings are checked; the packed planes' feature row is read from the device descriptors
+    if (!hash) read_shape(device_pointer<const int32_t>(j, "descriptors"));
+    raw_width = 0;
+    for (int32_t f : features) raw_width += f;
+    if (const Json* k = j.find("raw_width"); k && k->i64() != raw_width)
+        throw std::runtime_error("raw_width differs from the levels' features");
+    row = align16(raw_width);
+    if (row > kMaxRow) throw std::runtime_error("the levels' features exceed 80 columns");
+    levels16x2 = levels == 16 && row == 32 && raw_width == 32;
     xy.allocate(2 * kBatch);
     if (!rgb8) target.allocate(3 * kBatch);
     colors.allocate(kBatch);
     squares.allocate(kBatch);
-    raw.allocate(static_cast<size_t>(kWidth) * kBatch);
-    dz.allocate(static_cast<size_t>(kWidth) * kBatch);
+    raw.allocate(static_cast<size_t>(row) * kBatch);
+    dz.allocate(static_cast<size_t>(row) * kBatch);
     output.allocate(16 * static_cast<size_t>(kBatch));
-    vis.allocate(static_cast<size_t>(kLevels) * kBatch);
+    vis.allocate(static_cast<size_t>(levels) * kBatch);
     flag.allocate(1);
     grid_grad.allocate(total);
     grid_grad.zero(stream);
     grid_adam.allocate(total, stream);
-    decoder.reset(new Head(device_pointer<float>(j, "decoder"), kDecoderParams, stream));
+    decoder.reset(new Head(device_pointer<float>(j, "decoder"), decoder_params(row), stream));
     if (router) {
-        gate.reset(new Head(device_pointer<float>(j, "gate"), kGateParams, stream));
-        weighted.allocate(static_cast<size_t>(kWidth) * kBatch);
-        sigmoid.allocate(static_cast<size_t>(kLevels) * kBatch);
-        upstream.allocate(static_cast<size_t>(kWidth) * kBatch);
+        gate.reset(new Head(device_pointer<float>(j, "gate"), gate_params(row, levels), stream));
+        weighted.allocate(static_cast<size_t>(row) * kBatch);
+        sigmoid.allocate(static_cast<size_t>(levels) * kBatch);
+        upstream.allocate(static_cast<size_t>(row) * kBatch);
     }
     if (hash) hip(hipMemsetAsync(vis.data, 1, vis.count, stream), "hipMemsetAsync");
     configure(j);
@@ -378,9 +419,29 @@ Runtime::Runtime(const Json& j)
     hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
 
+// Per-level feature counts from the packed-plane descriptors (odie/model.py:100-101): F in
+// {1, 2, 4}, output columns the running sum in level order (the gate and decoder read them so).
+// The first call fixes the row layout; later descriptors (new supports) must keep it.
+void Runtime::read_shape(const int32_t* d) {
+    if (!d) throw std::runtime_error("null packed-plane pointer");
+    std::vector<int32_t> host(8 * static_cast<size_t>(levels));
+    hip(hipMemcpyAsync(host.data(), d, host.size() * 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+    hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    std::vector<int32_t> f(levels);
+    int offset = 0;
+    for (int l = 0; l < levels; ++l) {
+        f[l] = host[8 * l + 5];
+        if (f[l] != 1 && f[l] != 2 && f[l] != 4) throw std::runtime_error("plane features must be 1, 2 or 4");
+        if (host[8 * l + 6] != offset) throw std::runtime_error("plane features must fill the row in level order");
+        offset += f[l];
+    }
+    if (!features.empty() && f != features) throw std::runtime_error("the descriptors change the feature row");
+    features = f;
+}
+
 void Runtime::configure(const Json& j) {
     const int a = static_cast<int>(j.at("active").i64());
-    if (a < 2 || a > kLevels) throw std::runtime_error("Invalid active prefix");
+    if (a < 2 || a > levels) throw std::runtime_error("Invalid active prefix");
     const float glr = static_cast<float>(j.at("grid_lr").number());
     const float dlr = static_cast<float>(j.at("decoder_lr").number());
     const float wlr = gate ? static_cast<float>(j.at("gate_lr").number()) : 0.0f;
@@ -390,13 +451,7 @@ void Runtime::configure(const Json& j) {
         const int32_t* p = device_pointer<const int32_t>(j, "node_prefix");
         const uint8_t* c = device_pointer<const uint8_t>(j, "bitmap");
         if (!d || !b || !p || !c) throw std::runtime_error("null packed-plane pointer");
-        // the gate and decoder read 2 features per level in level order (odie/model.py:100-101)
-        std::vector<int32_t> host(8 * kLevels);
-        hip(hipMemcpyAsync(host.data(), d, host.size() * 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
-        hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
-        for (int l = 0; l < kLevels; ++l)
-            if (host[8 * l + 5] != 2 || host[8 * l + 6] != 2 * l)
-                throw std::runtime_error("this runtime builds 16 levels x 2 features in level order");
+        read_shape(d);
         desc = d;
         bits = b;
         prefix = p;
@@ -435,37 +490,45 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
     batch_input_kernel<<<(n + 255) / 256, 256, 0, stream>>>(ids, n, width, height, rx, ry, rgb, rgb8, xy.data,
                                                             colors.data, target.data);
     call(check_launch("odie_step: batch input"));
-    if (hash)
-        call(odie_grid_forward(xy.data, n, nullptr, 1, grid_half.data, total, ODIE_F16, hash_levels.data(), kLevels, 2,
-                               raw.data, kWidth, s));
-    else
-        call(packed_forward_internal(xy.data, n, grid, total, desc, kLevels, bits, prefix, cells, kWidth, active,
-                                     0x3C00, raw.data, vis.data, stream, true));
-    const uint16_t* features = raw.data;
-    if (gate) {
-        call(odie_gate_forward(raw.data, n, gate->half.data, vis.data, coarse, softplus, weighted.data, sigmoid.data, s));
-        features = weighted.data;
+    if (hash) {
+        call(odie_grid_forward(xy.data, n, nullptr, 1, grid_half.data, total, ODIE_F16, hash_levels.data(), levels,
+                               features[0], raw.data, row, s));
+        if (raw_width < row) {
+            const int64_t cells_to_pad = static_cast<int64_t>(n) * (row - raw_width);
+            pad_columns_kernel<<<static_cast<uint32_t>((cells_to_pad + 255) / 256), 256, 0, stream>>>(raw.data, n, row,
+                                                                                                      raw_width);
+            call(check_launch("odie_step: padding columns"));
+        }
+    } else {
+        call(packed_forward_internal(xy.data, n, grid, total, desc, levels, bits, prefix, cells, row, active, 0x3C00,
+                                     raw.data, vis.data, stream, levels16x2));
     }
-    call(odie_mlp_train(features, n, n, decoder->half.data, rgb8 ? colors.data : nullptr, nullptr, nullptr,
+    const uint16_t* inputs = raw.data;
+    if (gate) {
+        call(odie_gate_forward(raw.data, n, row, levels, features.data(), gate->half.data, vis.data, coarse, softplus,
+                               weighted.data, sigmoid.data, s));
+        inputs = weighted.data;
+    }
+    call(odie_mlp_train(inputs, n, row, n, decoder->half.data, rgb8 ? colors.data : nullptr, nullptr, nullptr,
                         rgb8 ? nullptr : target.data, nullptr, output.data, nullptr, squares.data, dz.data,
                         decoder->grad.data, s));
     const uint16_t* up = dz.data;
     if (gate) {
-        call(odie_gate_backward(raw.data, dz.data, n, gate->half.data, vis.data, sigmoid.data, coarse, softplus,
-                                upstream.data, gate->grad.data, s));
+        call(odie_gate_backward(raw.data, dz.data, n, row, levels, features.data(), gate->half.data, vis.data,
+                                sigmoid.data, coarse, softplus, upstream.data, gate->grad.data, s));
         up = upstream.data;
     }
     // grid: fp16 gradients (mode bit 4) carrying the loss scale 128 (odie/native/runtime.cu:298,304-305)
     const float grid_divisor = half_grads ? 1.0f : 0.0f;
     if (hash && update) {
         const AdamStep a = make_step(grid, grid_half.data, grid_adam, 1, grid_lr, 128.0f, grid_divisor);
-        call(grid_backward_adam_internal(xy.data, n, nullptr, 1, up, ODIE_F16, kWidth, total, hash_levels.data(),
-                                         kLevels, 2, a, stream));
+        call(grid_backward_adam_internal(xy.data, n, nullptr, 1, up, ODIE_F16, row, total, hash_levels.data(), levels,
+                                         features[0], a, stream));
     } else if (hash) {
-        call(odie_grid_backward(xy.data, n, nullptr, 1, up, ODIE_F16, kWidth, total, hash_levels.data(), kLevels, 2,
-                                grid_grad.data, 1, s));
+        call(odie_grid_backward(xy.data, n, nullptr, 1, up, ODIE_F16, row, total, hash_levels.data(), levels,
+                                features[0], grid_grad.data, 1, s));
     } else {
-        call(odie_packed_backward(xy.data, n, up, kWidth, desc, kLevels, bits, prefix, cells, grid_grad.data, total, s));
+        call(odie_packed_backward(xy.data, n, up, row, desc, levels, bits, prefix, cells, grid_grad.data, total, s));
         if (update) {
             const AdamStep a = make_step(grid, nullptr, grid_adam, 1, grid_lr, 128.0f, grid_divisor);
             call(launch_adam(a, grid_grad.data, 0, total, stream));

@@ -26,7 +26,7 @@ class DeviceScores:
             self.ymap = np.repeat(np.arange(self.resolution), np.diff(yb))
         else:
             self.resolution = resolution
-            xb, yb, self.ymap = cell_bounds(shape, resolution)
+            xb, yb, self.ymap = cell_bounds(shape, resolution, device=device)
         self.counts = (np.diff(yb).astype(np.int64)[:, None] * np.diff(xb)[None, :]).reshape(-1)
         self.xb = torch.from_numpy(xb).to(device)
         self.yb = torch.from_numpy(yb).to(device)

@@ -1,14 +1,16 @@
-"""Packed xy-plane layout and the PackedQuery op (odie/model.py).
+"""Packed xy planes: the on-demand representation's storage layout, its encode as a torch
+autograd op on this library's kernels, and the model built on them.
 
-make_layout / plane_closure / make_node_index follow odie/model.py:33-118: each level's
-retained nodes are the closure {c, c+1, c+R, c+R+1} mod align8(R^2) of its support; a
-level whose closure is every node is addressed directly, otherwise through a bitmap of
-present nodes (64 per uint64 word, LSB first) and an int32 exclusive per-word prefix of
-present-node counts.  Descriptor row: R, points, plane offset, node-word offset (-1 when
-direct), cell-bitmap byte offset, F, output feature offset, direct.
+Storage (the format of odie/model.py:37-118, which checkpoints and the native runtime read):
+level l keeps only the closure of its selected cells -- every corner c, c+1, c+R, c+R+1 of a
+selected cell, wrapped into the align8(R^2) node universe -- packed into a capacity of
+`plane_node_caps[l]` rows of F_l features.  A level whose closure is its whole universe is
+addressed directly; any other through a presence bitmap (64 nodes per uint64 word, LSB first)
+and an int32 exclusive prefix count per word.  One int32 descriptor row per level, columns in
+the order DESCRIPTOR_COLUMNS, tells the kernels where everything is.
 
-The layout is host bookkeeping done at initialization and at each plane activation;
-PackedQuery runs the encode on the GPU through libodie_amd.so.
+Building a layout is host bookkeeping at initialization and at each plane activation; queries
+run on the GPU (odie_packed_forward / odie_packed_backward).
 """
 import numpy as np
 import torch
@@ -19,33 +21,33 @@ COORDINATE_VERSION = 'unit-endpoints-native-fmaf-half-cell-align8-modulo-v1'
 LAYOUT_VERSION = 'packed-xy-only-native-closure-v1'
 ADDRESSING_VERSION = 'node-bitmap64-exclusive-prefix32-v1'
 INT32_MAX = 2 ** 31 - 1
+DESCRIPTOR_COLUMNS = ('resolution', 'points', 'plane_offset', 'node_word_offset', 'bitmap_byte_offset', 'features',
+                      'feature_offset', 'direct')
+CORNERS = (0, 1)          # x offsets of a cell's corners; y offsets are the same rows of R nodes
 
 
 def align8(value):
-    return (int(value) + 7) // 8 * 8
-
-
-def router_weights(logits, activation):
-    if activation == 'sigmoid':
-        return torch.sigmoid(logits)
-    if activation == 'softplus':
-        return torch.nn.functional.softplus(logits, beta=1., threshold=20.)
-    raise ValueError('Unknown router activation: ' + activation)
+    return -(-int(value) // 8) * 8
 
 
 def gate_coarse_levels(config):
-    count = int(config.get('gate_coarse_levels_K', config['coarse_levels']))
-    if not 0 <= count <= int(config['n_levels']) or int(config['coarse_levels']) != count:
+    """K, the leading levels whose gate is fixed at one; it must equal coarse_levels and stay
+    within the declared levels (odie/model.py:25-30)."""
+    levels = int(config['n_levels'])
+    coarse = int(config['coarse_levels'])
+    k = int(config.get('gate_coarse_levels_K', coarse))
+    if k != coarse or k < 0 or k > levels:
         raise ValueError('Gate K must agree with coarse_levels and remain within declared level count')
-    return count
+    return k
 
 
 def plane_closure(support, resolution):
-    """Sorted unique closure nodes of a flat bool support of R^2 cells (int64)."""
-    support = torch.as_tensor(support)
-    cells = support.nonzero(as_tuple=True)[0]
-    nodes = torch.cat([cells, cells + 1, cells + resolution, cells + resolution + 1])
-    return torch.unique(nodes.remainder(align8(resolution ** 2)), sorted=True)
+    """Sorted unique closure nodes (CPU int64 tensor) of a flat bool support of R^2 cells."""
+    mask = np.asarray(torch.as_tensor(support).cpu().numpy(), dtype=bool)
+    cells = np.flatnonzero(mask).astype(np.int64)
+    steps = np.array([dx + dy * resolution for dy in CORNERS for dx in CORNERS], dtype=np.int64)
+    corners = (cells[:, None] + steps[None, :]).reshape(-1) % align8(resolution * resolution)
+    return torch.from_numpy(np.unique(corners))
 
 
 def make_node_index(nodes, points):
@@ -68,65 +70,90 @@ def make_node_index(nodes, points):
 
 
 def _cell_bitmap(support, points):
+    """LSB-first visibility bits of the R^2 cells, padded to the node universe."""
     padded = np.zeros(points, dtype=np.uint8)
-    padded[:support.numel()] = support.numpy().astype(np.uint8)
+    padded[:support.numel()] = support.numpy()
     return torch.from_numpy(np.packbits(padded.reshape(-1, 8), axis=1, bitorder='little').reshape(-1))
 
 
-def make_layout(config, supports, plane_dims, plane_node_caps):
-    resolutions = list(config['resolutions'])
-    if not (len(resolutions) == len(supports) == len(plane_dims) == len(plane_node_caps) == int(config['n_levels'])) \
-            or not all(f in (1, 2, 4) for f in plane_dims):
+def _check_request(config, supports, plane_dims, plane_node_caps):
+    levels = int(config['n_levels'])
+    lengths = {len(config['resolutions']), len(supports), len(plane_dims), len(plane_node_caps)}
+    if lengths != {levels} or any(f not in (1, 2, 4) for f in plane_dims):
         raise ValueError('Require aligned level descriptors and F1/F2/F4 features')
     if config['representation'] != 'xy_planes':
         raise ValueError('XY-only representation is required')
     gate_coarse_levels(config)
-    if config['gate_topology'] != 'shared' or config['gate_position'] != 'feature':
+    if (config['gate_topology'], config['gate_position']) != ('shared', 'feature'):
         raise ValueError('Preserve the shared feature gate')
-    node_bitmaps, prefixes, bitmaps, descriptors, levels, clean = [], [], [], [], [], []
-    params = feature_offset = node_word_offset = bitmap_offset = 0
-    for level, (resolution, support, dim, cap) in enumerate(zip(resolutions, supports, plane_dims, plane_node_caps)):
-        if support.device.type != 'cpu' or support.dtype != torch.bool or support.shape != (resolution ** 2,):
+
+
+class _Layout:
+    """Running offsets and the per-level pieces of one layout, filled level by level."""
+
+    def __init__(self, full_prefix):
+        self.full_prefix = full_prefix
+        self.rows, self.levels, self.supports = [], [], []
+        self.words, self.prefixes, self.cells = [], [], []
+        self.params = self.columns = self.word_count = self.cell_bytes = 0
+
+    def add(self, level, resolution, support, dim, cap):
+        if support.device.type != 'cpu' or support.dtype != torch.bool or tuple(support.shape) != (resolution ** 2,):
             raise ValueError('Support must be a flat CPU bool R^2 tensor')
-        if level < int(config['initial_active_prefix']) and not bool(support.all()):
+        if level < self.full_prefix and not bool(support.all()):
             raise ValueError('Declared initial full-cover supports must remain full')
         support = support.clone()
         points = align8(resolution ** 2)
         nodes = plane_closure(support, resolution)
         if cap % 8 or not nodes.numel() <= cap <= points:
             raise ValueError('Aligned node capacity must contain the complete interpolation closure')
-        if points > INT32_MAX or params + cap * dim > INT32_MAX:
+        if points > INT32_MAX or self.params + cap * dim > INT32_MAX:
             raise ValueError('Native points and packed offsets must fit int32 addressing')
         direct = nodes.numel() == points
-        if direct:
-            index_offset, words = -1, 0
-        else:
-            node_bitmap, prefix = make_node_index(nodes, points)
-            index_offset, words = node_word_offset, node_bitmap.numel()
-            node_bitmaps.append(node_bitmap)
-            prefixes.append(prefix)
-            node_word_offset += words
-        bitmap = _cell_bitmap(support, points)
-        descriptors.append([resolution, points, params, index_offset, bitmap_offset, dim, feature_offset, int(direct)])
-        levels.append({'level': level, 'resolution': resolution, 'plane_dim': dim,
-                       'allowed_cells': int(support.sum()), 'plane_retained_nodes': nodes.numel(),
-                       'plane_node_capacity': cap, 'plane_unused_slots': cap - nodes.numel(),
-                       'native_plane_points': points, 'plane_offset': params,
-                       'feature_offset': feature_offset, 'nodes': nodes,
-                       'node_index_words': words, 'direct_node_access': direct})
-        bitmaps.append(bitmap)
-        clean.append(support)
-        params += cap * dim
-        feature_offset += dim
-        bitmap_offset += bitmap.numel()
-    return {'descriptors': torch.tensor(descriptors, dtype=torch.int32),
-            'node_bitmap': torch.cat(node_bitmaps) if node_bitmaps else torch.empty(0, dtype=torch.uint64),
-            'node_prefix': torch.cat(prefixes) if prefixes else torch.empty(0, dtype=torch.int32),
-            'bitmap': torch.cat(bitmaps), 'levels': levels, 'supports': clean,
-            'params': params, 'input_width': feature_offset}
+        word_offset, words = -1, 0
+        if not direct:
+            bitmap, prefix = make_node_index(nodes, points)
+            word_offset, words = self.word_count, bitmap.numel()
+            self.words.append(bitmap)
+            self.prefixes.append(prefix)
+            self.word_count += words
+        cells = _cell_bitmap(support, points)
+        self.rows.append((resolution, points, self.params, word_offset, self.cell_bytes, dim, self.columns,
+                          int(direct)))
+        # the per-level record the reference writes into its storage statistics
+        self.levels.append(dict(level=level, resolution=resolution, plane_dim=dim,
+                                allowed_cells=int(support.sum()), plane_retained_nodes=nodes.numel(),
+                                plane_node_capacity=cap, plane_unused_slots=cap - nodes.numel(),
+                                native_plane_points=points, plane_offset=self.params,
+                                feature_offset=self.columns, nodes=nodes, node_index_words=words,
+                                direct_node_access=direct))
+        self.cells.append(cells)
+        self.supports.append(support)
+        self.params += cap * dim
+        self.columns += dim
+        self.cell_bytes += cells.numel()
+
+    def result(self):
+        def joined(parts, dtype):
+            return torch.cat(parts) if parts else torch.empty(0, dtype=dtype)
+        return {'descriptors': torch.tensor(self.rows, dtype=torch.int32),
+                'node_bitmap': joined(self.words, torch.uint64), 'node_prefix': joined(self.prefixes, torch.int32),
+                'bitmap': torch.cat(self.cells), 'levels': self.levels, 'supports': self.supports,
+                'params': self.params, 'input_width': self.columns}
 
 
-def _device_layout(tensor):
+def make_layout(config, supports, plane_dims, plane_node_caps):
+    """Descriptors, addressing buffers and per-level records of the packed planes
+    (odie/model.py:64-118)."""
+    _check_request(config, supports, plane_dims, plane_node_caps)
+    layout = _Layout(int(config['initial_active_prefix']))
+    for level, args in enumerate(zip(config['resolutions'], supports, plane_dims, plane_node_caps)):
+        layout.add(level, *args)
+    return layout.result()
+
+
+def _nonempty(tensor):
+    """A device buffer is never empty: the kernels take a pointer even when a level needs none."""
     return tensor if tensor.numel() else torch.zeros(1, dtype=tensor.dtype, device=tensor.device)
 
 
@@ -142,7 +169,7 @@ def packed_forward(coordinates, grid, descriptors, node_bitmap, node_prefix, bit
     visibility = torch.empty((n, levels), dtype=torch.bool, device=coordinates.device)
     _lib.check(_lib.library().odie_packed_forward(
         coordinates.data_ptr(), n, grid.data_ptr(), grid.numel(), descriptors.data_ptr(), levels,
-        _device_layout(node_bitmap).data_ptr(), _device_layout(node_prefix).data_ptr(), bitmap.data_ptr(), width,
+        _nonempty(node_bitmap).data_ptr(), _nonempty(node_prefix).data_ptr(), bitmap.data_ptr(), width,
         features.data_ptr(), visibility.data_ptr(), _lib.stream_of(coordinates)))
     return features, visibility
 
@@ -155,14 +182,15 @@ def packed_backward(coordinates, upstream, descriptors, node_bitmap, node_prefix
     gradient = torch.empty(parameter_count, dtype=torch.float32, device=coordinates.device)
     _lib.check(_lib.library().odie_packed_backward(
         coordinates.data_ptr(), coordinates.shape[0], upstream.data_ptr(), upstream.shape[1],
-        descriptors.data_ptr(), descriptors.shape[0], _device_layout(node_bitmap).data_ptr(),
-        _device_layout(node_prefix).data_ptr(), bitmap.data_ptr(), gradient.data_ptr(), parameter_count,
+        descriptors.data_ptr(), descriptors.shape[0], _nonempty(node_bitmap).data_ptr(),
+        _nonempty(node_prefix).data_ptr(), bitmap.data_ptr(), gradient.data_ptr(), parameter_count,
         _lib.stream_of(coordinates)))
     return gradient
 
 
 class PackedQuery(torch.autograd.Function):
-    """Same contract as odie/model.py:137-151."""
+    """Same contract as odie/model.py:137-151: features and visibility forward, the fp32 grid
+    gradient backward."""
 
     @staticmethod
     def forward(ctx, coordinates, grid, descriptors, node_bitmap, node_prefix, bitmap, width):
@@ -180,36 +208,40 @@ class PackedQuery(torch.autograd.Function):
         return None, gradient, None, None, None, None, None
 
 
-class PackedPlanes:
-    """The packed xy-plane grid of PackedXYPlanes (odie/model.py:154-262) without its TCNN heads:
-    fp32 master `grid` in packed storage, the layout's addressing buffers on the device, the
-    active prefix, and the activation of the next plane's support.
+def plane_seed(seed, level):
+    """Seed of level l's feature draws (odie/model.py:211-212)."""
+    return (seed + 1000003 * (level + 1) + 104729 * 3) % (2 ** 31)
 
-    Plane values are inputs of the path (odie/model.py:208-224 draws them from a CUDA generator
-    stream); here a plane's native nodes draw N(0, feature_init_std) from the counter PRNG of
-    odie_amd.synth under the same per-level seed, so a plane is initialized exactly once and
-    identically on every machine.
+
+class PackedPlanes:
+    """The packed planes of PackedXYPlanes without its heads: fp32 master `grid` in packed
+    storage, the layout's addressing buffers on the device, the active prefix, and the
+    activation of the next plane's support (odie/model.py:154-262).
+
+    Plane values are inputs of the path: a plane's native nodes draw N(0, feature_init_std) from
+    the counter PRNG of odie_amd.synth under the level's seed, max(2, F) values per node of
+    which the first F are kept, so a plane is initialized exactly once and identically on every
+    machine.
     """
 
     def __init__(self, config, supports, plane_dims, plane_node_caps, device='cuda'):
         self.config = dict(config)
-        self.layout = make_layout(self.config, supports, plane_dims, plane_node_caps)
-        self.supports = self.layout['supports']
         self.plane_dims, self.plane_node_caps = list(plane_dims), list(plane_node_caps)
         self.n_levels = int(self.config['n_levels'])
-        self.input_width = self.layout['input_width']
         self.device = torch.device(device)
+        self._install(make_layout(self.config, supports, plane_dims, plane_node_caps))
+        self.input_width = self.layout['input_width']
         self.grid = torch.zeros(self.layout['params'], dtype=torch.float32, device=self.device)
         self.initialized_planes = [False] * self.n_levels
         for level, item in enumerate(self.layout['levels']):
             if item['nodes'].numel():
                 self._initialize_plane(level)
-        self._upload(self.layout)
         self.active_prefix = int(self.config.get('initial_active_prefix', self.n_levels))
 
-    def _upload(self, layout):
+    def _install(self, layout):
+        self.layout, self.supports = layout, layout['supports']
         for name in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap'):
-            setattr(self, name, _device_layout(layout[name]).to(self.device))
+            setattr(self, name, _nonempty(layout[name]).to(self.device))
 
     @torch.no_grad()
     def _initialize_plane(self, level):
@@ -217,20 +249,19 @@ class PackedPlanes:
         if self.initialized_planes[level]:
             raise RuntimeError('Each plane must be initialized exactly once')
         item = self.layout['levels'][level]
-        level_seed = (self.config['seed'] + 1000003 * (level + 1)) % (2 ** 31)
-        branch_seed = (level_seed + 104729 * 3) % (2 ** 31)
-        width = max(2, item['plane_dim'])
-        draws = synth.normal(branch_seed, 'plane', item['native_plane_points'] * width).reshape(-1, width)
-        nodes = item['nodes'].numpy()
-        values = (draws[nodes, :item['plane_dim']] * float(self.config['feature_init_std'])).astype(np.float32)
-        offset = item['plane_offset']
-        self.grid[offset:offset + values.size].copy_(torch.from_numpy(values.reshape(-1)))
+        draws = max(2, item['plane_dim'])
+        values = synth.normal(plane_seed(int(self.config['seed']), level), 'plane',
+                              item['native_plane_points'] * draws).reshape(-1, draws)
+        chosen = values[item['nodes'].numpy(), :item['plane_dim']] * float(self.config['feature_init_std'])
+        start = item['plane_offset']
+        flat = torch.from_numpy(chosen.astype(np.float32).reshape(-1))
+        self.grid[start:start + flat.numel()].copy_(flat)
         self.initialized_planes[level] = True
 
     @torch.no_grad()
     def activate_support(self, level, support):
-        """Add only the next unopened plane, retaining packed storage and offsets
-        (odie/model.py:226-257): same checks, same record."""
+        """Open the next plane with `support`, keeping the packed storage and every offset
+        (odie/model.py:226-257); returns the reference's activation record."""
         if level != self.active_prefix or not 2 <= level < self.n_levels:
             raise ValueError('Select the next unopened plane before advancing the prefix')
         if self.initialized_planes[level] or bool(self.supports[level].any()):
@@ -238,23 +269,19 @@ class PackedPlanes:
         resolution = self.config['resolutions'][level]
         if support.device.type != 'cpu' or support.dtype != torch.bool or support.shape != (resolution ** 2,):
             raise ValueError('New support must be a flat CPU bool R^2 tensor')
-        nodes = plane_closure(support, resolution)
-        cap = self.plane_node_caps[level]
-        if not 0 < nodes.numel() <= cap:
+        selected = plane_closure(support, resolution).numel()
+        if not 0 < selected <= self.plane_node_caps[level]:
             raise ValueError('New support requires a nonempty complete closure within its cap')
-        storage_pointer = self.grid.data_ptr()
-        updated = list(self.supports)
-        updated[level] = support.clone()
-        layout = make_layout(self.config, updated, self.plane_dims, self.plane_node_caps)
-        self._upload(layout)
-        self.layout, self.supports = layout, layout['supports']
-        points = layout['levels'][level]['native_plane_points']
+        storage = self.grid.data_ptr()
+        supports = [s if l != level else support.clone() for l, s in enumerate(self.supports)]
+        self._install(make_layout(self.config, supports, self.plane_dims, self.plane_node_caps))
         self._initialize_plane(level)
-        if self.grid.data_ptr() != storage_pointer:
+        if self.grid.data_ptr() != storage:
             raise AssertionError('Packed storage changed during plane activation')
+        points = self.layout['levels'][level]['native_plane_points']
         return {'level': level, 'initialized_once': True, 'grid_storage_unchanged': True,
-                'original_dense_f2_seed': (self.config['seed'] + 1000003 * (level + 1) + 104729 * 3) % (2 ** 31),
-                'native_dense_draw_shape': [points, max(2, self.plane_dims[level])], 'selected_nodes': nodes.numel()}
+                'original_dense_f2_seed': plane_seed(int(self.config['seed']), level),
+                'native_dense_draw_shape': [points, max(2, self.plane_dims[level])], 'selected_nodes': selected}
 
     def set_active_prefix(self, prefix):
         if not isinstance(prefix, int) or not 2 <= prefix <= self.n_levels:
@@ -270,84 +297,112 @@ class PackedPlanes:
                                  self.node_prefix, self.bitmap, self.input_width)
 
 
-# tiny-cuda-nn's seeds for the two heads (odie/model.py:191-193)
+# seeds of the two heads (odie/model.py:191-193)
 GATE_SEED, DECODER_SEED = 2000003, 4000037
 
 
+def make_heads(config, plane_dims, router_enabled, coarse, device):
+    """(gate or None, decoder) for rows of the levels' features padded to align16 columns, seeded
+    as the reference seeds its heads."""
+    from .decoder import Decoder
+    from .gate import Gate
+    width = (sum(plane_dims) + 15) // 16 * 16
+    if width > 80:
+        raise ValueError('the heads take at most 80 feature columns')
+    seed = int(config['seed'])
+    gate = (Gate(seed=(seed + GATE_SEED) % 2 ** 31, coarse=coarse,
+                 activation=config.get('router_output_activation', 'sigmoid'), device=device, features=plane_dims)
+            if router_enabled else None)
+    return gate, Decoder(seed=(seed + DECODER_SEED) % 2 ** 31, device=device, width=width)
+
+
+def heads_match(config, gate, decoder):
+    """The head sizes equal the configuration's gate_parameters / decoder_parameters."""
+    gate_size = gate.params.numel() if gate is not None else 0
+    return gate_size == config['gate_parameters'] and decoder.params.numel() == config['decoder_parameters']
+
+
+def decode_rows(raw, gate, decoder, visible=None):
+    """The heads on raw features [N, sum F] fp16: columns padded with ones to the decoder's
+    width, gated per level when there is a gate, decoded; RGB fp32 [N, 3]."""
+    rows = torch.ones((raw.shape[0], decoder.width), dtype=torch.float16, device=raw.device)
+    rows[:, :raw.shape[1]] = raw
+    decoder.sync_weights()
+    if gate is not None:
+        gate.sync_weights()
+        rows, _ = gate.forward(rows, visible=visible)
+    return decoder.forward(rows).float()[:, :3]
+
+
+def head_storage(grid_params, gate, decoder):
+    """The parameter and byte counts both models report (odie/model.py:281-314,
+    odie/hash_grid.py:64-80): fp16 payload, fp32 masters and Adam moments of grid and heads."""
+    gate_params = gate.params.numel() if gate is not None else 0
+    decoder_params = decoder.params.numel()
+    total = grid_params + gate_params + decoder_params
+    return {'actual_params': total, 'grid_params': grid_params, 'head_params': gate_params + decoder_params,
+            'gate_params': gate_params, 'decoder_params': decoder_params}, \
+        {'fp16_parameter_payload_bytes': 2 * total, 'fp32_master_bytes': 4 * total, 'adam_moment_bytes': 8 * total}
+
+
 class PackedXYPlanes(PackedPlanes):
-    """The on-demand model (odie/model.py:154-262): the packed planes with the router gate and the
-    decoder (Gate / Decoder, fp32 masters in `params`), 16 levels of 2 features (the width this
-    library's heads and runtime are built for).  forward(coordinates) is the reference's
-    evaluation path (odie/model.py:266-279): query, mask the levels past the active prefix, gate
-    by level with visibility, decode, first 3 outputs as fp32; it runs without autograd, training
-    goes through NativeOptimizer."""
+    """The on-demand model (odie/model.py:154-314): packed planes of F1/F2/F4 levels (2..20 of
+    them, at most 80 feature columns) with the router gate and the decoder (Gate / Decoder, fp32
+    masters in `params`).  forward(coordinates) is the reference's evaluation path
+    (odie/model.py:266-279) -- query, zero the levels past the active prefix, gate by level with
+    visibility, decode, first 3 outputs as fp32 -- run without autograd; training goes through
+    NativeOptimizer."""
 
     def __init__(self, config, supports, plane_dims, plane_node_caps, axis_mode='none', kernel_a=0.,
                  kernel_omega=1.5 * np.pi, device='cuda'):
         if axis_mode != 'none' or kernel_a != 0.:
             raise ValueError('No axis branches or non-linear interpolation kernel in this ablation')
-        from .decoder import Decoder, LEVELS, PARAMETERS as DECODER_PARAMETERS
-        if list(plane_dims) != [2] * LEVELS or int(config['n_levels']) != LEVELS:
-            raise ValueError('PackedXYPlanes runs %d levels of 2 features (the width of the heads)' % LEVELS)
         super().__init__(config, supports, plane_dims, plane_node_caps, device=device)
-        from .gate import Gate, PARAMETERS as GATE_PARAMETERS
         self.router_enabled = bool(config.get('router_enabled', True))
         self.gate_coarse_levels_K = gate_coarse_levels(config)
-        seed = int(config['seed'])
-        if ((GATE_PARAMETERS if self.router_enabled else 0) != config['gate_parameters'] or
-                DECODER_PARAMETERS != config['decoder_parameters']):
+        self.gate, self.decoder = make_heads(config, plane_dims, self.router_enabled, self.gate_coarse_levels_K,
+                                             device)
+        if not heads_match(config, self.gate, self.decoder):
             raise RuntimeError('Unexpected TCNN head allocation for the configured input width')
-        self.gate = (Gate(seed=(seed + GATE_SEED) % 2 ** 31, coarse=self.gate_coarse_levels_K,
-                          activation=config.get('router_output_activation', 'sigmoid'), device=device)
-                     if self.router_enabled else None)
-        self.decoder = Decoder(seed=(seed + DECODER_SEED) % 2 ** 31, device=device)
+        self.feature_levels = torch.tensor([l for l, f in enumerate(plane_dims) for _ in range(f)],
+                                           dtype=torch.int64, device=self.device)
 
     def forward(self, coordinates):
         with torch.no_grad():
             raw, visible = self.query_features(coordinates)
-            level = torch.arange(self.n_levels, device=raw.device)
-            active = level < self.active_prefix
-            raw = raw * active.repeat_interleave(2).to(raw.dtype)
-            self.decoder.sync_weights()
-            if self.gate is None:
-                return self.decoder.forward(raw).float()[:, :3]
-            self.gate.sync_weights()
-            # levels at or below K keep a gate of one; a prefix within them gates nothing else
-            weighted, _ = self.gate.forward(raw, visible=(visible & active).to(torch.uint8).contiguous())
-            return self.decoder.forward(weighted).float()[:, :3]
+            active = torch.arange(self.n_levels, device=raw.device) < self.active_prefix
+            raw = raw * active[self.feature_levels].to(raw.dtype)
+            visible = (visible & active).to(torch.uint8).contiguous()
+            return decode_rows(raw, self.gate, self.decoder, visible=visible)
 
     __call__ = forward
 
     def storage_stats(self):
-        grid = self.grid.numel()
-        gate = self.gate.params.numel() if self.gate is not None else 0
-        heads = gate + self.decoder.params.numel()
-        size = lambda t: t.numel() * t.element_size()
-        node_bitmaps, prefixes, bitmaps = size(self.node_bitmap), size(self.node_prefix), size(self.bitmap)
-        descriptors = size(self.descriptors)
-        gate_index = self.input_width * 8                     # the int64 feature -> level index
-        active_flags = self.n_levels + 2 * self.input_width   # bool per level, fp16 per feature
-        return {'actual_params': grid + heads, 'grid_params': grid, 'head_params': heads,
-                'gate_params': gate, 'decoder_params': self.decoder.params.numel(),
-                'router_enabled': self.router_enabled, 'axis_params': 0, 'plane_params': grid,
-                'plane_caps': self.plane_node_caps, 'fp16_parameter_payload_bytes': 2 * (grid + heads),
-                'fp32_master_bytes': 4 * (grid + heads), 'adam_moment_bytes': 8 * (grid + heads),
-                'full_gradient_bytes': 4 * (grid + heads), 'index_bytes': node_bitmaps + prefixes,
-                'node_bitmap_bytes': node_bitmaps, 'node_prefix_bytes': prefixes, 'bitmap_bytes': bitmaps,
-                'descriptor_bytes': descriptors,
-                'runtime_index_bytes': node_bitmaps + prefixes + bitmaps + descriptors + gate_index + active_flags,
-                'active_flag_bytes': active_flags, 'input_width': self.input_width,
-                'native_input_padding': (self.input_width + 15) // 16 * 16, 'axis_mode': 'none',
-                'active_layers_from_update1': int(self.config.get('initial_active_prefix', 2)),
-                'active_prefix': self.active_prefix, 'gate_coarse_levels_K': self.gate_coarse_levels_K,
-                'full_cover_coarse_layers': self.config.get('full_cover_coarse_layers', [0, 1]),
-                'plane_dims': self.plane_dims,
-                'coordinate_version': COORDINATE_VERSION, 'layout_version': LAYOUT_VERSION,
-                'addressing_version': ADDRESSING_VERSION, 'query_cuda_launches': 1, 'backward_cuda_launches': 1,
-                'forward_precision': 'P01 FP32 geometry and FP16 interpolation chain',
-                'gradient_precision': 'FP16 feature gradient, FP32 interpolation weights and atomicAdd',
-                'levels': [{key: value for key, value in level.items() if key != 'nodes'}
-                           for level in self.layout['levels']]}
+        counts, bytes_ = head_storage(self.grid.numel(), self.gate, self.decoder)
+        size = {name: getattr(self, name).numel() * getattr(self, name).element_size()
+                for name in ('node_bitmap', 'node_prefix', 'bitmap', 'descriptors')}
+        index = size['node_bitmap'] + size['node_prefix']
+        flags = self.n_levels + 2 * self.input_width      # a bool per level, an fp16 per feature column
+        lookup = 8 * self.input_width                      # the int64 feature -> level index
+        stats = dict(counts, router_enabled=self.router_enabled, axis_params=0, plane_params=counts['grid_params'],
+                     plane_caps=self.plane_node_caps, **bytes_,
+                     full_gradient_bytes=4 * counts['actual_params'], index_bytes=index,
+                     node_bitmap_bytes=size['node_bitmap'], node_prefix_bytes=size['node_prefix'],
+                     bitmap_bytes=size['bitmap'], descriptor_bytes=size['descriptors'],
+                     runtime_index_bytes=index + size['bitmap'] + size['descriptors'] + lookup + flags,
+                     active_flag_bytes=flags, input_width=self.input_width,
+                     native_input_padding=(self.input_width + 15) // 16 * 16, axis_mode='none',
+                     active_layers_from_update1=int(self.config.get('initial_active_prefix', 2)),
+                     active_prefix=self.active_prefix, gate_coarse_levels_K=self.gate_coarse_levels_K,
+                     full_cover_coarse_layers=self.config.get('full_cover_coarse_layers', [0, 1]),
+                     plane_dims=self.plane_dims, coordinate_version=COORDINATE_VERSION,
+                     layout_version=LAYOUT_VERSION, addressing_version=ADDRESSING_VERSION,
+                     query_cuda_launches=1, backward_cuda_launches=1,
+                     forward_precision='P01 FP32 geometry and FP16 interpolation chain',
+                     gradient_precision='FP16 feature gradient, FP32 interpolation weights and atomicAdd')
+        stats['levels'] = [{key: value for key, value in item.items() if key != 'nodes'}
+                           for item in self.layout['levels']]
+        return stats
 
 
 def build_model(config, supports, plane_dims, plane_node_caps, **kwargs):

@@ -1,13 +1,10 @@
-"""Host-side geometry of the selection path and the GPU top-k.
+"""Selection-side geometry and the GPU selectors: the residual's cell bounds, closure checks,
+top-k and the B2 exact greedy (odie/selection.py, odie/gpu_residual.py:75-179).
 
-native_thresholds restates odie/selection.py:16-42: for each region 1..R-1 the smallest fp32
-x in [0,1] with floor(fma(R-1, x, 0.5)) >= region, found by binary search over fp32 bit
-patterns against the exact rational rounding boundary of the fused result.  It is host set-up
-(the column/row bounds of the residual's cells), computed once per resolution.
+The cell bounds come from the encode's own geometry evaluated on the device (odie_cell_bounds):
+a pixel's cell is floor(fmaf(R-1, x, 0.5)) of its coordinate, as odie/selection.py:16-55 defines
+the map through fp32 thresholds.
 """
-from functools import lru_cache
-import struct
-
 import numpy as np
 import torch
 
@@ -18,45 +15,18 @@ def align8(value):
     return (int(value) + 7) // 8 * 8
 
 
-def _float_from_bits(bits):
-    return struct.unpack('<f', struct.pack('<I', bits))[0]
-
-
-@lru_cache(maxsize=128)
-def native_thresholds(resolution):
+def cell_bounds(shape, resolution, device='cuda'):
+    """(xb, yb, ymap): first pixel column/row of every native cell column/row, [R+1] int32 each
+    (odie/gpu_residual.py:49-62), and the cell row of every pixel row."""
+    height, width = shape
     if type(resolution) is not int or not 2 <= resolution <= 2 ** 23:
         raise ValueError('Resolution must be an integer between 2 and 2^23')
-    scale = resolution - 1
-    out = []
-    for region in range(1, resolution):
-        region_bits = struct.unpack('<I', struct.pack('<f', region))[0]
-        # fma rounds up to `region` once scale*x + 0.5 passes the midpoint between `region`
-        # and its fp32 predecessor; ties round to the even neighbour.
-        below_num, below_den = _float_from_bits(region_bits - 1).as_integer_ratio()
-        boundary_num = (region - 1) * below_den + below_num
-        boundary_den = 2 * below_den
-        even = region_bits % 2 == 0
-        lower, upper = 0, 0x3F800000
-        while lower < upper:
-            middle = (lower + upper) // 2
-            numerator, denominator = _float_from_bits(middle).as_integer_ratio()
-            left, right = scale * numerator * boundary_den, boundary_num * denominator
-            if left > right or (left == right and even):
-                upper = middle
-            else:
-                lower = middle + 1
-        out.append(_float_from_bits(lower))
-    return tuple(out)
-
-
-def cell_bounds(shape, resolution):
-    """(xb, yb): first pixel column/row of every native cell column/row (odie/gpu_residual.py:49-62)."""
-    height, width = shape
-    thresholds = np.asarray(native_thresholds(resolution), dtype=np.float32)
-    xmap = np.searchsorted(thresholds, np.arange(width, dtype=np.float32) / np.float32(width - 1), side='right')
-    ymap = np.searchsorted(thresholds, np.arange(height, dtype=np.float32) / np.float32(height - 1), side='right')
-    bounds = np.arange(resolution + 1)
-    return (np.searchsorted(xmap, bounds).astype(np.int32), np.searchsorted(ymap, bounds).astype(np.int32), ymap)
+    xb = torch.empty(resolution + 1, dtype=torch.int32, device=device)
+    yb = torch.empty(resolution + 1, dtype=torch.int32, device=device)
+    _lib.check(_lib.library().odie_cell_bounds(width, height, resolution, xb.data_ptr(), yb.data_ptr(),
+                                               _lib.stream_of(xb)))
+    xb, yb = xb.cpu().numpy(), yb.cpu().numpy()
+    return xb, yb, np.repeat(np.arange(resolution), np.diff(yb))
 
 
 def closure_nodes(cells, resolution):

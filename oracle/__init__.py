@@ -423,18 +423,28 @@ def route(ids, width, height, regions_x, regions_y):
 
 
 # --------------------------------------------------------------------------------------------
-# Decoder MLP 32 -> 64 -> 64 -> 16 (the FullyFusedMLP head, odie/hash_grid.py:32-34) and the
-# step's loss (odie/native/runtime.cu:53-63).  Weights: fp16 [7168] = W1 [64][32] | W2 [64][64]
-# | W3 [16][64], row-major [out][in].  Layers are computed in float64 and rounded once to fp16;
-# TCNN's own accumulation order is not restated (parity tolerance covers fp32 accumulation).
+# Decoder MLP width -> 64 -> 64 -> 16 (the FullyFusedMLP head, odie/hash_grid.py:32-34, with
+# n_input_dims W = align16 of the grid's features, odie/native/runtime.cu:17,190) and the step's
+# loss (odie/native/runtime.cu:53-63).  Weights: fp16 [64*W + 5120] = W1 [64][W] | W2 [64][64] |
+# W3 [16][64], row-major [out][in] (7168 at W = 32).  Layers are computed in float64 and rounded
+# once to fp16; TCNN's own accumulation order is not restated (parity tolerance covers fp32
+# accumulation).
 
 MLP_SHAPES = ((64, 32), (64, 64), (16, 64))
 
 
+def mlp_shapes(width=32):
+    return ((64, width), (64, 64), (16, 64))
+
+
 def mlp_weights(flat16):
+    """(W1, W2, W3) of a flat fp16 weight vector; the input width follows from its size."""
     flat16 = np.asarray(flat16, dtype=np.float16)
+    width, rest = divmod(flat16.size - 64 * 64 - 16 * 64, 64)
+    if rest or width < 1:
+        raise ValueError('decoder weights must hold 64*W + 5120 values')
     out, start = [], 0
-    for rows, cols in MLP_SHAPES:
+    for rows, cols in mlp_shapes(width):
         out.append(flat16[start:start + rows * cols].reshape(rows, cols))
         start += rows * cols
     return out
@@ -529,28 +539,38 @@ def mlp_step_f32(x16, flat16, targets, inputs, real, threads=1):
 
 
 # --------------------------------------------------------------------------------------------
-# Router gate (odie/native/runtime.cu:64-92,99-103; odie/model.py:17-22): gate MLP 32 -> 32 -> 16
-# (ReLU, no bias), s = 1 below `coarse`, else sigmoid / softplus of the fp16 logit; features of
-# level l scaled by fp16(s * visible).  Weights fp16 [1536] = Wg1 [32][32] | Wg2 [16][32].
+# Router gate (odie/native/runtime.cu:64-92,99-103; odie/model.py:17-22): gate MLP W -> 32 -> G
+# (ReLU, no bias; G = align16(levels)), s = 1 below `coarse`, else sigmoid / softplus of the fp16
+# logit; the `features[l]` columns of level l (in level order) scaled by fp16(s * visible), columns
+# past the levels' features set to 1.  Weights fp16 [32*W + 32*G] = Wg1 [32][W] | Wg2 [G][32]
+# (1536 for 16 levels of 2 features).
 
 GATE_SHAPES = ((32, 32), (16, 32))
 
 
-def gate_weights(flat16):
+def _levels_of(features):
+    return [l for l, f in enumerate(features) for _ in range(f)]
+
+
+def gate_weights(flat16, levels=16):
     flat16 = np.asarray(flat16, dtype=np.float16)
-    return flat16[:1024].reshape(32, 32), flat16[1024:1536].reshape(16, 32)
+    outputs = (levels + 15) // 16 * 16
+    width, rest = divmod(flat16.size - 32 * outputs, 32)
+    if rest or width < 1:
+        raise ValueError('gate weights must hold 32*W + 32*align16(levels) values')
+    return flat16[:32 * width].reshape(32, width), flat16[32 * width:].reshape(outputs, 32)
 
 
-def gate_logits(x16, flat16):
-    """(hidden fp16 [n, 32], logits fp16 [n, 16], magnitude bound of the logits)."""
-    w1, w2 = gate_weights(flat16)
+def gate_logits(x16, flat16, levels=16):
+    """(hidden fp16 [n, 32], logits fp16 [n, G], magnitude bound of the logits)."""
+    w1, w2 = gate_weights(flat16, levels)
     h, _ = mlp_layer(x16, w1, True)
     z, magnitude = mlp_layer(h, w2, False)
     return h, z, magnitude
 
 
 def gate_values(z16, coarse, softplus=False):
-    """s fp32 [n, 16] from fp16 logits (odie/native/runtime.cu:72); libm exp in float64, rounded."""
+    """s fp32 [n, G] from fp16 logits (odie/native/runtime.cu:72); libm exp in float64, rounded."""
     z = np.asarray(z16, dtype=np.float16).astype(np.float64)
     if softplus:
         s = np.where(z > 20.0, z, np.log1p(np.exp(z)))
@@ -561,27 +581,41 @@ def gate_values(z16, coarse, softplus=False):
     return s
 
 
-def gate_apply(x16, s, visible=None):
-    """weighted fp16 [n, 32]: feature 2l + c times fp16(s_l * visible_l) (one fp16 rounding)."""
-    s = np.asarray(s, dtype=np.float32)
-    vis = np.ones_like(s) if visible is None else np.asarray(visible, dtype=np.float32)
-    weight = (s * vis).astype(np.float16)
-    per_feature = np.repeat(weight, 2, axis=1).astype(np.float64)
-    return (np.asarray(x16, dtype=np.float16).astype(np.float64) * per_feature).astype(np.float16)
-
-
-def gate_back(x16, value16, s, coarse, softplus=False, visible=None):
-    """parallel_gate_back (odie/native/runtime.cu:77-91): direct fp16 [n, 32] and da fp16 [n, 16]
-    (loss scale 128 x value's scale), every fp16 operation one rounding of the exact result."""
-    x = np.asarray(x16, dtype=np.float16).astype(np.float64)
-    value = np.asarray(value16, dtype=np.float16).astype(np.float64)
-    s = np.asarray(s, dtype=np.float32)
+def gate_apply(x16, s, visible=None, features=None):
+    """weighted fp16 [n, W]: each column of level l times fp16(s_l * visible_l) (one fp16
+    rounding), columns past the levels' features 1."""
+    features = [2] * 16 if features is None else list(features)
+    s = np.asarray(s, dtype=np.float32)[:, :len(features)]
     vis = np.ones_like(s) if visible is None else np.asarray(visible, dtype=np.float32)
     weight = (s * vis).astype(np.float16).astype(np.float64)
-    direct = (value * np.repeat(weight, 2, axis=1)).astype(np.float16)
+    x = np.asarray(x16, dtype=np.float16).astype(np.float64)
+    out = np.ones(x.shape, dtype=np.float16)
+    columns = len(_levels_of(features))
+    out[:, :columns] = (x[:, :columns] * weight[:, _levels_of(features)]).astype(np.float16)
+    return out
+
+
+def gate_back(x16, value16, s, coarse, softplus=False, visible=None, features=None):
+    """parallel_gate_back (odie/native/runtime.cu:77-91): direct fp16 [n, W] (0 past the levels'
+    features) and da fp16 [n, L] (loss scale 128 x value's scale), every fp16 operation one
+    rounding of the exact result; a level's products are summed in column order from 0."""
+    features = [2] * 16 if features is None else list(features)
+    levels = len(features)
+    x = np.asarray(x16, dtype=np.float16).astype(np.float64)
+    value = np.asarray(value16, dtype=np.float16).astype(np.float64)
+    s = np.asarray(s, dtype=np.float32)[:, :levels]
+    vis = np.ones_like(s) if visible is None else np.asarray(visible, dtype=np.float32)
+    weight = (s * vis).astype(np.float16).astype(np.float64)
+    columns = _levels_of(features)
+    direct = np.zeros(x.shape, dtype=np.float16)
+    direct[:, :len(columns)] = (value[:, :len(columns)] * weight[:, columns]).astype(np.float16)
     products = (value * x).astype(np.float16).astype(np.float64)
-    reduced = (products[:, 0::2] + 0.0).astype(np.float16).astype(np.float64)   # 0 + first product
-    reduced = (reduced + products[:, 1::2]).astype(np.float16)
+    reduced = np.zeros(s.shape, dtype=np.float64)
+    start = 0
+    for level, count in enumerate(features):
+        for c in range(start, start + count):
+            reduced[:, level] = (reduced[:, level] + products[:, c]).astype(np.float16).astype(np.float64)
+        start += count
     incoming = reduced.astype(np.float32) * vis
     if softplus:
         derivative = incoming * (-np.expm1(-s.astype(np.float64))).astype(np.float32)
@@ -593,11 +627,15 @@ def gate_back(x16, value16, s, coarse, softplus=False, visible=None):
     return direct, da
 
 
-def gate_mlp_backward(x16, h16, da16, flat16):
-    """Gate MLP backward from the given hidden activations: d(raw) fp16 [n, 32] with its
-    magnitude bound, weight gradients float64 [1536] with theirs."""
-    w1, w2 = (w.astype(np.float64) for w in gate_weights(flat16))
-    x, h, da = (np.asarray(v, dtype=np.float16).astype(np.float64) for v in (x16, h16, da16))
+def gate_mlp_backward(x16, h16, da16, flat16, levels=16):
+    """Gate MLP backward from the given hidden activations and da [n, L] (zero for the logits past
+    L): d(raw) fp16 [n, W] with its magnitude bound, weight gradients float64 [32*W + 32*G] with
+    theirs."""
+    w1, w2 = (w.astype(np.float64) for w in gate_weights(flat16, levels))
+    x, h = (np.asarray(v, dtype=np.float16).astype(np.float64) for v in (x16, h16))
+    da = np.zeros((x.shape[0], w2.shape[0]))
+    given = np.asarray(da16, dtype=np.float16).astype(np.float64)
+    da[:, :given.shape[1]] = given
     dh = np.where(h > 0, da @ w2, 0.0).astype(np.float16).astype(np.float64)
     m1 = np.where(h > 0, np.abs(da) @ np.abs(w2), 0.0)
     dr = (dh @ w1).astype(np.float16)

@@ -101,11 +101,15 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert native.odie_adam_step(16, None, 16, 0, 16, 16, None, 10, 2, 1, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
     assert 'null' in native.odie_error().decode()     # variants 1 and 2 need the ages
     # decoder MLP: alignment, targets
-    assert native.odie_mlp_forward(8, 10, 16, 16, 0) == -1 and 'aligned' in native.odie_error().decode()
-    assert native.odie_mlp_train(16, 10, 10, 16, None, None, None, None, None, None, None, None, 16, 16, 0) == -1
+    assert native.odie_mlp_forward(8, 10, 32, 16, 16, 0) == -1 and 'aligned' in native.odie_error().decode()
+    assert native.odie_mlp_forward(16, 10, 24, 16, 16, 0) == -1 and 'width' in native.odie_error().decode()
+    assert native.odie_mlp_forward(16, 10, 96, 16, 16, 0) == -1 and 'width' in native.odie_error().decode()
+    assert native.odie_mlp_train(16, 10, 32, 10, 16, None, None, None, None, None, None, None, None, 16, 16, 0) == -1
     assert 'target' in native.odie_error().decode()
-    assert native.odie_mlp_train(16, 10, 0, 16, None, None, None, 16, None, None, None, None, 16, 16, 0) == -1
+    assert native.odie_mlp_train(16, 10, 32, 0, 16, None, None, None, 16, None, None, None, None, 16, 16, 0) == -1
     assert 'real' in native.odie_error().decode()
+    assert native.odie_mlp_train(16, 1 << 26, 80, 1, 16, 16, None, None, None, None, None, None, None, 16, 16, 0) == -1
+    assert '2^31' in native.odie_error().decode()
     assert native.odie_mlp_train_planes(16, 10, 10, 16, 16, None, None, None, None, None, None, None, None, 16, 16,
                                         0) == -1
     assert 'planes is null' in native.odie_error().decode()
@@ -123,11 +127,24 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert 'planes and blockmax must be' in native.odie_error().decode()
     assert native.odie_grid_backward_adam_planes(16, 10, None, 1, 16, 16, entries, levels, 16, 1, *adam) == -1
     assert '2 fp16 features' in native.odie_error().decode()
-    # router gate: coarse range, alignment
-    assert native.odie_gate_forward(16, 10, 16, None, 17, 0, 16, 16, 0) == -1 and 'coarse' in native.odie_error().decode()
-    assert native.odie_gate_forward(8, 10, 16, None, 0, 0, 16, 16, 0) == -1 and 'aligned' in native.odie_error().decode()
-    assert native.odie_gate_backward(16, 16, 10, 16, None, 16, 0, 0, 16, None, 0) == -1
+    # router gate: coarse range, alignment, feature layout
+    assert native.odie_gate_forward(16, 10, 32, 16, None, 16, None, 17, 0, 16, 16, 0) == -1
+    assert 'coarse' in native.odie_error().decode()
+    assert native.odie_gate_forward(8, 10, 32, 16, None, 16, None, 0, 0, 16, 16, 0) == -1
+    assert 'aligned' in native.odie_error().decode()
+    assert native.odie_gate_backward(16, 16, 10, 32, 16, None, 16, None, 16, 0, 0, 16, None, 0) == -1
     assert 'null' in native.odie_error().decode()
+    three = (C.c_int32 * 16)(*([2] * 15 + [3]))
+    assert native.odie_gate_forward(16, 10, 48, 16, three, 16, None, 0, 0, 16, 16, 0) == -1
+    assert '1, 2 or 4' in native.odie_error().decode()
+    f31 = (C.c_int32 * 16)(*([2] * 15 + [1]))
+    assert native.odie_gate_forward(16, 10, 48, 16, f31, 16, None, 0, 0, 16, 16, 0) == -1
+    assert 'align16' in native.odie_error().decode()
+    assert native.odie_gate_forward(16, 10, 32, 33, None, 16, None, 0, 0, 16, 16, 0) == -1
+    assert 'levels' in native.odie_error().decode()
+    # cell bounds: sizes
+    assert native.odie_cell_bounds(1, 8, 4, 16, 16, 0) == -1 and 'at least 2' in native.odie_error().decode()
+    assert native.odie_cell_bounds(8, 8, 1, 16, 16, 0) == -1 and 'resolution' in native.odie_error().decode()
     assert native.odie_adam_step(8, None, 8, 0, 8, 8, None, 10, 0, 0, 0.1, 0.9, 0.999, 1e-15, 1.0, 0) == -1
     assert 'step' in native.odie_error().decode()
     # greedy selector: n must be resolution^2, cap 8-aligned, chunk positive, tree large enough
@@ -162,17 +179,10 @@ def test_selection_tree_fits_the_callers_fan32_allocation(native):
     assert native.odie_selection_tree_ints(0) == -1
 
 
-def test_product_thresholds_equal_oracle(oracle):
-    import numpy as np
-    from odie_amd.selection import native_thresholds
-    for r in (2, 8, 13, 128, 1290):
-        assert np.array_equal(np.asarray(native_thresholds(r), dtype=np.float32), oracle.native_thresholds(r))
-
-
 def _settings(**change):
     settings = dict(stream=0, total=1024, width=64, height=64, mode=20, rgb=4096, grid=4096, decoder=4096,
                     descriptors=4096, node_bitmap=4096, node_prefix=4096, bitmap=4096, active=16, grid_lr=1e-2,
-                    decoder_lr=1e-3)
+                    decoder_lr=1e-3, levels=16)
     settings.update(change)
     return json.dumps({k: v for k, v in settings.items() if v is not None}).encode()
 
@@ -185,16 +195,22 @@ def _settings(**change):
     (_settings(total=0), 'invalid total'),
     (_settings(grid=0), 'null rgb or grid'),
     (_settings(grid=4100), '16-byte aligned'),
-    (_settings(levels=12), '16 levels'),
-    (_settings(raw_width=48), '32-wide'),
+    (_settings(levels=21), 'levels must be within 2..20'),
+    (_settings(levels=1), 'levels must be within 2..20'),
+    (_settings(levels=None), 'levels is required'),
+    (_settings(raw_width=96), 'raw_width must be within'),
     (_settings(router_activation='tanh'), 'router_activation'),
     (_settings(gate_coarse_levels=17), 'gate_coarse_levels'),
     (_settings(gate=4096, mode=4), 'parallel gate'),
     (_settings(gate=4096, mode=21), 'mode bit 1'),
     (_settings(hash_encoding=dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
                                   per_level_scale=1.5), mode=16), 'half gradients'),
+    (_settings(hash_encoding=dict(n_levels=21, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
+                                  per_level_scale=1.5), levels=None), 'levels must be within 2..20'),
+    (_settings(hash_encoding=dict(n_levels=8, n_features_per_level=3, log2_hashmap_size=12, base_resolution=4,
+                                  per_level_scale=1.5), levels=None), '1, 2 or 4'),
     (_settings(hash_encoding=dict(n_levels=8, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
-                                  per_level_scale=1.5)), '16 levels x 2 features'),
+                                  per_level_scale=1.5)), 'levels differs'),
     (_settings(hash_encoding=dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
                                   per_level_scale=1.5)), 'allocation differs'),
 ])

@@ -17,12 +17,27 @@ from odie_amd.gate import Gate
 pytestmark = pytest.mark.gpu
 
 
-def _case(n, seed):
+# level rows of the reference's configurations (odie/config.py:129; DIV2K [2]*15+[1], the L8 / L12 /
+# L20 ablations) and rows of mixed F1/F2/F4 levels whose columns straddle the 8-column lane groups
+SHAPES = {
+    '16x2': [2] * 16,
+    'div2k': [2] * 15 + [1],
+    'L8': [2] * 7 + [1],
+    'L12': [2] * 11 + [1],
+    'L20': [2] * 19 + [1],
+    'mixed': [2, 2, 2, 4, 1, 4, 2, 1, 4, 2, 2, 1, 4, 2],
+    '20x4': [4] * 20,
+}
+
+
+def _case(n, seed, features=None):
+    features = [2] * 16 if features is None else features
+    width = (sum(features) + 15) // 16 * 16
     for attempt in range(20):
-        x = (synth.normal(seed + 100 * attempt, 'gate_x', n * 32).reshape(n, 32) * 0.5).astype(np.float16)
-        gate = Gate(seed=seed + attempt, coarse=3)
+        x = (synth.normal(seed + 100 * attempt, 'gate_x', n * width).reshape(n, width) * 0.5).astype(np.float16)
+        gate = Gate(seed=seed + attempt, coarse=3, features=features)
         flat = gate.half.cpu().numpy()
-        w1 = oracle.gate_weights(flat)[0].astype(np.float64)
+        w1 = oracle.gate_weights(flat, len(features))[0].astype(np.float64)
         pre = x.astype(np.float64) @ w1.T
         margin = np.abs(pre) / (np.abs(x.astype(np.float64)) @ np.abs(w1).T + 1e-30)
         if margin.min() > 2.0 ** -18:     # fp32 sums in another order differ by < 2^-19 of it
@@ -30,24 +45,31 @@ def _case(n, seed):
     raise AssertionError('no input without near-zero pre-activations')
 
 
-@pytest.mark.parametrize('n,with_visible', [(4096, False), (1000, True)])
-def test_gate_forward_and_backward(n, with_visible):
-    x, gate, flat = _case(n, 3)
-    visible = synth.integers(5, 'vis', n * 16, 4).reshape(n, 16).astype(bool) if with_visible else None
+@pytest.mark.parametrize('n,with_visible,shape', [(4096, False, '16x2'), (1000, True, '16x2'), (3000, True, 'div2k'),
+                                                  (2000, True, 'L8'), (2000, False, 'L12'), (2500, True, 'L20'),
+                                                  (1500, True, 'mixed'), (1000, True, '20x4')])
+def test_gate_forward_and_backward(n, with_visible, shape):
+    features = SHAPES[shape]
+    levels, width = len(features), (sum(features) + 15) // 16 * 16
+    x, gate, flat = _case(n, 3, features)
+    visible = synth.integers(5, 'vis', n * levels, 4).reshape(n, levels).astype(bool) if with_visible else None
     xd = torch.from_numpy(x).cuda()
     vd = torch.from_numpy(visible.astype(np.uint8)).cuda() if with_visible else None
     weighted, s = gate.forward(xd, visible=vd)
     s = s.cpu().numpy()
-    h, z, _ = oracle.gate_logits(x, flat)
-    ref_s = oracle.gate_values(z, 3)
+    assert s.shape == (n, levels)
+    h, z, _ = oracle.gate_logits(x, flat, levels)
+    ref_s = oracle.gate_values(z, 3)[:, :levels]
+    z = z[:, :levels]
     # a one-ulp fp16 logit difference moves s by at most s(1-s) * 2^-10 * |z|
     assert np.all(np.abs(s - ref_s) <= ref_s * (1 - ref_s) * 2.0 ** -9 * (np.abs(z.astype(np.float64)) + 1) + 2.0 ** -22)
-    assert np.array_equal(weighted.cpu().numpy().view(np.uint16), oracle.gate_apply(x, s, visible).view(np.uint16))
+    assert np.array_equal(weighted.cpu().numpy().view(np.uint16),
+                          oracle.gate_apply(x, s, visible, features).view(np.uint16))
 
-    value = (synth.normal(7, 'gate_value', n * 32).reshape(n, 32) * 0.01).astype(np.float16)
+    value = (synth.normal(7, 'gate_value', n * width).reshape(n, width) * 0.01).astype(np.float16)
     upstream = gate.backward(xd, torch.from_numpy(value).cuda(), torch.from_numpy(s).cuda(), visible=vd)
-    direct, da = oracle.gate_back(x, value, s, 3, visible=visible)
-    dr, dr_magnitude, dweights, magnitude = oracle.gate_mlp_backward(x, h, da, flat)
+    direct, da = oracle.gate_back(x, value, s, 3, visible=visible, features=features)
+    dr, dr_magnitude, dweights, magnitude = oracle.gate_mlp_backward(x, h, da, flat, levels)
     expected = oracle.gate_upstream(direct, dr)
     got = upstream.cpu().numpy().astype(np.float64)
     tolerance = 2.0 ** -10 * np.abs(expected.astype(np.float64)) + 2.0 ** -10 * dr_magnitude / 128 + 2.0 ** -24

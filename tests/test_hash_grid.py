@@ -39,9 +39,23 @@ def test_hash_grid_refuses_what_the_reference_refuses(changes, supports, error, 
         HashGrid(_config(**changes), supports, [2] * 16, _caps(), device='cpu')
 
 
-def test_hash_grid_refuses_other_widths():
-    with pytest.raises(ValueError, match='levels of 2 features'):
+def test_hash_grid_refuses_planes_that_differ_from_the_encoding():
+    with pytest.raises(ValueError, match='features per level'):
         HashGrid(_config(), [], [2] * 15 + [1], _caps(), device='cpu')
+
+
+@pytest.mark.parametrize('levels,features', [(8, 2), (12, 4), (20, 1)])
+def test_hash_grid_takes_other_shapes(levels, features):
+    encoding = dict(ENCODING, n_levels=levels, n_features_per_level=features)
+    resolutions, caps = hash_grid_layout(encoding)
+    width = (levels * features + 15) // 16 * 16
+    config = _config(hash_encoding=encoding, n_levels=levels, initial_active_prefix=levels, resolutions=resolutions,
+                     plane_feature_dimensions=[features] * levels, decoder_parameters=64 * width + 5120,
+                     gate_parameters=32 * width + 32 * ((levels + 15) // 16 * 16))
+    model = HashGrid(config, [], [features] * levels, caps, device='cpu')
+    assert model.grid.numel() == features * sum(caps)
+    assert model.decoder.width == model.gate.width == width
+    assert model.storage_stats()['gate_params'] == config['gate_parameters']
 
 
 def test_hash_grid_refuses_a_table_that_differs_from_the_caps():

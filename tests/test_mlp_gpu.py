@@ -18,9 +18,9 @@ from odie_amd.decoder import Decoder, PARAMETERS
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(seed, n):
-    x = (synth.normal(seed, 'mlp_x', n * 32).reshape(n, 32) * 0.5).astype(np.float16)
-    decoder = Decoder(seed=seed)
+def _inputs(seed, n, width=32):
+    x = (synth.normal(seed, 'mlp_x', n * width).reshape(n, width) * 0.5).astype(np.float16)
+    decoder = Decoder(seed=seed, width=width)
     return x, decoder
 
 
@@ -33,9 +33,10 @@ def _close16(got, expected, magnitude):
                            expected.ravel()[np.flatnonzero(bad)[:4]])
 
 
-@pytest.mark.parametrize('n', [1, 31, 1000, 4096])
-def test_forward_matches_oracle(n):
-    x, decoder = _inputs(1, n)
+@pytest.mark.parametrize('n,width', [(1, 32), (31, 32), (1000, 32), (4096, 32), (1000, 16), (777, 48), (3000, 64),
+                                     (2049, 80)])
+def test_forward_matches_oracle(n, width):
+    x, decoder = _inputs(1, n, width)
     out = decoder.forward(torch.from_numpy(x).cuda()).cpu().numpy()
     flat = decoder.half.cpu().numpy()
     w1, w2, w3 = (w.astype(np.float64) for w in oracle.mlp_weights(flat))
@@ -48,8 +49,8 @@ def test_forward_matches_oracle(n):
     _close16(out, y, 2.0 ** 4 * m3)
 
 
-def _train_case(seed, n, *, rgb8=True, permute=True, real=None):
-    x, decoder = _inputs(seed, n)
+def _train_case(seed, n, *, rgb8=True, permute=True, real=None, width=32):
+    x, decoder = _inputs(seed, n, width)
     real = n if real is None else real
     rows = synth.integers(seed, 'rows', n, 1 << 30).argsort(kind='stable').astype(np.int32) if permute \
         else np.arange(n, dtype=np.int32)
@@ -77,15 +78,20 @@ def _train_case(seed, n, *, rgb8=True, permute=True, real=None):
     return x, decoder.half.cpu().numpy(), rows, image, ids, target, real, got
 
 
-@pytest.mark.parametrize('n,rgb8,permute,real', [
-    (4096, True, True, None),
-    (1000, False, False, None),     # ragged last tile, fp32 targets, identity rows
-    (2048, True, True, 1500),       # inputs >= real are padding rows
-    (1 << 17, True, True, None),    # every workgroup runs several tiles
-    (5000, 'colors', True, 4000),   # packed per-row targets (as odie_route writes them)
+@pytest.mark.parametrize('n,rgb8,permute,real,width', [
+    (4096, True, True, None, 32),
+    (1000, False, False, None, 32),     # ragged last tile, fp32 targets, identity rows
+    (2048, True, True, 1500, 32),       # inputs >= real are padding rows
+    (1 << 17, True, True, None, 32),    # every workgroup runs several tiles
+    (5000, 'colors', True, 4000, 32),   # packed per-row targets (as odie_route writes them)
+    (4096, True, True, None, 16),       # the input widths of the other level rows: 8 levels (16),
+    (3001, True, False, 2500, 48),      # 20 levels of F2/F1 (48), F4 rows (64, 80)
+    (1 << 16, 'colors', True, None, 64),
+    (5000, False, True, None, 80),
 ])
-def test_train_matches_oracle_stagewise(n, rgb8, permute, real):
-    x, flat, rows, image, ids, target, real, got = _train_case(7, n, rgb8=rgb8, permute=permute, real=real)
+def test_train_matches_oracle_stagewise(n, rgb8, permute, real, width):
+    x, flat, rows, image, ids, target, real, got = _train_case(7, n, rgb8=rgb8, permute=permute, real=real,
+                                                               width=width)
     w1, w2, w3 = oracle.mlp_weights(flat)
     xs = x  # tile row j reads x[j]
     h1 = got['hidden'][:, :64]

@@ -22,13 +22,24 @@ def _config(router=True, coarse=0, **changes):
     return config
 
 
-def _inputs(seed):
+def _inputs(seed, dims=None):
     supports, caps = [], []
     for level, r in enumerate(RESOLUTIONS):
         supports.append(torch.ones(r * r, dtype=torch.bool) if level < 8 else
                         torch.from_numpy(synth.uniform(seed + level, 'model_support', r * r) < 0.4))
         caps.append((r * r + 7) // 8 * 8)
-    return supports, [2] * 16, caps
+    return supports, [2] * 16 if dims is None else list(dims), caps
+
+
+# the reference's DIV2K rows (odie/config.py:129: [2]*15 + [1], 31 columns padded to 32) and a
+# row of mixed F1/F2/F4 levels (36 columns padded to 48)
+DIV2K_DIMS = [2] * 15 + [1]
+MIXED_DIMS = [1, 4, 2, 2, 4, 1, 2, 2, 2, 4, 2, 2, 1, 2, 1, 4]
+
+
+def _head_sizes(dims):
+    width = (sum(dims) + 15) // 16 * 16
+    return dict(decoder_parameters=64 * width + 5120, gate_parameters=32 * width + 32 * 16)
 
 
 @pytest.mark.parametrize('changes,kwargs,error,message', [
@@ -44,10 +55,16 @@ def test_packed_model_refuses_what_the_reference_refuses(changes, kwargs, error,
         PackedXYPlanes(_config(**changes), supports, dims, caps, device='cpu', **kwargs)
 
 
-def test_packed_model_refuses_other_feature_widths():
-    supports, dims, caps = _inputs(1)
-    with pytest.raises(ValueError, match='levels of 2 features'):
-        PackedXYPlanes(_config(), supports, [1] + dims[1:], caps, device='cpu')
+@pytest.mark.parametrize('dims', [DIV2K_DIMS, MIXED_DIMS])
+def test_packed_model_takes_mixed_feature_rows(dims):
+    supports, dims, caps = _inputs(1, dims)
+    model = PackedXYPlanes(_config(**_head_sizes(dims)), supports, dims, caps, device='cpu')
+    width = (sum(dims) + 15) // 16 * 16
+    assert model.input_width == sum(dims) and model.decoder.width == model.gate.width == width
+    assert model.gate.features == dims
+    with pytest.raises(RuntimeError, match='head allocation'):
+        PackedXYPlanes(_config(), supports, dims, caps, device='cpu') if width != 32 else \
+            PackedXYPlanes(_config(decoder_parameters=1), supports, dims, caps, device='cpu')
 
 
 def test_build_model_dispatches_on_the_representation():
@@ -63,31 +80,41 @@ def test_build_model_dispatches_on_the_representation():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('router,coarse,prefix', [(False, 0, 16), (True, 0, 16), (True, 2, 12), (True, 3, 3)])
-def test_packed_model_forward_follows_the_reference_gating(router, coarse, prefix):
-    """forward = decoder(raw * fp16(gate * (visible & level < prefix))), with raw past the prefix
-    zeroed and the first K gates one (odie/model.py:266-279), written here in torch from the
-    gate activations the kernel reports."""
-    supports, dims, caps = _inputs(3)
-    model = PackedXYPlanes(_config(router, coarse), supports, dims, caps)
+@pytest.mark.parametrize('router,coarse,prefix,dims', [(False, 0, 16, None), (True, 0, 16, None), (True, 2, 12, None),
+                                                       (True, 3, 3, None), (True, 0, 16, DIV2K_DIMS),
+                                                       (True, 2, 14, MIXED_DIMS), (False, 0, 16, MIXED_DIMS)])
+def test_packed_model_forward_follows_the_reference_gating(router, coarse, prefix, dims):
+    """forward = decoder(rows of raw * fp16(gate * (visible & level < prefix)), padded with ones
+    to align16 columns), with raw past the prefix zeroed and the first K gates one
+    (odie/model.py:266-279), written here in torch from the gate activations the kernel
+    reports."""
+    supports, dims, caps = _inputs(3, dims)
+    config = _config(router, coarse, **_head_sizes(dims))
+    if not router:
+        config['gate_parameters'] = 0
+    model = PackedXYPlanes(config, supports, dims, caps)
     model.set_active_prefix(prefix)
     xy = torch.from_numpy(synth.coordinates(3, 4000)).cuda()
     rgb = model.forward(xy)
     raw, visible = model.query_features(xy)
+    levels = torch.tensor([l for l, f in enumerate(dims) for _ in range(f)], device='cuda')
     active = torch.arange(16, device='cuda') < prefix
-    raw = raw * active.repeat_interleave(2).half()
+    raw = raw * active[levels].half()
+    width = model.decoder.width
+    rows = torch.ones((4000, width), dtype=torch.float16, device='cuda')
+    rows[:, :raw.shape[1]] = raw
     if router:
-        _, activation = model.gate.forward(raw)
+        _, activation = model.gate.forward(rows)
         gates = torch.cat([torch.ones_like(activation[:, :coarse]), activation[:, coarse:]], dim=1)
         if prefix <= coarse:
             gates = torch.ones_like(gates)
-        weights = (gates * (visible & active).float()).half().repeat_interleave(2, dim=1)
-        raw = raw * weights
-    want = model.decoder.forward(raw).float()[:, :3]
+        weights = (gates * (visible & active).float()).half()[:, levels]
+        rows[:, :raw.shape[1]] = raw * weights
+    want = model.decoder.forward(rows).float()[:, :3]
     assert rgb.shape == (4000, 3)
     assert torch.equal(rgb, want)
     if prefix < 16:
-        full = PackedXYPlanes(_config(router, coarse), supports, dims, caps)
+        full = PackedXYPlanes(config, supports, dims, caps)
         full.set_active_prefix(16)
         assert not torch.equal(rgb, full.forward(xy))
 

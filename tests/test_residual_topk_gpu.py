@@ -49,3 +49,21 @@ def test_topk_matches_oracle(n, k):
     values[4] = 0.0
     ids = topk_tiles(torch.from_numpy(values).cuda(), k).cpu().numpy()
     assert np.array_equal(ids, oracle.topk_ids(values, k))
+
+
+@pytest.mark.parametrize('shape,resolution', [((1365, 2048), 8), ((61, 97), 13), ((1000, 1000), 128), ((5, 7), 2),
+                                              ((64, 64), 1290), ((2040, 1536), 764)])
+def test_cell_bounds_match_the_oracle_thresholds(shape, resolution):
+    """odie_cell_bounds (the encode's fmaf geometry on the device) against the oracle's exact fp32
+    thresholds (pinned by exact rational arithmetic): the first pixel of every cell column/row."""
+    from odie_amd.selection import cell_bounds
+    height, width = shape
+    xb, yb, ymap = cell_bounds(shape, resolution)
+    thresholds = oracle.native_thresholds(resolution)
+    def expected(size):
+        cells = np.searchsorted(thresholds, np.arange(size, dtype=np.float32) / np.float32(size - 1), side='right')
+        return np.searchsorted(cells, np.arange(resolution + 1)).astype(np.int32), cells
+    want_x, _ = expected(width)
+    want_y, rows = expected(height)
+    assert np.array_equal(xb, want_x) and np.array_equal(yb, want_y)
+    assert np.array_equal(ymap, rows)

@@ -27,12 +27,29 @@ pytestmark = pytest.mark.gpu
 HASH = dict(otype='HashGrid', n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=4,
             per_level_scale=1.5)
 RESOLUTIONS = [4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128]
+# level rows of the reference's own configurations: DIV2K (odie/config.py:129, configs/baselines/
+# odie_div2k.json: [2]*15 + [1]) and the level ablations (configs/ablations/div2k_L8/L12/L20.json)
+SHAPES = {'16x2': [2] * 16, 'div2k': [2] * 15 + [1], 'L8': [2] * 7 + [1], 'L12': [2] * 11 + [1],
+          'L20': [2] * 19 + [1]}
 
 
-def _config(representation, router, coarse=0, activation='sigmoid'):
-    return dict(representation=representation, hash_encoding=HASH, n_levels=16, plane_feature_dimensions=[2] * 16,
-                router_enabled=router, target_storage='uint8', gate_coarse_levels_K=coarse,
-                router_output_activation=activation, grid_lr=1e-2, gate_lr=2e-3, decoder_lr=1e-3)
+def _resolutions(levels):
+    """levels resolutions from 4 to 128, nondecreasing (the 16-level list for 16 levels)."""
+    if levels == 16:
+        return RESOLUTIONS
+    return [int(round(4 * 32 ** (l / (levels - 1)))) for l in range(levels)]
+
+
+def _config(representation, router, coarse=0, activation='sigmoid', dims=None, encoding=None):
+    dims = [2] * 16 if dims is None else dims
+    return dict(representation=representation, hash_encoding=encoding or HASH, n_levels=len(dims),
+                plane_feature_dimensions=dims, router_enabled=router, target_storage='uint8',
+                gate_coarse_levels_K=coarse, router_output_activation=activation, grid_lr=1e-2, gate_lr=2e-3,
+                decoder_lr=1e-3)
+
+
+def _width(dims):
+    return (sum(dims) + 15) // 16 * 16
 
 
 def _stream():
@@ -43,19 +60,22 @@ def _image(seed, width, height):
     return torch.from_numpy(synth.image(seed, width, height)).cuda().contiguous()
 
 
-def _planes(seed):
+def _planes(seed, dims=None):
+    dims = [2] * 16 if dims is None else dims
+    resolutions = _resolutions(len(dims))
+    full = len(dims) // 2
     supports, caps = [], []
-    for level, r in enumerate(RESOLUTIONS):
-        if level < 8:
+    for level, r in enumerate(resolutions):
+        if level < full:
             supports.append(torch.ones(r * r, dtype=torch.bool))
         else:
             supports.append(torch.from_numpy(synth.uniform(seed + level, 'runtime_support', r * r) < 0.35))
         caps.append((r * r + 7) // 8 * 8)
-    config = dict(resolutions=RESOLUTIONS, n_levels=16, representation='xy_planes', coarse_levels=0,
-                  gate_topology='shared', gate_position='feature', initial_active_prefix=8, seed=seed,
+    config = dict(resolutions=resolutions, n_levels=len(dims), representation='xy_planes', coarse_levels=0,
+                  gate_topology='shared', gate_position='feature', initial_active_prefix=full, seed=seed,
                   feature_init_std=5e-2)
-    planes = PackedPlanes(config, supports, [2] * 16, caps)
-    planes.set_active_prefix(16)
+    planes = PackedPlanes(config, supports, dims, caps)
+    planes.set_active_prefix(len(dims))
     return planes
 
 
@@ -63,10 +83,13 @@ class Composition:
     """The step from the tested entry points, with its own copies of every weight."""
 
     def __init__(self, grid, decoder, gate, config, width, height, hash_levels=None, planes=None, half=True):
+        self.dims = list(config['plane_feature_dimensions'])
+        self.row = _width(self.dims)
         self.grid = grid.clone()
-        self.decoder = Decoder(weights=decoder.params.cpu().numpy())
+        self.decoder = Decoder(weights=decoder.params.cpu().numpy(), width=self.row)
         self.gate = None if gate is None else Gate(weights=gate.params.cpu().numpy(), coarse=gate.coarse,
-                                                   activation='softplus' if gate.softplus else 'sigmoid')
+                                                   activation='softplus' if gate.softplus else 'sigmoid',
+                                                   features=self.dims)
         self.levels, self.planes, self.half = hash_levels, planes, half
         self.table = self.grid.half() if hash_levels is not None else None
         self.grid_opt = FusedAdam(self.grid, config['grid_lr'], eps=1e-15, variant='tcnn', half_copy=self.table)
@@ -76,21 +99,23 @@ class Composition:
                                                             variant='tcnn_dense', half_copy=self.gate.half)
         self.width, self.height = width, height
 
-    def forward(self, ids, active=16):
+    def forward(self, ids, active=None):
         w = self.width
+        active = len(self.dims) if active is None else active
         rx = torch.tensor(np.float32(1.0 / (w - 1)), device='cuda')
         ry = torch.tensor(np.float32(1.0 / (self.height - 1)), device='cuda')
         xy = torch.stack([(ids % w).float() * rx, (ids // w).float() * ry], dim=1).contiguous()
         if self.levels is not None:
-            raw = grid_forward(xy, self.table, self.levels, 2, width=32)
+            raw = grid_forward(xy, self.table, self.levels, self.dims[0], width=self.row)
             vis = None
         else:
-            raw, vis = _packed_query(self.planes, self.grid, xy)
-            raw[:, 2 * active:] = 0
+            raw, vis = _packed_query(self.planes, self.grid, xy, self.row)
+            raw[:, sum(self.dims[:active]):] = 0
             vis[:, active:] = 0
+        raw[:, sum(self.dims):] = 1.0          # the row's padding columns (odie/native/runtime.cu:51)
         return xy, raw, vis
 
-    def step(self, ids, image, active=16, grid_gradient=None, update=True):
+    def step(self, ids, image, active=None, grid_gradient=None, update=True):
         xy, raw, vis = self.forward(ids, active)
         squares = torch.empty(ids.numel(), dtype=torch.float32, device='cuda')
         features, sigmoid = raw, None
@@ -99,7 +124,7 @@ class Composition:
         dz = self.decoder.train(features, rgb=image.reshape(-1), ids=ids, squares=squares)
         up = dz if self.gate is None else self.gate.backward(raw, dz, sigmoid, visible=vis)
         if self.levels is not None:
-            gradient = grid_backward(xy, up, self.levels, 2, expert_params=self.grid.numel())
+            gradient = grid_backward(xy, up, self.levels, self.dims[0], expert_params=self.grid.numel())
         else:
             gradient = _packed_gradient(self.planes, xy, up, self.grid.numel())
         if update:
@@ -111,13 +136,13 @@ class Composition:
         return raw, squares, gradient
 
 
-def _packed_query(planes, grid, xy):
-    n = xy.shape[0]
-    raw = torch.empty((n, 32), dtype=torch.float16, device='cuda')
-    vis = torch.empty((n, 16), dtype=torch.uint8, device='cuda')
+def _packed_query(planes, grid, xy, row):
+    n, levels = xy.shape[0], planes.n_levels
+    raw = torch.empty((n, row), dtype=torch.float16, device='cuda')
+    vis = torch.empty((n, levels), dtype=torch.uint8, device='cuda')
     _lib.check(_lib.library().odie_packed_forward(
-        xy.data_ptr(), n, grid.data_ptr(), grid.numel(), planes.descriptors.data_ptr(), 16,
-        planes.node_bitmap.data_ptr(), planes.node_prefix.data_ptr(), planes.bitmap.data_ptr(), 32, raw.data_ptr(),
+        xy.data_ptr(), n, grid.data_ptr(), grid.numel(), planes.descriptors.data_ptr(), levels,
+        planes.node_bitmap.data_ptr(), planes.node_prefix.data_ptr(), planes.bitmap.data_ptr(), row, raw.data_ptr(),
         vis.data_ptr(), _lib.stream_of(xy)))
     return raw, vis
 
@@ -125,7 +150,7 @@ def _packed_query(planes, grid, xy):
 def _packed_gradient(planes, xy, up, total):
     gradient = torch.empty(total, dtype=torch.float32, device='cuda')
     _lib.check(_lib.library().odie_packed_backward(
-        xy.data_ptr(), xy.shape[0], up.data_ptr(), 32, planes.descriptors.data_ptr(), 16,
+        xy.data_ptr(), xy.shape[0], up.data_ptr(), up.shape[1], planes.descriptors.data_ptr(), planes.n_levels,
         planes.node_bitmap.data_ptr(), planes.node_prefix.data_ptr(), planes.bitmap.data_ptr(), gradient.data_ptr(),
         total, _lib.stream_of(xy)))
     return gradient
@@ -135,29 +160,38 @@ def _bits(t):
     return t.detach().cpu().numpy().view(np.uint16 if t.dtype == torch.float16 else np.uint32)
 
 
-def _hash_model(seed, router, coarse=0, activation='sigmoid'):
-    levels, entries = grid_levels(HASH)
-    grid = torch.from_numpy((synth.normal(seed, 'runtime_grid', 2 * entries) * 0.05).astype(np.float32)).cuda()
-    gate = Gate(seed=seed + 1, coarse=coarse, activation=activation) if router else None
-    return NativeModel(Decoder(seed=seed), gate, grid=grid), levels
+def _hash_model(seed, router, coarse=0, activation='sigmoid', encoding=None):
+    encoding = encoding or HASH
+    levels, entries = grid_levels(encoding)
+    features = int(encoding['n_features_per_level'])
+    dims = [features] * int(encoding['n_levels'])
+    grid = torch.from_numpy((synth.normal(seed, 'runtime_grid', features * entries) * 0.05).astype(np.float32)).cuda()
+    gate = Gate(seed=seed + 1, coarse=coarse, activation=activation, features=dims) if router else None
+    return NativeModel(Decoder(seed=seed, width=_width(dims)), gate, grid=grid, active_prefix=len(dims)), levels
 
 
-@pytest.mark.parametrize('router,coarse,activation', [(False, 0, 'sigmoid'), (True, 2, 'sigmoid'),
-                                                       (True, 0, 'softplus')])
-def test_hash_step_matches_composition(router, coarse, activation):
+@pytest.mark.parametrize('router,coarse,activation,levels,features', [
+    (False, 0, 'sigmoid', 16, 2), (True, 2, 'sigmoid', 16, 2), (True, 0, 'softplus', 16, 2),
+    (True, 1, 'sigmoid', 8, 2),        # 16 columns
+    (True, 0, 'sigmoid', 12, 4),       # 48 columns
+    (False, 0, 'sigmoid', 20, 1),      # 20 columns padded to 32, G = 32 gate outputs
+])
+def test_hash_step_matches_composition(router, coarse, activation, levels, features):
     width, height = 97, 61
+    encoding = dict(HASH, n_levels=levels, n_features_per_level=features)
     with torch.cuda.stream(_stream()):
         image = _image(11, width, height)
-        config = _config('hash_grid', router, coarse, activation)
-        model, levels = _hash_model(5, router, coarse, activation)
-        ref = Composition(model.grid, model.decoder, model.gate, config, width, height, hash_levels=levels)
+        config = _config('hash_grid', router, coarse, activation, dims=[features] * levels, encoding=encoding)
+        model, grid_levels_ = _hash_model(5, router, coarse, activation, encoding)
+        row = _width([features] * levels)
+        ref = Composition(model.grid, model.decoder, model.gate, config, width, height, hash_levels=grid_levels_)
         opt = NativeOptimizer(model, image, (height, width), config, [model.grid])
         for step, n in enumerate((3000, 4089, 1, 2048)):
             ids = torch.from_numpy(synth.integers(step, 'runtime_ids', n, width * height)).cuda()
             opt.step_raw(ids)
             raw, squares, _ = ref.step(ids, image)
             torch.cuda.synchronize()
-            assert np.array_equal(_bits(opt.copied('raw', (n, 32), torch.float16)), _bits(raw)), step
+            assert np.array_equal(_bits(opt.copied('raw', (n, row), torch.float16)), _bits(raw)), step
             assert np.array_equal(_bits(opt.copied('squares', (n,), torch.float32)), _bits(squares)), step
             assert np.array_equal(_bits(model.grid), _bits(ref.grid)), step
             assert np.array_equal(_bits(model.decoder.params), _bits(ref.decoder.params)), step
@@ -166,16 +200,22 @@ def test_hash_step_matches_composition(router, coarse, activation):
         opt.close()
 
 
-@pytest.mark.parametrize('router,active,half', [(False, 16, True), (True, 16, True), (True, 12, True),
-                                                (False, 9, False)])
-def test_packed_step_matches_composition(router, active, half):
+@pytest.mark.parametrize('router,active,half,shape', [(False, 16, True, '16x2'), (True, 16, True, '16x2'),
+                                                      (True, 12, True, '16x2'), (False, 9, False, '16x2'),
+                                                      (True, 16, True, 'div2k'), (True, 11, True, 'div2k'),
+                                                      (True, 8, True, 'L8'), (True, 12, True, 'L12'),
+                                                      (True, 20, True, 'L20'), (False, 17, True, 'L20')])
+def test_packed_step_matches_composition(router, active, half, shape):
     width, height = 83, 64
+    dims = SHAPES[shape]
     with torch.cuda.stream(_stream()):
         image = _image(12, width, height)
-        config = _config('xy_planes', router, 1)
-        planes = _planes(3)
+        config = _config('xy_planes', router, 1, dims=dims)
+        planes = _planes(3, dims)
         planes.set_active_prefix(active)
-        model = NativeModel(Decoder(seed=4), Gate(seed=6, coarse=1) if router else None, planes=planes)
+        row = _width(dims)
+        model = NativeModel(Decoder(seed=4, width=row), Gate(seed=6, coarse=1, features=dims) if router else None,
+                            planes=planes)
         ref = Composition(model.grid, model.decoder, model.gate, config, width, height, planes=planes, half=half)
         opt, plane_views = make_native_optimizer(model, image, (height, width), config)
         if not half:
@@ -187,7 +227,7 @@ def test_packed_step_matches_composition(router, active, half):
             gradient = opt.copied('grid_grad', (model.grid.numel(),), torch.float32)
             raw, squares, expected = ref.step(ids, image, active, grid_gradient=gradient)
             torch.cuda.synchronize()
-            assert np.array_equal(_bits(opt.copied('raw', (n, 32), torch.float16)), _bits(raw)), step
+            assert np.array_equal(_bits(opt.copied('raw', (n, row), torch.float16)), _bits(raw)), step
             assert np.array_equal(_bits(opt.copied('squares', (n,), torch.float32)), _bits(squares)), step
             got, want = gradient.double().cpu().numpy(), expected.double().cpu().numpy()
             scale = np.abs(want).max() + 1e-30

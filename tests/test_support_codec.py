@@ -117,7 +117,7 @@ def test_artifact_round_trip(tmp_path):
                          feature_init_std=1e-2, plane_feature_dimensions=[2] * 5, cell_caps=caps,
                          gate_coarse_levels_K=1, router_output_activation='sigmoid')
     planes = PackedPlanes(configuration, supports, [2] * 5, caps, device='cpu')
-    decoder, gate = Decoder(seed=1, device='cpu'), Gate(seed=2, coarse=1, device='cpu')
+    decoder, gate = Decoder(seed=1, device="cpu", width=16), Gate(seed=2, coarse=1, device="cpu", features=[2] * 5)
     path = tmp_path / 'model_latest_fp16.pt'
     storage = write_artifact(path, configuration, planes, decoder, gate, epoch=3, optimizer_steps=30,
                              metrics={'mse': 0.01})
