@@ -55,10 +55,11 @@ def parse():
     parser.add_argument('--gpus', type=int, default=1)
     parser.add_argument('--steps', type=int, default=20)
     parser.add_argument('--warmup', type=int, default=3)
-    parser.add_argument('--cpu-seconds', type=float, default=15.0,
+    parser.add_argument('--cpu-seconds', type=float, default=24.0,
                         help='approximate budget of the CPU baseline sample')
     parser.add_argument('--no-cpu', action='store_true')
     parser.add_argument('--no-native', action='store_true', help='skip the 65536-id native step measurement')
+    parser.add_argument('--no-single', action='store_true', help='skip the single-expert 2^19-table fwd+bwd line')
     parser.add_argument('--native-steps', type=int, default=200)
     parser.add_argument('--no-reconstruction', action='store_true', help='skip the 32768^2 residual pass')
     parser.add_argument('--reconstruction-batch', type=int, default=1 << 26)
@@ -81,27 +82,28 @@ def copy_probe():
 
 
 def cpu_baseline(image, ids, table16, master, decoder16, levels, expert_params, budget):
-    """Time the oracle's port of the step on a bounded sample of the same ids: routing,
-    encode forward, decoder forward/loss/backward and encode backward per query; Adam over the
-    whole table once per batch, measured on a slice and scaled to the table."""
+    """Time the oracle's port of the step on a bounded sample of the same ids: routing, encode
+    forward, decoder forward/loss/backward and encode backward per query; Adam over the whole
+    table once per batch, measured on a slice and scaled to the table.  On all host cores, then on
+    one thread (the reference pins its CPU work to one thread, odie/runtime_env.py:10,
+    odie/train.py:72); each timing is the median of five runs."""
     import numpy as np
     import oracle
     rows = [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
     cores = len(os.sched_getaffinity(0))
-    experts = REGIONS * REGIONS
     total = table16.size
     rgb = image.reshape(-1, 3)
 
-    def per_query(count):
+    def per_query(count, threads):
         sample = ids[:count]
         started = time.perf_counter()
         _, perm, local, offsets = oracle.route(sample, WIDTH, HEIGHT, REGIONS, REGIONS)
         raw = oracle.hash_forward(local, table16, rows, 2, offsets=offsets, expert_params=expert_params,
-                                  threads=cores)
+                                  threads=threads)
         dz, _ = oracle.mlp_step_f32(raw, decoder16, oracle.mlp_targets(perm, rgb=rgb, ids=sample), perm, count,
-                                    threads=cores)
+                                    threads=threads)
         oracle.hash_backward_f32(local, dz, rows, 2, total, offsets=offsets, expert_params=expert_params,
-                                 threads=cores)
+                                 threads=threads)
         return time.perf_counter() - started
 
     def adam(count):
@@ -113,101 +115,224 @@ def cpu_baseline(image, ids, table16, master, decoder16, levels, expert_params, 
         oracle.adam(1, p, g, m, v, steps, 1, 1e-2, scale=128.0)
         return time.perf_counter() - started
 
-    # per-query rate from two sample sizes (the difference removes once-per-batch costs such
-    # as clearing the gradient), plus the once-per-batch part itself
-    probe = 1 << 14
-    rate = probe / per_query(probe)
-    small = int(min(len(ids) // 2, max(probe, rate * budget * 0.5 / 9)))
-    t_small = sorted(per_query(small) for _ in range(3))[1]
-    t_large = sorted(per_query(2 * small) for _ in range(3))[1]
-    marginal = max(t_large - t_small, 1e-9) / small
-    fixed = max(t_small - marginal * small, 0.0)
-    slice_ = 1 << 22
-    adam_seconds = sorted(adam(slice_) for _ in range(3))[1] * total / slice_
-    step_seconds = marginal * N_COORDS + fixed + adam_seconds
-    count = 2 * small
+    def median(run, *args):
+        return float(np.median([run(*args) for _ in range(5)]))
+
+    def measure(threads, seconds):
+        # per-query rate from two sample sizes (the difference removes once-per-batch costs such
+        # as clearing the gradient), plus the once-per-batch part itself; Adam runs on the
+        # OpenMP thread count the encode calls set
+        probe = 1 << 12
+        per_query(probe, threads)                      # warm-up (allocations, thread pools)
+        rate = probe / per_query(probe, threads)
+        small = int(min(len(ids) // 2, max(probe, rate * seconds * 0.5 / 15)))
+        t_small = median(per_query, small, threads)
+        t_large = median(per_query, 2 * small, threads)
+        marginal = max(t_large - t_small, 1e-9) / small
+        fixed = max(t_small - marginal * small, 0.0)
+        slice_ = 1 << 20 if threads == 1 else 1 << 22
+        per_query(probe, threads)
+        adam_seconds = median(adam, slice_) * total / slice_
+        step_seconds = marginal * N_COORDS + fixed + adam_seconds
+        return step_seconds, small
+
+    step_seconds, small = measure(cores, budget)
+    one_seconds, one_small = measure(1, budget)
     return dict(value=N_COORDS / step_seconds, unit='queries/s', cores=cores, kind='port',
-                sample='first %d and %d of the 2^22 ids through route+encode fwd+decoder+encode bwd (median '
-                       'of 3 each; per-query rate from the difference, OpenMP %d threads for encode and Adam, '
-                       'torch-CPU fp32 for the decoder), plus Adam over a 2^22-parameter slice scaled to the %d-parameter '
-                       'table, once per 2^22-query batch' % (count // 2, count, cores, total),
-                seconds_per_step=step_seconds,
+                sample='first %d and %d of the 2^22 ids through route+encode fwd+decoder+encode bwd (median of 5 '
+                       'each; per-query rate from the difference; OpenMP %d threads for encode and Adam, torch-CPU '
+                       'fp32 for the decoder), plus Adam over a 2^22-parameter slice scaled to the %d-parameter table, '
+                       'once per 2^22-query batch' % (small, 2 * small, cores, total),
+                seconds_per_step=step_seconds, one_thread={
+                    'value': N_COORDS / one_seconds, 'seconds_per_step': one_seconds, 'cores': 1,
+                    'sample': 'first %d and %d ids, median of 5; Adam over a 2^20-parameter slice' % (one_small,
+                                                                                                    2 * one_small)},
                 cpu=platform.processor() or platform.machine())
 
 
-NATIVE_RESOLUTIONS = [16, 23, 31, 43, 59, 81, 111, 153, 211, 291, 401, 554, 764, 1054, 1454, 2006]
-NATIVE_HASH = dict(otype='HashGrid', n_levels=16, n_features_per_level=2, log2_hashmap_size=19, base_resolution=16,
-                   per_level_scale=1.38)
+# The reference's own recorded runs the native-step lines reproduce (results/**/metrics.json, RTX
+# 3060): the final packed layout of DIV2K image 0036 at 16, 8 and 20 levels (resolutions, node
+# caps, feature dimensions, cells allowed per level, direct levels; 954,016 parameters each) and
+# the Tokyo hash-grid ablation's encoding, with the run's throughput rgb_processed_pixels /
+# optimization_loop_seconds.
+DIV2K_SHAPE = (1536, 2040)          # results/div2k_50/0036/odie/metrics.json:129-132 (H, W)
+DIV2K_RUNS = {
+    'div2k_L16': dict(  # results/div2k_50/0036/odie/metrics.json:237,767
+        resolutions=[8, 11, 15, 21, 29, 40, 56, 77, 106, 147, 203, 280, 387, 534, 738, 1020],
+        caps=[64, 128, 232, 448, 848, 1600, 3136, 5936, 11240, 21616, 41216, 78400, 87936, 87936, 87936, 87968],
+        allowed=[64, 121, 225, 441, 841, 1600, 3136, 5929, 11236, 21609, 41209, 78400, 87044, 84261, 74770, 63937],
+        direct=12, reference_pixels_per_s=157286400 / 4.524877033662051),
+    'div2k_L8': dict(   # results/expert_count/L8/0036/metrics.json:179,465
+        resolutions=[8, 16, 32, 64, 128, 255, 510, 1020],
+        caps=[64, 256, 1024, 4096, 16384, 65032, 257712, 257712],
+        allowed=[64, 256, 1024, 4096, 16384, 65025, 257237, 244883], direct=6, reference_pixels_per_s=44.0e6),
+    'div2k_L20': dict(  # results/expert_count/L20/0036/metrics.json:267,1009
+        resolutions=[8, 10, 13, 17, 22, 29, 37, 48, 62, 80, 103, 132, 171, 221, 285, 368, 474, 612, 790, 1020],
+        caps=[64, 104, 176, 296, 488, 848, 1376, 2304, 3848, 6400, 10616, 17424, 29248, 48848, 63560, 63560, 63560,
+              63560, 63560, 63584],
+        allowed=[64, 100, 169, 289, 484, 841, 1369, 2304, 3844, 6400, 10609, 17424, 29241, 48841, 62401, 62602, 59646,
+                 54137, 48024, 43053], direct=14, reference_pixels_per_s=27.5e6),
+}
+TOKYO_SHAPE = (21450, 56718)        # results/tokyo_components/no_on_demand/metrics.json:137-140
+TOKYO_HASH = dict(otype='HashGrid', n_levels=16, n_features_per_level=2, log2_hashmap_size=21, base_resolution=3,
+                  per_level_scale=1.8409329652786255)
+TOKYO_REFERENCE = 60830515200 / 3206.4612404829822   # no_on_demand/metrics.json:239,279
 
 
-def native_steps(image, steps):
-    """The reference's own training step (NativeOptimizer over the odie_* runtime) at its batch of
-    65536 ids, replayed from a captured graph: packed xy planes (16 full levels, R = 16..2006)
-    and the hash grid (16 levels, 2^19-entry tables), both with the router gate.  Reported
-    beside the headline, not as it."""
+def _recorded_planes(run):
+    """PackedPlanes with a recorded run's resolutions, caps and F2/F1 levels; each sparse level
+    selects a row-major run of its recorded cell count, shortened if needed so the closure fits
+    the cap (a run's own supports come from its image's residuals and are not recorded)."""
+    import torch
+    from odie_amd.model import PackedPlanes, plane_closure
+    levels = len(run['resolutions'])
+    supports = []
+    for level, (r, cap, allowed) in enumerate(zip(run['resolutions'], run['caps'], run['allowed'])):
+        support = torch.zeros(r * r, dtype=torch.bool)
+        if level < run['direct']:
+            support[:] = True
+        else:
+            count = allowed
+            while True:
+                support[:] = False
+                support[:count] = True
+                if plane_closure(support, r).numel() <= cap:
+                    break
+                count -= r
+        supports.append(support)
+    config = dict(resolutions=run['resolutions'], n_levels=levels, representation='xy_planes', coarse_levels=0,
+                  gate_topology='shared', gate_position='feature', initial_active_prefix=run['direct'], seed=1729,
+                  feature_init_std=1e-3)
+    planes = PackedPlanes(config, supports, [2] * (levels - 1) + [1], run['caps'])
+    planes.set_active_prefix(levels)
+    return planes
+
+
+def native_steps(steps):
+    """The reference's own training step (NativeOptimizer over the odie_* runtime, router on,
+    sigmoid gate) at its batch of 65536 ids, each step a stratified draw (odie_stratified_ids on
+    torch.rand's uniforms) and a replay of the captured step, timed together: the recorded DIV2K
+    0036 packed layouts at 16, 8 and 20 levels on a synthetic 2040x1536 image, and the Tokyo
+    hash-grid ablation (16 levels x 2, 2^21-entry tables) on a synthetic 56718x21450 image.
+    Reported beside the headline, with the reference's whole-run figure for the same
+    configuration (its training loop also draws, evaluates and selects supports)."""
     import numpy as np
     import torch
     from odie_amd import synth
     from odie_amd.config import grid_levels
     from odie_amd.decoder import Decoder
     from odie_amd.gate import Gate
-    from odie_amd.model import PackedPlanes
     from odie_amd.native_backend import NativeModel, NativeOptimizer, make_native_optimizer
-    from odie_amd.sampling import stratified_batches
+    from odie_amd.sampling import stratified_ids
 
-    target = torch.from_numpy(image).cuda().contiguous()
-    shape = image.shape[:2]
     out = {}
     stream = torch.cuda.Stream()
+    generator = torch.Generator(device='cuda').manual_seed(1729)
+
+    def run_steps(optimizer, shape):
+        optimizer.prepare_epoch()
+        draw = lambda: stratified_ids(torch.rand((65536, 2), device='cuda', generator=generator), shape)
+        for _ in range(5):
+            optimizer.train_batch(draw())
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            loss = optimizer.train_batch(draw())
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps, float(loss)
+
     with torch.cuda.stream(stream):
-        for kind in ('packed_planes', 'hash_grid'):
-            config = dict(representation='xy_planes' if kind == 'packed_planes' else 'hash_grid',
-                          hash_encoding=NATIVE_HASH, n_levels=16, plane_feature_dimensions=[2] * 16,
+        image = torch.from_numpy(synth.image(0, DIV2K_SHAPE[1], DIV2K_SHAPE[0])).cuda().contiguous()
+        for name, run in DIV2K_RUNS.items():
+            levels = len(run['resolutions'])
+            dims = [2] * (levels - 1) + [1]
+            planes = _recorded_planes(run)
+            width = (sum(dims) + 15) // 16 * 16
+            model = NativeModel(Decoder(seed=0, width=width), Gate(seed=1, features=dims), planes=planes)
+            config = dict(representation='xy_planes', n_levels=levels, plane_feature_dimensions=dims,
                           router_enabled=True, target_storage='uint8', gate_coarse_levels_K=0,
                           router_output_activation='sigmoid', grid_lr=1e-2, gate_lr=1e-3, decoder_lr=1e-3)
-            if kind == 'packed_planes':
-                supports = [torch.ones(r * r, dtype=torch.bool) for r in NATIVE_RESOLUTIONS]
-                caps = [(r * r + 7) // 8 * 8 for r in NATIVE_RESOLUTIONS]
-                planes = PackedPlanes(dict(resolutions=NATIVE_RESOLUTIONS, n_levels=16, representation='xy_planes',
-                                           coarse_levels=0, gate_topology='shared', gate_position='feature',
-                                           initial_active_prefix=16, seed=0, feature_init_std=1e-3),
-                                      supports, [2] * 16, caps)
-                model = NativeModel(Decoder(seed=0), Gate(seed=1), planes=planes)
-                optimizer, _ = make_native_optimizer(model, target, shape, config)
-            else:
-                _, entries = grid_levels(NATIVE_HASH)
-                grid = torch.from_numpy(synth.table(0, 2 * entries, name='native_hash')).cuda()
-                model = NativeModel(Decoder(seed=0), Gate(seed=1), grid=grid)
-                optimizer = NativeOptimizer(model, target, shape, config, [grid])
-            optimizer.prepare_epoch()
-            draw = stratified_batches(shape, 65536, torch.Generator(device='cuda').manual_seed(0))
-            samplings = {'': [next(draw) for _ in range(4)],
-                         '_uniform_ids': [torch.from_numpy(synth.integers(k, 'native_ids', 65536,
-                                                                          shape[0] * shape[1])).cuda()
-                                          for k in range(4)]}
-            for suffix, batches in samplings.items():
-                for k in range(5):
-                    optimizer.train_batch(batches[k % 4])
-                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                torch.cuda.synchronize()
-                start.record(stream)
-                for k in range(steps):
-                    optimizer.fixed.copy_(batches[k % 4])
-                    optimizer.graph.replay()
-                stop.record(stream)
-                torch.cuda.synchronize()
-                ms = start.elapsed_time(stop) / steps
-                loss = float(optimizer.squares.double().mean())
-                out[kind + suffix] = {'ms_per_step': ms, 'pixels_per_s': 65536 / (ms / 1e3),
-                                      'params': model.grid.numel(), 'loss': loss}
+            optimizer, _ = make_native_optimizer(model, image, DIV2K_SHAPE, config)
+            ms, loss = run_steps(optimizer, DIV2K_SHAPE)
             optimizer.close()
+            params = model.grid.numel() + model.gate.params.numel() + model.decoder.params.numel()
+            out[name] = {'ms_per_step': ms, 'pixels_per_s': 65536 / (ms / 1e3), 'params': params, 'levels': levels,
+                         'row_width': width, 'loss': loss,
+                         'reference_pixels_per_s': run['reference_pixels_per_s'],
+                         'vs_reference': 65536 / (ms / 1e3) / run['reference_pixels_per_s']}
+        del image
+        tokyo = synth.image_device(2, TOKYO_SHAPE[1], TOKYO_SHAPE[0]).contiguous()
+        levels, entries = grid_levels(TOKYO_HASH)
+        grid = torch.from_numpy(synth.table(0, 2 * entries, name='native_hash')).cuda()
+        model = NativeModel(Decoder(seed=0), Gate(seed=1), grid=grid)
+        config = dict(representation='hash_grid', hash_encoding=TOKYO_HASH, n_levels=16, plane_feature_dimensions=[2] * 16,
+                      router_enabled=True, target_storage='uint8', gate_coarse_levels_K=0,
+                      router_output_activation='sigmoid', grid_lr=1e-2, gate_lr=1e-3, decoder_lr=1e-3)
+        optimizer = NativeOptimizer(model, tokyo, TOKYO_SHAPE, config, [grid])
+        ms, loss = run_steps(optimizer, TOKYO_SHAPE)
+        optimizer.close()
+        out['tokyo_hash_grid'] = {'ms_per_step': ms, 'pixels_per_s': 65536 / (ms / 1e3), 'params': grid.numel() + 1536 + 7168,
+                                  'loss': loss, 'reference_pixels_per_s': TOKYO_REFERENCE,
+                                  'vs_reference': 65536 / (ms / 1e3) / TOKYO_REFERENCE}
+        del tokyo
     out['batch'] = 65536
     out['steps'] = steps
-    out['note'] = ('graph replays of odie_step (router on), ids resident, stratified batches as the '
-                   "reference's configurations draw them (the *_uniform_ids lines: ids uniform over the "
-                   'image); the reference records 34.8 M px/s (packed planes) and 19.0 M px/s (hash grid) '
-                   'for this step on an RTX 3060')
+    out['note'] = ('same configurations as the reference runs named in the keys (recorded layouts, sampling, router, '
+                   'batch); ours times a stratified draw plus a graph replay of the step per batch; the reference '
+                   'figure is its whole training loop (rgb_processed_pixels / optimization_loop_seconds on an RTX '
+                   '3060), which also evaluates and selects supports between stages')
     return out
+
+
+C2_ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=19, base_resolution=16, per_level_scale=1.38)
+C2_BYTES = {'forward': 328, 'backward': 1096}   # per query: xy 8 + gathers 256 + features 64; xy 8 + upstream 64 + 1024
+
+
+def single_expert_steps(steps):
+    """The single-expert workload: one 16-level x 2-feature fp16 hash grid (2^19-entry tables,
+    base 16, scale 1.38, 5,487,024 parameters), 2^22 coordinates uniform in [0,1)^2 (seed 0), an
+    upstream [2^22, 32] of N(0,1) rounded to fp16; forward encode and the backward scatter into
+    a zeroed fp32 gradient, timed with events on the stream they run on."""
+    import torch
+    from odie_amd import synth
+    from odie_amd.config import grid_levels
+    from odie_amd.encoding import grid_backward, grid_forward
+    levels, entries = grid_levels(C2_ENCODING)
+    n = N_COORDS
+    table = torch.from_numpy(synth.table(0, 2 * entries)).cuda().half()
+    xy = torch.from_numpy(synth.coordinates(0, n)).cuda()
+    upstream = torch.from_numpy(synth.upstream(0, n, 32)).cuda()
+    out = torch.empty((n, 32), dtype=torch.float16, device='cuda')
+    gradient = torch.empty(2 * entries, dtype=torch.float32, device='cuda')
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        grid_forward(xy, table, levels, 2, out=out)
+        grid_backward(xy, upstream, levels, 2, expert_params=2 * entries, gradient=gradient)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b, c in marks:
+        a.record(stream)
+        grid_forward(xy, table, levels, 2, out=out)
+        b.record(stream)
+        grid_backward(xy, upstream, levels, 2, expert_params=2 * entries, gradient=gradient)
+        c.record(stream)
+    torch.cuda.synchronize()
+    forward = sum(a.elapsed_time(b) for a, b, _ in marks) / steps
+    backward = sum(b.elapsed_time(c) for _, b, c in marks) / steps
+    total = forward + backward
+    gbs = lambda per, ms: n * per / (ms / 1e3) / 1e9
+    stage_gbs = {'forward': gbs(C2_BYTES['forward'], forward), 'backward': gbs(C2_BYTES['backward'], backward)}
+    dominant = 'backward' if backward >= forward else 'forward'
+    return {'coords': n, 'params': 2 * entries, 'ms': {'forward': forward, 'backward': backward},
+            'queries_per_s': n / (total / 1e3), 'GBps': gbs(sum(C2_BYTES.values()), total),
+            'pct_hbm_peak': 100 * gbs(sum(C2_BYTES.values()), total) / HBM_PEAK_GBS,
+            'roofline': {'bound': 'hbm', 'kernel': dominant, 'achieved': stage_gbs[dominant], 'peak': HBM_PEAK_GBS,
+                         'unit': 'GB/s', 'frac': stage_gbs[dominant] / HBM_PEAK_GBS,
+                         'algorithmic_bytes_per_launch': n * C2_BYTES[dominant],
+                         'avg_ms': backward if dominant == 'backward' else forward},
+            'stage_GBps': stage_gbs}
 
 
 C5_SIDE, C5_TILES, C5_RESIDUAL_TILE, C5_TOP = 32768, 32, 256, 512
@@ -353,6 +478,7 @@ def main():
     if traffic_file.exists():
         entry = json.loads(traffic_file.read_text()).get(dominant)
         traffic = entry['bytes'] if entry else None
+    physical = traffic / (stage_ms[dominant] / 1e3) / 1e9 if traffic else None
     encode_ms = stage_ms['encode_forward'] + stage_ms['encode_backward']
     loss = float(trainer.squares.double().mean())
     result = {
@@ -373,11 +499,14 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': '%s (%s)' % (dominant, KERNELS[dominant]),
                      'achieved': stage_gbs[dominant], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': stage_gbs[dominant] / HBM_PEAK_GBS, 'traffic': traffic,
+                     'physical_GBps': physical, 'frac_physical': physical / HBM_PEAK_GBS if physical else None,
                      'algorithmic_bytes_per_launch': stage_bytes[dominant], 'avg_ms': stage_ms[dominant]},
         'loss_after_timed_steps': loss,
     }
+    if not args.no_single:
+        result['single_expert'] = single_expert_steps(args.steps)
     if not args.no_native:
-        result['native_step'] = native_steps(image, args.native_steps)
+        result['native_step'] = native_steps(args.native_steps)
     if not args.no_reconstruction:
         result['reconstruction'] = reconstruction_pass(args.reconstruction_batch)
     if not args.no_gigapixel:
@@ -386,6 +515,7 @@ def main():
         result['cpu_baseline'] = cpu_baseline(image, ids_host, table16, master, decoder16, trainer.grid.levels,
                                               trainer.grid.expert_params, args.cpu_seconds)
         result['gpu_over_cpu'] = qps / result['cpu_baseline']['value']
+        result['gpu_over_cpu_one_thread'] = qps / result['cpu_baseline']['one_thread']['value']
     print(json.dumps(result))
 
 
