@@ -106,9 +106,11 @@ int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
  * 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),
  * "xcd_remap" (0/1: XCD-major block order), "backward_mode" (1: owner computes, 0: atomics),
- * "bucketed" (0/1: the owner's fine passes walk per-slice coordinate buckets), "owner_lds_bytes",
- * "row_screen", "paired_loads", "forward_lds_bytes".  Results do not depend on them beyond fp32
- * summation order and the owner's fixed-point scale. */
+ * "banded" (the owner's fine passes walk y-band lists of the coordinates: 0 never, 1 always,
+ * 2 (default) when the lists cut the estimated visits at least four times),
+ * "split_target" (banded: coordinate-level visits per owner work item, 0 = automatic),
+ * "owner_lds_bytes", "paired_loads", "forward_lds_bytes".  Results do not depend on them beyond
+ * fp32 summation order and the owner's fixed-point scale. */
 int odie_set_tuning(const char* key, int value);
 
 /* ---------------------------------------------------------------------------------------

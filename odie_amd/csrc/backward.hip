@@ -33,8 +33,24 @@ constexpr int kTransposeRows = 1024;  // rows per transpose block
 constexpr int kMaxRows = 128;         // rows per |upstream| maximum record (two waves of a pass)
 constexpr int kOwnerBlock = 1024;
 constexpr int kBatch = 4;             // coordinates per thread per owner-loop iteration
-constexpr int kRing = 128;            // per-wave LDS queue of candidate coordinates (power of two)
-constexpr int kRingBytes = kOwnerBlock / 64 * kRing * 4;
+constexpr int kWaves = kOwnerBlock / 64;
+
+// Band lists.  A coordinate with x and y in [0, 1] falls in y-band floor(y * kBands) (clamped);
+// any other coordinate (outside the unit square, or NaN) in the last slot, kBands.  A table row
+// of a dense level, or of a hashed one whose slices are aligned blocks wider than a row of
+// corners, is reached only from the cells just above and below it, so a slice of such a level
+// is reached only from a few bands plus that last slot.
+constexpr int kBands = 2047;
+constexpr int kBandSlots = kBands + 1;       // 2048 slots: 64 bitmap words, one per lane
+constexpr int kBandWords = kBandSlots / 32;
+constexpr int kBandBlock = 1024;
+constexpr int kBandPart = 16384;             // coordinates per counting workgroup
+constexpr int kMaxBandParts = 256;
+constexpr int kMaxRuns = kBandSlots / 2;     // runs of marked slots in 2048 bits
+// LDS after a banded pass's accumulators: slot bitmap, run list ranges, piece prefix, scan scratch
+constexpr int kReserveInts = kBandWords + 2 * kMaxRuns + (kMaxRuns + 1) + kWaves + 4;
+constexpr int kReserveBytes = (kReserveInts * 4 + 255) / 256 * 256;
+static_assert(kBandBlock == kOwnerBlock, "the block scan serves both kernels");
 
 struct TransposeArgs {
     const void* upstream;
@@ -183,41 +199,57 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
     }
 }
 
+// Work items.  Every expert has `items` of them, in this order: the coarse-group pass (levels
+// [0, group), when group > 0) split `group_splits` ways, then for each finer level l its
+// `slices[l]` slices, each split `splits[l]` ways (item first_item[l] + slice * splits[l] + s).
+// A split takes one share of the pass's coordinates.  Unbanded, split s of a pass walks the
+// s-th index range of the expert's coordinates and writes fp32 partial slices, summed by
+// split_reduce_kernel.  Banded, the fine passes walk only the coordinates listed in the y-band
+// slots their table rows can reach (band lists below), every pass bounds its fixed-point scale
+// over all of the expert's coordinates, and splits write the raw 64-bit sums, added exactly by
+// banded_reduce_kernel: the gradient does not depend on how a pass is split.
 struct OwnerArgs {
     const float* coords;
     const int32_t* offsets;
     const void* planes;
     const float* blockmax;
     float* grad;
-    float* partial;
+    float* partial;             // unbanded splits: fp32 [max split][experts][expert_params]
+    long long* partial64;       // banded splits: int64 [max split][experts][partial_floats]
+    int32_t* shifts;            // banded splits: [experts][passes] fixed-point shift (kNonFinite: NaN)
+    int64_t partial_floats;
     int64_t n;
     int64_t expert_params;
     int experts;
     int n_levels;
+    int features;
     int group;        // pass 0 covers levels [0, group) when group > 0
     int passes;       // passes per expert
-    int splits;       // coordinate splits per pass
+    int items;        // work items per expert
+    int group_splits;
+    int heavy;        // leading items of every expert scheduled first (work_of)
     int accumulate;   // 1: grad += slice
     int remap;
-    int split_passes; // passes 0 .. split_passes-1 are split `splits` ways
+    int banded;
     DevLevel level[ODIE_MAX_LEVELS];
     int first_pass[ODIE_MAX_LEVELS];
+    int first_item[ODIE_MAX_LEVELS];
     int slices[ODIE_MAX_LEVELS];
+    int splits[ODIE_MAX_LEVELS];
     int slice_entries[ODIE_MAX_LEVELS];
-    int row_bits[ODIE_MAX_LEVELS];   // > 0: slices are aligned 2^row_bits blocks screened by row
-    int cap;                         // int64 accumulators in LDS; the candidate rings follow them
+    int row_bits[ODIE_MAX_LEVELS];   // > 0: slices are aligned 2^row_bits blocks (hashed levels)
+    int cap;                         // int64 accumulators in LDS; the band workspace follows them
     int fused;                       // 1: apply the optimizer step instead of writing the gradient
     AdamStep adam;
-    // Bucketed fine passes: pass p >= fine_first of expert e walks only the coordinates listed
-    // in its bucket, list + start_e * fine_passes + (p - fine_first) * n_e, of length
-    // bucket_count[e * fine_passes + p - fine_first] (start_e, n_e: the expert's coordinates).
-    int bucketed;
-    int fine_first;
-    int fine_passes;
-    const int32_t* bucket_count;
-    const int32_t* bucket_list;
-    int slice_bits[ODIE_MAX_LEVELS]; // bucketed: slice of entry j is j >> slice_bits
+    // band lists (banded): coordinate indices of expert e ordered by y-band slot, slot b at
+    // list[start[e * (kBandSlots + 1) + b] .. start[... + b + 1]); valid when *ordered
+    const int32_t* band_start;
+    const int32_t* band_list;
+    const float2* band_sorted;
+    const int32_t* ordered;
 };
+
+constexpr int32_t kNonFinite = 1 << 30;   // shift recorded for a pass whose upstream bound is not finite
 
 enum LevelKind { kDense = 0, kHashedPow2 = 1, kGeneric = 2, kHashed24 = 3 };
 
@@ -359,166 +391,331 @@ __device__ inline void accumulate_level(const float* coords, const Elem<HALF>* p
     }
 }
 
-// The coordinates listed in list[k0, k1) against one level (a bucket of one slice).
+// Coordinates [base, stop) of expert e: offsets clamped into [0, n] and to a non-empty order.
+__device__ inline void expert_range(const int32_t* offsets, int64_t n, int e, int64_t& base, int64_t& stop) {
+    base = 0;
+    stop = n;
+    if (!offsets) return;
+    base = offsets[e] > 0 ? offsets[e] : 0;
+    stop = offsets[e + 1];
+    if (base > n) base = n;
+    if (stop > n) stop = n;
+    if (stop < base) stop = base;
+}
+
+__device__ inline int band_slot(float x, float y) {
+    if (!(x >= 0.0f && x <= 1.0f && y >= 0.0f && y <= 1.0f)) return kBands;
+    const int b = static_cast<int>(y * static_cast<float>(kBands));
+    return b < kBands ? b : kBands - 1;
+}
+
+// Exclusive prefix of v over the block's threads in thread order; total receives the block's sum.
+__device__ inline int32_t block_exclusive(int32_t v, int32_t* waves, int32_t& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int32_t x = v;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) waves[wave] = x;
+    __syncthreads();
+    int32_t before = 0;
+    total = 0;
+    for (int w = 0; w < kWaves; ++w) {
+        const int32_t s = waves[w];
+        if (w < wave) before += s;
+        total += s;
+    }
+    __syncthreads();
+    return before + x - v;
+}
+
+struct BandArgs {
+    const float* coords;
+    const int32_t* offsets;
+    int64_t n;
+    int experts;
+    int parts;        // counting workgroups per expert
+    int32_t* counts;  // [experts][parts][kBandSlots]: a part's slot counts, then its share's first offsets
+    int32_t* start;   // [experts][kBandSlots + 1]: list position of every slot of the expert, then its end
+    int32_t* list;    // [n]: coordinate index at every list position
+    float2* sorted;   // [n]: that coordinate's (x, y)
+    int32_t* ordered; // 1 when the expert ranges are in order (the lists are then exact)
+};
+
+// COUNT: every part of every expert counts its coordinates per slot.  PLACE (after
+// band_columns_kernel and band_start_kernel): the part writes its coordinates' indices and
+// (x, y) at the slots' cursors.  The order within a slot is free: the owner's integer sums do
+// not depend on it.
+// The grid is a multiple of kXcds; block -> (expert, part) is XCD-major, so the parts of an
+// expert run on one XCD and the lines of its list fill in that XCD's L2.
+template <bool PLACE>
+__global__ __launch_bounds__(kBandBlock) void band_kernel(BandArgs a) {
+    __shared__ int32_t slots[kBandSlots];
+    const uint32_t item = xcd_major(blockIdx.x, gridDim.x);
+    if (item >= static_cast<uint32_t>(a.experts) * a.parts) return;
+    const int e = item / a.parts, part = item % a.parts;
+    int64_t base, stop;
+    expert_range(a.offsets, a.n, e, base, stop);
+    const int64_t share = (stop - base + a.parts - 1) / a.parts;
+    const int64_t b0 = base + share * part < stop ? base + share * part : stop;
+    const int64_t b1 = b0 + share < stop ? b0 + share : stop;
+    int32_t* row = a.counts + (static_cast<int64_t>(e) * a.parts + part) * kBandSlots;
+    const int32_t* first = a.start + static_cast<int64_t>(e) * (kBandSlots + 1);
+    for (int t = threadIdx.x; t < kBandSlots; t += kBandBlock) slots[t] = PLACE ? first[t] + row[t] : 0;
+    __syncthreads();
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBandBlock) {
+        const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
+        const int32_t at = atomicAdd(&slots[band_slot(xy.x, xy.y)], 1);
+        if constexpr (PLACE) {
+            a.list[at] = static_cast<int32_t>(i);
+            a.sorted[at] = xy;
+        }
+    }
+    if constexpr (!PLACE) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < kBandSlots; t += kBandBlock) row[t] = slots[t];
+    }
+}
+
+// Per-slot scan over the parts: a group of `group` lanes (a power of two, at most 64) takes one
+// slot of one expert, each lane `per` consecutive parts.  Every part's count becomes its offset
+// within the slot (counts, in place) and the slot's total goes to start, for band_start_kernel.
+__global__ __launch_bounds__(kBandBlock) void band_columns_kernel(BandArgs a, int group, int per) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    const int slots_per_wave = 64 / group;
+    const int64_t column = wave * slots_per_wave + lane / group;   // expert * kBandSlots + slot
+    if (column >= static_cast<int64_t>(a.experts) * kBandSlots) return;   // whole groups leave together
+    const int e = static_cast<int>(column / kBandSlots), slot = static_cast<int>(column % kBandSlots);
+    const int j = lane % group;
+    const int p0 = j * per < a.parts ? j * per : a.parts;
+    const int p1 = p0 + per < a.parts ? p0 + per : a.parts;
+    int32_t* rows = a.counts + static_cast<int64_t>(e) * a.parts * kBandSlots + slot;
+    int32_t sum = 0;
+    for (int part = p0; part < p1; ++part) sum += rows[static_cast<int64_t>(part) * kBandSlots];
+    int32_t x = sum;
+    for (int d = 1; d < group; d <<= 1) {
+        const int32_t y = __shfl_up(x, d, group);
+        if (j >= d) x += y;
+    }
+    int32_t run = x - sum;
+    for (int part = p0; part < p1; ++part) {
+        int32_t* c = rows + static_cast<int64_t>(part) * kBandSlots;
+        const int32_t count = *c;
+        *c = run;
+        run += count;
+    }
+    if (j == group - 1) a.start[static_cast<int64_t>(e) * (kBandSlots + 1) + slot] = x;
+}
+
+// One workgroup per expert: the slot totals become the list position of every slot, from the
+// expert's first coordinate (and the end after them).  Block 0 records whether the offsets are
+// in order.
+__global__ __launch_bounds__(kBandBlock) void band_start_kernel(BandArgs a) {
+    __shared__ int32_t waves[kWaves];
+    const int e = blockIdx.x;
+    int64_t base, stop;
+    expert_range(a.offsets, a.n, e, base, stop);
+    if (e == 0) {
+        int bad = 0;
+        if (a.offsets)
+            for (int k = threadIdx.x; k < a.experts; k += kBandBlock) bad |= a.offsets[k] > a.offsets[k + 1];
+        bad = __syncthreads_or(bad);
+        if (threadIdx.x == 0) *a.ordered = !bad;
+    }
+    int32_t* first = a.start + static_cast<int64_t>(e) * (kBandSlots + 1);
+    constexpr int kPer = kBandSlots / kBandBlock;
+    int32_t total[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) total[k] = first[threadIdx.x + k * kBandBlock];
+    int32_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        int32_t all;
+        const int32_t before = block_exclusive(total[k], waves, all);
+        first[threadIdx.x + k * kBandBlock] = static_cast<int32_t>(base) + sum + before;
+        sum += all;
+    }
+    if (threadIdx.x == 0) first[kBandSlots] = static_cast<int32_t>(base) + sum;
+}
+
+// Bitmap word w's bits for the slots [lo, hi].
+__device__ inline uint32_t word_bits(int w, int lo, int hi) {
+    const int a = lo > 32 * w ? lo - 32 * w : 0;
+    const int b = hi < 32 * w + 31 ? hi - 32 * w : 31;
+    if (b < a) return 0u;
+    const uint32_t upto = b == 31 ? 0xffffffffu : (2u << b) - 1u;
+    return upto & ~((1u << a) - 1u);
+}
+
+// Slots [lo, hi] holding every coordinate in [0, 1]^2 whose cell row at this level,
+// floor(fma(scale, y, 0.5)), lies in [g0, g1].  fma rounds once (|error| <= 2^-24 (scale + 1)
+// in cell units) and y * kBands once (<= 2^-13 slots); the bounds are widened by both.
+__device__ inline void row_slots(const DevLevel& lv, int64_t g0, int64_t g1, int& lo, int& hi) {
+    const double s = lv.scale;
+    const double slack = ldexp(s + 1.0, -24);
+    double y0 = ((static_cast<double>(g0) - 0.5 - slack) / s) * kBands - 0x1p-12;
+    double y1 = ((static_cast<double>(g1) + 0.5 + slack) / s) * kBands + 0x1p-12;
+    y0 = y0 < 0.0 ? 0.0 : (y0 > kBands - 1 ? kBands - 1 : y0);
+    y1 = y1 < 0.0 ? 0.0 : (y1 > kBands - 1 ? kBands - 1 : y1);
+    lo = static_cast<int>(floor(y0));
+    hi = static_cast<int>(floor(y1));
+}
+
+// Cell rows reached by table entries [a, b) of a dense level through raw corner indices
+// cx + cy * res with 0 <= cx, cy <= cmax: cy in [ceil((a - cmax) / res), floor((b - 1) / res)],
+// and the cells just below those corners.
+__device__ inline void dense_rows(int64_t a, int64_t b, int64_t res, int64_t cmax, int64_t& g0, int64_t& g1) {
+    const int64_t over = a - cmax;
+    const int64_t cy0 = over <= 0 ? 0 : (over + res - 1) / res;
+    g0 = cy0 - 1;
+    g1 = (b - 1) / res;
+}
+
+// Fills the LDS slot bitmap `bits` of the slice [first, last) of level lv (row_bits > 0: the
+// aligned block `slice` of 2^row_bits entries of a hashed level).  Every thread takes part.
+__device__ inline void mark_slice(const DevLevel& lv, uint32_t first, uint32_t last, int row_bits, uint32_t slice,
+                                  uint32_t* bits) {
+    const float top = __builtin_fmaf(lv.scale, 1.0f, 0.5f);   // largest p: x, y in [0, 1], fma is monotone
+    const bool usable = lv.scale >= 1.0f && top < 16777216.0f;
+    const int64_t gmax = usable ? static_cast<int64_t>(floorf(top)) : 0;   // largest cell row or column
+    const int64_t cmax = gmax + 1;                                          // largest corner
+    const int64_t res = lv.res, size = lv.size;
+    bool all = !usable;
+    if (!lv.hashed) {
+        all |= cmax + cmax * res >= 2 * size;   // wrap_index's single subtraction covers every corner
+    } else {
+        all |= row_bits <= 0 || lv.mask == 0;
+    }
+    if (all || !lv.hashed) {
+        // one word per thread of wave 0; dense: the two raw ranges [first, last), [first, last) + size
+        int lo0 = 0, hi0 = kBands - 1, lo1 = 1, hi1 = 0;
+        if (!all) {
+            int64_t g0, g1;
+            dense_rows(first, last, res, cmax, g0, g1);
+            g0 = g0 < 0 ? 0 : g0;
+            g1 = g1 > gmax ? gmax : g1;
+            if (g0 <= g1) row_slots(lv, g0, g1, lo0, hi0); else { lo0 = 1; hi0 = 0; }
+            const int64_t a = first + size, b = last + size < cmax + cmax * res + 1 ? last + size : cmax + cmax * res + 1;
+            if (a < b) {
+                dense_rows(a, b, res, cmax, g0, g1);
+                g0 = g0 < 0 ? 0 : g0;
+                g1 = g1 > gmax ? gmax : g1;
+                if (g0 <= g1) row_slots(lv, g0, g1, lo1, hi1);
+            }
+        }
+        if (threadIdx.x < kBandWords) {
+            uint32_t w = word_bits(threadIdx.x, lo0, hi0) | word_bits(threadIdx.x, lo1, hi1);
+            if (threadIdx.x == kBandWords - 1) w |= 1u << 31;   // the slot of coordinates outside [0, 1]^2
+            bits[threadIdx.x] = w;
+        }
+        __syncthreads();
+        return;
+    }
+    // hashed, aligned blocks of 2^row_bits entries: corner (cx, cy) lies in block
+    // (((cy * prime) & mask) >> row_bits) ^ (cx >> row_bits) (within the mask), and cx >> row_bits
+    // takes the values 0 .. cmax >> row_bits; so row cy reaches block `slice` only when
+    // (((cy * prime) & mask) >> row_bits) ^ slice is one of them.  Cells cy - 1 and cy reach row cy.
+    if (threadIdx.x < kBandWords) bits[threadIdx.x] = threadIdx.x == kBandWords - 1 ? 1u << 31 : 0u;
+    __syncthreads();
+    const uint32_t columns = static_cast<uint32_t>(cmax >> row_bits);
+    for (int64_t cy = threadIdx.x; cy <= cmax; cy += kOwnerBlock) {
+        if ((((hash_row(static_cast<uint32_t>(cy), lv) & lv.mask) >> row_bits) ^ slice) > columns) continue;
+        int lo, hi;
+        row_slots(lv, cy - 1 > 0 ? cy - 1 : 0, cy < gmax ? cy : gmax, lo, hi);
+        for (int w = lo >> 5; w <= (hi >> 5); ++w) atomicOr(bits + w, word_bits(w, lo, hi));
+    }
+    __syncthreads();
+}
+
+// Turns the slot bitmap into runs of consecutive marked slots: the first list position of every
+// run (run_k0) and the runs' sizes concatenated (prefix[r]: list entries before run r, prefix[runs]:
+// all of them).  Returns the number of runs.
+__device__ inline int slice_runs(const uint32_t* bits, const int32_t* start, int32_t* run_k0, int32_t* run_k1,
+                                 int32_t* prefix, int32_t* scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int32_t* count = scratch + kWaves;
+    if (wave == 0) {
+        const uint32_t w = bits[lane];
+        const uint32_t below = __shfl_up(w, 1), above = __shfl_down(w, 1);
+        const uint32_t carry_in = lane > 0 ? below >> 31 : 0u;
+        const uint32_t carry_out = lane < kBandWords - 1 ? above & 1u : 0u;
+        uint32_t starts = w & ~((w << 1) | carry_in);
+        uint32_t ends = w & ~((w >> 1) | (carry_out << 31));
+        // a run may end in a later word: starts and ends are numbered separately
+        const int32_t cs = __popc(starts), ce = __popc(ends);
+        int32_t xs = cs, xe = ce;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int32_t ys = __shfl_up(xs, d), ye = __shfl_up(xe, d);
+            if (lane >= d) {
+                xs += ys;
+                xe += ye;
+            }
+        }
+        for (int32_t r = xs - cs; starts; starts &= starts - 1, ++r) run_k0[r] = 32 * lane + __ffs(starts) - 1;
+        for (int32_t r = xe - ce; ends; ends &= ends - 1, ++r) run_k1[r] = 32 * lane + __ffs(ends) - 1;
+        if (lane == 63) *count = xs;
+    }
+    __syncthreads();
+    const int runs = *count;
+    int32_t size = 0;
+    if (threadIdx.x < runs) {
+        const int32_t k0 = start[run_k0[threadIdx.x]], k1 = start[run_k1[threadIdx.x] + 1];
+        run_k0[threadIdx.x] = k0;
+        size = k1 - k0;
+    }
+    int32_t total;
+    const int32_t before = block_exclusive(size, scratch, total);
+    if (threadIdx.x < runs) prefix[threadIdx.x] = before;
+    if (threadIdx.x == 0) prefix[runs] = total;
+    __syncthreads();
+    return runs;
+}
+
+// Run holding concatenated position v: the largest r < runs with prefix[r] <= v.
+__device__ inline int find_run(const int32_t* prefix, int runs, int32_t v) {
+    int lo = 0, hi = runs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (prefix[mid] <= v) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Concatenated run positions [v0, v1) of a banded slice against one level.  Position v of run r
+// is list entry run_k0[r] + v - prefix[r]: its coordinate's (x, y) in `sorted`, its index (for
+// the upstream) in `list`.  Each wave walks its own contiguous share of [v0, v1), kBatch
+// positions per lane per iteration, 64 apart; a lane's run only moves forward.
 template <int F, bool HALF, int KIND>
-__device__ inline void accumulate_bucket(const float* coords, const Elem<HALF>* plane, const DevLevel lv,
-                                         const int32_t* list, int64_t k0, int64_t k1, uint32_t lo, uint32_t span,
-                                         float scale, unsigned long long* acc) {
-    for (int64_t k = k0 + threadIdx.x; k < k1; k += kBatch * kOwnerBlock) {
-        int32_t at[kBatch];
+__device__ inline void accumulate_runs(const float2* sorted, const Elem<HALF>* plane, const DevLevel lv,
+                                       const int32_t* list, const int32_t* run_k0, const int32_t* prefix, int runs,
+                                       int32_t v0, int32_t v1, uint32_t lo, uint32_t span, float scale,
+                                       unsigned long long* acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int32_t w0 = v0 + static_cast<int32_t>(static_cast<int64_t>(v1 - v0) * wave / kWaves);
+    const int32_t w1 = v0 + static_cast<int32_t>(static_cast<int64_t>(v1 - v0) * (wave + 1) / kWaves);
+    if (w0 >= w1) return;
+    int r = find_run(prefix, runs, w0);
+    for (int32_t v = w0 + lane; v < w1; v += kBatch * 64) {
+        int32_t k[kBatch];
+        bool ok[kBatch];
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
-            const int64_t kk = k + b * kOwnerBlock;
-            at[b] = list[kk < k1 ? kk : k0];
+            const int32_t p = v + b * 64 < w1 ? v + b * 64 : w1 - 1;
+            while (r + 1 < runs && prefix[r + 1] <= p) ++r;
+            k[b] = run_k0[r] + (p - prefix[r]);
+            ok[b] = v + b * 64 < w1;
         }
         float2 xy[kBatch];
         float us[kBatch][F];
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
-            xy[b] = reinterpret_cast<const float2*>(coords)[at[b]];
-            load_upstream<F, HALF>(plane, at[b], scale, k + b * kOwnerBlock < k1, us[b]);
+            xy[b] = sorted[k[b]];
+            load_upstream<F, HALF>(plane, list[k[b]], scale, ok[b], us[b]);
         }
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
-    }
-}
-
-// A hashed level whose table slice is the aligned block of 2^row_bits entries number `slice`,
-// with 2^row_bits above the level's resolution: corner (cx, cy) with cx <= res lands in slice
-// ((cy * 2654435761) & mask) >> row_bits whatever cx is, so a coordinate can only touch the
-// slice through its rows gy or gy+1.  Each wave screens its own contiguous share of the
-// coordinates with that y-only test, queues the candidates in its private LDS ring and runs
-// the full contribution only for them, 64 at a time.  Coordinates with x outside [0,1] are
-// always queued (their corner columns are not bounded by the resolution).
-template <int F, bool HALF>
-__device__ inline void accumulate_rows(const float* coords, const Elem<HALF>* plane, const DevLevel lv, int64_t b0,
-                                       int64_t b1, uint32_t lo, uint32_t span, float scale, unsigned long long* acc,
-                                       int32_t* ring, uint32_t row_bits, uint32_t slice) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int kWaves = kOwnerBlock / 64;
-    const int64_t per = ((b1 - b0 + kWaves - 1) / kWaves + 63) / 64 * 64;
-    const int64_t w0 = b0 + wave * per < b1 ? b0 + wave * per : b1;
-    const int64_t w1 = w0 + per < b1 ? w0 + per : b1;
-    const uint64_t below = (uint64_t{1} << lane) - 1;
-    const uint32_t row_mask = lv.mask >> row_bits;
-    uint32_t head = 0, count = 0;
-    auto drain = [&](uint32_t take) {
-        const bool active = static_cast<uint32_t>(lane) < take;
-        const int64_t i = active ? ring[(head + lane) & (kRing - 1)] : b0;
-        const float2 xy = reinterpret_cast<const float2*>(coords)[i];
-        float us[F];
-        load_upstream<F, HALF>(plane, i, scale, active, us);
-        if (lv.mask < (1u << 24)) contribute<F, kHashed24>(xy.x, xy.y, us, lv, lo, span, acc);
-        else contribute<F, kHashedPow2>(xy.x, xy.y, us, lv, lo, span, acc);
-        head += take;
-        count -= take;
-    };
-    for (int64_t g = w0; g < w1; g += 64 * kBatch) {
-        float2 xy[kBatch];
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int64_t i = g + b * 64 + lane;
-            xy[b] = reinterpret_cast<const float2*>(coords)[i < w1 ? i : b0];
-        }
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int64_t i = g + b * 64 + lane;
-            const float py = __builtin_fmaf(lv.scale, xy[b].y, 0.5f);
-            const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(floorf(py)));
-            const uint32_t r0 = (hash_row(gy, lv) >> row_bits) & row_mask;
-            const uint32_t r1 = (hash_row(gy + 1u, lv) >> row_bits) & row_mask;
-            const bool inside = xy[b].x >= 0.0f && xy[b].x <= 1.0f;
-            const bool pick = i < w1 && (r0 == slice || r1 == slice || !inside);
-            const uint64_t picks = __ballot(pick);
-            if (pick) ring[(head + count + __popcll(picks & below)) & (kRing - 1)] = static_cast<int32_t>(i);
-            count += __popcll(picks);
-            if (count >= 64) drain(64);
-        }
-    }
-    while (count > 0) drain(count < 64 ? count : 64);
-}
-
-// Bucketing of the fine passes: for every coordinate of an expert and every fine level, the
-// distinct slices its four corners fall in; each (expert, slice) bucket receives the
-// coordinate's index once.  A workgroup counts its share of one expert's coordinates per bucket
-// in LDS, reserves its run of every bucket with one global atomic, then writes the indices.
-// The order inside a bucket does not matter: the owner's integer sums are order free.
-constexpr int kBucketBlock = 256;
-
-template <int KIND>
-__device__ inline int slices_of(float x, float y, const DevLevel& lv, int bits, int slices[4]) {
-    const float px = __builtin_fmaf(lv.scale, x, 0.5f);
-    const float py = __builtin_fmaf(lv.scale, y, 0.5f);
-    const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(floorf(px)));
-    const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(floorf(py)));
-    uint32_t idx[4];
-    corner_index<KIND>(gx, gy, lv, idx);
-    int count = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int slice = static_cast<int>(idx[k] >> bits);
-        bool seen = false;
-#pragma unroll
-        for (int j = 0; j < k; ++j) seen |= j < count && slices[j] == slice;
-        if (!seen) slices[count++] = slice;
-    }
-    return count;
-}
-
-template <bool PLACE>
-__device__ inline void bucket_coordinate(const OwnerArgs& a, float x, float y, int32_t* bins, int32_t* list,
-                                         int64_t list_base, int64_t stride, int32_t index) {
-    for (int l = a.group; l < a.n_levels; ++l) {
-        const DevLevel& lv = a.level[l];
-        int slices[4];
-        int count;
-        switch (level_kind(lv)) {
-            case kHashed24: count = slices_of<kHashed24>(x, y, lv, a.slice_bits[l], slices); break;
-            case kHashedPow2: count = slices_of<kHashedPow2>(x, y, lv, a.slice_bits[l], slices); break;
-            case kGeneric: count = slices_of<kGeneric>(x, y, lv, a.slice_bits[l], slices); break;
-            default: count = slices_of<kDense>(x, y, lv, a.slice_bits[l], slices); break;
-        }
-        for (int j = 0; j < count; ++j) {
-            const int q = a.first_pass[l] - a.fine_first + (slices[j] < a.slices[l] ? slices[j] : a.slices[l] - 1);
-            const int32_t at = atomicAdd(bins + q, 1);
-            if constexpr (PLACE) list[list_base + static_cast<int64_t>(q) * stride + bins[a.fine_passes + q] + at] = index;
-        }
-    }
-}
-
-__global__ __launch_bounds__(kBucketBlock) void bucket_kernel(OwnerArgs a, int bsplits, int32_t* counts,
-                                                              int32_t* list) {
-    extern __shared__ int32_t bins[];   // [fine_passes] counts / cursors, then [fine_passes] run starts
-    const int e = blockIdx.x / bsplits, s = blockIdx.x % bsplits;
-    int64_t base = 0, stop = a.n;
-    if (a.offsets) {
-        base = a.offsets[e];
-        stop = a.offsets[e + 1];
-        if (stop < base) stop = base;
-        if (stop > a.n) stop = a.n;
-        if (base > stop) base = stop;
-    }
-    const int64_t share = (stop - base + bsplits - 1) / bsplits;
-    const int64_t b0 = base + share * s < stop ? base + share * s : stop;
-    const int64_t b1 = b0 + share < stop ? b0 + share : stop;
-    for (int q = threadIdx.x; q < a.fine_passes; q += kBucketBlock) bins[q] = 0;
-    __syncthreads();
-    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBucketBlock) {
-        const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
-        bucket_coordinate<false>(a, xy.x, xy.y, bins, nullptr, 0, 0, 0);
-    }
-    __syncthreads();
-    int32_t* row = counts + static_cast<int64_t>(e) * a.fine_passes;
-    for (int q = threadIdx.x; q < a.fine_passes; q += kBucketBlock) {
-        const int32_t c = bins[q];
-        bins[a.fine_passes + q] = c ? atomicAdd(row + q, c) : 0;
-        bins[q] = 0;
-    }
-    __syncthreads();
-    const int64_t list_base = base * a.fine_passes;
-    for (int64_t i = b0 + threadIdx.x; i < b1; i += kBucketBlock) {
-        const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
-        bucket_coordinate<true>(a, xy.x, xy.y, bins, list, list_base, stop - base, static_cast<int32_t>(i));
     }
 }
 
@@ -553,34 +750,35 @@ __device__ inline uint32_t work_of(uint32_t block, uint32_t blocks, int remap, u
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
-    __shared__ float reduce[kOwnerBlock / 64];
+    __shared__ float reduce[kWaves];
     using U = Elem<HALF>;
-    // Work items per expert: the first split_passes passes split `splits` ways (all of them, or
-    // only the coarse group pass), the others whole.
-    const int split_passes = a.split_passes;
-    const uint32_t per_expert = static_cast<uint32_t>(split_passes * a.splits + (a.passes - split_passes));
+    const uint32_t per_expert = static_cast<uint32_t>(a.items);
     const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
-    const uint32_t heavy = a.group > 0 && split_passes > 0 ? static_cast<uint32_t>(a.splits) : 0u;
-    const uint32_t work = work_of(blockIdx.x, gridDim.x, a.remap, per_expert, heavy);
+    const uint32_t work = work_of(blockIdx.x, gridDim.x, a.remap, per_expert, static_cast<uint32_t>(a.heavy));
     if (work >= total) return;
     const int e = work / per_expert;
     const int r = work % per_expert;
-    const int p = r < split_passes * a.splits ? r / a.splits : split_passes + (r - split_passes * a.splits);
-    const int s = r < split_passes * a.splits ? r % a.splits : 0;
-    const int splits = p < split_passes ? a.splits : 1;   // ways this pass is split
 
-    // Pass -> levels [l0, l1) and the slice [lo, hi) of the expert's gradient (in floats).
-    int l0, l1;
+    // Item -> pass p, split s of `splits`, levels [l0, l1) and the slice [lo, hi) of the
+    // expert's gradient (in floats).
+    const bool grouped = r < a.group_splits;
+    int p, s, splits, l0, l1, slice = 0;
     uint32_t lo, hi;
-    if (a.group > 0 && p == 0) {
+    if (grouped) {
+        p = 0;
+        s = r;
+        splits = a.group_splits;
         l0 = 0;
         l1 = a.group;
         lo = 0;
         hi = (a.level[a.group - 1].offset + a.level[a.group - 1].size) * F;
     } else {
         int l = a.group;
-        while (l + 1 < a.n_levels && a.first_pass[l + 1] <= p) ++l;
-        const int slice = p - a.first_pass[l];
+        while (l + 1 < a.n_levels && a.first_item[l + 1] <= r) ++l;
+        splits = a.splits[l];
+        slice = (r - a.first_item[l]) / splits;
+        s = (r - a.first_item[l]) % splits;
+        p = a.first_pass[l] + slice;
         const uint32_t first = static_cast<uint32_t>(slice) * a.slice_entries[l];
         uint32_t last = first + a.slice_entries[l];
         if (last > a.level[l].size) last = a.level[l].size;
@@ -591,22 +789,14 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     }
     const uint32_t span = hi - lo;
 
-    // Coordinates of this expert (and split).
-    int64_t base = 0, stop = a.n;
-    if (a.offsets) {
-        base = a.offsets[e];
-        stop = a.offsets[e + 1];
-        if (stop < base) stop = base;
-        if (stop > a.n) stop = a.n;
-        if (base > stop) base = stop;
-    }
+    // Coordinates of this expert, and this split's index range of them.
+    int64_t base, stop;
+    expert_range(a.offsets, a.n, e, base, stop);
     const int64_t share = (stop - base + splits - 1) / splits;
     const int64_t b0 = base + share * s < stop ? base + share * s : stop;
     const int64_t b1 = b0 + share < stop ? b0 + share : stop;
-    const bool bucket = a.bucketed && p >= a.fine_first;
-    // a bucketed pass bounds its scale over all of the expert's coordinates (every split of the
-    // pass then shares one scale); otherwise over this split's range
-    const int64_t m0 = bucket ? base : b0, m1 = bucket ? stop : b1;
+    // banded: every split of a pass bounds the scale over all of the expert's coordinates
+    const int64_t m0 = a.banded ? base : b0, m1 = a.banded ? stop : b1;
 
     // Fixed-point scale from the bound 4 * count * max|upstream| over this range and levels.
     float bound = 0.0f;
@@ -626,7 +816,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) acc[j] = 0ull;
     __syncthreads();
     float peak = 0.0f;
-    for (int w = 0; w < kOwnerBlock / 64; ++w) peak = (reduce[w] > peak || reduce[w] != reduce[w]) ? reduce[w] : peak;
+    for (int w = 0; w < kWaves; ++w) peak = (reduce[w] > peak || reduce[w] != reduce[w]) ? reduce[w] : peak;
     // Scale 2^shift: every contribution |w*u| <= peak maps below 2^31 (so it converts with one
     // rint + cvt_i32), and 4*count contributions of that size stay below 2^62 in the int64 sum.
     const double limit = 4.0 * static_cast<double>(m1 - m0) * static_cast<double>(peak);
@@ -640,34 +830,55 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     const float scale = ldexpf(1.0f, shift);
     const bool finite = !(peak != peak) && peak <= 3.0e38f;
 
-    int32_t* ring = reinterpret_cast<int32_t*>(acc + a.cap) + (threadIdx.x / 64) * kRing;
+    // A banded fine pass walks the pieces of its share of the band-list runs its rows reach.
+    const bool banded = a.banded && !grouped && *a.ordered;
+    int32_t* reserve = reinterpret_cast<int32_t*>(acc + a.cap);
+    uint32_t* bits = reinterpret_cast<uint32_t*>(reserve);
+    int32_t* run_k0 = reserve + kBandWords;
+    int32_t* run_k1 = run_k0 + kMaxRuns;
+    int32_t* prefix = run_k1 + kMaxRuns;
+    int32_t* scratch = prefix + kMaxRuns + 1;
+    int runs = 0;
+    int64_t q0 = 0, q1 = 0;
+    if (banded) {
+        const DevLevel& lv = a.level[l0];
+        mark_slice(lv, lo / F - lv.offset, hi / F - lv.offset, a.row_bits[l0], static_cast<uint32_t>(slice), bits);
+        runs = slice_runs(bits, a.band_start + static_cast<int64_t>(e) * (kBandSlots + 1), run_k0, run_k1, prefix,
+                          scratch);
+        const int64_t listed = prefix[runs];
+        q0 = listed * s / splits;
+        q1 = listed * (s + 1) / splits;
+    }
+
     for (int l = l0; l < l1; ++l) {
         const DevLevel lv = a.level[l];
         const U* plane = reinterpret_cast<const U*>(a.planes) + static_cast<size_t>(l) * a.n * F;
-        if (bucket) {
-            const int q = p - a.fine_first;
-            const int64_t count = a.bucket_count[static_cast<int64_t>(e) * a.fine_passes + q];
-            const int32_t* list = a.bucket_list + base * a.fine_passes + static_cast<int64_t>(q) * (stop - base);
-            const int64_t k0 = 0, k1 = count;
-            switch (level_kind(lv)) {
-                case kHashed24: accumulate_bucket<F, HALF, kHashed24>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
-                case kHashedPow2: accumulate_bucket<F, HALF, kHashedPow2>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
-                case kGeneric: accumulate_bucket<F, HALF, kGeneric>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
-                default: accumulate_bucket<F, HALF, kDense>(a.coords, plane, lv, list, k0, k1, lo, span, scale, acc); break;
+        const int kind = level_kind(lv);
+        if (banded) {
+            if (runs == 0) break;
+            switch (kind) {
+                case kHashed24: accumulate_runs<F, HALF, kHashed24>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                case kHashedPow2: accumulate_runs<F, HALF, kHashedPow2>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                case kGeneric: accumulate_runs<F, HALF, kGeneric>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                default: accumulate_runs<F, HALF, kDense>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
             }
-        } else if (a.row_bits[l] > 0 && !(a.group > 0 && p == 0))
-            accumulate_rows<F, HALF>(a.coords, plane, lv, b0, b1, lo, span, scale, acc, ring, a.row_bits[l],
-                                     static_cast<uint32_t>(p - a.first_pass[l]));
-        else if (lv.hashed && lv.mask && lv.mask < (1u << 24))
-            accumulate_level<F, HALF, kHashed24>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
-        else if (lv.hashed && lv.mask)
-            accumulate_level<F, HALF, kHashedPow2>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
-        else if (lv.hashed)
-            accumulate_level<F, HALF, kGeneric>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
-        else
-            accumulate_level<F, HALF, kDense>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+        } else {
+            switch (kind) {
+                case kHashed24: accumulate_level<F, HALF, kHashed24>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                case kHashedPow2: accumulate_level<F, HALF, kHashedPow2>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                case kGeneric: accumulate_level<F, HALF, kGeneric>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                default: accumulate_level<F, HALF, kDense>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+            }
+        }
     }
     __syncthreads();
+    if (splits > 1 && a.banded) {
+        // raw 64-bit sums: banded_reduce_kernel adds the splits exactly and applies the scale
+        long long* out = a.partial64 + (static_cast<int64_t>(s) * a.experts + e) * a.partial_floats + lo;
+        for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[j]);
+        if (s == 0 && threadIdx.x == 0) a.shifts[static_cast<int64_t>(e) * a.passes + p] = finite ? shift : kNonFinite;
+        return;
+    }
     const double unscale = ldexp(1.0, -shift);
     if (a.fused && splits == 1) {
         // The final gradient of these parameters is in LDS: update them right here.  One
@@ -675,15 +886,14 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         // any of them is used, to keep memory latency off the critical path.
         const AdamStep& o = a.adam;
         const int64_t first = static_cast<int64_t>(e) * a.expert_params + lo;
-        constexpr int kBatch = 4;
         for (uint32_t j0 = threadIdx.x; j0 < span; j0 += kBatch * kOwnerBlock) {
-            float g[kBatch], p[kBatch], m[kBatch], v[kBatch];
+            float g[kBatch], w[kBatch], m[kBatch], v[kBatch];
             uint32_t age[kBatch];
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
                 const uint32_t j = j0 + k * kOwnerBlock;
                 const int64_t i = first + (j < span ? j : 0);
-                p[k] = o.master[i];
+                w[k] = o.master[i];
                 m[k] = o.m[i];
                 v[k] = o.v[i];
                 age[k] = o.variant != 0 ? o.steps[i] : 0u;
@@ -695,13 +905,13 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                 const uint32_t j = j0 + k * kOwnerBlock;
                 if (j >= span) continue;
                 const int64_t i = first + j;
-                if (adam_math(o, g[k], p[k], m[k], v[k], age[k])) {
-                    o.master[i] = p[k];
+                if (adam_math(o, g[k], w[k], m[k], v[k], age[k])) {
+                    o.master[i] = w[k];
                     o.m[i] = m[k];
                     o.v[i] = v[k];
                     if (o.variant != 0) o.steps[i] = age[k];
                 }
-                if (o.half_copy) o.half_copy[i] = half_to_bits(__float2half_rn(p[k]));
+                if (o.half_copy) o.half_copy[i] = half_to_bits(__float2half_rn(w[k]));
             }
         }
         return;
@@ -714,6 +924,50 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         if (!finite) v = __builtin_nanf("");
         if (splits == 1 && a.accumulate) v += out[j];
         out[j] = v;
+    }
+}
+
+// Banded splits: every entry of the first partial_floats values of every expert whose pass is
+// split gets the exact sum of its splits' 64-bit partials, scaled by the pass's 2^-shift, and is
+// written (added with accumulate) or handed to the optimizer step, as the owner does unsplit.
+__global__ __launch_bounds__(256) void banded_reduce_kernel(OwnerArgs a) {
+    const int64_t count = static_cast<int64_t>(a.experts) * a.partial_floats;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t y = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; y < count; y += stride) {
+        const int e = static_cast<int>(y / a.partial_floats);
+        const int64_t x = y % a.partial_floats;
+        const uint32_t entry = static_cast<uint32_t>(x / a.features);
+        int l = 0;
+        while (l + 1 < a.n_levels && a.level[l + 1].offset <= entry) ++l;
+        int p = 0, splits = a.group_splits;
+        if (l >= a.group) {
+            p = a.first_pass[l] + static_cast<int>((entry - a.level[l].offset) / a.slice_entries[l]);
+            splits = a.splits[l];
+        }
+        if (splits <= 1) continue;
+        // eight independent loads in flight per round: the splits' partials are far apart
+        const long long* column = a.partial64 + static_cast<int64_t>(e) * a.partial_floats + x;
+        const int64_t step = static_cast<int64_t>(a.experts) * a.partial_floats;
+        long long sum = 0;
+        int s = 0;
+        for (; s + 8 <= splits; s += 8) {
+            long long v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = column[(s + k) * step];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sum += v[k];
+        }
+        for (; s < splits; ++s) sum += column[s * step];
+        const int32_t shift = a.shifts[static_cast<int64_t>(e) * a.passes + p];
+        float v = static_cast<float>(static_cast<double>(sum) * ldexp(1.0, -shift));
+        if (shift == kNonFinite) v = __builtin_nanf("");
+        const int64_t i = static_cast<int64_t>(e) * a.expert_params + x;
+        if (a.fused) {
+            adam_update(a.adam, i, v);
+        } else {
+            if (a.accumulate) v += a.grad[i];
+            a.grad[i] = v;
+        }
     }
 }
 
@@ -743,17 +997,19 @@ int allow_lds(Kernel kernel, size_t bytes) {
     return 0;
 }
 
-// Clears the bucket counts and fills the buckets of every fine pass.
-int launch_buckets(const OwnerArgs& o, int32_t* counts, int32_t* list, hipStream_t s) {
-    if (launch_fill_zero(reinterpret_cast<float*>(counts), static_cast<int64_t>(o.experts) * o.fine_passes, s))
-        return -1;
-    int64_t bsplits = (2048 + o.experts - 1) / o.experts;
-    const int64_t most = o.n / (static_cast<int64_t>(o.experts) * kBucketBlock);
-    if (bsplits > most) bsplits = most > 1 ? most : 1;
-    const size_t shmem = static_cast<size_t>(o.fine_passes) * 2 * sizeof(int32_t);
-    bucket_kernel<<<static_cast<uint32_t>(o.experts * bsplits), kBucketBlock, shmem, s>>>(o, static_cast<int>(bsplits),
-                                                                                           counts, list);
-    return check_launch("owner buckets");
+// Expected fraction of an expert's coordinates listed in the band runs of one slice of level
+// lv (uniform y), used only to size the splits: cell rows the slice's table rows are reached
+// from, over all cell rows, plus a slot at either end of every run.
+double band_coverage(const DevLevel& lv, int64_t entries, int64_t slices, int row_bits) {
+    const double top = std::floor(std::fmaf(lv.scale, 1.0f, 0.5f));
+    if (!(lv.scale >= 1.0f) || !(top < 16777216.0)) return 1.0;
+    const double rows = top + 1.0;                                     // cell rows
+    double share;
+    if (!lv.hashed) share = (static_cast<double>(entries) / lv.res + 3.0) / rows + 2.0 / kBands;
+    else if (row_bits > 0) share = (rows + 1.0) / slices * (std::floor((rows + 1.0) / std::ldexp(1.0, row_bits)) + 1.0) *
+                                   (2.0 / rows + 2.0 / kBands);
+    else share = 1.0;
+    return share < 1.0 ? share : 1.0;
 }
 
 }  // namespace
@@ -764,9 +1020,10 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const bool half = in.up_half != 0;
     const size_t elem = half ? 2 : 4;
     const int64_t lds_bytes = in.lds_bytes;
-    const int64_t cap = (lds_bytes - kRingBytes) / 8 - F;  // int64 accumulators per slice, minus entry rounding
+    // int64 accumulators per slice, minus entry rounding; the band workspace after them (kept in
+    // both modes so that both slice alike and choose the same coarse group)
+    const int64_t cap = (lds_bytes - kReserveBytes) / 8 - F;
     if (cap < 64) return fail("odie_grid_backward: LDS budget too small for the owner backward");
-
     OwnerArgs o{};
     o.coords = in.coords;
     o.offsets = in.offsets;
@@ -774,6 +1031,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.expert_params = in.expert_params;
     o.experts = in.experts;
     o.n_levels = L;
+    o.features = F;
     o.accumulate = in.accumulate;
     o.fused = in.adam != nullptr;
     if (in.adam) o.adam = *in.adam;
@@ -784,26 +1042,46 @@ int launch_owner_backward(const OwnerLaunch& in) {
         grouped += static_cast<int64_t>(in.levels[group].size) * F;
         ++group;
     }
+    int bits = 0;
+    while ((int64_t{2} << bits) * F <= cap) ++bits;   // 2^bits entries: largest block that fits
+    // Slices of the finer levels: as many equal parts as the LDS needs; banded, hashed levels
+    // take aligned blocks of 2^bits entries (a block is reached from the rows whose hash selects it).
+    const auto slice_level = [&](int l, bool band, int64_t& slices, int64_t& entries, int& row_bits) {
+        const DevLevel& lv = in.levels[l];
+        slices = (static_cast<int64_t>(lv.size) * F + cap - 1) / cap;
+        entries = (lv.size + slices - 1) / slices;
+        row_bits = 0;
+        if (band && lv.hashed && lv.mask && (int64_t{1} << bits) < lv.size) {
+            entries = int64_t{1} << bits;
+            slices = lv.size / entries;
+            row_bits = bits;
+        }
+    };
+    // Banded or not: band lists cost a pre-pass and make every listed visit a gather, so they
+    // pay when they cut the visits (coordinates times passes) at least four times over, as with
+    // few experts of large tables (measured on MI355X: 2.3x faster with one expert of 2^19-entry
+    // levels, 1.07x slower with 64 experts of 2^16).  Band lists hold int32 coordinate indices.
+    bool banded = in.banded == 1;
+    if (in.banded == 2 && group < L && in.n < (int64_t{1} << 31) - 1) {
+        double plain = group, listed = group;
+        for (int l = group; l < L; ++l) {
+            int64_t slices, entries;
+            int row_bits;
+            slice_level(l, false, slices, entries, row_bits);
+            plain += slices;
+            slice_level(l, true, slices, entries, row_bits);
+            listed += slices * band_coverage(in.levels[l], entries, slices, row_bits);
+        }
+        banded = listed * 4.0 <= plain;
+    }
+    banded = banded && in.n < (int64_t{1} << 31) - 1;
+    o.banded = banded;
     int passes = group > 0 ? 1 : 0;
     for (int l = 0; l < L; ++l) {
         o.level[l] = in.levels[l];
         if (l < group) continue;
-        const int64_t floats = static_cast<int64_t>(in.levels[l].size) * F;
-        int64_t slices = (floats + cap - 1) / cap;
-        int64_t entries = (in.levels[l].size + slices - 1) / slices;
-        int bits = 0;
-        while ((int64_t{2} << bits) * F <= cap) ++bits;   // 2^bits entries: largest block that fits
-        if (in.bucketed) {
-            // aligned power-of-two slices: the bucketing pass finds a corner's slice by a shift
-            entries = int64_t{1} << bits;
-            slices = (in.levels[l].size + entries - 1) / entries;
-            o.slice_bits[l] = bits;
-        } else if (in.row_screen && in.levels[l].hashed && in.levels[l].mask &&
-                   (int64_t{1} << bits) > in.levels[l].res && (int64_t{1} << bits) < in.levels[l].size) {
-            entries = int64_t{1} << bits;
-            slices = in.levels[l].size / entries;
-            o.row_bits[l] = bits;
-        }
+        int64_t slices, entries;
+        slice_level(l, banded, slices, entries, o.row_bits[l]);
         o.slices[l] = static_cast<int>(slices);
         o.slice_entries[l] = static_cast<int>(entries);
         o.first_pass[l] = passes;
@@ -812,76 +1090,161 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.group = group;
     o.passes = passes;
     o.cap = static_cast<int>(cap + F);
-    o.fine_first = group > 0 ? 1 : 0;
-    o.fine_passes = passes - o.fine_first;
-    o.bucketed = in.bucketed && o.fine_passes > 0 && static_cast<int64_t>(o.fine_passes) * 8 <= 64 * 1024 &&
-                 static_cast<int64_t>(o.fine_passes) * in.n < (int64_t{1} << 31);
-    // Splits.  Too few work items to fill the GPU: every pass is split over the coordinates (and
-    // the partials summed by split_reduce_kernel).  Otherwise only the coarse-group pass may be:
-    // it walks every coordinate through `group` fully landing levels, about group + 1 times the
-    // work of a fine slice (measured: ~6x with 5 levels), and when that alone exceeds one CU's
-    // share of the whole pass it would set the kernel's length (the native step's single-expert
-    // batch), so it is cut into pieces of about that share.
-    const int64_t per_pass = static_cast<int64_t>(in.experts) * passes;
-    int splits = 1;
-    int split_passes = passes;
-    if (per_pass < 128) {
-        const int64_t want = (512 + per_pass - 1) / per_pass;
-        const int64_t most = in.n / (static_cast<int64_t>(in.experts) * 16384);
-        splits = static_cast<int>(want < most ? want : (most > 1 ? most : 1));
-    } else if (group > 0) {
-        const double share = static_cast<double>(in.experts) * (passes + group) / kCus;   // fine-slice units
-        if (group + 1 > share) {
-            const int64_t want = static_cast<int64_t>(std::ceil((group + 1) / (share > 1.0 ? share : 1.0)));
-            const int64_t most = in.n / (static_cast<int64_t>(in.experts) * 4096);
-            splits = static_cast<int>(want < most ? want : (most > 1 ? most : 1));
-        }
-        split_passes = 1;
-    }
-    if (o.bucketed) split_passes = o.fine_first;   // a bucket is summed whole (its order varies)
-    if (splits == 1) split_passes = passes;
-    o.splits = splits;
-    o.split_passes = split_passes;
 
-    // Workspace: level-major planes, block maxima, split partials.
+    // Splits per pass.
+    int group_splits = group > 0 ? 1 : 0;
+    for (int l = group; l < L; ++l) o.splits[l] = 1;
+    int64_t max_splits = 1;
+    if (banded) {
+        // Size every item near a target share of the estimated work (coordinate-level visits):
+        // an eighth of a CU's share of the whole pass, at least 65536 visits (each item pays a
+        // fixed set-up; measured best on MI355X for one expert of 2^19-entry levels and 2^22
+        // coordinates).  A visit of the coarse group counts kGroupCost times: all of its
+        // contributions land in its slice (measured).
+        constexpr double kGroupCost = 2.5;
+        const double per = static_cast<double>(in.n) / in.experts;
+        double work = kGroupCost * group * per;
+        for (int l = group; l < L; ++l)
+            work += o.slices[l] * per * band_coverage(in.levels[l], o.slice_entries[l], o.slices[l], o.row_bits[l]);
+        constexpr double kLeastItem = 65536.0;
+        double target = in.split_target > 0 ? static_cast<double>(in.split_target) : work * in.experts / (8.0 * kCus);
+        if (in.split_target <= 0 && target < kLeastItem) target = kLeastItem;
+        const auto ways = [&](double visits, double most) {
+            const double w = std::ceil(visits / target);
+            return static_cast<int>(w < 1.0 ? 1.0 : (w > most ? most : w));
+        };
+        if (group > 0) group_splits = ways(kGroupCost * group * per, 256.0);
+        for (int l = group; l < L; ++l)
+            o.splits[l] = ways(per * band_coverage(in.levels[l], o.slice_entries[l], o.slices[l], o.row_bits[l]), 64.0);
+    } else {
+        // Too few work items to fill the GPU: every pass is split over the coordinates (and the
+        // partials summed by split_reduce_kernel).  Otherwise only the coarse-group pass may be:
+        // it walks every coordinate through `group` fully landing levels, about group + 1 times
+        // the work of a fine slice (measured: ~6x with 5 levels), and when that alone exceeds one
+        // CU's share of the whole pass it would set the kernel's length, so it is cut into
+        // pieces of about that share.
+        const int64_t per_pass = static_cast<int64_t>(in.experts) * passes;
+        int splits = 1;
+        bool all = false;
+        if (per_pass < 128) {
+            const int64_t want = (512 + per_pass - 1) / per_pass;
+            const int64_t most = in.n / (static_cast<int64_t>(in.experts) * 16384);
+            splits = static_cast<int>(want < most ? want : (most > 1 ? most : 1));
+            all = true;
+        } else if (group > 0) {
+            const double share = static_cast<double>(in.experts) * (passes + group) / kCus;   // fine-slice units
+            if (group + 1 > share) {
+                const int64_t want = static_cast<int64_t>(std::ceil((group + 1) / (share > 1.0 ? share : 1.0)));
+                const int64_t most = in.n / (static_cast<int64_t>(in.experts) * 4096);
+                splits = static_cast<int>(want < most ? want : (most > 1 ? most : 1));
+            }
+        }
+        if (group > 0) group_splits = splits;
+        if (all)
+            for (int l = group; l < L; ++l) o.splits[l] = splits;
+    }
+    int items = group_splits;
+    int heavy = group_splits;
+    bool leading = banded;   // banded: the split levels' items (each about the target) come first
+    int64_t split_floats = group_splits > 1 ? grouped : 0;   // values of the expert that splits cover
+    for (int l = group; l < L; ++l) {
+        o.first_item[l] = items;
+        items += o.slices[l] * o.splits[l];
+        if (o.splits[l] > 1) split_floats = static_cast<int64_t>(in.levels[l].offset + in.levels[l].size) * F;
+        leading = leading && o.splits[l] > 1;
+        if (leading) heavy = items;
+        if (o.splits[l] > max_splits) max_splits = o.splits[l];
+    }
+    if (group_splits > max_splits) max_splits = group_splits;
+    o.items = items;
+    o.group_splits = group_splits;
+    o.heavy = heavy;
+    if (static_cast<int64_t>(in.experts) * items >= (int64_t{1} << 31))
+        return fail("odie_grid_backward: too many owner work items");
+
+    // Workspace: level-major planes, block maxima, split partials, band lists.
     const int64_t row_blocks = (in.n + kTransposeRows - 1) / kTransposeRows;
     const int64_t records = (in.n + kMaxRows - 1) / kMaxRows;
-    const size_t planes_bytes = in.planes ? 0 : (static_cast<size_t>(in.n) * L * F * elem + 255) / 256 * 256;
-    const size_t max_bytes = in.planes ? 0 : (static_cast<size_t>(records) * L * 4 + 255) / 256 * 256;
+    const auto align = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+    const size_t planes_bytes = in.planes ? 0 : align(static_cast<size_t>(in.n) * L * F * elem);
+    const size_t max_bytes = in.planes ? 0 : align(static_cast<size_t>(records) * L * 4);
     const size_t total_params = static_cast<size_t>(in.experts) * in.expert_params;
-    const size_t partial_bytes = (splits > 1 ? static_cast<size_t>(splits) * total_params * 4 + 255 : 0) / 256 * 256;
-    const size_t count_bytes =
-        o.bucketed ? (static_cast<size_t>(in.experts) * o.fine_passes * 4 + 255) / 256 * 256 : 0;
-    const size_t list_bytes = o.bucketed ? static_cast<size_t>(in.n) * o.fine_passes * 4 : 0;
-    char* space = static_cast<char*>(
-        workspace(planes_bytes + max_bytes + partial_bytes + count_bytes + list_bytes, in.stream));
+    const bool split = max_splits > 1;
+    const size_t partial_bytes = split && !banded ? align(static_cast<size_t>(max_splits) * total_params * 4) : 0;
+    const size_t partial64_bytes =
+        split && banded ? align(static_cast<size_t>(max_splits) * in.experts * split_floats * 8) : 0;
+    const size_t shift_bytes = split && banded ? align(static_cast<size_t>(in.experts) * passes * 4) : 0;
+    const bool lists = banded && group < L;
+    const int parts = [&] {
+        const int64_t want = (in.n / in.experts + kBandPart - 1) / kBandPart;
+        return static_cast<int>(want < 1 ? 1 : (want > kMaxBandParts ? kMaxBandParts : want));
+    }();
+    const size_t count_bytes = lists ? align(static_cast<size_t>(in.experts) * parts * kBandSlots * 4) : 0;
+    const size_t start_bytes = lists ? align(static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4 + 4) : 0;
+    const size_t list_bytes = lists ? align(static_cast<size_t>(in.n) * 4) : 0;
+    const size_t sorted_bytes = lists ? align(static_cast<size_t>(in.n) * 8) : 0;
+    const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, shift_bytes,
+                            count_bytes, start_bytes, list_bytes, sorted_bytes};
+    constexpr int kParts = sizeof(sizes) / sizeof(sizes[0]);
+    size_t at[kParts], sum = 0;
+    for (int k = 0; k < kParts; ++k) {
+        at[k] = sum;
+        sum += sizes[k];
+    }
+    char* space = static_cast<char*>(workspace(sum, in.stream));
     if (!space) return -1;
     // upstream already level-major with its maxima (the caller wrote them): no transpose
     const bool given = in.planes != nullptr;
-    o.planes = given ? in.planes : space;
-    o.blockmax = given ? in.blockmax : reinterpret_cast<float*>(space + planes_bytes);
-    o.partial = reinterpret_cast<float*>(space + planes_bytes + max_bytes);
-    int32_t* bucket_count = reinterpret_cast<int32_t*>(space + planes_bytes + max_bytes + partial_bytes);
-    int32_t* bucket_list = reinterpret_cast<int32_t*>(space + planes_bytes + max_bytes + partial_bytes + count_bytes);
-    o.bucket_count = bucket_count;
-    o.bucket_list = bucket_list;
+    o.planes = given ? in.planes : space + at[0];
+    o.blockmax = given ? in.blockmax : reinterpret_cast<float*>(space + at[1]);
+    o.partial = reinterpret_cast<float*>(space + at[2]);
+    o.partial64 = reinterpret_cast<long long*>(space + at[3]);
+    o.partial_floats = split_floats;
+    o.shifts = reinterpret_cast<int32_t*>(space + at[4]);
+    o.band_start = reinterpret_cast<const int32_t*>(space + at[6]);
+    o.band_list = reinterpret_cast<const int32_t*>(space + at[7]);
+    o.band_sorted = reinterpret_cast<const float2*>(space + at[8]);
+    o.ordered = reinterpret_cast<const int32_t*>(space + at[6] + static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4);
     o.grad = in.grad;
+    hipStream_t s = in.stream;
+
+    if (lists) {
+        BandArgs b{};
+        b.coords = in.coords;
+        b.offsets = in.offsets;
+        b.n = in.n;
+        b.experts = in.experts;
+        b.parts = parts;
+        b.counts = reinterpret_cast<int32_t*>(space + at[5]);
+        b.start = reinterpret_cast<int32_t*>(space + at[6]);
+        b.list = reinterpret_cast<int32_t*>(space + at[7]);
+        b.sorted = reinterpret_cast<float2*>(space + at[8]);
+        b.ordered = const_cast<int32_t*>(o.ordered);
+        const uint32_t blocks = round_up(static_cast<uint32_t>(in.experts) * parts, kXcds);
+        int group = 1;
+        while (group < parts && group < 64) group <<= 1;
+        const int per = (parts + group - 1) / group;
+        const int64_t column_waves = static_cast<int64_t>(in.experts) * kBandSlots / (64 / group);
+        const uint32_t column_blocks = static_cast<uint32_t>((column_waves + kWaves - 1) / kWaves);
+        band_kernel<false><<<blocks, kBandBlock, 0, s>>>(b);
+        band_columns_kernel<<<column_blocks, kBandBlock, 0, s>>>(b, group, per);
+        band_start_kernel<<<static_cast<uint32_t>(in.experts), kBandBlock, 0, s>>>(b);
+        band_kernel<true><<<blocks, kBandBlock, 0, s>>>(b);
+        if (check_launch("owner band lists")) return -1;
+    }
 
     TransposeArgs t{};
     t.upstream = in.upstream;
-    t.planes = space;
-    t.blockmax = reinterpret_cast<float*>(space + planes_bytes);
+    t.planes = space + at[0];
+    t.blockmax = reinterpret_cast<float*>(space + at[1]);
     t.n = in.n;
     t.width = in.up_width;
     t.n_levels = L;
     t.vec_rows = (reinterpret_cast<uintptr_t>(in.upstream) % 16 == 0) && (in.up_width * elem) % 16 == 0 &&
                  (L * F * elem) % 16 == 0;
     const uint32_t tblocks = static_cast<uint32_t>(row_blocks);
-    const size_t shmem = static_cast<size_t>(cap + F) * 8 + kRingBytes;
-    const uint32_t total =
-        static_cast<uint32_t>(in.experts * (static_cast<int64_t>(split_passes) * splits + (passes - split_passes)));
-    const uint32_t oblocks = round_up(total, kXcds);
-    hipStream_t s = in.stream;
+    const size_t shmem = static_cast<size_t>(cap + F) * 8 + kReserveBytes;
+    const uint32_t oblocks = round_up(static_cast<uint32_t>(static_cast<int64_t>(in.experts) * items), kXcds);
 
 #define ODIE_TRANSPOSE(FF, HH)                                                                          \
     do {                                                                                                \
@@ -893,7 +1256,6 @@ int launch_owner_backward(const OwnerLaunch& in) {
     } while (0)
 #define ODIE_OWNER(FF, HH)                                                                              \
     do {                                                                                                \
-        if (o.bucketed && launch_buckets(o, bucket_count, bucket_list, s)) return -1;                  \
         if (allow_lds(owner_kernel<FF, HH>, shmem)) return -1;                                          \
         owner_kernel<FF, HH><<<oblocks, kOwnerBlock, shmem, s>>>(o);                                    \
     } while (0)
@@ -911,15 +1273,19 @@ int launch_owner_backward(const OwnerLaunch& in) {
 #undef ODIE_BOTH
 #undef ODIE_OWNER
 #undef ODIE_TRANSPOSE
-    if (splits > 1 && split_passes > 0) {
-        // only the coarse group pass split: the expert's first values
-        const int64_t prefix = split_passes < passes
-            ? static_cast<int64_t>(in.levels[group - 1].offset + in.levels[group - 1].size) * F
-            : in.expert_params;
+    if (split && banded) {
+        int64_t blocks = (static_cast<int64_t>(in.experts) * split_floats + 255) / 256;
+        if (blocks > 16384) blocks = 16384;
+        banded_reduce_kernel<<<static_cast<uint32_t>(blocks), 256, 0, s>>>(o);
+    } else if (split) {
+        // the group pass alone split: the expert's first values; every pass split: all levels
+        const int64_t levels_end = static_cast<int64_t>(in.levels[L - 1].offset + in.levels[L - 1].size) * F;
+        const int64_t prefix = group == L || o.splits[L - 1] > 1 ? levels_end : grouped;
         int64_t blocks = (static_cast<int64_t>(in.experts) * prefix + 255) / 256;
         if (blocks > 16384) blocks = 16384;
         split_reduce_kernel<<<static_cast<uint32_t>(blocks), 256, 0, s>>>(o.partial, in.grad,
-                                                                          static_cast<int64_t>(total_params), splits,
+                                                                          static_cast<int64_t>(total_params),
+                                                                          static_cast<int>(max_splits),
                                                                           in.accumulate, o.fused, o.adam,
                                                                           in.expert_params, prefix);
     }

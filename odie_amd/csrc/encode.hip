@@ -47,8 +47,8 @@ struct Tuning {
     int lds_bytes = 65536;
     int xcd_remap = 1;
     int backward_mode = 1;          // 0: LDS + global fp32 atomics, 1: owner computes
-    int row_screen = 0;             // owner: screen hashed slices by row (measured slower)
-    int bucketed = 0;               // owner: fine passes walk per-slice coordinate buckets (measured slower)
+    int banded = 2;                 // owner: fine passes walk y-band lists (0 never, 1 always, 2 when they pay)
+    int split_target = 0;           // owner, banded: coordinate-level visits per work item (0: automatic)
     int packed_lds = 1;             // packed backward: coarse levels accumulated in LDS
     int packed_blocks = 256;        // packed backward with LDS: most blocks (each flushes its partials once)
     int paired_loads = 0;           // forward: 16-byte corner-pair loads (measured no gain)
@@ -586,8 +586,8 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "lds_bytes" && value >= 0 && value <= 160 * 1024) t.lds_bytes = value;
     else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
     else if (key == "backward_mode" && (value == 0 || value == 1)) t.backward_mode = value;
-    else if (key == "row_screen" && (value == 0 || value == 1)) t.row_screen = value;
-    else if (key == "bucketed" && (value == 0 || value == 1)) t.bucketed = value;
+    else if (key == "banded" && value >= 0 && value <= 2) t.banded = value;
+    else if (key == "split_target" && value >= 0) t.split_target = value;
     else if (key == "packed_lds" && (value == 0 || value == 1)) t.packed_lds = value;
     else if (key == "packed_blocks" && value >= 1 && value <= 65536) t.packed_blocks = value;
     else if (key == "paired_loads" && (value == 0 || value == 1)) t.paired_loads = value;
@@ -684,8 +684,8 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
         o.levels = a.level;
         o.lds_bytes = t.owner_lds_bytes;
         o.remap = t.xcd_remap;
-        o.row_screen = t.row_screen;
-        o.bucketed = t.bucketed;
+        o.banded = t.banded;
+        o.split_target = t.split_target;
         o.stream = s;
         return launch_owner_backward(o);
     }
@@ -772,8 +772,8 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
     o.levels = a.level;
     o.lds_bytes = t.owner_lds_bytes;
     o.remap = t.xcd_remap;
-    o.row_screen = t.row_screen;
-    o.bucketed = t.bucketed;
+    o.banded = t.banded;
+    o.split_target = t.split_target;
     o.stream = s;
     o.adam = &adam;
     return launch_owner_backward(o);

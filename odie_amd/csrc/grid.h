@@ -116,8 +116,8 @@ struct OwnerLaunch {
     const DevLevel* levels;   // host array [n_levels]
     int64_t lds_bytes;
     int remap;
-    int row_screen;
-    int bucketed;             // fine passes walk per-slice coordinate buckets
+    int banded;               // fine passes walk y-band lists: 0 never, 1 always, 2 when they pay
+    int64_t split_target;     // banded: coordinate-level visits per work item (0: chosen per launch)
     hipStream_t stream;
     const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad
     const void* planes;       // non-null: upstream already level-major [n_levels][n][features]

@@ -53,14 +53,22 @@ def test_single_grid_forward_bit_exact(dtype):
     assert not mismatch.any(), 'mismatches at %s' % (np.argwhere(mismatch)[:5],)
 
 
-@pytest.fixture(params=[(1, 1), (1, 0), (0, 0)], ids=['owner-buckets', 'owner', 'atomics'])
+@pytest.fixture(params=[(1, 1), (1, 0), (0, 0)], ids=['owner-banded', 'owner', 'atomics'])
 def backward_mode(request):
-    mode, bucketed = request.param
+    mode, banded = request.param
     _lib.set_tuning('backward_mode', mode)
-    _lib.set_tuning('bucketed', bucketed)
+    _lib.set_tuning('banded', banded)
     yield mode
     _lib.set_tuning('backward_mode', 1)
-    _lib.set_tuning('bucketed', 0)
+    _lib.set_tuning('banded', 2)
+
+
+def _tuned(key, value, default, call):
+    _lib.set_tuning(key, value)
+    try:
+        return call()
+    finally:
+        _lib.set_tuning(key, default)
 
 
 @pytest.mark.parametrize('lds_bytes', [0, 65536])
@@ -125,28 +133,67 @@ def test_owner_backward_is_order_independent():
     check_gradient(grads[0], expected, magnitude, 'banded')
 
 
-@pytest.mark.parametrize('log2,experts,n', [(16, 64, 1 << 20), (14, 16, 300000), (12, 3, 5000)])
-def test_bucketed_owner_is_bit_identical(log2, experts, n):
-    """The bucketed fine passes only skip coordinates whose corners miss the slice: with one
-    workgroup per (expert, pass) the gradient is the same integer sum, bit for bit."""
+def _expert_batch(seed, log2, experts, n, outside=False):
     levels, entries = grid_levels(encoding(log2=log2))
-    params = entries * 2
-    counts = np.random.default_rng(log2).multinomial(n, np.ones(experts) / experts)
+    counts = np.random.default_rng(seed).multinomial(n, np.ones(experts) / experts)
     offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).cuda()
-    xy = torch.from_numpy(synth.coordinates(log2, n)).cuda()
-    up = torch.from_numpy(synth.upstream(log2, n, 32)).cuda().half()
-    results = []
-    for bucketed in (1, 0):
-        _lib.set_tuning('bucketed', bucketed)
-        try:
-            results.append(grid_backward(xy, up, levels, 2, offsets=offsets, experts=experts, expert_params=params))
-        finally:
-            _lib.set_tuning('bucketed', 0)
-    got, want = results[0].cpu().numpy(), results[1].cpu().numpy()
-    if experts >= 16:     # no coordinate splits: the same fixed-point scale per workgroup
+    xy = synth.coordinates(seed, n)
+    if outside:   # off the unit square: the band lists' last slot, visited by every slice
+        xy[::97, 0] = 1.5
+        xy[5::101, 1] = -0.25
+        xy[7::211] = (-3.0, 2.5)
+    up = torch.from_numpy(synth.upstream(seed, n, 32)).cuda()
+    return levels, entries * 2, offsets, torch.from_numpy(xy).cuda(), up
+
+
+@pytest.mark.parametrize('log2,experts,n,outside', [(16, 64, 1 << 20, False), (14, 16, 300000, True),
+                                                    (19, 1, 1 << 20, False), (12, 3, 5000, True)])
+def test_banded_owner_matches_unbanded(log2, experts, n, outside):
+    """The banded fine passes skip only coordinates whose corners cannot reach the slice, and
+    every pass bounds its fixed-point scale over the expert's coordinates: where the unbanded
+    owner does not split a pass either (64 experts of 16384 coordinates), the gradient is the
+    same integer sum bit for bit; otherwise both are within fp32 rounding of each other."""
+    levels, params, offsets, xy, up = _expert_batch(log2, log2, experts, n, outside)
+    run = lambda: grid_backward(xy, up.half(), levels, 2, offsets=offsets, experts=experts, expert_params=params)
+    banded = _tuned('banded', 1, 2, run)
+    plain = _tuned('banded', 0, 2, run)
+    got, want = banded.cpu().numpy(), plain.cpu().numpy()
+    if experts == 64:
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     else:
-        assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+        finite = np.isfinite(want)
+        assert np.array_equal(finite, np.isfinite(got))
+        assert np.allclose(got[finite], want[finite], rtol=1e-5, atol=1e-6 * np.abs(want[finite]).max())
+
+
+@pytest.mark.parametrize('log2,experts,n', [(19, 1, 1 << 20), (14, 16, 300000), (12, 3, 5000)])
+def test_banded_splits_are_exact(log2, experts, n):
+    """Banded splits write 64-bit partial sums at one scale per pass and are added exactly: the
+    gradient is the same bit for bit however finely the passes are split."""
+    levels, params, offsets, xy, up = _expert_batch(log2 + 1, log2, experts, n)
+    run = lambda: grid_backward(xy, up.half(), levels, 2, offsets=offsets, experts=experts, expert_params=params)
+    _lib.set_tuning('banded', 1)
+    try:
+        auto = run()
+        fine = _tuned('split_target', 1024, 0, run)
+        whole = _tuned('split_target', 1 << 30, 0, run)
+    finally:
+        _lib.set_tuning('banded', 2)
+    assert torch.equal(auto, fine) and torch.equal(auto, whole)
+
+
+def test_banded_owner_with_unordered_offsets():
+    """Offsets that decrease somewhere make the expert ranges overlap: the band lists are not
+    used and the fine passes walk the experts' index ranges, as the unbanded owner does."""
+    levels, entries = grid_levels(encoding(log2=14))
+    experts, n = 16, 40000
+    bounds = np.linspace(0, n, experts + 1).astype(np.int32)
+    bounds[5], bounds[6] = bounds[6], bounds[5]
+    offsets = torch.from_numpy(bounds).cuda()
+    xy = torch.from_numpy(synth.coordinates(41, n)).cuda()
+    up = torch.from_numpy(synth.upstream(41, n, 32)).cuda()
+    run = lambda: grid_backward(xy, up, levels, 2, offsets=offsets, experts=experts, expert_params=entries * 2)
+    assert torch.equal(_tuned('banded', 1, 2, run), _tuned('banded', 0, 2, run))
 
 
 def test_experts_forward_and_backward(backward_mode):
