@@ -109,8 +109,10 @@ int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t
  * "banded" (the owner's fine passes walk y-band lists of the coordinates: 0 never, 1 always,
  * 2 (default) when the lists cut the estimated visits at least four times),
  * "split_target" (banded: coordinate-level visits per owner work item, 0 = automatic),
- * "owner_lds_bytes", "paired_loads", "forward_lds_bytes".  Results do not depend on them beyond
- * fp32 summation order and the owner's fixed-point scale. */
+ * "owner_lds_bytes", "paired_loads", "forward_lds_bytes", "packed_owner" (1: the packed-plane
+ * backward computes each slice of the gradient in one workgroup, 0 (default): global atomics),
+ * "packed_splits" (0 = automatic).  Results do not depend on them beyond fp32 summation order
+ * and the owner's fixed-point scale. */
 int odie_set_tuning(const char* key, int value);
 
 /* ---------------------------------------------------------------------------------------
@@ -125,6 +127,11 @@ int odie_packed_forward(const float* coords, int64_t n, const float* grid, int64
                         const int32_t* node_prefix, const uint8_t* bitmap, int width,
                         uint16_t* features, uint8_t* visibility, uint64_t stream);
 
+/* gradient (fp32 [parameter_count]) is written whole, not accumulated, with fp32 atomics as
+ * the reference does (summation order free).  With the tuning key "packed_owner" = 1 each slice
+ * of it is summed by one workgroup in 64-bit fixed point instead: deterministic, each
+ * contribution the fp32 product w * u rounded to 2^-30 of the largest |u| of its levels; the
+ * plane offsets must then ascend with the level (the layout's order). */
 int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
                          const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
                          const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,

@@ -323,16 +323,23 @@ __device__ inline void contribute(float x, float y, const float* us, const DevLe
     for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int c = 0; c < F; ++c) q[k][c] = round_to_int(w[k] * us[c]);
-    const uint32_t shift = lv.offset * F - lo;
+    // feature-planar slice (feature c of entry e at c * entries + e): the 64-bit adds of one
+    // instruction spread over every bank pair, where entry-major order would use every fourth
+    const uint32_t entries = span / F;
+    const uint32_t shift = lv.offset - lo / F;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t slot = idx[k] * F + shift;
-        if (slot >= span) continue;
+        const uint32_t entry = idx[k] + shift;
+        if (entry >= entries) continue;
 #pragma unroll
         for (int c = 0; c < F; ++c)
-            atomicAdd(acc + slot + c, static_cast<unsigned long long>(static_cast<long long>(q[k][c])));
+            atomicAdd(acc + c * entries + entry, static_cast<unsigned long long>(static_cast<long long>(q[k][c])));
     }
 }
+
+// LDS accumulator of value j (entry j / F, feature j % F) of a slice of `span` values.
+template <int F>
+__device__ inline uint32_t planar(uint32_t j, uint32_t span) { return (j % F) * (span / F) + j / F; }
 
 template <int F, bool HALF>
 __device__ inline void load_upstream(const Elem<HALF>* plane, int64_t at, float scale, bool valid, float* us) {
@@ -875,7 +882,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     if (splits > 1 && a.banded) {
         // raw 64-bit sums: banded_reduce_kernel adds the splits exactly and applies the scale
         long long* out = a.partial64 + (static_cast<int64_t>(s) * a.experts + e) * a.partial_floats + lo;
-        for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[j]);
+        for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[planar<F>(j, span)]);
         if (s == 0 && threadIdx.x == 0) a.shifts[static_cast<int64_t>(e) * a.passes + p] = finite ? shift : kNonFinite;
         return;
     }
@@ -897,7 +904,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                 m[k] = o.m[i];
                 v[k] = o.v[i];
                 age[k] = o.variant != 0 ? o.steps[i] : 0u;
-                g[k] = static_cast<float>(static_cast<double>(static_cast<long long>(acc[j < span ? j : 0])) * unscale);
+                g[k] = static_cast<float>(static_cast<double>(static_cast<long long>(acc[planar<F>(j < span ? j : 0, span)])) * unscale);
                 if (!finite) g[k] = __builtin_nanf("");
             }
 #pragma unroll
@@ -920,7 +927,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                                : a.partial + static_cast<size_t>(s) * a.experts * a.expert_params +
                                      static_cast<size_t>(e) * a.expert_params + lo;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) {
-        float v = static_cast<float>(static_cast<double>(static_cast<long long>(acc[j])) * unscale);
+        float v = static_cast<float>(static_cast<double>(static_cast<long long>(acc[planar<F>(j, span)])) * unscale);
         if (!finite) v = __builtin_nanf("");
         if (splits == 1 && a.accumulate) v += out[j];
         out[j] = v;
@@ -986,6 +993,199 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial,
             adam_update(adam, x, v);
         else
             grad[x] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Owner-computes backward of packed xy planes (the reference's grid_back,
+// odie/native/runtime.cu:111-137, without atomics).  Workgroup b owns the parameters
+// [b*cap, (b+1)*cap) -- whole levels or a part of one, in plane-offset order -- and walks the
+// coordinates (a share of them when split) through every level whose parameters meet its
+// slice, adding w_k * u (the fp32 product) as 64-bit fixed point in LDS.  One scale per slice
+// from the largest |u| over its levels' columns; split slices write their raw sums and
+// packed_reduce_kernel adds them exactly, so the gradient is the same however it is split.
+// ---------------------------------------------------------------------------------------
+struct PackedOwnerArgs {
+    const float* coords;
+    const uint16_t* upstream;     // fp16 [n][width]
+    const int32_t* desc;
+    const uint64_t* node_bitmap;
+    const int32_t* prefix;
+    const uint8_t* bitmap;
+    const uint32_t* bounds;       // [levels]: largest fp16 magnitude (bits) of each level's columns
+    float* gradient;
+    long long* partial;           // [splits][params] when splits > 1
+    int32_t* shifts;              // [slices] when splits > 1
+    int64_t n;
+    int64_t params;
+    int levels;
+    int width;
+    int cap;                      // values per slice
+    int splits;
+};
+
+// Largest |u| of every level's upstream columns, as fp16 magnitude bits (their unsigned order
+// is the magnitude order, NaN above infinity).  bounds must be zero on entry.
+__global__ __launch_bounds__(256) void packed_bound_kernel(PackedOwnerArgs a, uint32_t* bounds) {
+    __shared__ uint32_t peak[ODIE_MAX_LEVELS];
+    if (threadIdx.x < ODIE_MAX_LEVELS) peak[threadIdx.x] = 0u;
+    __syncthreads();
+    for (int l = 0; l < a.levels; ++l) {
+        const int32_t* d = a.desc + 8 * l;
+        uint32_t mine = 0u;
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.n;
+             i += static_cast<int64_t>(gridDim.x) * 256) {
+            const uint16_t* row = a.upstream + static_cast<size_t>(i) * a.width;
+            for (int c = 0; c < d[5]; ++c) {
+                const int col = d[6] + c;
+                if (col < a.width) {
+                    const uint32_t m = row[col] & 0x7fffu;
+                    mine = m > mine ? m : mine;
+                }
+            }
+        }
+        if (mine) atomicMax(peak + l, mine);
+    }
+    __syncthreads();
+    if (threadIdx.x < a.levels && peak[threadIdx.x]) atomicMax(bounds + threadIdx.x, peak[threadIdx.x]);
+}
+
+__device__ inline int64_t level_end(const PackedOwnerArgs& a, int l) {
+    return l + 1 < a.levels ? static_cast<int64_t>(a.desc[8 * (l + 1) + 2]) : a.params;
+}
+
+// Coordinates [b0, b1) against one level of F features (1, 2 or 4; direct or ranked rows):
+// every stage issues the loads of all kPackedBatch coordinates of a thread before using any of them
+// (positions, cell bits, upstream values, the rank words of the four corners).
+constexpr int kPackedBatch = 2;   // coordinates per thread per iteration (fits 128 VGPRs with F = 4)
+
+template <int F, bool DIRECT>
+__device__ inline void packed_level(const PackedOwnerArgs& a, const int32_t* d, int64_t b0, int64_t b1, int64_t lo,
+                                    int64_t hi, float scale, unsigned long long* acc) {
+    const int r = d[0], points = d[1], column = d[6];
+    const int64_t first = d[2];
+    for (int64_t i0 = b0 + threadIdx.x; i0 < b1; i0 += kPackedBatch * kOwnerBlock) {
+        float2 xy[kPackedBatch];
+#pragma unroll
+        for (int b = 0; b < kPackedBatch; ++b) {
+            const int64_t i = i0 + b * kOwnerBlock;
+            xy[b] = reinterpret_cast<const float2*>(a.coords)[i < b1 ? i : b0];
+        }
+        int cell[kPackedBatch];
+        float w[kPackedBatch][4];
+        uint8_t bits[kPackedBatch];
+        float us[kPackedBatch][F];
+#pragma unroll
+        for (int b = 0; b < kPackedBatch; ++b) {
+            plane_geometry(xy[b].x, xy[b].y, r, cell[b], w[b]);
+            bits[b] = a.bitmap[d[4] + (cell[b] >> 3)];
+            const int64_t i = i0 + b * kOwnerBlock;
+            const uint16_t* row = a.upstream + static_cast<size_t>(i < b1 ? i : b0) * a.width;
+#pragma unroll
+            for (int c = 0; c < F; ++c)
+                us[b][c] = column + c < a.width ? __half2float(bits_to_half(row[column + c])) * scale : 0.0f;
+        }
+        int node[kPackedBatch][4];
+        int32_t base[kPackedBatch][4];
+        uint64_t word[kPackedBatch][4];
+#pragma unroll
+        for (int b = 0; b < kPackedBatch; ++b)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                node[b][k] = (cell[b] + (k & 1) + (k >> 1) * r) % points;
+                if constexpr (!DIRECT) {
+                    const int at = d[3] + (node[b][k] >> 6);
+                    base[b][k] = a.prefix[at];
+                    word[b][k] = a.node_bitmap[at];
+                }
+            }
+#pragma unroll
+        for (int b = 0; b < kPackedBatch; ++b) {
+            const bool on = i0 + b * kOwnerBlock < b1 && ((bits[b] >> (cell[b] & 7)) & 1);
+            if (!on) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                int rank = node[b][k];
+                if constexpr (!DIRECT)
+                    rank = base[b][k] + __popcll(word[b][k] & ((uint64_t{1} << (node[b][k] & 63)) - uint64_t{1}));
+#pragma unroll
+                for (int c = 0; c < F; ++c) {
+                    int64_t p = first + static_cast<int64_t>(rank) * F + c;
+                    p = p < 0 ? 0 : (p >= a.params ? a.params - 1 : p);
+                    const int32_t q = round_to_int(w[b][k] * us[b][c]);
+                    if (p >= lo && p < hi)
+                        atomicAdd(acc + (p - lo), static_cast<unsigned long long>(static_cast<long long>(q)));
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kOwnerBlock) void packed_owner_kernel(PackedOwnerArgs a) {
+    extern __shared__ unsigned long long acc[];
+    const int slice = blockIdx.x / a.splits, s = blockIdx.x % a.splits;
+    const int64_t lo = static_cast<int64_t>(slice) * a.cap;
+    const int64_t hi = lo + a.cap < a.params ? lo + a.cap : a.params;
+    const uint32_t span = static_cast<uint32_t>(hi - lo);
+    // scale from the largest |u| of the levels that meet the slice
+    float peak = 0.0f;
+    for (int l = 0; l < a.levels; ++l) {
+        if (level_end(a, l) <= lo || a.desc[8 * l + 2] >= hi) continue;
+        const float m = __half2float(bits_to_half(static_cast<uint16_t>(a.bounds[l])));
+        peak = (m > peak || m != m) ? m : peak;
+    }
+    const double limit = 4.0 * static_cast<double>(a.n) * static_cast<double>(peak);
+    int shift = 60;
+    if (peak > 0.0f && limit <= 1.0e300) {
+        const int by_value = 30 - ilogb(peak);
+        const int by_sum = 61 - ilogb(limit);
+        shift = by_value < by_sum ? by_value : by_sum;
+    }
+    if (shift > 120) shift = 120;
+    const float scale = ldexpf(1.0f, shift);
+    const bool finite = !(peak != peak) && peak <= 3.0e38f;
+    for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) acc[j] = 0ull;
+    __syncthreads();
+    const int64_t share = (a.n + a.splits - 1) / a.splits;
+    const int64_t b0 = share * s < a.n ? share * s : a.n;
+    const int64_t b1 = b0 + share < a.n ? b0 + share : a.n;
+    for (int l = 0; l < a.levels; ++l) {
+        if (level_end(a, l) <= lo || a.desc[8 * l + 2] >= hi) continue;
+        const int32_t* d = a.desc + 8 * l;
+        const bool direct = d[7] != 0;
+        switch (d[5]) {
+            case 1: direct ? packed_level<1, true>(a, d, b0, b1, lo, hi, scale, acc)
+                           : packed_level<1, false>(a, d, b0, b1, lo, hi, scale, acc); break;
+            case 2: direct ? packed_level<2, true>(a, d, b0, b1, lo, hi, scale, acc)
+                           : packed_level<2, false>(a, d, b0, b1, lo, hi, scale, acc); break;
+            default: direct ? packed_level<4, true>(a, d, b0, b1, lo, hi, scale, acc)
+                            : packed_level<4, false>(a, d, b0, b1, lo, hi, scale, acc); break;
+        }
+    }
+    __syncthreads();
+    if (a.splits > 1) {
+        long long* out = a.partial + static_cast<int64_t>(s) * a.params + lo;
+        for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[j]);
+        if (s == 0 && threadIdx.x == 0) a.shifts[slice] = finite ? shift : kNonFinite;
+        return;
+    }
+    const double unscale = ldexp(1.0, -shift);
+    for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) {
+        float v = static_cast<float>(static_cast<double>(static_cast<long long>(acc[j])) * unscale);
+        if (!finite) v = __builtin_nanf("");
+        a.gradient[lo + j] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void packed_reduce_kernel(PackedOwnerArgs a) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t x = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; x < a.params; x += stride) {
+        long long sum = 0;
+        for (int s = 0; s < a.splits; ++s) sum += a.partial[static_cast<int64_t>(s) * a.params + x];
+        const int32_t shift = a.shifts[x / a.cap];
+        float v = static_cast<float>(static_cast<double>(sum) * ldexp(1.0, -shift));
+        if (shift == kNonFinite) v = __builtin_nanf("");
+        a.gradient[x] = v;
     }
 }
 
@@ -1290,6 +1490,61 @@ int launch_owner_backward(const OwnerLaunch& in) {
                                                                           in.expert_params, prefix);
     }
     return check_launch("odie_grid_backward");
+}
+
+int launch_packed_owner(const float* coords, int64_t n, const uint16_t* upstream, int width, const int32_t* desc,
+                        int levels, const uint64_t* node_bitmap, const int32_t* node_prefix, const uint8_t* bitmap,
+                        float* gradient, int64_t params, int64_t lds_bytes, int64_t splits, hipStream_t stream) {
+    const int64_t cap = lds_bytes / 8;
+    if (cap < 1024) return fail("odie_packed_backward: LDS budget too small for the owner backward");
+    const int64_t slices = (params + cap - 1) / cap;
+    if (slices > (int64_t{1} << 24)) return fail("odie_packed_backward: too many parameters");
+    // Split the coordinates when the slices alone leave CUs idle: about kCus workgroups, each
+    // walking at least 4096 coordinates (splits > 0: that many).
+    if (splits <= 0) {
+        splits = (kCus + slices - 1) / slices;
+        const int64_t most = n / 4096 > 1 ? n / 4096 : 1;
+        if (splits > most) splits = most;
+        if (splits > 64) splits = 64;
+    }
+    if (splits < 1) splits = 1;
+    const auto align = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+    const size_t bound_bytes = align(static_cast<size_t>(ODIE_MAX_LEVELS) * 4);
+    const size_t partial_bytes = splits > 1 ? align(static_cast<size_t>(splits) * params * 8) : 0;
+    const size_t shift_bytes = splits > 1 ? align(static_cast<size_t>(slices) * 4) : 0;
+    char* space = static_cast<char*>(workspace(bound_bytes + partial_bytes + shift_bytes, stream));
+    if (!space) return -1;
+    PackedOwnerArgs a{};
+    a.coords = coords;
+    a.upstream = upstream;
+    a.desc = desc;
+    a.node_bitmap = node_bitmap;
+    a.prefix = node_prefix;
+    a.bitmap = bitmap;
+    a.bounds = reinterpret_cast<const uint32_t*>(space);
+    a.gradient = gradient;
+    a.partial = reinterpret_cast<long long*>(space + bound_bytes);
+    a.shifts = reinterpret_cast<int32_t*>(space + bound_bytes + partial_bytes);
+    a.n = n;
+    a.params = params;
+    a.levels = levels;
+    a.width = width;
+    a.cap = static_cast<int>(cap);
+    a.splits = static_cast<int>(splits);
+    uint32_t* bounds = reinterpret_cast<uint32_t*>(space);
+    if (launch_fill_zero(reinterpret_cast<float*>(bounds), ODIE_MAX_LEVELS, stream)) return -1;
+    int64_t bound_blocks = (n + 255) / 256;
+    if (bound_blocks > 1024) bound_blocks = 1024;
+    packed_bound_kernel<<<static_cast<uint32_t>(bound_blocks), 256, 0, stream>>>(a, bounds);
+    const size_t shmem = static_cast<size_t>(cap) * 8;
+    if (allow_lds(packed_owner_kernel, shmem)) return -1;
+    packed_owner_kernel<<<static_cast<uint32_t>(slices * splits), kOwnerBlock, shmem, stream>>>(a);
+    if (splits > 1) {
+        int64_t blocks = (params + 255) / 256;
+        if (blocks > 16384) blocks = 16384;
+        packed_reduce_kernel<<<static_cast<uint32_t>(blocks), 256, 0, stream>>>(a);
+    }
+    return check_launch("odie_packed_backward");
 }
 
 }  // namespace odie

@@ -73,6 +73,47 @@ __device__ inline uint32_t half2_level(const uint32_t g[4], const float w[4]) {
 template <bool HALF>
 using Elem = typename std::conditional<HALF, __half, float>::type;
 
+// Packed xy planes (odie/packed_kernels.cu:12-88 semantics).  Descriptor row d of a level:
+// d[0] resolution R, d[1] points, d[2] plane offset, d[3] node word offset, d[4] cell bitmap
+// byte offset, d[5] features, d[6] feature offset, d[7] direct (1: row = node).
+//
+// Geometry at integer resolution R: p = fma(R-1, x, 0.5), cell = floor(px) + floor(py)*R.
+// The cell's integer corner is clamped into the plane so that any input addresses memory
+// inside the layout; for x, y in [0,1] the clamp never changes the corner.
+__device__ inline void plane_geometry(float x, float y, int r, int& cell, float w[4]) {
+    const float px = __builtin_fmaf(static_cast<float>(r - 1), x, 0.5f);
+    const float py = __builtin_fmaf(static_cast<float>(r - 1), y, 0.5f);
+    int ix = static_cast<int>(floorf(px)), iy = static_cast<int>(floorf(py));
+    const float fx = px - static_cast<float>(ix), fy = py - static_cast<float>(iy);
+    ix = ix < 0 ? 0 : (ix > r - 1 ? r - 1 : ix);
+    iy = iy < 0 ? 0 : (iy > r - 1 ? r - 1 : iy);
+    cell = ix + iy * r;
+    w[0] = (1.0f - fx) * (1.0f - fy);
+    w[1] = fx * (1.0f - fy);
+    w[2] = (1.0f - fx) * fy;
+    w[3] = fx * fy;
+}
+
+// Parameter of feature c of corner k of `cell`: node (cell + k%2 + (k/2) R) mod points, its row
+// (the node itself, or its rank among the stored nodes: word prefix + popcount below it),
+// plane offset + row * features + c, clamped into the parameters.
+__device__ inline int64_t packed_param(const int32_t* d, const uint64_t* node_bitmap, const int32_t* prefix,
+                                       int64_t params, int cell, int k, int c) {
+    const int node = (cell + (k & 1) + (k >> 1) * d[0]) % d[1];
+    int row = node;
+    if (!d[7]) {
+        const int word = d[3] + (node >> 6), bit = node & 63;
+        const uint64_t mask = (uint64_t{1} << bit) - uint64_t{1};
+        row = prefix[word] + __popcll(node_bitmap[word] & mask);
+    }
+    int64_t p = static_cast<int64_t>(d[2]) + static_cast<int64_t>(row) * d[5] + c;
+    return p < 0 ? 0 : (p >= params ? params - 1 : p);
+}
+
+__device__ inline bool cell_visible(const int32_t* d, const uint8_t* bitmap, int cell) {
+    return (bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1;
+}
+
 // Host: device rows of an odie_grid_level table (levels contiguous from entry 0); entries
 // receives the table's entry count.  Returns 0, or -1 with the error set.
 inline int make_dev_levels(const char* what, const odie_grid_level* levels, int n_levels, DevLevel* out,
@@ -124,6 +165,12 @@ struct OwnerLaunch {
     const float* blockmax;    // with planes: max |upstream| per 128-row record and level
 };
 int launch_owner_backward(const OwnerLaunch& launch);
+
+// Owner-computes backward of packed xy planes (backward.hip): gradient [params] fp32, every
+// value written once.  upstream fp16 [n][width]; descriptors device [levels][8].
+int launch_packed_owner(const float* coords, int64_t n, const uint16_t* upstream, int width, const int32_t* desc,
+                        int levels, const uint64_t* node_bitmap, const int32_t* node_prefix, const uint8_t* bitmap,
+                        float* gradient, int64_t params, int64_t lds_bytes, int64_t splits, hipStream_t stream);
 
 // odie_grid_backward_adam with the optimizer step already formed (adam.h), so that callers
 // can set fields the C ABI does not expose (the fp16 gradient store).

@@ -285,19 +285,67 @@ def test_grid_encoding_module_autograd():
     check_gradient(module.params.grad, expected, magnitude, 'autograd')
 
 
-def _packed_layout(seed):
+def _packed_layout(seed, resolutions=(8, 13, 20, 32, 51, 81), dims=(2, 2, 2, 2, 1, 4), dense=3):
     from odie_amd.model import make_layout, plane_closure
     rng = np.random.default_rng(seed)
-    resolutions = [8, 13, 20, 32, 51, 81]
     supports, caps = [], []
     for level, r in enumerate(resolutions):
-        support = np.ones(r * r, dtype=bool) if level < 3 else rng.random(r * r) < 0.3
+        support = np.ones(r * r, dtype=bool) if level < dense else rng.random(r * r) < 0.3
         nodes = plane_closure(torch.as_tensor(support), r)
         supports.append(torch.as_tensor(support))
         caps.append(min((r * r + 7) // 8 * 8, (nodes.numel() + 7) // 8 * 8 + 8 * level))
-    config = dict(resolutions=resolutions, n_levels=6, representation='xy_planes', coarse_levels=0,
-                  gate_topology='shared', gate_position='feature', initial_active_prefix=3)
-    return make_layout(config, supports, [2, 2, 2, 2, 1, 4], caps)
+    config = dict(resolutions=list(resolutions), n_levels=len(resolutions), representation='xy_planes',
+                  coarse_levels=0, gate_topology='shared', gate_position='feature', initial_active_prefix=3)
+    return make_layout(config, supports, list(dims), caps)
+
+
+def _packed_gradient(layout, xy, up, **tuning):
+    from odie_amd.model import packed_backward
+    dev = {k: layout[k].cuda() for k in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap')}
+    settings = dict(dict(packed_owner=1), **tuning)
+    for key, value in settings.items():
+        _lib.set_tuning(key, value)
+    try:
+        return packed_backward(xy, up, dev['descriptors'], dev['node_bitmap'], dev['node_prefix'], dev['bitmap'],
+                               layout['params'])
+    finally:
+        _lib.set_tuning('packed_owner', 0)
+        _lib.set_tuning('packed_splits', 0)
+
+
+# Nine levels of 8..512 cells (the finer ones 30% supported), mixed F1/F2/F4: about 1.4e6
+# parameters, so the owner's slices span several levels at the coarse end and split the fine ones.
+BIG_PLANES = dict(resolutions=(8, 13, 20, 32, 64, 128, 256, 384, 512), dims=(2, 2, 2, 2, 4, 2, 2, 1, 2), dense=5)
+
+
+def test_packed_owner_matches_oracle_and_atomics():
+    """The owner-computes packed backward against the oracle (multi-slice layout, off-square and
+    edge coordinates) and against the global-atomics kernel it replaces (fp32 order only)."""
+    layout = _packed_layout(4, **BIG_PLANES)
+    n, width = 30000, 32
+    xy = synth.coordinates(17, n)
+    xy[:4] = [(0, 0), (1, 1), (0, 1), (1, 0)]
+    up = synth.upstream(17, n, width)
+    d_xy, d_up = torch.from_numpy(xy).cuda(), torch.from_numpy(up).cuda()
+    owner = _packed_gradient(layout, d_xy, d_up)
+    atomics = _packed_gradient(layout, d_xy, d_up, packed_owner=0)
+    host = {k: layout[k].numpy() for k in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap')}
+    expected, magnitude = oracle.packed_backward(xy, up, host, layout['params'])
+    check_gradient(owner, expected, magnitude, 'packed owner')
+    check_gradient(atomics, expected, magnitude, 'packed atomics')
+
+
+@pytest.mark.parametrize('seed,n', [(5, 30000), (6, 4097), (7, 1)])
+def test_packed_owner_splits_are_exact(seed, n):
+    """Splits share one fixed-point scale per slice and sum 64-bit partials: the gradient is the
+    same bit for bit for any split count, and from run to run."""
+    layout = _packed_layout(seed, **BIG_PLANES)
+    d_xy = torch.from_numpy(synth.coordinates(seed, n)).cuda()
+    d_up = torch.from_numpy(synth.upstream(seed, n, 32)).cuda()
+    first = _packed_gradient(layout, d_xy, d_up)
+    for splits in (1, 3, 7):
+        assert torch.equal(first, _packed_gradient(layout, d_xy, d_up, packed_splits=splits)), splits
+    assert torch.equal(first, _packed_gradient(layout, d_xy, d_up))
 
 
 def test_packed_planes_forward_backward():
