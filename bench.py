@@ -392,25 +392,27 @@ def gigapixel_steps(steps):
     parameters + 7168 decoder parameters, 31 MiB in fp16, under the 50 MiB budget), 2^24 pixel
     ids per step; the same step as the headline.  Measured on stratified batches (one pixel per
     8x8 stratum, strata row by row: the reference's gigapixel configurations draw them so), then
-    on ids uniform over the image.  Reported beside the headline, not as it."""
+    on ids uniform over the image.  The stratified draw is fused into the route
+    (odie_route_stratified: torch.rand's uniforms in, the ids never written).  Reported beside
+    the headline, not as it."""
     import torch
     from odie_amd import synth
-    from odie_amd.sampling import stratified_batches
     from odie_amd.trainer import ExpertTrainer
     side, n = C5_SIDE, 1 << 24
     image = synth.image_device(1, side, side)
     trainer = ExpertTrainer(image, C5_ENCODING, C5_TILES, C5_TILES, n, grid_lr=1e-2, decoder_lr=1e-3, seed=1)
-    draw = stratified_batches((side, side), n, torch.Generator(device='cuda').manual_seed(1))
+    generator = torch.Generator(device='cuda').manual_seed(1)
     out = {'coords': n, 'experts': trainer.grid.experts, 'params': trainer.grid.table.numel(), 'steps': steps}
-    for name, batches in (('stratified', [next(draw) for _ in range(2)]),
-                          ('uniform_ids', [torch.from_numpy(synth.integers(k, 'gigapixel_ids', n, side * side)).cuda()
-                                           for k in range(2)])):
-        trainer.step(batches[0])
+    stratified = [torch.rand((n, 2), device='cuda', generator=generator) for _ in range(2)]
+    uniform = [torch.from_numpy(synth.integers(k, 'gigapixel_ids', n, side * side)).cuda() for k in range(2)]
+    for name, batches, step in (('stratified', stratified, lambda b: trainer.step(None, uniforms=b)),
+                                ('uniform_ids', uniform, trainer.step)):
+        step(batches[0])
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for k in range(steps):
-            trainer.step(batches[k % 2])
+            step(batches[k % 2])
         stop.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(stop) / steps

@@ -166,6 +166,14 @@ int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions
                int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
                uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream);
 
+/* odie_route on a stratified draw, with the draw fused in (odie/data.py:63-80, the id of slot i
+ * as odie_stratified_ids computes it): uniforms fp32 [n][2] (torch.rand's draws) in place of
+ * ids, n a square power of two.  The ids are never written; perm[j] is the stratified slot
+ * placed at slot j.  Same outputs, bit for bit, as odie_route on odie_stratified_ids' ids. */
+int odie_route_stratified(const float* uniforms, int64_t n, int width, int height, int regions_x, int regions_y,
+                          int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
+                          uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream);
+
 /* odie_route without the workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  It allocates nothing: its scratch is a static device array of

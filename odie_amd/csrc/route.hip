@@ -22,6 +22,7 @@
 #include <string>
 
 #include "common.h"
+#include "sampling.h"
 #include "tiles.h"
 #include "../../include/odie_amd.h"
 
@@ -35,6 +36,9 @@ constexpr int kMaxExperts = kMaxRegions * kMaxRegions;
 
 struct RouteArgs {
     const int64_t* ids;
+    const float* uniforms;  // in place of ids: slot i is the pixel of stratified slot i (side x side strata)
+    int side;
+    float inv_side;
     int32_t* expert_out;
     int32_t* perm;
     float* coords;
@@ -65,7 +69,10 @@ struct Bounds {
 
 __device__ inline void locate(const RouteArgs& a, const Bounds& b, int64_t i, int& expert, uint32_t& x, uint32_t& y,
                               int& rx, int& ry) {
-    const uint32_t id = static_cast<uint32_t>(a.ids[i]);
+    const uint32_t id = static_cast<uint32_t>(
+        a.uniforms ? stratified_id(reinterpret_cast<const float2*>(a.uniforms)[i], i, a.side, a.inv_side,
+                                   static_cast<int>(a.width), static_cast<int>(a.height))
+                   : a.ids[i]);
     x = id % a.width;
     y = id / a.width;
     if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
@@ -402,7 +409,7 @@ namespace odie {
 namespace {
 
 // Checks the arguments common to odie_route and odie_route_noalloc (nothing is queued).
-int route_check(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y, int32_t* perm,
+int route_check(const void* ids, int64_t n, int width, int height, int regions_x, int regions_y, int32_t* perm,
                 float* coords, int32_t* offsets, const uint8_t* rgb, uint32_t* colors) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_route: n must be within [0, 2^31-1]");
     if (regions_x < 1 || regions_y < 1 || regions_x > kMaxRegions || regions_y > kMaxRegions)
@@ -422,10 +429,13 @@ int route_check(const int64_t* ids, int64_t n, int width, int height, int region
 // the caller) as its scratch.
 int route_launch(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
                  int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
-                 uint32_t* colors, void* workspace, uint64_t stream) {
+                 uint32_t* colors, void* workspace, uint64_t stream, const float* uniforms = nullptr, int side = 0) {
     const int experts = regions_x * regions_y;
     RouteArgs a{};
     a.ids = ids;
+    a.uniforms = uniforms;
+    a.side = side;
+    a.inv_side = side > 0 ? 1.0f / static_cast<float>(side) : 0.0f;
     a.expert_out = expert;
     a.perm = perm;
     a.coords = coords;
@@ -522,6 +532,22 @@ ODIE_API int odie_route(const int64_t* ids, int64_t n, int width, int height, in
         return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
     return route_launch(ids, n, width, height, regions_x, regions_y, expert, perm, coords, offsets, rgb, colors,
                         workspace, stream);
+}
+
+ODIE_API int odie_route_stratified(const float* uniforms, int64_t n, int width, int height, int regions_x,
+                                   int regions_y, int32_t* expert, int32_t* perm, float* coords, int32_t* offsets,
+                                   const uint8_t* rgb, uint32_t* colors, void* workspace, int64_t workspace_bytes,
+                                   uint64_t stream) {
+    if (route_check(uniforms, n, width, height, regions_x, regions_y, perm, coords, offsets, rgb, colors)) return -1;
+    int side = 1;
+    while (static_cast<int64_t>(side) * side < n) side *= 2;
+    if (n < 1 || static_cast<int64_t>(side) * side != n)
+        return fail("Stratified sampling requires a square power-of-two batch size");
+    if (reinterpret_cast<uintptr_t>(uniforms) % 8) return fail("odie_route_stratified: uniforms must be 8-byte aligned");
+    if (!workspace || workspace_bytes < odie_route_workspace(n, regions_x * regions_y))
+        return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
+    return route_launch(nullptr, n, width, height, regions_x, regions_y, expert, perm, coords, offsets, rgb, colors,
+                        workspace, stream, uniforms, side);
 }
 
 ODIE_API int odie_route_noalloc(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,

@@ -4,6 +4,7 @@
 // are exact), pixel = trunc(uv * (W, H)) clamped to the image, id = y * W + x -- the reference's
 // torch expression, evaluated per slot.
 #include "common.h"
+#include "sampling.h"
 #include "../../include/odie_amd.h"
 
 namespace odie {
@@ -13,15 +14,7 @@ __global__ __launch_bounds__(256) void stratified_kernel(const float* uniforms, 
                                                          int width, int height, int64_t* ids) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= batch) return;
-    const float2 u = reinterpret_cast<const float2*>(uniforms)[j];
-    const float sx = static_cast<float>(j % side) * inv_side, sy = static_cast<float>(j / side) * inv_side;
-    const float ux = u.x * inv_side + sx, uy = u.y * inv_side + sy;
-    const float fx = ux * static_cast<float>(width), fy = uy * static_cast<float>(height);
-    // .long() truncates toward zero; the clamps follow (odie/data.py:79-80)
-    int64_t x = static_cast<int64_t>(fx), y = static_cast<int64_t>(fy);
-    x = x < 0 ? 0 : (x > width - 1 ? width - 1 : x);
-    y = y < 0 ? 0 : (y > height - 1 ? height - 1 : y);
-    ids[j] = y * width + x;
+    ids[j] = stratified_id(reinterpret_cast<const float2*>(uniforms)[j], j, side, inv_side, width, height);
 }
 
 }  // namespace

@@ -26,13 +26,25 @@ class Routing:
         self.colors = colors
 
 
-def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None, rgb=None):
+def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None, rgb=None,
+          uniforms=None):
     """Route int64 pixel ids [N] (CUDA) to regions_x*regions_y tile experts and compact.  With
-    rgb (CUDA uint8 [H*W*3]) each slot also receives its pixel's packed colour."""
-    if ids.dtype != torch.int64 or ids.ndim != 1 or not ids.is_cuda:
-        raise ValueError('ids must be a CUDA int64 [N] tensor')
-    ids = ids.contiguous()
-    n, experts = ids.numel(), regions_x * regions_y
+    rgb (CUDA uint8 [H*W*3]) each slot also receives its pixel's packed colour.  With
+    uniforms (CUDA fp32 [N, 2], N a square power of two) and ids None, the ids are those of
+    the stratified draw on those uniforms (odie_stratified_ids), computed inside the route."""
+    if uniforms is not None:
+        if ids is not None:
+            raise ValueError('give ids or uniforms, not both')
+        if uniforms.dtype != torch.float32 or uniforms.ndim != 2 or uniforms.shape[1] != 2 or not uniforms.is_cuda:
+            raise ValueError('uniforms must be a CUDA fp32 [N, 2] tensor')
+        ids = uniforms.contiguous()
+        entry = 'odie_route_stratified'
+    else:
+        if ids is None or ids.dtype != torch.int64 or ids.ndim != 1 or not ids.is_cuda:
+            raise ValueError('ids must be a CUDA int64 [N] tensor')
+        ids = ids.contiguous()
+        entry = 'odie_route'
+    n, experts = ids.shape[0], regions_x * regions_y
     lib = _lib.library()
     need = lib.odie_route_workspace(n, experts)
     if need < 0:
@@ -46,7 +58,7 @@ def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=No
                       torch.empty(n, dtype=torch.int32, device=device) if rgb is not None else None)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
-    _lib.check(lib.odie_route(ids.data_ptr(), n, width, height, regions_x, regions_y, _lib.ptr(out.expert),
+    _lib.check(getattr(lib, entry)(ids.data_ptr(), n, width, height, regions_x, regions_y, _lib.ptr(out.expert),
                               out.perm.data_ptr(), out.coords.data_ptr(), out.offsets.data_ptr(),
                               _lib.ptr(rgb), _lib.ptr(out.colors if rgb is not None else None), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
                               _lib.stream_of(ids)))

@@ -89,17 +89,20 @@ class ExpertTrainer:
         if self.grid.width != 32:
             raise ValueError('the decoder takes 32 input features (16 levels x 2)')
 
-    def step(self, ids, update=True, mark=None):
+    def step(self, ids, update=True, mark=None, uniforms=None):
         """Train on int64 pixel ids [n] (n <= batch); returns the squared errors fp32 [n] in
-        routed order (entry j belongs to ids[self.routing.perm[j]]).
+        routed order (entry j belongs to ids[self.routing.perm[j]]).  With ids None and
+        uniforms fp32 [n, 2], the batch is the stratified draw on those uniforms, computed
+        inside the route (the ids never reach memory; perm[j] is then a stratified slot).
         mark(name), if given, is called after each stage is queued (for stage timing)."""
-        n = ids.numel()
+        n = ids.numel() if ids is not None else uniforms.shape[0]
         if not 1 <= n <= self.batch:
             raise ValueError('batch size must be within 1..%d' % self.batch)
         mark = mark or (lambda name: None)
         r = self.routing
         view = Routing(r.perm[:n], r.coords[:n], r.offsets, None, r.colors[:n])
-        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, rgb=self.rgb)
+        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, rgb=self.rgb,
+              uniforms=uniforms)
         mark('route')
         raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
         mark('encode_forward')

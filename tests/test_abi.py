@@ -258,6 +258,18 @@ def test_reconstruct_scores_rejects_bad_arguments(native):
         assert message in native.odie_error().decode()
 
 
+def test_route_stratified_rejects_bad_arguments(native):
+    args = lambda uniforms, n: (uniforms, n, 2048, 1365, 8, 8, None, 8, 8, 8, None, None, 8, 1 << 20, 0)
+    assert native.odie_route_stratified(*args(8, 8)) == -1          # not a square
+    assert 'square power-of-two' in native.odie_error().decode()
+    assert native.odie_route_stratified(*args(8, 12)) == -1
+    assert native.odie_route_stratified(*args(12, 16)) == -1        # misaligned uniforms
+    assert 'aligned' in native.odie_error().decode()
+    assert native.odie_route_stratified(*args(None, 16)) == -1
+    assert native.odie_route_stratified(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, None, None, 8, 4, 0) == -1
+    assert 'workspace' in native.odie_error().decode()
+
+
 def test_stratified_ids_reject_bad_arguments(native):
     assert native.odie_stratified_ids(8, 8, 10, 10, 8, 0) == -1
     assert 'square power-of-two' in native.odie_error().decode()

@@ -59,3 +59,30 @@ def test_route_clustered_ids_and_empty_experts():
 def test_route_empty_batch():
     result = route(torch.zeros(0, dtype=torch.int64, device='cuda'), 2048, 1365, 8, 8)
     assert result.offsets.cpu().tolist() == [0] * 65
+
+
+@pytest.mark.parametrize('width,height,rx,ry,n', [
+    (2048, 1365, 8, 8, 1 << 16),        # the native step's batch over the 64-expert image
+    (32768, 32768, 32, 32, 1 << 20),    # the gigapixel image's 1024 tiles
+    (100, 37, 3, 5, 64),                # ragged tiles, strata larger than pixels
+])
+def test_route_stratified_fuses_the_draw(width, height, rx, ry, n):
+    """odie_route_stratified (the stratified draw computed inside the route) equals the route of
+    odie_stratified_ids' ids bit for bit: experts, perm, local coordinates, offsets, colours;
+    the oracle's stratified ids and route pin both."""
+    from odie_amd.sampling import stratified_ids
+    uniforms = torch.rand((n, 2), device='cuda', generator=torch.Generator(device='cuda').manual_seed(n))
+    uniforms[0] = torch.tensor([0.0, 0.0])
+    uniforms[-1] = torch.tensor([float.fromhex('0x1.fffffep-1')] * 2)   # largest fp32 below 1
+    image = torch.from_numpy(synth.integers(n, 'image', width * height * 3, 256).astype(np.uint8)).cuda()
+    ids = stratified_ids(uniforms, (height, width))
+    fused = route(None, width, height, rx, ry, with_expert=True, rgb=image, uniforms=uniforms)
+    plain = route(ids, width, height, rx, ry, with_expert=True, rgb=image)
+    for name in ('expert', 'perm', 'offsets', 'colors'):
+        assert torch.equal(getattr(fused, name), getattr(plain, name)), name
+    assert torch.equal(fused.coords.view(torch.int32), plain.coords.view(torch.int32))
+    expected = oracle.stratified_ids(uniforms.cpu().numpy(), width, height)
+    assert np.array_equal(ids.cpu().numpy(), expected)
+    _, perm, local, offsets = oracle.route(expected, width, height, rx, ry)
+    assert np.array_equal(fused.perm.cpu().numpy(), perm)
+    assert np.array_equal(fused.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
