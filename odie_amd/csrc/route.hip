@@ -67,12 +67,19 @@ struct Bounds {
     int32_t y0[kMaxRegions + 1];
 };
 
-__device__ inline void locate(const RouteArgs& a, const Bounds& b, int64_t i, int& expert, uint32_t& x, uint32_t& y,
-                              int& rx, int& ry) {
-    const uint32_t id = static_cast<uint32_t>(
+// Pixel id of input i (its low 32 bits: ids are below 2^32 once clamped into the image).
+__device__ inline uint32_t pixel_id(const RouteArgs& a, int64_t i) {
+    return static_cast<uint32_t>(
         a.uniforms ? stratified_id(reinterpret_cast<const float2*>(a.uniforms)[i], i, a.side, a.inv_side,
                                    static_cast<int>(a.width), static_cast<int>(a.height))
                    : a.ids[i]);
+}
+
+// The walks below load kAhead groups of 64 ids per wave before placing any of them.
+constexpr int kAhead = 8;
+
+__device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t id, int& expert, uint32_t& x,
+                                 uint32_t& y, int& rx, int& ry) {
     x = id % a.width;
     y = id / a.width;
     if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
@@ -101,11 +108,21 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
     if (part < a.parts) {
         const int64_t begin = static_cast<int64_t>(part) * a.part;
         const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
-        for (int64_t i = begin + lane; i < end; i += 64) {
-            int expert, rx, ry;
-            uint32_t x, y;
-            locate(a, bounds, i, expert, x, y, rx, ry);
-            atomicAdd(mine + expert, 1);
+        for (int64_t g = begin; g < end; g += 64 * kAhead) {
+            uint32_t id[kAhead];
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) {
+                const int64_t i = g + k * 64 + lane;
+                id[k] = i < end ? pixel_id(a, i) : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) {
+                if (g + k * 64 + lane >= end) continue;
+                int expert, rx, ry;
+                uint32_t x, y;
+                locate_id(a, bounds, id[k], expert, x, y, rx, ry);
+                atomicAdd(mine + expert, 1);
+            }
         }
     }
     __syncthreads();
@@ -204,39 +221,49 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
     const int64_t begin = static_cast<int64_t>(part) * a.part;
     const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
     const uint64_t below = (uint64_t{1} << lane) - 1;
-    for (int64_t group = begin; group < end; group += 64) {
-        const int64_t i = group + lane;
-        const bool valid = i < end;
-        int expert = -1, rx = 0, ry = 0;
-        uint32_t x = 0, y = 0;
-        if (valid) locate(a, bounds, i, expert, x, y, rx, ry);
-        // Lanes holding the same expert: the AND over the id's bits of ballot(bit) or its
-        // complement (one ballot per bit, whatever the number of distinct experts).  Every
-        // lane reads the running count of its expert, then the lowest lane of each expert
-        // advances it; the LDS reads of one instruction precede its writes in the wave.
-        uint64_t same = __ballot(valid);
-        for (int bit = 0; bit < a.expert_bits; ++bit) {
-            const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
-            same &= ((expert >> bit) & 1) ? ones : ~ones;
+    for (int64_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
+        uint32_t ids[kAhead];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int64_t i = ahead + k * 64 + lane;
+            ids[k] = i < end ? pixel_id(a, i) : 0u;
         }
-        int32_t base = 0, rank = 0;
-        if (valid) {
-            rank = __popcll(same & below);
-            base = mine[expert];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        if (valid && rank == 0) mine[expert] = base + __popcll(same);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (valid) {
-            const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.parts + part]) + base + rank;
-            a.perm[slot] = static_cast<int32_t>(i);
-            const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
-            const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
-            reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
-            if (a.expert_out) a.expert_out[i] = expert;
-            // the pixel's index for route_colors_kernel (below 2^32: the image size is bounded)
-            if (a.colors) a.colors[slot] = y * a.width + x;
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int64_t group = ahead + k * 64;
+            const int64_t i = group + lane;
+            const bool valid = i < end;
+            int expert = -1, rx = 0, ry = 0;
+            uint32_t x = 0, y = 0;
+            if (valid) locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
+            // Lanes holding the same expert: the AND over the id's bits of ballot(bit) or its
+            // complement (one ballot per bit, whatever the number of distinct experts).  Every
+            // lane reads the running count of its expert, then the lowest lane of each expert
+            // advances it; the LDS reads of one instruction precede its writes in the wave.
+            uint64_t same = __ballot(valid);
+            for (int bit = 0; bit < a.expert_bits; ++bit) {
+                const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
+                same &= ((expert >> bit) & 1) ? ones : ~ones;
+            }
+            int32_t base = 0, rank = 0;
+            if (valid) {
+                rank = __popcll(same & below);
+                base = mine[expert];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (valid && rank == 0) mine[expert] = base + __popcll(same);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (valid) {
+                const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.parts + part]) + base + rank;
+                a.perm[slot] = static_cast<int32_t>(i);
+                const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
+                const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
+                reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
+                if (a.expert_out) a.expert_out[i] = expert;
+                // the pixel's index for route_colors_kernel (below 2^32: the image size is bounded)
+                if (a.colors) a.colors[slot] = y * a.width + x;
+            }
         }
     }
 }
@@ -335,34 +362,44 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
     const int64_t begin = static_cast<int64_t>(part) * a.part;
     const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
     const uint64_t below = (uint64_t{1} << lane) - 1;
-    for (int64_t group = begin; group < end; group += 64) {
-        const int64_t i = group + lane;
-        const bool valid = i < end;
-        int expert = -1, rx = 0, ry = 0;
-        uint32_t x = 0, y = 0;
-        if (valid) locate(a, bounds, i, expert, x, y, rx, ry);
-        uint64_t same = __ballot(valid);
-        for (int bit = 0; bit < a.expert_bits; ++bit) {
-            const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
-            same &= ((expert >> bit) & 1) ? ones : ~ones;
+    for (int64_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
+        uint32_t ids[kAhead];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int64_t i = ahead + k * 64 + lane;
+            ids[k] = i < end ? pixel_id(a, i) : 0u;
         }
-        int32_t base = 0, rank = 0;
-        if (valid) {
-            rank = __popcll(same & below);
-            base = t.running[expert];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        if (valid && rank == 0) t.running[expert] = base + __popcll(same);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (valid) {
-            const int32_t local = t.start[expert] + base + rank;
-            t.slot[local] = a.counts[static_cast<int64_t>(expert) * a.parts + part] + base + rank;
-            t.index[local] = static_cast<int32_t>(i);
-            t.u[local] = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
-            t.v[local] = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
-            t.pixel[local] = y * a.width + x;
-            if (a.expert_out) a.expert_out[i] = expert;
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int64_t group = ahead + k * 64;
+            const int64_t i = group + lane;
+            const bool valid = i < end;
+            int expert = -1, rx = 0, ry = 0;
+            uint32_t x = 0, y = 0;
+            if (valid) locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
+            uint64_t same = __ballot(valid);
+            for (int bit = 0; bit < a.expert_bits; ++bit) {
+                const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
+                same &= ((expert >> bit) & 1) ? ones : ~ones;
+            }
+            int32_t base = 0, rank = 0;
+            if (valid) {
+                rank = __popcll(same & below);
+                base = t.running[expert];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (valid && rank == 0) t.running[expert] = base + __popcll(same);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (valid) {
+                const int32_t local = t.start[expert] + base + rank;
+                t.slot[local] = a.counts[static_cast<int64_t>(expert) * a.parts + part] + base + rank;
+                t.index[local] = static_cast<int32_t>(i);
+                t.u[local] = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
+                t.v[local] = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
+                t.pixel[local] = y * a.width + x;
+                if (a.expert_out) a.expert_out[i] = expert;
+            }
         }
     }
     __syncthreads();
