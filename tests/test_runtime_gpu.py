@@ -4,7 +4,8 @@ tested entry points on the same inputs: the hash-grid step bit for bit (its back
 deterministic), the packed-plane step with the grid gradient within the encode-backward
 tolerance (fp32 atomics) and every update bit for bit from that gradient; a captured graph
 replayed with eager work between replays, bit for bit against eager steps; the optimizer-state
-summaries.  Gradients reach the optimizers through fp16 stores as in the reference: the grid's
+summaries; and one packed-plane step at the reference's level rows against the oracle, stage by
+stage.  Gradients reach the optimizers through fp16 stores as in the reference: the grid's
 fp16(g) at loss scale 128, the heads' fp16(fp16(g) / 128) at 128 (odie/native/runtime.cu:
 298-309, kernels.cuh:140-143)."""
 import json
@@ -13,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+import oracle
 from odie_amd import _lib, synth
 from odie_amd.config import grid_levels
 from odie_amd.decoder import Decoder
@@ -315,4 +317,191 @@ def test_runtime_rejects_invalid_steps():
         opt.step_raw(torch.full((256,), width * height + 5, dtype=torch.int64, device='cuda'), update=False)
         torch.cuda.synchronize()
         assert torch.isfinite(opt.copied('squares', (256,), torch.float32)).all()
+        opt.close()
+
+
+
+def _layer_bound(expected, magnitude):
+    """fp16 rounding of a layer's output (2^-10 relative) plus fp32 accumulation order (2^-16 of
+    its magnitude sum)."""
+    return 2.0 ** -10 * np.abs(expected.astype(np.float64)) + 2.0 ** -16 * magnitude + 2.0 ** -24
+
+
+def _heads_match_oracle(raw, visible, dims, coarse, gate0, decoder0, image, ids, got):
+    """The gate and decoder stages of one runtime step against the oracle, from the runtime's
+    features `raw` (fp16 [n, row] on the GPU): the gate's s (from the same launch run again on raw)
+    within fp16-logit rounding and the gated features bit-exact given s; the decoder launch run
+    again with its hidden layers exported reproduces the runtime's outputs and squares bit for bit,
+    its layers within the per-layer bars, squares bit-exact, dz and the decoder gradient within
+    the decoder bars; the gate's upstream and gradient within the gate bars.  `got` holds the
+    runtime's output, squares, decoder_grad and gate_grad.  Returns the upstream (fp16 [n, row])
+    the grid gradient is formed from."""
+    n, levels = raw.shape[0], len(dims)
+    raw_host, ids_host = raw.cpu().numpy(), ids.cpu().numpy()
+    inputs = raw
+    if gate0 is not None:
+        gate16 = gate0.astype(np.float16)
+        probe = Gate(weights=gate0, coarse=coarse, features=dims)
+        vis = None if visible is None else torch.from_numpy(visible.astype(np.uint8)).cuda()
+        weighted, s = probe.forward(raw, visible=vis)
+        s_host = s.cpu().numpy()
+        h_gate, z, _ = oracle.gate_logits(raw_host, gate16, levels)
+        ref_s, z = oracle.gate_values(z, coarse)[:, :levels], z[:, :levels].astype(np.float64)
+        assert np.all(np.abs(s_host - ref_s) <= ref_s * (1 - ref_s) * 2.0 ** -9 * (np.abs(z) + 1) + 2.0 ** -22)
+        assert np.array_equal(weighted.cpu().numpy().view(np.uint16),
+                              oracle.gate_apply(raw_host, s_host, visible, dims).view(np.uint16))
+        inputs = weighted
+
+    decoder16 = decoder0.astype(np.float16)
+    out = torch.empty((n, 16), dtype=torch.float16, device='cuda')
+    hidden = torch.empty((n, 128), dtype=torch.float16, device='cuda')
+    again = torch.empty(n, dtype=torch.float32, device='cuda')
+    dz = Decoder(weights=decoder0, width=raw.shape[1]).train(inputs, rgb=image.reshape(-1), ids=ids, out=out,
+                                                             hidden=hidden, squares=again)
+    x16, h, dz, output = inputs.cpu().numpy(), hidden.cpu().numpy(), dz.cpu().numpy(), got['output']
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), output.view(np.uint16))
+    assert np.array_equal(again.cpu().numpy(), got['squares'])
+    w1, w2, w3 = oracle.mlp_weights(decoder16)
+    for value, (want, magnitude) in ((h[:, :64], oracle.mlp_layer(x16, w1, True)),
+                                     (h[:, 64:], oracle.mlp_layer(h[:, :64], w2, True)),
+                                     (output, oracle.mlp_layer(h[:, 64:], w3, False))):
+        assert np.all(np.abs(value.astype(np.float64) - want) <= _layer_bound(want, magnitude))
+    slots = np.arange(n)
+    targets = oracle.mlp_targets(slots, rgb=image.cpu().numpy().reshape(-1, 3), ids=ids_host)
+    dy, ref_squares = oracle.mlp_loss(output, targets, slots, n)
+    assert np.array_equal(got['squares'], ref_squares)
+    ref_dz, dz_magnitude, ref_dw, dw_magnitude = oracle.mlp_backward(x16, h[:, :64], h[:, 64:], dy, decoder16)
+    assert np.all(np.abs(dz.astype(np.float64) - ref_dz) <=
+                  2.0 ** -10 * np.abs(ref_dz.astype(np.float64)) + 2.0 ** -10 * dz_magnitude + 2.0 ** -24)
+    assert np.all(np.abs(got['decoder_grad'].astype(np.float64) - ref_dw) <= 2.0 ** -9 * dw_magnitude + 1e-6)
+    if gate0 is None:
+        return dz
+    upstream = probe.backward(raw, torch.from_numpy(dz).cuda(), s, visible=vis).cpu().numpy()
+    direct, da = oracle.gate_back(raw_host, dz, s_host, coarse, visible=visible, features=dims)
+    dr, dr_magnitude, dweights, magnitude = oracle.gate_mlp_backward(raw_host, h_gate, da, gate16, levels)
+    want = oracle.gate_upstream(direct, dr).astype(np.float64)
+    assert np.all(np.abs(upstream.astype(np.float64) - want) <=
+                  2.0 ** -10 * np.abs(want) + 2.0 ** -10 * dr_magnitude / 128 + 2.0 ** -24)
+    assert np.all(np.abs(got['gate_grad'].astype(np.float64) - dweights) <= 2.0 ** -9 * magnitude + 1e-6)
+    return upstream
+
+
+def _fetch(opt, n, row, model):
+    """The runtime's buffers after a step, on the host."""
+    got = dict(output=opt.copied('output', (n, 16), torch.float16),
+               squares=opt.copied('squares', (n,), torch.float32),
+               grid_grad=opt.copied('grid_grad', (model.grid.numel(),), torch.float32),
+               decoder_grad=opt.copied('decoder_grad', (model.decoder.params.numel(),), torch.float32))
+    if model.gate is not None:
+        got['gate_grad'] = opt.copied('gate_grad', (model.gate.params.numel(),), torch.float32)
+    raw = opt.copied('raw', (n, row), torch.float16)
+    torch.cuda.synchronize()
+    return raw, {k: v.cpu().numpy() for k, v in got.items()}
+
+
+def _coordinates(ids_host, width, height):
+    """The pixel centres' unit coordinates of odie/native/runtime.cu:34-36, in fp32."""
+    rx, ry = np.float32(1.0 / (width - 1)), np.float32(1.0 / (height - 1))
+    return np.stack([(ids_host % width).astype(np.float32) * rx, (ids_host // width).astype(np.float32) * ry], 1)
+
+
+def _check_gradient(grid_grad, grad, magnitude):
+    """fp32 atomics or fixed point: order only."""
+    bound = 1e-4 * magnitude + 2.0 ** -32 * float(magnitude.max(initial=0.0)) + 1e-30
+    bad = np.abs(grid_grad.astype(np.float64) - grad) > bound
+    assert not bad.any(), '%d/%d gradient entries out of tolerance' % (bad.sum(), bad.size)
+
+
+@pytest.mark.parametrize('shape,router,active', [('div2k', True, 16), ('L20', True, 13), ('16x2', False, 11)])
+def test_packed_step_matches_oracle(shape, router, active):
+    """One odie_step of the packed-plane runtime at the reference's level rows against the oracle,
+    stage by stage, each stage from the runtime's own output of the previous one: the features
+    bit-exact (levels past the active prefix zero, padding columns one); the heads as
+    _heads_match_oracle checks them; the grid gradient within the encode-backward bar of the
+    oracle's gradient of the runtime's upstream; the three Adam updates from the runtime's fp16
+    gradients (grid: fp16(g) at loss scale 128; heads: fp16(fp16(g) / 128) at 128) within the
+    Adam bar."""
+    width, height, n, coarse = 83, 64, 3000, 1
+    dims = SHAPES[shape]
+    row, columns = _width(dims), sum(dims)
+    print('packed runtime step vs oracle: %s, router %s, active %d' % (shape, router, active), flush=True)
+    with torch.cuda.stream(_stream()):
+        image = _image(16, width, height)
+        config = _config('xy_planes', router, coarse, dims=dims)
+        planes = _planes(5, dims)
+        planes.set_active_prefix(active)
+        model = NativeModel(Decoder(seed=7, width=row),
+                            Gate(seed=8, coarse=coarse, features=dims) if router else None, planes=planes)
+        opt, _ = make_native_optimizer(model, image, (height, width), config)
+        grid0 = model.grid.cpu().numpy()
+        decoder0 = model.decoder.params.cpu().numpy()
+        gate0 = model.gate.params.cpu().numpy() if router else None
+        ids_host = synth.integers(60, 'runtime_ids', n, width * height)
+        ids = torch.from_numpy(ids_host).cuda()
+        opt.step_raw(ids)
+        raw, got = _fetch(opt, n, row, model)
+
+        xy = _coordinates(ids_host, width, height)
+        layout = {k: getattr(planes, k).cpu().numpy() for k in ('descriptors', 'node_bitmap', 'node_prefix', 'bitmap')}
+        expected, visible = oracle.packed_forward(xy, grid0, layout, row)
+        expected[:, sum(dims[:active]):] = 0
+        expected[:, columns:] = 1.0
+        visible[:, active:] = False
+        assert np.array_equal(raw.cpu().numpy().view(np.uint16), expected.view(np.uint16))
+        up = _heads_match_oracle(raw, visible, dims, coarse, gate0, decoder0, image, ids, got)
+        _check_gradient(got['grid_grad'], *oracle.packed_backward(xy, up, layout, grid0.size))
+
+        def adam(variant, start, gradient, lr):
+            m, v = np.zeros(start.size), np.zeros(start.size)
+            steps = np.zeros(start.size, dtype=np.uint32)
+            return oracle.adam(variant, start.astype(np.float64), gradient, m, v, steps, 1, lr, scale=128.0)
+
+        def head_gradient(g):
+            return (g.astype(np.float16).astype(np.float32) / np.float32(128.0)).astype(np.float16).astype(np.float64)
+
+        updates = [(model.grid, adam(1, grid0, got['grid_grad'].astype(np.float16).astype(np.float64), 1e-2)),
+                   (model.decoder.params, adam(2, decoder0, head_gradient(got['decoder_grad']), 1e-3))]
+        if router:
+            updates.append((model.gate.params, adam(2, gate0, head_gradient(got['gate_grad']), 2e-3)))
+        for params, want in updates:
+            assert np.allclose(params.cpu().numpy().astype(np.float64), want, rtol=1e-5, atol=1e-7)
+        opt.close()
+
+
+@pytest.mark.parametrize('router,coarse,levels,features', [(True, 2, 16, 2), (False, 0, 20, 1), (True, 0, 12, 4)])
+def test_hash_step_matches_oracle(router, coarse, levels, features):
+    """One odie_step of the hash-grid runtime without the update (which writes the grid gradient
+    out instead of fusing it into Adam) against the oracle: the features of the fp16 table
+    bit-exact with padding columns one, the heads as _heads_match_oracle checks them, and the grid
+    gradient within the encode-backward bar of the oracle's gradient of the runtime's upstream;
+    no parameter moves."""
+    width, height, n = 97, 61, 3000
+    encoding = dict(HASH, n_levels=levels, n_features_per_level=features)
+    dims = [features] * levels
+    row = _width(dims)
+    print('hash runtime step vs oracle: %d x F%d, router %s' % (levels, features, router), flush=True)
+    with torch.cuda.stream(_stream()):
+        image = _image(17, width, height)
+        config = _config('hash_grid', router, coarse, dims=dims, encoding=encoding)
+        model, hash_levels = _hash_model(6, router, coarse, encoding=encoding)
+        opt = NativeOptimizer(model, image, (height, width), config, [model.grid])
+        grid0 = model.grid.cpu().numpy()
+        decoder0 = model.decoder.params.cpu().numpy()
+        gate0 = model.gate.params.cpu().numpy() if router else None
+        ids_host = synth.integers(61, 'runtime_ids', n, width * height)
+        ids = torch.from_numpy(ids_host).cuda()
+        opt.step_raw(ids, update=False)
+        raw, got = _fetch(opt, n, row, model)
+
+        xy = _coordinates(ids_host, width, height)
+        rows = [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in hash_levels]
+        expected = oracle.hash_forward(xy, grid0.astype(np.float16), rows, features, expert_params=grid0.size,
+                                       width=row)
+        expected[:, levels * features:] = 1.0
+        assert np.array_equal(raw.cpu().numpy().view(np.uint16), expected.view(np.uint16))
+        up = _heads_match_oracle(raw, None, dims, coarse, gate0, decoder0, image, ids, got)
+        _check_gradient(got['grid_grad'], *oracle.hash_backward(xy, up, rows, features, grid0.size,
+                                                                expert_params=grid0.size))
+        assert np.array_equal(_bits(model.grid), grid0.view(np.uint32))
+        assert np.array_equal(_bits(model.decoder.params), decoder0.view(np.uint32))
         opt.close()
