@@ -65,6 +65,10 @@ __device__ inline void stage_model(const ReconArgs& a, const TileBounds& bounds,
             tb.ry[j] = bounds.ry[j];
         }
     }
+    if (threadIdx.x == 0) {
+        tb.sx = bounds.sx;
+        tb.sy = bounds.sy;
+    }
     __syncthreads();
 }
 
@@ -75,7 +79,7 @@ __device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const _
     const uint32_t x = id % a.width;
     uint32_t y = id / a.width;
     if (y >= a.height) y = a.height - 1;
-    const int tx = tile_of(tb.x0, a.regions_x, x), ty = tile_of(tb.y0, a.regions_y, y);
+    const int tx = tile_of(tb.x0, a.regions_x, tb.sx, x), ty = tile_of(tb.y0, a.regions_y, tb.sy, y);
     const int t = ty * a.regions_x + tx;
     int slot = a.slots ? a.slots[t] : t;
     if (slot >= a.experts || !valid) slot = -1;

@@ -60,6 +60,7 @@ struct RouteArgs {
     int32_t y0[kMaxRegions + 1];
     float rx[kMaxRegions];   // fp32(1/(tile_width-1))
     float ry[kMaxRegions];
+    float sx, sy;            // fp32(regions_x / width), fp32(regions_y / height)
 };
 
 struct Bounds {
@@ -83,8 +84,8 @@ __device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t i
     x = id % a.width;
     y = id / a.width;
     if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
-    rx = tile_of(b.x0, a.regions_x, x);
-    ry = tile_of(b.y0, a.regions_y, y);
+    rx = tile_of(b.x0, a.regions_x, a.sx, x);
+    ry = tile_of(b.y0, a.regions_y, a.sy, y);
     expert = ry * a.regions_x + rx;
 }
 
@@ -298,43 +299,29 @@ __global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t
     }
 }
 
-// The scatter with one wave per block staging its sub-chunk in LDS: the wave first places
-// every id of its sub-chunk at its position inside the sub-chunk's expert-ordered output
-// (the run of expert e starts at the sum of the sub-chunk's counts of the experts before e),
-// then writes the runs out in order, so consecutive lanes store consecutive slots.  Same slots
-// as route_scatter_kernel; the stores are whole runs instead of one id per expert per group.
-struct Staging {
-    int32_t* running;  // [experts] ids of each expert placed so far
-    int32_t* start;    // [experts] first local position of each expert's run
-    int32_t* slot;     // [part] global slot of local position j
-    int32_t* index;    // [part] input index
-    float* u;
-    float* v;
-    uint32_t* pixel;
-};
-
-__device__ inline Staging staging(int32_t* lds, int experts, int part) {
-    Staging t;
-    t.running = lds;
-    t.start = lds + experts;
-    t.slot = lds + 2 * experts;
-    t.index = t.slot + part;
-    t.u = reinterpret_cast<float*>(t.index + part);
-    t.v = t.u + part;
-    t.pixel = reinterpret_cast<uint32_t*>(t.v + part);
-    return t;
+// The scatter with one wave per block staging its sub-chunk in LDS.  The wave first places
+// every id of its sub-chunk at its position inside the sub-chunk's expert-ordered output (the
+// run of expert e starts at the sum of the sub-chunk's counts of the experts before e),
+// recording only the id's offset inside the sub-chunk; then its lanes take consecutive
+// positions, reload those ids (the sub-chunk's own, from cache), locate them again and store
+// them at consecutive slots.  Same slots as route_scatter_kernel; the stores are whole runs,
+// and with 2 or 4 bytes of LDS per id many waves share a CU.
+template <typename Local>
+inline size_t staging_bytes(int experts, int part) {
+    return static_cast<size_t>(2) * experts * 4 + static_cast<size_t>(part) * sizeof(Local);
 }
 
-inline size_t staging_bytes(int experts, int part) { return (static_cast<size_t>(2) * experts + 5 * part) * 4; }
-
+template <typename Local>
 __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
     extern __shared__ int32_t lds[];
     __shared__ Bounds bounds;
     load_bounds(a, bounds);
     const int lane = threadIdx.x;
-    const int part = blockIdx.x;
+    const int part = static_cast<int>(xcd_major(blockIdx.x, gridDim.x));
     if (part >= a.parts) return;
-    const Staging t = staging(lds, a.experts, a.part);
+    int32_t* start = lds;                  // [experts] first local position of each expert's run
+    int32_t* running = lds + a.experts;    // [experts] ids of each expert placed so far
+    Local* local = reinterpret_cast<Local*>(lds + 2 * a.experts);   // [part] offset of position j's id
     // local run starts: exclusive scan over the experts of this sub-chunk's counts (count(e, part)
     // is the difference of consecutive scanned offsets in expert-major order)
     const int64_t last = static_cast<int64_t>(a.experts) * a.parts - 1;
@@ -353,8 +340,8 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
             if (lane >= d) inclusive += other;
         }
         if (e < a.experts) {
-            t.start[e] = carry + inclusive - c;
-            t.running[e] = 0;
+            start[e] = carry + inclusive - c;
+            running[e] = 0;
         }
         carry += __shfl(inclusive, 63);
     }
@@ -371,8 +358,7 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
-            const int64_t group = ahead + k * 64;
-            const int64_t i = group + lane;
+            const int64_t i = ahead + k * 64 + lane;
             const bool valid = i < end;
             int expert = -1, rx = 0, ry = 0;
             uint32_t x = 0, y = 0;
@@ -385,30 +371,48 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
             int32_t base = 0, rank = 0;
             if (valid) {
                 rank = __popcll(same & below);
-                base = t.running[expert];
+                base = running[expert];
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
-            if (valid && rank == 0) t.running[expert] = base + __popcll(same);
+            if (valid && rank == 0) running[expert] = base + __popcll(same);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             if (valid) {
-                const int32_t local = t.start[expert] + base + rank;
-                t.slot[local] = a.counts[static_cast<int64_t>(expert) * a.parts + part] + base + rank;
-                t.index[local] = static_cast<int32_t>(i);
-                t.u[local] = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
-                t.v[local] = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
-                t.pixel[local] = y * a.width + x;
+                local[start[expert] + base + rank] = static_cast<Local>(i - begin);
                 if (a.expert_out) a.expert_out[i] = expert;
             }
         }
     }
     __syncthreads();
+    // global slot of local position j of expert e's run: counts(e, part) - start[e] + j
+    for (int e = lane; e < a.experts; e += 64) start[e] = a.counts[static_cast<int64_t>(e) * a.parts + part] - start[e];
+    __syncthreads();
     const int32_t count = static_cast<int32_t>(end - begin);
-    for (int32_t j = lane; j < count; j += 64) {
-        const int32_t slot = t.slot[j];
-        a.perm[slot] = t.index[j];
-        reinterpret_cast<float2*>(a.coords)[slot] = make_float2(t.u[j], t.v[j]);
-        if (a.colors) a.colors[slot] = t.pixel[j];
+    for (int32_t j0 = 0; j0 < count; j0 += 64 * kAhead) {
+        int32_t at[kAhead];
+        uint32_t ids[kAhead];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int32_t j = j0 + k * 64 + lane;
+            at[k] = j < count ? static_cast<int32_t>(local[j]) : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) ids[k] = j0 + k * 64 + lane < count ? pixel_id(a, begin + at[k]) : 0u;
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int32_t j = j0 + k * 64 + lane;
+            if (j >= count) continue;
+            int expert, rx, ry;
+            uint32_t x, y;
+            locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
+            const int64_t slot = static_cast<int64_t>(start[expert]) + j;
+            a.perm[slot] = static_cast<int32_t>(begin + at[k]);
+            const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
+            const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
+            reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
+            // the pixel's index for route_colors_kernel
+            if (a.colors) a.colors[slot] = y * a.width + x;
+        }
     }
 }
 
@@ -506,6 +510,8 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
             a.rx[r] = tb.rx[r];
             a.ry[r] = tb.ry[r];
         }
+        a.sx = tb.sx;
+        a.sy = tb.sy;
     }
     const hipStream_t s = as_stream(stream);
     const size_t shmem = static_cast<size_t>(kWaves) * experts * 4;
@@ -518,10 +524,19 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
     route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
     route_scan_apply_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
-    // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU)
-    const size_t staged = staging_bytes(experts, a.part);
-    if (staged + sizeof(Bounds) <= 40 * 1024)
-        route_scatter_staged_kernel<<<static_cast<uint32_t>(a.parts), 64, staged, s>>>(a);
+    // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU); sub-chunk
+    // offsets take 16 bits up to 2^16 ids.  A stratified batch lists its strata row by row, so
+    // consecutive ids mostly share an expert and the direct scatter's stores already come in runs.
+    const uint32_t staged_blocks = round_up(static_cast<uint32_t>(a.parts), kXcds);
+    const bool fits16 = a.part <= 65536 && staging_bytes<uint16_t>(experts, a.part) + sizeof(Bounds) <= 40 * 1024;
+    const bool fits32 = staging_bytes<int32_t>(experts, a.part) + sizeof(Bounds) <= 40 * 1024;
+    const bool short_offsets = !uniforms && fits16;
+    const bool staged = short_offsets || (!uniforms && fits32);
+    if (short_offsets)
+        route_scatter_staged_kernel<uint16_t>
+            <<<staged_blocks, 64, staging_bytes<uint16_t>(experts, a.part), s>>>(a);
+    else if (staged)
+        route_scatter_staged_kernel<int32_t><<<staged_blocks, 64, staging_bytes<int32_t>(experts, a.part), s>>>(a);
     else
         route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     if (colors) {

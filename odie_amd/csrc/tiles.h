@@ -14,6 +14,7 @@ struct TileBounds {
     int32_t y0[kMaxTiles + 1];
     float rx[kMaxTiles];
     float ry[kMaxTiles];
+    float sx, sy;   // fp32(regions_x / width), fp32(regions_y / height): tile_of's estimate
 };
 
 inline void make_tile_bounds(int width, int height, int regions_x, int regions_y, TileBounds& b) {
@@ -28,16 +29,21 @@ inline void make_tile_bounds(int width, int height, int regions_x, int regions_y
         b.rx[r] = static_cast<float>(1.0 / static_cast<double>(tw - 1));
         b.ry[r] = static_cast<float>(1.0 / static_cast<double>(th - 1));
     }
+    b.sx = static_cast<float>(static_cast<double>(regions_x) / width);
+    b.sy = static_cast<float>(static_cast<double>(regions_y) / height);
 }
 
-// Largest r < regions with bounds[r] <= v.
-__device__ inline int tile_of(const int32_t* bounds, int regions, uint32_t v) {
-    int lo = 0, hi = regions - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (static_cast<uint32_t>(bounds[mid]) <= v) lo = mid; else hi = mid - 1;
-    }
-    return lo;
+// Largest r < regions with bounds[r] <= v.  With bounds[r] = ceil(r * extent / regions) that is
+// floor(v * regions / extent) (bounds[r] <= v iff r * extent <= v * regions for integer v),
+// capped at regions - 1.  The fp32 estimate v * scale (scale = fp32(regions / extent)) is within
+// 2^-16 of v * regions / extent for r < 64, so its floor is off by at most one, either way: one
+// comparison with the neighbouring bound fixes it.
+__device__ inline int tile_of(const int32_t* bounds, int regions, float scale, uint32_t v) {
+    int r = static_cast<int>(static_cast<float>(v) * scale);
+    r = r < 0 ? 0 : (r > regions - 1 ? regions - 1 : r);
+    if (r + 1 < regions && static_cast<uint32_t>(bounds[r + 1]) <= v) ++r;
+    else if (r > 0 && static_cast<uint32_t>(bounds[r]) > v) --r;
+    return r;
 }
 
 }  // namespace odie
