@@ -131,9 +131,10 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
         for (int e = lane; e < a.experts; e += 64) a.counts[static_cast<int64_t>(e) * a.parts + part] = mine[e];
 }
 
-// Exclusive scan of counts (expert-major) in place, in three launches: every block sums a
-// segment of kScanSegment counts, one block scans those sums, every block rescans its
-// segment from its offset.  offsets[e] = first slot of expert e; offsets[E] = n.
+// Exclusive scan of counts (expert-major) in place: every block sums a segment of kScanSegment
+// counts; then every block rescans its segment from its offset, the sum of the segments before
+// it (added up by the block itself when there are at most 1024 segments, else scanned by one
+// block in a launch between the two).  offsets[e] = first slot of expert e; offsets[E] = n.
 constexpr int kScanBlock = 256;
 constexpr int kScanSegment = 1024;  // counts per scan block (4 per thread)
 
@@ -186,8 +187,20 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_top_kernel(RouteArgs a,
     if (threadIdx.x == 0) a.offsets[a.experts] = static_cast<int32_t>(a.n);
 }
 
+// SUMS_SCANNED: block_sums already holds each segment's offset (route_scan_top_kernel ran);
+// otherwise every block adds up the sums of the segments before its own (few segments).
+template <bool SUMS_SCANNED>
 __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs a) {
     __shared__ int32_t shared[kScanBlock];
+    int32_t offset;
+    if constexpr (SUMS_SCANNED) {
+        offset = a.block_sums[blockIdx.x];
+    } else {
+        int32_t before = 0;
+        for (uint32_t b = threadIdx.x; b < blockIdx.x; b += kScanBlock) before += a.block_sums[b];
+        block_exclusive_scan(before, shared, offset);
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.offsets[a.experts] = static_cast<int32_t>(a.n);
+    }
     const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
     constexpr int kPer = kScanSegment / kScanBlock;
     const int64_t begin = static_cast<int64_t>(blockIdx.x) * kScanSegment + threadIdx.x * kPer;
@@ -198,7 +211,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
         sum += values[j];
     }
     int32_t block_total;
-    int32_t running = a.block_sums[blockIdx.x] + block_exclusive_scan(sum, shared, block_total);
+    int32_t running = offset + block_exclusive_scan(sum, shared, block_total);
     for (int j = 0; j < kPer; ++j) {
         const int64_t k = begin + j;
         if (k < total) {
@@ -276,7 +289,8 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
 constexpr int kColorsPer = 8;
 constexpr int kColorsChunk = kRouteBlock * kColorsPer;
 
-__global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t* rgb, uint32_t* colors, int64_t n) {
+__global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t* rgb, uint32_t* colors, int64_t n,
+                                                                  uint64_t image_bytes, bool words) {
     const int64_t begin = static_cast<int64_t>(xcd_major(blockIdx.x, gridDim.x)) * kColorsChunk + threadIdx.x;
     uint32_t pixel[kColorsPer];
 #pragma unroll
@@ -284,18 +298,25 @@ __global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t
         const int64_t i = begin + k * kRouteBlock;
         pixel[k] = i < n ? colors[i] : 0u;
     }
-    uint32_t r[kColorsPer], g[kColorsPer], b[kColorsPer];
+    // A pixel's three bytes from the 8-byte window at the dword below them (one load; the base
+    // is 4-byte aligned when `words`), or byte by byte where that window would pass the image's end.
+    uint32_t c[kColorsPer];
 #pragma unroll
     for (int k = 0; k < kColorsPer; ++k) {
-        const uint8_t* at = rgb + 3 * static_cast<uint64_t>(pixel[k]);
-        r[k] = at[0];
-        g[k] = at[1];
-        b[k] = at[2];
+        const uint64_t at = 3 * static_cast<uint64_t>(pixel[k]);
+        const uint64_t word = at & ~uint64_t{3};
+        if (words && word + 8 <= image_bytes) {
+            const uint2 w = *reinterpret_cast<const uint2*>(rgb + word);
+            const uint64_t both = (static_cast<uint64_t>(w.y) << 32) | w.x;
+            c[k] = static_cast<uint32_t>(both >> (8 * (at - word))) & 0xffffffu;
+        } else {
+            c[k] = rgb[at] | (static_cast<uint32_t>(rgb[at + 1]) << 8) | (static_cast<uint32_t>(rgb[at + 2]) << 16);
+        }
     }
 #pragma unroll
     for (int k = 0; k < kColorsPer; ++k) {
         const int64_t i = begin + k * kRouteBlock;
-        if (i < n) colors[i] = r[k] | (g[k] << 8) | (b[k] << 16);
+        if (i < n) colors[i] = c[k];
     }
 }
 
@@ -522,8 +543,12 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     if (sblocks > kScanBlock * 64) return fail("odie_route: too many counts to scan");
     route_count_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
-    route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
-    route_scan_apply_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
+    if (sblocks <= kScanBlock * 4) {
+        route_scan_apply_kernel<false><<<sblocks, kScanBlock, 0, s>>>(a);
+    } else {
+        route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
+        route_scan_apply_kernel<true><<<sblocks, kScanBlock, 0, s>>>(a);
+    }
     // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU); sub-chunk
     // offsets take 16 bits up to 2^16 ids.  A stratified batch lists its strata row by row, so
     // consecutive ids mostly share an expert and the direct scatter's stores already come in runs.
@@ -541,7 +566,9 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
         route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     if (colors) {
         const uint32_t chunks = round_up(static_cast<uint32_t>((n + kColorsChunk - 1) / kColorsChunk), kXcds);
-        route_colors_kernel<<<chunks, kRouteBlock, 0, s>>>(rgb, colors, n);
+        const uint64_t image_bytes = 3 * static_cast<uint64_t>(width) * static_cast<uint64_t>(height);
+        const bool words = reinterpret_cast<uintptr_t>(rgb) % 4 == 0;
+        route_colors_kernel<<<chunks, kRouteBlock, 0, s>>>(rgb, colors, n, image_bytes, words);
     }
     return check_launch("odie_route");
 }
