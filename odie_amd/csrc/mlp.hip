@@ -394,31 +394,36 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
     }
 }
 
-// dweights[p] = sum over workgroups of partials[b][p] in a fixed order: four lane groups of a
-// 256-thread block take the workgroups b = q, q+4, q+8, ... (q = group), eight loads in flight
-// per step, and the four group sums are added in group order.
+// dweights[p] = sum over workgroups of partials[b][p] in a fixed order: the 16 lane groups of a
+// 1024-thread block take the workgroups b = q, q+16, q+32, ... (q = group), eight loads in
+// flight per step, and the sixteen group sums are added in group order.
 constexpr int kReduceParams = 64;
-__global__ __launch_bounds__(256) void mlp_reduce_kernel(const float* partials, int blocks, int params,
-                                                         float* dweights) {
-    __shared__ float group_sum[4][kReduceParams];
+constexpr int kReduceGroups = 16;
+__global__ __launch_bounds__(kReduceParams * kReduceGroups) void mlp_reduce_kernel(const float* partials, int blocks,
+                                                                                   int params, float* dweights) {
+    __shared__ float group_sum[kReduceGroups][kReduceParams];
     const int local = threadIdx.x % kReduceParams, q = threadIdx.x / kReduceParams;
     const int p = blockIdx.x * kReduceParams + local;
     float total = 0.0f;
     if (p < params) {
         int b = q;
-        for (; b + 28 < blocks; b += 32) {
+        for (; b + 7 * kReduceGroups < blocks; b += 8 * kReduceGroups) {
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = partials[static_cast<int64_t>(b + 4 * j) * params + p];
+            for (int j = 0; j < 8; ++j) v[j] = partials[static_cast<int64_t>(b + kReduceGroups * j) * params + p];
 #pragma unroll
             for (int j = 0; j < 8; ++j) total += v[j];
         }
-        for (; b < blocks; b += 4) total += partials[static_cast<int64_t>(b) * params + p];
+        for (; b < blocks; b += kReduceGroups) total += partials[static_cast<int64_t>(b) * params + p];
     }
     group_sum[q][local] = total;
     __syncthreads();
-    if (q == 0 && p < params)
-        dweights[p] = ((group_sum[0][local] + group_sum[1][local]) + group_sum[2][local]) + group_sum[3][local];
+    if (q == 0 && p < params) {
+        float sum = group_sum[0][local];
+#pragma unroll
+        for (int g = 1; g < kReduceGroups; ++g) sum += group_sum[g][local];
+        dweights[p] = sum;
+    }
 }
 
 int mlp_blocks(int64_t n) {
@@ -496,7 +501,8 @@ int mlp_train(const char* name, const uint16_t* x, int64_t n, int width, int64_t
         }
     }
     if (check_launch(name)) return -1;
-    mlp_reduce_kernel<<<static_cast<uint32_t>((params + kReduceParams - 1) / kReduceParams), 256, 0, s>>>(
+    mlp_reduce_kernel<<<static_cast<uint32_t>((params + kReduceParams - 1) / kReduceParams),
+                        kReduceParams * kReduceGroups, 0, s>>>(
         partials, blocks, static_cast<int>(params), dweights);
     return check_launch((who + " reduce").c_str());
 }
