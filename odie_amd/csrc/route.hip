@@ -344,17 +344,20 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
     int32_t* running = lds + a.experts;    // [experts] ids of each expert placed so far
     Local* local = reinterpret_cast<Local*>(lds + 2 * a.experts);   // [part] offset of position j's id
     // local run starts: exclusive scan over the experts of this sub-chunk's counts (count(e, part)
-    // is the difference of consecutive scanned offsets in expert-major order)
+    // is the difference of consecutive scanned offsets in expert-major order).  The counts are
+    // fetched first, with no dependence between experts, and parked in `running`.
     const int64_t last = static_cast<int64_t>(a.experts) * a.parts - 1;
+#pragma unroll 4
+    for (int e = lane; e < a.experts; e += 64) {
+        const int64_t k = static_cast<int64_t>(e) * a.parts + part;
+        const int32_t next = k < last ? a.counts[k + 1] : static_cast<int32_t>(a.n);
+        running[e] = next - a.counts[k];
+    }
+    __syncthreads();
     int32_t carry = 0;
     for (int e0 = 0; e0 < a.experts; e0 += 64) {
         const int e = e0 + lane;
-        int32_t c = 0;
-        if (e < a.experts) {
-            const int64_t k = static_cast<int64_t>(e) * a.parts + part;
-            const int32_t next = k < last ? a.counts[k + 1] : static_cast<int32_t>(a.n);
-            c = next - a.counts[k];
-        }
+        const int32_t c = e < a.experts ? running[e] : 0;
         int32_t inclusive = c;
         for (int d = 1; d < 64; d <<= 1) {
             const int32_t other = __shfl_up(inclusive, d);
