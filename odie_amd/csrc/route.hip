@@ -326,13 +326,11 @@ __global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t
 // recording only the id's offset inside the sub-chunk; then its lanes take consecutive
 // positions, reload those ids (the sub-chunk's own, from cache), locate them again and store
 // them at consecutive slots.  Same slots as route_scatter_kernel; the stores are whole runs,
-// and with 2 or 4 bytes of LDS per id many waves share a CU.
-template <typename Local>
+// and with 2 bytes of LDS per id many waves share a CU.
 inline size_t staging_bytes(int experts, int part) {
-    return static_cast<size_t>(2) * experts * 4 + static_cast<size_t>(part) * sizeof(Local);
+    return static_cast<size_t>(2) * experts * 4 + static_cast<size_t>(part) * sizeof(uint16_t);
 }
 
-template <typename Local>
 __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
     extern __shared__ int32_t lds[];
     __shared__ Bounds bounds;
@@ -342,7 +340,7 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
     if (part >= a.parts) return;
     int32_t* start = lds;                  // [experts] first local position of each expert's run
     int32_t* running = lds + a.experts;    // [experts] ids of each expert placed so far
-    Local* local = reinterpret_cast<Local*>(lds + 2 * a.experts);   // [part] offset of position j's id
+    uint16_t* local = reinterpret_cast<uint16_t*>(lds + 2 * a.experts);   // [part] offset of position j's id
     // local run starts: exclusive scan over the experts of this sub-chunk's counts (count(e, part)
     // is the difference of consecutive scanned offsets in expert-major order).  The counts are
     // fetched first, with no dependence between experts, and parked in `running`.
@@ -402,7 +400,7 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
             if (valid && rank == 0) running[expert] = base + __popcll(same);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             if (valid) {
-                local[start[expert] + base + rank] = static_cast<Local>(i - begin);
+                local[start[expert] + base + rank] = static_cast<uint16_t>(i - begin);
                 if (a.expert_out) a.expert_out[i] = expert;
             }
         }
@@ -552,19 +550,13 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
         route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
         route_scan_apply_kernel<true><<<sblocks, kScanBlock, 0, s>>>(a);
     }
-    // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU); sub-chunk
-    // offsets take 16 bits up to 2^16 ids.  A stratified batch lists its strata row by row, so
-    // consecutive ids mostly share an expert and the direct scatter's stores already come in runs.
-    const uint32_t staged_blocks = round_up(static_cast<uint32_t>(a.parts), kXcds);
-    const bool fits16 = a.part <= 65536 && staging_bytes<uint16_t>(experts, a.part) + sizeof(Bounds) <= 40 * 1024;
-    const bool fits32 = staging_bytes<int32_t>(experts, a.part) + sizeof(Bounds) <= 40 * 1024;
-    const bool short_offsets = !uniforms && fits16;
-    const bool staged = short_offsets || (!uniforms && fits32);
-    if (short_offsets)
-        route_scatter_staged_kernel<uint16_t>
-            <<<staged_blocks, 64, staging_bytes<uint16_t>(experts, a.part), s>>>(a);
-    else if (staged)
-        route_scatter_staged_kernel<int32_t><<<staged_blocks, 64, staging_bytes<int32_t>(experts, a.part), s>>>(a);
+    // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU; then a
+    // sub-chunk holds at most 2^14 ids, whose offsets take 16 bits).  A stratified batch lists its
+    // strata row by row, so consecutive ids mostly share an expert and the direct scatter's stores
+    // already come in runs.
+    const size_t staging = staging_bytes(experts, a.part);
+    if (!uniforms && staging + sizeof(Bounds) <= 40 * 1024)
+        route_scatter_staged_kernel<<<round_up(static_cast<uint32_t>(a.parts), kXcds), 64, staging, s>>>(a);
     else
         route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     if (colors) {

@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
     (100, 37, 3, 5, 4099),              # ragged tiles, n not a multiple of 64
     (64, 64, 1, 1, 777),                # a single expert
     (7, 5, 2, 2, 1),
+    (4096, 4096, 60, 60, 1 << 23),      # 3600 experts: too many for the staged scatter's LDS
 ])
 def test_route_matches_oracle(width, height, rx, ry, n):
     ids = synth.integers(17, 'ids', n, width * height)
@@ -28,12 +29,20 @@ def test_route_matches_oracle(width, height, rx, ry, n):
     assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
 
 
-@pytest.mark.parametrize('width,height,rx,ry,n', [(2048, 1365, 8, 8, 1 << 18), (100, 37, 3, 5, 4099)])
-def test_route_gathers_slot_colors(width, height, rx, ry, n):
+@pytest.mark.parametrize('width,height,rx,ry,n,offset', [(2048, 1365, 8, 8, 1 << 18, 0), (100, 37, 3, 5, 4099, 0),
+                                                          (100, 37, 3, 5, 4099, 1)])
+def test_route_gathers_slot_colors(width, height, rx, ry, n, offset):
+    """Colors are read in 8-byte windows from a 4-byte aligned image, byte by byte at its last
+    pixels and from an image that starts off a 4-byte boundary (offset 1)."""
     ids = synth.integers(23, 'ids', n, width * height)
     ids[:5] = width * height + np.arange(5)          # past the image: clamped to the last row
+    ids[5:8] = width * height - 1 - np.arange(3)     # the image's last pixels
     image = synth.integers(23, 'image', width * height * 3, 256).astype(np.uint8)
-    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, rgb=torch.from_numpy(image).cuda())
+    buffer = torch.zeros(width * height * 3 + offset, dtype=torch.uint8, device='cuda')
+    rgb = buffer[offset:]
+    rgb.copy_(torch.from_numpy(image))
+    assert rgb.data_ptr() % 4 == offset
+    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, rgb=rgb)
     _, perm, _, _ = oracle.route(ids, width, height, rx, ry)
     clamped = ids.astype(np.uint32).astype(np.int64)
     x, y = clamped % width, np.minimum(clamped // width, height - 1)
