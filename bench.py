@@ -60,6 +60,8 @@ def parse():
     parser.add_argument('--no-cpu', action='store_true')
     parser.add_argument('--no-native', action='store_true', help='skip the 65536-id native step measurement')
     parser.add_argument('--no-single', action='store_true', help='skip the single-expert 2^19-table fwd+bwd line')
+    parser.add_argument('--single-only', action='store_true',
+                        help='print only the single-expert 2^19-table fwd+bwd line (for kernel traces of it)')
     parser.add_argument('--native-steps', type=int, default=200)
     parser.add_argument('--no-reconstruction', action='store_true', help='skip the 32768^2 residual pass')
     parser.add_argument('--reconstruction-batch', type=int, default=1 << 26)
@@ -431,6 +433,9 @@ def main():
         print('bench.py measures one GPU: this build has no multi-GPU path (each GPU would run '
               'its own share of the experts); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
+    if args.single_only:
+        print(json.dumps({'single_expert': single_expert_steps(args.steps)}))
+        return
     import numpy as np
     import torch
     from odie_amd import synth
