@@ -479,6 +479,71 @@ __global__ __launch_bounds__(kBlock) void packed_forward16x2_kernel(PackedArgs a
     reinterpret_cast<uint4*>(a.visibility)[i] = make_uint4(vis[0], vis[1], vis[2], vis[3]);
 }
 
+// packed_forward_kernel for rows of fp16 pairs: every level 2 features at output offset 2l but the
+// last, which may hold one (the reference's F2 layouts with an F1 finest level, rows of align16
+// of the features, PAIRS = width / 2).  The row is kept in registers and written with 16-byte
+// stores, the visibility bytes in 4-byte words where they fall on word boundaries.  Same
+// arithmetic, same bits.
+template <int PAIRS>
+__global__ __launch_bounds__(kBlock) void packed_forward_pairs_kernel(PackedArgs a) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= a.n) return;
+    const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
+    const uint32_t pad = a.pad;
+    uint32_t pairs[PAIRS];
+    uint32_t vis[PAIRS / 4];
+#pragma unroll
+    for (int q = 0; q < PAIRS / 4; ++q) vis[q] = 0;
+#pragma unroll
+    for (int l = 0; l < PAIRS; ++l) {
+        pairs[l] = pad | (pad << 16);
+        if (l < a.levels) {
+            const int32_t* d = a.desc + 8 * l;
+            int cell;
+            float w[4];
+            plane_geometry(p.x, p.y, d[0], cell, w);
+            const bool on = l < a.active && ((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1);
+            vis[l / 4] |= static_cast<uint32_t>(on) << (8 * (l % 4));
+            const bool two = d[5] == 2;
+            __half v0 = __float2half(0.0f), v1 = __float2half(0.0f);
+            if (on) {
+                float2 g[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int64_t at = plane_param(a, d, cell, k, 0);
+                    if (two) {
+                        g[k] = *reinterpret_cast<const float2*>(a.grid + at);
+                    } else {
+                        g[k].x = a.grid[at];
+                        g[k].y = 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const __half wk = __float2half_rn(keep_fp32(w[k]));
+                    v0 = __hfma(wk, __float2half_rn(g[k].x), v0);
+                    v1 = __hfma(wk, __float2half_rn(g[k].y), v1);
+                }
+            }
+            pairs[l] = static_cast<uint32_t>(half_to_bits(v0)) |
+                       ((two ? static_cast<uint32_t>(half_to_bits(v1)) : pad) << 16);
+        }
+    }
+    uint4* row = reinterpret_cast<uint4*>(a.features + static_cast<size_t>(i) * (2 * PAIRS));
+#pragma unroll
+    for (int j = 0; j < PAIRS / 4; ++j) row[j] = make_uint4(pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2], pairs[4 * j + 3]);
+    uint8_t* vrow = a.visibility + static_cast<size_t>(i) * a.levels;
+    if (a.levels % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < PAIRS / 4; ++q)
+            if (4 * q < a.levels) reinterpret_cast<uint32_t*>(vrow)[q] = vis[q];
+    } else {
+#pragma unroll
+        for (int l = 0; l < PAIRS; ++l)
+            if (l < a.levels) vrow[l] = static_cast<uint8_t>(vis[l / 4] >> (8 * (l % 4)));
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void packed_backward_kernel(PackedArgs a) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= a.n) return;
@@ -816,7 +881,8 @@ namespace odie {
 int packed_forward_internal(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
                             const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
                             const int32_t* node_prefix, const uint8_t* bitmap, int width, int active, uint16_t pad,
-                            uint16_t* features, uint8_t* visibility, hipStream_t stream, bool levels16x2) {
+                            uint16_t* features, uint8_t* visibility, hipStream_t stream, bool levels16x2,
+                            bool pairs) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_packed_forward: n must be within [0, 2^31-1]");
     if (levels < 2 || levels > ODIE_MAX_LEVELS) return fail("odie_packed_forward: descriptor must have 2..32 levels");
     if (width < 2 || width > 128) return fail("odie_packed_forward: feature width must be within 2..128");
@@ -841,11 +907,21 @@ int packed_forward_internal(const float* coords, int64_t n, const float* grid, i
     a.active = active;
     a.pad = pad;
     const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
-    if (levels16x2 && levels == 16 && width == 32 && reinterpret_cast<uintptr_t>(features) % 16 == 0 &&
-        reinterpret_cast<uintptr_t>(visibility) % 16 == 0 && reinterpret_cast<uintptr_t>(grid) % 8 == 0)
+    const bool aligned = reinterpret_cast<uintptr_t>(features) % 16 == 0 && reinterpret_cast<uintptr_t>(grid) % 8 == 0;
+    if (levels16x2 && levels == 16 && width == 32 && aligned && reinterpret_cast<uintptr_t>(visibility) % 16 == 0) {
         packed_forward16x2_kernel<<<blocks, kBlock, 0, stream>>>(a);
-    else
+    } else if (pairs && aligned && reinterpret_cast<uintptr_t>(visibility) % 4 == 0 && width % 16 == 0 &&
+               width >= 2 * levels && width <= 80) {
+        switch (width / 2) {
+            case 8: packed_forward_pairs_kernel<8><<<blocks, kBlock, 0, stream>>>(a); break;
+            case 16: packed_forward_pairs_kernel<16><<<blocks, kBlock, 0, stream>>>(a); break;
+            case 24: packed_forward_pairs_kernel<24><<<blocks, kBlock, 0, stream>>>(a); break;
+            case 32: packed_forward_pairs_kernel<32><<<blocks, kBlock, 0, stream>>>(a); break;
+            default: packed_forward_pairs_kernel<40><<<blocks, kBlock, 0, stream>>>(a); break;
+        }
+    } else {
         packed_forward_kernel<<<blocks, kBlock, 0, stream>>>(a);
+    }
     return check_launch("odie_packed_forward");
 }
 

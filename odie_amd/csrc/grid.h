@@ -189,10 +189,13 @@ int grid_backward_adam_planes_internal(const float* coords, int64_t n, const int
 // The packed-plane forward with the native step's active prefix (levels >= active are off)
 // and the fp16 bits written past the last level (the runtime pads with 1.0).  levels16x2: the
 // caller guarantees 16 levels of 2 features at output offsets 2l (the faster kernel applies).
+// pairs: the caller guarantees 2 features at output offset 2l for every level but the last,
+// which has 1 or 2 (the pairs kernel applies when the row is a multiple of 16 columns).
 int packed_forward_internal(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
                             const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
                             const int32_t* node_prefix, const uint8_t* bitmap, int width, int active, uint16_t pad,
-                            uint16_t* features, uint8_t* visibility, hipStream_t stream, bool levels16x2 = false);
+                            uint16_t* features, uint8_t* visibility, hipStream_t stream, bool levels16x2 = false,
+                            bool pairs = false);
 
 
 }  // namespace odie

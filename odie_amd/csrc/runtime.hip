@@ -278,6 +278,7 @@ struct Runtime {
     int raw_width = 0, row = 0;       // RAW = sum of the levels' features, W = align16(RAW)
     std::vector<int32_t> features;    // F of each level (the descriptors' column 5)
     bool levels16x2 = false;          // 16 levels x 2 features in level order (the forward's fast path)
+    bool pairs = false;               // 2 features per level but the last (1 or 2): rows of fp16 pairs
     int active = 0, coarse = 0, softplus = 0;
     float grid_lr = 0.0f;
     // packed planes (odie/model.py:100-101)
@@ -394,6 +395,8 @@ Runtime::Runtime(const Json& j)
     row = align16(raw_width);
     if (row > kMaxRow) throw std::runtime_error("the levels' features exceed 80 columns");
     levels16x2 = levels == 16 && row == 32 && raw_width == 32;
+    pairs = !features.empty() && (features.back() == 1 || features.back() == 2);
+    for (size_t l = 0; l + 1 < features.size(); ++l) pairs = pairs && features[l] == 2;
     xy.allocate(2 * kBatch);
     if (!rgb8) target.allocate(3 * kBatch);
     colors.allocate(kBatch);
@@ -501,7 +504,7 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
         }
     } else {
         call(packed_forward_internal(xy.data, n, grid, total, desc, levels, bits, prefix, cells, row, active, 0x3C00,
-                                     raw.data, vis.data, stream, levels16x2));
+                                     raw.data, vis.data, stream, levels16x2, pairs));
     }
     const uint16_t* inputs = raw.data;
     if (gate) {
