@@ -32,7 +32,7 @@ RESOLUTIONS = [4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128]
 # level rows of the reference's own configurations: DIV2K (odie/config.py:129, configs/baselines/
 # odie_div2k.json: [2]*15 + [1]) and the level ablations (configs/ablations/div2k_L8/L12/L20.json)
 SHAPES = {'16x2': [2] * 16, 'div2k': [2] * 15 + [1], 'L8': [2] * 7 + [1], 'L12': [2] * 11 + [1],
-          'L20': [2] * 19 + [1]}
+          'L20': [2] * 19 + [1], '12x2': [2] * 12}
 
 
 def _resolutions(levels):
@@ -206,7 +206,8 @@ def test_hash_step_matches_composition(router, coarse, activation, levels, featu
                                                       (True, 12, True, '16x2'), (False, 9, False, '16x2'),
                                                       (True, 16, True, 'div2k'), (True, 11, True, 'div2k'),
                                                       (True, 8, True, 'L8'), (True, 12, True, 'L12'),
-                                                      (True, 20, True, 'L20'), (False, 17, True, 'L20')])
+                                                      (True, 20, True, 'L20'), (False, 17, True, 'L20'),
+                                                      (True, 12, True, '12x2'), (True, 9, True, '12x2')])
 def test_packed_step_matches_composition(router, active, half, shape):
     width, height = 83, 64
     dims = SHAPES[shape]
