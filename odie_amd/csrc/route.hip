@@ -439,9 +439,9 @@ __global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
 }
 
 int route_plan(int64_t n, int experts, int& part, int& parts) {
-    // Sub-chunks of at least 1024 ids, few enough that experts*parts stays <= 2^22 (16 MiB of
-    // counts): with many experts a sub-chunk stays short enough to keep every CU busy.
-    int64_t p = 1024;
+    // Sub-chunks of at least 512 ids, few enough that experts*parts stays <= 2^22 (16 MiB of
+    // counts): a wave walks its sub-chunk serially, so short ones keep more waves on every CU.
+    int64_t p = 512;
     while ((n + p - 1) / p * experts > (int64_t{1} << 22)) p *= 2;
     part = static_cast<int>(p);
     parts = static_cast<int>((n + p - 1) / p);
