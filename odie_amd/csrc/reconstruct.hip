@@ -79,7 +79,7 @@ __device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const _
     const uint32_t x = id % a.width;
     uint32_t y = id / a.width;
     if (y >= a.height) y = a.height - 1;
-    const int tx = tile_of(tb.x0, a.regions_x, tb.sx, x), ty = tile_of(tb.y0, a.regions_y, tb.sy, y);
+    const int tx = tile_of(a.regions_x, a.width, tb.sx, x), ty = tile_of(a.regions_y, a.height, tb.sy, y);
     const int t = ty * a.regions_x + tx;
     int slot = a.slots ? a.slots[t] : t;
     if (slot >= a.experts || !valid) slot = -1;

@@ -84,8 +84,8 @@ __device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t i
     x = id % a.width;
     y = id / a.width;
     if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
-    rx = tile_of(b.x0, a.regions_x, a.sx, x);
-    ry = tile_of(b.y0, a.regions_y, a.sy, y);
+    rx = tile_of(a.regions_x, a.width, a.sx, x);
+    ry = tile_of(a.regions_y, a.height, a.sy, y);
     expert = ry * a.regions_x + rx;
 }
 
@@ -320,122 +320,226 @@ __global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t
     }
 }
 
-// The scatter with one wave per block staging its sub-chunk in LDS.  The wave first places
-// every id of its sub-chunk at its position inside the sub-chunk's expert-ordered output (the
-// run of expert e starts at the sum of the sub-chunk's counts of the experts before e),
-// recording only the id's offset inside the sub-chunk; then its lanes take consecutive
-// positions, reload those ids (the sub-chunk's own, from cache), locate them again and store
-// them at consecutive slots.  Same slots as route_scatter_kernel; the stores are whole runs,
-// and with 2 bytes of LDS per id many waves share a CU.
-inline size_t staging_bytes(int experts, int part) {
-    return static_cast<size_t>(2) * experts * 4 + static_cast<size_t>(part) * sizeof(uint16_t);
+// The scatter with a block of W waves staging a group of consecutive sub-chunks in LDS.  The
+// sub-chunks' runs of one expert are consecutive in the output (the scanned counts are
+// expert-major, then sub-chunk order), so the group's ids form one run per expert.  The block
+//   1. copies the group's pixel ids (32 bits each) into LDS with coalesced loads;
+//   2. cuts the group into W slices, one per wave, and each wave locates the ids of its slice,
+//      keeps each id's expert and counts its slice's ids per expert;
+//   3. scans those counts (expert-major, then slice order) into each slice's first position
+//      for each expert inside the group's expert-ordered output;
+//   4. each wave places the ids of its slice in order (lanes sharing an expert take their order
+//      from ballots), recording only the id's offset inside the group;
+//   5. the block's lanes take consecutive positions, fetch those ids from LDS, locate them
+//      again and store them at consecutive slots of the output.
+// Same slots as route_scatter_kernel; the stores are whole runs, the ids are read from memory
+// once, and the serial placement is split W ways.
+constexpr int kStagedMaxWaves = 8;
+
+inline size_t staging_bytes(int experts, int part, int waves, int group) {
+    return static_cast<size_t>(4) * experts * (1 + waves) + static_cast<size_t>(8) * part * group;
 }
 
-__global__ __launch_bounds__(64) void route_scatter_staged_kernel(RouteArgs a) {
+template <int W>
+__global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs a, int group) {
     extern __shared__ int32_t lds[];
     __shared__ Bounds bounds;
+    __shared__ int32_t wave_sums[W];
     load_bounds(a, bounds);
-    const int lane = threadIdx.x;
-    const int part = static_cast<int>(xcd_major(blockIdx.x, gridDim.x));
-    if (part >= a.parts) return;
-    int32_t* start = lds;                  // [experts] first local position of each expert's run
-    int32_t* running = lds + a.experts;    // [experts] ids of each expert placed so far
-    uint16_t* local = reinterpret_cast<uint16_t*>(lds + 2 * a.experts);   // [part] offset of position j's id
-    // local run starts: exclusive scan over the experts of this sub-chunk's counts (count(e, part)
-    // is the difference of consecutive scanned offsets in expert-major order).  The counts are
-    // fetched first, with no dependence between experts, and parked in `running`.
-    const int64_t last = static_cast<int64_t>(a.experts) * a.parts - 1;
-#pragma unroll 4
-    for (int e = lane; e < a.experts; e += 64) {
-        const int64_t k = static_cast<int64_t>(e) * a.parts + part;
-        const int32_t next = k < last ? a.counts[k + 1] : static_cast<int32_t>(a.n);
-        running[e] = next - a.counts[k];
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int first = static_cast<int>(xcd_major(blockIdx.x, gridDim.x)) * group;   // the group's first sub-chunk
+    if (first >= a.parts) return;
+    const int members = a.parts - first < group ? a.parts - first : group;
+    const int64_t group_begin = static_cast<int64_t>(first) * a.part;
+    const int64_t group_end = group_begin + static_cast<int64_t>(members) * a.part;
+    const int32_t count = static_cast<int32_t>((group_end < a.n ? group_end : a.n) - group_begin);
+    const int experts = a.experts;
+    const int32_t ids_cap = group * a.part;
+    int32_t* base = lds;                                                   // [experts]
+    uint32_t* hist = reinterpret_cast<uint32_t*>(lds + experts);           // [W][experts]
+    uint32_t* held = hist + W * experts;                                   // [ids_cap] the group's ids
+    uint16_t* tag = reinterpret_cast<uint16_t*>(held + ids_cap);           // [ids_cap] expert of id j
+    uint16_t* local = tag + ids_cap;                                       // [ids_cap] offset of position j's id
+    // base[e] = slot of the group's first id of expert e: the scanned count of (e, first)
+    for (int e = tid; e < experts; e += 64 * W) {
+        base[e] = a.counts[static_cast<int64_t>(e) * a.parts + first];
+#pragma unroll
+        for (int w = 0; w < W; ++w) hist[w * experts + e] = 0u;
+    }
+    for (int32_t j0 = 0; j0 < count; j0 += 64 * W * 2 * kAhead) {
+        uint32_t ids[2 * kAhead];
+#pragma unroll
+        for (int k = 0; k < 2 * kAhead; ++k) {
+            const int32_t j = j0 + k * 64 * W + tid;
+            ids[k] = j < count ? pixel_id(a, group_begin + j) : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < 2 * kAhead; ++k) {
+            const int32_t j = j0 + k * 64 * W + tid;
+            if (j < count) held[j] = ids[k];
+        }
     }
     __syncthreads();
-    int32_t carry = 0;
-    for (int e0 = 0; e0 < a.experts; e0 += 64) {
-        const int e = e0 + lane;
-        const int32_t c = e < a.experts ? running[e] : 0;
-        int32_t inclusive = c;
+    // slices of whole groups of 64 ids
+    const int32_t slice = ((count + W - 1) / W + 63) / 64 * 64;
+    const int32_t begin = wave * slice < count ? wave * slice : count;
+    const int32_t end = begin + slice < count ? begin + slice : count;
+    uint32_t* mine = hist + wave * experts;
+    for (int32_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
+        uint32_t ids[kAhead];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int32_t j = ahead + k * 64 + lane;
+            ids[k] = held[j < end ? j : end - 1];
+        }
+        int tags[kAhead];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            int rx, ry;
+            uint32_t x, y;
+            locate_id(a, bounds, ids[k], tags[k], x, y, rx, ry);
+        }
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+            const int32_t j = ahead + k * 64 + lane;
+            if (j < end) {
+                tag[j] = static_cast<uint16_t>(tags[k]);
+                atomicAdd(&mine[tags[k]], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    // exclusive scan over (expert, slice): thread t takes experts [t*per, (t+1)*per)
+    {
+        const int per = (experts + 64 * W - 1) / (64 * W);
+        int32_t sum = 0;
+        for (int q = 0; q < per; ++q) {
+            const int e = tid * per + q;
+            if (e < experts) {
+#pragma unroll
+                for (int w = 0; w < W; ++w) sum += static_cast<int32_t>(hist[w * experts + e]);
+            }
+        }
+        int32_t inclusive = sum;
         for (int d = 1; d < 64; d <<= 1) {
             const int32_t other = __shfl_up(inclusive, d);
             if (lane >= d) inclusive += other;
         }
-        if (e < a.experts) {
-            start[e] = carry + inclusive - c;
-            running[e] = 0;
+        if (lane == 63) wave_sums[wave] = inclusive;
+        __syncthreads();
+        int32_t at = inclusive - sum;
+        for (int w = 0; w < wave; ++w) at += wave_sums[w];
+        for (int q = 0; q < per; ++q) {
+            const int e = tid * per + q;
+            if (e < experts) {
+                base[e] -= at;
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const int32_t c = static_cast<int32_t>(hist[w * experts + e]);
+                    hist[w * experts + e] = static_cast<uint32_t>(at);
+                    at += c;
+                }
+            }
         }
-        carry += __shfl(inclusive, 63);
     }
     __syncthreads();
-    const int64_t begin = static_cast<int64_t>(part) * a.part;
-    const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
-    const uint64_t below = (uint64_t{1} << lane) - 1;
-    for (int64_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
-        uint32_t ids[kAhead];
+    {
+        const uint64_t below = (uint64_t{1} << lane) - 1;
+        for (int32_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
+            int tags[kAhead];
 #pragma unroll
-        for (int k = 0; k < kAhead; ++k) {
-            const int64_t i = ahead + k * 64 + lane;
-            ids[k] = i < end ? pixel_id(a, i) : 0u;
-        }
+            for (int k = 0; k < kAhead; ++k) {
+                const int32_t j = ahead + k * 64 + lane;
+                const int t = static_cast<int>(tag[j < end ? j : end - 1]);
+                tags[k] = j < end ? t : -1;
+            }
+            // lanes sharing an expert, for the kAhead groups at once (independent ballots)
+            uint64_t same[kAhead];
 #pragma unroll
-        for (int k = 0; k < kAhead; ++k) {
-            const int64_t i = ahead + k * 64 + lane;
-            const bool valid = i < end;
-            int expert = -1, rx = 0, ry = 0;
-            uint32_t x = 0, y = 0;
-            if (valid) locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
-            uint64_t same = __ballot(valid);
+            for (int k = 0; k < kAhead; ++k) same[k] = __ballot(tags[k] >= 0);
             for (int bit = 0; bit < a.expert_bits; ++bit) {
-                const uint64_t ones = __ballot(valid && ((expert >> bit) & 1));
-                same &= ((expert >> bit) & 1) ? ones : ~ones;
+#pragma unroll
+                for (int k = 0; k < kAhead; ++k) {
+                    const bool one = (tags[k] >> bit) & 1;
+                    const uint64_t ones = __ballot(tags[k] >= 0 && one);
+                    same[k] &= one ? ones : ~ones;
+                }
             }
-            int32_t base = 0, rank = 0;
-            if (valid) {
-                rank = __popcll(same & below);
-                base = running[expert];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            if (valid && rank == 0) running[expert] = base + __popcll(same);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (valid) {
-                local[start[expert] + base + rank] = static_cast<uint16_t>(i - begin);
-                if (a.expert_out) a.expert_out[i] = expert;
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) {
+                const int32_t j = ahead + k * 64 + lane;
+                const bool valid = j < end;
+                const int expert = tags[k];
+                int32_t position = 0, rank = 0;
+                if (valid) {
+                    rank = __popcll(same[k] & below);
+                    position = static_cast<int32_t>(mine[expert]);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                if (valid && rank == 0) mine[expert] = static_cast<uint32_t>(position + __popcll(same[k]));
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (valid) {
+                    local[position + rank] = static_cast<uint16_t>(j);
+                    if (a.expert_out) a.expert_out[group_begin + j] = expert;
+                }
             }
         }
     }
     __syncthreads();
-    // global slot of local position j of expert e's run: counts(e, part) - start[e] + j
-    for (int e = lane; e < a.experts; e += 64) start[e] = a.counts[static_cast<int64_t>(e) * a.parts + part] - start[e];
-    __syncthreads();
-    const int32_t count = static_cast<int32_t>(end - begin);
-    for (int32_t j0 = 0; j0 < count; j0 += 64 * kAhead) {
+    for (int32_t j0 = 0; j0 < count; j0 += 64 * W * kAhead) {
         int32_t at[kAhead];
         uint32_t ids[kAhead];
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
-            const int32_t j = j0 + k * 64 + lane;
-            at[k] = j < count ? static_cast<int32_t>(local[j]) : 0;
+            const int32_t j = j0 + k * 64 * W + tid;
+            at[k] = static_cast<int32_t>(local[j < count ? j : count - 1]);
         }
 #pragma unroll
-        for (int k = 0; k < kAhead; ++k) ids[k] = j0 + k * 64 + lane < count ? pixel_id(a, begin + at[k]) : 0u;
+        for (int k = 0; k < kAhead; ++k) ids[k] = held[at[k]];
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
-            const int32_t j = j0 + k * 64 + lane;
-            if (j >= count) continue;
+            const int32_t j = j0 + k * 64 * W + tid;
             int expert, rx, ry;
             uint32_t x, y;
             locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
-            const int64_t slot = static_cast<int64_t>(start[expert]) + j;
-            a.perm[slot] = static_cast<int32_t>(begin + at[k]);
-            const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
-            const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
-            reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
-            // the pixel's index for route_colors_kernel
-            if (a.colors) a.colors[slot] = y * a.width + x;
+            if (j < count) {
+                const int64_t slot = static_cast<int64_t>(base[expert]) + j;
+                a.perm[slot] = static_cast<int32_t>(group_begin + at[k]);
+                const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
+                const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
+                reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
+                // the pixel's index for route_colors_kernel
+                if (a.colors) a.colors[slot] = y * a.width + x;
+            }
         }
     }
+}
+
+// Waves per staged-scatter block and sub-chunks per group: 8 waves if the staging of one
+// sub-chunk then fits the LDS budget (two blocks per CU), else 4; and the most sub-chunks, up to
+// 8, that still fit.  waves = 0 when not even one sub-chunk with 4 waves fits.
+constexpr size_t kStagingBudget = 72 * 1024;
+
+void staged_shape(int experts, int part, int& waves, int& group) {
+    const size_t budget = kStagingBudget - sizeof(Bounds) - kStagedMaxWaves * 4;
+    for (waves = kStagedMaxWaves; waves >= 4; waves /= 2)
+        for (group = 8; group >= 1; group /= 2)
+            if (staging_bytes(experts, part, waves, group) <= budget) return;
+    waves = 0;
+    group = 0;
+}
+
+template <int W>
+int launch_staged(const RouteArgs& a, int group, hipStream_t s) {
+    const uint32_t groups = round_up(static_cast<uint32_t>((a.parts + group - 1) / group), kXcds);
+    const size_t staging = staging_bytes(a.experts, a.part, W, group);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(route_scatter_staged_kernel<W>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(staging)) != hipSuccess)
+        return fail("odie_route: LDS attribute of the staged scatter");
+    route_scatter_staged_kernel<W><<<groups, 64 * W, staging, s>>>(a, group);
+    return 0;
 }
 
 int route_plan(int64_t n, int experts, int& part, int& parts) {
@@ -550,15 +654,16 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
         route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
         route_scan_apply_kernel<true><<<sblocks, kScanBlock, 0, s>>>(a);
     }
-    // staged scatter when a sub-chunk's staging fits 40 KB of LDS (several waves per CU; then a
-    // sub-chunk holds at most 2^14 ids, whose offsets take 16 bits).  A stratified batch lists its
+    // staged scatter when a group's staging fits the LDS budget.  A stratified batch lists its
     // strata row by row, so consecutive ids mostly share an expert and the direct scatter's stores
     // already come in runs.
-    const size_t staging = staging_bytes(experts, a.part);
-    if (!uniforms && staging + sizeof(Bounds) <= 40 * 1024)
-        route_scatter_staged_kernel<<<round_up(static_cast<uint32_t>(a.parts), kXcds), 64, staging, s>>>(a);
-    else
+    int waves = 0, group = 0;
+    staged_shape(experts, a.part, waves, group);
+    if (!uniforms && waves > 0) {
+        if ((waves == 8 ? launch_staged<8>(a, group, s) : launch_staged<4>(a, group, s)) != 0) return -1;
+    } else {
         route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
+    }
     if (colors) {
         const uint32_t chunks = round_up(static_cast<uint32_t>((n + kColorsChunk - 1) / kColorsChunk), kXcds);
         const uint64_t image_bytes = 3 * static_cast<uint64_t>(width) * static_cast<uint64_t>(height);

@@ -37,13 +37,15 @@ inline void make_tile_bounds(int width, int height, int regions_x, int regions_y
 // floor(v * regions / extent) (bounds[r] <= v iff r * extent <= v * regions for integer v),
 // capped at regions - 1.  The fp32 estimate v * scale (scale = fp32(regions / extent)) is within
 // 2^-16 of v * regions / extent for r < 64, so its floor is off by at most one, either way: one
-// comparison with the neighbouring bound fixes it.
-__device__ inline int tile_of(const int32_t* bounds, int regions, float scale, uint32_t v) {
+// comparison of exact 64-bit products each way fixes it, with no table and no branch.
+__device__ inline int tile_of(int regions, uint32_t extent, float scale, uint32_t v) {
     int r = static_cast<int>(static_cast<float>(v) * scale);
     r = r < 0 ? 0 : (r > regions - 1 ? regions - 1 : r);
-    if (r + 1 < regions && static_cast<uint32_t>(bounds[r + 1]) <= v) ++r;
-    else if (r > 0 && static_cast<uint32_t>(bounds[r]) > v) --r;
-    return r;
+    const uint32_t ur = static_cast<uint32_t>(r);
+    const uint64_t scaled = static_cast<uint64_t>(v) * static_cast<uint32_t>(regions);
+    const bool up = (ur + 1 < static_cast<uint32_t>(regions)) & (static_cast<uint64_t>(ur + 1) * extent <= scaled);
+    const bool down = static_cast<uint64_t>(ur) * extent > scaled;
+    return r + static_cast<int>(up) - static_cast<int>(down);
 }
 
 }  // namespace odie
