@@ -12,11 +12,11 @@
 // in their original order inside each expert (numpy argsort(kind='stable') order, the tie
 // rule the reference uses for rankings, odie/selection.py:116).
 //   pass 1  each wave counts the experts of its own sub-chunk (LDS histogram per wave)
-//   pass 2  one workgroup scans the counts, expert-major then sub-chunk order
-//   pass 3  each wave walks its sub-chunk 64 ids at a time; lanes sharing an expert get
-//           their order from a ballot over the wave (peel loop, one iteration per distinct
-//           expert in the group), and a per-wave running count in LDS carries the order
-//           across groups.  No global atomics, so the result is deterministic.
+//   pass 2  a parallel scan of the counts, expert-major then sub-chunk order
+//   pass 3  the scatter: lanes sharing an expert get their order from one ballot per bit of
+//           the expert id, a running count in LDS carries it across groups of 64, and the
+//           staged form writes each expert's run of a group of sub-chunks out in one piece.
+//           No global atomics, so the result is deterministic.
 #include <map>
 #include <mutex>
 #include <string>
@@ -114,15 +114,14 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
 #pragma unroll
             for (int k = 0; k < kAhead; ++k) {
                 const int64_t i = g + k * 64 + lane;
-                id[k] = i < end ? pixel_id(a, i) : 0u;
+                id[k] = pixel_id(a, i < end ? i : end - 1);
             }
 #pragma unroll
             for (int k = 0; k < kAhead; ++k) {
-                if (g + k * 64 + lane >= end) continue;
                 int expert, rx, ry;
                 uint32_t x, y;
                 locate_id(a, bounds, id[k], expert, x, y, rx, ry);
-                atomicAdd(mine + expert, 1);
+                if (g + k * 64 + lane < end) atomicAdd(mine + expert, 1);
             }
         }
     }

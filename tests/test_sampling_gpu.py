@@ -24,6 +24,22 @@ def test_stratified_ids_match_the_oracle(shape, batch):
     assert ids.min() >= 0 and ids.max() < shape[0] * shape[1]
 
 
+def test_stratified_ids_clamp_out_of_range_draws():
+    """Uniforms outside [0, 1), pixel coordinates beyond the int32 range included: the
+    truncation saturates and the clamps put the pixel on the image's border, as the oracle's
+    64-bit truncation and clamps do; a NaN lands on 0 in both.  (Coordinates beyond the int64
+    range are left out: a float -> int64 conversion out of range differs between platforms.)"""
+    shape, batch = (1365, 2048), 64
+    uniforms = torch.rand((batch, 2), device='cuda', generator=torch.Generator(device='cuda').manual_seed(5))
+    odd = torch.tensor([[-3.0, 2.5], [1e10, -1e10], [-0.4, 0.999], [1e14, -1e14], [float('nan'), 0.5],
+                        [0.5, float('nan')], [-1e-30, 1.0]], device='cuda')
+    uniforms[:odd.shape[0]] = odd
+    ids = stratified_ids(uniforms, shape).cpu().numpy()
+    with np.errstate(invalid='ignore'):
+        expected = oracle.stratified_ids(uniforms.cpu().numpy(), shape[1], shape[0])
+    assert np.array_equal(ids, expected)
+
+
 def test_stratified_rejects_non_square_batches():
     with pytest.raises(RuntimeError, match='square power-of-two'):
         stratified_ids(torch.rand((8, 2), device='cuda'), (10, 10))
