@@ -90,14 +90,15 @@ __device__ inline uint32_t pick4(const uint4& v, uint32_t j) {
 }
 
 template <int F, bool HALF, int LMAX>
-__device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, const uint32_t* staged, int64_t i) {
+__device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, const Elem<HALF>* table,
+                                  const uint32_t* staged, int64_t i) {
     using T = Elem<HALF>;
     const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
     T vals[LMAX * F];
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) {
         if (l < a.n_levels) {
-            const DevLevel& lv = a.level[l];
+            const DevLevel lv = levels[l];
             uint32_t idx[4];
             float w[4];
             grid_corners(lv, p.x, p.y, idx, w);
@@ -202,6 +203,15 @@ __device__ inline void encode_row(const GridArgs& a, const Elem<HALF>* table, co
 
 template <int F, bool HALF, int LMAX>
 __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
+    // The level descriptors are read from an LDS copy: taken from the kernel arguments, sixteen
+    // levels' descriptors would be held in scalar registers across the whole unrolled row and
+    // spilled, and every basic block of the row would reload them lane by lane.
+    __shared__ DevLevel levels[LMAX];
+    constexpr int kLevelWords = LMAX * static_cast<int>(sizeof(DevLevel) / 4);
+    static_assert(kLevelWords <= kBlock, "one thread per descriptor word");
+    if (static_cast<int>(threadIdx.x) < kLevelWords)
+        reinterpret_cast<uint32_t*>(levels)[threadIdx.x] = reinterpret_cast<const uint32_t*>(a.level)[threadIdx.x];
+    __syncthreads();
     const uint32_t block = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
     int64_t begin = static_cast<int64_t>(block) * a.chunk;
     if (begin >= a.n) return;
@@ -218,7 +228,7 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
             for (int j = threadIdx.x; j < a.stage_entries / 4; j += kBlock) reinterpret_cast<uint4*>(staged)[j] = src[j];
             __syncthreads();
         }
-        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) encode_row<F, HALF, LMAX>(a, table, staged, i);
+        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) encode_row<F, HALF, LMAX>(a, levels, table, staged, i);
         begin = stop;
     }
 }
