@@ -34,8 +34,30 @@ __device__ inline uint32_t wrap_index(uint32_t v, const DevLevel& lv) {
     return v < lv.size ? v : v % lv.size;
 }
 
+// The four corner indices of one level reduced mod the table size (wrap_index on each): a mask
+// for power-of-two tables; otherwise one conditional subtraction, and the remainder only when a
+// lane's index is still out of range after it (coordinates far off the unit square).
+__device__ inline void wrap_corners(uint32_t idx[4], const DevLevel& lv) {
+    if (lv.mask) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) idx[k] &= lv.mask;
+        return;
+    }
+    bool far = false;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        idx[k] = idx[k] >= lv.size ? idx[k] - lv.size : idx[k];
+        far |= idx[k] >= lv.size;
+    }
+    if (far) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) idx[k] = idx[k] < lv.size ? idx[k] : idx[k] % lv.size;
+    }
+}
+
 // tiny-cuda-nn grid geometry: p = fma(scale, x, 0.5), corner = floor(p), fraction p - floor(p);
 // corners (0,0),(1,0),(0,1),(1,1); dense index x + y*res, hashed x ^ y*2654435761, mod size.
+// The row terms are formed once per row of corners.
 __device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32_t idx[4], float w[4]) {
     const float px = __builtin_fmaf(lv.scale, x, 0.5f);
     const float py = __builtin_fmaf(lv.scale, y, 0.5f);
@@ -47,12 +69,20 @@ __device__ inline void grid_corners(const DevLevel& lv, float x, float y, uint32
     w[1] = fx * (1.0f - fy);
     w[2] = (1.0f - fx) * fy;
     w[3] = fx * fy;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t cx = gx + static_cast<uint32_t>(k & 1), cy = gy + static_cast<uint32_t>(k >> 1);
-        const uint32_t raw = lv.hashed ? (cx ^ hash_row(cy, lv)) : (cx + cy * lv.res);
-        idx[k] = wrap_index(raw, lv);
+    if (lv.hashed) {
+        const uint32_t h0 = hash_row(gy, lv), h1 = hash_row(gy + 1u, lv);
+        idx[0] = gx ^ h0;
+        idx[1] = (gx + 1u) ^ h0;
+        idx[2] = gx ^ h1;
+        idx[3] = (gx + 1u) ^ h1;
+    } else {
+        const uint32_t base = gx + gy * lv.res;
+        idx[0] = base;
+        idx[1] = base + 1u;
+        idx[2] = base + lv.res;
+        idx[3] = base + lv.res + 1u;
     }
+    wrap_corners(idx, lv);
 }
 
 // One fp16 level of 2 features: acc = fma(fp16(w_k), entry_k, acc) over the corners in order,
