@@ -42,21 +42,16 @@ struct ReconArgs {
     DevLevel level[kLevels];
 };
 
-__device__ inline DevLevel pick(const DevLevel& first, const DevLevel& second, bool take_second) {
-    DevLevel d;
-    d.scale = take_second ? second.scale : first.scale;
-    d.res = take_second ? second.res : first.res;
-    d.size = take_second ? second.size : first.size;
-    d.mask = take_second ? second.mask : first.mask;
-    d.offset = take_second ? second.offset : first.offset;
-    d.hashed = take_second ? second.hashed : first.hashed;
-    d.prime = take_second ? second.prime : first.prime;
-    return d;
-}
-
-// Per-block copies of the decoder's forward weights and the tile bounds.
-__device__ inline void stage_model(const ReconArgs& a, const TileBounds& bounds, _Float16* w, TileBounds& tb) {
+// Per-block copies of the decoder's forward weights, the tile bounds and the level descriptors
+// (read from LDS, the descriptors stay out of the scalar registers the unrolled levels would
+// otherwise spill).
+__device__ inline void stage_model(const ReconArgs& a, const TileBounds& bounds, _Float16* w, TileBounds& tb,
+                                   DevLevel* levels) {
     stage_forward_weights<2>(a.weights, w);
+    constexpr int kLevelWords = kLevels * static_cast<int>(sizeof(DevLevel) / 4);
+    static_assert(kLevelWords <= kReconBlock, "one thread per descriptor word");
+    if (static_cast<int>(threadIdx.x) < kLevelWords)
+        reinterpret_cast<uint32_t*>(levels)[threadIdx.x] = reinterpret_cast<const uint32_t*>(a.level)[threadIdx.x];
     for (int j = threadIdx.x; j <= kMaxTiles; j += kReconBlock) {
         tb.x0[j] = bounds.x0[j];
         tb.y0[j] = bounds.y0[j];
@@ -74,7 +69,8 @@ __device__ inline void stage_model(const ReconArgs& a, const TileBounds& bounds,
 
 // The wave's 32 pixels (pixel s of lane (g, s) is `id`, `valid` when it is real): the encode of
 // lane (g, s)'s eight levels (pairs) and the decoder output rows of lane group g (out).
-__device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const _Float16* w, uint32_t id, bool valid,
+__device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const DevLevel* levels, const _Float16* w,
+                               uint32_t id, bool valid,
                                int g, int s, uint32_t pairs[2][4], half8& out) {
     const uint32_t x = id % a.width;
     uint32_t y = id / a.width;
@@ -90,8 +86,8 @@ __device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const _
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            // both half-waves' levels are read with uniform indices, then selected per lane
-            const DevLevel lv = pick(a.level[8 * kt + j], a.level[8 * kt + 4 + j], g != 0);
+            // lane group g encodes level 8kt + 4g + j
+            const DevLevel lv = levels[8 * kt + 4 * g + j];
             uint32_t idx[4];
             float wk[4];
             grid_corners(lv, u, v, idx, wk);
@@ -122,7 +118,8 @@ __device__ inline void rgb_of(const half8& out, float& r, float& gr, float& b) {
 __global__ __launch_bounds__(kReconBlock) void reconstruct_kernel(ReconArgs a, TileBounds bounds) {
     __shared__ _Float16 w[kForwardHalfs];
     __shared__ TileBounds tb;
-    stage_model(a, bounds, w, tb);
+    __shared__ DevLevel levels[kLevels];
+    stage_model(a, bounds, w, tb, levels);
     const int lane = threadIdx.x % 64, g = lane / 32, s = lane % 32;
     const int64_t tiles = (a.n + 31) / 32;
     const int64_t waves = static_cast<int64_t>(gridDim.x) * kReconWaves;
@@ -132,7 +129,7 @@ __global__ __launch_bounds__(kReconBlock) void reconstruct_kernel(ReconArgs a, T
         const bool valid = row < a.n;
         uint32_t pairs[2][4];
         half8 out;
-        predict(a, tb, w, static_cast<uint32_t>(a.begin + (valid ? row : 0)), valid, g, s, pairs, out);
+        predict(a, tb, levels, w, static_cast<uint32_t>(a.begin + (valid ? row : 0)), valid, g, s, pairs, out);
         if (!valid) continue;
         if (a.features) {
 #pragma unroll
@@ -176,7 +173,8 @@ __device__ inline double lane_double(double value, int lane) {
 __global__ __launch_bounds__(kReconBlock) void score_kernel(ReconArgs a, TileBounds bounds, ScoreArgs sc) {
     __shared__ _Float16 w[kForwardHalfs];
     __shared__ TileBounds tb;
-    stage_model(a, bounds, w, tb);
+    __shared__ DevLevel levels[kLevels];
+    stage_model(a, bounds, w, tb, levels);
     const int lane = threadIdx.x % 64, g = lane / 32, s = lane % 32;
     const int cells = sc.resolution * sc.resolution;
     const float inv255 = 1.0f / 255.0f;
@@ -192,7 +190,7 @@ __global__ __launch_bounds__(kReconBlock) void score_kernel(ReconArgs a, TileBou
                 const uint32_t id = static_cast<uint32_t>(y) * a.width + static_cast<uint32_t>(xs + (valid ? s : 0));
                 uint32_t pairs[2][4];
                 half8 out;
-                predict(a, tb, w, id, valid, g, s, pairs, out);
+                predict(a, tb, levels, w, id, valid, g, s, pairs, out);
                 double term = 0.0;
                 if (g == 0 && valid) {
                     float p0, p1, p2;
