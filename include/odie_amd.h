@@ -104,7 +104,8 @@ int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t
 
 /* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
- * 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),
+ * 256; forward_chunk 0 (default) = 1024 when at least half of the table fits the forward's
+ * LDS staging, else 256), "lds_bytes" (LDS budget of the backward's coarse-level accumulator, <= 160 KiB),
  * "xcd_remap" (0/1: XCD-major block order), "backward_mode" (1: owner computes, 0: atomics),
  * "banded" (the owner's fine passes walk y-band lists of the coordinates: 0 never, 1 always,
  * 2 (default) when the lists cut the estimated visits at least four times),

@@ -42,7 +42,8 @@ struct GridArgs {
 
 // Tuning knobs (set through odie_set_tuning; defaults chosen by measurement).
 struct Tuning {
-    int forward_chunk = 256;
+    int forward_chunk = 0;           // forward: coordinates per block (0: 1024 when at least half of
+                                     // the table is staged in LDS, so that the staging is amortized, else 256)
     int backward_chunk = 8192;
     int lds_bytes = 65536;
     int xcd_remap = 1;
@@ -634,7 +635,7 @@ int launch_fill_zero(float* data, int64_t count, hipStream_t stream) {
 
 int set_grid_tuning(const std::string& key, int value) {
     Tuning& t = tuning();
-    if (key == "forward_chunk" && value >= kBlock && value % kBlock == 0) t.forward_chunk = value;
+    if (key == "forward_chunk" && value >= 0 && value % kBlock == 0) t.forward_chunk = value;
     else if (key == "backward_chunk" && value >= kBlock && value % kBlock == 0) t.backward_chunk = value;
     else if (key == "lds_bytes" && value >= 0 && value <= 160 * 1024) t.lds_bytes = value;
     else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
@@ -689,6 +690,14 @@ ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* of
             }
             a.stage_entries = static_cast<int>(staged);
         }
+    }
+    if (a.chunk == 0) {
+        // Each block copies the staged levels into LDS once: with most of a small table staged
+        // (the 1024-expert gigapixel grid: 28 of its 32 KB) that copy dominates 256 rows; with a
+        // large table (2.2 MB at the 64-expert headline) the other levels' gathers go through L2,
+        // where 256-row blocks measured faster.
+        const int64_t entries = static_cast<int64_t>(levels[n_levels - 1].offset) + levels[n_levels - 1].size;
+        a.chunk = 2 * static_cast<int64_t>(a.stage_entries) >= entries ? 1024 : 256;
     }
     a.vec_rows = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (out_width * elem) % 16 == 0;
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_forward: coords must be 8-byte aligned");
