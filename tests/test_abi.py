@@ -85,7 +85,8 @@ def test_route_rejects_bad_arguments(native):
     assert 'two pixels' in native.odie_error().decode()
     assert native.odie_route(8, 16, 2048, 1365, 8, 8, None, 8, 8, 8, None, None, 8, 4, 0) == -1
     assert 'workspace' in native.odie_error().decode()
-    assert native.odie_route_workspace(1 << 22, 64) == 64 * 4096 * 4 + 256 * 4
+    # 2^22 ids in 8192 sub-chunks of 512: 64 x 8192 counts, then one sum per 1024 of them
+    assert native.odie_route_workspace(1 << 22, 64) == 64 * 8192 * 4 + 512 * 4
     assert native.odie_route_workspace(1 << 24, 4096) > 0
     for n, experts in ((5, 4097), (5, 0), (-1, 4), (1 << 31, 4)):   # outside [0, 2^31-1] x [1, 64*64]
         assert native.odie_route_workspace(n, experts) == -1

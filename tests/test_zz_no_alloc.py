@@ -46,7 +46,7 @@ def _compare(seed, width, height, regions_x, regions_y, n):
 def test_noalloc_route_matches_route_twice():
     lib = _lib.library()
     assert lib.odie_route_workspace(1 << 22, 64) <= LIMIT
-    _compare(31, 2048, 1365, 8, 8, 1 << 22)          # the 64-expert step's route, 2 MiB of scratch
+    _compare(31, 2048, 1365, 8, 8, 1 << 22)          # the 64-expert step's route, 2 MiB + 2 KiB of scratch
     _compare(32, 1000, 999, 16, 16, 300001)          # fewer ids over more (ragged) experts
 
 
