@@ -68,16 +68,33 @@ struct Bounds {
     int32_t y0[kMaxRegions + 1];
 };
 
-// Pixel id of input i (its low 32 bits: ids are below 2^32 once clamped into the image).
-__device__ inline uint32_t pixel_id(const RouteArgs& a, int64_t i) {
-    return static_cast<uint32_t>(
-        a.uniforms ? stratified_id(reinterpret_cast<const float2*>(a.uniforms)[i], i, a.side, a.inv_side,
-                                   static_cast<int>(a.width), static_cast<int>(a.height))
-                   : a.ids[i]);
-}
-
 // The walks below load kAhead groups of 64 ids per wave before placing any of them.
 constexpr int kAhead = 8;
+
+// Pixel ids (their low 32 bits: ids are below 2^32 once clamped into the image) of inputs
+// first + k * stride (k < K), each index past `last` clamped to it; slot i of a stratified batch
+// is the pixel its uniforms draw.  The choice between stored ids and the draw is made once for
+// all K, so that every load is issued before any of them is used.
+template <int K>
+__device__ inline void pixel_ids(const RouteArgs& a, int64_t first, int64_t stride, int64_t last, uint32_t id[K]) {
+    if (a.uniforms) {
+        float2 u[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int64_t i = first + k * stride < last ? first + k * stride : last;
+            u[k] = reinterpret_cast<const float2*>(a.uniforms)[i];
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int64_t i = first + k * stride < last ? first + k * stride : last;
+            id[k] = static_cast<uint32_t>(stratified_id(u[k], i, a.side, a.inv_side, static_cast<int>(a.width),
+                                                        static_cast<int>(a.height)));
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k) id[k] = static_cast<uint32_t>(a.ids[first + k * stride < last ? first + k * stride : last]);
+    }
+}
 
 __device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t id, int& expert, uint32_t& x,
                                  uint32_t& y, int& rx, int& ry) {
@@ -111,11 +128,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
         const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
         for (int64_t g = begin; g < end; g += 64 * kAhead) {
             uint32_t id[kAhead];
-#pragma unroll
-            for (int k = 0; k < kAhead; ++k) {
-                const int64_t i = g + k * 64 + lane;
-                id[k] = pixel_id(a, i < end ? i : end - 1);
-            }
+            pixel_ids<kAhead>(a, g + lane, 64, end - 1, id);
 #pragma unroll
             for (int k = 0; k < kAhead; ++k) {
                 int expert, rx, ry;
@@ -236,11 +249,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
     const uint64_t below = (uint64_t{1} << lane) - 1;
     for (int64_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
         uint32_t ids[kAhead];
-#pragma unroll
-        for (int k = 0; k < kAhead; ++k) {
-            const int64_t i = ahead + k * 64 + lane;
-            ids[k] = i < end ? pixel_id(a, i) : 0u;
-        }
+        pixel_ids<kAhead>(a, ahead + lane, 64, end - 1, ids);
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
             const int64_t group = ahead + k * 64;
@@ -367,11 +376,12 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
         for (int w = 0; w < W; ++w) hist[w * experts + e] = 0u;
     }
     for (int32_t j0 = 0; j0 < count; j0 += 64 * W * 2 * kAhead) {
+        // stored ids only: stratified batches take the direct scatter
         uint32_t ids[2 * kAhead];
 #pragma unroll
         for (int k = 0; k < 2 * kAhead; ++k) {
             const int32_t j = j0 + k * 64 * W + tid;
-            ids[k] = j < count ? pixel_id(a, group_begin + j) : 0u;
+            ids[k] = j < count ? static_cast<uint32_t>(a.ids[group_begin + j]) : 0u;
         }
 #pragma unroll
         for (int k = 0; k < 2 * kAhead; ++k) {
