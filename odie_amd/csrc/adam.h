@@ -91,4 +91,15 @@ int make_adam_step(const char* what, float* master, uint16_t* half_copy, float* 
 // fp16 when grad_half); buffers 16-byte aligned (fp16 ones 8-byte).
 int launch_adam(const AdamStep& a, const void* grad, int grad_half, int64_t n, hipStream_t stream);
 
+// One launch over up to kAdamSegments parameter sets (each its own step, gradient and count):
+// the same per-parameter updates as launch_adam on each set.
+constexpr int kAdamSegments = 3;
+struct AdamSet {
+    AdamStep step;
+    const void* grad;
+    int grad_half;
+    int64_t n;
+};
+int launch_adam_sets(const AdamSet* sets, int count, hipStream_t stream);
+
 }  // namespace odie

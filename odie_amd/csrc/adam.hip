@@ -46,9 +46,11 @@ namespace {
 
 constexpr int kAdamBlock = 256;
 
-__global__ __launch_bounds__(kAdamBlock) void adam_kernel(AdamStep a, const void* grad, int grad_half, int64_t n) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kAdamBlock * 4;
-    for (int64_t base = (static_cast<int64_t>(blockIdx.x) * kAdamBlock + threadIdx.x) * 4; base < n; base += stride) {
+// The update of parameters [0, n) by block `block` of `blocks`: four per thread and step.
+__device__ inline void adam_range(const AdamStep& a, const void* grad, int grad_half, int64_t n, int64_t block,
+                                  int64_t blocks) {
+    const int64_t stride = blocks * kAdamBlock * 4;
+    for (int64_t base = (block * kAdamBlock + threadIdx.x) * 4; base < n; base += stride) {
         if (base + 4 <= n) {
             float g[4];
             if (grad_half) {
@@ -96,13 +98,53 @@ __global__ __launch_bounds__(kAdamBlock) void adam_kernel(AdamStep a, const void
     }
 }
 
+__global__ __launch_bounds__(kAdamBlock) void adam_kernel(AdamStep a, const void* grad, int grad_half, int64_t n) {
+    adam_range(a, grad, grad_half, n, blockIdx.x, gridDim.x);
+}
+
+// Several parameter sets in one launch: block b updates set k with first[k] <= b < first[k+1].
+struct AdamSegments {
+    AdamStep step[kAdamSegments];
+    const void* grad[kAdamSegments];
+    int grad_half[kAdamSegments];
+    int64_t n[kAdamSegments];
+    int64_t first[kAdamSegments + 1];
+    int count;
+};
+
+__global__ __launch_bounds__(kAdamBlock) void adam_segments_kernel(AdamSegments s) {
+    int k = 0;
+    while (k + 1 < s.count && static_cast<int64_t>(blockIdx.x) >= s.first[k + 1]) ++k;
+    adam_range(s.step[k], s.grad[k], s.grad_half[k], s.n[k], blockIdx.x - s.first[k], s.first[k + 1] - s.first[k]);
+}
+
+int64_t adam_blocks(int64_t n) {
+    const int64_t blocks = (n + kAdamBlock * 4 - 1) / (kAdamBlock * 4);
+    return blocks > 16384 ? 16384 : blocks;
+}
+
 }  // namespace
 
 int launch_adam(const AdamStep& a, const void* grad, int grad_half, int64_t n, hipStream_t stream) {
     if (n == 0) return 0;
-    int64_t blocks = (n + kAdamBlock * 4 - 1) / (kAdamBlock * 4);
-    if (blocks > 16384) blocks = 16384;
-    adam_kernel<<<static_cast<uint32_t>(blocks), kAdamBlock, 0, stream>>>(a, grad, grad_half, n);
+    adam_kernel<<<static_cast<uint32_t>(adam_blocks(n)), kAdamBlock, 0, stream>>>(a, grad, grad_half, n);
+    return check_launch("adam step");
+}
+
+int launch_adam_sets(const AdamSet* sets, int count, hipStream_t stream) {
+    if (count < 1 || count > kAdamSegments) return fail("adam step: 1 to 3 parameter sets per launch");
+    AdamSegments s{};
+    s.first[0] = 0;
+    for (int k = 0; k < count; ++k) {
+        s.step[k] = sets[k].step;
+        s.grad[k] = sets[k].grad;
+        s.grad_half[k] = sets[k].grad_half;
+        s.n[k] = sets[k].n;
+        s.first[k + 1] = s.first[k] + adam_blocks(sets[k].n);
+    }
+    s.count = count;
+    if (s.first[count] == 0) return 0;
+    adam_segments_kernel<<<static_cast<uint32_t>(s.first[count]), kAdamBlock, 0, stream>>>(s);
     return check_launch("adam step");
 }
 

@@ -523,6 +523,8 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
     }
     // grid: fp16 gradients (mode bit 4) carrying the loss scale 128 (odie/native/runtime.cu:298,304-305)
     const float grid_divisor = half_grads ? 1.0f : 0.0f;
+    AdamSet sets[kAdamSegments];   // the optimizer steps left for one launch at the end
+    int pending = 0;
     if (hash && update) {
         const AdamStep a = make_step(grid, grid_half.data, grid_adam, 1, grid_lr, 128.0f, grid_divisor);
         call(grid_backward_adam_internal(xy.data, n, nullptr, 1, up, ODIE_F16, row, total, hash_levels.data(), levels,
@@ -532,19 +534,20 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
                                 features[0], grid_grad.data, 1, s));
     } else {
         call(odie_packed_backward(xy.data, n, up, row, desc, levels, bits, prefix, cells, grid_grad.data, total, s));
-        if (update) {
-            const AdamStep a = make_step(grid, nullptr, grid_adam, 1, grid_lr, 128.0f, grid_divisor);
-            call(launch_adam(a, grid_grad.data, 0, total, stream));
-        }
+        if (update)
+            sets[pending++] = AdamSet{make_step(grid, nullptr, grid_adam, 1, grid_lr, 128.0f, grid_divisor),
+                                      grid_grad.data, 0, total};
     }
-    // heads: fp16 gradients carrying 16384, halved to 128 unless mode bit 1 (:300-303,306-309)
-    if (update)
+    // heads: fp16 gradients carrying 16384, halved to 128 unless mode bit 1 (:300-303,306-309).  The
+    // parameter sets are disjoint, so their updates share one launch.
+    if (update) {
         for (Head* h : {gate.get(), decoder.get()})
-            if (h) {
-                const AdamStep a = make_step(h->master, h->half.data, h->adam, 2, h->lr, fused ? 16384.0f : 128.0f,
-                                             fused ? 1.0f : 128.0f);
-                call(launch_adam(a, h->grad.data, 0, h->count, stream));
-            }
+            if (h)
+                sets[pending++] = AdamSet{make_step(h->master, h->half.data, h->adam, 2, h->lr, fused ? 16384.0f : 128.0f,
+                                                    fused ? 1.0f : 128.0f),
+                                          h->grad.data, 0, h->count};
+        call(launch_adam_sets(sets, pending, stream));
+    }
 }
 
 std::string Runtime::pointers() const {
