@@ -956,24 +956,25 @@ ODIE_API int odie_packed_forward(const float* coords, int64_t n, const float* gr
                                    bitmap, width, levels, 0, features, visibility, as_stream(stream));
 }
 
-ODIE_API int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
-                                  const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
-                                  const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
-                                  int64_t parameter_count, uint64_t stream) {
+namespace odie {
+
+int packed_backward_internal(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
+                             const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                             const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
+                             int64_t parameter_count, hipStream_t s, bool zeroed) {
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail("odie_packed_backward: n must be within [0, 2^31-1]");
     if (levels < 2 || levels > ODIE_MAX_LEVELS) return fail("odie_packed_backward: descriptor must have 2..32 levels");
     if (up_width < 2 || up_width > 128) return fail("odie_packed_backward: upstream width must be within 2..128");
     if (parameter_count < 0) return fail("odie_packed_backward: parameter count must be nonnegative");
     if (parameter_count > 0 && !gradient) return fail("odie_packed_backward: gradient is null");
-    const hipStream_t s = as_stream(stream);
-    if (n == 0 || parameter_count == 0) return launch_fill_zero(gradient, parameter_count, s);
+    if (n == 0 || parameter_count == 0) return zeroed ? 0 : launch_fill_zero(gradient, parameter_count, s);
     if (!coords || !upstream || !descriptors || !bitmap) return fail("odie_packed_backward: null pointer");
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_packed_backward: coords must be 8-byte aligned");
     const Tuning& t = tuning();
     if (t.packed_owner)   // owner computes: every value written once, deterministic order
         return launch_packed_owner(coords, n, upstream, up_width, descriptors, levels, node_bitmap, node_prefix, bitmap,
                                    gradient, parameter_count, t.owner_lds_bytes, t.packed_splits, s);
-    if (launch_fill_zero(gradient, parameter_count, s)) return -1;
+    if (!zeroed && launch_fill_zero(gradient, parameter_count, s)) return -1;
     PackedArgs a{};
     a.coords = coords;
     a.desc = descriptors;
@@ -997,4 +998,14 @@ ODIE_API int odie_packed_backward(const float* coords, int64_t n, const uint16_t
         packed_backward_kernel<<<blocks, kBlock, 0, s>>>(a);
     }
     return check_launch("odie_packed_backward");
+}
+
+}  // namespace odie
+
+ODIE_API int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
+                                  const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                                  const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
+                                  int64_t parameter_count, uint64_t stream) {
+    return packed_backward_internal(coords, n, upstream, up_width, descriptors, levels, node_bitmap, node_prefix,
+                                    bitmap, gradient, parameter_count, as_stream(stream), false);
 }

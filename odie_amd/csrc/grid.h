@@ -221,6 +221,13 @@ int grid_backward_adam_planes_internal(const float* coords, int64_t n, const int
 // caller guarantees 16 levels of 2 features at output offsets 2l (the faster kernel applies).
 // pairs: the caller guarantees 2 features at output offset 2l for every level but the last,
 // which has 1 or 2 (the pairs kernel applies when the row is a multiple of 16 columns).
+// odie_packed_backward on `s`; zeroed: the caller has already cleared `gradient` (the atomics
+// path then adds into it without clearing it first).
+int packed_backward_internal(const float* coords, int64_t n, const uint16_t* upstream, int up_width,
+                             const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
+                             const int32_t* node_prefix, const uint8_t* bitmap, float* gradient,
+                             int64_t parameter_count, hipStream_t s, bool zeroed);
+
 int packed_forward_internal(const float* coords, int64_t n, const float* grid, int64_t parameter_count,
                             const int32_t* descriptors, int levels, const uint64_t* node_bitmap,
                             const int32_t* node_prefix, const uint8_t* bitmap, int width, int active, uint16_t pad,

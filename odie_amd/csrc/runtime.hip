@@ -175,11 +175,16 @@ void call(int status) {
 // ids -> xy and targets (odie/native/runtime.cu:30-38): x = fp32(id % W) * fp32(1/(W-1)), y
 // likewise; an RGB8 image gives the pixel's bytes packed r | g << 8 | b << 16 (the decoder scales
 // them by 1/255), an fp32 image its three values.  Ids past the image clamp to its last row, so
-// every read stays inside the image and the planes (the reference reads past them).
+// every read stays inside the image and the planes (the reference reads past them).  The same
+// launch clears `clear` [count] (the packed backward's gradient, which it then only adds into),
+// so that the step takes no launch of its own for that.
 __global__ __launch_bounds__(256) void batch_input_kernel(const int64_t* ids, int n, uint32_t width, uint32_t height,
                                                           float rx, float ry, const void* rgb, int rgb8, float* xy,
-                                                          uint32_t* colors, float* target) {
+                                                          uint32_t* colors, float* target, float* clear, int64_t count) {
     const int i = blockIdx.x * 256 + threadIdx.x;
+    const int64_t threads = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t j = i; j < count / 4; j += threads) reinterpret_cast<float4*>(clear)[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t j = count / 4 * 4 + i; j < count; j += threads) clear[j] = 0.0f;
     if (i >= n) return;
     const uint32_t id = static_cast<uint32_t>(ids[i]);
     const uint32_t x = id % width, y = min(id / width, height - 1);
@@ -490,8 +495,11 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
     const uint64_t s = reinterpret_cast<uint64_t>(stream);
     const float rx = static_cast<float>(1.0 / static_cast<double>(width - 1));
     const float ry = static_cast<float>(1.0 / static_cast<double>(height - 1));
+    // the packed backward adds into a gradient cleared here (its owner form writes every value)
+    const bool clear = !hash;
     batch_input_kernel<<<(n + 255) / 256, 256, 0, stream>>>(ids, n, width, height, rx, ry, rgb, rgb8, xy.data,
-                                                            colors.data, target.data);
+                                                            colors.data, target.data, clear ? grid_grad.data : nullptr,
+                                                            clear ? total : 0);
     call(check_launch("odie_step: batch input"));
     if (hash) {
         call(odie_grid_forward(xy.data, n, nullptr, 1, grid_half.data, total, ODIE_F16, hash_levels.data(), levels,
@@ -533,7 +541,8 @@ void Runtime::step(const int64_t* ids, int n, bool update) {
         call(odie_grid_backward(xy.data, n, nullptr, 1, up, ODIE_F16, row, total, hash_levels.data(), levels,
                                 features[0], grid_grad.data, 1, s));
     } else {
-        call(odie_packed_backward(xy.data, n, up, row, desc, levels, bits, prefix, cells, grid_grad.data, total, s));
+        call(packed_backward_internal(xy.data, n, up, row, desc, levels, bits, prefix, cells, grid_grad.data, total,
+                                      stream, clear));
         if (update)
             sets[pending++] = AdamSet{make_step(grid, nullptr, grid_adam, 1, grid_lr, 128.0f, grid_divisor),
                                       grid_grad.data, 0, total};
