@@ -114,33 +114,36 @@ __device__ inline void load_bounds(const RouteArgs& a, Bounds& b) {
     __syncthreads();
 }
 
+// Each wave counts one sub-chunk; the block's kWaves counts of each expert are consecutive in the
+// expert-major count array, so they are written as one run.
 __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
-    extern __shared__ int32_t hist[];  // [kWaves][experts]
+    extern __shared__ int32_t hist[];  // [experts][kWaves] counts of the block's sub-chunks
     __shared__ Bounds bounds;
     load_bounds(a, bounds);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const int part = blockIdx.x * kWaves + wave;
-    int32_t* mine = hist + wave * a.experts;
-    for (int e = lane; e < a.experts; e += 64) mine[e] = 0;
+    const int first = static_cast<int>(blockIdx.x) * kWaves;
+    for (int j = threadIdx.x; j < a.experts * kWaves; j += kRouteBlock) hist[j] = 0;
     __syncthreads();
-    if (part < a.parts) {
-        const int64_t begin = static_cast<int64_t>(part) * a.part;
+    if (first + wave < a.parts) {
+        const int64_t begin = static_cast<int64_t>(first + wave) * a.part;
         const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
         for (int64_t g = begin; g < end; g += 64 * kAhead) {
             uint32_t id[kAhead];
             pixel_ids<kAhead>(a, g + lane, 64, end - 1, id);
 #pragma unroll
-            for (int k = 0; k < kAhead; ++k) {
+            for (int j = 0; j < kAhead; ++j) {
                 int expert, rx, ry;
                 uint32_t x, y;
-                locate_id(a, bounds, id[k], expert, x, y, rx, ry);
-                if (g + k * 64 + lane < end) atomicAdd(mine + expert, 1);
+                locate_id(a, bounds, id[j], expert, x, y, rx, ry);
+                if (g + j * 64 + lane < end) atomicAdd(hist + expert * kWaves + wave, 1);
             }
         }
     }
     __syncthreads();
-    if (part < a.parts)
-        for (int e = lane; e < a.experts; e += 64) a.counts[static_cast<int64_t>(e) * a.parts + part] = mine[e];
+    for (int j = threadIdx.x; j < a.experts * kWaves; j += kRouteBlock) {
+        const int e = j / kWaves, k = j % kWaves;
+        if (first + k < a.parts) a.counts[static_cast<int64_t>(e) * a.parts + first + k] = hist[j];
+    }
 }
 
 // Exclusive scan of counts (expert-major) in place: every block sums a segment of kScanSegment
