@@ -604,6 +604,10 @@ __global__ __launch_bounds__(kBlock) void packed_backward_lds_kernel(PackedArgs 
             float w[4];
             plane_geometry(p.x, p.y, d[0], cell, w);
             if (!((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1)) continue;
+            // the corners' rows once for all features of the level
+            int rows[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) rows[k] = packed_row(d, a.node_bitmap, a.prefix, cell, k);
             for (int c = 0; c < d[5]; ++c) {
                 const int col = d[6] + c;
                 if (col >= a.width) continue;
@@ -611,7 +615,7 @@ __global__ __launch_bounds__(kBlock) void packed_backward_lds_kernel(PackedArgs 
                 if (value == 0.0f) continue;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int64_t param = plane_param(a, d, cell, k, c);
+                    const int64_t param = packed_at(d, a.params, rows[k], c);
                     if (l < lds_levels && param < lds_floats) atomicAdd(lds + param, w[k] * value);
                     else atomicAdd(a.gradient + param, w[k] * value);
                 }

@@ -127,17 +127,25 @@ __device__ inline void plane_geometry(float x, float y, int r, int& cell, float 
 // Parameter of feature c of corner k of `cell`: node (cell + k%2 + (k/2) R) mod points, its row
 // (the node itself, or its rank among the stored nodes: word prefix + popcount below it),
 // plane offset + row * features + c, clamped into the parameters.
+// Row of corner k of `cell` (the first half of packed_param; the same for every feature).
+__device__ inline int packed_row(const int32_t* d, const uint64_t* node_bitmap, const int32_t* prefix, int cell,
+                                 int k) {
+    const int node = (cell + (k & 1) + (k >> 1) * d[0]) % d[1];
+    if (d[7]) return node;
+    const int word = d[3] + (node >> 6), bit = node & 63;
+    const uint64_t mask = (uint64_t{1} << bit) - uint64_t{1};
+    return prefix[word] + __popcll(node_bitmap[word] & mask);
+}
+
+// Parameter of feature c of a corner in row `row`, clamped into the parameters.
+__device__ inline int64_t packed_at(const int32_t* d, int64_t params, int row, int c) {
+    const int64_t p = static_cast<int64_t>(d[2]) + static_cast<int64_t>(row) * d[5] + c;
+    return p < 0 ? 0 : (p >= params ? params - 1 : p);
+}
+
 __device__ inline int64_t packed_param(const int32_t* d, const uint64_t* node_bitmap, const int32_t* prefix,
                                        int64_t params, int cell, int k, int c) {
-    const int node = (cell + (k & 1) + (k >> 1) * d[0]) % d[1];
-    int row = node;
-    if (!d[7]) {
-        const int word = d[3] + (node >> 6), bit = node & 63;
-        const uint64_t mask = (uint64_t{1} << bit) - uint64_t{1};
-        row = prefix[word] + __popcll(node_bitmap[word] & mask);
-    }
-    int64_t p = static_cast<int64_t>(d[2]) + static_cast<int64_t>(row) * d[5] + c;
-    return p < 0 ? 0 : (p >= params ? params - 1 : p);
+    return packed_at(d, params, packed_row(d, node_bitmap, prefix, cell, k), c);
 }
 
 __device__ inline bool cell_visible(const int32_t* d, const uint8_t* bitmap, int cell) {
