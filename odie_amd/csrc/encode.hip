@@ -429,13 +429,18 @@ __global__ __launch_bounds__(kBlock) void packed_forward_kernel(PackedArgs a) {
             plane_geometry(p.x, p.y, d[0], cell, w);
             const bool on = l < a.active && ((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1);
             vis[l / 4] |= static_cast<uint32_t>(on) << (8 * (l % 4));
+            int rows[4] = {0, 0, 0, 0};
+            if (on) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) rows[k] = packed_row(d, a.node_bitmap, a.prefix, cell, k);
+            }
             for (int c = 0; c < d[5]; ++c) {
                 __half v = __float2half(0.0f);
                 if (on) {
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
                         v = __hfma(__float2half_rn(keep_fp32(w[k])),
-                                   __float2half_rn(a.grid[plane_param(a, d, cell, k, c)]), v);
+                                   __float2half_rn(a.grid[packed_at(d, a.params, rows[k], c)]), v);
                 }
                 row[d[6] + c] = half_to_bits(v);
             }
@@ -566,13 +571,16 @@ __global__ __launch_bounds__(kBlock) void packed_backward_kernel(PackedArgs a) {
         float w[4];
         plane_geometry(p.x, p.y, d[0], cell, w);
         if (!((a.bitmap[d[4] + (cell >> 3)] >> (cell & 7)) & 1)) continue;
+        int rows[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rows[k] = packed_row(d, a.node_bitmap, a.prefix, cell, k);
         for (int c = 0; c < d[5]; ++c) {
             const int col = d[6] + c;
             if (col >= a.width) continue;
             const float value = __half2float(bits_to_half(urow[col]));
             if (value == 0.0f) continue;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) atomicAdd(a.gradient + plane_param(a, d, cell, k, c), w[k] * value);
+            for (int k = 0; k < 4; ++k) atomicAdd(a.gradient + packed_at(d, a.params, rows[k], c), w[k] * value);
         }
     }
 }
