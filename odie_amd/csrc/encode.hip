@@ -51,7 +51,7 @@ struct Tuning {
     int banded = 2;                 // owner: fine passes walk y-band lists (0 never, 1 always, 2 when they pay)
     int split_target = 0;           // owner, banded: coordinate-level visits per work item (0: automatic)
     int packed_owner = 0;           // packed backward: 1 owner computes (deterministic), 0 global atomics
-                                    // (measured faster on the 65536-id native steps: 0.34 vs 0.60 ms)
+                                    // (measured faster on the 65536-id native steps: 0.30 vs 0.56 ms)
     int packed_splits = 0;          // packed owner: coordinate splits per slice (0: automatic)
     int packed_lds = 1;             // packed backward with atomics: coarse levels accumulated in LDS
     int packed_blocks = 256;        // packed backward with LDS: most blocks (each flushes its partials once)
