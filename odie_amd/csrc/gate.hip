@@ -471,7 +471,11 @@ ODIE_API int odie_gate_forward(const uint16_t* raw, int64_t n, int width, int le
     a.levels = levels;
     a.coarse = coarse;
     a.softplus = softplus ? 1 : 0;
-    const uint32_t blocks = static_cast<uint32_t>(gate_blocks(n));
+    // one tile per wave (the forward has no per-block partials to bound the block count)
+    const int64_t tiles = (n + 31) / 32;
+    int64_t forward_blocks = (tiles + kGateWaves - 1) / kGateWaves;
+    forward_blocks = forward_blocks < 1 ? 1 : (forward_blocks > 8192 ? 8192 : forward_blocks);
+    const uint32_t blocks = static_cast<uint32_t>(forward_blocks);
     const hipStream_t s = as_stream(stream);
     ODIE_GATE_SWITCH(gate_forward_kernel, width / 16, (levels + 15) / 16, blocks, s, a);
     return check_launch("odie_gate_forward");
