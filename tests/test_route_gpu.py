@@ -29,6 +29,23 @@ def test_route_matches_oracle(width, height, rx, ry, n):
     assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
 
 
+def test_route_tiles_at_every_bound_of_a_large_image():
+    """Tile lookup (an fp32 estimate corrected by exact 64-bit product comparisons) at and around
+    every tile bound of a 100003 x 42948 image (4.29e9 pixels, just under 2^32) cut into 60 x 60
+    tiles whose bounds fall between pixels: experts, order and local coordinates bit-exact."""
+    width, height, rx, ry = 100003, 42948, 60, 60
+    xs = np.unique(np.clip([(r * width + rx - 1) // rx + d for r in range(rx + 1) for d in (-1, 0, 1)], 0, width - 1))
+    ys = np.unique(np.clip([(r * height + ry - 1) // ry + d for r in range(ry + 1) for d in (-1, 0, 1)], 0, height - 1))
+    ids = (ys[:, None].astype(np.int64) * width + xs[None, :]).reshape(-1)
+    ids = np.concatenate([ids, synth.integers(29, 'ids', 4096, width * height)])
+    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, with_expert=True)
+    expert, perm, local, offsets = oracle.route(ids, width, height, rx, ry)
+    assert np.array_equal(result.expert.cpu().numpy(), expert)
+    assert np.array_equal(result.offsets.cpu().numpy(), offsets)
+    assert np.array_equal(result.perm.cpu().numpy(), perm)
+    assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
+
+
 @pytest.mark.parametrize('width,height,rx,ry,n,offset', [(2048, 1365, 8, 8, 1 << 18, 0), (100, 37, 3, 5, 4099, 0),
                                                           (100, 37, 3, 5, 4099, 1)])
 def test_route_gathers_slot_colors(width, height, rx, ry, n, offset):
