@@ -296,8 +296,10 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
 // Target colors in slot order.  route_scatter leaves each slot's pixel index in colors; the
 // slots of one expert are contiguous and lie in one tile of the image, and consecutive chunks
 // of slots run on one XCD (xcd_major), so each XCD gathers the bytes of its own run of tiles
-// through its L2 instead of fetching a line of the image for every id.
-constexpr int kColorsPer = 8;
+// through its L2 instead of fetching a line of the image for every id.  One slot per thread: the
+// most blocks in flight (measured against 2, 4, 8 and 16 slots per thread: 19.7 against
+// 20.2-22.8 us at 2^22 slots, 359 against 364-388 us for 2^24 slots of a 3.2 GB image).
+constexpr int kColorsPer = 1;
 constexpr int kColorsChunk = kRouteBlock * kColorsPer;
 
 __global__ __launch_bounds__(kRouteBlock) void route_colors_kernel(const uint8_t* rgb, uint32_t* colors, int64_t n,
