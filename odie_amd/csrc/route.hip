@@ -68,8 +68,11 @@ struct Bounds {
     int32_t y0[kMaxRegions + 1];
 };
 
-// The walks below load kAhead groups of 64 ids per wave before placing any of them.
-constexpr int kAhead = 8;
+// The walks below load kAhead groups of 64 ids per wave before placing any of them (the direct
+// scatter kDirectAhead: on stratified batches, whose draw it forms itself, more loads in flight
+// paid; the count and staged walks measured faster with fewer).
+constexpr int kAhead = 4;
+constexpr int kDirectAhead = 8;
 
 // Pixel ids (their low 32 bits: ids are below 2^32 once clamped into the image) of inputs
 // first + k * stride (k < K), each index past `last` clamped to it; slot i of a stratified batch
@@ -250,11 +253,11 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
     const int64_t begin = static_cast<int64_t>(part) * a.part;
     const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
     const uint64_t below = (uint64_t{1} << lane) - 1;
-    for (int64_t ahead = begin; ahead < end; ahead += 64 * kAhead) {
-        uint32_t ids[kAhead];
-        pixel_ids<kAhead>(a, ahead + lane, 64, end - 1, ids);
+    for (int64_t ahead = begin; ahead < end; ahead += 64 * kDirectAhead) {
+        uint32_t ids[kDirectAhead];
+        pixel_ids<kDirectAhead>(a, ahead + lane, 64, end - 1, ids);
 #pragma unroll
-        for (int k = 0; k < kAhead; ++k) {
+        for (int k = 0; k < kDirectAhead; ++k) {
             const int64_t group = ahead + k * 64;
             const int64_t i = group + lane;
             const bool valid = i < end;
