@@ -33,6 +33,7 @@ constexpr int kTransposeRows = 1024;  // rows per transpose block
 constexpr int kMaxRows = 128;         // rows per |upstream| maximum record (two waves of a pass)
 constexpr int kOwnerBlock = 1024;
 constexpr int kBatch = 4;             // coordinates per thread per owner-loop iteration
+constexpr int kGroupBatch = 2;        // the same in the coarse-group pass, whose adds all land
 constexpr int kWaves = kOwnerBlock / 64;
 
 // Band lists.  A coordinate with x and y in [0, 1] falls in y-band floor(y * kBands) (clamped);
@@ -379,22 +380,22 @@ __device__ inline int64_t lane_offset() {
 // iteration, kOwnerBlock apart, at lane_offset<KIND>() within each run; loads are issued
 // unconditionally (clamped index) before any arithmetic.  A thread stops once its first
 // coordinate is past b1: its later ones are too.
-template <int F, bool HALF, int KIND>
+template <int F, bool HALF, int KIND, int B = kBatch>
 __device__ inline void accumulate_level(const float* coords, const Elem<HALF>* plane, const DevLevel lv, int64_t b0,
                                         int64_t b1, uint32_t lo, uint32_t span, float scale,
                                         unsigned long long* acc) {
-    for (int64_t i = b0 + lane_offset<KIND>(); i < b1; i += kBatch * kOwnerBlock) {
-        float2 xy[kBatch];
-        float us[kBatch][F];
+    for (int64_t i = b0 + lane_offset<KIND>(); i < b1; i += B * kOwnerBlock) {
+        float2 xy[B];
+        float us[B][F];
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
+        for (int b = 0; b < B; ++b) {
             const int64_t ii = i + b * kOwnerBlock;
             const int64_t at = ii < b1 ? ii : b0;
             xy[b] = reinterpret_cast<const float2*>(coords)[at];
             load_upstream<F, HALF>(plane, at, scale, ii < b1, us[b]);
         }
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
+        for (int b = 0; b < B; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
     }
 }
 
@@ -871,10 +872,16 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
             }
         } else {
             switch (kind) {
-                case kHashed24: accumulate_level<F, HALF, kHashed24>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                case kHashed24:
+                    if (grouped) accumulate_level<F, HALF, kHashed24, kGroupBatch>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    else accumulate_level<F, HALF, kHashed24>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    break;
                 case kHashedPow2: accumulate_level<F, HALF, kHashedPow2>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
                 case kGeneric: accumulate_level<F, HALF, kGeneric>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
-                default: accumulate_level<F, HALF, kDense>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                default:
+                    if (grouped) accumulate_level<F, HALF, kDense, kGroupBatch>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    else accumulate_level<F, HALF, kDense>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    break;
             }
         }
     }
