@@ -92,7 +92,7 @@ int odie_grid_backward_adam(const float* coords, int64_t n, const int32_t* offse
                             float lr, float beta1, float beta2, float eps, float loss_scale, uint64_t stream);
 
 /* odie_grid_backward_adam for features = 2 with the fp16 upstream given as odie_mlp_train_planes
- * writes it (planes uint32 [n_levels][n], blockmax fp32 [ceil(n/128)][n_levels]) instead of rows
+ * writes it (planes uint32 [n_levels][n], blockmax fp32 [ceil(n/128)][2 n_levels]) instead of rows
  * [n, up_width]: the same update, bit for bit, without transposing the upstream.  No counterpart
  * in the reference (see odie_mlp_train_planes). */
 int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,
@@ -288,8 +288,8 @@ int odie_mlp_train(const uint16_t* x, int64_t n, int width, int64_t real, const 
 
 /* odie_mlp_train at width 32 (16 levels x 2 features) with dz written in the layout
  * odie_grid_backward_adam_planes reads instead of rows: planes uint32 [16][n] (plane l, row j = the fp16 pair of columns 2l, 2l+1 of dz row j)
- * and blockmax fp32 [ceil(n/128)][16] (record r, level l = max |dz| over rows 128r..128r+127
- * and both features of level l; NaN if any of them is NaN).  Same values as odie_mlp_train's
+ * and blockmax fp32 [ceil(n/128)][32] (record r, column 2l + f = max |dz| of feature f of level l
+ * over rows 128r..128r+127; NaN if any of them is NaN).  Same values as odie_mlp_train's
  * dz, bit for bit.  No counterpart in the reference: it saves the encode backward's transposition
  * of dz, a layout change of this implementation. */
 int odie_mlp_train_planes(const uint16_t* x, int64_t n, int64_t real, const uint16_t* weights,

@@ -4,17 +4,19 @@
 // near 0.2 T op/s, while LDS 64-bit integer atomics (ds_add_u64) reach ~2.4 T op/s.  So the
 // gradient is not scattered into HBM at all:
 //   1. transpose  the upstream rows [N, L*F] into level-major planes [L][N][F] and record
-//                 the largest |upstream| of every 1024-row block and level;
+//                 the largest |upstream| of every 128-row record and column (level, feature);
 //   2. owner      one workgroup owns one slice of one expert's gradient (a group of coarse
 //                 levels, or a part of one finer level) that fits in LDS.  It walks every
 //                 coordinate of its expert, evaluates the geometry of its level(s) and adds
 //                 the contributions that land in its slice as 64-bit fixed-point integers
-//                 (ds_add_u64).  The fixed-point scale 2^S is chosen per workgroup from
-//                 max|upstream| over its coordinates and levels: every contribution stays
-//                 below 2^31 and 4*count of them below 2^62, so nothing can overflow; each
-//                 contribution is the fp32 product w_k * upstream (as in the reference,
-//                 odie/packed_kernels.cu:84) rounded to the nearest multiple of 2^-S.  The
-//                 slice is then converted to fp32 and written with plain coalesced stores.
+//                 (ds_add_u64).  Every (level, feature) of the slice has its own fixed-point
+//                 scale 2^S, chosen from max|upstream| of that column over the workgroup's
+//                 coordinates: every contribution stays below 2^31 and 4*count of them below
+//                 2^62, so nothing can overflow; each contribution is the fp32 product
+//                 w_k * upstream (as in the reference, odie/packed_kernels.cu:84) rounded to the
+//                 nearest multiple of 2^-S, so its error is at most 2^-31 of the largest |u| of
+//                 its own level and feature, whatever the other columns hold.  The slice is
+//                 then converted to fp32 and written with plain coalesced stores.
 //                 Integer sums are associative, so the gradient does not depend on the
 //                 order in which lanes add.
 //   3. reduce     only when one expert's coordinates are split over several workgroups per
@@ -66,37 +68,39 @@ struct TransposeArgs {
 // Maximum of two |upstream| records; NaN wins, so the owner pass sees a non-finite bound.
 __device__ inline float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
 
-// Record q of the block (rows q*128.. of its 1024) is waves 2*(q%2) and 2*(q%2)+1 of pass q/2.
-__device__ inline void write_records(const TransposeArgs& a, const float* waves, int lmax) {
+// Record q of the block (rows q*128.. of its 1024) is waves 2*(q%2) and 2*(q%2)+1 of pass q/2;
+// `waves` holds `stride` column maxima per wave, of which the first `columns` are used.
+__device__ inline void write_records(const TransposeArgs& a, const float* waves, int stride, int columns) {
     constexpr int kRecords = kTransposeRows / kMaxRows;
-    for (int t = threadIdx.x; t < kRecords * a.n_levels; t += kTransposeBlock) {
-        const int q = t / a.n_levels, l = t % a.n_levels;
+    for (int t = threadIdx.x; t < kRecords * columns; t += kTransposeBlock) {
+        const int q = t / columns, j = t % columns;
         const int64_t record = static_cast<int64_t>(blockIdx.x) * kRecords + q;
         if (record * kMaxRows >= a.n) continue;
-        const float* pass = waves + (q / 2) * (kTransposeBlock / 64) * lmax;
+        const float* pass = waves + (q / 2) * (kTransposeBlock / 64) * stride;
         const int w = 2 * (q % 2);
-        a.blockmax[record * a.n_levels + l] = nan_max(pass[w * lmax + l], pass[(w + 1) * lmax + l]);
+        a.blockmax[record * columns + j] = nan_max(pass[w * stride + j], pass[(w + 1) * stride + j]);
     }
 }
 
+// Rows [N, width] -> level-major planes [L][N][F], and the largest |upstream| of every 128-row
+// record and column (level l, feature c: column l*F + c).
 template <int F, bool HALF, int LMAX>
 __global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArgs a) {
     using U = Elem<HALF>;
     constexpr int kPasses = kTransposeRows / kTransposeBlock;
-    __shared__ float waves[kPasses][kTransposeBlock / 64][LMAX];
+    constexpr int kColumns = LMAX * F;
+    __shared__ float waves[kPasses][kTransposeBlock / 64][kColumns];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int used = a.n_levels * F;
     for (int r = 0; r < kPasses; ++r) {
         const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
-        float peak[LMAX];
-#pragma unroll
-        for (int l = 0; l < LMAX; ++l) peak[l] = 0.0f;
-        if (i < a.n) {
+        const bool valid = i < a.n;
+        U vals[kColumns];
+        if (valid) {
             const U* row = reinterpret_cast<const U*>(a.upstream) + static_cast<size_t>(i) * a.width;
-            U vals[LMAX * F];
             if (a.vec_rows) {
                 constexpr int kPer = 16 / sizeof(U);
-                constexpr int kChunks = (LMAX * F + kPer - 1) / kPer;
+                constexpr int kChunks = (kColumns + kPer - 1) / kPer;
 #pragma unroll
                 for (int j = 0; j < kChunks; ++j) {
                     if (j * kPer < used) {
@@ -104,12 +108,12 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArg
                         const U* parts = reinterpret_cast<const U*>(&v);
 #pragma unroll
                         for (int q = 0; q < kPer; ++q)
-                            if (j * kPer + q < LMAX * F) vals[j * kPer + q] = parts[q];
+                            if (j * kPer + q < kColumns) vals[j * kPer + q] = parts[q];
                     }
                 }
             } else {
 #pragma unroll
-                for (int c = 0; c < LMAX * F; ++c)
+                for (int c = 0; c < kColumns; ++c)
                     if (c < used) vals[c] = row[c];
             }
             U* planes = reinterpret_cast<U*>(a.planes);
@@ -125,34 +129,33 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArg
 #pragma unroll
                         for (int c = 0; c < F; ++c) dst[c] = vals[l * F + c];
                     }
-#pragma unroll
-                    for (int c = 0; c < F; ++c) peak[l] = nan_max(peak[l], fabsf(static_cast<float>(vals[l * F + c])));
                 }
             }
         }
         // the wave's 64 rows lie in one record of kMaxRows = 128 rows
 #pragma unroll
-        for (int l = 0; l < LMAX; ++l) {
-            if (l < a.n_levels) {
-                float m = peak[l];
+        for (int j = 0; j < kColumns; ++j) {
+            if (j < used) {
+                float m = valid ? fabsf(static_cast<float>(vals[j])) : 0.0f;
                 for (int step = 32; step; step >>= 1) m = nan_max(m, __shfl_xor(m, step));
-                if (lane == 0) waves[r][wave][l] = m;
+                if (lane == 0) waves[r][wave][j] = m;
             }
         }
     }
     __syncthreads();
-    write_records(a, &waves[0][0][0], LMAX);
+    write_records(a, &waves[0][0][0], kColumns, used);
 }
 
 // fp16 pairs (F = 2), levels a multiple of 4 and 16-byte rows: every thread loads its four
-// rows first (16-byte loads), then writes one dword per level and row; |u| maxima are packed
-// 16-bit magnitude maxima, two levels per dword, reduced over the wave's 64 rows (one half of
-// a 128-row record).
+// rows first (16-byte loads), then writes one dword per level and row; the per-feature |u|
+// maxima of each level (two 16-bit magnitudes per dword) are reduced over the 32 lanes of each
+// lane group eight levels at a time (group_max8), then over the record's two waves and four lane
+// groups.
 template <int LMAX>
 __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(TransposeArgs a) {
     constexpr int kPasses = kTransposeRows / kTransposeBlock;
     constexpr int kChunks = LMAX / 4;  // 16-byte chunks per row (4 levels each)
-    __shared__ uint32_t waves[kPasses][kTransposeBlock / 64][LMAX / 2];   // level pairs
+    __shared__ uint32_t waves[kPasses][kTransposeBlock / 64][2][LMAX];   // per lane group and level
     uint4 rows[kPasses][kChunks];
     const int chunks = a.n_levels / 4;
 #pragma unroll
@@ -164,12 +167,12 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
         for (int j = 0; j < kChunks; ++j) rows[r][j] = j < chunks ? row[j] : make_uint4(0, 0, 0, 0);
     }
     uint32_t* planes = reinterpret_cast<uint32_t*>(a.planes);
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
 #pragma unroll
     for (int r = 0; r < kPasses; ++r) {
         const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
         const bool valid = i < a.n;
-        uint32_t peak[LMAX / 2];
+        uint32_t peak[LMAX];
 #pragma unroll
         for (int j = 0; j < kChunks; ++j) {
             const uint32_t words[4] = {rows[r][j].x, rows[r][j].y, rows[r][j].z, rows[r][j].w};
@@ -177,26 +180,28 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
 #pragma unroll
                 for (int q = 0; q < 4; ++q) planes[static_cast<size_t>(4 * j + q) * a.n + i] = words[q];
             }
-            peak[2 * j] = valid ? pair_peak(words[0], words[1]) : 0u;
-            peak[2 * j + 1] = valid ? pair_peak(words[2], words[3]) : 0u;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) peak[4 * j + q] = valid ? pair_magnitudes(words[q]) : 0u;
         }
 #pragma unroll
-        for (int p = 0; p < LMAX / 2; ++p) {
-            if (2 * p < a.n_levels) {
-                uint32_t m = peak[p];
-                for (int step = 32; step; step >>= 1) m = pair_max(m, __shfl_xor(m, step));
-                if (lane == 0) waves[r][wave][p] = m;
+        for (int k = 0; k < LMAX / 8; ++k) {
+            if (8 * k < a.n_levels) {   // uniform: the whole wave takes part in group_max8
+                const uint32_t m = group_max8(peak + 8 * k, lane);
+                if (s < 8) waves[r][wave][g][8 * k + s] = m;
             }
         }
     }
     __syncthreads();
     constexpr int kRecords = kTransposeRows / kMaxRows;
-    for (int t = threadIdx.x; t < kRecords * a.n_levels; t += kTransposeBlock) {
-        const int q = t / a.n_levels, l = t % a.n_levels;
+    const int columns = 2 * a.n_levels;
+    for (int t = threadIdx.x; t < kRecords * columns; t += kTransposeBlock) {
+        const int q = t / columns, j = t % columns, l = j / 2, f = j % 2;
         const int64_t record = static_cast<int64_t>(blockIdx.x) * kRecords + q;
         if (record * kMaxRows >= a.n) continue;
-        const uint32_t both = pair_max(waves[q / 2][2 * (q % 2)][l / 2], waves[q / 2][2 * (q % 2) + 1][l / 2]);
-        a.blockmax[record * a.n_levels + l] = __half2float(bits_to_half(static_cast<uint16_t>(both >> (16 * (l % 2)))));
+        const int w = 2 * (q % 2);
+        const auto& pass = waves[q / 2];
+        const uint32_t both = pair_max(pair_max(pass[w][0][l], pass[w][1][l]), pair_max(pass[w + 1][0][l], pass[w + 1][1][l]));
+        a.blockmax[record * columns + j] = __half2float(bits_to_half(static_cast<uint16_t>(both >> (16 * f))));
     }
 }
 
@@ -208,16 +213,17 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
 // split_reduce_kernel.  Banded, the fine passes walk only the coordinates listed in the y-band
 // slots their table rows can reach (band lists below), every pass bounds its fixed-point scale
 // over all of the expert's coordinates, and splits write the raw 64-bit sums, added exactly by
-// banded_reduce_kernel: the gradient does not depend on how a pass is split.
+// banded_reduce_kernel: the gradient does not depend on how a pass is split.  Every pass has one
+// fixed-point scale per column (level, feature) it covers.
 struct OwnerArgs {
     const float* coords;
     const int32_t* offsets;
     const void* planes;
-    const float* blockmax;
+    const float* blockmax;      // [records][n_levels * features]: max |upstream| per 128-row record and column
     float* grad;
     float* partial;             // unbanded splits: fp32 [max split][experts][expert_params]
     long long* partial64;       // banded splits: int64 [max split][experts][partial_floats]
-    int32_t* shifts;            // banded splits: [experts][passes] fixed-point shift (kNonFinite: NaN)
+    int32_t* shifts;            // banded splits: [experts][n_levels][features] fixed-point shift (kNonFinite: NaN)
     int64_t partial_floats;
     int64_t n;
     int64_t expert_params;
@@ -225,7 +231,6 @@ struct OwnerArgs {
     int n_levels;
     int features;
     int group;        // pass 0 covers levels [0, group) when group > 0
-    int passes;       // passes per expert
     int items;        // work items per expert
     int group_splits;
     int heavy;        // leading items of every expert scheduled first (work_of)
@@ -233,7 +238,6 @@ struct OwnerArgs {
     int remap;
     int banded;
     DevLevel level[ODIE_MAX_LEVELS];
-    int first_pass[ODIE_MAX_LEVELS];
     int first_item[ODIE_MAX_LEVELS];
     int slices[ODIE_MAX_LEVELS];
     int splits[ODIE_MAX_LEVELS];
@@ -250,7 +254,34 @@ struct OwnerArgs {
     const int32_t* ordered;
 };
 
-constexpr int32_t kNonFinite = 1 << 30;   // shift recorded for a pass whose upstream bound is not finite
+constexpr int32_t kNonFinite = 1 << 30;   // shift of a column whose upstream bound is not finite
+constexpr int kMaxColumns = 128;          // (level, feature) columns of one pass: one LDS word each
+
+// Fixed-point shift of a column whose contributions are w * u with |u| <= peak (the bits of a
+// non-negative float, or a NaN), `count` coordinates of them: 2^shift * peak stays below 2^31, so
+// one contribution converts with one rint + cvt_i32, and 4 * count of them below 2^62 in the
+// int64 sum.  The quantum is 2^-shift <= 2^-30 peak (count < 2^29).  kNonFinite for a NaN or
+// infinite peak.
+__device__ inline int32_t column_shift(uint32_t peak_bits, int64_t count) {
+    const float peak = __uint_as_float(peak_bits);
+    if (!(peak <= 3.0e38f)) return kNonFinite;
+    int shift = 60;
+    if (peak > 0.0f) {
+        const int by_value = 30 - ilogb(peak);
+        const int by_sum = 61 - ilogb(4.0 * static_cast<double>(count) * static_cast<double>(peak));
+        shift = by_value < by_sum ? by_value : by_sum;
+    }
+    return shift > 120 ? 120 : shift;
+}
+
+// 2^shift as the multiplier of the upstream values (1 for a non-finite column: its values are NaN).
+__device__ inline float shift_scale(int32_t shift) { return shift == kNonFinite ? 1.0f : ldexpf(1.0f, shift); }
+
+// The fp32 gradient value of a raw 64-bit fixed-point sum at `shift`.
+__device__ inline float unscaled(long long sum, int32_t shift) {
+    if (shift == kNonFinite) return __builtin_nanf("");
+    return static_cast<float>(static_cast<double>(sum) * ldexp(1.0, -shift));
+}
 
 enum LevelKind { kDense = 0, kHashedPow2 = 1, kGeneric = 2, kHashed24 = 3 };
 
@@ -343,7 +374,7 @@ template <int F>
 __device__ inline uint32_t planar(uint32_t j, uint32_t span) { return (j % F) * (span / F) + j / F; }
 
 template <int F, bool HALF>
-__device__ inline void load_upstream(const Elem<HALF>* plane, int64_t at, float scale, bool valid, float* us) {
+__device__ inline void load_upstream(const Elem<HALF>* plane, int64_t at, const float* scale, bool valid, float* us) {
     if constexpr (HALF && F == 2) {
         const uint32_t word = *reinterpret_cast<const uint32_t*>(plane + at * F);
         us[0] = __half2float(bits_to_half(static_cast<uint16_t>(word & 0xffffu)));
@@ -353,7 +384,7 @@ __device__ inline void load_upstream(const Elem<HALF>* plane, int64_t at, float 
         for (int c = 0; c < F; ++c) us[c] = static_cast<float>(plane[at * F + c]);
     }
 #pragma unroll
-    for (int c = 0; c < F; ++c) us[c] = valid ? us[c] * scale : 0.0f;
+    for (int c = 0; c < F; ++c) us[c] = valid ? us[c] * scale[c] : 0.0f;
 }
 
 // Offset of this thread's coordinate within each run of kOwnerBlock.  Hashed levels take the
@@ -382,7 +413,7 @@ __device__ inline int64_t lane_offset() {
 // coordinate is past b1: its later ones are too.
 template <int F, bool HALF, int KIND, int B = kBatch>
 __device__ inline void accumulate_level(const float* coords, const Elem<HALF>* plane, const DevLevel lv, int64_t b0,
-                                        int64_t b1, uint32_t lo, uint32_t span, float scale,
+                                        int64_t b1, uint32_t lo, uint32_t span, const float* scale,
                                         unsigned long long* acc) {
     for (int64_t i = b0 + lane_offset<KIND>(); i < b1; i += B * kOwnerBlock) {
         float2 xy[B];
@@ -698,7 +729,7 @@ __device__ inline int find_run(const int32_t* prefix, int runs, int32_t v) {
 template <int F, bool HALF, int KIND>
 __device__ inline void accumulate_runs(const float2* sorted, const Elem<HALF>* plane, const DevLevel lv,
                                        const int32_t* list, const int32_t* run_k0, const int32_t* prefix, int runs,
-                                       int32_t v0, int32_t v1, uint32_t lo, uint32_t span, float scale,
+                                       int32_t v0, int32_t v1, uint32_t lo, uint32_t span, const float* scale,
                                        unsigned long long* acc) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int32_t w0 = v0 + static_cast<int32_t>(static_cast<int64_t>(v1 - v0) * wave / kWaves);
@@ -755,10 +786,17 @@ __device__ inline uint32_t work_of(uint32_t block, uint32_t blocks, int remap, u
     return (m / light) * per_expert + heavy + m % light;
 }
 
+// Fixed-point scales of level l's F columns (column (l - l0) * F + c of the pass).
+template <int F>
+__device__ inline void level_scales(const uint32_t* peaks, int l, int l0, int64_t count, float* scale) {
+#pragma unroll
+    for (int c = 0; c < F; ++c) scale[c] = shift_scale(column_shift(peaks[(l - l0) * F + c], count));
+}
+
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
-    __shared__ float reduce[kWaves];
+    __shared__ uint32_t peaks[kMaxColumns];   // per column of the pass: largest |upstream| (float bits)
     using U = Elem<HALF>;
     const uint32_t per_expert = static_cast<uint32_t>(a.items);
     const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
@@ -770,10 +808,9 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     // Item -> pass p, split s of `splits`, levels [l0, l1) and the slice [lo, hi) of the
     // expert's gradient (in floats).
     const bool grouped = r < a.group_splits;
-    int p, s, splits, l0, l1, slice = 0;
+    int s, splits, l0, l1, slice = 0;
     uint32_t lo, hi;
     if (grouped) {
-        p = 0;
         s = r;
         splits = a.group_splits;
         l0 = 0;
@@ -786,7 +823,6 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         splits = a.splits[l];
         slice = (r - a.first_item[l]) / splits;
         s = (r - a.first_item[l]) % splits;
-        p = a.first_pass[l] + slice;
         const uint32_t first = static_cast<uint32_t>(slice) * a.slice_entries[l];
         uint32_t last = first + a.slice_entries[l];
         if (last > a.level[l].size) last = a.level[l].size;
@@ -796,6 +832,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         hi = (a.level[l].offset + last) * F;
     }
     const uint32_t span = hi - lo;
+    const int columns = (l1 - l0) * F;   // at most kMaxColumns (the launch bounds the coarse group)
 
     // Coordinates of this expert, and this split's index range of them.
     int64_t base, stop;
@@ -806,37 +843,29 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     // banded: every split of a pass bounds the scale over all of the expert's coordinates
     const int64_t m0 = a.banded ? base : b0, m1 = a.banded ? stop : b1;
 
-    // Fixed-point scale from the bound 4 * count * max|upstream| over this range and levels.
-    float bound = 0.0f;
-    if (m1 > m0) {
-        const int64_t r0 = m0 / kMaxRows, r1 = (m1 - 1) / kMaxRows;
-        const int levels = l1 - l0;
-        for (int64_t t = threadIdx.x; t < (r1 - r0 + 1) * levels; t += kOwnerBlock) {
-            const float v = a.blockmax[(r0 + t / levels) * a.n_levels + l0 + t % levels];
-            bound = (v > bound || v != v) ? v : bound;
-        }
-    }
-    for (int step = 32; step; step >>= 1) {
-        const float other = __shfl_xor(bound, step);
-        bound = (other > bound || other != other) ? other : bound;
-    }
-    if (threadIdx.x % 64 == 0) reduce[threadIdx.x / 64] = bound;
+    // Largest |upstream| of every column over the 128-row records of [m0, m1): thread t takes
+    // column t % columns and every (kOwnerBlock / columns)-th record, then one LDS maximum per
+    // thread (float bits of non-negative values and NaN order as unsigned integers).
+    if (threadIdx.x < kMaxColumns) peaks[threadIdx.x] = 0u;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) acc[j] = 0ull;
     __syncthreads();
-    float peak = 0.0f;
-    for (int w = 0; w < kWaves; ++w) peak = (reduce[w] > peak || reduce[w] != reduce[w]) ? reduce[w] : peak;
-    // Scale 2^shift: every contribution |w*u| <= peak maps below 2^31 (so it converts with one
-    // rint + cvt_i32), and 4*count contributions of that size stay below 2^62 in the int64 sum.
-    const double limit = 4.0 * static_cast<double>(m1 - m0) * static_cast<double>(peak);
-    int shift = 60;
-    if (peak > 0.0f && limit <= 1.0e300) {
-        const int by_value = 30 - ilogb(peak);
-        const int by_sum = 61 - ilogb(limit);
-        shift = by_value < by_sum ? by_value : by_sum;
+    {
+        const int per = kOwnerBlock / columns;
+        const int column = threadIdx.x % columns, first = threadIdx.x / columns;
+        uint32_t mine = 0u;
+        if (m1 > m0 && first < per) {
+            const int64_t r0 = m0 / kMaxRows, r1 = (m1 - 1) / kMaxRows;
+            const int64_t stride = static_cast<int64_t>(a.n_levels) * F;
+            const float* at = a.blockmax + static_cast<int64_t>(l0) * F + column;
+            for (int64_t q = r0 + first; q <= r1; q += per) {
+                const uint32_t v = __float_as_uint(at[q * stride]) & 0x7fffffffu;
+                mine = v > mine ? v : mine;
+            }
+        }
+        if (mine) atomicMax(peaks + column, mine);
     }
-    if (shift > 120) shift = 120;
-    const float scale = ldexpf(1.0f, shift);
-    const bool finite = !(peak != peak) && peak <= 3.0e38f;
+    __syncthreads();
+    const int64_t count = m1 - m0;
 
     // A banded fine pass walks the pieces of its share of the band-list runs its rows reach.
     const bool banded = a.banded && !grouped && *a.ordered;
@@ -862,6 +891,8 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         const DevLevel lv = a.level[l];
         const U* plane = reinterpret_cast<const U*>(a.planes) + static_cast<size_t>(l) * a.n * F;
         const int kind = level_kind(lv);
+        float scale[F];
+        level_scales<F>(peaks, l, l0, count, scale);
         if (banded) {
             if (runs == 0) break;
             switch (kind) {
@@ -887,13 +918,28 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     }
     __syncthreads();
     if (splits > 1 && a.banded) {
-        // raw 64-bit sums: banded_reduce_kernel adds the splits exactly and applies the scale
+        // raw 64-bit sums: banded_reduce_kernel adds the splits exactly and applies the scales
         long long* out = a.partial64 + (static_cast<int64_t>(s) * a.experts + e) * a.partial_floats + lo;
         for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[planar<F>(j, span)]);
-        if (s == 0 && threadIdx.x == 0) a.shifts[static_cast<int64_t>(e) * a.passes + p] = finite ? shift : kNonFinite;
+        if (s == 0 && threadIdx.x < columns)
+            a.shifts[(static_cast<int64_t>(e) * a.n_levels + l0) * F + threadIdx.x] = column_shift(peaks[threadIdx.x], count);
         return;
     }
-    const double unscale = ldexp(1.0, -shift);
+    // Value j of the slice is feature j % F of entry lo / F + j / F.  A thread's j only grows, so
+    // its level (and the shifts of that level's columns) only moves forward.
+    int level = l0;
+    int32_t shift[F];
+#pragma unroll
+    for (int c = 0; c < F; ++c) shift[c] = column_shift(peaks[c], count);
+    const auto shift_of = [&](uint32_t j) {
+        const uint32_t entry = lo / F + j / F;
+        if (level + 1 < l1 && a.level[level + 1].offset <= entry) {
+            while (level + 1 < l1 && a.level[level + 1].offset <= entry) ++level;
+#pragma unroll
+            for (int c = 0; c < F; ++c) shift[c] = column_shift(peaks[(level - l0) * F + c], count);
+        }
+        return shift[j % F];
+    };
     if (a.fused && splits == 1) {
         // The final gradient of these parameters is in LDS: update them right here.  One
         // workgroup holds the CU, so the loads of four elements per thread are issued before
@@ -911,8 +957,8 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                 m[k] = o.m[i];
                 v[k] = o.v[i];
                 age[k] = o.variant != 0 ? o.steps[i] : 0u;
-                g[k] = static_cast<float>(static_cast<double>(static_cast<long long>(acc[planar<F>(j < span ? j : 0, span)])) * unscale);
-                if (!finite) g[k] = __builtin_nanf("");
+                const uint32_t jj = j < span ? j : 0;
+                g[k] = unscaled(static_cast<long long>(acc[planar<F>(jj, span)]), j < span ? shift_of(j) : 0);
             }
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
@@ -934,16 +980,17 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                                : a.partial + static_cast<size_t>(s) * a.experts * a.expert_params +
                                      static_cast<size_t>(e) * a.expert_params + lo;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) {
-        float v = static_cast<float>(static_cast<double>(static_cast<long long>(acc[planar<F>(j, span)])) * unscale);
-        if (!finite) v = __builtin_nanf("");
+        float v = unscaled(static_cast<long long>(acc[planar<F>(j, span)]), shift_of(j));
         if (splits == 1 && a.accumulate) v += out[j];
         out[j] = v;
     }
 }
 
 // Banded splits: every entry of the first partial_floats values of every expert whose pass is
-// split gets the exact sum of its splits' 64-bit partials, scaled by the pass's 2^-shift, and is
-// written (added with accumulate) or handed to the optimizer step, as the owner does unsplit.
+// split gets the exact sum of its splits' 64-bit partials, scaled by its column's 2^-shift (the
+// same in every pass and split of the level: each bounds it over all of the expert's
+// coordinates), and is written (added with accumulate) or handed to the optimizer step, as the
+// owner does unsplit.
 __global__ __launch_bounds__(256) void banded_reduce_kernel(OwnerArgs a) {
     const int64_t count = static_cast<int64_t>(a.experts) * a.partial_floats;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
@@ -953,11 +1000,7 @@ __global__ __launch_bounds__(256) void banded_reduce_kernel(OwnerArgs a) {
         const uint32_t entry = static_cast<uint32_t>(x / a.features);
         int l = 0;
         while (l + 1 < a.n_levels && a.level[l + 1].offset <= entry) ++l;
-        int p = 0, splits = a.group_splits;
-        if (l >= a.group) {
-            p = a.first_pass[l] + static_cast<int>((entry - a.level[l].offset) / a.slice_entries[l]);
-            splits = a.splits[l];
-        }
+        const int splits = l >= a.group ? a.splits[l] : a.group_splits;
         if (splits <= 1) continue;
         // eight independent loads in flight per round: the splits' partials are far apart
         const long long* column = a.partial64 + static_cast<int64_t>(e) * a.partial_floats + x;
@@ -972,9 +1015,7 @@ __global__ __launch_bounds__(256) void banded_reduce_kernel(OwnerArgs a) {
             for (int k = 0; k < 8; ++k) sum += v[k];
         }
         for (; s < splits; ++s) sum += column[s * step];
-        const int32_t shift = a.shifts[static_cast<int64_t>(e) * a.passes + p];
-        float v = static_cast<float>(static_cast<double>(sum) * ldexp(1.0, -shift));
-        if (shift == kNonFinite) v = __builtin_nanf("");
+        float v = unscaled(sum, a.shifts[(static_cast<int64_t>(e) * a.n_levels + l) * a.features + x % a.features]);
         const int64_t i = static_cast<int64_t>(e) * a.expert_params + x;
         if (a.fused) {
             adam_update(a.adam, i, v);
@@ -1008,8 +1049,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial,
 // odie/native/runtime.cu:111-137, without atomics).  Workgroup b owns the parameters
 // [b*cap, (b+1)*cap) -- whole levels or a part of one, in plane-offset order -- and walks the
 // coordinates (a share of them when split) through every level whose parameters meet its
-// slice, adding w_k * u (the fp32 product) as 64-bit fixed point in LDS.  One scale per slice
-// from the largest |u| over its levels' columns; split slices write their raw sums and
+// slice, adding w_k * u (the fp32 product) as 64-bit fixed point in LDS.  One scale per
+// upstream column (level, feature), from that column's largest |u| over all coordinates, so every
+// slice and split of a level shares it; split slices write their raw sums and
 // packed_reduce_kernel adds them exactly, so the gradient is the same however it is split.
 // ---------------------------------------------------------------------------------------
 struct PackedOwnerArgs {
@@ -1019,10 +1061,9 @@ struct PackedOwnerArgs {
     const uint64_t* node_bitmap;
     const int32_t* prefix;
     const uint8_t* bitmap;
-    const uint32_t* bounds;       // [levels]: largest fp16 magnitude (bits) of each level's columns
+    const uint32_t* bounds;       // [width]: largest fp16 magnitude (bits) of each upstream column
     float* gradient;
     long long* partial;           // [splits][params] when splits > 1
-    int32_t* shifts;              // [slices] when splits > 1
     int64_t n;
     int64_t params;
     int levels;
@@ -1031,34 +1072,38 @@ struct PackedOwnerArgs {
     int splits;
 };
 
-// Largest |u| of every level's upstream columns, as fp16 magnitude bits (their unsigned order
-// is the magnitude order, NaN above infinity).  bounds must be zero on entry.
-__global__ __launch_bounds__(256) void packed_bound_kernel(PackedOwnerArgs a, uint32_t* bounds) {
-    __shared__ uint32_t peak[ODIE_MAX_LEVELS];
-    if (threadIdx.x < ODIE_MAX_LEVELS) peak[threadIdx.x] = 0u;
+constexpr int kBoundBlock = 256;
+
+// Largest |u| of every upstream column, as fp16 magnitude bits (their unsigned order is the
+// magnitude order, NaN above infinity).  Thread t takes column t % width of every
+// (kBoundBlock / width)-th row.  bounds must be zero on entry; width <= kBoundBlock.
+__global__ __launch_bounds__(kBoundBlock) void packed_bound_kernel(PackedOwnerArgs a, uint32_t* bounds) {
+    __shared__ uint32_t peak[kBoundBlock];
+    peak[threadIdx.x] = 0u;
     __syncthreads();
-    for (int l = 0; l < a.levels; ++l) {
-        const int32_t* d = a.desc + 8 * l;
-        uint32_t mine = 0u;
-        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.n;
-             i += static_cast<int64_t>(gridDim.x) * 256) {
-            const uint16_t* row = a.upstream + static_cast<size_t>(i) * a.width;
-            for (int c = 0; c < d[5]; ++c) {
-                const int col = d[6] + c;
-                if (col < a.width) {
-                    const uint32_t m = row[col] & 0x7fffu;
-                    mine = m > mine ? m : mine;
-                }
-            }
+    const int per = kBoundBlock / a.width;
+    const int column = threadIdx.x % a.width, first = threadIdx.x / a.width;
+    uint32_t mine = 0u;
+    if (first < per) {
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * per + first; i < a.n; i += static_cast<int64_t>(gridDim.x) * per) {
+            const uint32_t m = a.upstream[static_cast<size_t>(i) * a.width + column] & 0x7fffu;
+            mine = m > mine ? m : mine;
         }
-        if (mine) atomicMax(peak + l, mine);
     }
+    if (mine) atomicMax(peak + column, mine);
     __syncthreads();
-    if (threadIdx.x < a.levels && peak[threadIdx.x]) atomicMax(bounds + threadIdx.x, peak[threadIdx.x]);
+    if (threadIdx.x < a.width && peak[threadIdx.x]) atomicMax(bounds + threadIdx.x, peak[threadIdx.x]);
 }
 
 __device__ inline int64_t level_end(const PackedOwnerArgs& a, int l) {
     return l + 1 < a.levels ? static_cast<int64_t>(a.desc[8 * (l + 1) + 2]) : a.params;
+}
+
+// Fixed-point shift of feature c of the level with descriptor d (upstream column d[6] + c).
+__device__ inline int32_t packed_shift(const PackedOwnerArgs& a, const int32_t* d, int c) {
+    const int column = d[6] + c;
+    const uint32_t m = column < a.width ? a.bounds[column] : 0u;
+    return column_shift(__float_as_uint(__half2float(bits_to_half(static_cast<uint16_t>(m)))), a.n);
 }
 
 // Coordinates [b0, b1) against one level of F features (1, 2 or 4; direct or ranked rows):
@@ -1068,9 +1113,12 @@ constexpr int kPackedBatch = 2;   // coordinates per thread per iteration (fits 
 
 template <int F, bool DIRECT>
 __device__ inline void packed_level(const PackedOwnerArgs& a, const int32_t* d, int64_t b0, int64_t b1, int64_t lo,
-                                    int64_t hi, float scale, unsigned long long* acc) {
+                                    int64_t hi, unsigned long long* acc) {
     const int r = d[0], points = d[1], column = d[6];
     const int64_t first = d[2];
+    float scale[F];
+#pragma unroll
+    for (int c = 0; c < F; ++c) scale[c] = shift_scale(packed_shift(a, d, c));
     for (int64_t i0 = b0 + threadIdx.x; i0 < b1; i0 += kPackedBatch * kOwnerBlock) {
         float2 xy[kPackedBatch];
 #pragma unroll
@@ -1090,7 +1138,7 @@ __device__ inline void packed_level(const PackedOwnerArgs& a, const int32_t* d, 
             const uint16_t* row = a.upstream + static_cast<size_t>(i < b1 ? i : b0) * a.width;
 #pragma unroll
             for (int c = 0; c < F; ++c)
-                us[b][c] = column + c < a.width ? __half2float(bits_to_half(row[column + c])) * scale : 0.0f;
+                us[b][c] = column + c < a.width ? __half2float(bits_to_half(row[column + c])) * scale[c] : 0.0f;
         }
         int node[kPackedBatch][4];
         int32_t base[kPackedBatch][4];
@@ -1128,29 +1176,29 @@ __device__ inline void packed_level(const PackedOwnerArgs& a, const int32_t* d, 
     }
 }
 
+// Level of parameter p: the last level whose plane offset is <= p (levels in offset order).
+__device__ inline int packed_level_of(const PackedOwnerArgs& a, int64_t p) {
+    int lo = 0, hi = a.levels - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.desc[8 * mid + 2] <= p) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Shift of parameter p (feature (p - offset) % F of its level).
+__device__ inline int32_t packed_param_shift(const PackedOwnerArgs& a, int64_t p) {
+    const int32_t* d = a.desc + 8 * packed_level_of(a, p);
+    const int features = d[5] > 0 ? d[5] : 1;
+    return packed_shift(a, d, static_cast<int>((p - d[2]) % features));
+}
+
 __global__ __launch_bounds__(kOwnerBlock) void packed_owner_kernel(PackedOwnerArgs a) {
     extern __shared__ unsigned long long acc[];
     const int slice = blockIdx.x / a.splits, s = blockIdx.x % a.splits;
     const int64_t lo = static_cast<int64_t>(slice) * a.cap;
     const int64_t hi = lo + a.cap < a.params ? lo + a.cap : a.params;
     const uint32_t span = static_cast<uint32_t>(hi - lo);
-    // scale from the largest |u| of the levels that meet the slice
-    float peak = 0.0f;
-    for (int l = 0; l < a.levels; ++l) {
-        if (level_end(a, l) <= lo || a.desc[8 * l + 2] >= hi) continue;
-        const float m = __half2float(bits_to_half(static_cast<uint16_t>(a.bounds[l])));
-        peak = (m > peak || m != m) ? m : peak;
-    }
-    const double limit = 4.0 * static_cast<double>(a.n) * static_cast<double>(peak);
-    int shift = 60;
-    if (peak > 0.0f && limit <= 1.0e300) {
-        const int by_value = 30 - ilogb(peak);
-        const int by_sum = 61 - ilogb(limit);
-        shift = by_value < by_sum ? by_value : by_sum;
-    }
-    if (shift > 120) shift = 120;
-    const float scale = ldexpf(1.0f, shift);
-    const bool finite = !(peak != peak) && peak <= 3.0e38f;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) acc[j] = 0ull;
     __syncthreads();
     const int64_t share = (a.n + a.splits - 1) / a.splits;
@@ -1161,27 +1209,22 @@ __global__ __launch_bounds__(kOwnerBlock) void packed_owner_kernel(PackedOwnerAr
         const int32_t* d = a.desc + 8 * l;
         const bool direct = d[7] != 0;
         switch (d[5]) {
-            case 1: direct ? packed_level<1, true>(a, d, b0, b1, lo, hi, scale, acc)
-                           : packed_level<1, false>(a, d, b0, b1, lo, hi, scale, acc); break;
-            case 2: direct ? packed_level<2, true>(a, d, b0, b1, lo, hi, scale, acc)
-                           : packed_level<2, false>(a, d, b0, b1, lo, hi, scale, acc); break;
-            default: direct ? packed_level<4, true>(a, d, b0, b1, lo, hi, scale, acc)
-                            : packed_level<4, false>(a, d, b0, b1, lo, hi, scale, acc); break;
+            case 1: direct ? packed_level<1, true>(a, d, b0, b1, lo, hi, acc)
+                           : packed_level<1, false>(a, d, b0, b1, lo, hi, acc); break;
+            case 2: direct ? packed_level<2, true>(a, d, b0, b1, lo, hi, acc)
+                           : packed_level<2, false>(a, d, b0, b1, lo, hi, acc); break;
+            default: direct ? packed_level<4, true>(a, d, b0, b1, lo, hi, acc)
+                            : packed_level<4, false>(a, d, b0, b1, lo, hi, acc); break;
         }
     }
     __syncthreads();
     if (a.splits > 1) {
         long long* out = a.partial + static_cast<int64_t>(s) * a.params + lo;
         for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[j]);
-        if (s == 0 && threadIdx.x == 0) a.shifts[slice] = finite ? shift : kNonFinite;
         return;
     }
-    const double unscale = ldexp(1.0, -shift);
-    for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) {
-        float v = static_cast<float>(static_cast<double>(static_cast<long long>(acc[j])) * unscale);
-        if (!finite) v = __builtin_nanf("");
-        a.gradient[lo + j] = v;
-    }
+    for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock)
+        a.gradient[lo + j] = unscaled(static_cast<long long>(acc[j]), packed_param_shift(a, lo + j));
 }
 
 __global__ __launch_bounds__(256) void packed_reduce_kernel(PackedOwnerArgs a) {
@@ -1189,10 +1232,7 @@ __global__ __launch_bounds__(256) void packed_reduce_kernel(PackedOwnerArgs a) {
     for (int64_t x = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; x < a.params; x += stride) {
         long long sum = 0;
         for (int s = 0; s < a.splits; ++s) sum += a.partial[static_cast<int64_t>(s) * a.params + x];
-        const int32_t shift = a.shifts[x / a.cap];
-        float v = static_cast<float>(static_cast<double>(sum) * ldexp(1.0, -shift));
-        if (shift == kNonFinite) v = __builtin_nanf("");
-        a.gradient[x] = v;
+        a.gradient[x] = unscaled(sum, packed_param_shift(a, x));
     }
 }
 
@@ -1245,7 +1285,9 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.remap = in.remap;
     int group = 0;
     int64_t grouped = 0;
-    while (group < L && grouped + static_cast<int64_t>(in.levels[group].size) * F <= cap) {
+    // the coarse group: the leading levels whose values fit the slice, at most kMaxColumns columns
+    while (group < L && grouped + static_cast<int64_t>(in.levels[group].size) * F <= cap &&
+           (group + 1) * F <= kMaxColumns) {
         grouped += static_cast<int64_t>(in.levels[group].size) * F;
         ++group;
     }
@@ -1291,11 +1333,9 @@ int launch_owner_backward(const OwnerLaunch& in) {
         slice_level(l, banded, slices, entries, o.row_bits[l]);
         o.slices[l] = static_cast<int>(slices);
         o.slice_entries[l] = static_cast<int>(entries);
-        o.first_pass[l] = passes;
         passes += static_cast<int>(slices);
     }
     o.group = group;
-    o.passes = passes;
     o.cap = static_cast<int>(cap + F);
 
     // Splits per pass.
@@ -1374,13 +1414,13 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const int64_t records = (in.n + kMaxRows - 1) / kMaxRows;
     const auto align = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
     const size_t planes_bytes = in.planes ? 0 : align(static_cast<size_t>(in.n) * L * F * elem);
-    const size_t max_bytes = in.planes ? 0 : align(static_cast<size_t>(records) * L * 4);
+    const size_t max_bytes = in.planes ? 0 : align(static_cast<size_t>(records) * L * F * 4);
     const size_t total_params = static_cast<size_t>(in.experts) * in.expert_params;
     const bool split = max_splits > 1;
     const size_t partial_bytes = split && !banded ? align(static_cast<size_t>(max_splits) * total_params * 4) : 0;
     const size_t partial64_bytes =
         split && banded ? align(static_cast<size_t>(max_splits) * in.experts * split_floats * 8) : 0;
-    const size_t shift_bytes = split && banded ? align(static_cast<size_t>(in.experts) * passes * 4) : 0;
+    const size_t shift_bytes = split && banded ? align(static_cast<size_t>(in.experts) * L * F * 4) : 0;
     const bool lists = banded && group < L;
     const int parts = [&] {
         const int64_t want = (in.n / in.experts + kBandPart - 1) / kBandPart;
@@ -1516,10 +1556,10 @@ int launch_packed_owner(const float* coords, int64_t n, const uint16_t* upstream
     }
     if (splits < 1) splits = 1;
     const auto align = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
-    const size_t bound_bytes = align(static_cast<size_t>(ODIE_MAX_LEVELS) * 4);
+    if (width > kBoundBlock) return fail("odie_packed_backward: upstream width above 256");
+    const size_t bound_bytes = align(static_cast<size_t>(width) * 4);
     const size_t partial_bytes = splits > 1 ? align(static_cast<size_t>(splits) * params * 8) : 0;
-    const size_t shift_bytes = splits > 1 ? align(static_cast<size_t>(slices) * 4) : 0;
-    char* space = static_cast<char*>(workspace(bound_bytes + partial_bytes + shift_bytes, stream));
+    char* space = static_cast<char*>(workspace(bound_bytes + partial_bytes, stream));
     if (!space) return -1;
     PackedOwnerArgs a{};
     a.coords = coords;
@@ -1531,7 +1571,6 @@ int launch_packed_owner(const float* coords, int64_t n, const uint16_t* upstream
     a.bounds = reinterpret_cast<const uint32_t*>(space);
     a.gradient = gradient;
     a.partial = reinterpret_cast<long long*>(space + bound_bytes);
-    a.shifts = reinterpret_cast<int32_t*>(space + bound_bytes + partial_bytes);
     a.n = n;
     a.params = params;
     a.levels = levels;
@@ -1539,10 +1578,12 @@ int launch_packed_owner(const float* coords, int64_t n, const uint16_t* upstream
     a.cap = static_cast<int>(cap);
     a.splits = static_cast<int>(splits);
     uint32_t* bounds = reinterpret_cast<uint32_t*>(space);
-    if (launch_fill_zero(reinterpret_cast<float*>(bounds), ODIE_MAX_LEVELS, stream)) return -1;
-    int64_t bound_blocks = (n + 255) / 256;
+    if (launch_fill_zero(reinterpret_cast<float*>(bounds), width, stream)) return -1;
+    const int64_t rows_per_block = kBoundBlock / width;
+    int64_t bound_blocks = (n + rows_per_block - 1) / rows_per_block;
     if (bound_blocks > 1024) bound_blocks = 1024;
-    packed_bound_kernel<<<static_cast<uint32_t>(bound_blocks), 256, 0, stream>>>(a, bounds);
+    if (bound_blocks < 1) bound_blocks = 1;
+    packed_bound_kernel<<<static_cast<uint32_t>(bound_blocks), kBoundBlock, 0, stream>>>(a, bounds);
     const size_t shmem = static_cast<size_t>(cap) * 8;
     if (allow_lds(packed_owner_kernel, shmem)) return -1;
     packed_owner_kernel<<<static_cast<uint32_t>(slices * splits), kOwnerBlock, shmem, stream>>>(a);

@@ -54,19 +54,46 @@ __device__ inline __half bits_to_half(uint16_t bits) { return __ushort_as_half(b
 // the same way, with Inf and NaN above every finite value), two 16-bit maxima per dword.
 typedef uint16_t magnitude2 __attribute__((ext_vector_type(2)));
 
-// {max |feature| of level A, max |feature| of level B} from the fp16 feature pairs of two levels.
-__device__ inline uint32_t pair_peak(uint32_t level_a, uint32_t level_b) {
-    const magnitude2 x = __builtin_bit_cast(magnitude2, level_a & 0x7fff7fffu);
-    const magnitude2 y = __builtin_bit_cast(magnitude2, level_b & 0x7fff7fffu);
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_shufflevector(x, y, 0, 2),
-                                                                  __builtin_shufflevector(x, y, 1, 3)));
-}
-
 // Per-half maximum of two such dwords (v_pk_max_u16).
 __device__ inline uint32_t pair_max(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(magnitude2, a),
                                                                   __builtin_bit_cast(magnitude2, b)));
 }
+
+// The two fp16 magnitudes of a feature pair (sign bits cleared): per-feature maxima of such
+// words, taken with pair_max, are each feature's largest |value|.
+__device__ inline uint32_t pair_magnitudes(uint32_t pair) { return pair & 0x7fff7fffu; }
+
+template <int kControl> __device__ inline uint32_t dpp_move(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kControl, 0xF, 0xF, false));
+}
+
+// Per-half maxima of eight dwords over the 32 lanes of a lane group (lanes 0-31 or 32-63; the
+// whole wave active).  A reduction tree that halves the dwords a lane holds at every step: the
+// half-row mirror (lane i <-> i ^ 7 within 8, which flips bit 2) trades dwords 0-3 against 4-7 by
+// bit 2 of the lane, quad swaps by bits 1 and 0, so that lane i holds dword i % 8 over its 8
+// lanes; a rotation by 8 within the row of 16 and a swizzle pairing i with i ^ 16 finish.  Lane i
+// returns the maximum of dword i % 8 over the group (about 30 instructions where eight separate
+// 32-lane reductions take 80).
+__device__ inline uint32_t group_max8(const uint32_t d[8], int lane) {
+    const bool b2 = (lane >> 2) & 1, b1 = (lane >> 1) & 1, b0 = lane & 1;
+    uint32_t x4[4], x2[2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t keep = b2 ? d[k + 4] : d[k], send = b2 ? d[k] : d[k + 4];
+        x4[k] = pair_max(keep, dpp_move<0x141>(send));   // row_half_mirror
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t keep = b1 ? x4[k + 2] : x4[k], send = b1 ? x4[k] : x4[k + 2];
+        x2[k] = pair_max(keep, dpp_move<0x4E>(send));    // quad_perm [2, 3, 0, 1]
+    }
+    const uint32_t keep = b0 ? x2[1] : x2[0], send = b0 ? x2[0] : x2[1];
+    uint32_t x = pair_max(keep, dpp_move<0xB1>(send));  // quad_perm [1, 0, 3, 2]
+    x = pair_max(x, dpp_move<0x128>(x));                  // row_ror:8
+    return pair_max(x, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), 0x401F)));  // xor 16
+}
+
 __device__ inline uint16_t half_to_bits(__half value) { return __half_as_ushort(value); }
 
 }  // namespace odie

@@ -131,7 +131,7 @@ struct MlpArgs {
     uint16_t* dz;             // fp16 [n][in] = fp16(fp16(dL/dx) / 128), or null with planes
     float* partials;          // fp32 [blocks][64*in + 5120]
     uint32_t* planes;         // dz as level-major fp16 pairs [16][n], or null
-    float* blockmax;          // with planes: max |dz| per 128-row record and level [n/128][16]
+    float* blockmax;          // with planes: max |dz| per 128-row record and column [n/128][32] (column 2l + f)
 };
 
 // Forward of one tile: x (B operand of layer 1, KT K steps) -> h1, h2 (B operands of the next

@@ -24,20 +24,6 @@
 namespace odie {
 namespace {
 
-// Per-half maximum of a level-pair dword over the 32 lanes of a lane group (the whole wave
-// active): DPP within rows of 16 lanes (the two quad swaps, half-row mirror, row mirror), then a
-// swizzle that pairs lane i with lane i ^ 16.
-template <int kControl> __device__ inline uint32_t dpp(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kControl, 0xF, 0xF, false));
-}
-__device__ inline uint32_t group_max(uint32_t v) {
-    v = pair_max(v, dpp<0xB1>(v));    // quad_perm [1, 0, 3, 2]
-    v = pair_max(v, dpp<0x4E>(v));    // quad_perm [2, 3, 0, 1]
-    v = pair_max(v, dpp<0x141>(v));   // row_half_mirror
-    v = pair_max(v, dpp<0x140>(v));   // row_mirror
-    return pair_max(v, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F)));  // xor 16
-}
-
 template <int KT> __device__ inline void load_x(const uint16_t* x, int64_t row, bool valid, int g, half8 xb[KT]) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
@@ -185,7 +171,7 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
     constexpr int kNB = P1::kColumnBlocks;   // 32-row blocks of dX
     __shared__ _Float16 w[S::kWeightHalfs];
     __shared__ __attribute__((aligned(16))) _Float16 T[round_rows<KT>() * kRS];
-    __shared__ uint32_t records[kMlpWaves][2][4];   // per wave and lane group: level-pair |dz| maxima
+    __shared__ uint32_t records[kMlpWaves][2][8];   // per wave and lane group: per-feature |dz| maxima of 8 levels
     stage_weights<KT>(a.weights, w);
     __syncthreads();
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
@@ -294,19 +280,16 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                         a.planes[(8 * q + 5 + 2 * g) * a.n + row] = bits[q].w;
                     }
                 }
-                // this round's 128 rows are one record: level-pair maxima over the 32 lanes of
-                // this lane group, then over the four waves (after the barrier below)
-                uint32_t peak[4];
+                // this round's 128 rows are one record: per-feature maxima of the lane group's
+                // eight levels over its 32 lanes (lane s < 8 ends with word s), then over the four
+                // waves (after the barrier below)
+                const uint32_t words[8] = {bits[0].x, bits[0].y, bits[0].z, bits[0].w,
+                                           bits[1].x, bits[1].y, bits[1].z, bits[1].w};
+                uint32_t peak[8];
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    peak[2 * q] = valid ? pair_peak(bits[q].x, bits[q].y) : 0u;
-                    peak[2 * q + 1] = valid ? pair_peak(bits[q].z, bits[q].w) : 0u;
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    peak[j] = group_max(peak[j]);
-                    if (s == 0) records[wave][g][j] = peak[j];
-                }
+                for (int j = 0; j < 8; ++j) peak[j] = valid ? pair_magnitudes(words[j]) : 0u;
+                const uint32_t mine = group_max8(peak, lane);
+                if (s < 8) records[wave][g][s] = mine;
             } else if (valid) {
                 uint16_t* p = a.dz + row * S::kIn;
 #pragma unroll
@@ -327,13 +310,16 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) T[(kXRow + kt * 16 + 8 * g + e) * kRS + column] = xb[kt][e];
         __syncthreads();
-        if (PLANES && threadIdx.x < 16) {
-            // level L = 8q + 4h + 2g + b sits in word 2q + h of lane group g, half b
-            const int level = threadIdx.x, q = level / 8, h = (level / 4) % 2, lg = (level / 2) % 2, b = level % 2;
+        if (PLANES && threadIdx.x < 32) {
+            // column 2L + f (level L, feature f); level L = 8q + 4h + 2g + b is word 4q + 2h + b
+            // of lane group g
+            const int level = threadIdx.x / 2, f = threadIdx.x % 2;
+            const int q = level / 8, h = (level / 4) % 2, lg = (level / 2) % 2, b = level % 2;
             uint32_t m = 0;
 #pragma unroll
-            for (int v = 0; v < kMlpWaves; ++v) m = pair_max(m, records[v][lg][2 * q + h]);
-            a.blockmax[(base / kMlpWaves) * 16 + level] = __half2float(bits_to_half(static_cast<uint16_t>(m >> (16 * b))));
+            for (int v = 0; v < kMlpWaves; ++v) m = pair_max(m, records[v][lg][4 * q + 2 * h + b]);
+            a.blockmax[(base / kMlpWaves) * 32 + threadIdx.x] =
+                __half2float(bits_to_half(static_cast<uint16_t>(m >> (16 * f))));
         }
 #pragma unroll
         for (int k = 0; k < P1::kSlots; ++k) {

@@ -88,8 +88,9 @@ class Decoder:
     def train_planes(self, x, real=None, *, colors=None, rgb=None, ids=None, target=None, rows=None, out=None,
                      hidden=None, squares=None, planes=None, blockmax=None):
         """train() with dz written for ExpertGrid.backward_adam_planes: planes int32 [16, n] (the
-        fp16 feature pair of each level and row) and blockmax fp32 [ceil(n/128), 16] (max |dz|
-        per 128-row record and level).  Returns (planes, blockmax).  Width 32 only."""
+        fp16 feature pair of each level and row) and blockmax fp32 [ceil(n/128), 32] (max |dz|
+        per 128-row record and column: level l, feature f at 2l + f).  Returns (planes, blockmax).
+        Width 32 only."""
         if self.width != INPUT:
             raise ValueError('the planes layout is built for width 32 (16 levels x 2 features)')
         x = _features(x, self.width)
@@ -101,11 +102,12 @@ class Decoder:
         if planes is None:
             planes = torch.empty((LEVELS, n), dtype=torch.int32, device=x.device)
         if blockmax is None:
-            blockmax = torch.empty((records, LEVELS), dtype=torch.float32, device=x.device)
+            blockmax = torch.empty((records, 2 * LEVELS), dtype=torch.float32, device=x.device)
         if tuple(planes.shape) != (LEVELS, n) or planes.dtype != torch.int32 or not planes.is_contiguous():
             raise ValueError('planes must be a contiguous int32 [16, n] tensor')
-        if tuple(blockmax.shape) != (records, LEVELS) or blockmax.dtype != torch.float32 or not blockmax.is_contiguous():
-            raise ValueError('blockmax must be a contiguous fp32 [ceil(n/128), 16] tensor')
+        if (tuple(blockmax.shape) != (records, 2 * LEVELS) or blockmax.dtype != torch.float32
+                or not blockmax.is_contiguous()):
+            raise ValueError('blockmax must be a contiguous fp32 [ceil(n/128), 32] tensor')
         _lib.check(_lib.library().odie_mlp_train_planes(
             x.data_ptr(), n, real, self.half.data_ptr(), _lib.ptr(colors), _lib.ptr(rgb), _lib.ptr(ids),
             _lib.ptr(target), _lib.ptr(rows), _lib.ptr(out), _lib.ptr(hidden), _lib.ptr(squares), planes.data_ptr(),

@@ -108,16 +108,16 @@ class ExpertGrid:
 
     def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0):
         """backward_adam with the fp16 upstream given as Decoder.train_planes writes it (planes
-        int32 [levels, N], blockmax fp32 [ceil(N/128), levels]): the same update, bit for bit."""
+        int32 [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same update, bit for bit."""
         from .encoding import _check_coords, _offsets_arg
         _check_coords(coords)
         n = coords.shape[0]
         levels = len(self.levels)
         if tuple(planes.shape) != (levels, n) or planes.dtype != torch.int32 or not planes.is_contiguous():
             raise ValueError('planes must be a contiguous int32 [levels, N] tensor')
-        if (tuple(blockmax.shape) != ((n + 127) // 128, levels) or blockmax.dtype != torch.float32
+        if (tuple(blockmax.shape) != ((n + 127) // 128, 2 * levels) or blockmax.dtype != torch.float32
                 or not blockmax.is_contiguous()):
-            raise ValueError('blockmax must be a contiguous fp32 [ceil(N/128), levels] tensor')
+            raise ValueError('blockmax must be a contiguous fp32 [ceil(N/128), 2 levels] tensor')
         if optimizer.master.numel() != self.experts * self.expert_params:
             raise ValueError('the optimizer must own this table\'s fp32 master')
         offsets = _offsets_arg(offsets, self.experts, n)

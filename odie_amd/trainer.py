@@ -85,7 +85,7 @@ class ExpertTrainer:
         self.planes = planes and fused and not router
         if self.planes:
             self.plane_buffer = torch.empty(16 * batch, dtype=torch.int32, device=device)
-            self.max_buffer = torch.empty(16 * ((batch + 127) // 128), dtype=torch.float32, device=device)
+            self.max_buffer = torch.empty(32 * ((batch + 127) // 128), dtype=torch.float32, device=device)
         if self.grid.width != 32:
             raise ValueError('the decoder takes 32 input features (16 levels x 2)')
 
@@ -113,7 +113,7 @@ class ExpertTrainer:
         if self.planes and update:
             planes, blockmax = self.decoder.train_planes(
                 features, n, colors=view.colors, squares=self.squares[:n], planes=self.plane_buffer[:16 * n].view(16, n),
-                blockmax=self.max_buffer[:16 * ((n + 127) // 128)].view(-1, 16))
+                blockmax=self.max_buffer[:32 * ((n + 127) // 128)].view(-1, 32))
             mark('decoder')
             self.grid.backward_adam_planes(view.coords, view.offsets, planes, blockmax, self.grid_optimizer,
                                            loss_scale=GRID_SCALE)

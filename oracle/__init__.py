@@ -78,10 +78,10 @@ def lib():
         handle.ora_f2h.argtypes, handle.ora_f2h.restype = [C.c_float], C.c_uint16
         handle.ora_hfma.argtypes, handle.ora_hfma.restype = [C.c_uint16] * 3, C.c_uint16
         handle.ora_hash_forward.argtypes = [P, P, I, I64, P, I, P, I, I, I, P, I]
-        handle.ora_hash_backward.argtypes = [P, P, I, I64, P, I, P, I, I, I, P, P]
+        handle.ora_hash_backward.argtypes = [P, P, I, I64, P, I, P, I, I, I, P, P, P]
         handle.ora_hash_backward_f32.argtypes = [P, P, I, I64, P, P, I, I, I, P, I]
         handle.ora_packed_forward.argtypes = [P, I64, P, P, I, P, P, P, I, P, P, I]
-        handle.ora_packed_backward.argtypes = [P, I64, P, I, P, I, P, P, P, P, P]
+        handle.ora_packed_backward.argtypes = [P, I64, P, I, P, I, P, P, P, P, P, P]
         handle.ora_residual.argtypes = [P, P, I, I64, I64, I, I, P, P, P]
         handle.ora_adam.argtypes = [I, P, P, P, P, P, I64, I64, C.c_double, C.c_double, C.c_double,
                                     C.c_double, C.c_double]
@@ -166,20 +166,22 @@ def hash_forward(xy, table, rows, features, *, offsets=None, expert_params=None,
     return out
 
 
-def hash_backward(xy, upstream, rows, features, total, *, offsets=None, expert_params=None):
-    """(gradient fp64 [total], magnitude fp64 [total]) -- exact-order-free checker."""
+def hash_backward(xy, upstream, rows, features, total, *, offsets=None, expert_params=None, counts=False):
+    """(gradient fp64 [total], magnitude fp64 [total]) -- exact-order-free checker; with counts,
+    also the number of contributions of every entry (fp64 [total])."""
     xy = np.ascontiguousarray(xy, dtype=np.float32)
     upstream = np.ascontiguousarray(upstream)
     offsets, experts = _offsets(offsets, len(xy))
     expert_params = expert_params or total // experts
     grad = np.zeros(total, dtype=np.float64)
     magnitude = np.zeros(total, dtype=np.float64)
+    count = np.zeros(total, dtype=np.float64) if counts else None
     half = upstream.dtype == np.float16
     values = upstream.view(np.uint16) if half else np.ascontiguousarray(upstream, dtype=np.float32)
     lib().ora_hash_backward(_p(xy), _p(offsets), experts, expert_params, _p(values),
                             1 if half else 0, _levels(rows), len(rows), features, upstream.shape[1],
-                            _p(grad), _p(magnitude))
-    return grad, magnitude
+                            _p(grad), _p(magnitude), _p(count))
+    return (grad, magnitude, count) if counts else (grad, magnitude)
 
 
 def hash_backward_f32(xy, upstream, rows, features, total, *, offsets=None, expert_params=None, threads=1):
@@ -212,7 +214,7 @@ def packed_forward(xy, grid, layout, width, threads=1):
     return out, vis.astype(bool)
 
 
-def packed_backward(xy, upstream, layout, total):
+def packed_backward(xy, upstream, layout, total, counts=False):
     xy = np.ascontiguousarray(xy, dtype=np.float32)
     upstream = np.ascontiguousarray(upstream, dtype=np.float16)
     desc = np.ascontiguousarray(layout['descriptors'], dtype=np.int32)
@@ -221,9 +223,11 @@ def packed_backward(xy, upstream, layout, total):
     bitmap = np.ascontiguousarray(layout['bitmap'], dtype=np.uint8)
     grad = np.zeros(total, dtype=np.float64)
     magnitude = np.zeros(total, dtype=np.float64)
+    count = np.zeros(total, dtype=np.float64) if counts else None
     lib().ora_packed_backward(_p(xy), len(xy), _p(upstream.view(np.uint16)), upstream.shape[1], _p(desc),
-                              len(desc), _p(node_bitmap), _p(prefix), _p(bitmap), _p(grad), _p(magnitude))
-    return grad, magnitude
+                              len(desc), _p(node_bitmap), _p(prefix), _p(bitmap), _p(grad), _p(magnitude),
+                              _p(count))
+    return (grad, magnitude, count) if counts else (grad, magnitude)
 
 
 # ---------------------------------------------------------------------------------------

@@ -236,11 +236,12 @@ API void ora_hash_forward(const float* xy, const int64_t* offsets, int experts, 
 
 /* Backward checker: grad[param] = sum of w_k * upstream over every (coordinate, corner)
  * that reads it, in double, plus the sum of absolute contributions (the scale of the
- * allowed fp32 summation error).  Zero upstream values are skipped, as in
+ * allowed fp32 summation error) and, when count is not null, the number of contributions
+ * (each one rounded once by a fixed-point sum).  Zero upstream values are skipped, as in
  * odie/packed_kernels.cu:79-80.  upstream is fp16 [n, width] (dtype 1) or fp32. */
 API void ora_hash_backward(const float* xy, const int64_t* offsets, int experts, int64_t expert_params,
                            const void* upstream, int up_dtype, const ora_level* levels, int n_levels,
-                           int features, int width, double* grad, double* magnitude) {
+                           int features, int width, double* grad, double* magnitude, double* count) {
     const int64_t n = offsets[experts];
     for (int64_t i = 0; i < n; ++i) {
         const int e = expert_of(offsets, experts, i);
@@ -259,6 +260,7 @@ API void ora_hash_backward(const float* xy, const int64_t* offsets, int experts,
                     const int64_t p = base + ((int64_t)lv->offset + idx[k]) * features + c;
                     grad[p] += (double)add;
                     if (magnitude) magnitude[p] += fabs((double)add);
+                    if (count) count[p] += 1.0;
                 }
             }
         }
@@ -360,7 +362,8 @@ API void ora_packed_forward(const float* xy, int64_t n, const float* grid, const
 
 API void ora_packed_backward(const float* xy, int64_t n, const uint16_t* upstream, int width,
                              const int32_t* descriptors, int n_levels, const uint64_t* node_bitmap,
-                             const int32_t* prefix, const uint8_t* bitmap, double* grad, double* magnitude) {
+                             const int32_t* prefix, const uint8_t* bitmap, double* grad, double* magnitude,
+                             double* count) {
     for (int64_t i = 0; i < n; ++i) {
         for (int l = 0; l < n_levels; ++l) {
             const int32_t* d = descriptors + 8 * l;
@@ -378,6 +381,7 @@ API void ora_packed_backward(const float* xy, int64_t n, const uint16_t* upstrea
                     const int64_t p = d[2] + (int64_t)row * d[5] + c;
                     grad[p] += (double)add;
                     if (magnitude) magnitude[p] += fabs((double)add);
+                    if (count) count[p] += 1.0;
                 }
             }
         }

@@ -109,9 +109,9 @@ def test_grid_backward_adam_planes_equals_rows(experts, n, variant):
     for step in range(2):
         upstream = torch.from_numpy(synth.upstream(10 + step, n, 32)).cuda()
         planes = upstream.view(torch.int32).t().contiguous()
-        level = torch.zeros((records * 128, 16), dtype=torch.float32, device='cuda')
-        level[:n] = upstream.abs().view(n, 16, 2).amax(dim=2).float()
-        blockmax = level.view(records, 128, 16).amax(dim=1).contiguous()
+        column = torch.zeros((records * 128, 32), dtype=torch.float32, device='cuda')
+        column[:n] = upstream.abs().view(n, 32).float()
+        blockmax = column.view(records, 128, 32).amax(dim=1).contiguous()
         grids[0].backward_adam_planes(coords, offsets, planes, blockmax, optimizers[0], loss_scale=128.0)
         grids[1].backward_adam(coords, offsets, upstream, optimizers[1], loss_scale=128.0)
     for name in ('master', 'm', 'v'):

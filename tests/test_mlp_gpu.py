@@ -134,13 +134,13 @@ def test_empty_batch_zeroes_weight_gradient():
 
 
 def _record_maxima(dz):
-    """max |dz| per 128-row record and level (torch's amax keeps NaN), fp32 [ceil(n/128), 16]."""
+    """max |dz| per 128-row record and column (torch's amax keeps NaN), fp32 [ceil(n/128), 32]."""
     n = dz.shape[0]
     records = (n + 127) // 128
-    level = dz.abs().view(n, 16, 2).amax(dim=2).float()
-    padded = torch.zeros((records * 128, 16), dtype=torch.float32, device=dz.device)
-    padded[:n] = level
-    return padded.view(records, 128, 16).amax(dim=1)
+    column = dz.abs().view(n, 32).float()
+    padded = torch.zeros((records * 128, 32), dtype=torch.float32, device=dz.device)
+    padded[:n] = column
+    return padded.view(records, 128, 32).amax(dim=1)
 
 
 @pytest.mark.parametrize('n,poison', [(1, False), (1000, False), (4096 + 37, False), (1 << 17, False), (3000, True)])

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import oracle
+from oracle.bounds import check_gradient, hash_quantum, packed_quantum
 from odie_amd import _lib, synth
 from odie_amd.config import grid_levels
 from odie_amd.decoder import Decoder
@@ -406,11 +407,9 @@ def _coordinates(ids_host, width, height):
     return np.stack([(ids_host % width).astype(np.float32) * rx, (ids_host // width).astype(np.float32) * ry], 1)
 
 
-def _check_gradient(grid_grad, grad, magnitude):
-    """fp32 atomics or fixed point: order only."""
-    bound = 1e-4 * magnitude + 2.0 ** -32 * float(magnitude.max(initial=0.0)) + 1e-30
-    bad = np.abs(grid_grad.astype(np.float64) - grad) > bound
-    assert not bad.any(), '%d/%d gradient entries out of tolerance' % (bad.sum(), bad.size)
+def _check_gradient(grid_grad, grad, magnitude, counts, quantum):
+    """fp32 atomics or fixed point: order and each entry's quantum only."""
+    check_gradient(grid_grad, grad, magnitude, counts, quantum, 'runtime grid gradient')
 
 
 @pytest.mark.parametrize('shape,router,active', [('div2k', True, 16), ('L20', True, 13), ('16x2', False, 11)])
@@ -450,7 +449,8 @@ def test_packed_step_matches_oracle(shape, router, active):
         visible[:, active:] = False
         assert np.array_equal(raw.cpu().numpy().view(np.uint16), expected.view(np.uint16))
         up = _heads_match_oracle(raw, visible, dims, coarse, gate0, decoder0, image, ids, got)
-        _check_gradient(got['grid_grad'], *oracle.packed_backward(xy, up, layout, grid0.size))
+        _check_gradient(got['grid_grad'], *oracle.packed_backward(xy, up, layout, grid0.size, counts=True),
+                        packed_quantum(up, layout, grid0.size))
 
         def adam(variant, start, gradient, lr):
             m, v = np.zeros(start.size), np.zeros(start.size)
@@ -502,7 +502,8 @@ def test_hash_step_matches_oracle(router, coarse, levels, features):
         assert np.array_equal(raw.cpu().numpy().view(np.uint16), expected.view(np.uint16))
         up = _heads_match_oracle(raw, None, dims, coarse, gate0, decoder0, image, ids, got)
         _check_gradient(got['grid_grad'], *oracle.hash_backward(xy, up, rows, features, grid0.size,
-                                                                expert_params=grid0.size))
+                                                                expert_params=grid0.size, counts=True),
+                        hash_quantum(up, rows, features, grid0.size))
         assert np.array_equal(_bits(model.grid), grid0.view(np.uint32))
         assert np.array_equal(_bits(model.decoder.params), decoder0.view(np.uint32))
         opt.close()

@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import oracle
+from oracle.bounds import check_gradient, hash_quantum
 from odie_amd import synth
 from odie_amd.trainer import ExpertTrainer
 
@@ -71,10 +72,12 @@ def test_training_step_matches_oracle(regions, batch, n):
 
     # grid gradient from the GPU's dz (loss scale 128)
     total = trainer.grid.table.numel()
-    grad, magnitude = oracle.hash_backward(local, dz, rows, 2, total, offsets=offsets,
-                                           expert_params=trainer.grid.expert_params)
+    params = trainer.grid.expert_params
+    grad, magnitude, counts = oracle.hash_backward(local, dz, rows, 2, total, offsets=offsets, expert_params=params,
+                                                   counts=True)
     got = trainer.gradient.cpu().numpy().astype(np.float64)
-    assert np.all(np.abs(got - grad) <= 1e-4 * magnitude + 2.0 ** -32 * magnitude.max() + 1e-30)
+    check_gradient(got, grad, magnitude, counts, hash_quantum(dz, rows, 2, total, offsets=offsets,
+                                                              expert_params=params), 'step')
 
     # Adam: grid (per-parameter ages, zero gradients skipped, scale 128) and decoder
     # (per-parameter ages, no skip, scale 16384), each from the GPU's gradient
