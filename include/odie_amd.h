@@ -7,6 +7,9 @@
  *  - streams are hipStream_t values passed as uint64_t (0 = the null stream);
  *  - functions return 0 on success and -1 on failure, leaving a message that
  *    odie_error() returns (thread-local, valid until the next failing call on the thread);
+ *    selection_init, selection_chunk and score_chunk, whose reference counterparts return the
+ *    CUDA runtime's error code, return the HIP runtime's instead (hipErrorInvalidValue for a
+ *    refused argument, the launch's code for a failed launch), with the message set as well;
  *  - arguments are validated before any device work is queued, so a call that fails has
  *    queued nothing;
  *  - fp16 data is IEEE binary16 (uint16_t bit patterns on the host side);

@@ -15,6 +15,13 @@ namespace odie {
 std::string& error_slot();
 int fail(const std::string& message);
 int check_launch(const char* what);
+// For the entry points whose reference counterparts return the CUDA runtime's error code
+// (selection_init, selection_chunk, score_chunk: `return int(cudaGetLastError())`, turned into a
+// message by the caller through the runtime's error-string call): the HIP runtime's code instead
+// of -1 -- hipErrorInvalidValue for a refused argument, the launch's own code for a failed
+// launch -- with the message left in odie_error() as well.
+int fail_code(const std::string& message, hipError_t code = hipErrorInvalidValue);
+int launch_code(const char* what);
 // Library-owned device scratch of at least `bytes`, one buffer per device, grown on demand (at
 // least doubling; an outgrown buffer is kept until the process ends, so work already queued or
 // captured in a graph keeps a valid address; steady-state calls allocate nothing).  Calls that

@@ -24,6 +24,17 @@ int check_launch(const char* what) {
     return 0;
 }
 
+int fail_code(const std::string& message, hipError_t code) {
+    error_slot() = message;
+    return static_cast<int>(code);
+}
+
+int launch_code(const char* what) {
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess) return fail_code(std::string(what) + ": " + hipGetErrorString(status), status);
+    return 0;
+}
+
 void* workspace(size_t bytes, hipStream_t stream) {
     static std::mutex lock;
     static std::map<int, std::pair<void*, size_t>> buffers;

@@ -357,17 +357,19 @@ ODIE_API int64_t odie_selection_tree_ints(int n) {
     return tree_ints(tree_shape(n));
 }
 
-// Same signature as selection_init (odie/native/selection_cuda.cu:208-220).  host_offsets /
+// Same signature as selection_init (odie/native/selection_cuda.cu:208-220), and the same failure
+// value: the runtime's error code (hipErrorInvalidValue for a refused argument), the message in
+// odie_error().  host_offsets /
 // host_sizes / levels describe the caller's fan-32 tree allocation; this selector lays out its
 // own fan-64 tree, which needs no more ints than that allocation (checked when given).
 ODIE_API int selection_init(const double* scores, int n, int points, int* missing, uint8_t* chosen, uint8_t* nodes,
                             int* tree, int64_t* stats, const int* host_offsets, const int* host_sizes, int levels,
                             uint64_t stream) {
-    if (check_common("selection_init", scores, n, points, missing, chosen, nodes, tree, stats)) return -1;
+    if (check_common("selection_init", scores, n, points, missing, chosen, nodes, tree, stats)) return hipErrorInvalidValue;
     const TreeShape shape = tree_shape(n);
     if (host_offsets && host_sizes && levels > 0) {
         const int64_t available = static_cast<int64_t>(host_offsets[levels - 1]) + 5LL * host_sizes[levels - 1];
-        if (available < tree_ints(shape)) return fail("selection_init: tree buffer too small");
+        if (available < tree_ints(shape)) return fail_code("selection_init: tree buffer too small");
     }
     GreedyArgs a{};
     a.scores = scores;
@@ -386,7 +388,7 @@ ODIE_API int selection_init(const double* scores, int n, int points, int* missin
         const int64_t waves = shape.size[level] * kCats;
         build_kernel<<<static_cast<uint32_t>((waves + 3) / 4), 256, 0, s>>>(a, level);
     }
-    return check_launch("selection_init");
+    return launch_code("selection_init");
 }
 
 // Same signature as selection_chunk (odie/native/selection_cuda.cu:222-230); offsets, sizes and
@@ -398,11 +400,11 @@ ODIE_API int selection_chunk(const double* scores, int n, int points, int resolu
     (void)offsets;
     (void)sizes;
     (void)levels;
-    if (check_common("selection_chunk", scores, n, points, missing, chosen, nodes, tree, stats)) return -1;
+    if (check_common("selection_chunk", scores, n, points, missing, chosen, nodes, tree, stats)) return hipErrorInvalidValue;
     if (resolution < 2 || static_cast<int64_t>(resolution) * resolution != n)
-        return fail("selection_chunk: n must be resolution^2");
-    if (cap < 0 || cap % 8 || cap > points) return fail("selection_chunk: cap must be 8-aligned within points");
-    if (chunk < 1) return fail("selection_chunk: chunk must be positive");
+        return fail_code("selection_chunk: n must be resolution^2");
+    if (cap < 0 || cap % 8 || cap > points) return fail_code("selection_chunk: cap must be 8-aligned within points");
+    if (chunk < 1) return fail_code("selection_chunk: chunk must be positive");
     GreedyArgs a{};
     a.scores = scores;
     a.missing = missing;
@@ -419,5 +421,5 @@ ODIE_API int selection_chunk(const double* scores, int n, int points, int resolu
     a.chunk = chunk;
     a.shape = tree_shape(n);
     greedy_kernel<<<1, kGreedyBlock, static_cast<size_t>(a.shape.lds_ints) * 4, as_stream(stream)>>>(a);
-    return check_launch("selection_chunk");
+    return launch_code("selection_chunk");
 }

@@ -103,16 +103,17 @@ ODIE_API int odie_cell_bounds(int width, int height, int resolution, int32_t* xb
 // Same signature and meaning as score_chunk (odie/residual_cuda.cu:45-52): pixels [begin, end)
 // of a width-wide image, prediction fp32 [end-begin, 3], target uint8 or fp32 [end-begin, 3],
 // cells of rows first_y.. (active_cells of them) with column/row bounds xb[R+1], yb[R+1];
-// totals (fp64 [R*R]) are read and updated.  Returns 0 or -1 (see odie_error).
+// totals (fp64 [R*R]) are read and updated.  Returns 0, or the runtime's error code as the
+// reference does (hipErrorInvalidValue for a refused argument; the message in odie_error()).
 ODIE_API int score_chunk(const float* prediction, const void* target, int64_t begin, int64_t end, int width,
                          int resolution, int first_y, int active_cells, const int* xb, const int* yb, double* totals,
                          bool rgb8, uint64_t stream) {
-    if (width < 1 || resolution < 1) return fail("score_chunk: width and resolution must be positive");
-    if (begin < 0 || end < begin) return fail("score_chunk: need 0 <= begin <= end");
+    if (width < 1 || resolution < 1) return fail_code("score_chunk: width and resolution must be positive");
+    if (begin < 0 || end < begin) return fail_code("score_chunk: need 0 <= begin <= end");
     if (first_y < 0 || active_cells < 0 || first_y + (active_cells + resolution - 1) / resolution > resolution)
-        return fail("score_chunk: cell rows out of range");
+        return fail_code("score_chunk: cell rows out of range");
     if (end == begin || active_cells == 0) return 0;
-    if (!prediction || !target || !xb || !yb || !totals) return fail("score_chunk: null pointer");
+    if (!prediction || !target || !xb || !yb || !totals) return fail_code("score_chunk: null pointer");
     const uint32_t blocks = static_cast<uint32_t>((active_cells + kResidualBlock - 1) / kResidualBlock);
     const hipStream_t s = as_stream(stream);
     if (rgb8)
@@ -121,5 +122,5 @@ ODIE_API int score_chunk(const float* prediction, const void* target, int64_t be
     else
         accumulate_kernel<false><<<blocks, kResidualBlock, 0, s>>>(prediction, target, begin, end, width, resolution,
                                                                    first_y, active_cells, xb, yb, totals);
-    return check_launch("score_chunk");
+    return launch_code("score_chunk");
 }

@@ -10,6 +10,9 @@ from odie_amd import _lib
 from odie_amd.config import grid_levels
 
 
+HIP_ERROR_INVALID_VALUE = 1   # hipErrorInvalidValue
+
+
 def test_every_declared_symbol_is_exported(native):
     declared = _lib.declared_symbols()
     assert 'odie_grid_forward' in declared and 'odie_error' in declared
@@ -93,7 +96,7 @@ def test_route_rejects_bad_arguments(native):
 
 
 def test_selection_entry_points_reject_bad_arguments(native):
-    assert native.score_chunk(8, 8, 5, 3, 10, 4, 0, 4, 8, 8, 8, True, 0) == -1
+    assert native.score_chunk(8, 8, 5, 3, 10, 4, 0, 4, 8, 8, 8, True, 0) == HIP_ERROR_INVALID_VALUE
     assert 'begin' in native.odie_error().decode()
     assert native.odie_topk(8, 10, 11, 8, 0) == -1
     assert 'k must be' in native.odie_error().decode()
@@ -150,16 +153,44 @@ def test_selection_entry_points_reject_bad_arguments(native):
     assert 'step' in native.odie_error().decode()
     # greedy selector: n must be resolution^2, cap 8-aligned, chunk positive, tree large enough
     args = [8, 4096, 4096, 63, 256, True, 8, 8, 8, 8, None, None, 0, 512, 8, None, 0]
-    assert native.selection_chunk(*args) == -1 and 'resolution^2' in native.odie_error().decode()
+    refused = HIP_ERROR_INVALID_VALUE
+    assert native.selection_chunk(*args) == refused and 'resolution^2' in native.odie_error().decode()
     args[3], args[4] = 64, 100
-    assert native.selection_chunk(*args) == -1 and 'cap' in native.odie_error().decode()
+    assert native.selection_chunk(*args) == refused and 'cap' in native.odie_error().decode()
     args[4], args[13] = 256, 0
-    assert native.selection_chunk(*args) == -1 and 'chunk' in native.odie_error().decode()
+    assert native.selection_chunk(*args) == refused and 'chunk' in native.odie_error().decode()
     offsets, sizes = (C.c_int * 1)(0), (C.c_int * 1)(10)
-    assert native.selection_init(8, 4096, 4096, 8, 8, 8, 8, 8, offsets, sizes, 1, 0) == -1
+    assert native.selection_init(8, 4096, 4096, 8, 8, 8, 8, 8, offsets, sizes, 1, 0) == refused
     assert 'too small' in native.odie_error().decode()
-    assert native.selection_init(8, 4096, 4100, 8, 8, 8, 8, 8, None, None, 0, 0) == -1
+    assert native.selection_init(8, 4096, 4100, 8, 8, 8, 8, 8, None, None, 0, 0) == refused
     assert 'points' in native.odie_error().decode()
+
+
+def test_reference_check_of_the_runtime_code(native):
+    """selection_init, selection_chunk and score_chunk fail as the reference's do, with the
+    runtime's error code (odie/native/selection_cuda.cu:217,229, odie/residual_cuda.cu:51:
+    `return int(cudaGetLastError())`), so the reference's unchanged check -- a nonzero result
+    raises RuntimeError with the runtime's string for it (odie/selection_cuda.py:49-51) -- run on
+    the HIP runtime raises with that string, and odie_error() keeps this library's message."""
+    runtime = C.CDLL('libamdhip64.so')
+    runtime.hipGetErrorString.argtypes = [C.c_int]
+    runtime.hipGetErrorString.restype = C.c_char_p
+
+    def check(result):   # the reference's Cuda.check, with the HIP runtime's error string
+        if result:
+            raise RuntimeError(runtime.hipGetErrorString(result).decode())
+
+    check(native.score_chunk(None, None, 0, 0, 8, 4, 0, 0, None, None, None, True, 0))   # nothing to do
+    calls = [
+        (lambda: native.score_chunk(8, 8, 5, 3, 10, 4, 0, 4, 8, 8, 8, True, 0), 'score_chunk: need 0 <= begin'),
+        (lambda: native.selection_init(8, 4096, 4100, 8, 8, 8, 8, 8, None, None, 0, 0), 'selection_init: points'),
+        (lambda: native.selection_chunk(8, 4096, 4096, 63, 256, True, 8, 8, 8, 8, None, None, 0, 512, 8, None, 0),
+         'selection_chunk: n must be resolution^2'),
+    ]
+    for call, message in calls:
+        with pytest.raises(RuntimeError, match='invalid argument'):
+            check(call())
+        assert native.odie_error().decode().startswith(message)
 
 
 def test_selection_tree_fits_the_callers_fan32_allocation(native):
