@@ -183,8 +183,9 @@ int odie_route_stratified(const float* uniforms, int64_t n, int width, int heigh
  * counterpart in the reference.  It allocates nothing: its scratch is a static device array of
  * ODIE_ROUTE_NOALLOC_BYTES (4 MiB + 64 KiB) that every GPU the library runs on holds until the
  * process ends, resolved once per device.  Calls whose odie_route_workspace(n, E) exceeds it
- * fail (-1, nothing queued): up to 2^24 ids over 64 experts, 2^22 over 256 and 2^18 over
- * 4096 fit.  Every call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * fail (-1, nothing queued): up to 2^23 ids over 64 experts, 2^21 over 256, 2^19 over 1024 and
+ * 2^17 over 4096 fit (exactly: n <= 8510976, 2127360, 531456 and 132608); 2^24 ids over 64
+ * experts do not.  Every call on one GPU shares that GPU's array, so calls that overlap on one GPU
  * (different streams without ordering, or several host threads) race and give wrong results.
  * Same outputs as odie_route, bit for bit. */
 #define ODIE_ROUTE_NOALLOC_BYTES ((int64_t)((4 << 20) + (64 << 10)))

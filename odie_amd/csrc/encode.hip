@@ -528,7 +528,9 @@ __global__ __launch_bounds__(kBlock) void packed_forward_pairs_kernel(PackedArgs
                 for (int k = 0; k < 4; ++k) {
                     const int64_t at = plane_param(a, d, cell, k, 0);
                     if (two) {
-                        g[k] = *reinterpret_cast<const float2*>(a.grid + at);
+                        // even, both features inside; a clamped index (descriptors out of step with
+                        // the bitmaps) stays an aligned pair inside the grid (params is a multiple of 8)
+                        g[k] = *reinterpret_cast<const float2*>(a.grid + (at < a.params - 1 ? at : a.params - 2));
                     } else {
                         g[k].x = a.grid[at];
                         g[k].y = 0.0f;

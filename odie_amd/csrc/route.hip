@@ -19,6 +19,7 @@
 //           No global atomics, so the result is deterministic.
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 
 #include "common.h"
@@ -548,13 +549,28 @@ void staged_shape(int experts, int part, int& waves, int& group) {
     group = 0;
 }
 
+// The staged scatter's dynamic LDS limit, raised to the whole staging budget once per device
+// and kernel shape (not per call: a call under graph capture then makes no attribute change).
+template <int W>
+int allow_staging() {
+    static std::mutex lock;
+    static std::set<int> devices;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return fail("odie_route: no current device");
+    std::lock_guard<std::mutex> guard(lock);
+    if (devices.count(device)) return 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(route_scatter_staged_kernel<W>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kStagingBudget)) != hipSuccess)
+        return fail("odie_route: LDS attribute of the staged scatter");
+    devices.insert(device);
+    return 0;
+}
+
 template <int W>
 int launch_staged(const RouteArgs& a, int group, hipStream_t s) {
     const uint32_t groups = round_up(static_cast<uint32_t>((a.parts + group - 1) / group), kXcds);
     const size_t staging = staging_bytes(a.experts, a.part, W, group);
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(route_scatter_staged_kernel<W>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(staging)) != hipSuccess)
-        return fail("odie_route: LDS attribute of the staged scatter");
+    if (allow_staging<W>()) return -1;
     route_scatter_staged_kernel<W><<<groups, 64 * W, staging, s>>>(a, group);
     return 0;
 }
