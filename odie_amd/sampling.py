@@ -32,40 +32,57 @@ def stratified_batches(shape, batch, generator, device='cuda'):
         yield stratified_ids(torch.rand((batch, 2), device=device, generator=generator), shape)
 
 
+# Batch generators of the reference's sampling modes (odie/data.py:47-106).  The torch RNG is
+# consumed in the reference's order and sizes (one randperm over the pixels for 'global' and
+# 'global_full'; for 'chunked' one over the chunks, then one per chunk as it is visited), so a
+# seeded generator yields the same ids.  The permutations are cut into batches by _cut.
+
+def _cut(order, batch, *, base=0, wrap=False, device=None):
+    """Consecutive slices of `batch` entries of a 1-D permutation, plus `base`.  With wrap, the
+    last slice is completed from the start of the permutation (positions taken modulo its
+    length), so every batch is full; with device, slices move there as int64."""
+    total = order.numel()
+    for first in range(0, total, batch):
+        if wrap and first + batch > total:
+            ids = order[(first + torch.arange(batch, device=order.device)) % total]
+        else:
+            ids = order[first:first + batch]
+        if device is not None:
+            ids = ids.to(device=device, dtype=torch.int64)
+        yield ids + base if base else ids
+
+
 def full_batches(pixels, batch, generator, device='cuda'):
-    """A global permutation once, padded with its beginning (odie/data.py:47-60)."""
-    dtype = torch.int32 if pixels <= 2 ** 31 - 1 else torch.int64
+    """Every pixel once in a permutation drawn on the generator's device (CPU for giant images;
+    int32 while the ids fit), the last batch completed from its start; each batch moves to
+    `device` as int64 on its own (odie/data.py:47-60)."""
+    dtype = torch.int32 if pixels < 2 ** 31 else torch.int64
     order = torch.randperm(pixels, dtype=dtype, device=generator.device, generator=generator)
-    for begin in range(0, pixels, batch):
-        ids = order[begin:begin + batch]
-        if ids.numel() < batch:
-            padding = torch.arange(batch - ids.numel(), device=order.device) % pixels
-            ids = torch.cat((ids, order[padding]))
-        yield ids.to(device=device, dtype=torch.int64)
+    yield from _cut(order, batch, wrap=True, device=device)
+
+
+def _chunked(pixels, batch, generator, chunk, device):
+    if chunk <= 0 or chunk % batch:
+        raise ValueError('Chunk size must be a positive multiple of batch size')
+    chunks = -(-pixels // chunk)
+    for k in torch.randperm(chunks, device=device, generator=generator).cpu().tolist():
+        size = min(chunk, pixels - k * chunk)
+        yield from _cut(torch.randperm(size, device=device, generator=generator), batch, base=k * chunk)
 
 
 def shuffled_batches(pixels, batch, generator, mode='global', chunk=4194304, device='cuda', shape=None):
-    """The reference's sampling modes (odie/data.py:83-106)."""
-    if mode == 'global_full':
+    """Pixel ids of one epoch in `mode` (odie/data.py:83-106): 'global' (one permutation),
+    'global_full' (full_batches), 'chunked' (chunks of `chunk` ids in random order, each
+    permuted) or 'stratified' (stratified_batches; `shape` is the image's (H, W))."""
+    if mode == 'global':
+        yield from _cut(torch.randperm(pixels, device=device, generator=generator), batch)
+    elif mode == 'global_full':
         yield from full_batches(pixels, batch, generator, device)
+    elif mode == 'chunked':
+        yield from _chunked(pixels, batch, generator, chunk, device)
     elif mode == 'stratified':
         if shape is None or len(shape) != 2 or shape[0] * shape[1] != pixels or min(shape) < 2:
             raise ValueError('Stratified sampling requires the matching image shape')
         yield from stratified_batches(shape, batch, generator, device)
-    elif mode == 'global':
-        permutation = torch.randperm(pixels, device=device, generator=generator)
-        for begin in range(0, pixels, batch):
-            yield permutation[begin:begin + batch]
-    elif mode == 'chunked':
-        if chunk <= 0 or chunk % batch:
-            raise ValueError('Chunk size must be a positive multiple of batch size')
-        count = (pixels + chunk - 1) // chunk
-        order = torch.randperm(count, device=device, generator=generator).cpu().tolist()
-        for block in order:
-            start = block * chunk
-            size = min(chunk, pixels - start)
-            permutation = torch.randperm(size, device=device, generator=generator)
-            for begin in range(0, size, batch):
-                yield permutation[begin:begin + batch] + start
     else:
         raise ValueError('sampling must be global, chunked, global_full or stratified')

@@ -200,32 +200,48 @@ def _same_bytes(a, b):
     return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
 
 
+# Entries of an artifact that hold its supports, in either storage (legacy bitmaps or records).
+_SUPPORT_ENTRIES = ('support_bitmaps', 'support_encodings', 'support_storage_version')
+
+
+def _reload_checked(path, supports, *, configuration=None, parameters=None):
+    """Loads an artifact just written and checks that nothing changed on the way: its supports
+    decode to `supports`, and (when given) its configuration and the bytes of every named
+    parameter are the ones written.  Returns the reloaded artifact."""
+    reloaded = torch.load(path, map_location='cpu', weights_only=True)
+    if configuration is not None and reloaded['configuration'] != configuration:
+        raise AssertionError('Saved configuration changed during round trip')
+    decoded = decode_supports(reloaded)
+    if len(decoded) != len(supports) or not all(torch.equal(a, b) for a, b in zip(supports, decoded)):
+        raise AssertionError('Saved supports changed during round trip')
+    if parameters is not None:
+        stored = reloaded['parameters']
+        changed = [name for name, value in parameters.items() if name not in stored or not _same_bytes(value, stored[name])]
+        if changed:
+            raise AssertionError('Saved weights changed during round trip: ' + ', '.join(changed))
+    return reloaded
+
+
 def compress_checkpoint(source, destination):
-    """Rewrite an artifact with layerwise support records, its weights untouched, and verify the
-    copy by reloading it (odie/support_codec.py:161-188).  Never overwrites."""
+    """Rewrite an artifact with its supports as layerwise records (the smallest stream per
+    level) and every other entry as it was; the copy is reloaded and checked before the record
+    of the rewrite is returned (the keys of odie/support_codec.py:161-188).  Never overwrites."""
     source, destination = Path(source), Path(destination)
     if destination.exists():
         raise FileExistsError(destination)
-    original = torch.load(source, map_location='cpu', weights_only=True)
-    supports = decode_supports(original)
-    encodings = encode_supports(supports)
-    dropped = ('support_bitmaps', 'support_encodings', 'support_storage_version')
-    packed = {key: value for key, value in original.items() if key not in dropped}
-    packed['support_storage_version'] = STORAGE_VERSION
-    packed['support_encodings'] = encodings
+    artifact = torch.load(source, map_location='cpu', weights_only=True)
+    supports = decode_supports(artifact)
+    records = encode_supports(supports)
+    rewritten = {key: value for key, value in artifact.items() if key not in _SUPPORT_ENTRIES}
+    rewritten.update(support_storage_version=STORAGE_VERSION, support_encodings=records)
     destination.parent.mkdir(parents=True, exist_ok=True)
-    with destination.open('xb') as stream:
-        torch.save(packed, stream)
-    reloaded = torch.load(destination, map_location='cpu', weights_only=True)
-    if not all(torch.equal(a, b) for a, b in zip(supports, decode_supports(reloaded))):
-        raise AssertionError('Repacked checkpoint changed supports')
-    weights = reloaded['parameters']
-    if not all(_same_bytes(value, weights[name]) for name, value in original['parameters'].items()):
-        raise AssertionError('Repacked checkpoint changed weights')
-    payload = sum(p.numel() * p.element_size() for p in weights.values())
-    return dict(source=str(source), output=str(destination), source_bytes=source.stat().st_size,
-                checkpoint_bytes=destination.stat().st_size, fp16_parameter_payload_bytes=payload,
-                support_storage=support_storage_statistics(encodings), roundtrip_verified=True)
+    with destination.open('xb') as stream:        # exclusive: a file that appeared meanwhile is kept
+        torch.save(rewritten, stream)
+    weights = _reload_checked(destination, supports, parameters=artifact['parameters'])['parameters']
+    return {'source': str(source), 'output': str(destination), 'source_bytes': source.stat().st_size,
+            'checkpoint_bytes': destination.stat().st_size,
+            'fp16_parameter_payload_bytes': sum(w.numel() * w.element_size() for w in weights.values()),
+            'support_storage': support_storage_statistics(records), 'roundtrip_verified': True}
 
 
 def model_parameters(planes, decoder, gate=None):
@@ -250,11 +266,7 @@ def write_artifact(path, configuration, planes, decoder, gate=None, *, settings=
                 'parameters': model_parameters(planes, decoder, gate), 'checkpoint': 'latest',
                 'epoch': epoch, 'optimizer_steps': optimizer_steps, 'metrics': metrics or {}}
     torch.save(artifact, path)
-    reloaded = torch.load(path, map_location='cpu', weights_only=True)
-    if reloaded['configuration'] != configuration:
-        raise AssertionError('Saved configuration changed during round trip')
-    if not all(torch.equal(a, b) for a, b in zip(planes.supports, decode_supports(reloaded))):
-        raise AssertionError('Saved supports changed during round trip')
+    _reload_checked(path, planes.supports, configuration=configuration, parameters=artifact['parameters'])
     return support_storage_statistics(encodings)
 
 
