@@ -60,6 +60,7 @@ def parse():
     parser.add_argument('--no-cpu', action='store_true')
     parser.add_argument('--no-native', action='store_true', help='skip the 65536-id native step measurement')
     parser.add_argument('--no-single', action='store_true', help='skip the single-expert 2^19-table fwd+bwd line')
+    parser.add_argument('--no-c1', action='store_true', help='skip the single-expert fp32 forward of 2^18 coords')
     parser.add_argument('--single-only', action='store_true',
                         help='print only the single-expert 2^19-table fwd+bwd line (for kernel traces of it)')
     parser.add_argument('--native-steps', type=int, default=200)
@@ -337,6 +338,103 @@ def single_expert_steps(steps):
             'stage_GBps': stage_gbs}
 
 
+def encode_literal(trainer, steps):
+    """The headline metric's own definition, encode fwd+bwd with nothing else: on the step's
+    routed batch (64 experts, 2^22 coordinates) and the decoder's upstream planes of the last
+    timed step, the encode forward and the encode backward writing the fp32 gradient of all
+    70.7 M parameters (the owner pass, no optimizer step), timed with events on their stream.
+    1424 B per query (328 forward + 1096 backward)."""
+    import torch
+    n = N_COORDS
+    view = trainer.routing
+    coords, offsets = view.coords[:n], view.offsets
+    planes = trainer.plane_buffer[:16 * n].view(16, n)
+    blockmax = trainer.max_buffer[:32 * ((n + 127) // 128)].view(-1, 32)
+    out = trainer.raw[:n]
+    gradient = torch.empty(trainer.grid.table.numel(), dtype=torch.float32, device=coords.device)
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        trainer.grid.forward(coords, offsets, out=out)
+        trainer.grid.backward_planes(coords, offsets, planes, blockmax, gradient=gradient)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b, c in marks:
+        a.record(stream)
+        trainer.grid.forward(coords, offsets, out=out)
+        b.record(stream)
+        trainer.grid.backward_planes(coords, offsets, planes, blockmax, gradient=gradient)
+        c.record(stream)
+    torch.cuda.synchronize()
+    forward = sum(a.elapsed_time(b) for a, b, _ in marks) / steps
+    backward = sum(b.elapsed_time(c) for _, b, c in marks) / steps
+    per = STAGE_BYTES['encode_forward'] + STAGE_BYTES['encode_backward']
+    gbs = n * per / ((forward + backward) / 1e3) / 1e9
+    return {'ms': {'forward': forward, 'backward': backward}, 'queries_per_s': n / ((forward + backward) / 1e3),
+            'GBps': gbs, 'pct_hbm_peak': 100 * gbs / HBM_PEAK_GBS,
+            'backward_GBps': n * STAGE_BYTES['encode_backward'] / (backward / 1e3) / 1e9,
+            'kernels': 'grid_forward_kernel; owner_kernel writing the gradient (upstream planes from the decoder)'}
+
+
+C1_ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=19, base_resolution=16, per_level_scale=1.38)
+C1_COORDS = 1 << 18
+C1_BYTES = 648   # per query: xy 8 + 16 levels * 4 corners * 2 features * 4 B gathers + 32 * 4 B features
+
+
+def c1_forward(steps, cpu):
+    """The single-expert fp32 forward: 16 levels x 2 fp32 features, 2^19-entry tables, base 16,
+    scale 1.38, tables U(-1e-4, 1e-4) (seed 0); the forward encode of 2^18 coordinates uniform in
+    [0,1)^2 (seed 0) into fp32 [2^18, 32].  GPU: events around `steps` launches after a warm-up,
+    the output compared with the oracle's bit for bit; CPU: the oracle's C forward on all host
+    cores and on one thread, medians of five."""
+    import numpy as np
+    import torch
+    import oracle
+    from odie_amd import synth
+    from odie_amd.config import grid_levels
+    from odie_amd.encoding import grid_forward
+    levels, entries = grid_levels(C1_ENCODING)
+    rows = [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
+    table = synth.table(0, 2 * entries)
+    xy = synth.coordinates(0, C1_COORDS)
+    d_table, d_xy = torch.from_numpy(table).cuda(), torch.from_numpy(xy).cuda()
+    out = torch.empty((C1_COORDS, 32), dtype=torch.float32, device='cuda')
+    stream = torch.cuda.current_stream()
+    for _ in range(5):
+        grid_forward(d_xy, d_table, levels, 2, out=out)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        grid_forward(d_xy, d_table, levels, 2, out=out)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    gpu_ms = start.elapsed_time(stop) / steps
+    result = {'coords': C1_COORDS, 'params': 2 * entries, 'dtype': 'f32', 'gpu_ms': gpu_ms,
+              'queries_per_s': C1_COORDS / (gpu_ms / 1e3),
+              'GBps': C1_COORDS * C1_BYTES / (gpu_ms / 1e3) / 1e9,
+              'pct_hbm_peak': 100 * C1_COORDS * C1_BYTES / (gpu_ms / 1e3) / 1e9 / HBM_PEAK_GBS}
+    if cpu:
+        cores = len(os.sched_getaffinity(0))
+
+        def median(threads):
+            times = []
+            for _ in range(5):
+                started = time.perf_counter()
+                expected = oracle.hash_forward(xy, table, rows, 2, threads=threads)
+                times.append(time.perf_counter() - started)
+            return float(np.median(times)), expected
+
+        cpu_s, expected = median(cores)
+        one_s, _ = median(1)
+        result['matches_oracle'] = bool(np.array_equal(out.cpu().numpy().view(np.uint32), expected.view(np.uint32)))
+        result['cpu_baseline'] = {'value': C1_COORDS / cpu_s, 'unit': 'queries/s', 'cores': cores, 'kind': 'port',
+                                  'seconds': cpu_s, 'sample': 'the whole 2^18-coordinate forward, median of 5',
+                                  'one_thread': {'value': C1_COORDS / one_s, 'seconds': one_s, 'cores': 1}}
+        result['gpu_over_cpu'] = result['queries_per_s'] / result['cpu_baseline']['value']
+        result['gpu_over_cpu_one_thread'] = result['queries_per_s'] / result['cpu_baseline']['one_thread']['value']
+    return result
+
+
 C5_SIDE, C5_TILES, C5_RESIDUAL_TILE, C5_TOP = 32768, 32, 256, 512
 C5_ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=9, base_resolution=16,
                    per_level_scale=1.38)
@@ -510,6 +608,9 @@ def main():
                      'algorithmic_bytes_per_launch': stage_bytes[dominant], 'avg_ms': stage_ms[dominant]},
         'loss_after_timed_steps': loss,
     }
+    result['encode_fwd_bwd_literal'] = encode_literal(trainer, args.steps)
+    if not args.no_c1:
+        result['c1_forward'] = c1_forward(200, not args.no_cpu)
     if not args.no_single:
         result['single_expert'] = single_expert_steps(args.steps)
     if not args.no_native:

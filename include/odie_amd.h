@@ -81,6 +81,16 @@ int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, i
                        const odie_grid_level* levels, int n_levels, int features,
                        float* gradient, int zero_first, uint64_t stream);
 
+/* odie_grid_backward for features = 2 with the fp16 upstream in the layout
+ * odie_mlp_train_planes writes (planes uint32 [n_levels][n], blockmax fp32
+ * [ceil(n/128)][2 n_levels]) instead of rows: the same gradient, bit for bit, without
+ * transposing the upstream.  expert_params must equal the levels' table size.  No counterpart
+ * in the reference (the backward of odie_grid_backward_adam_planes without the optimizer step). */
+int odie_grid_backward_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                              const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                              const odie_grid_level* levels, int n_levels, int features,
+                              float* gradient, int zero_first, uint64_t stream);
+
 /* Encode backward fused with the optimizer step: the gradient of every table value (as
  * odie_grid_backward with zero_first = 1 computes it) is applied to master / m / v / steps /
  * half_copy by the Adam update of odie_adam_step (variant, step, lr, betas, eps, loss_scale as

@@ -213,8 +213,9 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
 // split_reduce_kernel.  Banded, the fine passes walk only the coordinates listed in the y-band
 // slots their table rows can reach (band lists below), every pass bounds its fixed-point scale
 // over all of the expert's coordinates, and splits write the raw 64-bit sums, added exactly by
-// banded_reduce_kernel: the gradient does not depend on how a pass is split.  Every pass has one
-// fixed-point scale per column (level, feature) it covers.
+// banded_reduce_kernel: the gradient does not depend on how a pass is split.  Every column
+// (level, feature) of an expert has one fixed-point scale, from its peak over the expert's
+// coordinates (column_peaks_kernel), shared by every pass and split that covers it.
 struct OwnerArgs {
     const float* coords;
     const int32_t* offsets;
@@ -223,7 +224,8 @@ struct OwnerArgs {
     float* grad;
     float* partial;             // unbanded splits: fp32 [max split][experts][expert_params]
     long long* partial64;       // banded splits: int64 [max split][experts][partial_floats]
-    int32_t* shifts;            // banded splits: [experts][n_levels][features] fixed-point shift (kNonFinite: NaN)
+    const uint32_t* peaks;      // [experts][n_levels * features]: max |upstream| of each column over the
+                                // records that meet the expert's coordinates (float bits; NaN above all)
     int64_t partial_floats;
     int64_t n;
     int64_t expert_params;
@@ -255,7 +257,6 @@ struct OwnerArgs {
 };
 
 constexpr int32_t kNonFinite = 1 << 30;   // shift of a column whose upstream bound is not finite
-constexpr int kMaxColumns = 128;          // (level, feature) columns of one pass: one LDS word each
 
 // Fixed-point shift of a column whose contributions are w * u with |u| <= peak (the bits of a
 // non-negative float, or a NaN), `count` coordinates of them: 2^shift * peak stays below 2^31, so
@@ -786,17 +787,53 @@ __device__ inline uint32_t work_of(uint32_t block, uint32_t blocks, int remap, u
     return (m / light) * per_expert + heavy + m % light;
 }
 
-// Fixed-point scales of level l's F columns (column (l - l0) * F + c of the pass).
+// Largest |upstream| of every column (level l, feature c: l * F + c) of every expert, over the
+// 128-row records that meet the expert's coordinates, as float bits (non-negative floats and NaN
+// order as unsigned integers).  Block (x, e) takes every gridDim.x-th run of kPeakRecords of
+// expert e's records; thread t takes column t % columns of every (kPeakBlock / columns)-th
+// record of the run; one LDS, then one global maximum per column.  peaks must be zero on entry.
+constexpr int kPeakBlock = 256;
+constexpr int kPeakRecords = 256;
+
+__global__ __launch_bounds__(kPeakBlock) void column_peaks_kernel(OwnerArgs a, uint32_t* peaks) {
+    __shared__ uint32_t block_peak[kPeakBlock];
+    const int e = blockIdx.y;
+    const int columns = a.n_levels * a.features;   // <= kPeakBlock (checked at launch)
+    block_peak[threadIdx.x] = 0u;
+    __syncthreads();
+    int64_t base, stop;
+    expert_range(a.offsets, a.n, e, base, stop);
+    uint32_t mine = 0u;
+    const int per = kPeakBlock / columns;
+    const int column = threadIdx.x % columns, first = threadIdx.x / columns;
+    if (stop > base && first < per) {
+        const int64_t r0 = base / kMaxRows, r1 = (stop - 1) / kMaxRows;
+        for (int64_t run = r0 + static_cast<int64_t>(blockIdx.x) * kPeakRecords; run <= r1;
+             run += static_cast<int64_t>(gridDim.x) * kPeakRecords) {
+            const int64_t end = run + kPeakRecords - 1 < r1 ? run + kPeakRecords - 1 : r1;
+            for (int64_t q = run + first; q <= end; q += per) {
+                const uint32_t v = __float_as_uint(a.blockmax[q * columns + column]) & 0x7fffffffu;
+                mine = v > mine ? v : mine;
+            }
+        }
+    }
+    if (mine) atomicMax(block_peak + column, mine);
+    __syncthreads();
+    if (threadIdx.x < columns && block_peak[threadIdx.x])
+        atomicMax(peaks + static_cast<int64_t>(e) * columns + threadIdx.x, block_peak[threadIdx.x]);
+}
+
+// Fixed-point shifts of level l's F columns of expert e, whose count coordinates the peaks cover.
 template <int F>
-__device__ inline void level_scales(const uint32_t* peaks, int l, int l0, int64_t count, float* scale) {
+__device__ inline void level_shifts(const OwnerArgs& a, int e, int l, int64_t count, int32_t* shift) {
+    const uint32_t* peak = a.peaks + (static_cast<int64_t>(e) * a.n_levels + l) * F;
 #pragma unroll
-    for (int c = 0; c < F; ++c) scale[c] = shift_scale(column_shift(peaks[(l - l0) * F + c], count));
+    for (int c = 0; c < F; ++c) shift[c] = column_shift(peak[c], count);
 }
 
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
-    __shared__ uint32_t peaks[kMaxColumns];   // per column of the pass: largest |upstream| (float bits)
     using U = Elem<HALF>;
     const uint32_t per_expert = static_cast<uint32_t>(a.items);
     const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
@@ -832,40 +869,17 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         hi = (a.level[l].offset + last) * F;
     }
     const uint32_t span = hi - lo;
-    const int columns = (l1 - l0) * F;   // at most kMaxColumns (the launch bounds the coarse group)
 
-    // Coordinates of this expert, and this split's index range of them.
+    // Coordinates of this expert, and this split's index range of them.  The scales are the
+    // expert's (its column peaks and coordinate count), whichever share a split walks.
     int64_t base, stop;
     expert_range(a.offsets, a.n, e, base, stop);
     const int64_t share = (stop - base + splits - 1) / splits;
     const int64_t b0 = base + share * s < stop ? base + share * s : stop;
     const int64_t b1 = b0 + share < stop ? b0 + share : stop;
-    // banded: every split of a pass bounds the scale over all of the expert's coordinates
-    const int64_t m0 = a.banded ? base : b0, m1 = a.banded ? stop : b1;
-
-    // Largest |upstream| of every column over the 128-row records of [m0, m1): thread t takes
-    // column t % columns and every (kOwnerBlock / columns)-th record, then one LDS maximum per
-    // thread (float bits of non-negative values and NaN order as unsigned integers).
-    if (threadIdx.x < kMaxColumns) peaks[threadIdx.x] = 0u;
+    const int64_t count = stop - base;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) acc[j] = 0ull;
     __syncthreads();
-    {
-        const int per = kOwnerBlock / columns;
-        const int column = threadIdx.x % columns, first = threadIdx.x / columns;
-        uint32_t mine = 0u;
-        if (m1 > m0 && first < per) {
-            const int64_t r0 = m0 / kMaxRows, r1 = (m1 - 1) / kMaxRows;
-            const int64_t stride = static_cast<int64_t>(a.n_levels) * F;
-            const float* at = a.blockmax + static_cast<int64_t>(l0) * F + column;
-            for (int64_t q = r0 + first; q <= r1; q += per) {
-                const uint32_t v = __float_as_uint(at[q * stride]) & 0x7fffffffu;
-                mine = v > mine ? v : mine;
-            }
-        }
-        if (mine) atomicMax(peaks + column, mine);
-    }
-    __syncthreads();
-    const int64_t count = m1 - m0;
 
     // A banded fine pass walks the pieces of its share of the band-list runs its rows reach.
     const bool banded = a.banded && !grouped && *a.ordered;
@@ -891,8 +905,11 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         const DevLevel lv = a.level[l];
         const U* plane = reinterpret_cast<const U*>(a.planes) + static_cast<size_t>(l) * a.n * F;
         const int kind = level_kind(lv);
+        int32_t shift[F];
+        level_shifts<F>(a, e, l, count, shift);
         float scale[F];
-        level_scales<F>(peaks, l, l0, count, scale);
+#pragma unroll
+        for (int c = 0; c < F; ++c) scale[c] = shift_scale(shift[c]);
         if (banded) {
             if (runs == 0) break;
             switch (kind) {
@@ -921,22 +938,18 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         // raw 64-bit sums: banded_reduce_kernel adds the splits exactly and applies the scales
         long long* out = a.partial64 + (static_cast<int64_t>(s) * a.experts + e) * a.partial_floats + lo;
         for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) out[j] = static_cast<long long>(acc[planar<F>(j, span)]);
-        if (s == 0 && threadIdx.x < columns)
-            a.shifts[(static_cast<int64_t>(e) * a.n_levels + l0) * F + threadIdx.x] = column_shift(peaks[threadIdx.x], count);
         return;
     }
     // Value j of the slice is feature j % F of entry lo / F + j / F.  A thread's j only grows, so
     // its level (and the shifts of that level's columns) only moves forward.
     int level = l0;
     int32_t shift[F];
-#pragma unroll
-    for (int c = 0; c < F; ++c) shift[c] = column_shift(peaks[c], count);
+    level_shifts<F>(a, e, level, count, shift);
     const auto shift_of = [&](uint32_t j) {
         const uint32_t entry = lo / F + j / F;
         if (level + 1 < l1 && a.level[level + 1].offset <= entry) {
             while (level + 1 < l1 && a.level[level + 1].offset <= entry) ++level;
-#pragma unroll
-            for (int c = 0; c < F; ++c) shift[c] = column_shift(peaks[(level - l0) * F + c], count);
+            level_shifts<F>(a, e, level, count, shift);
         }
         return shift[j % F];
     };
@@ -1015,7 +1028,10 @@ __global__ __launch_bounds__(256) void banded_reduce_kernel(OwnerArgs a) {
             for (int k = 0; k < 8; ++k) sum += v[k];
         }
         for (; s < splits; ++s) sum += column[s * step];
-        float v = unscaled(sum, a.shifts[(static_cast<int64_t>(e) * a.n_levels + l) * a.features + x % a.features]);
+        int64_t base, stop;
+        expert_range(a.offsets, a.n, e, base, stop);
+        const uint32_t peak = a.peaks[(static_cast<int64_t>(e) * a.n_levels + l) * a.features + x % a.features];
+        float v = unscaled(sum, column_shift(peak, stop - base));
         const int64_t i = static_cast<int64_t>(e) * a.expert_params + x;
         if (a.fused) {
             adam_update(a.adam, i, v);
@@ -1271,6 +1287,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     // both modes so that both slice alike and choose the same coarse group)
     const int64_t cap = (lds_bytes - kReserveBytes) / 8 - F;
     if (cap < 64) return fail("odie_grid_backward: LDS budget too small for the owner backward");
+    if (L * F > kPeakBlock) return fail("odie_grid_backward: more than 256 (level, feature) columns");
     OwnerArgs o{};
     o.coords = in.coords;
     o.offsets = in.offsets;
@@ -1285,9 +1302,8 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.remap = in.remap;
     int group = 0;
     int64_t grouped = 0;
-    // the coarse group: the leading levels whose values fit the slice, at most kMaxColumns columns
-    while (group < L && grouped + static_cast<int64_t>(in.levels[group].size) * F <= cap &&
-           (group + 1) * F <= kMaxColumns) {
+    // the coarse group: the leading levels whose values fit the slice
+    while (group < L && grouped + static_cast<int64_t>(in.levels[group].size) * F <= cap) {
         grouped += static_cast<int64_t>(in.levels[group].size) * F;
         ++group;
     }
@@ -1420,7 +1436,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t partial_bytes = split && !banded ? align(static_cast<size_t>(max_splits) * total_params * 4) : 0;
     const size_t partial64_bytes =
         split && banded ? align(static_cast<size_t>(max_splits) * in.experts * split_floats * 8) : 0;
-    const size_t shift_bytes = split && banded ? align(static_cast<size_t>(in.experts) * L * F * 4) : 0;
+    const size_t peak_bytes = align(static_cast<size_t>(in.experts) * L * F * 4);
     const bool lists = banded && group < L;
     const int parts = [&] {
         const int64_t want = (in.n / in.experts + kBandPart - 1) / kBandPart;
@@ -1430,7 +1446,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t start_bytes = lists ? align(static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4 + 4) : 0;
     const size_t list_bytes = lists ? align(static_cast<size_t>(in.n) * 4) : 0;
     const size_t sorted_bytes = lists ? align(static_cast<size_t>(in.n) * 8) : 0;
-    const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, shift_bytes,
+    const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, peak_bytes,
                             count_bytes, start_bytes, list_bytes, sorted_bytes};
     constexpr int kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t at[kParts], sum = 0;
@@ -1447,7 +1463,8 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.partial = reinterpret_cast<float*>(space + at[2]);
     o.partial64 = reinterpret_cast<long long*>(space + at[3]);
     o.partial_floats = split_floats;
-    o.shifts = reinterpret_cast<int32_t*>(space + at[4]);
+    uint32_t* peaks = reinterpret_cast<uint32_t*>(space + at[4]);
+    o.peaks = peaks;
     o.band_start = reinterpret_cast<const int32_t*>(space + at[6]);
     o.band_list = reinterpret_cast<const int32_t*>(space + at[7]);
     o.band_sorted = reinterpret_cast<const float2*>(space + at[8]);
@@ -1501,8 +1518,18 @@ int launch_owner_backward(const OwnerLaunch& in) {
         } else if (L <= 16) transpose_kernel<FF, HH, 16><<<tblocks, kTransposeBlock, 0, s>>>(t);        \
         else transpose_kernel<FF, HH, 32><<<tblocks, kTransposeBlock, 0, s>>>(t);                       \
     } while (0)
+    // every column's peak over each expert's records, then the owner pass
+    const auto launch_peaks = [&]() {
+        if (launch_fill_zero(reinterpret_cast<float*>(peaks), static_cast<int64_t>(in.experts) * L * F, s)) return -1;
+        const int64_t runs = (records + static_cast<int64_t>(kPeakRecords) * in.experts - 1) /
+                             (static_cast<int64_t>(kPeakRecords) * in.experts);
+        const dim3 grid(static_cast<uint32_t>(runs < 1 ? 1 : runs), static_cast<uint32_t>(in.experts));
+        column_peaks_kernel<<<grid, kPeakBlock, 0, s>>>(o, peaks);
+        return 0;
+    };
 #define ODIE_OWNER(FF, HH)                                                                              \
     do {                                                                                                \
+        if (launch_peaks()) return -1;                                                                  \
         if (allow_lds(owner_kernel<FF, HH>, shmem)) return -1;                                          \
         owner_kernel<FF, HH><<<oblocks, kOwnerBlock, shmem, s>>>(o);                                    \
     } while (0)

@@ -803,12 +803,14 @@ namespace odie {
 
 namespace {
 
-// Shared body of the two fused entry points: upstream rows (transposed by the owner launch)
-// or, with planes set, the level-major fp16 planes and their 128-row maxima.
+// Shared body of the fused entry points and of odie_grid_backward_planes: upstream rows
+// (transposed by the owner launch) or, with planes set, the level-major fp16 planes and their
+// 128-row column maxima; with adam the optimizer step is applied in the owner's flush, without
+// it the gradient is written (zero_first = 0: added) to `gradient`.
 int backward_adam(const char* name, const float* coords, int64_t n, const int32_t* offsets, int experts,
                   const void* upstream, int up_dtype, int up_width, const uint32_t* planes, const float* blockmax,
                   int64_t expert_params, const odie_grid_level* levels, int n_levels, int features,
-                  const AdamStep& adam, hipStream_t s) {
+                  const AdamStep* adam, float* gradient, int zero_first, hipStream_t s) {
     GridArgs a{};
     if (validate_grid(name, coords, n, offsets, experts, expert_params, levels, n_levels, features, a)) return -1;
     if (planes || blockmax) {
@@ -822,14 +824,16 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
         if (n > 0 && !upstream) return fail(std::string(name) + ": upstream is null");
     }
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail(std::string(name) + ": coords must be 8-byte aligned");
+    if (!adam && !gradient) return fail(std::string(name) + ": gradient is null");
     const int64_t table = static_cast<int64_t>(a.level[n_levels - 1].offset + a.level[n_levels - 1].size) * features;
     if (table >= (int64_t{1} << 31)) return fail(std::string(name) + ": one table must hold fewer than 2^31 values");
     if (expert_params != table) return fail(std::string(name) + ": expert_params must equal the levels' table size");
     const int64_t total = expert_params * experts;
     if (n == 0) {   // every gradient is zero
+        if (!adam) return zero_first ? launch_fill_zero(gradient, total, s) : 0;
         float* zero = static_cast<float*>(workspace(static_cast<size_t>(total) * 4, s));
         if (!zero || launch_fill_zero(zero, total, s)) return -1;
-        return launch_adam(adam, zero, 0, total, s);
+        return launch_adam(*adam, zero, 0, total, s);
     }
     const Tuning& t = tuning();
     OwnerLaunch o{};
@@ -840,8 +844,8 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
     o.up_width = planes ? n_levels * features : up_width;
     o.planes = planes;
     o.blockmax = blockmax;
-    o.grad = nullptr;
-    o.accumulate = 0;
+    o.grad = adam ? nullptr : gradient;
+    o.accumulate = adam || zero_first ? 0 : 1;
     o.n = n;
     o.expert_params = expert_params;
     o.experts = experts;
@@ -853,7 +857,7 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
     o.banded = t.banded;
     o.split_target = t.split_target;
     o.stream = s;
-    o.adam = &adam;
+    o.adam = adam;
     return launch_owner_backward(o);
 }
 
@@ -864,7 +868,7 @@ int grid_backward_adam_internal(const float* coords, int64_t n, const int32_t* o
                                 const odie_grid_level* levels, int n_levels, int features, const AdamStep& adam,
                                 hipStream_t s) {
     return backward_adam("odie_grid_backward_adam", coords, n, offsets, experts, upstream, up_dtype, up_width, nullptr,
-                         nullptr, expert_params, levels, n_levels, features, adam, s);
+                         nullptr, expert_params, levels, n_levels, features, &adam, nullptr, 0, s);
 }
 
 int grid_backward_adam_planes_internal(const float* coords, int64_t n, const int32_t* offsets, int experts,
@@ -872,7 +876,7 @@ int grid_backward_adam_planes_internal(const float* coords, int64_t n, const int
                                        const odie_grid_level* levels, int n_levels, int features,
                                        const AdamStep& adam, hipStream_t s) {
     return backward_adam("odie_grid_backward_adam_planes", coords, n, offsets, experts, nullptr, ODIE_F16, 0, planes,
-                         blockmax, expert_params, levels, n_levels, features, adam, s);
+                         blockmax, expert_params, levels, n_levels, features, &adam, nullptr, 0, s);
 }
 
 }  // namespace odie
@@ -902,6 +906,15 @@ ODIE_API int odie_grid_backward_adam_planes(const float* coords, int64_t n, cons
         return -1;
     return grid_backward_adam_planes_internal(coords, n, offsets, experts, planes, blockmax, expert_params, levels,
                                               n_levels, features, adam, as_stream(stream));
+}
+
+ODIE_API int odie_grid_backward_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                       const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                       const odie_grid_level* levels, int n_levels, int features, float* gradient,
+                                       int zero_first, uint64_t stream) {
+    return backward_adam("odie_grid_backward_planes", coords, n, offsets, experts, nullptr, ODIE_F16, 0, planes,
+                         blockmax, expert_params, levels, n_levels, features, nullptr, gradient, zero_first,
+                         as_stream(stream));
 }
 
 ODIE_API int odie_set_tuning(const char* key, int value) {

@@ -106,10 +106,8 @@ class ExpertGrid:
             optimizer.lr, optimizer.betas[0], optimizer.betas[1], optimizer.eps, float(loss_scale),
             _lib.stream_of(coords)))
 
-    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0):
-        """backward_adam with the fp16 upstream given as Decoder.train_planes writes it (planes
-        int32 [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same update, bit for bit."""
-        from .encoding import _check_coords, _offsets_arg
+    def _check_planes(self, coords, planes, blockmax):
+        from .encoding import _check_coords
         _check_coords(coords)
         n = coords.shape[0]
         levels = len(self.levels)
@@ -118,13 +116,38 @@ class ExpertGrid:
         if (tuple(blockmax.shape) != ((n + 127) // 128, 2 * levels) or blockmax.dtype != torch.float32
                 or not blockmax.is_contiguous()):
             raise ValueError('blockmax must be a contiguous fp32 [ceil(N/128), 2 levels] tensor')
+
+    def backward_planes(self, coords, offsets, planes, blockmax, gradient=None, accumulate=False):
+        """backward() with the fp16 upstream given as Decoder.train_planes writes it (planes int32
+        [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same gradient, bit for bit."""
+        from .encoding import _offsets_arg
+        self._check_planes(coords, planes, blockmax)
+        total = self.experts * self.expert_params
+        if gradient is None:
+            gradient = torch.empty(total, dtype=torch.float32, device=coords.device)
+            accumulate = False
+        elif gradient.dtype != torch.float32 or gradient.numel() != total or not gradient.is_contiguous():
+            raise ValueError('gradient must be a contiguous fp32 tensor of experts * expert_params values')
+        offsets = _offsets_arg(offsets, self.experts, coords.shape[0])
+        _lib.check(_lib.library().odie_grid_backward_planes(
+            coords.data_ptr(), coords.shape[0], _lib.ptr(offsets), self.experts, planes.data_ptr(),
+            blockmax.data_ptr(), self.expert_params, self.levels, len(self.levels), self.features,
+            gradient.data_ptr(), 0 if accumulate else 1, _lib.stream_of(coords)))
+        return gradient
+
+    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0):
+        """backward_adam with the fp16 upstream given as Decoder.train_planes writes it (planes
+        int32 [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same update, bit for bit."""
+        from .encoding import _offsets_arg
+        self._check_planes(coords, planes, blockmax)
+        n = coords.shape[0]
         if optimizer.master.numel() != self.experts * self.expert_params:
             raise ValueError('the optimizer must own this table\'s fp32 master')
         offsets = _offsets_arg(offsets, self.experts, n)
         optimizer.step_count += 1
         _lib.check(_lib.library().odie_grid_backward_adam_planes(
             coords.data_ptr(), n, _lib.ptr(offsets), self.experts, planes.data_ptr(), blockmax.data_ptr(),
-            self.expert_params, self.levels, levels, self.features, optimizer.master.data_ptr(),
+            self.expert_params, self.levels, len(self.levels), self.features, optimizer.master.data_ptr(),
             _lib.ptr(optimizer.half_copy), optimizer.m.data_ptr(), optimizer.v.data_ptr(), _lib.ptr(optimizer.steps),
             optimizer.variant_code, optimizer.step_count, optimizer.lr, optimizer.betas[0], optimizer.betas[1],
             optimizer.eps, float(loss_scale), _lib.stream_of(coords)))

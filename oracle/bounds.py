@@ -13,10 +13,9 @@ each contribution to the nearest multiple of q.  For fp32 atomic sums q is 0.
 The owner backward forms every (level, feature) column of an expert's gradient at its own
 scale: q = 2^-shift with shift = min(30 - ilogb(P), 61 - ilogb(4 * count * P)), capped at 120
 (60 when P = 0), where P is the largest |u| of that column over the 128-row records that meet
-the pass's coordinates and count the number of those coordinates.  A pass never covers more
-than its expert's coordinates, and a split of one fewer, so P and count taken over the expert's
-range give an upper bound of q for every way the backward may split it.  The packed-plane owner
-takes P over all coordinates and count = n.
+the expert's coordinates and count the number of those coordinates -- one scale per column
+whichever pass or split of the expert covers it.  The packed-plane owner takes P over all
+coordinates and count = n.
 """
 import numpy as np
 

@@ -465,3 +465,27 @@ def test_packed_owner_scale_per_level():
     _check_relative(first, bar, 'packed owner, levels 10^6 apart')
     for splits in (1, 5):
         assert torch.equal(first, _packed_gradient(layout, d_xy, d_up, packed_splits=splits)), splits
+
+
+@pytest.mark.parametrize('experts,n', [(8, 50000), (1, 4097), (3, 1)])
+def test_planes_backward_equals_rows(experts, n):
+    """odie_grid_backward_planes on the upstream in the decoder's planes layout (level-major fp16
+    pairs and per-column 128-row maxima) gives odie_grid_backward's gradient bit for bit, and
+    accumulates into a given gradient."""
+    from odie_amd.experts import ExpertGrid
+    encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=8, per_level_scale=1.4)
+    grid = ExpertGrid(encoding, experts)
+    coords = torch.from_numpy(synth.coordinates(51, n)).cuda()
+    counts = np.diff(np.linspace(0, n, experts + 1).astype(np.int64))
+    offsets = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).cuda()
+    upstream = torch.from_numpy(synth.upstream(51, n, 32)).cuda()
+    planes = upstream.view(torch.int32).t().contiguous()
+    records = (n + 127) // 128
+    column = torch.zeros((records * 128, 32), dtype=torch.float32, device='cuda')
+    column[:n] = upstream.abs().float()
+    blockmax = column.view(records, 128, 32).amax(dim=1).contiguous()
+    rows = grid.backward(coords, offsets, upstream)
+    via_planes = grid.backward_planes(coords, offsets, planes, blockmax)
+    assert torch.equal(rows.view(torch.int32), via_planes.view(torch.int32))
+    twice = grid.backward_planes(coords, offsets, planes, blockmax, gradient=via_planes.clone(), accumulate=True)
+    assert torch.equal(twice, 2 * rows)
