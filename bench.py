@@ -436,6 +436,8 @@ def c1_forward(steps, cpu):
 
 
 C5_SIDE, C5_TILES, C5_RESIDUAL_TILE, C5_TOP = 32768, 32, 256, 512
+C4_BUDGET_PARAMS = 50 * 2 ** 20 // 2     # 50 MiB of fp16 parameters
+C4_DECODER_PARAMS = 7168
 C5_ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=9, base_resolution=16,
                    per_level_scale=1.38)
 
@@ -493,16 +495,29 @@ def gigapixel_steps(steps):
     ids per step; the same step as the headline.  Measured on stratified batches (one pixel per
     8x8 stratum, strata row by row: the reference's gigapixel configurations draw them so), then
     on ids uniform over the image.  The stratified draw is fused into the route
-    (odie_route_stratified: torch.rand's uniforms in, the ids never written).  Reported beside
-    the headline, not as it."""
+    (odie_route_stratified: torch.rand's uniforms in, the ids never written).  Experts go to the
+    non-flat tiles (RGB8 range > 0) in tile order while their parameters fit the 50 MiB fp16
+    budget less the decoder's (allocate_tiles); the route takes that tile -> expert map
+    (odie_route_allocated), and the ids of tiles left without an expert read zero features.
+    Reported beside the headline, not as it."""
     import torch
     from odie_amd import synth
+    from odie_amd.config import grid_levels
+    from odie_amd.experts import allocate_tiles
     from odie_amd.trainer import ExpertTrainer
     side, n = C5_SIDE, 1 << 24
     image = synth.image_device(1, side, side)
-    trainer = ExpertTrainer(image, C5_ENCODING, C5_TILES, C5_TILES, n, grid_lr=1e-2, decoder_lr=1e-3, seed=1)
+    expert_params = 2 * grid_levels(C5_ENCODING)[1]
+    budget = C4_BUDGET_PARAMS - C4_DECODER_PARAMS
+    slots, experts = allocate_tiles(image, C5_TILES, C5_TILES, expert_params, budget)
+    trainer = ExpertTrainer(image, C5_ENCODING, C5_TILES, C5_TILES, n, grid_lr=1e-2, decoder_lr=1e-3, seed=1,
+                            slots=slots, experts=experts)
     generator = torch.Generator(device='cuda').manual_seed(1)
-    out = {'coords': n, 'experts': trainer.grid.experts, 'params': trainer.grid.table.numel(), 'steps': steps}
+    out = {'coords': n, 'experts': trainer.grid.experts, 'params': trainer.grid.table.numel(), 'steps': steps,
+           'allocation': {'tiles': C5_TILES * C5_TILES, 'non_flat_tiles': int((slots >= 0).sum()),
+                          'experts': experts, 'budget_params': budget, 'expert_params': expert_params,
+                          'rule': 'non-flat tiles (largest per-channel RGB8 range > 0) in tile order, while '
+                                  'experts * expert_params <= 26,214,400 (50 MiB fp16) - 7168 decoder params'}}
     stratified = [torch.rand((n, 2), device='cuda', generator=generator) for _ in range(2)]
     uniform = [torch.from_numpy(synth.integers(k, 'gigapixel_ids', n, side * side)).cuda() for k in range(2)]
     for name, batches, step in (('stratified', stratified, lambda b: trainer.step(None, uniforms=b)),

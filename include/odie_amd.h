@@ -57,8 +57,9 @@ typedef struct odie_grid_level {
 
 /* Forward encode of n coordinates in [0,1]^2 (coords fp32 [n,2]).
  * Experts: coordinates [offsets[e], offsets[e+1]) read the table at params + e*expert_params
- * (offsets: device int32 [experts+1], nondecreasing, offsets[0]=0, offsets[experts]=n);
- * experts = 1 with offsets = NULL is a single grid.
+ * (offsets: device int32 [experts+1], nondecreasing, offsets[0]=0, offsets[experts] <= n;
+ * rows from offsets[experts] on belong to no expert: zero features, and no gradient in the
+ * backward entry points); experts = 1 with offsets = NULL is a single grid.
  * param_dtype ODIE_F16: fp16 table, fp16 fused multiply-add chain, fp16 output;
  * ODIE_F32: fp32 table, fp32 chain, fp32 output.  levels: host array [n_levels].
  * Output row i: level l feature c at column l*features + c of out_width >= n_levels*features
@@ -187,6 +188,23 @@ int odie_route(const int64_t* ids, int64_t n, int width, int height, int regions
 int odie_route_stratified(const float* uniforms, int64_t n, int width, int height, int regions_x, int regions_y,
                           int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
                           uint32_t* colors, void* workspace, int64_t workspace_bytes, uint64_t stream);
+
+/* odie_route (ids) or odie_route_stratified (uniforms; exactly one of the two non-null) with
+ * only some tiles owning an expert, as the gigapixel workload allocates experts to the tiles that
+ * pass a predicate under a parameter budget (the analogue of the reference's supports,
+ * odie/model.py:226-257, whose cells off the support read zero features).  slots: device int32
+ * [regions_x*regions_y], tile -> expert in [0, experts); any other value: the tile has no
+ * expert.  Ids are grouped by their tile's expert as odie_route groups them by tile, and the ids
+ * of tiles without an expert follow every expert's, in input order: offsets int32 [experts + 1]
+ * holds each expert's first slot and, at offsets[experts], the first of those (they run to n).
+ * Their local coordinates and colours are formed as for any id; expert (nullable) reports -1 for
+ * them.  odie_grid_forward gives rows from offsets[experts] on zero features, and the backward
+ * gives them no gradient.  workspace: odie_route_workspace(n, experts + 1) bytes; experts within
+ * 1..4095.  No counterpart in the reference. */
+int odie_route_allocated(const int64_t* ids, const float* uniforms, int64_t n, int width, int height, int regions_x,
+                         int regions_y, const int32_t* slots, int experts, int32_t* expert, int32_t* perm,
+                         float* coords, int32_t* offsets, const uint8_t* rgb, uint32_t* colors, void* workspace,
+                         int64_t workspace_bytes, uint64_t stream);
 
 /* odie_route without the workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No

@@ -84,6 +84,14 @@ __device__ inline int64_t segment_end(const GridArgs& a, int e, int64_t i, int64
     return stop;
 }
 
+// First row past every expert: rows from offsets[experts] on (the ids of tiles without an
+// expert, as odie_route_allocated leaves them) belong to none -- zero features, no gradient.
+__device__ inline int64_t owned_end(const GridArgs& a) {
+    if (!a.offsets) return a.n;
+    const int64_t last = a.offsets[a.experts];
+    return last < 0 ? 0 : (last > a.n ? a.n : last);
+}
+
 __device__ inline uint32_t pick4(const uint4& v, uint32_t j) {
     const uint32_t low = (j & 1u) ? v.y : v.x;
     const uint32_t high = (j & 1u) ? v.w : v.z;
@@ -216,8 +224,17 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
     const uint32_t block = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
     int64_t begin = static_cast<int64_t>(block) * a.chunk;
     if (begin >= a.n) return;
-    const int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
+    int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
     extern __shared__ uint32_t staged[];
+    const int64_t owned = owned_end(a);
+    for (int64_t i = (begin > owned ? begin : owned) + threadIdx.x; i < end; i += kBlock) {
+        Elem<HALF>* row = reinterpret_cast<Elem<HALF>*>(a.out) + static_cast<size_t>(i) * a.width;
+        for (int c = 0; c < a.width; ++c) row[c] = Elem<HALF>(0.0f);
+    }
+    if (owned < end) {
+        if (owned <= begin) return;
+        end = owned;
+    }
     while (begin < end) {
         const int e = expert_at(a, begin);
         const int64_t stop = segment_end(a, e, begin, end);
@@ -241,8 +258,11 @@ __global__ __launch_bounds__(kBlock) void grid_backward_kernel(GridArgs a) {
     const uint32_t block = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
     int64_t begin = static_cast<int64_t>(block) * a.chunk;
     if (begin >= a.n) return;
-    const int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
+    int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
     const int used = a.n_levels * F;
+    const int64_t owned = owned_end(a);
+    if (owned <= begin) return;
+    if (owned < end) end = owned;
     while (begin < end) {
         const int e = expert_at(a, begin);
         const int64_t stop = segment_end(a, e, begin, end);

@@ -48,13 +48,16 @@ struct RouteArgs {
     uint32_t* colors;       // packed r | g << 8 | b << 16 of each slot's pixel, or null
     int32_t* counts;   // [experts * parts]
     int32_t* block_sums;  // [ceil(experts * parts / kScanSegment)]
+    const int32_t* slots; // tile -> expert, or null (expert = tile); with slots, bucket `owned` holds
+                          // the ids of tiles without an expert (slot outside [0, owned))
+    int owned;            // experts owning tiles (with slots; experts = owned + 1 buckets)
     int64_t n;
     uint32_t width;
     uint32_t height;
     int regions_x;
     int regions_y;
-    int experts;
-    int expert_bits;   // bits of the largest expert id
+    int experts;       // buckets of the counting sort
+    int expert_bits;   // bits of the largest bucket id
     int part;          // ids per wave sub-chunk (multiple of 64)
     int parts;         // number of sub-chunks
     int32_t x0[kMaxRegions + 1];
@@ -108,6 +111,15 @@ __device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t i
     rx = tile_of(a.regions_x, a.width, a.sx, x);
     ry = tile_of(a.regions_y, a.height, a.sy, y);
     expert = ry * a.regions_x + rx;
+    if (a.slots) {
+        const int32_t slot = a.slots[expert];
+        expert = slot >= 0 && slot < a.owned ? slot : a.owned;
+    }
+}
+
+// The expert reported for an id in bucket `expert`: -1 for the bucket of tiles without one.
+__device__ inline int32_t reported(const RouteArgs& a, int expert) {
+    return a.slots && expert == a.owned ? -1 : expert;
 }
 
 __device__ inline void load_bounds(const RouteArgs& a, Bounds& b) {
@@ -203,7 +215,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_top_kernel(RouteArgs a,
             running += value;
         }
     }
-    if (threadIdx.x == 0) a.offsets[a.experts] = static_cast<int32_t>(a.n);
+    if (threadIdx.x == 0 && !a.slots) a.offsets[a.experts] = static_cast<int32_t>(a.n);
 }
 
 // SUMS_SCANNED: block_sums already holds each segment's offset (route_scan_top_kernel ran);
@@ -218,7 +230,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
         int32_t before = 0;
         for (uint32_t b = threadIdx.x; b < blockIdx.x; b += kScanBlock) before += a.block_sums[b];
         block_exclusive_scan(before, shared, offset);
-        if (blockIdx.x == 0 && threadIdx.x == 0) a.offsets[a.experts] = static_cast<int32_t>(a.n);
+        if (blockIdx.x == 0 && threadIdx.x == 0 && !a.slots) a.offsets[a.experts] = static_cast<int32_t>(a.n);
     }
     const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
     constexpr int kPer = kScanSegment / kScanBlock;
@@ -289,7 +301,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
                 const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
                 const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
                 reinterpret_cast<float2*>(a.coords)[slot] = make_float2(u, v);
-                if (a.expert_out) a.expert_out[i] = expert;
+                if (a.expert_out) a.expert_out[i] = reported(a, expert);
                 // the pixel's index for route_colors_kernel (below 2^32: the image size is bounded)
                 if (a.colors) a.colors[slot] = y * a.width + x;
             }
@@ -500,7 +512,7 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 if (valid) {
                     local[position + rank] = static_cast<uint16_t>(j);
-                    if (a.expert_out) a.expert_out[group_begin + j] = expert;
+                    if (a.expert_out) a.expert_out[group_begin + j] = reported(a, expert);
                 }
             }
         }
@@ -629,9 +641,13 @@ int route_check(const void* ids, int64_t n, int width, int height, int regions_x
 // the caller) as its scratch.
 int route_launch(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,
                  int32_t* expert, int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb,
-                 uint32_t* colors, void* workspace, uint64_t stream, const float* uniforms = nullptr, int side = 0) {
-    const int experts = regions_x * regions_y;
+                 uint32_t* colors, void* workspace, uint64_t stream, const float* uniforms = nullptr, int side = 0,
+                 const int32_t* slots = nullptr, int owned = 0) {
+    // buckets of the counting sort: one per tile, or one per expert and the one of tiles without
+    const int experts = slots ? owned + 1 : regions_x * regions_y;
     RouteArgs a{};
+    a.slots = slots;
+    a.owned = owned;
     a.ids = ids;
     a.uniforms = uniforms;
     a.side = side;
@@ -645,8 +661,8 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     a.counts = static_cast<int32_t*>(workspace);
     {
         int part, parts;
-        route_plan(n, regions_x * regions_y, part, parts);
-        const int64_t counts = (static_cast<int64_t>(regions_x) * regions_y * parts * 4 + 255) / 256 * 256;
+        route_plan(n, experts, part, parts);
+        const int64_t counts = (static_cast<int64_t>(experts) * parts * 4 + 255) / 256 * 256;
         a.block_sums = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + counts);
     }
     a.n = n;
@@ -676,7 +692,7 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     const size_t shmem = static_cast<size_t>(kWaves) * experts * 4;
     if (shmem + sizeof(Bounds) > 64 * 1024) return fail("odie_route: too many experts for the LDS histogram");
     const uint32_t blocks = static_cast<uint32_t>((a.parts + kWaves - 1) / kWaves);
-    if (n == 0) return launch_fill_zero(reinterpret_cast<float*>(offsets), experts + 1, s);
+    if (n == 0) return launch_fill_zero(reinterpret_cast<float*>(offsets), slots ? owned + 1 : experts + 1, s);
     const int sblocks = static_cast<int>(scan_blocks(n, experts));
     if (sblocks > kScanBlock * 64) return fail("odie_route: too many counts to scan");
     route_count_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
@@ -760,6 +776,31 @@ ODIE_API int odie_route_stratified(const float* uniforms, int64_t n, int width, 
         return fail("odie_route: workspace must hold odie_route_workspace(n, experts) bytes");
     return route_launch(nullptr, n, width, height, regions_x, regions_y, expert, perm, coords, offsets, rgb, colors,
                         workspace, stream, uniforms, side);
+}
+
+ODIE_API int odie_route_allocated(const int64_t* ids, const float* uniforms, int64_t n, int width, int height,
+                                  int regions_x, int regions_y, const int32_t* slots, int experts, int32_t* expert,
+                                  int32_t* perm, float* coords, int32_t* offsets, const uint8_t* rgb, uint32_t* colors,
+                                  void* workspace, int64_t workspace_bytes, uint64_t stream) {
+    if ((ids == nullptr) == (uniforms == nullptr) && n > 0)
+        return fail("odie_route_allocated: give exactly one of ids and uniforms");
+    if (route_check(ids ? static_cast<const void*>(ids) : uniforms, n, width, height, regions_x, regions_y, perm,
+                    coords, offsets, rgb, colors))
+        return -1;
+    if (experts < 1 || experts >= kMaxExperts) return fail("odie_route_allocated: experts must be within 1..4095");
+    if (!slots) return fail("odie_route_allocated: slots is null");
+    int side = 0;
+    if (uniforms) {
+        side = 1;
+        while (static_cast<int64_t>(side) * side < n) side *= 2;
+        if (static_cast<int64_t>(side) * side != n)
+            return fail("Stratified sampling requires a square power-of-two batch size");
+        if (reinterpret_cast<uintptr_t>(uniforms) % 8) return fail("odie_route_allocated: uniforms must be 8-byte aligned");
+    }
+    if (n > 0 && (!workspace || workspace_bytes < odie_route_workspace(n, experts + 1)))
+        return fail("odie_route_allocated: workspace must hold odie_route_workspace(n, experts + 1) bytes");
+    return route_launch(ids, n, width, height, regions_x, regions_y, expert, perm, coords, offsets, rgb, colors,
+                        workspace, stream, uniforms, side, slots, experts);
 }
 
 ODIE_API int odie_route_noalloc(const int64_t* ids, int64_t n, int width, int height, int regions_x, int regions_y,

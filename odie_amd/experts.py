@@ -27,11 +27,14 @@ class Routing:
 
 
 def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None, rgb=None,
-          uniforms=None):
+          uniforms=None, slots=None, experts=None):
     """Route int64 pixel ids [N] (CUDA) to regions_x*regions_y tile experts and compact.  With
     rgb (CUDA uint8 [H*W*3]) each slot also receives its pixel's packed colour.  With
     uniforms (CUDA fp32 [N, 2], N a square power of two) and ids None, the ids are those of
-    the stratified draw on those uniforms (odie_stratified_ids), computed inside the route."""
+    the stratified draw on those uniforms (odie_stratified_ids), computed inside the route.
+    With slots (CUDA int32 [regions_x*regions_y], tile -> expert in [0, experts), any other
+    value: no expert) the tiles share `experts` experts; ids of tiles without one follow every
+    expert's, from offsets[experts] on (odie_route_allocated)."""
     if uniforms is not None:
         if ids is not None:
             raise ValueError('give ids or uniforms, not both')
@@ -44,9 +47,18 @@ def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=No
             raise ValueError('ids must be a CUDA int64 [N] tensor')
         ids = ids.contiguous()
         entry = 'odie_route'
-    n, experts = ids.shape[0], regions_x * regions_y
+    n, tiles = ids.shape[0], regions_x * regions_y
+    if slots is not None:
+        if (slots.dtype != torch.int32 or slots.numel() != tiles or not slots.is_cuda
+                or not slots.is_contiguous()):
+            raise ValueError('slots must be a contiguous CUDA int32 tensor of regions_x * regions_y entries')
+        if experts is None or not 1 <= experts < 4096:
+            raise ValueError('experts must be within 1..4095 with slots')
+    else:
+        experts = tiles
+    buckets = experts + 1 if slots is not None else experts
     lib = _lib.library()
-    need = lib.odie_route_workspace(n, experts)
+    need = lib.odie_route_workspace(n, buckets)
     if need < 0:
         raise ValueError('invalid routing size')
     device = ids.device
@@ -58,11 +70,56 @@ def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=No
                       torch.empty(n, dtype=torch.int32, device=device) if rgb is not None else None)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
+    colors = out.colors if rgb is not None else None
+    if slots is not None:
+        stratified = entry == 'odie_route_stratified'
+        _lib.check(lib.odie_route_allocated(None if stratified else ids.data_ptr(),
+                                            ids.data_ptr() if stratified else None, n, width, height, regions_x,
+                                            regions_y, slots.data_ptr(), experts, _lib.ptr(out.expert),
+                                            out.perm.data_ptr(), out.coords.data_ptr(), out.offsets.data_ptr(),
+                                            _lib.ptr(rgb), _lib.ptr(colors), workspace.data_ptr(),
+                                            workspace.numel() * workspace.element_size(), _lib.stream_of(ids)))
+        return out
     _lib.check(getattr(lib, entry)(ids.data_ptr(), n, width, height, regions_x, regions_y, _lib.ptr(out.expert),
-                              out.perm.data_ptr(), out.coords.data_ptr(), out.offsets.data_ptr(),
-                              _lib.ptr(rgb), _lib.ptr(out.colors if rgb is not None else None), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-                              _lib.stream_of(ids)))
+                                   out.perm.data_ptr(), out.coords.data_ptr(), out.offsets.data_ptr(),
+                                   _lib.ptr(rgb), _lib.ptr(colors), workspace.data_ptr(),
+                                   workspace.numel() * workspace.element_size(), _lib.stream_of(ids)))
     return out
+
+
+def tile_ranges(image, regions_x, regions_y):
+    """RGB8 range of every tile (uint8 image [H, W, 3], on any device): the largest, over the
+    three channels, of the channel's largest minus smallest byte in the tile -- 0 exactly for a
+    tile of one colour.  int32 [regions_y * regions_x] in tile order, with the route's tile bounds."""
+    image = torch.as_tensor(image)
+    height, width = image.shape[:2]
+    xs, ys = tile_bounds(width, regions_x), tile_bounds(height, regions_y)
+    ranges = torch.empty(regions_y * regions_x, dtype=torch.int32)
+    for ry in range(regions_y):
+        band = image[ys[ry]:ys[ry + 1]]
+        top, bottom = band.amax(dim=0).int(), band.amin(dim=0).int()   # [W, 3]: per column and channel
+        for rx in range(regions_x):
+            spread = top[xs[rx]:xs[rx + 1]].amax(dim=0) - bottom[xs[rx]:xs[rx + 1]].amin(dim=0)
+            ranges[ry * regions_x + rx] = int(spread.max())
+    return ranges
+
+
+def allocate_tiles(image, regions_x, regions_y, expert_params, budget_params):
+    """Experts for the non-flat tiles (tile_ranges > 0), in tile order, while their parameters
+    fit the budget: returns (slots int32 [regions_y * regions_x] with -1 for tiles left without
+    an expert, experts).  A flat tile is one colour: the decoder reproduces it from the zero
+    features every id without an expert reads, as the reference leaves cells off its supports
+    (odie/model.py:226-257)."""
+    ranges = tile_ranges(image, regions_x, regions_y)
+    most = int(budget_params // expert_params)
+    slots = torch.full((regions_x * regions_y,), -1, dtype=torch.int32)
+    experts = 0
+    for tile in torch.nonzero(ranges > 0).flatten().tolist():
+        if experts == most:
+            break
+        slots[tile] = experts
+        experts += 1
+    return slots, experts
 
 
 class ExpertGrid:

@@ -20,6 +20,11 @@ encode backward's own level-major layout with its 128-row maxima (odie_mlp_train
 odie_grid_backward_adam_planes), so the backward does not transpose it; the result is the same,
 bit for bit.
 
+With slots (int32 [regions_y * regions_x], tile -> expert, -1: none; allocate_tiles forms it
+from a predicate and a parameter budget) only `experts` tables exist: ids of tiles without an
+expert are routed after every expert's (odie_route_allocated), read zero features and train only
+the decoder, as the reference's cells off their supports do.
+
 Every buffer is allocated once, at construction, for `batch` ids; a step allocates nothing
 on the device beyond the library's grow-once workspace.
 """
@@ -38,7 +43,7 @@ GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:
 class ExpertTrainer:
     def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
                  device='cuda', fused=True, router=False, gate_lr=1e-3, coarse_levels=0, activation='sigmoid',
-                 planes=True):
+                 planes=True, slots=None, experts=None):
         if isinstance(image, torch.Tensor):    # already on the device (gigapixel images)
             if image.dtype != torch.uint8 or image.ndim != 3 or image.shape[2] != 3:
                 raise ValueError('image must be uint8 [height, width, 3]')
@@ -52,7 +57,18 @@ class ExpertTrainer:
         self.regions = (regions_x, regions_y)
         self.batch = batch
         self.fused = fused          # grid Adam applied inside the encode backward
-        experts = regions_x * regions_y
+        tiles = regions_x * regions_y
+        if slots is not None:
+            slots = torch.as_tensor(slots, dtype=torch.int32)
+            if slots.numel() != tiles or experts is None or not 1 <= experts < 4096:
+                raise ValueError('slots must map every tile; experts within 1..4095')
+            if experts == tiles and torch.equal(slots.cpu(), torch.arange(tiles, dtype=torch.int32)):
+                slots = None   # every tile owns its own expert: the plain route, the same result
+        if slots is None:
+            experts, self.slots = tiles, None
+        else:
+            self.slots = slots.to(device).contiguous()
+        self.experts = experts
         self.rgb = rgb
         self.grid = ExpertGrid(encoding, experts, dtype=torch.float16, device=device)
         total = self.grid.table.numel()
@@ -74,7 +90,7 @@ class ExpertTrainer:
                                torch.empty((batch, 2), dtype=torch.float32, device=device),
                                torch.empty(experts + 1, dtype=torch.int32, device=device), None,
                                torch.empty(batch, dtype=torch.int32, device=device))
-        need = _lib.library().odie_route_workspace(batch, experts)
+        need = _lib.library().odie_route_workspace(batch, experts + (self.slots is not None))
         if need < 0:
             raise ValueError('invalid batch size for routing')
         self.workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
@@ -102,7 +118,7 @@ class ExpertTrainer:
         r = self.routing
         view = Routing(r.perm[:n], r.coords[:n], r.offsets, None, r.colors[:n])
         route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, rgb=self.rgb,
-              uniforms=uniforms)
+              uniforms=uniforms, slots=self.slots, experts=self.experts if self.slots is not None else None)
         mark('route')
         raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
         mark('encode_forward')

@@ -407,10 +407,13 @@ def adam(variant, param, grad, m, v, steps, step, lr, beta1=0.9, beta2=0.999, ep
     return param
 
 
-def route(ids, width, height, regions_x, regions_y):
+def route(ids, width, height, regions_x, regions_y, slots=None, experts=None):
     """Routing spec restated with integer division: expert = (y*RY//H)*RX + x*RX//W, local
     coordinate fp32(x - x0) * fp32(1/(tile-1)); returns (expert, perm, local_xy, offsets)
-    with perm the stable ascending-expert order."""
+    with perm the stable ascending-expert order.  With slots (tile -> expert; a value outside
+    [0, experts) means none), an id's expert is its tile's slot, the ids of tiles without one
+    follow every expert's in input order, offsets has experts + 1 entries (offsets[experts]:
+    the first of those) and their expert is -1."""
     ids = np.asarray(ids, dtype=np.int64).astype(np.uint32).astype(np.int64)
     x, y = ids % width, np.minimum(ids // width, height - 1)
     rx, ry = x * regions_x // width, y * regions_y // height
@@ -421,7 +424,14 @@ def route(ids, width, height, regions_x, regions_y):
     y1 = -((-(ry + 1) * height) // regions_y)
     u = (x - x0).astype(np.float32) * (1.0 / (x1 - x0 - 1).astype(np.float64)).astype(np.float32)
     v = (y - y0).astype(np.float32) * (1.0 / (y1 - y0 - 1).astype(np.float64)).astype(np.float32)
-    perm, offsets = compact(expert, regions_x * regions_y)
+    if slots is None:
+        perm, offsets = compact(expert, regions_x * regions_y)
+    else:
+        slot = np.asarray(slots, dtype=np.int64)[expert]
+        owned = (slot >= 0) & (slot < experts)
+        perm, offsets = compact(np.where(owned, slot, experts), experts + 1)
+        offsets = offsets[:experts + 1]
+        expert = np.where(owned, slot, -1)
     local = np.stack([u, v], axis=1).astype(np.float32)[perm]
     return expert.astype(np.int32), perm, local, offsets
 

@@ -307,3 +307,21 @@ def test_stratified_ids_reject_bad_arguments(native):
     assert 'square power-of-two' in native.odie_error().decode()
     assert native.odie_stratified_ids(8, 12, 10, 10, 8, 0) == -1
     assert native.odie_stratified_ids(None, 16, 10, 10, 8, 0) == -1
+
+
+def test_route_allocated_rejects_bad_arguments(native):
+    # every call below fails a check before anything is queued (the pointers are never used)
+    args = [8, None, 100, 640, 480, 4, 4, 8, 9, None, 8, 8, 8, None, None, 8, 1 << 20, 0]
+    bad = list(args)
+    bad[1] = 8                                             # ids and uniforms both given
+    assert native.odie_route_allocated(*bad) == -1 and 'exactly one' in native.odie_error().decode()
+    bad = list(args)
+    bad[8] = 4096                                          # experts + 1 buckets above 4096
+    assert native.odie_route_allocated(*bad) == -1 and '1..4095' in native.odie_error().decode()
+    bad = list(args)
+    bad[7] = None                                          # no slot map
+    assert native.odie_route_allocated(*bad) == -1 and 'slots is null' in native.odie_error().decode()
+    bad = list(args)
+    bad[16] = native.odie_route_workspace(100, 9) - 4       # workspace sized for the experts alone
+    assert native.odie_route_workspace(100, 10) > native.odie_route_workspace(100, 9) - 4
+    assert native.odie_route_allocated(*bad) == -1 and 'experts + 1' in native.odie_error().decode()

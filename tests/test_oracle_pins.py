@@ -709,6 +709,36 @@ def test_route_against_per_pixel_brute_force(oracle, width, height, regions_x, r
     assert last == np.float32(1.0) - np.float32(2.0 ** -24)   # the rounding the third case exercises
 
 
+@pytest.mark.parametrize('width,height,regions_x,regions_y,slots,experts', [
+    (23, 17, 3, 5, [4, -1, 0, 9, 2, 1, -1, 3, 5, 6, -3, 7, 8, 10, 11], 12),   # shuffled, with gaps
+    (7, 5, 2, 2, [0, 0, -1, 1], 2),                                          # two tiles share an expert
+    (7, 5, 2, 2, [-1, -1, -1, -1], 1),                                       # no tile owns one
+])
+def test_route_with_slots_against_a_python_sort(oracle, width, height, regions_x, regions_y, slots, experts):
+    """oracle.route with a slot map against the plain route (pinned by the per-pixel brute force
+    above) and a Python sort: an id's expert is its tile's slot (-1 outside [0, experts)), the
+    order is the stable sort by (slot, or experts for none), offsets count the experts and the
+    first id without one, and the local coordinates are the tile's, whichever slot it maps to."""
+    pixels = width * height
+    ids = np.concatenate([np.arange(pixels), np.arange(pixels)[::-3], pixels + np.arange(4)]).astype(np.int64)
+    tile, plain_perm, plain_local, _ = oracle.route(ids, width, height, regions_x, regions_y)
+    expert, perm, local, offsets = oracle.route(ids, width, height, regions_x, regions_y, slots=slots,
+                                                experts=experts)
+    owner = [slots[t] if 0 <= slots[t] < experts else -1 for t in tile.tolist()]
+    assert expert.tolist() == owner
+    key = [e if e >= 0 else experts for e in owner]
+    order = sorted(range(len(ids)), key=lambda i: key[i])
+    assert list(perm) == order
+    assert list(offsets) == [sum(1 for k in key if k < e) for e in range(experts + 1)]
+    where = {j: k for k, j in enumerate(plain_perm)}     # slot of each input in the plain route
+    assert np.array_equal(local.view(np.uint32), plain_local[[where[j] for j in order]].view(np.uint32))
+    tiles = regions_x * regions_y
+    identity = oracle.route(ids, width, height, regions_x, regions_y, slots=list(range(tiles)), experts=tiles)
+    plain = oracle.route(ids, width, height, regions_x, regions_y)
+    for got, want in zip(identity, plain):
+        assert np.array_equal(got, want)
+
+
 def test_gate_upstream_matches_exact_rational_arithmetic(oracle):
     """hash_router_gradient (odie/native/runtime.cu:99-103) in exact arithmetic: the router's input
     gradient is divided by 128 in fp32 (exact: a power of two inside the fp32 range), rounded once

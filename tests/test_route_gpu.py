@@ -112,3 +112,96 @@ def test_route_stratified_fuses_the_draw(width, height, rx, ry, n):
     _, perm, local, offsets = oracle.route(expected, width, height, rx, ry)
     assert np.array_equal(fused.perm.cpu().numpy(), perm)
     assert np.array_equal(fused.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
+
+
+def _slot_map(seed, tiles, experts):
+    """A tile -> expert map over `tiles` tiles: `experts` of them own an expert (shuffled), the
+    others hold -1 or a value out of range (both mean none)."""
+    rng = np.random.default_rng(seed)
+    slots = np.full(tiles, -1, dtype=np.int32)
+    owners = rng.permutation(tiles)[:experts]
+    slots[owners] = rng.permutation(experts).astype(np.int32)
+    spare = np.flatnonzero(slots < 0)
+    slots[spare[::3]] = experts + 7
+    return slots
+
+
+@pytest.mark.parametrize('width,height,rx,ry,experts,n', [
+    (2048, 1365, 8, 8, 41, 1 << 20),        # 41 of 64 tiles own an expert
+    (32768, 32768, 32, 32, 700, 1 << 20),   # 700 of the gigapixel image's 1024 tiles
+    (100, 37, 3, 5, 1, 4099),               # one expert, ragged tiles
+    (4096, 4096, 60, 60, 3000, 1 << 21),    # too many buckets for the staged scatter's LDS
+])
+def test_route_allocated_matches_oracle(width, height, rx, ry, experts, n):
+    """odie_route_allocated: ids grouped by their tile's expert, the ids of tiles without one
+    after all experts in input order; experts (-1 for those), perm, local coordinates, offsets
+    [experts + 1] and colours bit-exact against the oracle's route with the same slot map, for
+    stored ids and for the stratified draw."""
+    slots = _slot_map(n, rx * ry, experts)
+    ids = synth.integers(19, 'ids', n, width * height)
+    image = torch.from_numpy(synth.integers(19, 'image', width * height * 3, 256).astype(np.uint8)).cuda() \
+        if width * height <= 1 << 24 else None
+    d_slots = torch.from_numpy(slots).cuda()
+    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, with_expert=True, rgb=image,
+                   slots=d_slots, experts=experts)
+    expert, perm, local, offsets = oracle.route(ids, width, height, rx, ry, slots=slots, experts=experts)
+    assert np.array_equal(result.expert.cpu().numpy(), expert)
+    assert np.array_equal(result.offsets.cpu().numpy(), offsets)
+    assert np.array_equal(result.perm.cpu().numpy(), perm)
+    assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
+    if image is not None:
+        pixel = image.cpu().numpy().reshape(-1, 3)[np.minimum(ids, width * height - 1)[perm]].astype(np.uint32)
+        colors = pixel[:, 0] | (pixel[:, 1] << 8) | (pixel[:, 2] << 16)
+        assert np.array_equal(result.colors.cpu().numpy().view(np.uint32), colors)
+    side = 1 << ((n.bit_length() - 1) // 2)
+    if side * side == n:
+        uniforms = torch.rand((n, 2), device='cuda', generator=torch.Generator(device='cuda').manual_seed(n))
+        fused = route(None, width, height, rx, ry, with_expert=True, uniforms=uniforms, slots=d_slots,
+                      experts=experts)
+        drawn = oracle.stratified_ids(uniforms.cpu().numpy(), width, height)
+        expert, perm, local, offsets = oracle.route(drawn, width, height, rx, ry, slots=slots, experts=experts)
+        assert np.array_equal(fused.expert.cpu().numpy(), expert)
+        assert np.array_equal(fused.offsets.cpu().numpy(), offsets)
+        assert np.array_equal(fused.perm.cpu().numpy(), perm)
+        assert np.array_equal(fused.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
+
+
+def test_forward_gives_rows_without_an_expert_zero_features():
+    """Rows from offsets[experts] on (the ids of tiles without an expert) encode to zero features
+    and receive no gradient; the other rows match the oracle's encode bit for bit and its gradient
+    within the bar."""
+    from odie_amd.config import grid_levels
+    from odie_amd.encoding import grid_backward, grid_forward
+    from oracle.bounds import check_gradient, hash_quantum
+    width, height, rx, ry, experts, n = 640, 480, 4, 4, 9, 50000
+    slots = _slot_map(5, rx * ry, experts)
+    ids = synth.integers(37, 'ids', n, width * height)
+    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, slots=torch.from_numpy(slots).cuda(),
+                   experts=experts)
+    _, perm, local, offsets = oracle.route(ids, width, height, rx, ry, slots=slots, experts=experts)
+    owned = int(offsets[experts])
+    assert 0 < owned < n
+    encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=8, per_level_scale=1.4)
+    levels, entries = grid_levels(encoding)
+    params = 2 * entries
+    table = synth.table(37, experts * params, -1.0, 1.0).astype(np.float16)
+    features = grid_forward(result.coords, torch.from_numpy(table).cuda(), levels, 2, offsets=result.offsets,
+                            experts=experts, expert_params=params).cpu().numpy()
+    rows = [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
+    expected = oracle.hash_forward(local[:owned], table, rows, 2, offsets=offsets, expert_params=params)
+    assert np.array_equal(features[:owned].view(np.uint16), expected.view(np.uint16))
+    assert not features[owned:].view(np.uint16).any()
+    up = synth.upstream(37, n, 32)
+    for mode in (1, 0):   # owner, then the atomics kernel
+        from odie_amd import _lib
+        _lib.set_tuning('backward_mode', mode)
+        try:
+            grad = grid_backward(result.coords, torch.from_numpy(up).cuda(), levels, 2, offsets=result.offsets,
+                                 experts=experts, expert_params=params).cpu().numpy()
+        finally:
+            _lib.set_tuning('backward_mode', 1)
+        want, magnitude, counts = oracle.hash_backward(local[:owned], up[:owned], rows, 2, experts * params,
+                                                       offsets=offsets, expert_params=params, counts=True)
+        check_gradient(grad, want, magnitude, counts, hash_quantum(up, rows, 2, experts * params,
+                                                                    offsets=offsets, expert_params=params),
+                       'rows without an expert, mode %d' % mode)

@@ -3,6 +3,7 @@ each mode's invariants, and the seeded stream -- the generators draw torch's per
 reference's order and sizes, so a seeded generator's batches are those permutations cut into
 batches (the reference's full_batches pads its last batch with the permutation's beginning;
 chunked mode permutes the chunk order first, then each chunk as it is visited)."""
+import numpy as np
 import pytest
 import torch
 
@@ -63,3 +64,26 @@ def test_modes_are_checked():
         next(shuffled_batches(100, 16, _generator(1), mode='stratified', shape=(10, 11), device='cpu'))
     with pytest.raises(ValueError, match='sampling must be'):
         next(shuffled_batches(100, 16, _generator(1), mode='tiles', device='cpu'))
+
+
+def test_allocate_tiles_takes_non_flat_tiles_under_the_budget():
+    """Flat tiles (one colour) get no expert; the others get experts in tile order until the
+    parameter budget is spent; the tile ranges use the route's ceil bounds."""
+    from odie_amd.experts import allocate_tiles, tile_bounds, tile_ranges
+    rng = np.random.default_rng(3)
+    height, width, rx, ry = 50, 70, 4, 3
+    image = rng.integers(0, 256, (height, width, 3), dtype=np.uint8)
+    xs, ys = tile_bounds(width, rx), tile_bounds(height, ry)
+    flat = [1, 6, 7]
+    for t in flat:
+        image[ys[t // rx]:ys[t // rx + 1], xs[t % rx]:xs[t % rx + 1]] = (12, 200, 12 + t)
+    image[ys[2]:ys[3], xs[3]:xs[4]] = (5, 5, 5)                     # tile 11: one colour but for
+    image[ys[2]:ys[3], xs[3]:xs[3] + 1, 1] = 6                      # one column a shade off
+    ranges = tile_ranges(torch.from_numpy(image), rx, ry)
+    assert [int(v) for v in ranges[flat]] == [0, 0, 0]          # one colour each (channels differ)
+    assert int(ranges[11]) == 1 and (ranges[[t for t in range(rx * ry) if t not in flat]] > 0).all()
+    slots, experts = allocate_tiles(torch.from_numpy(image), rx, ry, expert_params=100, budget_params=10 ** 6)
+    assert experts == rx * ry - 3 and [int(slots[t]) for t in flat] == [-1, -1, -1]
+    assert [int(v) for v in slots[slots >= 0]] == list(range(experts))
+    slots, experts = allocate_tiles(torch.from_numpy(image), rx, ry, expert_params=100, budget_params=450)
+    assert experts == 4 and [int(v) for v in slots[:8]] == [0, -1, 1, 2, 3, -1, -1, -1]

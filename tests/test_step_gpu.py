@@ -21,11 +21,24 @@ def rows_of(levels):
     return [(r.scale, r.resolution, r.size, r.offset, r.hashed) for r in levels]
 
 
-@pytest.mark.parametrize('regions,batch,n', [((2, 2), 4096, 3000), ((3, 2), 2048, 2048)])
-def test_training_step_matches_oracle(regions, batch, n):
+@pytest.mark.parametrize('regions,batch,n,flat', [((2, 2), 4096, 3000, ()), ((3, 2), 2048, 2048, ()),
+                                                   ((3, 2), 4096, 4000, (1, 4))])
+def test_training_step_matches_oracle(regions, batch, n, flat):
+    """flat: tiles painted one colour, left without an expert by allocate_tiles (their ids read
+    zero features and train the decoder only)."""
+    from odie_amd.experts import allocate_tiles, tile_bounds
     width, height = 96, 70
     image = synth.image(3, width, height)
-    trainer = ExpertTrainer(image, ENCODING, *regions, batch, seed=3, fused=False)
+    xs, ys = tile_bounds(width, regions[0]), tile_bounds(height, regions[1])
+    for t in flat:
+        image[ys[t // regions[0]]:ys[t // regions[0] + 1], xs[t % regions[0]]:xs[t % regions[0] + 1]] = (40, 90, 7)
+    slots, experts = None, None
+    if flat:
+        from odie_amd.config import grid_levels
+        params = 2 * grid_levels(ENCODING)[1]
+        slots, experts = allocate_tiles(torch.from_numpy(image), *regions, params, 64 * params)
+        assert experts == regions[0] * regions[1] - len(flat)
+    trainer = ExpertTrainer(image, ENCODING, *regions, batch, seed=3, fused=False, slots=slots, experts=experts)
     ids_host = synth.integers(3, 'step_ids', n, width * height)
     ids = torch.from_numpy(ids_host).cuda()
     master0 = trainer.master.cpu().numpy().astype(np.float64)
@@ -35,12 +48,17 @@ def test_training_step_matches_oracle(regions, batch, n):
     squares = trainer.step(ids).cpu().numpy()
     torch.cuda.synchronize()
 
-    # routing and encode forward: bit-exact
-    _, perm, local, offsets = oracle.route(ids_host, width, height, *regions)
+    # routing and encode forward: bit-exact (ids without an expert last, with zero features)
+    _, perm, local, offsets = oracle.route(ids_host, width, height, *regions, slots=slots, experts=experts)
+    owned = int(offsets[-1])
+    assert (owned < n) == bool(flat)
     assert np.array_equal(trainer.routing.perm[:n].cpu().numpy(), perm)
     assert np.array_equal(trainer.routing.coords[:n].cpu().numpy().view(np.uint32), local.view(np.uint32))
+    assert np.array_equal(trainer.routing.offsets.cpu().numpy(), offsets)
     rows = rows_of(trainer.grid.levels)
-    raw = oracle.hash_forward(local, table0, rows, 2, offsets=offsets, expert_params=trainer.grid.expert_params)
+    raw = np.zeros((n, 32), dtype=np.float16)
+    raw[:owned] = oracle.hash_forward(local[:owned], table0, rows, 2, offsets=offsets,
+                                      expert_params=trainer.grid.expert_params)
     assert np.array_equal(trainer.raw[:n].cpu().numpy().view(np.uint16), raw.view(np.uint16))
 
     # decoder: the same launch with hidden activations and outputs exported gives the same dz
@@ -73,8 +91,8 @@ def test_training_step_matches_oracle(regions, batch, n):
     # grid gradient from the GPU's dz (loss scale 128)
     total = trainer.grid.table.numel()
     params = trainer.grid.expert_params
-    grad, magnitude, counts = oracle.hash_backward(local, dz, rows, 2, total, offsets=offsets, expert_params=params,
-                                                   counts=True)
+    grad, magnitude, counts = oracle.hash_backward(local[:owned], dz[:owned], rows, 2, total, offsets=offsets,
+                                                   expert_params=params, counts=True)
     got = trainer.gradient.cpu().numpy().astype(np.float64)
     check_gradient(got, grad, magnitude, counts, hash_quantum(dz, rows, 2, total, offsets=offsets,
                                                               expert_params=params), 'step')
