@@ -248,6 +248,19 @@ int odie_cell_bounds(int width, int height, int resolution, int32_t* xb, int32_t
  * (odie/native/selection_cuda.cu:14-17).  No counterpart entry point in the reference. */
 int odie_topk(const double* scores, int64_t n, int64_t k, int32_t* ids, uint64_t stream);
 
+/* B1, the mean-rank admission of select_mean_rank (odie/selection.py:108-126), on the device:
+ * the R^2 cells ranked by descending score (fp64 [R^2], finite and >= 0 -- the caller checks, as
+ * the reference's _validate does), ties by ascending cell id (the sign-cleared FP64 key of
+ * odie_topk), each admitted in rank order when the closure nodes it adds -- its corners
+ * (cell + {0, 1, R, R+1}) mod align8(R^2) not yet taken, a corner listed twice counted twice --
+ * keep the running count within cap (8-aligned, at most align8(R^2)).  Writes chosen uint8 [R^2],
+ * nodes uint8 [align8(R^2)] (1: taken) and stats int64 [2] = {nodes counted against the cap,
+ * cells walked = R^2}.  workspace: odie_select_mean_rank_workspace(R) bytes (-1 unless
+ * 1 <= R^2 <= 2^24).  No counterpart entry point in the reference (its B1 runs in numpy). */
+int64_t odie_select_mean_rank_workspace(int resolution);
+int odie_select_mean_rank(const double* scores, int resolution, int cap, uint8_t* chosen, uint8_t* nodes,
+                          int64_t* stats, void* workspace, int64_t workspace_bytes, uint64_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * B2 exact greedy support selection on the device (odie/selection.py:129-207): free cells
  * (no new closure node) are taken first, in ascending id; otherwise the cell with the best

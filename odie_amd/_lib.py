@@ -37,6 +37,8 @@ SIGNATURES = {
     'odie_packed_backward': ([_P, _I64, _P, _I, _P, _I, _P, _P, _P, _P, _I64, _U64], _I),
     'odie_route_workspace': ([_I64, _I], _I64),
     'odie_route': ([_P, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _U64], _I),
+    'odie_select_mean_rank_workspace': ([_I], _I64),
+    'odie_select_mean_rank': ([_P, _I, _I, _P, _P, _P, _P, _I64, _U64], _I),
     'odie_route_allocated': ([_P, _P, _I64, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _U64], _I),
     'odie_route_noalloc': ([_P, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _U64], _I),
     'odie_route_stratified': ([_P, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _U64], _I),

@@ -1,5 +1,6 @@
 """Selection-side geometry and the GPU selectors: the residual's cell bounds, closure checks,
-top-k and the B2 exact greedy (odie/selection.py, odie/gpu_residual.py:75-179).
+top-k, the B1 mean-rank admission and the B2 exact greedy (odie/selection.py,
+odie/gpu_residual.py:75-179).
 
 The cell bounds come from the encode's own geometry evaluated on the device (odie_cell_bounds):
 a pixel's cell is floor(fmaf(R-1, x, 0.5)) of its coordinate, as odie/selection.py:16-55 defines
@@ -131,3 +132,33 @@ def select_device(scores, resolution, cap, normalize_by_cost=True, trace=False, 
     if trace:
         return selected, nodes, iterations, state.trace[:iterations]
     return selected, nodes, iterations
+
+
+def select_mean_rank(mean, resolution, cap):
+    """B1 (odie/selection.py:108-126) on the device: cells ranked by descending score, ties by
+    ascending cell id, each admitted when the closure nodes it adds keep the count within the
+    node cap (odie_select_mean_rank).  mean: fp64 scores [R^2] (CUDA); the reference's argument
+    checks and its record.  Returns (selected bool [R^2] on the device, record)."""
+    mean = torch.as_tensor(mean)
+    if (mean.dtype != torch.float64 or mean.ndim != 1 or mean.numel() != resolution ** 2
+            or not bool(torch.isfinite(mean).all()) or bool((mean < 0).any())):
+        raise ValueError('Scores must be a finite nonnegative R^2 vector')
+    if type(cap) is not int or cap % 8 or not 0 <= cap <= align8(resolution ** 2):
+        raise ValueError('Node cap must be 8-aligned and within the native plane')
+    mean = mean.to('cuda' if not mean.is_cuda else mean.device).contiguous()
+    lib, device = _lib.library(), mean.device
+    need = int(lib.odie_select_mean_rank_workspace(resolution))
+    if need < 0:
+        raise ValueError('resolution^2 must be within 1..2^24')
+    n = resolution * resolution
+    workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    chosen = torch.empty(n, dtype=torch.uint8, device=device)
+    nodes = torch.empty(align8(n), dtype=torch.uint8, device=device)
+    stats = torch.empty(2, dtype=torch.int64, device=device)
+    _lib.check(lib.odie_select_mean_rank(mean.data_ptr(), resolution, cap, chosen.data_ptr(), nodes.data_ptr(),
+                                         stats.data_ptr(), workspace.data_ptr(), need, _lib.stream_of(mean)))
+    selected = chosen.bool()
+    record = selection_record(selected.cpu().numpy(), nodes.bool().cpu().numpy(), resolution, cap,
+                              'B1 live RGB region mean; stable cell ranking adapted to complete node cap',
+                              int(stats[1]))
+    return selected, record

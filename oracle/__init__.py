@@ -32,7 +32,8 @@ PINS = {
     'residual': 'numpy bincount restatement of odie/selection.py:58-73',
     'native_thresholds': 'exact rational fma boundaries brute-forced over fp32 bit patterns',
     'select_benefit_cost': 'O(n^2) brute-force greedy on tiny resolutions with planted ties',
-    'select_mean_rank': 'brute-force restatement on tiny resolutions',
+    'select_mean_rank': 'brute force over every subset of tiny grids (R <= 4) with planted ties: the first '
+                        'feasible subset in rank order (tests/test_oracle_pins.py)',
     'adam': 'torch.optim.Adam on the CPU (torch-style variant)',
     'compaction/topk': 'numpy.argsort(kind="stable")',
     'mlp': 'torch.nn.functional.linear/relu in float64 on the CPU (same fp16 weights and inputs); '

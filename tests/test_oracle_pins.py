@@ -388,6 +388,42 @@ def test_b1_mean_rank_respects_cap_and_order(oracle):
     assert np.array_equal(closure, np.flatnonzero(nodes))
 
 
+def _subset_cost(cells, resolution, points):
+    """Node slots a set of cells (listed in rank order) spends under B1's count: each cell's four
+    corner entries that no earlier cell of the set touched, an entry listed twice counted twice."""
+    seen, cost = set(), 0
+    for cell in cells:
+        entries = [(cell + d) % points for d in (0, 1, resolution, resolution + 1)]
+        cost += sum(1 for e in entries if e not in seen)
+        seen.update(entries)
+    return cost
+
+
+@pytest.mark.parametrize('resolution,cap,seed', [(1, 0, 0), (1, 8, 1), (2, 8, 2), (3, 8, 3), (3, 16, 4),
+                                                 (4, 8, 5), (4, 16, 6), (4, 24, 7)])
+def test_b1_mean_rank_is_the_first_feasible_subset_in_rank_order(oracle, resolution, cap, seed):
+    """B1 against a brute force over every subset of the cells of tiny grids with planted ties:
+    with the ranking (score descending, id ascending) as priority, the admitted set is the
+    feasible subset (node slots spent within the cap) whose indicator vector in rank order is
+    largest -- the walk's admit-if-it-fits rule, stated without the walk.  Catches a reversed
+    ranking, a wrong tie order and a wrong slot count (R = 1 lists corner 1 twice)."""
+    rng = np.random.default_rng(seed)
+    cells, points = resolution ** 2, oracle_align8(resolution ** 2)
+    scores = rng.choice([0.0, 0.5, 0.5, 2.0, 2.0, 3.0], size=cells)
+    ranking = sorted(range(cells), key=lambda c: (-scores[c], c))
+    best = None
+    for mask in range(1 << cells):
+        members = [c for c in ranking if mask >> c & 1]
+        if _subset_cost(members, resolution, points) > cap:
+            continue
+        vector = tuple(int(mask >> c & 1) for c in ranking)
+        if best is None or vector > best[0]:
+            best = (vector, members)
+    selected, nodes = oracle.select_mean_rank(scores, resolution, cap)
+    assert sorted(np.flatnonzero(selected).tolist()) == sorted(best[1])
+    assert np.array_equal(np.flatnonzero(nodes), oracle.closure_nodes(best[1], resolution) if best[1] else [])
+
+
 def test_topk_and_compaction_against_python_sort(oracle):
     rng = np.random.default_rng(43)
     scores = rng.choice([0.5, 1.5, 2.5, 7.0], size=1000)
