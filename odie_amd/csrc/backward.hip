@@ -254,6 +254,11 @@ struct OwnerArgs {
     const int32_t* band_list;
     const float2* band_sorted;
     const int32_t* ordered;
+    // slice masks (unbanded hashed levels cut into at most 8 aligned blocks of 2^row_bits entries):
+    // byte i of plane mask_plane[l] has bit s set when a corner of coordinate i lands in block s
+    const uint8_t* masks;
+    int mask_plane[ODIE_MAX_LEVELS];   // -1: no mask for the level
+    int ring_at;                       // byte offset of the waves' rings in the dynamic LDS
 };
 
 constexpr int32_t kNonFinite = 1 << 30;   // shift of a column whose upstream bound is not finite
@@ -335,22 +340,29 @@ __device__ inline int level_kind(const DevLevel& lv) {
 // us[c] = upstream feature c times the fixed-point scale 2^S ((w*u)*2^S == w*(u*2^S) exactly:
 // scaling by a power of two commutes with rounding).  Contributions are rounded to integers
 // before the (divergent) slice test so the masked part of the wave is only the LDS add.
-template <int F, int KIND>
-__device__ inline void contribute(float x, float y, const float* us, const DevLevel& lv, uint32_t lo, uint32_t span,
-                                  unsigned long long* acc) {
+// Bilinear weights and table entries of the four corners of (x, y) at one level (the forward's
+// grid_corners, per level kind).
+template <int KIND>
+__device__ inline void corner_geometry(float x, float y, const DevLevel& lv, uint32_t idx[4], float w[4]) {
     const float px = __builtin_fmaf(lv.scale, x, 0.5f);
     const float py = __builtin_fmaf(lv.scale, y, 0.5f);
     const float flx = floorf(px), fly = floorf(py);
     const uint32_t gx = static_cast<uint32_t>(static_cast<int32_t>(flx));
     const uint32_t gy = static_cast<uint32_t>(static_cast<int32_t>(fly));
     const float fx = px - flx, fy = py - fly;
-    float w[4];
     w[0] = (1.0f - fx) * (1.0f - fy);
     w[1] = fx * (1.0f - fy);
     w[2] = (1.0f - fx) * fy;
     w[3] = fx * fy;
-    uint32_t idx[4];
     corner_index<KIND>(gx, gy, lv, idx);
+}
+
+template <int F, int KIND>
+__device__ inline void contribute(float x, float y, const float* us, const DevLevel& lv, uint32_t lo, uint32_t span,
+                                  unsigned long long* acc) {
+    float w[4];
+    uint32_t idx[4];
+    corner_geometry<KIND>(x, y, lv, idx, w);
     int32_t q[4][F];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -428,6 +440,119 @@ __device__ inline void accumulate_level(const float* coords, const Elem<HALF>* p
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
+    }
+}
+
+// A masked slice: each wave scans its runs of 256 of the coordinates [b0, b1) through their mask
+// bytes (the next run's bytes loaded before the current run is used), queues those with a corner
+// in block `block` of the level in a ring of kRing indices in LDS (ballot positions, no barrier:
+// the ring is the wave's own), and evaluates kTake queued coordinates at a time, six per lane
+// with all their loads issued first -- so the geometry runs only for coordinates that land
+// (about 1.9 of a hashed level's 8 blocks per coordinate, 1 to 2 of a dense level's) instead of
+// for all of them.
+constexpr int kRing = 384;                  // >= kTake - 1 + 64: a group of 64's hits always fit
+constexpr int kTake = 256;
+constexpr int kRingBytes = kWaves * kRing * 4;
+static_assert(kRing >= kTake - 1 + 64 && kRing <= 2 * kTake, "ring bound and single-subtraction wrap");
+
+__device__ inline uint32_t ring_slot(uint32_t at) { return at < kRing ? at : at - kRing; }   // at < 2 kRing
+
+template <int F, bool HALF, int KIND>
+__device__ inline void accumulate_masked(const float* coords, const Elem<HALF>* plane, const uint8_t* mask,
+                                         const DevLevel lv, int64_t b0, int64_t b1, uint32_t block, uint32_t lo,
+                                         uint32_t span, const float* scale, unsigned long long* acc,
+                                         int32_t* ring) {
+    constexpr int kPer = kTake / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t below = (uint64_t{1} << lane) - 1;
+    uint32_t head = 0, count = 0;   // wave-uniform; head < kRing
+    const auto evaluate = [&](uint32_t take) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        int32_t at[kPer];
+        bool ok[kPer];
+#pragma unroll
+        for (int b = 0; b < kPer; ++b) {
+            const uint32_t k = static_cast<uint32_t>(lane) + 64u * b;
+            ok[b] = k < take;
+            at[b] = ring[ring_slot(head + (ok[b] ? k : 0u))];
+        }
+        float2 xy[kPer];
+        float us[kPer][F];
+#pragma unroll
+        for (int b = 0; b < kPer; ++b) {
+            xy[b] = reinterpret_cast<const float2*>(coords)[at[b]];
+            load_upstream<F, HALF>(plane, at[b], scale, ok[b], us[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < kPer; ++b)
+            if (64u * b < take) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        head = ring_slot(head + take);
+        count -= take;
+    };
+    const auto load_run = [&](int64_t run, uint32_t m[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t i = run + 64 * q + lane;
+            m[q] = i < b1 ? mask[i] : 0u;
+        }
+    };
+    uint32_t next[4];
+    int64_t run = b0 + 256 * wave;
+    if (run < b1) load_run(run, next);
+    for (; run < b1; run += 256 * kWaves) {
+        uint32_t m[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) m[q] = next[q];
+        if (run + 256 * kWaves < b1) load_run(run + 256 * kWaves, next);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool hit = (m[q] >> block) & 1u;
+            const uint64_t ballot = __ballot(hit);
+            if (hit) ring[ring_slot(head + count + static_cast<uint32_t>(__popcll(ballot & below)))] =
+                static_cast<int32_t>(run + 64 * q + lane);
+            count += static_cast<uint32_t>(__popcll(ballot));
+            if (count >= kTake) evaluate(kTake);
+        }
+    }
+    while (count > 0) evaluate(count < kTake ? count : kTake);
+}
+
+// Mask bytes of the masked levels: plane p, byte i = the aligned blocks of 2^bits[p] entries of
+// level level[p] that the corners of coordinate i land in (bit s: block s).
+constexpr int kMaxMaskPlanes = 16;
+
+struct MaskArgs {
+    const float* coords;
+    uint8_t* masks;
+    int64_t n;
+    int planes;
+    int bits[kMaxMaskPlanes];
+    DevLevel level[kMaxMaskPlanes];
+};
+
+__global__ __launch_bounds__(256) void slice_mask_kernel(MaskArgs a) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.n) return;
+    const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
+    for (int p = 0; p < a.planes; ++p) {
+        const DevLevel lv = a.level[p];
+        uint32_t idx[4];
+        float w[4];
+        switch (level_kind(lv)) {
+            case kHashed24: corner_geometry<kHashed24>(xy.x, xy.y, lv, idx, w); break;
+            case kHashedPow2: corner_geometry<kHashedPow2>(xy.x, xy.y, lv, idx, w); break;
+            case kGeneric: corner_geometry<kGeneric>(xy.x, xy.y, lv, idx, w); break;
+            default: corner_geometry<kDense>(xy.x, xy.y, lv, idx, w); break;
+        }
+        uint32_t byte = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) byte |= 1u << (idx[k] >> a.bits[p]);
+        a.masks[static_cast<int64_t>(p) * a.n + i] = static_cast<uint8_t>(byte);
     }
 }
 
@@ -918,6 +1043,15 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                 case kGeneric: accumulate_runs<F, HALF, kGeneric>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
                 default: accumulate_runs<F, HALF, kDense>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
             }
+        } else if (!grouped && a.masks && a.mask_plane[l] >= 0) {
+            const uint8_t* mask = a.masks + static_cast<int64_t>(a.mask_plane[l]) * a.n;
+            int32_t* ring = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(acc) + a.ring_at) + (threadIdx.x >> 6) * kRing;
+            switch (kind) {
+                case kHashed24: accumulate_masked<F, HALF, kHashed24>(a.coords, plane, mask, lv, b0, b1, static_cast<uint32_t>(slice), lo, span, scale, acc, ring); break;
+                case kHashedPow2: accumulate_masked<F, HALF, kHashedPow2>(a.coords, plane, mask, lv, b0, b1, static_cast<uint32_t>(slice), lo, span, scale, acc, ring); break;
+                case kGeneric: accumulate_masked<F, HALF, kGeneric>(a.coords, plane, mask, lv, b0, b1, static_cast<uint32_t>(slice), lo, span, scale, acc, ring); break;
+                default: accumulate_masked<F, HALF, kDense>(a.coords, plane, mask, lv, b0, b1, static_cast<uint32_t>(slice), lo, span, scale, acc, ring); break;
+            }
         } else {
             switch (kind) {
                 case kHashed24:
@@ -1311,12 +1445,17 @@ int launch_owner_backward(const OwnerLaunch& in) {
     while ((int64_t{2} << bits) * F <= cap) ++bits;   // 2^bits entries: largest block that fits
     // Slices of the finer levels: as many equal parts as the LDS needs; banded, hashed levels
     // take aligned blocks of 2^bits entries (a block is reached from the rows whose hash selects it).
-    const auto slice_level = [&](int l, bool band, int64_t& slices, int64_t& entries, int& row_bits) {
+    // Masked levels take aligned blocks of 2^bits entries too (the last one short on a dense level).
+    const auto slice_level = [&](int l, bool band, bool masked, int64_t& slices, int64_t& entries, int& row_bits) {
         const DevLevel& lv = in.levels[l];
         slices = (static_cast<int64_t>(lv.size) * F + cap - 1) / cap;
         entries = (lv.size + slices - 1) / slices;
         row_bits = 0;
-        if (band && lv.hashed && lv.mask && (int64_t{1} << bits) < lv.size) {
+        if (masked) {
+            entries = int64_t{1} << bits;
+            slices = (lv.size + entries - 1) / entries;
+            row_bits = bits;
+        } else if (band && lv.hashed && lv.mask && (int64_t{1} << bits) < lv.size) {
             entries = int64_t{1} << bits;
             slices = lv.size / entries;
             row_bits = bits;
@@ -1332,21 +1471,38 @@ int launch_owner_backward(const OwnerLaunch& in) {
         for (int l = group; l < L; ++l) {
             int64_t slices, entries;
             int row_bits;
-            slice_level(l, false, slices, entries, row_bits);
+            slice_level(l, false, false, slices, entries, row_bits);
             plain += slices;
-            slice_level(l, true, slices, entries, row_bits);
+            slice_level(l, true, false, slices, entries, row_bits);
             listed += slices * band_coverage(in.levels[l], entries, slices, row_bits);
         }
         banded = listed * 4.0 <= plain;
     }
     banded = banded && in.n < (int64_t{1} << 31) - 1;
     o.banded = banded;
+    // Slice masks (unbanded): a level cut into 2..8 aligned blocks of 2^bits entries whose
+    // accumulators leave room for the waves' rings in the dynamic LDS.
+    const size_t shmem = static_cast<size_t>(cap + F) * 8 + kReserveBytes;
+    MaskArgs mask_args{};
+    for (int l = 0; l < L; ++l) o.mask_plane[l] = -1;
+    for (int l = group; l < L && in.masks && !banded; ++l) {
+        const DevLevel& lv = in.levels[l];
+        const int64_t block = int64_t{1} << bits;
+        const bool fits = static_cast<size_t>(block * F * 8 + kRingBytes) <= shmem;
+        if (block < lv.size && (lv.size + block - 1) / block <= 8 && fits && mask_args.planes < kMaxMaskPlanes) {
+            o.mask_plane[l] = mask_args.planes;
+            mask_args.bits[mask_args.planes] = bits;
+            mask_args.level[mask_args.planes] = lv;
+            ++mask_args.planes;
+        }
+    }
+    o.ring_at = static_cast<int>(shmem - kRingBytes);
     int passes = group > 0 ? 1 : 0;
     for (int l = 0; l < L; ++l) {
         o.level[l] = in.levels[l];
         if (l < group) continue;
         int64_t slices, entries;
-        slice_level(l, banded, slices, entries, o.row_bits[l]);
+        slice_level(l, banded, o.mask_plane[l] >= 0, slices, entries, o.row_bits[l]);
         o.slices[l] = static_cast<int>(slices);
         o.slice_entries[l] = static_cast<int>(entries);
         passes += static_cast<int>(slices);
@@ -1446,8 +1602,9 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t start_bytes = lists ? align(static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4 + 4) : 0;
     const size_t list_bytes = lists ? align(static_cast<size_t>(in.n) * 4) : 0;
     const size_t sorted_bytes = lists ? align(static_cast<size_t>(in.n) * 8) : 0;
+    const size_t mask_bytes = align(static_cast<size_t>(in.n) * mask_args.planes);
     const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, peak_bytes,
-                            count_bytes, start_bytes, list_bytes, sorted_bytes};
+                            count_bytes, start_bytes, list_bytes, sorted_bytes, mask_bytes};
     constexpr int kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t at[kParts], sum = 0;
     for (int k = 0; k < kParts; ++k) {
@@ -1469,6 +1626,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.band_list = reinterpret_cast<const int32_t*>(space + at[7]);
     o.band_sorted = reinterpret_cast<const float2*>(space + at[8]);
     o.ordered = reinterpret_cast<const int32_t*>(space + at[6] + static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4);
+    o.masks = mask_args.planes ? reinterpret_cast<const uint8_t*>(space + at[9]) : nullptr;
     o.grad = in.grad;
     hipStream_t s = in.stream;
 
@@ -1507,7 +1665,6 @@ int launch_owner_backward(const OwnerLaunch& in) {
     t.vec_rows = (reinterpret_cast<uintptr_t>(in.upstream) % 16 == 0) && (in.up_width * elem) % 16 == 0 &&
                  (L * F * elem) % 16 == 0;
     const uint32_t tblocks = static_cast<uint32_t>(row_blocks);
-    const size_t shmem = static_cast<size_t>(cap + F) * 8 + kReserveBytes;
     const uint32_t oblocks = round_up(static_cast<uint32_t>(static_cast<int64_t>(in.experts) * items), kXcds);
 
 #define ODIE_TRANSPOSE(FF, HH)                                                                          \
@@ -1518,8 +1675,14 @@ int launch_owner_backward(const OwnerLaunch& in) {
         } else if (L <= 16) transpose_kernel<FF, HH, 16><<<tblocks, kTransposeBlock, 0, s>>>(t);        \
         else transpose_kernel<FF, HH, 32><<<tblocks, kTransposeBlock, 0, s>>>(t);                       \
     } while (0)
-    // every column's peak over each expert's records, then the owner pass
+    // every column's peak over each expert's records, the slice masks, then the owner pass
     const auto launch_peaks = [&]() {
+        if (mask_args.planes) {
+            mask_args.coords = in.coords;
+            mask_args.masks = const_cast<uint8_t*>(o.masks);
+            mask_args.n = in.n;
+            slice_mask_kernel<<<static_cast<uint32_t>((in.n + 255) / 256), 256, 0, s>>>(mask_args);
+        }
         if (launch_fill_zero(reinterpret_cast<float*>(peaks), static_cast<int64_t>(in.experts) * L * F, s)) return -1;
         const int64_t runs = (records + static_cast<int64_t>(kPeakRecords) * in.experts - 1) /
                              (static_cast<int64_t>(kPeakRecords) * in.experts);

@@ -50,6 +50,8 @@ struct Tuning {
     int backward_mode = 1;          // 0: LDS + global fp32 atomics, 1: owner computes
     int banded = 2;                 // owner: fine passes walk y-band lists (0 never, 1 always, 2 when they pay)
     int split_target = 0;           // owner, banded: coordinate-level visits per work item (0: automatic)
+    int owner_masks = 1;            // owner, unbanded: hashed slices walk only the coordinates whose
+                                    // slice mask reaches them (0: every coordinate)
     int packed_owner = 0;           // packed backward: 1 owner computes (deterministic), 0 global atomics
                                     // (measured faster on the 65536-id native steps: 0.30 vs 0.56 ms)
     int packed_splits = 0;          // packed owner: coordinate splits per slice (0: automatic)
@@ -675,6 +677,7 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "xcd_remap" && (value == 0 || value == 1)) t.xcd_remap = value;
     else if (key == "backward_mode" && (value == 0 || value == 1)) t.backward_mode = value;
     else if (key == "banded" && value >= 0 && value <= 2) t.banded = value;
+    else if (key == "owner_masks" && (value == 0 || value == 1)) t.owner_masks = value;
     else if (key == "split_target" && value >= 0) t.split_target = value;
     else if (key == "packed_owner" && (value == 0 || value == 1)) t.packed_owner = value;
     else if (key == "packed_splits" && value >= 0 && value <= 64) t.packed_splits = value;
@@ -783,6 +786,7 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
         o.lds_bytes = t.owner_lds_bytes;
         o.remap = t.xcd_remap;
         o.banded = t.banded;
+        o.masks = t.owner_masks;
         o.split_target = t.split_target;
         o.stream = s;
         return launch_owner_backward(o);
@@ -875,6 +879,7 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
     o.lds_bytes = t.owner_lds_bytes;
     o.remap = t.xcd_remap;
     o.banded = t.banded;
+    o.masks = t.owner_masks;
     o.split_target = t.split_target;
     o.stream = s;
     o.adam = adam;

@@ -196,6 +196,7 @@ struct OwnerLaunch {
     int64_t lds_bytes;
     int remap;
     int banded;               // fine passes walk y-band lists: 0 never, 1 always, 2 when they pay
+    int masks;                // unbanded hashed slices walk only coordinates whose slice mask reaches them
     int64_t split_target;     // banded: coordinate-level visits per work item (0: chosen per launch)
     hipStream_t stream;
     const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad

@@ -489,3 +489,20 @@ def test_planes_backward_equals_rows(experts, n):
     assert torch.equal(rows.view(torch.int32), via_planes.view(torch.int32))
     twice = grid.backward_planes(coords, offsets, planes, blockmax, gradient=via_planes.clone(), accumulate=True)
     assert torch.equal(twice, 2 * rows)
+
+
+@pytest.mark.parametrize('log2,experts,n,outside', [(16, 64, 1 << 20, False), (14, 16, 300000, True),
+                                                    (15, 3, 5000, True), (16, 1, 65536, False)])
+def test_owner_masks_are_bit_identical(log2, experts, n, outside):
+    """Hashed slices that walk only the coordinates whose slice masks reach them form the same
+    integer sums as slices that walk every coordinate: the gradient bit for bit (coordinates off
+    the unit square included), for 2- to 8-block levels."""
+    levels, params, offsets, xy, up = _expert_batch(log2 + 3, log2, experts, n, outside)
+    run = lambda: grid_backward(xy, up.half(), levels, 2, offsets=offsets, experts=experts, expert_params=params)
+    _lib.set_tuning('banded', 0)
+    try:
+        masked = _tuned('owner_masks', 1, 1, run)
+        plain = _tuned('owner_masks', 0, 1, run)
+    finally:
+        _lib.set_tuning('banded', 2)
+    assert torch.equal(masked.view(torch.int32), plain.view(torch.int32))
