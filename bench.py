@@ -61,6 +61,8 @@ def parse():
     parser.add_argument('--no-native', action='store_true', help='skip the 65536-id native step measurement')
     parser.add_argument('--no-single', action='store_true', help='skip the single-expert 2^19-table fwd+bwd line')
     parser.add_argument('--no-c1', action='store_true', help='skip the single-expert fp32 forward of 2^18 coords')
+    parser.add_argument('--no-literal', action='store_true',
+                        help='skip the encode fwd+bwd measurement without the optimizer step')
     parser.add_argument('--single-only', action='store_true',
                         help='print only the single-expert 2^19-table fwd+bwd line (for kernel traces of it)')
     parser.add_argument('--native-steps', type=int, default=200)
@@ -623,7 +625,8 @@ def main():
                      'algorithmic_bytes_per_launch': stage_bytes[dominant], 'avg_ms': stage_ms[dominant]},
         'loss_after_timed_steps': loss,
     }
-    result['encode_fwd_bwd_literal'] = encode_literal(trainer, args.steps)
+    if not args.no_literal:
+        result['encode_fwd_bwd_literal'] = encode_literal(trainer, args.steps)
     if not args.no_c1:
         result['c1_forward'] = c1_forward(200, not args.no_cpu)
     if not args.no_single:

@@ -254,9 +254,11 @@ struct OwnerArgs {
     const int32_t* band_list;
     const float2* band_sorted;
     const int32_t* ordered;
-    // slice masks (unbanded hashed levels cut into at most 8 aligned blocks of 2^row_bits entries):
-    // byte i of plane mask_plane[l] has bit s set when a corner of coordinate i lands in block s
+    // slice masks (unbanded levels cut into at most 8 aligned blocks of 2^row_bits entries):
+    // byte i of plane mask_plane[l] (planes mask_stride bytes apart) has bit s set when a corner
+    // of coordinate i lands in block s
     const uint8_t* masks;
+    int64_t mask_stride;
     int mask_plane[ODIE_MAX_LEVELS];   // -1: no mask for the level
     int ring_at;                       // byte offset of the waves' rings in the dynamic LDS
 };
@@ -523,20 +525,29 @@ __device__ inline void accumulate_masked(const float* coords, const Elem<HALF>* 
 }
 
 // Mask bytes of the masked levels: plane p, byte i = the aligned blocks of 2^bits[p] entries of
-// level level[p] that the corners of coordinate i land in (bit s: block s).
+// level level[p] that the corners of coordinate i land in (bit s: block s).  Planes are `stride`
+// bytes apart.  The launch also clears the column peaks (zero words).
 constexpr int kMaxMaskPlanes = 16;
 
 struct MaskArgs {
     const float* coords;
     uint8_t* masks;
+    uint32_t* peaks;     // cleared here for column_peaks_kernel
+    int64_t peak_words;
     int64_t n;
+    int64_t stride;
     int planes;
     int bits[kMaxMaskPlanes];
     DevLevel level[kMaxMaskPlanes];
 };
 
+// One coordinate per thread, every plane (measured on MI355X: 44 us for 2^22 coordinates and 10
+// planes; a shortcut that takes a hashed level's blocks from the row hashes alone, four
+// coordinates per thread with word stores, descriptors from LDS, or one plane per block row were
+// all slower, 58-90 us).
 __global__ __launch_bounds__(256) void slice_mask_kernel(MaskArgs a) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    for (int64_t j = i; j < a.peak_words; j += static_cast<int64_t>(gridDim.x) * 256) a.peaks[j] = 0u;
     if (i >= a.n) return;
     const float2 xy = reinterpret_cast<const float2*>(a.coords)[i];
     for (int p = 0; p < a.planes; ++p) {
@@ -552,7 +563,7 @@ __global__ __launch_bounds__(256) void slice_mask_kernel(MaskArgs a) {
         uint32_t byte = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) byte |= 1u << (idx[k] >> a.bits[p]);
-        a.masks[static_cast<int64_t>(p) * a.n + i] = static_cast<uint8_t>(byte);
+        a.masks[static_cast<int64_t>(p) * a.stride + i] = static_cast<uint8_t>(byte);
     }
 }
 
@@ -918,7 +929,7 @@ __device__ inline uint32_t work_of(uint32_t block, uint32_t blocks, int remap, u
 // expert e's records; thread t takes column t % columns of every (kPeakBlock / columns)-th
 // record of the run; one LDS, then one global maximum per column.  peaks must be zero on entry.
 constexpr int kPeakBlock = 256;
-constexpr int kPeakRecords = 256;
+constexpr int kPeakRecords = 32;
 
 __global__ __launch_bounds__(kPeakBlock) void column_peaks_kernel(OwnerArgs a, uint32_t* peaks) {
     __shared__ uint32_t block_peak[kPeakBlock];
@@ -1044,7 +1055,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                 default: accumulate_runs<F, HALF, kDense>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
             }
         } else if (!grouped && a.masks && a.mask_plane[l] >= 0) {
-            const uint8_t* mask = a.masks + static_cast<int64_t>(a.mask_plane[l]) * a.n;
+            const uint8_t* mask = a.masks + static_cast<int64_t>(a.mask_plane[l]) * a.mask_stride;
             int32_t* ring = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(acc) + a.ring_at) + (threadIdx.x >> 6) * kRing;
             switch (kind) {
                 case kHashed24: accumulate_masked<F, HALF, kHashed24>(a.coords, plane, mask, lv, b0, b1, static_cast<uint32_t>(slice), lo, span, scale, acc, ring); break;
@@ -1602,7 +1613,8 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t start_bytes = lists ? align(static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4 + 4) : 0;
     const size_t list_bytes = lists ? align(static_cast<size_t>(in.n) * 4) : 0;
     const size_t sorted_bytes = lists ? align(static_cast<size_t>(in.n) * 8) : 0;
-    const size_t mask_bytes = align(static_cast<size_t>(in.n) * mask_args.planes);
+    const int64_t mask_stride = static_cast<int64_t>(align(static_cast<size_t>(in.n)));
+    const size_t mask_bytes = static_cast<size_t>(mask_stride) * mask_args.planes;
     const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, peak_bytes,
                             count_bytes, start_bytes, list_bytes, sorted_bytes, mask_bytes};
     constexpr int kParts = sizeof(sizes) / sizeof(sizes[0]);
@@ -1627,6 +1639,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.band_sorted = reinterpret_cast<const float2*>(space + at[8]);
     o.ordered = reinterpret_cast<const int32_t*>(space + at[6] + static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4);
     o.masks = mask_args.planes ? reinterpret_cast<const uint8_t*>(space + at[9]) : nullptr;
+    o.mask_stride = mask_stride;
     o.grad = in.grad;
     hipStream_t s = in.stream;
 
@@ -1677,13 +1690,18 @@ int launch_owner_backward(const OwnerLaunch& in) {
     } while (0)
     // every column's peak over each expert's records, the slice masks, then the owner pass
     const auto launch_peaks = [&]() {
-        if (mask_args.planes) {
+        const int64_t peak_words = static_cast<int64_t>(in.experts) * L * F;
+        if (mask_args.planes) {   // the mask launch clears the peaks as well
             mask_args.coords = in.coords;
             mask_args.masks = const_cast<uint8_t*>(o.masks);
+            mask_args.peaks = peaks;
+            mask_args.peak_words = peak_words;
             mask_args.n = in.n;
+            mask_args.stride = mask_stride;
             slice_mask_kernel<<<static_cast<uint32_t>((in.n + 255) / 256), 256, 0, s>>>(mask_args);
+        } else if (launch_fill_zero(reinterpret_cast<float*>(peaks), peak_words, s)) {
+            return -1;
         }
-        if (launch_fill_zero(reinterpret_cast<float*>(peaks), static_cast<int64_t>(in.experts) * L * F, s)) return -1;
         const int64_t runs = (records + static_cast<int64_t>(kPeakRecords) * in.experts - 1) /
                              (static_cast<int64_t>(kPeakRecords) * in.experts);
         const dim3 grid(static_cast<uint32_t>(runs < 1 ? 1 : runs), static_cast<uint32_t>(in.experts));
