@@ -40,12 +40,26 @@ struct AdamStep {
     float inv_bc2_sqrt;     // variant 0: 1 / sqrt(1 - b2^t)
     float log_beta1;        // variants 1, 2: ln b1, ln b2
     float log_beta2;
+    uint32_t rate_first;    // variants 1, 2: the first age of a 256-entry rate table (ages <= the step)
     float half_divisor;     // > 0: gradient rounded through fp16 first (see above); 0: as given
 };
 
+// The step size of variants 1 and 2 at age t: lr * sqrt(1 - b2^t) / (1 - b1^t).
+__device__ inline float adam_rate(const AdamStep& a, uint32_t t) {
+    const float age_f = static_cast<float>(t);
+    return a.lr * sqrtf(-expm1f(age_f * a.log_beta2)) / -expm1f(age_f * a.log_beta1);
+}
+
+// A caller may hold adam_rate of the kRateTable ages from rate_first on (a parameter's age never
+// exceeds the step count, and those that moved on every recent step have the latest ones): a
+// table entry is the function's own value, so the update is the same bit for bit with or without it.
+constexpr int kRateTable = 256;
+
 // Updates p, m, v (and the age) from gradient g (still carrying the loss scale); returns
-// false when the parameter is skipped (variant 1, zero gradient).
-__device__ inline bool adam_math(const AdamStep& a, float g, float& p, float& m, float& v, uint32_t& age) {
+// false when the parameter is skipped (variant 1, zero gradient).  rates: null, or adam_rate of
+// the ages rate_first .. rate_first + kRateTable - 1.
+__device__ inline bool adam_math(const AdamStep& a, float g, float& p, float& m, float& v, uint32_t& age,
+                                 const float* rates = nullptr) {
     if (a.half_divisor > 0.0f)
         g = __half2float(__float2half_rn(__half2float(__float2half_rn(g)) / a.half_divisor));
     g = g * a.inv_scale;
@@ -55,8 +69,8 @@ __device__ inline bool adam_math(const AdamStep& a, float g, float& p, float& m,
         v = a.beta2 * v + (1.0f - a.beta2) * (g * g);
         const uint32_t t = age + 1;
         age = t;
-        const float age_f = static_cast<float>(t);
-        const float rate = a.lr * sqrtf(-expm1f(age_f * a.log_beta2)) / -expm1f(age_f * a.log_beta1);
+        const uint32_t slot = t - a.rate_first;   // wraps past the table for t < rate_first
+        const float rate = rates && slot < kRateTable ? rates[slot] : adam_rate(a, t);
         p = p - rate * (m / (sqrtf(v) + a.eps));
     } else {
         m = a.beta1 * m + (1.0f - a.beta1) * g;

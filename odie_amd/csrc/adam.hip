@@ -33,6 +33,7 @@ int make_adam_step(const char* what, float* master, uint16_t* half_copy, float* 
     a.inv_scale = 1.0f / loss_scale;
     a.log_beta1 = static_cast<float>(std::log(static_cast<double>(beta1)));
     a.log_beta2 = static_cast<float>(std::log(static_cast<double>(beta2)));
+    a.rate_first = step >= kRateTable ? static_cast<uint32_t>(step - kRateTable + 1) : 1u;
     if (variant == 0) {
         const double bc1 = 1.0 - std::pow(static_cast<double>(beta1), static_cast<double>(step));
         const double bc2 = 1.0 - std::pow(static_cast<double>(beta2), static_cast<double>(step));

@@ -970,6 +970,7 @@ __device__ inline void level_shifts(const OwnerArgs& a, int e, int l, int64_t co
 template <int F, bool HALF>
 __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     extern __shared__ unsigned long long acc[];
+    __shared__ float rates[kRateTable];   // fused flush: the optimizer's step size of the recent ages
     using U = Elem<HALF>;
     const uint32_t per_expert = static_cast<uint32_t>(a.items);
     const uint32_t total = static_cast<uint32_t>(a.experts) * per_expert;
@@ -1015,6 +1016,8 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
     const int64_t b1 = b0 + share < stop ? b0 + share : stop;
     const int64_t count = stop - base;
     for (uint32_t j = threadIdx.x; j < span; j += kOwnerBlock) acc[j] = 0ull;
+    if (a.fused && a.adam.variant != 0 && threadIdx.x < kRateTable)
+        rates[threadIdx.x] = adam_rate(a.adam, a.adam.rate_first + threadIdx.x);
     __syncthreads();
 
     // A banded fine pass walks the pieces of its share of the band-list runs its rows reach.
@@ -1123,7 +1126,7 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
                 const uint32_t j = j0 + k * kOwnerBlock;
                 if (j >= span) continue;
                 const int64_t i = first + j;
-                if (adam_math(o, g[k], w[k], m[k], v[k], age[k])) {
+                if (adam_math(o, g[k], w[k], m[k], v[k], age[k], rates)) {
                     o.master[i] = w[k];
                     o.m[i] = m[k];
                     o.v[i] = v[k];

@@ -59,7 +59,7 @@ struct Tuning {
     int packed_blocks = 256;        // packed backward with LDS: most blocks (each flushes its partials once)
     int paired_loads = 0;           // forward: 16-byte corner-pair loads (measured no gain)
     int forward_lds_bytes = 28672;  // forward: LDS budget for staged coarse levels (0: off)
-    int owner_lds_bytes = 162816;   // 160 KiB minus static LDS
+    int owner_lds_bytes = 162816;   // 160 KiB minus the owner kernel's static 1 KiB (its Adam rate table)
 };
 Tuning& tuning() {
     static Tuning t;

@@ -146,3 +146,35 @@ def test_fused_backward_with_split_group_pass():
         x, y = (getattr(o, name).cpu().numpy() for o in optimizers)
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
     assert np.array_equal(optimizers[0].steps.cpu().numpy(), optimizers[1].steps.cpu().numpy())
+
+
+@pytest.mark.parametrize('variant', ['tcnn', 'tcnn_dense'])
+def test_fused_flush_with_old_and_recent_ages(variant):
+    """Step 300 with per-parameter ages spread over 0..299: the fused flush takes the step size of
+    the latest 256 ages from a per-workgroup table and computes older ones directly; the update is
+    the unfused optimizer's bit for bit."""
+    from odie_amd.experts import ExpertGrid
+    encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=12, base_resolution=8, per_level_scale=1.4)
+    n, experts = 20000, 4
+    grids, optimizers = [], []
+    for _ in range(2):
+        grid = ExpertGrid(encoding, experts, dtype=torch.float16)
+        master = torch.from_numpy(synth.table(8, grid.table.numel())).cuda()
+        grid.table.copy_(master)
+        grids.append(grid)
+        opt = FusedAdam(master, lr=1e-2, variant=variant, half_copy=grid.table)
+        ages = synth.integers(21, 'ages', master.numel(), 300).astype(np.int32)
+        opt.steps.copy_(torch.from_numpy(ages).cuda())
+        opt.m.copy_(master * 1e-3)
+        opt.v.copy_(master * master * 1e-4)
+        opt.step_count = 299
+        optimizers.append(opt)
+    coords = torch.from_numpy(synth.coordinates(9, n)).cuda()
+    offsets = torch.from_numpy(np.linspace(0, n, experts + 1).astype(np.int32)).cuda()
+    upstream = torch.from_numpy(synth.upstream(23, n, 32)).cuda()
+    grids[0].backward_adam(coords, offsets, upstream, optimizers[0], loss_scale=128.0)
+    optimizers[1].step(grids[1].backward(coords, offsets, upstream), loss_scale=128.0)
+    for name in ('master', 'm', 'v', 'steps'):
+        x, y = (getattr(o, name).cpu().numpy() for o in optimizers)
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+    assert np.array_equal(grids[0].table.cpu().numpy().view(np.uint16), grids[1].table.cpu().numpy().view(np.uint16))
