@@ -70,6 +70,8 @@ def parse():
     parser.add_argument('--reconstruction-batch', type=int, default=1 << 26)
     parser.add_argument('--no-gigapixel', action='store_true', help='skip the 1024-expert 2^24-id step')
     parser.add_argument('--gigapixel-steps', type=int, default=5)
+    parser.add_argument('--tune', action='append', default=[], metavar='KEY=VALUE',
+                        help='odie_set_tuning before the run (repeatable), e.g. owner_masks=0')
     parser.add_argument('--copy-probe', action='store_true',
                         help='only run a plain 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE)')
     return parser.parse_args()
@@ -548,6 +550,13 @@ def main():
         print('bench.py measures one GPU: this build has no multi-GPU path (each GPU would run '
               'its own share of the experts); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
+    if args.tune:
+        import torch
+        torch.zeros(1, device='cuda')   # the runtime up before the library loads
+        from odie_amd import _lib
+        for item in args.tune:
+            key, value = item.split('=')
+            _lib.set_tuning(key, int(value))
     if args.single_only:
         print(json.dumps({'single_expert': single_expert_steps(args.steps)}))
         return
