@@ -297,6 +297,16 @@ C2_ENCODING = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=19, ba
 C2_BYTES = {'forward': 328, 'backward': 1096}   # per query: xy 8 + gathers 256 + features 64; xy 8 + upstream 64 + 1024
 
 
+def profiled_traffic(stage):
+    """HBM bytes per launch of a stage's kernels from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (calibrated against a plain copy), or None when that stage was not profiled."""
+    traffic_file = ROOT / 'profiles' / 'traffic.json'
+    if not traffic_file.exists():
+        return None
+    entry = json.loads(traffic_file.read_text()).get(stage)
+    return entry['bytes'] if entry else None
+
+
 def single_expert_steps(steps):
     """The single-expert workload: one 16-level x 2-feature fp16 hash grid (2^19-entry tables,
     base 16, scale 1.38, 5,487,024 parameters), 2^22 coordinates uniform in [0,1)^2 (seed 0), an
@@ -332,13 +342,16 @@ def single_expert_steps(steps):
     gbs = lambda per, ms: n * per / (ms / 1e3) / 1e9
     stage_gbs = {'forward': gbs(C2_BYTES['forward'], forward), 'backward': gbs(C2_BYTES['backward'], backward)}
     dominant = 'backward' if backward >= forward else 'forward'
+    traffic = profiled_traffic('single_expert_' + dominant)
     return {'coords': n, 'params': 2 * entries, 'ms': {'forward': forward, 'backward': backward},
             'queries_per_s': n / (total / 1e3), 'GBps': gbs(sum(C2_BYTES.values()), total),
             'pct_hbm_peak': 100 * gbs(sum(C2_BYTES.values()), total) / HBM_PEAK_GBS,
             'roofline': {'bound': 'hbm', 'kernel': dominant, 'achieved': stage_gbs[dominant], 'peak': HBM_PEAK_GBS,
                          'unit': 'GB/s', 'frac': stage_gbs[dominant] / HBM_PEAK_GBS,
                          'algorithmic_bytes_per_launch': n * C2_BYTES[dominant],
-                         'avg_ms': backward if dominant == 'backward' else forward},
+                         'avg_ms': backward if dominant == 'backward' else forward, 'traffic': traffic,
+                         'frac_physical': traffic / ((backward if dominant == 'backward' else forward) / 1e3)
+                         / 1e9 / HBM_PEAK_GBS if traffic else None},
             'stage_GBps': stage_gbs}
 
 
@@ -604,11 +617,7 @@ def main():
     qps = N_COORDS / (ms / 1e3)
     step_gbs = sum(stage_bytes.values()) / (ms / 1e3) / 1e9
     dominant = max(stage_ms, key=stage_ms.get)
-    traffic_file = ROOT / 'profiles' / 'traffic.json'
-    traffic = None
-    if traffic_file.exists():
-        entry = json.loads(traffic_file.read_text()).get(dominant)
-        traffic = entry['bytes'] if entry else None
+    traffic = profiled_traffic(dominant)
     physical = traffic / (stage_ms[dominant] / 1e3) / 1e9 if traffic else None
     encode_ms = stage_ms['encode_forward'] + stage_ms['encode_backward']
     loss = float(trainer.squares.double().mean())
