@@ -89,9 +89,20 @@ __device__ inline half8 relu8(half8 x) {
 
 // dh where the forward activation h is nonzero, +0 elsewhere: min(bits(h), 1) is 1 or 0 per
 // value and multiplies the bit pattern of dh (v_pk_min_u16, v_pk_mul_lo_u16).
+// dh where the forward activation h is nonzero, +0 elsewhere: min(bits(h), 1) is 1 or 0 per
+// value and multiplies the bit pattern of dh (v_pk_min_u16, v_pk_mul_lo_u16).  Written as asm:
+// from the ReLU before it the compiler would otherwise turn the two packed integer ops into
+// per-half compares and selects, five times the work.
+__device__ inline uint32_t mask_word(uint32_t dh, uint32_t h, uint32_t ones) {
+    uint32_t r;
+    asm("v_pk_min_u16 %0, %1, %3\n\tv_pk_mul_lo_u16 %0, %0, %2" : "=&v"(r) : "v"(h), "v"(dh), "v"(ones));
+    return r;
+}
 __device__ inline half8 mask8(half8 dh, half8 h) {
-    const ushort8 keep = __builtin_elementwise_min(__builtin_bit_cast(ushort8, h), (ushort8)(uint16_t{1}));
-    return __builtin_bit_cast(half8, __builtin_bit_cast(ushort8, dh) * keep);
+    const u32x4 d = __builtin_bit_cast(u32x4, dh), m = __builtin_bit_cast(u32x4, h);
+    const uint32_t ones = 0x00010001u;
+    return __builtin_bit_cast(half8, (u32x4){mask_word(d.x, m.x, ones), mask_word(d.y, m.y, ones),
+                                             mask_word(d.z, m.z, ones), mask_word(d.w, m.w, ones)});
 }
 
 // Weights into LDS in the six operand layouts (once per workgroup).

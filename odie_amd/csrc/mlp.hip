@@ -14,10 +14,10 @@
 // one lane pair, and the accumulator layout of one layer (lane l: sample l%32, rows
 // 8*(v/4) + 4*(l/32) + v%4) is exactly the B operand of the next layer once the weights' K
 // columns are permuted the same way (slot_of below), so activations never leave registers.
-// Weight gradients contract over samples: each round of 4 tiles is transposed through a
-// workgroup LDS buffer and contracted by the waves, each owning a quarter of the gradient in
-// registers across all rounds; partials per workgroup are reduced by a second kernel in a
-// fixed order: deterministic.
+// Weight gradients contract over samples: each wave transposes its own tile through its own LDS
+// region and accumulates every weight gradient in its registers with 16x16x32 products (no
+// workgroup barrier in the loop); the four waves' gradients are summed in wave order at the end
+// and the workgroups' partials by a second kernel in a fixed order: deterministic.
 #include "mlp.h"
 #include "../../include/odie_amd.h"
 
@@ -66,139 +66,102 @@ template <int KT> struct TileInput {
     uint32_t color;
 };
 
-// The next tile's row of this lane, advanced by a fixed stride each round and kept in one
-// pinned 32-bit register: every prefetch load then addresses base (a kernel argument, in
-// scalar registers) + a 32-bit byte offset derived from it, with no temporary address
-// register whose reuse could force an early wait on the loads in flight.
-__device__ inline uint32_t pin(uint32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-template <class T> __device__ inline T load_at(const T* base, uint32_t byte_offset) {
-    return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_offset);
-}
-
-// Loop-carried row and byte offsets of the next tile's loads (each advanced by a constant).
-struct TileCursor {
-    uint32_t row;       // row index
-    uint32_t off4;      // row * 4
-    uint32_t offx;      // row * 2 * in + 16 * g
-};
-
-template <int KT> __device__ inline void advance(TileCursor& c, uint32_t rows) {
-    c.row = pin(c.row + rows);
-    c.off4 = pin(c.off4 + rows * 4u);
-    c.offx = pin(c.offx + rows * (32u * KT));
-}
-
-template <int KT> __device__ inline void fetch_tile(const MlpArgs& a, const TileCursor& c, TileInput<KT>& in) {
-    const bool valid = c.row < a.n;
+template <int KT> __device__ inline void fetch_tile(const MlpArgs& a, int64_t row, int g, TileInput<KT>& in) {
+    const bool valid = row < a.n;
     // the small loads first: memory counters drain in issue order, so an early wait on them
     // leaves the 64-byte x loads in flight
-    in.input = valid ? (a.rows ? load_at(a.rows, c.off4) : static_cast<int32_t>(c.row)) : 0;
-    in.color = valid && a.colors ? load_at(a.colors, c.off4) : 0u;
-    const half8* x = reinterpret_cast<const half8*>(a.x);
+    in.input = valid ? (a.rows ? a.rows[row] : static_cast<int32_t>(row)) : 0;
+    in.color = valid && a.colors ? a.colors[row] : 0u;
+    const half8* x = reinterpret_cast<const half8*>(a.x + row * (16 * KT) + 8 * g);
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt)   // + 32 kt bytes on the base, not the offset
-        in.xb[kt] = valid ? load_at(x + 2 * kt, c.offx) : half8{};
+    for (int kt = 0; kt < KT; ++kt) in.xb[kt] = valid ? x[2 * kt] : half8{};
 }
 
-// Shared transposition buffer of one round (4 tiles = 128 samples): feature-major rows of
-// 128 samples, padded so that 16-byte reads of 16 consecutive rows hit distinct banks.
-constexpr int kRoundSamples = 32 * kMlpWaves;
-constexpr int kRS = kRoundSamples + 8;
-// phase 1 rows: dy outputs 0..2, h2 (64), dh1 (64), x (in); phase 2 rows: dh2 (64), h1 (64)
-constexpr int kDyRow = 0, kH2Row = 3, kDh1Row = 67, kXRow = 131;
-template <int KT> constexpr int round_rows() { return kXRow + 16 * KT; }
+// Per-wave transposition region: feature-major rows of the 32 samples of the wave's current
+// tile, 40 halfs (80 bytes) apart.  A lane writes one sample of a feature (the 32 lanes of a lane
+// group fill one 64-byte row; the two groups' rows, 4 apart, fall on opposite halves of the
+// banks) and reads 8 samples of one row as a 16x16x32 operand (8 lanes cover 8 rows at 8
+// distinct 16-byte bank offsets).  Rows: phase 1 dy 0..2 (3..15 hold stale values whose products
+// fall in gradient rows that are never written out) and h2 16..79; phase 2 dh2 0..63 and h1
+// 64..127; phase 3 dh1 0..63 and x 64...
+constexpr int kTS = 40;
+template <int KT> constexpr int region_rows() { return 64 + 16 * KT > 128 ? 64 + 16 * KT : 128; }
 
-// Writes this wave's 32 samples of 32*blocks features held in accumulator-row order
-// (h[t][e] = feature feature_of(t, g, e)) into rows first.. of the round buffer.
-__device__ inline void put_features(_Float16* T, int first, int column, const half8* h, int blocks, int g) {
-    for (int t = 0; t < 2 * blocks; ++t)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) T[(first + feature_of(t, g, e)) * kRS + column] = h[t][e];
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+
+// Orders this wave's LDS accesses: lanes read what other lanes of the same wave wrote (the LDS
+// executes one wave's instructions in issue order; this keeps the compiler from moving them).
+__device__ inline void wave_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// One 32x32 block of a weight gradient: sum over the round's 128 samples of rows a0..
-// (M side, rows a0 + s for lanes s < a_rows) times rows b0.. (N side, lanes s < b_rows) of the
-// round buffer; DUAL alternates two accumulators so that consecutive MFMAs do not depend on
-// each other (their sum is the block).
-template <bool DUAL>
-__device__ inline void round_block(const _Float16* T, int a0, int b0, int a_rows, int b_rows, int g, int s,
-                                   f32x16& acc0, f32x16& acc1) {
+// Writes this lane's sample column s of 16*halves features held in accumulator-row order
+// (h[t][e] = feature feature_of(t, g, e)) into rows first.. of the region.
+// Odd elements are stored from the high half of their dword (ds_write_b16_d16_hi).
+__device__ inline void put_rows(_Float16* R, int first, int s, const half8* h, int halves, int g) {
+    uint16_t* r = reinterpret_cast<uint16_t*>(R) + s;
+    for (int t = 0; t < halves; ++t) {
+        const u32x4 d = __builtin_bit_cast(u32x4, h[t]);
 #pragma unroll
-    for (int kt = 0; kt < kRoundSamples / 16; kt += 2) {
-        const half8 a0v = s < a_rows ? lds8(T + (a0 + s) * kRS + kt * 16 + 8 * g) : half8{};
-        const half8 a1v = s < a_rows ? lds8(T + (a0 + s) * kRS + kt * 16 + 16 + 8 * g) : half8{};
-        const half8 b0v = s < b_rows ? lds8(T + (b0 + s) * kRS + kt * 16 + 8 * g) : half8{};
-        const half8 b1v = s < b_rows ? lds8(T + (b0 + s) * kRS + kt * 16 + 16 + 8 * g) : half8{};
-        acc0 = mfma(a0v, b0v, acc0);
-        if constexpr (DUAL) acc1 = mfma(a1v, b1v, acc1);
-        else acc0 = mfma(a1v, b1v, acc0);
+        for (int e = 0; e < 8; e += 2) {
+            r[(first + feature_of(t, g, e)) * kTS] = static_cast<uint16_t>(d[e / 2]);
+            r[(first + feature_of(t, g, e + 1)) * kTS] = static_cast<uint16_t>(d[e / 2] >> 16);
+        }
     }
 }
 
-// Phase-1 gradient blocks of the round: dW3 (dy x h2, two 32-column blocks) then dW1 (dh1 x x,
-// two 32-row blocks times ceil(in/32) column blocks); wave w owns blocks w, w + 4, ...
-template <int KT> struct Phase1 {
-    static constexpr int kColumnBlocks = (KT + 1) / 2;
-    static constexpr int kBlocks = 2 + 2 * kColumnBlocks;
-    static constexpr int kSlots = (kBlocks + kMlpWaves - 1) / kMlpWaves;   // 1 (in <= 32) or 2
-};
-
-// Block b of phase 1: A rows, B rows and their counts; dW1 block (mb, nb) = b - 2 = mb * NB + nb.
-template <int KT> __device__ inline void phase1_block(int b, int& a0, int& b0, int& a_rows, int& b_rows) {
-    if (b < 2) {
-        a0 = kDyRow, a_rows = 3, b0 = kH2Row + 32 * b, b_rows = 32;
-    } else {
-        const int mb = (b - 2) / Phase1<KT>::kColumnBlocks, nb = (b - 2) % Phase1<KT>::kColumnBlocks;
-        a0 = kDh1Row + 32 * mb, a_rows = 32, b0 = kXRow + 32 * nb;
-        b_rows = 16 * KT - 32 * nb < 32 ? 16 * KT - 32 * nb : 32;
-    }
+// 16x16x32 operand of rows first + 16*block ..: lane l holds row first + 16*block + l%16,
+// samples 8*(l/16) .. +7 (the contraction runs over the tile's 32 samples).
+__device__ inline half8 rows16(const _Float16* R, int first, int block, int lane) {
+    return lds8(R + (first + 16 * block + (lane & 15)) * kTS + 8 * (lane >> 4));
 }
 
-// Work split: each wave computes the forward, loss and input gradient of its own tile in
-// registers; the weight gradients are contracted per round of 4 tiles through the shared
-// buffer in two phases (1: dW3 = dy x h2 and dW1 = dh1 x x; 2: dW2 = dh2 x h1), each wave
-// owning its own 32x32 gradient blocks (Phase1 above; phase 2: one dW2 block per wave), so no
-// cross-wave reduction is needed.  PLANES (in = 32 only) writes dz as level-major planes.
-template <int KT, bool PLANES>
-__global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
+// Work split: each wave takes tiles of 32 samples in turn (below: how records of 128 rows are
+// handed out) and computes, per tile, the forward, loss and input gradient in registers (the accumulator layout of one
+// layer is the B operand of the next), then the tile's share of every weight gradient: the tile's
+// activations and gradients pass through the wave's own LDS region (one fp16 per sample and
+// feature) and come back with the samples in the K positions of 16x16x32 products accumulated in
+// the wave's registers (dW3 4 blocks, dW2 16, dW1 4*KT).  No workgroup barrier inside the loop;
+// at the end the four waves' gradients are summed in wave order through LDS, and the workgroups'
+// partials by mlp_reduce_kernel in a fixed order: deterministic.  PLANES (in = 32 only) writes dz
+// as level-major planes with each 128-row record's per-column maxima.
+template <int KT, bool PLANES, bool WHOLE>
+__global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(MlpArgs a) {
     using S = Shape<KT>;
-    using P1 = Phase1<KT>;
     static_assert(!PLANES || KT == 2, "the planes layout is built for 16 levels x 2 features");
-    constexpr int kNB = P1::kColumnBlocks;   // 32-row blocks of dX
+    constexpr int kNB = (KT + 1) / 2;   // 32-row blocks of dX
+    constexpr int kRows = region_rows<KT>();
+    static_assert(kMlpWaves * kRows * kTS * 2 >= S::kParams * 4, "the regions hold the workgroup's gradient");
     __shared__ _Float16 w[S::kWeightHalfs];
-    __shared__ __attribute__((aligned(16))) _Float16 T[round_rows<KT>() * kRS];
-    __shared__ uint32_t records[kMlpWaves][2][8];   // per wave and lane group: per-feature |dz| maxima of 8 levels
+    __shared__ __attribute__((aligned(16))) _Float16 T[kMlpWaves * kRows * kTS];
     stage_weights<KT>(a.weights, w);
     __syncthreads();
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
-    const int column = 32 * wave + s;   // this lane's sample column in the round buffer
-    f32x16 gA[P1::kSlots], gA1 = zero16(), gB = zero16(), gB1 = zero16();
+    _Float16* R = T + wave * kRows * kTS;
+    f32x4 gW3[4], gW2[4][4], gW1[4][KT];
 #pragma unroll
-    for (int k = 0; k < P1::kSlots; ++k) gA[k] = zero16();
+    for (int i = 0; i < 4; ++i) {
+        gW3[i] = f32x4{};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gW2[i][j] = f32x4{};
+#pragma unroll
+        for (int j = 0; j < KT; ++j) gW1[i][j] = f32x4{};
+    }
     const int64_t tiles = (a.n + 31) / 32;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kMlpWaves;
     const float inv255 = 1.0f / 255.0f;
     const float denominator = static_cast<float>(3 * a.real);
-    TileCursor cursor;
-    {
-        const uint32_t row0 = static_cast<uint32_t>((blockIdx.x * kMlpWaves + wave) * 32 + s);
-        cursor = {pin(row0), pin(row0 * 4u), pin(row0 * (32u * KT) + 16u * g)};
-    }
-    const uint32_t row_stride = static_cast<uint32_t>(stride * 32);
-    // One round on the tile whose inputs are in `current` (loaded a round earlier).
-    auto round = [&](int64_t base, const TileInput<KT>& current) {
-        const int64_t tile = base + wave;
+    // with PLANES: per-feature |dz| maxima of the lane group's 8 levels (lane i: word i % 8) over
+    // the last tile processed, and over the current record
+    uint32_t tile_peak = 0, record_peak = 0;
+    auto process = [&](int64_t tile, const TileInput<KT>& current) {
         const int64_t row = tile * 32 + s;
-        const bool valid = tile < tiles && row < a.n;
-        half8 xb[KT], h1[4], h2[4];
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) xb[kt] = current.xb[kt];
+        const bool valid = row < a.n;
+        half8 h1[4], h2[4];
         f32x16 acc3;
-        forward_tile<KT>(w, g, s, xb, h1, h2, acc3);
+        forward_tile<KT>(w, g, s, current.xb, h1, h2, acc3);
         const int64_t input = current.input;
         const half8 y = round8(acc3, 0);
         half8 dy{};
@@ -232,6 +195,17 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                 *reinterpret_cast<uint2*>(hrow + 64 + feature_of(t, g, 4)) = make_uint2(b2.z, b2.w);
             }
         }
+        // dW3 += dy (x) h2 over the tile's samples
+        if (g == 0)
+#pragma unroll
+            for (int c = 0; c < 3; ++c) R[c * kTS + s] = dy[c];
+        put_rows(R, 16, s, h2, 4, g);
+        wave_fence();
+        {
+            const half8 A = rows16(R, 0, 0, lane);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) gW3[j] = mfma16(A, rows16(R, 16, j, lane), gW3[j]);
+        }
         // input gradients: dH2 = relu'(h2) * (W3^T dy), dH1 = relu'(h1) * (W2^T dH2), dX = W1^T dH1
         half8 dh2[4], dh1[4];
 #pragma unroll
@@ -239,6 +213,22 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
             const f32x16 acc = mfma(lds8(w + S::kW3t + (mb * 32 + s) * kS16 + 8 * g), dy, zero16());
             dh2[2 * mb] = mask8(round8(acc, 0), h2[2 * mb]);
             dh2[2 * mb + 1] = mask8(round8(acc, 8), h2[2 * mb + 1]);
+        }
+        // dW2 += dh2 (x) h1
+        wave_fence();
+        put_rows(R, 0, s, dh2, 4, g);
+        put_rows(R, 64, s, h1, 4, g);
+        wave_fence();
+        {
+            half8 B[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) B[j] = rows16(R, 64, j, lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const half8 A = rows16(R, 0, i, lane);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) gW2[i][j] = mfma16(A, B[j], gW2[i][j]);
+            }
         }
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
@@ -248,6 +238,31 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                 acc = mfma(lds8(w + S::kW2t + (mb * 32 + s) * kS64 + 16 * t + 8 * g), dh2[t], acc);
             dh1[2 * mb] = mask8(round8(acc, 0), h1[2 * mb]);
             dh1[2 * mb + 1] = mask8(round8(acc, 8), h1[2 * mb + 1]);
+        }
+        // dW1 += dh1 (x) x
+        wave_fence();
+        put_rows(R, 0, s, dh1, 4, g);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            const u32x4 d = __builtin_bit_cast(u32x4, current.xb[kt]);
+            uint16_t* r = reinterpret_cast<uint16_t*>(R) + (64 + 16 * kt + 8 * g) * kTS + s;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                r[e * kTS] = static_cast<uint16_t>(d[e / 2]);
+                r[(e + 1) * kTS] = static_cast<uint16_t>(d[e / 2] >> 16);
+            }
+        }
+        wave_fence();
+        {
+            half8 A[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) A[i] = rows16(R, 0, i, lane);
+#pragma unroll
+            for (int j = 0; j < KT; ++j) {
+                const half8 B = rows16(R, 64, j, lane);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gW1[i][j] = mfma16(A[i], B, gW1[i][j]);
+            }
         }
         {
             // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value.  K step
@@ -280,16 +295,14 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                         a.planes[(8 * q + 5 + 2 * g) * a.n + row] = bits[q].w;
                     }
                 }
-                // this round's 128 rows are one record: per-feature maxima of the lane group's
-                // eight levels over its 32 lanes (lane s < 8 ends with word s), then over the four
-                // waves (after the barrier below)
+                // per-feature maxima of the lane group's eight levels over its 32 lanes (every
+                // lane i ends with word i % 8)
                 const uint32_t words[8] = {bits[0].x, bits[0].y, bits[0].z, bits[0].w,
                                            bits[1].x, bits[1].y, bits[1].z, bits[1].w};
                 uint32_t peak[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) peak[j] = valid ? pair_magnitudes(words[j]) : 0u;
-                const uint32_t mine = group_max8(peak, lane);
-                if (s < 8) records[wave][g][s] = mine;
+                tile_peak = group_max8(peak, lane);
             } else if (valid) {
                 uint16_t* p = a.dz + row * S::kIn;
 #pragma unroll
@@ -299,85 +312,93 @@ __global__ __launch_bounds__(kMlpBlock) void mlp_train_kernel(MlpArgs a) {
                 }
             }
         }
-        // phase 1: dW3 = sum dy (x) h2, dW1 = sum dh1 (x) x
-        if (g == 0)
-#pragma unroll
-            for (int c = 0; c < 3; ++c) T[(kDyRow + c) * kRS + column] = dy[c];
-        put_features(T, kH2Row, column, h2, 2, g);
-        put_features(T, kDh1Row, column, dh1, 2, g);
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) T[(kXRow + kt * 16 + 8 * g + e) * kRS + column] = xb[kt][e];
-        __syncthreads();
-        if (PLANES && threadIdx.x < 32) {
-            // column 2L + f (level L, feature f); level L = 8q + 4h + 2g + b is word 4q + 2h + b
-            // of lane group g
-            const int level = threadIdx.x / 2, f = threadIdx.x % 2;
-            const int q = level / 8, h = (level / 4) % 2, lg = (level / 2) % 2, b = level % 2;
-            uint32_t m = 0;
-#pragma unroll
-            for (int v = 0; v < kMlpWaves; ++v) m = pair_max(m, records[v][lg][4 * q + 2 * h + b]);
-            a.blockmax[(base / kMlpWaves) * 32 + threadIdx.x] =
-                __half2float(bits_to_half(static_cast<uint16_t>(m >> (16 * f))));
-        }
-#pragma unroll
-        for (int k = 0; k < P1::kSlots; ++k) {
-            const int block = wave + kMlpWaves * k;
-            if (block < P1::kBlocks) {
-                int a0, b0, a_rows, b_rows;
-                phase1_block<KT>(block, a0, b0, a_rows, b_rows);
-                if constexpr (P1::kSlots == 1) round_block<true>(T, a0, b0, a_rows, b_rows, g, s, gA[k], gA1);
-                else round_block<false>(T, a0, b0, a_rows, b_rows, g, s, gA[k], gA1);
-            }
-        }
-        __syncthreads();
-        // phase 2: dW2 = sum dh2 (x) h1; rows 0..63 = dh2, 64..127 = h1
-        put_features(T, 0, column, dh2, 2, g);
-        put_features(T, 64, column, h1, 2, g);
-        __syncthreads();
-        round_block<true>(T, 32 * (wave >> 1), 64 + 32 * (wave & 1), 32, 32, g, s, gB, gB1);
-        __syncthreads();
-
     };
-    // Unrolled by two with ping-pong input buffers, so that a round never copies the next
-    // round's prefetch (a copy would have to wait for it).
-    TileInput<KT> even, odd;
-    fetch_tile<KT>(a, cursor, even);
-    for (int64_t base = static_cast<int64_t>(blockIdx.x) * kMlpWaves; base < tiles; base += 2 * stride) {
-        advance<KT>(cursor, row_stride);
-        fetch_tile<KT>(a, cursor, odd);
-        round(base, even);
-        if (base + stride >= tiles) break;
-        advance<KT>(cursor, row_stride);
-        fetch_tile<KT>(a, cursor, even);
-        round(base + stride, odd);
-    }
-    // This workgroup's partial: each wave writes its own blocks (accumulator element v of
-    // lane (g, s) is row 8*(v/4) + 4g + v%4, column s of the block).
-    if constexpr (P1::kSlots == 1) gA[0] += gA1;
-    gB += gB1;
-    float* out = a.partials + static_cast<int64_t>(blockIdx.x) * S::kParams;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int r = 8 * (v / 4) + 4 * g + v % 4;
-        out[S::kW1 + (32 * (wave >> 1) + r) * kHid + 32 * (wave & 1) + s] = gB[v];
-    }
-#pragma unroll
-    for (int k = 0; k < P1::kSlots; ++k) {
-        const int block = wave + kMlpWaves * k;
-        if (block >= P1::kBlocks) continue;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int r = 8 * (v / 4) + 4 * g + v % 4;
-            if (block < 2) {
-                if (v < 8) out[S::kW1 + kW2 + r * kHid + 32 * block + s] = gA[k][v];
-            } else {
-                const int mb = (block - 2) / P1::kColumnBlocks, nb = (block - 2) % P1::kColumnBlocks;
-                if (32 * nb + s < S::kIn) out[(32 * mb + r) * S::kIn + 32 * nb + s] = gA[k][v];
+    // Two ways to hand out the 128-row records (4 tiles), chosen from n alone, so that the row and
+    // planes layouts give every wave the same tiles in the same order (bit-identical gradients):
+    // whole records per wave when there are at least four per wave (WHOLE; no barrier at all), else a
+    // record per workgroup, tile w to wave w (the record's maxima then meet through LDS, one
+    // barrier pair per record).  Either way two tiles per step with ping-pong input buffers, so
+    // that a tile never copies the next tile's prefetch (a copy would have to wait for it).
+    const int64_t records = (tiles + 3) / 4;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kMlpWaves;
+    constexpr bool whole = WHOLE;   // the host's choice: records >= 4 * waves
+    // this wave's sequence of tiles: position i -> tile_of(i); in the shared mode every wave of a
+    // workgroup has the same count, so the barriers below are uniform
+    const int64_t first = whole ? static_cast<int64_t>(blockIdx.x) * kMlpWaves + wave : static_cast<int64_t>(blockIdx.x);
+    const int64_t step = whole ? waves : static_cast<int64_t>(gridDim.x);
+    const int64_t count = first < records ? ((records - 1 - first) / step + 1) * (whole ? 4 : 1) : 0;
+    auto tile_of = [&](int64_t i) {
+        return whole ? (first + (i / 4) * step) * 4 + i % 4 : (first + i * step) * 4 + wave;
+    };
+    // level L = 8q + 4h + 2g + b of column 2L + f is word 4q + 2h + b of lane group g
+    const int level = lane / 2, f = lane % 2;
+    const int lg = (level / 2) % 2, word = 4 * (level / 8) + 2 * ((level / 4) % 2) + level % 2;
+    __shared__ uint32_t pairs[kMlpWaves][32];
+    auto finish = [&](int64_t i) {   // after the tile at position i
+        if constexpr (PLANES) {
+            record_peak = pair_max(record_peak, tile_peak);
+            if (whole && i % 4 != 3) return;
+            // lanes 0..31 hold the pair of their column 2L + f
+            const uint32_t m = static_cast<uint32_t>(__shfl(static_cast<int>(record_peak), 32 * lg + word));
+            record_peak = 0;
+            const int64_t record = tile_of(i) / 4;
+            if constexpr (WHOLE) {
+                if (lane < 32) a.blockmax[record * 32 + lane] = __half2float(bits_to_half(static_cast<uint16_t>(m >> (16 * f))));
+                return;
             }
+            // the four waves' tiles of the record meet in LDS
+            if (lane < 32) pairs[wave][lane] = m;
+            __syncthreads();
+            if (threadIdx.x < 32) {
+                uint32_t total = 0;
+#pragma unroll
+                for (int v = 0; v < kMlpWaves; ++v) total = pair_max(total, pairs[v][threadIdx.x]);
+                a.blockmax[record * 32 + threadIdx.x] = __half2float(bits_to_half(static_cast<uint16_t>(total >> (16 * f))));
+            }
+            __syncthreads();
         }
+    };
+    TileInput<KT> even, odd;
+    if (count) fetch_tile<KT>(a, tile_of(0) * 32 + s, g, even);
+    for (int64_t i = 0; i < count; i += 2) {
+        fetch_tile<KT>(a, tile_of(i + 1) * 32 + s, g, odd);
+        tile_peak = 0;
+        if (tile_of(i) < tiles) process(tile_of(i), even);
+        finish(i);
+        if (i + 1 >= count) break;
+        fetch_tile<KT>(a, tile_of(i + 2) * 32 + s, g, even);
+        tile_peak = 0;
+        if (tile_of(i + 1) < tiles) process(tile_of(i + 1), odd);
+        finish(i + 1);
     }
+    // The workgroup's partial: the four waves' gradients summed in wave order in LDS (lane l holds
+    // rows 4 * (l / 16) + v, column l % 16 of each 16x16 block), then written out.
+    __syncthreads();
+    float* P = reinterpret_cast<float*>(T);
+    const int rq = 4 * (lane >> 4), cn = lane & 15;
+    for (int turn = 0; turn < kMlpWaves; ++turn) {
+        if (wave == turn) {
+            auto put = [&](int p, float v) { P[p] = turn ? P[p] + v : v; };
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int r = 16 * i + rq + v;
+#pragma unroll
+                    for (int j = 0; j < KT; ++j) put(r * S::kIn + 16 * j + cn, gW1[i][j][v]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) put(S::kW1 + r * kHid + 16 * j + cn, gW2[i][j][v]);
+                }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)   // rows 3..15 of dW3 are zero: dy has three outputs
+                    put(S::kW1 + kW2 + (rq + v) * kHid + 16 * j + cn, rq + v < 3 ? gW3[j][v] : 0.0f);
+        }
+        __syncthreads();
+    }
+    float* out = a.partials + static_cast<int64_t>(blockIdx.x) * S::kParams;
+    for (int p = threadIdx.x; p < S::kParams; p += kMlpBlock) out[p] = P[p];
 }
 
 // dweights[p] = sum over workgroups of partials[b][p] in a fixed order: the 16 lane groups of a
@@ -475,17 +496,24 @@ int mlp_train(const char* name, const uint16_t* x, int64_t n, int width, int64_t
     if (!partials) return -1;
     MlpArgs a{x, weights, n, real, colors, rgb, ids, target, rows, out, hidden, squares, planes ? nullptr : dz, partials,
               planes, planes ? blockmax : nullptr};
+    // whole 128-row records per wave when there are at least four per wave (see the kernel)
+    const int64_t records = ((n + 31) / 32 + 3) / 4;
+    const bool whole = records >= int64_t{4} * blocks * kMlpWaves;
+#define ODIE_TRAIN(KT, PLANES)                                                                      \
+    (whole ? mlp_train_kernel<KT, PLANES, true><<<blocks, kMlpBlock, 0, s>>>(a)                    \
+           : mlp_train_kernel<KT, PLANES, false><<<blocks, kMlpBlock, 0, s>>>(a))
     if (planes) {
-        mlp_train_kernel<2, true><<<blocks, kMlpBlock, 0, s>>>(a);
+        ODIE_TRAIN(2, true);
     } else {
         switch (kt) {
-            case 1: mlp_train_kernel<1, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
-            case 2: mlp_train_kernel<2, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
-            case 3: mlp_train_kernel<3, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
-            case 4: mlp_train_kernel<4, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
-            default: mlp_train_kernel<5, false><<<blocks, kMlpBlock, 0, s>>>(a); break;
+            case 1: ODIE_TRAIN(1, false); break;
+            case 2: ODIE_TRAIN(2, false); break;
+            case 3: ODIE_TRAIN(3, false); break;
+            case 4: ODIE_TRAIN(4, false); break;
+            default: ODIE_TRAIN(5, false); break;
         }
     }
+#undef ODIE_TRAIN
     if (check_launch(name)) return -1;
     mlp_reduce_kernel<<<static_cast<uint32_t>((params + kReduceParams - 1) / kReduceParams),
                         kReduceParams * kReduceGroups, 0, s>>>(

@@ -83,6 +83,7 @@ def _train_case(seed, n, *, rgb8=True, permute=True, real=None, width=32):
     (1000, False, False, None, 32),     # ragged last tile, fp32 targets, identity rows
     (2048, True, True, 1500, 32),       # inputs >= real are padding rows
     (1 << 17, True, True, None, 32),    # every workgroup runs several tiles
+    ((1 << 20) + 4133, True, True, None, 32),   # whole 128-row records per wave, ragged last record
     (5000, 'colors', True, 4000, 32),   # packed per-row targets (as odie_route writes them)
     (4096, True, True, None, 16),       # the input widths of the other level rows: 8 levels (16),
     (3001, True, False, 2500, 48),      # 20 levels of F2/F1 (48), F4 rows (64, 80)
@@ -143,7 +144,8 @@ def _record_maxima(dz):
     return padded.view(records, 128, 32).amax(dim=1)
 
 
-@pytest.mark.parametrize('n,poison', [(1, False), (1000, False), (4096 + 37, False), (1 << 17, False), (3000, True)])
+@pytest.mark.parametrize('n,poison', [(1, False), (1000, False), (4096 + 37, False), (1 << 17, False), (3000, True),
+                                     ((1 << 20) + 37, False)])
 def test_train_planes_equals_rows(n, poison):
     """odie_mlp_train_planes writes odie_mlp_train's dz, bit for bit, as level-major planes with
     exact 128-row maxima (NaN where a row of the record is NaN); outputs and gradients agree."""
