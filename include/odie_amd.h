@@ -126,8 +126,9 @@ int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t
  * "split_target" (banded: coordinate-level visits per owner work item, 0 = automatic),
  * "owner_lds_bytes", "paired_loads", "forward_lds_bytes", "packed_owner" (1: the packed-plane
  * backward computes each slice of the gradient in one workgroup, 0 (default): global atomics),
- * "packed_splits" (0 = automatic).  Results do not depend on them beyond fp32 summation order
- * and the owner's fixed-point scale. */
+ * "packed_splits" (0 = automatic), "route_part" (the routes' smallest sub-chunk of ids, a power
+ * of two within 64..65536, default 512; size route workspaces after setting it).  Results do
+ * not depend on them beyond fp32 summation order and the owner's fixed-point scale. */
 int odie_set_tuning(const char* key, int value);
 
 /* ---------------------------------------------------------------------------------------
@@ -168,10 +169,11 @@ int odie_packed_backward(const float* coords, int64_t n, const uint16_t* upstrea
  *   coords[j] local (u, v) of that id                         (fp32 [n, 2])
  *   offsets   first slot of every expert, offsets[E] = n       (int32 [E+1])
  * expert (nullable) receives each input's expert id in input order (int32 [n]).
- * rgb / colors (both null or both set): colors[j] = r | g << 8 | b << 16 of the pixel
+ * colors (nullable, uint32 [n]): with rgb, colors[j] = r | g << 8 | b << 16 of the pixel
  *   (y*W + x, with y clamped as above) of slot j, read from the RGB8 image rgb [H*W][3] --
  *   the training target of the slot, gathered in slot order so each tile's bytes are read
- *   through one L2.
+ *   through one L2; without rgb, colors[j] = y*W + x, the pixel index itself (odie_mlp_train
+ *   gathers the target from it).  rgb without colors is refused.
  * workspace: caller-owned device scratch of odie_route_workspace(n, E) bytes (-1 for n outside
  *   [0, 2^31-1] or E outside [1, 4096]).
  * --------------------------------------------------------------------------------------- */
@@ -313,9 +315,10 @@ int odie_adam_step(float* master, uint16_t* half_copy, const void* grad, int gra
  *
  * odie_mlp_train: forward, the step's loss (loss_grad, odie/native/runtime.cu:53-63) and
  * backward in one pass.  Tile row j reads x[j]; its input row is i = rows[j] (rows null:
- * i = j).  Target of tile row j, first given source wins: byte c of colors[j] * (1/255)
- * (colors: uint32 [n] packed as odie_route writes them); rgb[3*ids[i] + c] * (1/255);
- * target[3*i + c] (fp32).
+ * i = j).  Target of tile row j, first given source wins: with colors and rgb,
+ * rgb[3*colors[j] + c] * (1/255) (colors: uint32 [n] pixel indexes, as odie_route writes them
+ * without rgb); with colors alone, byte c of colors[j] * (1/255) (colors packed as odie_route
+ * writes them with rgb); rgb[3*ids[i] + c] * (1/255); target[3*i + c] (fp32).
  * dy_c = fp16(fp16(2*d_c/(3*real)*128)*128) for c < 3 (zero for i >= real), d = y - t.
  * Writes dz fp16 [n][width] = fp16(fp16(dL/dx * 16384) / 128) at row j (the grid's upstream,
  * half_unscale at odie/native/runtime.cu:282), dweights fp32 [64*width + 5120] = dL/dW * 16384

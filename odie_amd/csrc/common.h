@@ -101,6 +101,9 @@ __device__ inline uint32_t group_max8(const uint32_t d[8], int lane) {
     return pair_max(x, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), 0x401F)));  // xor 16
 }
 
+// Route launch knobs (route.hip), set through odie_set_tuning's "route_" keys.
+int set_route_tuning(const std::string& key, int value);
+
 __device__ inline uint16_t half_to_bits(__half value) { return __half_as_ushort(value); }
 
 }  // namespace odie

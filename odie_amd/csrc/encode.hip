@@ -944,6 +944,7 @@ ODIE_API int odie_grid_backward_planes(const float* coords, int64_t n, const int
 
 ODIE_API int odie_set_tuning(const char* key, int value) {
     if (!key) return fail("odie_set_tuning: key is null");
+    if (std::string(key).rfind("route_", 0) == 0) return set_route_tuning(key, value);
     return set_grid_tuning(key, value);
 }
 

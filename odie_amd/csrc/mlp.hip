@@ -66,15 +66,27 @@ template <int KT> struct TileInput {
     uint32_t color;
 };
 
+// Every load is issued unconditionally, from a row clamped into [0, n) and from x in place of
+// a null rows or colors (the values are then replaced): straight-line loads let the compiler
+// count the memory operations in flight exactly, where loads under branches made it wait for
+// the next tile's prefetch at the first product of the current one.
 template <int KT> __device__ inline void fetch_tile(const MlpArgs& a, int64_t row, int g, TileInput<KT>& in) {
     const bool valid = row < a.n;
+    const int64_t r = valid ? row : a.n - 1;
+    const int32_t* rows = a.rows ? a.rows : reinterpret_cast<const int32_t*>(a.x);
+    const uint32_t* colors = a.colors ? a.colors : reinterpret_cast<const uint32_t*>(a.x);
     // the small loads first: memory counters drain in issue order, so an early wait on them
     // leaves the 64-byte x loads in flight
-    in.input = valid ? (a.rows ? a.rows[row] : static_cast<int32_t>(row)) : 0;
-    in.color = valid && a.colors ? a.colors[row] : 0u;
-    const half8* x = reinterpret_cast<const half8*>(a.x + row * (16 * KT) + 8 * g);
+    const int32_t input = rows[r];
+    const uint32_t color = colors[r];
+    const half8* x = reinterpret_cast<const half8*>(a.x + r * (16 * KT) + 8 * g);
+    half8 xb[KT];
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) in.xb[kt] = valid ? x[2 * kt] : half8{};
+    for (int kt = 0; kt < KT; ++kt) xb[kt] = x[2 * kt];
+    in.input = !valid ? 0 : a.rows ? input : static_cast<int32_t>(row);
+    in.color = valid && a.colors ? color : 0u;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) in.xb[kt] = valid ? xb[kt] : half8{};
 }
 
 // Per-wave transposition region: feature-major rows of the 32 samples of the wave's current
@@ -159,6 +171,25 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
     auto process = [&](int64_t tile, const TileInput<KT>& current) {
         const int64_t row = tile * 32 + s;
         const bool valid = row < a.n;
+        // with colors and rgb together, colors holds the slot's pixel index: its three bytes are
+        // loaded here, a forward pass ahead of the loss, and kept apart until the loss reads them
+        // (joining them here would wait for the loads at once)
+        const bool gather = a.colors && a.rgb;
+        uint32_t byte[3] = {0u, 0u, 0u};
+        if (gather) {   // every lane (both lane groups of a sample read the same bytes), no branch
+            // three byte loads from addresses the compiler cannot see as adjacent (it would merge
+            // them into a 16-bit load whose split waits for it at once)
+            typedef const __attribute__((address_space(1))) uint8_t* global_bytes;
+            global_bytes p[3];
+            p[0] = (global_bytes)(a.rgb + 3 * static_cast<uint64_t>(current.color));   // generic -> global
+#pragma unroll
+            for (int c = 1; c < 3; ++c) {
+                p[c] = p[0] + c;
+                asm volatile("" : "+v"(p[c]));
+            }
+#pragma unroll
+            for (int c = 0; c < 3; ++c) byte[c] = *p[c];
+        }
         half8 h1[4], h2[4];
         f32x16 acc3;
         forward_tile<KT>(w, g, s, current.xb, h1, h2, acc3);
@@ -172,7 +203,8 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
             if (input < a.real) {
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
-                    const float t = a.colors ? __fmul_rn(static_cast<float>((current.color >> (8 * c)) & 0xffu), inv255)
+                    const uint32_t value = gather ? byte[c] : (current.color >> (8 * c)) & 0xffu;
+                    const float t = a.colors ? __fmul_rn(static_cast<float>(value), inv255)
                                   : a.rgb ? __fmul_rn(static_cast<float>(a.rgb[3 * a.ids[input] + c]), inv255)
                                           : a.target[3 * input + c];
                     const float d = static_cast<float>(y[c]) - t;

@@ -28,6 +28,7 @@ struct ReconArgs {
     int64_t begin;
     int64_t n;
     uint32_t width;
+    Divisor by_width;      // id / width with one multiply-high
     uint32_t height;
     int regions_x;
     int regions_y;
@@ -72,8 +73,8 @@ __device__ inline void stage_model(const ReconArgs& a, const TileBounds& bounds,
 __device__ inline void predict(const ReconArgs& a, const TileBounds& tb, const DevLevel* levels, const _Float16* w,
                                uint32_t id, bool valid,
                                int g, int s, uint32_t pairs[2][4], half8& out) {
-    const uint32_t x = id % a.width;
-    uint32_t y = id / a.width;
+    uint32_t y = divide(id, a.by_width);
+    const uint32_t x = id - y * a.width;
     if (y >= a.height) y = a.height - 1;
     const int tx = tile_of(a.regions_x, a.width, tb.sx, x), ty = tile_of(a.regions_y, a.height, tb.sy, y);
     const int t = ty * a.regions_x + tx;
@@ -248,6 +249,7 @@ static int model_args(const char* what, int width, int height, int regions_x, in
     if (!table || !weights) return fail(w + ": null pointer");
     if (reinterpret_cast<uintptr_t>(table) % 4) return fail(w + ": table must be 4-byte aligned");
     a.width = static_cast<uint32_t>(width);
+    a.by_width = make_divisor(a.width);
     a.height = static_cast<uint32_t>(height);
     a.regions_x = regions_x;
     a.regions_y = regions_y;

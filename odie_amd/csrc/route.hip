@@ -54,12 +54,15 @@ struct RouteArgs {
     int64_t n;
     uint32_t width;
     uint32_t height;
+    Divisor by_width;      // id / width with one multiply-high
     int regions_x;
     int regions_y;
     int experts;       // buckets of the counting sort
     int expert_bits;   // bits of the largest bucket id
     int part;          // ids per wave sub-chunk (multiple of 64)
     int parts;         // number of sub-chunks
+    int per_column;    // sub-chunks per column of the counts (1, or the staged scatter's group)
+    int columns;       // columns of the expert-major counts: ceil(parts / per_column)
     int32_t x0[kMaxRegions + 1];
     int32_t y0[kMaxRegions + 1];
     float rx[kMaxRegions];   // fp32(1/(tile_width-1))
@@ -105,8 +108,8 @@ __device__ inline void pixel_ids(const RouteArgs& a, int64_t first, int64_t stri
 
 __device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t id, int& expert, uint32_t& x,
                                  uint32_t& y, int& rx, int& ry) {
-    x = id % a.width;
-    y = id / a.width;
+    y = divide(id, a.by_width);
+    x = id - y * a.width;
     if (y >= a.height) y = a.height - 1;  // ids past the image clamp to its last row
     rx = tile_of(a.regions_x, a.width, a.sx, x);
     ry = tile_of(a.regions_y, a.height, a.sy, y);
@@ -130,19 +133,61 @@ __device__ inline void load_bounds(const RouteArgs& a, Bounds& b) {
     __syncthreads();
 }
 
-// Each wave counts one sub-chunk; the block's kWaves counts of each expert are consecutive in the
-// expert-major count array, so they are written as one run.
+// Counts per expert of every sub-chunk (per_column 1: each wave counts one sub-chunk, and the
+// block's kWaves counts of each expert are consecutive in the expert-major array, so they are
+// written as one run), or of every group of per_column consecutive sub-chunks (GROUPED: a block
+// per group, its waves taking the group's sub-chunks in turn; the staged scatter needs no finer
+// offsets, and the scans then run over per_column times fewer counts).
+template <bool GROUPED>
 __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
-    extern __shared__ int32_t hist[];  // [experts][kWaves] counts of the block's sub-chunks
+    extern __shared__ int32_t hist[];  // [experts][kWaves] counts of the block's sub-chunks, or [experts]
     __shared__ Bounds bounds;
     load_bounds(a, bounds);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const int first = static_cast<int>(blockIdx.x) * kWaves;
-    for (int j = threadIdx.x; j < a.experts * kWaves; j += kRouteBlock) hist[j] = 0;
+    constexpr int kSlots = GROUPED ? 1 : kWaves;
+    const int first = static_cast<int>(blockIdx.x) * (GROUPED ? a.per_column : kWaves);
+    const int members = GROUPED ? a.per_column : kWaves;
+    for (int j = threadIdx.x; j < a.experts * kSlots; j += kRouteBlock) hist[j] = 0;
     __syncthreads();
-    if (first + wave < a.parts) {
-        const int64_t begin = static_cast<int64_t>(first + wave) * a.part;
+    if constexpr (GROUPED) {
+        // the group's ids as 16-byte pairs (ids 16-byte aligned: checked by the host), every
+        // pair of a round of kPairs per thread loaded before any is used
+        constexpr int kPairs = 8;
+        const int64_t begin = static_cast<int64_t>(first) * a.part;
+        const int64_t group_end = begin + static_cast<int64_t>(members) * a.part;
+        const int64_t end = group_end < a.n ? group_end : a.n;
+        const int4* pairs = reinterpret_cast<const int4*>(a.ids + begin);
+        const int64_t count = end - begin, npairs = count / 2;   // whole pairs; an odd last id alone
+        for (int64_t round = 0; round < npairs; round += kRouteBlock * kPairs) {
+            int4 two[kPairs];
+#pragma unroll
+            for (int k = 0; k < kPairs; ++k) {
+                const int64_t q = round + k * kRouteBlock + threadIdx.x;
+                two[k] = pairs[q < npairs ? q : npairs - 1];
+            }
+#pragma unroll
+            for (int k = 0; k < kPairs; ++k) {
+                const int64_t q = round + k * kRouteBlock + threadIdx.x;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    int expert, rx, ry;
+                    uint32_t x, y;
+                    locate_id(a, bounds, static_cast<uint32_t>(h ? two[k].z : two[k].x), expert, x, y, rx, ry);
+                    if (q < npairs) atomicAdd(hist + expert, 1);
+                }
+            }
+        }
+        if ((count & 1) && threadIdx.x == 0) {
+            int expert, rx, ry;
+            uint32_t x, y;
+            locate_id(a, bounds, static_cast<uint32_t>(a.ids[end - 1]), expert, x, y, rx, ry);
+            atomicAdd(hist + expert, 1);
+        }
+    }
+    for (int k = wave; !GROUPED && k < members && first + k < a.parts; k += kWaves) {
+        const int64_t begin = static_cast<int64_t>(first + k) * a.part;
         const int64_t end = begin + a.part < a.n ? begin + a.part : a.n;
+        int32_t* counter = hist + (GROUPED ? 0 : wave);
         for (int64_t g = begin; g < end; g += 64 * kAhead) {
             uint32_t id[kAhead];
             pixel_ids<kAhead>(a, g + lane, 64, end - 1, id);
@@ -151,14 +196,19 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
                 int expert, rx, ry;
                 uint32_t x, y;
                 locate_id(a, bounds, id[j], expert, x, y, rx, ry);
-                if (g + j * 64 + lane < end) atomicAdd(hist + expert * kWaves + wave, 1);
+                if (g + j * 64 + lane < end) atomicAdd(counter + expert * kSlots, 1);
             }
         }
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < a.experts * kWaves; j += kRouteBlock) {
-        const int e = j / kWaves, k = j % kWaves;
-        if (first + k < a.parts) a.counts[static_cast<int64_t>(e) * a.parts + first + k] = hist[j];
+    if constexpr (GROUPED) {
+        for (int e = threadIdx.x; e < a.experts; e += kRouteBlock)
+            a.counts[static_cast<int64_t>(e) * a.columns + blockIdx.x] = hist[e];
+    } else {
+        for (int j = threadIdx.x; j < a.experts * kWaves; j += kRouteBlock) {
+            const int e = j / kWaves, k = j % kWaves;
+            if (first + k < a.parts) a.counts[static_cast<int64_t>(e) * a.columns + first + k] = hist[j];
+        }
     }
 }
 
@@ -187,7 +237,7 @@ __device__ inline int32_t block_exclusive_scan(int32_t value, int32_t* shared, i
 
 __global__ __launch_bounds__(kScanBlock) void route_scan_reduce_kernel(RouteArgs a) {
     __shared__ int32_t shared[kScanBlock];
-    const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
+    const int64_t total = static_cast<int64_t>(a.experts) * a.columns;
     const int64_t begin = static_cast<int64_t>(blockIdx.x) * kScanSegment + threadIdx.x * (kScanSegment / kScanBlock);
     int32_t sum = 0;
     for (int j = 0; j < kScanSegment / kScanBlock; ++j)
@@ -232,7 +282,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
         block_exclusive_scan(before, shared, offset);
         if (blockIdx.x == 0 && threadIdx.x == 0 && !a.slots) a.offsets[a.experts] = static_cast<int32_t>(a.n);
     }
-    const int64_t total = static_cast<int64_t>(a.experts) * a.parts;
+    const int64_t total = static_cast<int64_t>(a.experts) * a.columns;
     constexpr int kPer = kScanSegment / kScanBlock;
     const int64_t begin = static_cast<int64_t>(blockIdx.x) * kScanSegment + threadIdx.x * kPer;
     int32_t values[kPer];
@@ -247,7 +297,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
         const int64_t k = begin + j;
         if (k < total) {
             a.counts[k] = running;
-            if (k % a.parts == 0) a.offsets[k / a.parts] = running;
+            if (k % a.columns == 0) a.offsets[k / a.columns] = running;
         }
         running += values[j];
     }
@@ -296,7 +346,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
             if (valid && rank == 0) mine[expert] = base + __popcll(same);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             if (valid) {
-                const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.parts + part]) + base + rank;
+                const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.columns + part]) + base + rank;
                 a.perm[slot] = static_cast<int32_t>(i);
                 const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
                 const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
@@ -392,7 +442,7 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
     uint16_t* local = tag + ids_cap;                                       // [ids_cap] offset of position j's id
     // base[e] = slot of the group's first id of expert e: the scanned count of (e, first)
     for (int e = tid; e < experts; e += 64 * W) {
-        base[e] = a.counts[static_cast<int64_t>(e) * a.parts + first];
+        base[e] = a.counts[static_cast<int64_t>(e) * a.columns + first / a.per_column];
 #pragma unroll
         for (int w = 0; w < W; ++w) hist[w * experts + e] = 0u;
     }
@@ -587,10 +637,16 @@ int launch_staged(const RouteArgs& a, int group, hipStream_t s) {
     return 0;
 }
 
+int& route_min_part() {
+    static int part = 512;
+    return part;
+}
+
 int route_plan(int64_t n, int experts, int& part, int& parts) {
-    // Sub-chunks of at least 512 ids, few enough that experts*parts stays <= 2^22 (16 MiB of
-    // counts): a wave walks its sub-chunk serially, so short ones keep more waves on every CU.
-    int64_t p = 512;
+    // Sub-chunks of at least route_min_part() ids, few enough that experts*parts stays <= 2^22
+    // (16 MiB of counts): a wave walks its sub-chunk serially, so short ones keep more waves on
+    // every CU.
+    int64_t p = route_min_part();
     while ((n + p - 1) / p * experts > (int64_t{1} << 22)) p *= 2;
     part = static_cast<int>(p);
     parts = static_cast<int>((n + p - 1) / p);
@@ -599,6 +655,14 @@ int route_plan(int64_t n, int experts, int& part, int& parts) {
 }
 
 }  // namespace
+
+int set_route_tuning(const std::string& key, int value) {
+    // the workspace size follows the part, so a caller sizes it after the setting
+    if (key == "route_part" && value >= 64 && value <= (1 << 16) && (value & (value - 1)) == 0) route_min_part() = value;
+    else return fail("odie_set_tuning: unknown key or value out of range: " + key);
+    return 0;
+}
+
 }  // namespace odie
 
 using namespace odie;
@@ -632,7 +696,7 @@ int route_check(const void* ids, int64_t n, int width, int height, int regions_x
         return fail("odie_route: images are limited to 2^32 pixels (32-bit pixel ids)");
     if (!offsets) return fail("odie_route: offsets is null");
     if (n > 0 && (!ids || !perm || !coords)) return fail("odie_route: ids, perm and coords must be non-null");
-    if ((rgb == nullptr) != (colors == nullptr)) return fail("odie_route: rgb and colors go together");
+    if (rgb && !colors) return fail("odie_route: rgb needs colors");
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_route: coords must be 8-byte aligned");
     return 0;
 }
@@ -667,6 +731,7 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     }
     a.n = n;
     a.width = static_cast<uint32_t>(width);
+    a.by_width = make_divisor(a.width);
     a.height = static_cast<uint32_t>(height);
     a.regions_x = regions_x;
     a.regions_y = regions_y;
@@ -674,6 +739,15 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     a.expert_bits = 0;
     while ((1 << a.expert_bits) < experts) ++a.expert_bits;
     route_plan(n, experts, a.part, a.parts);
+    // staged scatter when a group's staging fits the LDS budget.  A stratified batch lists its
+    // strata row by row, so consecutive ids mostly share an expert and the direct scatter's stores
+    // already come in runs.
+    int waves = 0, group = 0;
+    staged_shape(experts, a.part, waves, group);
+    // (the grouped count reads the ids as 16-byte pairs)
+    const bool staged = !uniforms && waves > 0 && reinterpret_cast<uintptr_t>(ids) % 16 == 0;
+    a.per_column = staged ? group : 1;
+    a.columns = (a.parts + a.per_column - 1) / a.per_column;
     {
         TileBounds tb;
         make_tile_bounds(width, height, regions_x, regions_y, tb);
@@ -693,9 +767,10 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     if (shmem + sizeof(Bounds) > 64 * 1024) return fail("odie_route: too many experts for the LDS histogram");
     const uint32_t blocks = static_cast<uint32_t>((a.parts + kWaves - 1) / kWaves);
     if (n == 0) return launch_fill_zero(reinterpret_cast<float*>(offsets), slots ? owned + 1 : experts + 1, s);
-    const int sblocks = static_cast<int>(scan_blocks(n, experts));
+    const int sblocks = static_cast<int>((static_cast<int64_t>(experts) * a.columns + kScanSegment - 1) / kScanSegment);
     if (sblocks > kScanBlock * 64) return fail("odie_route: too many counts to scan");
-    route_count_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
+    if (staged) route_count_kernel<true><<<a.columns, kRouteBlock, static_cast<size_t>(experts) * 4, s>>>(a);
+    else route_count_kernel<false><<<blocks, kRouteBlock, shmem, s>>>(a);
     route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
     if (sblocks <= kScanBlock * 4) {
         route_scan_apply_kernel<false><<<sblocks, kScanBlock, 0, s>>>(a);
@@ -703,17 +778,12 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
         route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
         route_scan_apply_kernel<true><<<sblocks, kScanBlock, 0, s>>>(a);
     }
-    // staged scatter when a group's staging fits the LDS budget.  A stratified batch lists its
-    // strata row by row, so consecutive ids mostly share an expert and the direct scatter's stores
-    // already come in runs.
-    int waves = 0, group = 0;
-    staged_shape(experts, a.part, waves, group);
-    if (!uniforms && waves > 0) {
+    if (staged) {
         if ((waves == 8 ? launch_staged<8>(a, group, s) : launch_staged<4>(a, group, s)) != 0) return -1;
     } else {
         route_scatter_kernel<<<blocks, kRouteBlock, shmem, s>>>(a);
     }
-    if (colors) {
+    if (rgb) {
         const uint32_t chunks = round_up(static_cast<uint32_t>((n + kColorsChunk - 1) / kColorsChunk), kXcds);
         const uint64_t image_bytes = 3 * static_cast<uint64_t>(width) * static_cast<uint64_t>(height);
         const bool words = reinterpret_cast<uintptr_t>(rgb) % 4 == 0;

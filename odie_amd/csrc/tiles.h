@@ -9,6 +9,27 @@ namespace odie {
 
 constexpr int kMaxTiles = 64;   // tiles per axis
 
+// Unsigned 32-bit division by an invariant divisor d >= 1 with one multiply-high: Granlund and
+// Montgomery, "Division by invariant integers using multiplication" (PLDI 1994), Figure 4.1:
+// l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, then n / d = (t + ((n - t) >> sh1)) >> sh2
+// with t = mulhi(m, n), sh1 = min(l, 1), sh2 = max(l - 1, 0), exact for every 32-bit n.
+struct Divisor {
+    uint32_t magic;
+    uint32_t sh1, sh2;
+};
+
+inline Divisor make_divisor(uint32_t d) {
+    uint32_t l = 0;
+    while (l < 32 && (uint64_t{1} << l) < d) ++l;
+    const uint64_t m = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;
+    return Divisor{static_cast<uint32_t>(m), l < 1 ? l : 1u, l > 1 ? l - 1 : 0u};
+}
+
+__device__ inline uint32_t divide(uint32_t n, const Divisor& d) {
+    const uint32_t t = __umulhi(d.magic, n);
+    return (t + ((n - t) >> d.sh1)) >> d.sh2;
+}
+
 struct TileBounds {
     int32_t x0[kMaxTiles + 1];
     int32_t y0[kMaxTiles + 1];

@@ -68,15 +68,15 @@ class Decoder:
                                                    out.data_ptr(), _lib.stream_of(x)))
         return out
 
-    def train(self, x, real=None, *, colors=None, rgb=None, ids=None, target=None, rows=None, out=None, hidden=None,
-              squares=None, dz=None):
+    def train(self, x, real=None, *, colors=None, pixels=None, rgb=None, ids=None, target=None, rows=None, out=None,
+              hidden=None, squares=None, dz=None):
         """Forward + loss + backward.  Returns dz fp16 [n, width] (the grid's upstream at loss
-        scale 128); self.grad receives dL/dW at loss scale 16384."""
+        scale 128); self.grad receives dL/dW at loss scale 16384.  The target of row j: colors[j]
+        (packed RGB8), or the pixel pixels[j] of rgb, or pixel ids[rows[j]] of rgb, or target."""
         x = _features(x, self.width)
         n = x.shape[0]
         real = n if real is None else int(real)
-        if colors is None and ((rgb is None) == (target is None) or (rgb is not None and ids is None)):
-            raise ValueError('give colors, rgb with ids, or target')
+        colors, rgb, ids = _target_source(colors, pixels, rgb, ids, target)
         if dz is None:
             dz = torch.empty((n, self.width), dtype=torch.float16, device=x.device)
         _lib.check(_lib.library().odie_mlp_train(
@@ -85,8 +85,8 @@ class Decoder:
             _lib.stream_of(x)))
         return dz
 
-    def train_planes(self, x, real=None, *, colors=None, rgb=None, ids=None, target=None, rows=None, out=None,
-                     hidden=None, squares=None, planes=None, blockmax=None):
+    def train_planes(self, x, real=None, *, colors=None, pixels=None, rgb=None, ids=None, target=None, rows=None,
+                     out=None, hidden=None, squares=None, planes=None, blockmax=None):
         """train() with dz written for ExpertGrid.backward_adam_planes: planes int32 [16, n] (the
         fp16 feature pair of each level and row) and blockmax fp32 [ceil(n/128), 32] (max |dz|
         per 128-row record and column: level l, feature f at 2l + f).  Returns (planes, blockmax).
@@ -96,8 +96,7 @@ class Decoder:
         x = _features(x, self.width)
         n = x.shape[0]
         real = n if real is None else int(real)
-        if colors is None and ((rgb is None) == (target is None) or (rgb is not None and ids is None)):
-            raise ValueError('give colors, rgb with ids, or target')
+        colors, rgb, ids = _target_source(colors, pixels, rgb, ids, target)
         records = (n + 127) // 128
         if planes is None:
             planes = torch.empty((LEVELS, n), dtype=torch.int32, device=x.device)
@@ -113,6 +112,17 @@ class Decoder:
             _lib.ptr(target), _lib.ptr(rows), _lib.ptr(out), _lib.ptr(hidden), _lib.ptr(squares), planes.data_ptr(),
             blockmax.data_ptr(), self.grad.data_ptr(), _lib.stream_of(x)))
         return planes, blockmax
+
+
+def _target_source(colors, pixels, rgb, ids, target):
+    """The (colors, rgb, ids) arguments of odie_mlp_train for one target source: packed colors;
+    pixel indexes with the image (passed as colors with rgb); rgb with ids; or fp32 target."""
+    given = [colors is not None, pixels is not None, ids is not None, target is not None]
+    if sum(given) != 1 or (pixels is not None or ids is not None) != (rgb is not None):
+        raise ValueError('give colors, pixels with rgb, rgb with ids, or target')
+    if pixels is not None:
+        return pixels, rgb, None
+    return colors, rgb, ids
 
 
 def _features(x, width):

@@ -27,9 +27,10 @@ class Routing:
 
 
 def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=None, workspace=None, rgb=None,
-          uniforms=None, slots=None, experts=None):
+          uniforms=None, slots=None, experts=None, pixels=False):
     """Route int64 pixel ids [N] (CUDA) to regions_x*regions_y tile experts and compact.  With
-    rgb (CUDA uint8 [H*W*3]) each slot also receives its pixel's packed colour.  With
+    rgb (CUDA uint8 [H*W*3]) each slot also receives its pixel's packed colour in out.colors;
+    with pixels=True (and no rgb) out.colors receives the slot's pixel index instead.  With
     uniforms (CUDA fp32 [N, 2], N a square power of two) and ids None, the ids are those of
     the stratified draw on those uniforms (odie_stratified_ids), computed inside the route.
     With slots (CUDA int32 [regions_x*regions_y], tile -> expert in [0, experts), any other
@@ -67,10 +68,12 @@ def route(ids, width, height, regions_x, regions_y, *, with_expert=False, out=No
                       torch.empty((n, 2), dtype=torch.float32, device=device),
                       torch.empty(experts + 1, dtype=torch.int32, device=device),
                       torch.empty(n, dtype=torch.int32, device=device) if with_expert else None,
-                      torch.empty(n, dtype=torch.int32, device=device) if rgb is not None else None)
+                      torch.empty(n, dtype=torch.int32, device=device) if rgb is not None or pixels else None)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
-    colors = out.colors if rgb is not None else None
+    if pixels and rgb is not None:
+        raise ValueError('pixels=True writes pixel indexes in place of the colours of rgb')
+    colors = out.colors if rgb is not None or pixels else None
     if slots is not None:
         stratified = entry == 'odie_route_stratified'
         _lib.check(lib.odie_route_allocated(None if stratified else ids.data_ptr(),

@@ -4,7 +4,7 @@ This is the native step of the reference (Probe::step, odie/native/runtime.cu:24
 the hash-grid representation with the router disabled), with the single hash grid replaced
 by one hash grid per image tile:
 
-  ids --route--> (perm, local xy, offsets, targets)   odie_route (no reference counterpart)
+  ids --route--> (perm, local xy, offsets, pixels)    odie_route (no reference counterpart)
       --encode forward--> raw fp16 [n, 32]            GridEncoding fwd       (:260)
       --decoder + loss + backward--> dz, dW           decoder fwd/bwd, loss  (:270-273, :53-63)
       --encode backward--> grid gradient (scale 128)  GridEncoding bwd       (:282-287)
@@ -117,7 +117,8 @@ class ExpertTrainer:
         mark = mark or (lambda name: None)
         r = self.routing
         view = Routing(r.perm[:n], r.coords[:n], r.offsets, None, r.colors[:n])
-        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, rgb=self.rgb,
+        # the route writes each slot's pixel index; the decoder reads the target's bytes itself
+        route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, pixels=True,
               uniforms=uniforms, slots=self.slots, experts=self.experts if self.slots is not None else None)
         mark('route')
         raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n])
@@ -128,7 +129,7 @@ class ExpertTrainer:
         # squared errors stay in routed order (slot j is id perm[j]); their mean is the loss
         if self.planes and update:
             planes, blockmax = self.decoder.train_planes(
-                features, n, colors=view.colors, squares=self.squares[:n], planes=self.plane_buffer[:16 * n].view(16, n),
+                features, n, pixels=view.colors, rgb=self.rgb, squares=self.squares[:n], planes=self.plane_buffer[:16 * n].view(16, n),
                 blockmax=self.max_buffer[:32 * ((n + 127) // 128)].view(-1, 32))
             mark('decoder')
             self.grid.backward_adam_planes(view.coords, view.offsets, planes, blockmax, self.grid_optimizer,
@@ -138,7 +139,7 @@ class ExpertTrainer:
             self.decoder_optimizer.step(self.decoder.grad, loss_scale=HEAD_SCALE)
             mark('decoder_adam')
             return self.squares[:n]
-        self.decoder.train(features, n, colors=view.colors, squares=self.squares[:n], dz=self.dz[:n])
+        self.decoder.train(features, n, pixels=view.colors, rgb=self.rgb, squares=self.squares[:n], dz=self.dz[:n])
         upstream = self.dz[:n]
         if self.gate is not None:
             upstream = self.gate.backward(raw, self.dz[:n], sigmoid, upstream=self.upstream[:n])

@@ -60,14 +60,12 @@ def test_headline_step_matches_oracle():
     squares = trainer.step(ids).cpu().numpy()
     torch.cuda.synchronize()
 
-    # route: expert order, local coordinates, offsets and slot colours
+    # route: expert order, local coordinates, offsets and each slot's pixel index
     _, perm, local, offsets = oracle.route(ids_host, width, height, regions, regions)
     assert np.array_equal(trainer.routing.perm[:n].cpu().numpy(), perm)
     assert np.array_equal(trainer.routing.coords[:n].cpu().numpy().view(np.uint32), local.view(np.uint32))
     assert np.array_equal(trainer.routing.offsets.cpu().numpy(), offsets)
-    pixel = image.reshape(-1, 3)[ids_host[perm]].astype(np.uint32)
-    colors = pixel[:, 0] | (pixel[:, 1] << 8) | (pixel[:, 2] << 16)
-    assert np.array_equal(trainer.routing.colors[:n].cpu().numpy().view(np.uint32), colors)
+    assert np.array_equal(trainer.routing.colors[:n].cpu().numpy(), ids_host[perm])
 
     # encode forward
     rows, params = rows_of(trainer.grid.levels), trainer.grid.expert_params
@@ -79,7 +77,7 @@ def test_headline_step_matches_oracle():
     out = torch.empty((n, 16), dtype=torch.float16, device='cuda')
     hidden = torch.empty((n, 128), dtype=torch.float16, device='cuda')
     again = torch.empty(n, dtype=torch.float32, device='cuda')
-    dz = probe.train(trainer.raw[:n], n, colors=trainer.routing.colors[:n], out=out, hidden=hidden,
+    dz = probe.train(trainer.raw[:n], n, pixels=trainer.routing.colors[:n], rgb=trainer.rgb, out=out, hidden=hidden,
                      squares=again).cpu().numpy()
     planes = trainer.plane_buffer[:16 * n].view(16, n).cpu().numpy().view(np.uint32)
     assert np.array_equal(planes, np.ascontiguousarray(dz).view(np.uint32).T)

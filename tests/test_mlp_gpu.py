@@ -68,6 +68,8 @@ def _train_case(seed, n, *, rgb8=True, permute=True, real=None, width=32):
         pixel = image.reshape(-1, 3)[ids[rows]].astype(np.uint32)
         packed = (pixel[:, 0] | (pixel[:, 1] << 8) | (pixel[:, 2] << 16)).astype(np.uint32).view(np.int32)
         kwargs.update(colors=torch.from_numpy(packed).cuda())
+    elif rgb8 == 'pixels':   # each tile row's pixel index, the target's bytes read by the decoder
+        kwargs.update(pixels=torch.from_numpy(ids[rows].astype(np.int32)).cuda(), rgb=torch.from_numpy(image).cuda())
     elif rgb8:
         kwargs.update(rgb=torch.from_numpy(image).cuda(), ids=torch.from_numpy(ids).cuda())
     else:
@@ -85,6 +87,8 @@ def _train_case(seed, n, *, rgb8=True, permute=True, real=None, width=32):
     (1 << 17, True, True, None, 32),    # every workgroup runs several tiles
     ((1 << 20) + 4133, True, True, None, 32),   # whole 128-row records per wave, ragged last record
     (5000, 'colors', True, 4000, 32),   # packed per-row targets (as odie_route writes them)
+    (5000, 'pixels', True, 4000, 32),   # per-row pixel indexes into the image
+    ((1 << 20) + 99, 'pixels', True, None, 32),
     (4096, True, True, None, 16),       # the input widths of the other level rows: 8 levels (16),
     (3001, True, False, 2500, 48),      # 20 levels of F2/F1 (48), F4 rows (64, 80)
     (1 << 16, 'colors', True, None, 64),

@@ -46,6 +46,29 @@ def test_route_tiles_at_every_bound_of_a_large_image():
     assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
 
 
+@pytest.mark.parametrize('width,height,rx,ry', [(2, 2, 1, 1), (3, 1000, 1, 4), (7, 5, 2, 2), (1024, 999, 4, 4),
+                                          (65535, 65537, 60, 60), (65536, 65535, 60, 60), (65537, 65535, 60, 60),
+                                          (100003, 42948, 60, 60)])
+def test_route_splits_ids_at_every_kind_of_row_bound(width, height, rx, ry):
+    """id -> (x, y) by one multiply-high with the width's magic number (Granlund and
+    Montgomery's division by invariant integers): ids at, just before and just after row bounds,
+    the image's last pixel, ids past it (clamped to the last row) up to 2^32 - 1; pixel indexes,
+    experts, order and local coordinates bit-exact against integer division."""
+    rows = np.unique(np.concatenate([[0, 1, height - 1], synth.integers(31, 'rows', 200, height)]))
+    ids = (rows[:, None].astype(np.int64) * width + np.array([0, 1, width - 1, width])[None, :]).reshape(-1)
+    top = (1 << 32) - 1
+    ids = np.concatenate([ids, [width * height - 1, min(width * height, top), top, top - width]])
+    ids = ids[(ids >= 0) & (ids <= top)]
+    result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, with_expert=True, pixels=True)
+    expert, perm, local, offsets = oracle.route(ids, width, height, rx, ry)
+    x, y = ids % width, np.minimum(ids // width, height - 1)
+    assert np.array_equal(result.colors.cpu().numpy().view(np.uint32), (y * width + x)[perm].astype(np.uint32))
+    assert np.array_equal(result.expert.cpu().numpy(), expert)
+    assert np.array_equal(result.offsets.cpu().numpy(), offsets)
+    assert np.array_equal(result.perm.cpu().numpy(), perm)
+    assert np.array_equal(result.coords.cpu().numpy().view(np.uint32), local.view(np.uint32))
+
+
 @pytest.mark.parametrize('width,height,rx,ry,n,offset', [(2048, 1365, 8, 8, 1 << 18, 0), (100, 37, 3, 5, 4099, 0),
                                                           (100, 37, 3, 5, 4099, 1)])
 def test_route_gathers_slot_colors(width, height, rx, ry, n, offset):
@@ -67,6 +90,10 @@ def test_route_gathers_slot_colors(width, height, rx, ry, n, offset):
     expected = pixel[:, 0] | (pixel[:, 1] << 8) | (pixel[:, 2] << 16)
     assert np.array_equal(result.colors.cpu().numpy().view(np.uint32), expected)
     assert np.array_equal(result.perm.cpu().numpy(), perm)
+    # without the image: each slot's pixel index itself (the decoder gathers the bytes)
+    indexes = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, pixels=True)
+    assert np.array_equal(indexes.colors.cpu().numpy(), (y * width + x)[perm])
+    assert np.array_equal(indexes.perm.cpu().numpy(), perm)
 
 
 def test_route_clustered_ids_and_empty_experts():

@@ -179,7 +179,7 @@ def test_router_step_composes_the_tested_stages():
     raw = trainer.raw[:3000]
     weighted, sigmoid = gate.forward(raw)
     assert np.array_equal(weighted.cpu().numpy().view(np.uint16), trainer.weighted[:3000].cpu().numpy().view(np.uint16))
-    dz = decoder.train(weighted, 3000, colors=trainer.routing.colors[:3000])
+    dz = decoder.train(weighted, 3000, pixels=trainer.routing.colors[:3000], rgb=trainer.rgb)
     upstream = gate.backward(raw, dz, sigmoid)
     assert np.array_equal(upstream.cpu().numpy().view(np.uint16), trainer.upstream[:3000].cpu().numpy().view(np.uint16))
     gradient = trainer.grid.backward(trainer.routing.coords[:3000], trainer.routing.offsets, upstream)
