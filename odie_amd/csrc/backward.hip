@@ -63,7 +63,31 @@ struct TransposeArgs {
     int width;
     int n_levels;
     int vec_rows;
+    // with the band lists: position i of the planes takes upstream row list[i] when *ordered (the
+    // lists then hold every coordinate of its expert once), so that the owner's banded walk reads
+    // its upstream values in list order, as it reads the sorted coordinates; row i otherwise
+    const int32_t* list;
+    const int32_t* ordered;
+    const int32_t* offsets;   // the experts' ranges (null: one expert over [0, n))
+    int experts;
 };
+
+// Positions [lo, hi) the band lists cover when *ordered: from the first expert's first
+// coordinate to the last one's end, clamped as the owner clamps the ranges.  Positions outside
+// (ids routed to no expert) have no list entry and keep their own row.
+__device__ inline void listed_range(const TransposeArgs& a, int64_t& lo, int64_t& hi) {
+    lo = 0;
+    hi = a.n;
+    if (!a.offsets) return;
+    const int64_t first = a.offsets[0], last = a.offsets[a.experts];
+    lo = first < 0 ? 0 : (first > a.n ? a.n : first);
+    hi = last > a.n ? a.n : (last < lo ? lo : last);
+}
+
+// Upstream row of plane position i.
+__device__ inline int64_t source_row(const TransposeArgs& a, bool by_list, int64_t lo, int64_t hi, int64_t i) {
+    return by_list && i >= lo && i < hi ? static_cast<int64_t>(a.list[i]) : i;
+}
 
 // Maximum of two |upstream| records; NaN wins, so the owner pass sees a non-finite bound.
 __device__ inline float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
@@ -92,12 +116,15 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_kernel(TransposeArg
     __shared__ float waves[kPasses][kTransposeBlock / 64][kColumns];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int used = a.n_levels * F;
+    const bool by_list = a.list && *a.ordered;
+    int64_t lo, hi;
+    listed_range(a, lo, hi);
     for (int r = 0; r < kPasses; ++r) {
         const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
         const bool valid = i < a.n;
         U vals[kColumns];
         if (valid) {
-            const U* row = reinterpret_cast<const U*>(a.upstream) + static_cast<size_t>(i) * a.width;
+            const U* row = reinterpret_cast<const U*>(a.upstream) + static_cast<size_t>(source_row(a, by_list, lo, hi, i)) * a.width;
             if (a.vec_rows) {
                 constexpr int kPer = 16 / sizeof(U);
                 constexpr int kChunks = (kColumns + kPer - 1) / kPer;
@@ -158,11 +185,19 @@ __global__ __launch_bounds__(kTransposeBlock) void transpose_half2_kernel(Transp
     __shared__ uint32_t waves[kPasses][kTransposeBlock / 64][2][LMAX];   // per lane group and level
     uint4 rows[kPasses][kChunks];
     const int chunks = a.n_levels / 4;
+    const bool by_list = a.list && *a.ordered;
+    int64_t lo, hi;
+    listed_range(a, lo, hi);
+    int64_t source[kPasses];   // every pass's row index loaded before any row
 #pragma unroll
     for (int r = 0; r < kPasses; ++r) {
         const int64_t i = static_cast<int64_t>(blockIdx.x) * kTransposeRows + r * kTransposeBlock + threadIdx.x;
+        source[r] = source_row(a, by_list, lo, hi, i < a.n ? i : 0);
+    }
+#pragma unroll
+    for (int r = 0; r < kPasses; ++r) {
         const uint4* row = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.upstream) +
-                                                          static_cast<size_t>(i < a.n ? i : 0) * a.width);
+                                                          static_cast<size_t>(source[r]) * a.width);
 #pragma unroll
         for (int j = 0; j < kChunks; ++j) rows[r][j] = j < chunks ? row[j] : make_uint4(0, 0, 0, 0);
     }
@@ -254,6 +289,10 @@ struct OwnerArgs {
     const int32_t* band_list;
     const float2* band_sorted;
     const int32_t* ordered;
+    // 1: the planes (and their record maxima) are in band-list order when *ordered (the backward
+    // transposed them so); every pass then reads coordinates from band_sorted and upstream values
+    // at the same list position
+    int band_planes;
     // slice masks (unbanded levels cut into at most 8 aligned blocks of 2^row_bits entries):
     // byte i of plane mask_plane[l] (planes mask_stride bytes apart) has bit s set when a corner
     // of coordinate i lands in block s
@@ -860,11 +899,11 @@ __device__ inline int find_run(const int32_t* prefix, int runs, int32_t v) {
 }
 
 // Concatenated run positions [v0, v1) of a banded slice against one level.  Position v of run r
-// is list entry run_k0[r] + v - prefix[r]: its coordinate's (x, y) in `sorted`, its index (for
-// the upstream) in `list`.  Each wave walks its own contiguous share of [v0, v1), kBatch
+// is list entry run_k0[r] + v - prefix[r]: its coordinate's (x, y) in `sorted`, its upstream at
+// the same entry of band-ordered planes (by_list), else at its index in `list`.  Each wave walks its own contiguous share of [v0, v1), kBatch
 // positions per lane per iteration, 64 apart; a lane's run only moves forward.
 template <int F, bool HALF, int KIND>
-__device__ inline void accumulate_runs(const float2* sorted, const Elem<HALF>* plane, const DevLevel lv,
+__device__ inline void accumulate_runs(const float2* sorted, bool by_list, const Elem<HALF>* plane, const DevLevel lv,
                                        const int32_t* list, const int32_t* run_k0, const int32_t* prefix, int runs,
                                        int32_t v0, int32_t v1, uint32_t lo, uint32_t span, const float* scale,
                                        unsigned long long* acc) {
@@ -888,7 +927,7 @@ __device__ inline void accumulate_runs(const float2* sorted, const Elem<HALF>* p
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
             xy[b] = sorted[k[b]];
-            load_upstream<F, HALF>(plane, list[k[b]], scale, ok[b], us[b]);
+            load_upstream<F, HALF>(plane, by_list ? k[b] : list[k[b]], scale, ok[b], us[b]);
         }
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) contribute<F, KIND>(xy[b].x, xy[b].y, us[b], lv, lo, span, acc);
@@ -1040,6 +1079,10 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         q1 = listed * (s + 1) / splits;
     }
 
+    // band-ordered planes: coordinates and upstream values at the same list positions, in every
+    // pass (an expert's list positions are its index range, so the passes' ranges are unchanged)
+    const bool by_list = a.band_planes && *a.ordered;
+    const float* coords = by_list ? reinterpret_cast<const float*>(a.band_sorted) : a.coords;
     for (int l = l0; l < l1; ++l) {
         const DevLevel lv = a.level[l];
         const U* plane = reinterpret_cast<const U*>(a.planes) + static_cast<size_t>(l) * a.n * F;
@@ -1052,10 +1095,10 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         if (banded) {
             if (runs == 0) break;
             switch (kind) {
-                case kHashed24: accumulate_runs<F, HALF, kHashed24>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
-                case kHashedPow2: accumulate_runs<F, HALF, kHashedPow2>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
-                case kGeneric: accumulate_runs<F, HALF, kGeneric>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
-                default: accumulate_runs<F, HALF, kDense>(a.band_sorted, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                case kHashed24: accumulate_runs<F, HALF, kHashed24>(a.band_sorted, by_list, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                case kHashedPow2: accumulate_runs<F, HALF, kHashedPow2>(a.band_sorted, by_list, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                case kGeneric: accumulate_runs<F, HALF, kGeneric>(a.band_sorted, by_list, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
+                default: accumulate_runs<F, HALF, kDense>(a.band_sorted, by_list, plane, lv, a.band_list, run_k0, prefix, runs, static_cast<int32_t>(q0), static_cast<int32_t>(q1), lo, span, scale, acc); break;
             }
         } else if (!grouped && a.masks && a.mask_plane[l] >= 0) {
             const uint8_t* mask = a.masks + static_cast<int64_t>(a.mask_plane[l]) * a.mask_stride;
@@ -1069,14 +1112,14 @@ __global__ __launch_bounds__(kOwnerBlock) void owner_kernel(OwnerArgs a) {
         } else {
             switch (kind) {
                 case kHashed24:
-                    if (grouped) accumulate_level<F, HALF, kHashed24, kGroupBatch>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
-                    else accumulate_level<F, HALF, kHashed24>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    if (grouped) accumulate_level<F, HALF, kHashed24, kGroupBatch>(coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    else accumulate_level<F, HALF, kHashed24>(coords, plane, lv, b0, b1, lo, span, scale, acc);
                     break;
-                case kHashedPow2: accumulate_level<F, HALF, kHashedPow2>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
-                case kGeneric: accumulate_level<F, HALF, kGeneric>(a.coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                case kHashedPow2: accumulate_level<F, HALF, kHashedPow2>(coords, plane, lv, b0, b1, lo, span, scale, acc); break;
+                case kGeneric: accumulate_level<F, HALF, kGeneric>(coords, plane, lv, b0, b1, lo, span, scale, acc); break;
                 default:
-                    if (grouped) accumulate_level<F, HALF, kDense, kGroupBatch>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
-                    else accumulate_level<F, HALF, kDense>(a.coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    if (grouped) accumulate_level<F, HALF, kDense, kGroupBatch>(coords, plane, lv, b0, b1, lo, span, scale, acc);
+                    else accumulate_level<F, HALF, kDense>(coords, plane, lv, b0, b1, lo, span, scale, acc);
                     break;
             }
         }
@@ -1671,7 +1714,16 @@ int launch_owner_backward(const OwnerLaunch& in) {
         if (check_launch("owner band lists")) return -1;
     }
 
+    // the backward's own transpose writes the planes in band-list order (read in order by every
+    // pass) for a single expert; planes the caller hands over stay in index order, and so do
+    // several experts' (a 128-row record across two experts' ranges would hold other rows in list
+    // order, and the column peaks it feeds, hence the fixed-point scales, would move)
+    o.band_planes = lists && !given && in.experts == 1;
     TransposeArgs t{};
+    t.list = o.band_planes ? o.band_list : nullptr;
+    t.ordered = o.ordered;
+    t.offsets = in.offsets;
+    t.experts = in.experts;
     t.upstream = in.upstream;
     t.planes = space + at[0];
     t.blockmax = reinterpret_cast<float*>(space + at[1]);

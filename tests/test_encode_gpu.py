@@ -174,6 +174,26 @@ def test_banded_owner_matches_unbanded(log2, experts, n, outside):
         assert np.allclose(got[finite], want[finite], rtol=1e-5, atol=1e-6 * np.abs(want[finite]).max())
 
 
+def test_single_expert_band_order_against_the_oracle():
+    """One expert (its offsets dropped: every row is its) with band lists: the backward transposes
+    the upstream in band-list order and every pass reads it at the list positions.  Off-square
+    coordinates (the lists' last slot) and a ragged last 128-row record; the gradient within the
+    oracle's bar, and within fp32 rounding of the index-order (unbanded) owner."""
+    levels, entries = grid_levels(encoding(log2=17))
+    params, n = entries * 2, 300001
+    xy = synth.coordinates(41, n)
+    xy[::97, 0] = 1.5
+    xy[7::211] = (-3.0, 2.5)
+    up = synth.upstream(41, n, 32)
+    d_xy, d_up = torch.from_numpy(xy).cuda(), torch.from_numpy(up).cuda().half()
+    run = lambda: grid_backward(d_xy, d_up, levels, 2, expert_params=params)
+    banded = _tuned('banded', 1, 2, run)
+    plain = _tuned('banded', 0, 2, run)
+    got, want = banded.cpu().numpy(), plain.cpu().numpy()
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+    check_gradient(banded, hash_bar(xy, up.astype(np.float16), levels, 2, params), 'band order')
+
+
 @pytest.mark.parametrize('log2,experts,n', [(19, 1, 1 << 20), (14, 16, 300000), (12, 3, 5000)])
 def test_banded_splits_are_exact(log2, experts, n):
     """Banded splits write 64-bit partial sums at one scale per pass and are added exactly: the
