@@ -934,8 +934,8 @@ __device__ inline void accumulate_runs(const float2* sorted, bool by_list, const
     }
 }
 
-// Block -> work item.  Remapped, each XCD takes a contiguous chunk of the items (an expert's
-// slices share its coordinates in that XCD's L2).  Inside a chunk the heavy items -- the
+// Block -> work item.  Remapped (with at least one expert per XCD), each XCD takes a contiguous
+// chunk of the items (an expert's slices share its coordinates in that XCD's L2).  Inside a chunk the heavy items -- the
 // splits of every expert's coarse-group pass, `heavy` per expert, which walk all coordinates
 // through several fully landing levels and take about six times as long as a fine slice --
 // come first, so that they start at once instead of finishing after everything else.  A
@@ -1490,7 +1490,12 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.accumulate = in.accumulate;
     o.fused = in.adam != nullptr;
     if (in.adam) o.adam = *in.adam;
-    o.remap = in.remap;
+    // XCD-major items only when every XCD's chunk holds whole experts: with fewer experts than
+    // XCDs a chunk is a run of one expert's items, so the coarse-group splits (the heaviest,
+    // numbered first) would all land on the first XCDs (measured, one expert of 2^19-entry levels
+    // and 2^22 coordinates: 1.00 ms remapped against 0.80 ms in launch order, which deals the
+    // items round-robin over the XCDs).
+    o.remap = in.remap && in.experts >= kXcds;
     int group = 0;
     int64_t grouped = 0;
     // the coarse group: the leading levels whose values fit the slice
@@ -1573,7 +1578,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     int64_t max_splits = 1;
     if (banded) {
         // Size every item near a target share of the estimated work (coordinate-level visits):
-        // an eighth of a CU's share of the whole pass, at least 65536 visits (each item pays a
+        // an eighth of a CU's share of the whole pass (less, below), at least 65536 visits (each item pays a
         // fixed set-up; measured best on MI355X for one expert of 2^19-entry levels and 2^22
         // coordinates).  A visit of the coarse group counts kGroupCost times: all of its
         // contributions land in its slice (measured).
@@ -1583,7 +1588,15 @@ int launch_owner_backward(const OwnerLaunch& in) {
         for (int l = group; l < L; ++l)
             work += o.slices[l] * per * band_coverage(in.levels[l], o.slice_entries[l], o.slices[l], o.row_bits[l]);
         constexpr double kLeastItem = 65536.0;
-        double target = in.split_target > 0 ? static_cast<double>(in.split_target) : work * in.experts / (8.0 * kCus);
+        // With band-ordered planes (one expert, the backward's own transpose) a visit reads its
+        // upstream value in order instead of gathering it, so the fixed cost of an item weighs
+        // more: 1/2.8 of a CU's share there, ~195000 visits for the same single expert (measured
+        // in launch order: 0.79 ms at fixed splits of 190000 and 200000 visits, 0.81-0.84 ms
+        // from 100000 to 230000, 0.86 ms at an eighth, ~68000 -- the time moves in steps as the
+        // ways per pass round up).
+        const bool band_order = group < L && !in.planes && in.experts == 1;
+        const double share = band_order ? 2.8 : 8.0;
+        double target = in.split_target > 0 ? static_cast<double>(in.split_target) : work * in.experts / (share * kCus);
         if (in.split_target <= 0 && target < kLeastItem) target = kLeastItem;
         const auto ways = [&](double visits, double most) {
             const double w = std::ceil(visits / target);
