@@ -89,15 +89,46 @@ template <int KT> __device__ inline void fetch_tile(const MlpArgs& a, int64_t ro
     for (int kt = 0; kt < KT; ++kt) in.xb[kt] = valid ? xb[kt] : half8{};
 }
 
-// Per-wave transposition region: feature-major rows of the 32 samples of the wave's current
-// tile, 40 halfs (80 bytes) apart.  A lane writes one sample of a feature (the 32 lanes of a lane
-// group fill one 64-byte row; the two groups' rows, 4 apart, fall on opposite halves of the
-// banks) and reads 8 samples of one row as a 16x16x32 operand (8 lanes cover 8 rows at 8
-// distinct 16-byte bank offsets).  Rows: phase 1 dy 0..2 (3..15 hold stale values whose products
-// fall in gradient rows that are never written out) and h2 16..79; phase 2 dh2 0..63 and h1
-// 64..127; phase 3 dh1 0..63 and x 64...
-constexpr int kTS = 40;
-template <int KT> constexpr int region_rows() { return 64 + 16 * KT > 128 ? 64 + 16 * KT : 128; }
+// Per-wave transposition region: two sample-major matrices of the wave's current 32 samples,
+// A (dy, then dh2, then dh1) and B (h2, then h1, then x), each sample a 160-byte row of up to 80
+// fp16 features in 8-byte chunks of 4.  Chunk q of sample s sits at byte
+//   s * 160 + 32 * (q / 4) + 8 * ((q % 4) ^ ((s / 4) % 4)),
+// so that every 16 lanes of both access patterns meet 16 distinct 8-byte slots of a 128-byte bank
+// line (no bank conflict): a lane stores its sample's feature chunks with ds_write_b64 (16 consecutive samples, one
+// chunk: slots 4 * ((s + q / 4) % 4) + (q % 4 ^ s / 4 % 4), all distinct), and a 16x16x32 operand
+// comes back with two ds_read_b64_tr_b16 (within a 16-lane group lane j fetches chunk 4b + j % 4
+// of sample k0 + j / 4, and the read hands lane 4a + e element e of the chunks fetched by lanes a,
+// a + 4, a + 8, a + 12: feature 16b + 4a + e of samples k0 .. k0 + 3).  Phase 1 puts dy in chunk 0
+// of A; chunks 1..3 hold stale values whose products fall in gradient rows that are never
+// written out.
+constexpr int kRowBytes = 160;
+constexpr int kMatrixBytes = 32 * kRowBytes;
+constexpr int kRegionBytes = 2 * kMatrixBytes;
+
+typedef int16_t short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v* lds_short4;
+
+// Byte offset, within a matrix, of chunk q (q % 4 == lo) of sample s: lo ^ the sample's swizzle.
+__device__ inline int chunk_at(int s, int lo) { return s * kRowBytes + 8 * (lo ^ ((s >> 2) & 3)); }
+
+// Stores this lane's sample (byte row `at_lo`/`at_hi`: chunks 4t + g and 4t + 2 + g, see chunk_at)
+// of 16*halves features held in accumulator-row order (elements 0..3 of h[t] are features
+// 16t + 4g + 0..3, elements 4..7 features 16t + 8 + 4g + 0..3).
+__device__ inline void put_chunks(char* M, int at_lo, int at_hi, const half8* h, int halves) {
+    for (int t = 0; t < halves; ++t) {
+        const u32x4 d = __builtin_bit_cast(u32x4, h[t]);
+        *reinterpret_cast<uint2*>(M + at_lo + 32 * t) = make_uint2(d.x, d.y);
+        *reinterpret_cast<uint2*>(M + at_hi + 32 * t) = make_uint2(d.z, d.w);
+    }
+}
+
+// 16x16x32 operand of features 16*block .. +15 of matrix M: lane l holds feature 16*block + l%16,
+// samples 8*(l/16) .. +7.  at[h] is the lane's fetch address for samples 8*(l/16) + 4h .. +3.
+__device__ inline half8 operand16(const char* M, const int at[2], int block) {
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)(M + at[0] + 32 * block));
+    const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4)(M + at[1] + 32 * block));
+    return __builtin_bit_cast(half8, (short8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
@@ -108,27 +139,6 @@ __device__ inline void wave_fence() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Writes this lane's sample column s of 16*halves features held in accumulator-row order
-// (h[t][e] = feature feature_of(t, g, e)) into rows first.. of the region.
-// Odd elements are stored from the high half of their dword (ds_write_b16_d16_hi).
-__device__ inline void put_rows(_Float16* R, int first, int s, const half8* h, int halves, int g) {
-    uint16_t* r = reinterpret_cast<uint16_t*>(R) + s;
-    for (int t = 0; t < halves; ++t) {
-        const u32x4 d = __builtin_bit_cast(u32x4, h[t]);
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            r[(first + feature_of(t, g, e)) * kTS] = static_cast<uint16_t>(d[e / 2]);
-            r[(first + feature_of(t, g, e + 1)) * kTS] = static_cast<uint16_t>(d[e / 2] >> 16);
-        }
-    }
-}
-
-// 16x16x32 operand of rows first + 16*block ..: lane l holds row first + 16*block + l%16,
-// samples 8*(l/16) .. +7 (the contraction runs over the tile's 32 samples).
-__device__ inline half8 rows16(const _Float16* R, int first, int block, int lane) {
-    return lds8(R + (first + 16 * block + (lane & 15)) * kTS + 8 * (lane >> 4));
 }
 
 // Work split: each wave takes tiles of 32 samples in turn (below: how records of 128 rows are
@@ -145,14 +155,24 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
     using S = Shape<KT>;
     static_assert(!PLANES || KT == 2, "the planes layout is built for 16 levels x 2 features");
     constexpr int kNB = (KT + 1) / 2;   // 32-row blocks of dX
-    constexpr int kRows = region_rows<KT>();
-    static_assert(kMlpWaves * kRows * kTS * 2 >= S::kParams * 4, "the regions hold the workgroup's gradient");
+    static_assert(kMlpWaves * kRegionBytes >= S::kParams * 4, "the regions hold the workgroup's gradient");
+    static_assert(16 * KT <= 80, "a matrix row holds at most 80 features");
     __shared__ _Float16 w[S::kWeightHalfs];
-    __shared__ __attribute__((aligned(16))) _Float16 T[kMlpWaves * kRows * kTS];
+    __shared__ __attribute__((aligned(16))) char T[kMlpWaves * kRegionBytes];
     stage_weights<KT>(a.weights, w);
     __syncthreads();
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, g = lane / 32, s = lane % 32;
-    _Float16* R = T + wave * kRows * kTS;
+    // wave: uniform over the wave, in a scalar register (so are the tile positions derived from it)
+    const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int g = lane / 32, s = lane % 32;
+    char* const MA = T + wave * kRegionBytes;
+    char* const MB = MA + kMatrixBytes;
+    // store addresses of this lane's sample: chunks 4t + g, 4t + 2 + g (hidden layers), 4kt + 2g,
+    // 4kt + 2g + 1 (x); fetch addresses of its operand rows: samples 8 * (lane / 16) + 4h + j / 4,
+    // chunk j % 4 (j = lane % 16)
+    const int at_lo = chunk_at(s, g), at_hi = chunk_at(s, g ^ 2);
+    const int at_x0 = chunk_at(s, 2 * g), at_x1 = chunk_at(s, 2 * g + 1);
+    const int at_op[2] = {chunk_at(8 * (lane >> 4) + ((lane & 15) >> 2), lane & 3),
+                          chunk_at(8 * (lane >> 4) + 4 + ((lane & 15) >> 2), lane & 3)};
     f32x4 gW3[4], gW2[4][4], gW1[4][KT];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -168,14 +188,14 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
     // with PLANES: per-feature |dz| maxima of the lane group's 8 levels (lane i: word i % 8) over
     // the last tile processed, and over the current record
     uint32_t tile_peak = 0, record_peak = 0;
-    auto process = [&](int64_t tile, const TileInput<KT>& current) {
-        const int64_t row = tile * 32 + s;
-        const bool valid = row < a.n;
-        // with colors and rgb together, colors holds the slot's pixel index: its three bytes are
-        // loaded here, a forward pass ahead of the loss, and kept apart until the loss reads them
-        // (joining them here would wait for the loads at once)
-        const bool gather = a.colors && a.rgb;
-        uint32_t byte[3] = {0u, 0u, 0u};
+    // With colors and rgb together, colors holds the slot's pixel index: the tile's three target
+    // bytes are loaded before the next tile's prefetch is issued, so that the loss waits for them
+    // alone (memory counters drain in issue order: loaded after the prefetch, they would make the
+    // loss wait for the whole prefetch as well), and kept apart until the loss reads them (joining
+    // them at once would wait for the loads there).
+    const bool gather = a.colors && a.rgb;
+    auto gather_bytes = [&](const TileInput<KT>& current, uint32_t byte[3]) {
+        byte[0] = byte[1] = byte[2] = 0u;
         if (gather) {   // every lane (both lane groups of a sample read the same bytes), no branch
             // three byte loads from addresses the compiler cannot see as adjacent (it would merge
             // them into a 16-bit load whose split waits for it at once)
@@ -190,6 +210,10 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
 #pragma unroll
             for (int c = 0; c < 3; ++c) byte[c] = *p[c];
         }
+    };
+    auto process = [&](int64_t tile, const TileInput<KT>& current, const uint32_t byte[3]) {
+        const int64_t row = tile * 32 + s;
+        const bool valid = row < a.n;
         half8 h1[4], h2[4];
         f32x16 acc3;
         forward_tile<KT>(w, g, s, current.xb, h1, h2, acc3);
@@ -227,17 +251,14 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
                 *reinterpret_cast<uint2*>(hrow + 64 + feature_of(t, g, 4)) = make_uint2(b2.z, b2.w);
             }
         }
-        // dW3 += dy (x) h2 over the tile's samples
-        if (g == 0)
-#pragma unroll
-            for (int c = 0; c < 3; ++c) R[c * kTS + s] = dy[c];
-        put_rows(R, 16, s, h2, 4, g);
-        wave_fence();
-        {
-            const half8 A = rows16(R, 0, 0, lane);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) gW3[j] = mfma16(A, rows16(R, 16, j, lane), gW3[j]);
+        // Each phase stores a pair of layers into the region, computes the next input gradient
+        // from registers (after which those layers' registers are free), then the weight
+        // gradient from the region: dW3 += dy (x) h2 over the tile's samples
+        if (g == 0) {   // dy: features 0..2 of chunk 0, feature 3 zero
+            const u32x4 d = __builtin_bit_cast(u32x4, dy);
+            *reinterpret_cast<uint2*>(MA + at_lo) = make_uint2(d.x, d.y);
         }
+        put_chunks(MB, at_lo, at_hi, h2, 4);
         // input gradients: dH2 = relu'(h2) * (W3^T dy), dH1 = relu'(h1) * (W2^T dH2), dX = W1^T dH1
         half8 dh2[4], dh1[4];
 #pragma unroll
@@ -246,22 +267,16 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
             dh2[2 * mb] = mask8(round8(acc, 0), h2[2 * mb]);
             dh2[2 * mb + 1] = mask8(round8(acc, 8), h2[2 * mb + 1]);
         }
-        // dW2 += dh2 (x) h1
-        wave_fence();
-        put_rows(R, 0, s, dh2, 4, g);
-        put_rows(R, 64, s, h1, 4, g);
         wave_fence();
         {
-            half8 B[4];
+            const half8 A = operand16(MA, at_op, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) B[j] = rows16(R, 64, j, lane);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const half8 A = rows16(R, 0, i, lane);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) gW2[i][j] = mfma16(A, B[j], gW2[i][j]);
-            }
+            for (int j = 0; j < 4; ++j) gW3[j] = mfma16(A, operand16(MB, at_op, j), gW3[j]);
         }
+        // dW2 += dh2 (x) h1
+        wave_fence();
+        put_chunks(MA, at_lo, at_hi, dh2, 4);
+        put_chunks(MB, at_lo, at_hi, h1, 4);
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
             f32x16 acc = zero16();
@@ -271,30 +286,26 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
             dh1[2 * mb] = mask8(round8(acc, 0), h1[2 * mb]);
             dh1[2 * mb + 1] = mask8(round8(acc, 8), h1[2 * mb + 1]);
         }
-        // dW1 += dh1 (x) x
-        wave_fence();
-        put_rows(R, 0, s, dh1, 4, g);
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-            const u32x4 d = __builtin_bit_cast(u32x4, current.xb[kt]);
-            uint16_t* r = reinterpret_cast<uint16_t*>(R) + (64 + 16 * kt + 8 * g) * kTS + s;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                r[e * kTS] = static_cast<uint16_t>(d[e / 2]);
-                r[(e + 1) * kTS] = static_cast<uint16_t>(d[e / 2] >> 16);
-            }
-        }
         wave_fence();
         {
-            half8 A[4];
+            half8 B[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) A[i] = rows16(R, 0, i, lane);
+            for (int j = 0; j < 4; ++j) B[j] = operand16(MB, at_op, j);
 #pragma unroll
-            for (int j = 0; j < KT; ++j) {
-                const half8 B = rows16(R, 64, j, lane);
+            for (int i = 0; i < 4; ++i) {
+                const half8 A = operand16(MA, at_op, i);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) gW1[i][j] = mfma16(A[i], B, gW1[i][j]);
+                for (int j = 0; j < 4; ++j) gW2[i][j] = mfma16(A, B[j], gW2[i][j]);
             }
+        }
+        // dW1 += dh1 (x) x
+        wave_fence();
+        put_chunks(MA, at_lo, at_hi, dh1, 4);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {   // x: features 16kt + 8g + 0..7 of the lane's sample
+            const u32x4 d = __builtin_bit_cast(u32x4, current.xb[kt]);
+            *reinterpret_cast<uint2*>(MB + at_x0 + 32 * kt) = make_uint2(d.x, d.y);
+            *reinterpret_cast<uint2*>(MB + at_x1 + 32 * kt) = make_uint2(d.z, d.w);
         }
         {
             // fp16(fp16(dx) / 128): one fp16 multiply by 2^-7 rounds the same exact value.  K step
@@ -319,12 +330,19 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
             }
             if constexpr (PLANES) {
                 if (valid) {
+                    // level 8q + 2g + c at planes + (8q + c) * n (uniform: a scalar base) + the lane's
+                    // 32-bit offset of plane 2g, row `row` (below 12n bytes; the host keeps 64n < 2^32)
+                    const uint32_t at = static_cast<uint32_t>(2 * g * a.n + row) * 4u;
+                    const auto put = [&](int level, uint32_t v) {
+                        char* const base = reinterpret_cast<char*>(a.planes) + static_cast<int64_t>(level) * a.n * 4;
+                        *reinterpret_cast<uint32_t*>(base + at) = v;
+                    };
 #pragma unroll
                     for (int q = 0; q < 2; ++q) {
-                        a.planes[(8 * q + 2 * g) * a.n + row] = bits[q].x;
-                        a.planes[(8 * q + 2 * g + 1) * a.n + row] = bits[q].y;
-                        a.planes[(8 * q + 4 + 2 * g) * a.n + row] = bits[q].z;
-                        a.planes[(8 * q + 5 + 2 * g) * a.n + row] = bits[q].w;
+                        put(8 * q, bits[q].x);
+                        put(8 * q + 1, bits[q].y);
+                        put(8 * q + 4, bits[q].z);
+                        put(8 * q + 5, bits[q].w);
                     }
                 }
                 // per-feature maxima of the lane group's eight levels over its 32 lanes (every
@@ -342,6 +360,18 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
                     *reinterpret_cast<uint2*>(p + 16 * ks + 4 * g) = make_uint2(bits[ks].x, bits[ks].y);
                     *reinterpret_cast<uint2*>(p + 16 * ks + 8 + 4 * g) = make_uint2(bits[ks].z, bits[ks].w);
                 }
+            }
+        }
+        wave_fence();
+        {
+            half8 A[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) A[i] = operand16(MA, at_op, i);
+#pragma unroll
+            for (int j = 0; j < KT; ++j) {
+                const half8 B = operand16(MB, at_op, j);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gW1[i][j] = mfma16(A[i], B, gW1[i][j]);
             }
         }
     };
@@ -363,14 +393,14 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
         return whole ? (first + (i / 4) * step) * 4 + i % 4 : (first + i * step) * 4 + wave;
     };
     // level L = 8q + 4h + 2g + b of column 2L + f is word 4q + 2h + b of lane group g
-    const int level = lane / 2, f = lane % 2;
-    const int lg = (level / 2) % 2, word = 4 * (level / 8) + 2 * ((level / 4) % 2) + level % 2;
     __shared__ uint32_t pairs[kMlpWaves][32];
     auto finish = [&](int64_t i) {   // after the tile at position i
         if constexpr (PLANES) {
             record_peak = pair_max(record_peak, tile_peak);
             if (whole && i % 4 != 3) return;
             // lanes 0..31 hold the pair of their column 2L + f
+            const int level = lane / 2, f = lane % 2;
+            const int lg = (level / 2) % 2, word = 4 * (level / 8) + 2 * ((level / 4) % 2) + level % 2;
             const uint32_t m = static_cast<uint32_t>(__shfl(static_cast<int>(record_peak), 32 * lg + word));
             record_peak = 0;
             const int64_t record = tile_of(i) / 4;
@@ -391,16 +421,19 @@ __global__ __launch_bounds__(kMlpBlock, KT <= 3 ? 2 : 1) void mlp_train_kernel(M
         }
     };
     TileInput<KT> even, odd;
+    uint32_t bytes[3];
     if (count) fetch_tile<KT>(a, tile_of(0) * 32 + s, g, even);
     for (int64_t i = 0; i < count; i += 2) {
+        gather_bytes(even, bytes);
         fetch_tile<KT>(a, tile_of(i + 1) * 32 + s, g, odd);
         tile_peak = 0;
-        if (tile_of(i) < tiles) process(tile_of(i), even);
+        if (tile_of(i) < tiles) process(tile_of(i), even, bytes);
         finish(i);
         if (i + 1 >= count) break;
+        gather_bytes(odd, bytes);
         fetch_tile<KT>(a, tile_of(i + 2) * 32 + s, g, even);
         tile_peak = 0;
-        if (tile_of(i + 1) < tiles) process(tile_of(i + 1), odd);
+        if (tile_of(i + 1) < tiles) process(tile_of(i + 1), odd, bytes);
         finish(i + 1);
     }
     // The workgroup's partial: the four waves' gradients summed in wave order in LDS (lane l holds
