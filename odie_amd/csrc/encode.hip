@@ -57,7 +57,7 @@ struct Tuning {
     int packed_splits = 0;          // packed owner: coordinate splits per slice (0: automatic)
     int packed_lds = 1;             // packed backward with atomics: coarse levels accumulated in LDS
     int packed_blocks = 256;        // packed backward with LDS: most blocks (each flushes its partials once)
-    int paired_loads = 0;           // forward: 16-byte corner-pair loads (measured no gain)
+    int paired_loads = 2;           // forward: 16-byte corner-pair loads (0 off, 1 on, 2: tables past one L2)
     int forward_lds_bytes = 28672;  // forward: LDS budget for staged coarse levels (0: off)
     int owner_lds_bytes = 162816;   // 160 KiB minus the owner kernel's static 1 KiB (its Adam rate table)
 };
@@ -683,7 +683,7 @@ int set_grid_tuning(const std::string& key, int value) {
     else if (key == "packed_splits" && value >= 0 && value <= 64) t.packed_splits = value;
     else if (key == "packed_lds" && (value == 0 || value == 1)) t.packed_lds = value;
     else if (key == "packed_blocks" && value >= 1 && value <= 65536) t.packed_blocks = value;
-    else if (key == "paired_loads" && (value == 0 || value == 1)) t.paired_loads = value;
+    else if (key == "paired_loads" && value >= 0 && value <= 2) t.paired_loads = value;
     else if (key == "forward_lds_bytes" && value >= 0 && value <= 65536) t.forward_lds_bytes = value;
     else if (key == "owner_lds_bytes" && value >= 4096 && value <= 162816) t.owner_lds_bytes = value;
     else return fail("odie_set_tuning: unknown key or value out of range: " + key);
@@ -714,8 +714,15 @@ ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* of
     a.remap = tuning().xcd_remap;
     {
         const uint64_t entries = static_cast<uint64_t>(levels[n_levels - 1].offset) + levels[n_levels - 1].size;
-        a.paired = tuning().paired_loads && half && features == 2 && reinterpret_cast<uintptr_t>(params) % 16 == 0 &&
-                   entries % 4 == 0 && (expert_params * 2) % 16 == 0;
+        // Corner pairs from one 16-byte group load pay where an expert's table is larger than one
+        // XCD's L2 (4 MB) and the gathers miss it: one request for corners (x, y) and (x+1, y)
+        // instead of two (measured, one expert of 2^19-entry levels, 11 MB: 0.611 -> 0.581 ms).
+        // With the table in L2 the gathers hit and the pair's selects cost more than the second
+        // request (64 experts of 2^16-entry levels, 2.2 MB each: 0.453 -> 0.458 ms).
+        const int mode = tuning().paired_loads;
+        const bool past_l2 = expert_params * 2 > (int64_t{4} << 20);
+        a.paired = (mode == 1 || (mode == 2 && past_l2)) && half && features == 2 &&
+                   reinterpret_cast<uintptr_t>(params) % 16 == 0 && entries % 4 == 0 && (expert_params * 2) % 16 == 0;
         // Stage the longest prefix of levels that fits the budget (entries of 4 bytes).
         if (half && features == 2 && reinterpret_cast<uintptr_t>(params) % 16 == 0 && (expert_params * 2) % 16 == 0) {
             int64_t staged = 0;

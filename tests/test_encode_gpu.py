@@ -62,6 +62,25 @@ def test_single_grid_forward_bit_exact(dtype):
     assert not mismatch.any(), 'mismatches at %s' % (np.argwhere(mismatch)[:5],)
 
 
+@pytest.mark.parametrize('log2', [14, 19])
+@pytest.mark.parametrize('mode', [0, 1, 2], ids=['single', 'pairs', 'auto'])
+def test_forward_corner_pairs_bit_exact(mode, log2):
+    """The fp16 forward's 16-byte corner-pair loads (tuning key paired_loads: off, on, and the
+    default, on only for tables past 4 MB) against the oracle, on a table that fits one L2
+    (2^14 entries) and one that does not (2^19): the odd corner outside its group of four
+    entries takes the single load."""
+    enc = encoding(log2=log2)
+    levels, entries = grid_levels(enc)
+    n = 1 << 15
+    xy = synth.coordinates(3, n)
+    table = synth.table(3, entries * 2).astype(np.float16)
+    out = _tuned('paired_loads', mode, 2, lambda: grid_forward(torch.from_numpy(xy).cuda(),
+                                                               torch.from_numpy(table).cuda(), levels, 2))
+    expected = oracle.hash_forward(xy, table, rows_of(levels), 2, threads=0)
+    mismatch = out.cpu().numpy().view(np.uint16) != expected.view(np.uint16)
+    assert not mismatch.any(), 'mismatches at %s' % (np.argwhere(mismatch)[:5],)
+
+
 @pytest.fixture(params=[(1, 1), (1, 0), (0, 0)], ids=['owner-banded', 'owner', 'atomics'])
 def backward_mode(request):
     mode, banded = request.param
