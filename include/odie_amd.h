@@ -116,6 +116,35 @@ int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t
                                    int64_t step, float lr, float beta1, float beta2, float eps, float loss_scale,
                                    uint64_t stream);
 
+/* Slice masks carried from the encode forward to the encode backward.  No counterpart in the
+ * reference: a split of this library's owner backward, for training steps that run
+ * odie_grid_forward and then odie_grid_backward_adam_planes on the same coordinates.  The
+ * backward's unbanded hashed slices walk only the coordinates whose corners reach them; it
+ * forms a byte per (coordinate, such level) itself in a pass over the coordinates, which the
+ * forward can write instead, since it forms every corner index already.
+ *
+ * odie_grid_mask_bytes: the bytes of that mask buffer for this batch and grid under the
+ * current tuning (0 when the backward would use no masks; -1 on invalid arguments).
+ * odie_grid_forward_masks: odie_grid_forward that also writes the masks (mask_bytes at least
+ * odie_grid_mask_bytes; masks may be null when that is 0).
+ * odie_grid_backward_adam_planes_masks: odie_grid_backward_adam_planes that reads those masks
+ * instead of forming them: the same update, bit for bit, when they were written by
+ * odie_grid_forward_masks for the same coords, n, offsets, experts and levels, with no
+ * odie_set_tuning call in between. */
+int64_t odie_grid_mask_bytes(int64_t n, int experts, int64_t expert_params, const odie_grid_level* levels,
+                             int n_levels, int features);
+int odie_grid_forward_masks(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                            const void* params, int64_t expert_params, int param_dtype,
+                            const odie_grid_level* levels, int n_levels, int features, void* out, int out_width,
+                            uint8_t* masks, int64_t mask_bytes, uint64_t stream);
+int odie_grid_backward_adam_planes_masks(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                         const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                         const odie_grid_level* levels, int n_levels, int features, float* master,
+                                         uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant,
+                                         int64_t step, float lr, float beta1, float beta2, float eps,
+                                         float loss_scale, const uint8_t* masks, int64_t mask_bytes,
+                                         uint64_t stream);
+
 /* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of
  * 256; forward_chunk 0 (default) = 1024 when at least half of the table fits the forward's

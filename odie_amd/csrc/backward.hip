@@ -566,7 +566,6 @@ __device__ inline void accumulate_masked(const float* coords, const Elem<HALF>* 
 // Mask bytes of the masked levels: plane p, byte i = the aligned blocks of 2^bits[p] entries of
 // level level[p] that the corners of coordinate i land in (bit s: block s).  Planes are `stride`
 // bytes apart.  The launch also clears the column peaks (zero words).
-constexpr int kMaxMaskPlanes = 16;
 
 struct MaskArgs {
     const float* coords;
@@ -1558,6 +1557,22 @@ int launch_owner_backward(const OwnerLaunch& in) {
             ++mask_args.planes;
         }
     }
+    const int64_t mask_stride = (in.n + 255) / 256 * 256;
+    if (in.plan_out) {
+        MaskPlan& plan = *in.plan_out;
+        plan = MaskPlan{};
+        plan.planes = mask_args.planes;
+        plan.stride = mask_stride;
+        for (int l = 0; l < L; ++l)
+            if (o.mask_plane[l] >= 0) {
+                plan.level[o.mask_plane[l]] = l;
+                plan.bits[o.mask_plane[l]] = mask_args.bits[o.mask_plane[l]];
+            }
+        return 0;
+    }
+    const bool given_masks = in.given_masks && mask_args.planes > 0;
+    if (given_masks && in.given_mask_bytes < mask_stride * mask_args.planes)
+        return fail("odie_grid_backward: the given slice masks are shorter than the plan's planes");
     o.ring_at = static_cast<int>(shmem - kRingBytes);
     int passes = group > 0 ? 1 : 0;
     for (int l = 0; l < L; ++l) {
@@ -1672,8 +1687,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t start_bytes = lists ? align(static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4 + 4) : 0;
     const size_t list_bytes = lists ? align(static_cast<size_t>(in.n) * 4) : 0;
     const size_t sorted_bytes = lists ? align(static_cast<size_t>(in.n) * 8) : 0;
-    const int64_t mask_stride = static_cast<int64_t>(align(static_cast<size_t>(in.n)));
-    const size_t mask_bytes = static_cast<size_t>(mask_stride) * mask_args.planes;
+    const size_t mask_bytes = given_masks ? 0 : static_cast<size_t>(mask_stride) * mask_args.planes;
     const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, peak_bytes,
                             count_bytes, start_bytes, list_bytes, sorted_bytes, mask_bytes};
     constexpr int kParts = sizeof(sizes) / sizeof(sizes[0]);
@@ -1697,7 +1711,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.band_list = reinterpret_cast<const int32_t*>(space + at[7]);
     o.band_sorted = reinterpret_cast<const float2*>(space + at[8]);
     o.ordered = reinterpret_cast<const int32_t*>(space + at[6] + static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4);
-    o.masks = mask_args.planes ? reinterpret_cast<const uint8_t*>(space + at[9]) : nullptr;
+    o.masks = !mask_args.planes ? nullptr : given_masks ? in.given_masks : reinterpret_cast<const uint8_t*>(space + at[9]);
     o.mask_stride = mask_stride;
     o.grad = in.grad;
     hipStream_t s = in.stream;
@@ -1759,7 +1773,7 @@ int launch_owner_backward(const OwnerLaunch& in) {
     // every column's peak over each expert's records, the slice masks, then the owner pass
     const auto launch_peaks = [&]() {
         const int64_t peak_words = static_cast<int64_t>(in.experts) * L * F;
-        if (mask_args.planes) {   // the mask launch clears the peaks as well
+        if (mask_args.planes && !given_masks) {   // the mask launch clears the peaks as well
             mask_args.coords = in.coords;
             mask_args.masks = const_cast<uint8_t*>(o.masks);
             mask_args.peaks = peaks;

@@ -37,6 +37,9 @@ struct GridArgs {
     int paired;      // forward, fp16 F=2: 16-byte group loads (table 16-byte aligned, entries % 4 == 0)
     int stage_levels;   // forward, fp16 F=2: coarse levels read from an LDS copy of the expert's table
     int stage_entries;  // entries staged (multiple of 4)
+    uint8_t* masks;     // forward: the owner backward's slice masks written on the way (MaskPlan), or null
+    int64_t mask_stride;
+    int32_t mask_info[ODIE_MAX_LEVELS];   // level l: its mask plane | bits << 8, or -1
     DevLevel level[ODIE_MAX_LEVELS];
 };
 
@@ -101,8 +104,8 @@ __device__ inline uint32_t pick4(const uint4& v, uint32_t j) {
 }
 
 template <int F, bool HALF, int LMAX>
-__device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, const Elem<HALF>* table,
-                                  const uint32_t* staged, int64_t i) {
+__device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, const int32_t* mask_info,
+                                  const Elem<HALF>* table, const uint32_t* staged, int64_t i) {
     using T = Elem<HALF>;
     const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
     T vals[LMAX * F];
@@ -113,6 +116,18 @@ __device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, con
             uint32_t idx[4];
             float w[4];
             grid_corners(lv, p.x, p.y, idx, w);
+            if (a.masks) {
+                // the owner backward's slice mask of this level: the aligned blocks of 2^bits
+                // entries that the corners land in (the level-local indices it forms itself)
+                const int32_t info = __builtin_amdgcn_readfirstlane(mask_info[l]);
+                if (info >= 0) {
+                    const uint32_t bits = static_cast<uint32_t>(info) >> 8;
+                    uint32_t byte = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) byte |= 1u << (idx[k] >> bits);
+                    a.masks[static_cast<int64_t>(info & 0xff) * a.mask_stride + i] = static_cast<uint8_t>(byte);
+                }
+            }
             const T* t = table + static_cast<size_t>(lv.offset) * F;
             if constexpr (HALF && F == 2) {
                 // Corners (0,1) and (2,3) usually sit in one aligned 16-byte group of four
@@ -218,10 +233,12 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
     // levels' descriptors would be held in scalar registers across the whole unrolled row and
     // spilled, and every basic block of the row would reload them lane by lane.
     __shared__ DevLevel levels[LMAX];
+    __shared__ int32_t mask_info[LMAX];
     constexpr int kLevelWords = LMAX * static_cast<int>(sizeof(DevLevel) / 4);
     static_assert(kLevelWords <= kBlock, "one thread per descriptor word");
     if (static_cast<int>(threadIdx.x) < kLevelWords)
         reinterpret_cast<uint32_t*>(levels)[threadIdx.x] = reinterpret_cast<const uint32_t*>(a.level)[threadIdx.x];
+    if (static_cast<int>(threadIdx.x) < LMAX) mask_info[threadIdx.x] = a.mask_info[threadIdx.x];
     __syncthreads();
     const uint32_t block = a.remap ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
     int64_t begin = static_cast<int64_t>(block) * a.chunk;
@@ -248,7 +265,8 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
             for (int j = threadIdx.x; j < a.stage_entries / 4; j += kBlock) reinterpret_cast<uint4*>(staged)[j] = src[j];
             __syncthreads();
         }
-        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) encode_row<F, HALF, LMAX>(a, levels, table, staged, i);
+        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock)
+            encode_row<F, HALF, LMAX>(a, levels, mask_info, table, staged, i);
         begin = stop;
     }
 }
@@ -694,17 +712,57 @@ int set_grid_tuning(const std::string& key, int value) {
 
 using namespace odie;
 
-ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                               const void* params, int64_t expert_params, int param_dtype,
-                               const odie_grid_level* levels, int n_levels, int features,
-                               void* out, int out_width, uint64_t stream) {
+namespace {
+
+// The slice-mask plan that odie_grid_backward_adam_planes forms for this grid and batch under
+// the current tuning (the owner backward's own planning, asked for the plan alone).
+int mask_plan(int64_t n, int experts, int64_t expert_params, const GridArgs& a, int n_levels, int features,
+              MaskPlan& plan) {
+    const Tuning& t = tuning();
+    OwnerLaunch o{};
+    o.n = n;
+    o.experts = experts;
+    o.expert_params = expert_params;
+    o.n_levels = n_levels;
+    o.features = features;
+    o.levels = a.level;
+    o.lds_bytes = t.owner_lds_bytes;
+    o.remap = t.xcd_remap;
+    o.banded = t.banded;
+    o.masks = t.owner_masks;
+    o.split_target = t.split_target;
+    o.up_half = 1;
+    o.up_width = n_levels * features;
+    o.plan_out = &plan;
+    return launch_owner_backward(o);
+}
+
+// odie_grid_forward, writing the owner backward's slice masks on the way when `masks` is
+// non-null (mask_bytes long, at least odie_grid_mask_bytes).
+int grid_forward(const char* who, const float* coords, int64_t n, const int32_t* offsets, int experts,
+                 const void* params, int64_t expert_params, int param_dtype, const odie_grid_level* levels,
+                 int n_levels, int features, void* out, int out_width, uint8_t* masks, int64_t mask_bytes,
+                 uint64_t stream) {
     GridArgs a{};
-    if (validate_grid("odie_grid_forward", coords, n, offsets, experts, expert_params, levels, n_levels, features, a))
+    if (validate_grid(who, coords, n, offsets, experts, expert_params, levels, n_levels, features, a))
         return -1;
-    if (param_dtype != ODIE_F32 && param_dtype != ODIE_F16) return fail("odie_grid_forward: param_dtype must be 0 (fp32) or 1 (fp16)");
-    if (out_width < n_levels * features) return fail("odie_grid_forward: out_width is smaller than n_levels*features");
+    for (int l = 0; l < ODIE_MAX_LEVELS; ++l) a.mask_info[l] = -1;
+    if (masks && n > 0) {
+        MaskPlan plan;
+        if (mask_plan(n, experts, expert_params, a, n_levels, features, plan)) return -1;
+        if (plan.planes > 0) {
+            if (mask_bytes < plan.stride * plan.planes)
+                return fail(std::string(who) + ": masks is shorter than odie_grid_mask_bytes");
+            a.masks = masks;
+            a.mask_stride = plan.stride;
+            for (int p = 0; p < plan.planes; ++p) a.mask_info[plan.level[p]] = p | (plan.bits[p] << 8);
+        }
+    }
+    const std::string w(who);
+    if (param_dtype != ODIE_F32 && param_dtype != ODIE_F16) return fail(w + ": param_dtype must be 0 (fp32) or 1 (fp16)");
+    if (out_width < n_levels * features) return fail(w + ": out_width is smaller than n_levels*features");
     if (n == 0) return 0;
-    if (!params || !out) return fail("odie_grid_forward: params and out must be non-null");
+    if (!params || !out) return fail(w + ": params and out must be non-null");
     const bool half = param_dtype == ODIE_F16;
     const size_t elem = half ? 2 : 4;
     a.params = params;
@@ -744,12 +802,51 @@ ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* of
         a.chunk = 2 * static_cast<int64_t>(a.stage_entries) >= entries ? 1024 : 256;
     }
     a.vec_rows = (reinterpret_cast<uintptr_t>(out) % 16 == 0) && (out_width * elem) % 16 == 0;
-    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail("odie_grid_forward: coords must be 8-byte aligned");
+    if (reinterpret_cast<uintptr_t>(coords) % 8) return fail(w + ": coords must be 8-byte aligned");
     const uint32_t blocks = grid_blocks(n, a.chunk);
     const hipStream_t s = as_stream(stream);
     ODIE_GRID_DISPATCH(grid_forward_kernel, features, half, n_levels, blocks,
                        static_cast<size_t>(a.stage_entries) * 4, s, a);
-    return check_launch("odie_grid_forward");
+    return check_launch(who);
+}
+
+}  // namespace
+
+ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                               const void* params, int64_t expert_params, int param_dtype,
+                               const odie_grid_level* levels, int n_levels, int features,
+                               void* out, int out_width, uint64_t stream) {
+    return grid_forward("odie_grid_forward", coords, n, offsets, experts, params, expert_params, param_dtype, levels,
+                        n_levels, features, out, out_width, nullptr, 0, stream);
+}
+
+ODIE_API int64_t odie_grid_mask_bytes(int64_t n, int experts, int64_t expert_params,
+                                      const odie_grid_level* levels, int n_levels, int features) {
+    const std::string w("odie_grid_mask_bytes");
+    if (n < 0 || n > (int64_t{1} << 31) - 1) return fail(w + ": n must be within [0, 2^31-1]");
+    if (experts < 1) return fail(w + ": experts must be >= 1");
+    if (!levels) return fail(w + ": levels is null");
+    if (n_levels < 1 || n_levels > ODIE_MAX_LEVELS) return fail(w + ": n_levels must be within 1..32");
+    if (features != 1 && features != 2 && features != 4 && features != 8)
+        return fail(w + ": features per level must be 1, 2, 4 or 8");
+    GridArgs a{};
+    uint64_t entries = 0;
+    if (make_dev_levels("odie_grid_mask_bytes", levels, n_levels, a.level, entries)) return -1;
+    if (expert_params < static_cast<int64_t>(entries) * features)
+        return fail(w + ": expert_params is smaller than the levels' table");
+    if (n == 0) return 0;
+    MaskPlan plan;
+    if (mask_plan(n, experts, expert_params, a, n_levels, features, plan)) return -1;
+    return plan.stride * plan.planes;
+}
+
+ODIE_API int odie_grid_forward_masks(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                     const void* params, int64_t expert_params, int param_dtype,
+                                     const odie_grid_level* levels, int n_levels, int features, void* out,
+                                     int out_width, uint8_t* masks, int64_t mask_bytes, uint64_t stream) {
+    if (n > 0 && !masks && mask_bytes > 0) return fail("odie_grid_forward_masks: masks is null");
+    return grid_forward("odie_grid_forward_masks", coords, n, offsets, experts, params, expert_params, param_dtype,
+                        levels, n_levels, features, out, out_width, masks, mask_bytes, stream);
 }
 
 ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, int experts,
@@ -841,7 +938,8 @@ namespace {
 int backward_adam(const char* name, const float* coords, int64_t n, const int32_t* offsets, int experts,
                   const void* upstream, int up_dtype, int up_width, const uint32_t* planes, const float* blockmax,
                   int64_t expert_params, const odie_grid_level* levels, int n_levels, int features,
-                  const AdamStep* adam, float* gradient, int zero_first, hipStream_t s) {
+                  const AdamStep* adam, float* gradient, int zero_first, hipStream_t s,
+                  const uint8_t* masks = nullptr, int64_t mask_bytes = 0) {
     GridArgs a{};
     if (validate_grid(name, coords, n, offsets, experts, expert_params, levels, n_levels, features, a)) return -1;
     if (planes || blockmax) {
@@ -890,6 +988,8 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
     o.split_target = t.split_target;
     o.stream = s;
     o.adam = adam;
+    o.given_masks = masks;
+    o.given_mask_bytes = mask_bytes;
     return launch_owner_backward(o);
 }
 
@@ -938,6 +1038,23 @@ ODIE_API int odie_grid_backward_adam_planes(const float* coords, int64_t n, cons
         return -1;
     return grid_backward_adam_planes_internal(coords, n, offsets, experts, planes, blockmax, expert_params, levels,
                                               n_levels, features, adam, as_stream(stream));
+}
+
+ODIE_API int odie_grid_backward_adam_planes_masks(const float* coords, int64_t n, const int32_t* offsets,
+                                                  int experts, const uint32_t* planes, const float* blockmax,
+                                                  int64_t expert_params, const odie_grid_level* levels, int n_levels,
+                                                  int features, float* master, uint16_t* half_copy, float* m, float* v,
+                                                  uint32_t* steps, int variant, int64_t step, float lr, float beta1,
+                                                  float beta2, float eps, float loss_scale, const uint8_t* masks,
+                                                  int64_t mask_bytes, uint64_t stream) {
+    AdamStep adam;
+    if (make_adam_step("odie_grid_backward_adam_planes_masks", master, half_copy, m, v, steps, variant, step, lr,
+                       beta1, beta2, eps, loss_scale, true, adam))
+        return -1;
+    if (n > 0 && !masks && mask_bytes > 0) return fail("odie_grid_backward_adam_planes_masks: masks is null");
+    return backward_adam("odie_grid_backward_adam_planes_masks", coords, n, offsets, experts, nullptr, ODIE_F16, 0,
+                         planes, blockmax, expert_params, levels, n_levels, features, &adam, nullptr, 0,
+                         as_stream(stream), masks, mask_bytes);
 }
 
 ODIE_API int odie_grid_backward_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,

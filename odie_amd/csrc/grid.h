@@ -179,6 +179,17 @@ inline int make_dev_levels(const char* what, const odie_grid_level* levels, int 
 // Host-side description of one owner-computes backward launch (backward.hip).
 struct AdamStep;
 
+// The owner backward's slice masks: plane p (`stride` bytes, stride >= n) belongs to level
+// level[p], and its byte i has bit s set when a corner of coordinate i lands in the aligned block
+// s of 2^bits[p] entries of that level.
+constexpr int kMaxMaskPlanes = 16;
+struct MaskPlan {
+    int planes;
+    int level[kMaxMaskPlanes];
+    int bits[kMaxMaskPlanes];
+    int64_t stride;
+};
+
 struct OwnerLaunch {
     const float* coords;
     const int32_t* offsets;   // null for a single grid
@@ -202,6 +213,10 @@ struct OwnerLaunch {
     const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad
     const void* planes;       // non-null: upstream already level-major [n_levels][n][features]
     const float* blockmax;    // with planes: max |upstream| per 128-row record and level
+    MaskPlan* plan_out;       // non-null: only fill in the slice-mask plan (no launch, no workspace)
+    const uint8_t* given_masks;   // non-null: the slice masks, already written (by the forward) per
+                                  // the plan, given_mask_bytes long; else the backward forms them
+    int64_t given_mask_bytes;
 };
 int launch_owner_backward(const OwnerLaunch& launch);
 

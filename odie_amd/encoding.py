@@ -29,9 +29,20 @@ def _offsets_arg(offsets, experts, n):
     return offsets
 
 
+def grid_mask_bytes(n, levels, features, *, experts=1, expert_params):
+    """Bytes of the slice masks that grid_forward(masks=...) writes for the encode backward
+    (odie_grid_mask_bytes; 0 when the backward would use none)."""
+    size = _lib.library().odie_grid_mask_bytes(n, experts, expert_params, levels, len(levels), features)
+    if size < 0:
+        _lib.check(-1)
+    return size
+
+
 def grid_forward(coords, table, levels, features, *, offsets=None, experts=1, expert_params=None,
-                 width=None, out=None):
-    """Encode coords [N,2] into [N, width] features of the table's dtype."""
+                 width=None, out=None, masks=None):
+    """Encode coords [N,2] into [N, width] features of the table's dtype.  With masks (uint8,
+    at least grid_mask_bytes long) the forward also writes the encode backward's slice masks
+    (odie_grid_forward_masks)."""
     _check_coords(coords)
     if table.dtype not in _DTYPES or not table.is_cuda or not table.is_contiguous():
         raise ValueError('table must be a contiguous CUDA fp32 or fp16 tensor')
@@ -45,10 +56,18 @@ def grid_forward(coords, table, levels, features, *, offsets=None, experts=1, ex
         out = torch.empty((n, width), dtype=table.dtype, device=coords.device)
     elif out.dtype != table.dtype or out.shape != (n, width) or not out.is_contiguous():
         raise ValueError('out must be a contiguous [N, width] tensor of the table dtype')
-    _lib.check(_lib.library().odie_grid_forward(
+    if masks is None:
+        _lib.check(_lib.library().odie_grid_forward(
+            coords.data_ptr(), n, _lib.ptr(offsets), experts, table.data_ptr(), expert_params,
+            _DTYPES[table.dtype], levels, len(levels), features, out.data_ptr(), width,
+            _lib.stream_of(coords)))
+        return out
+    if masks.dtype != torch.uint8 or not masks.is_cuda or not masks.is_contiguous():
+        raise ValueError('masks must be a contiguous CUDA uint8 tensor')
+    _lib.check(_lib.library().odie_grid_forward_masks(
         coords.data_ptr(), n, _lib.ptr(offsets), experts, table.data_ptr(), expert_params,
         _DTYPES[table.dtype], levels, len(levels), features, out.data_ptr(), width,
-        _lib.stream_of(coords)))
+        _lib.ptr(masks), masks.numel(), _lib.stream_of(coords)))
     return out
 
 

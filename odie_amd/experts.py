@@ -9,7 +9,7 @@ import torch
 
 from . import _lib
 from .config import grid_levels
-from .encoding import grid_backward, grid_forward
+from .encoding import grid_backward, grid_forward, grid_mask_bytes
 
 
 def tile_bounds(size, regions):
@@ -137,9 +137,16 @@ class ExpertGrid:
         self.width = len(self.levels) * self.features
         self.table = torch.zeros(experts * self.expert_params, dtype=dtype, device=device)
 
-    def forward(self, coords, offsets, out=None):
+    def forward(self, coords, offsets, out=None, masks=None):
+        """Features [N, width]; with masks (uint8, at least mask_bytes(N)) also the encode
+        backward's slice masks, for backward_adam_planes(masks=...)."""
         return grid_forward(coords, self.table, self.levels, self.features, offsets=offsets,
-                            experts=self.experts, expert_params=self.expert_params, width=self.width, out=out)
+                            experts=self.experts, expert_params=self.expert_params, width=self.width, out=out,
+                            masks=masks)
+
+    def mask_bytes(self, n):
+        """Bytes of the slice masks forward(masks=...) writes for a batch of n coordinates."""
+        return grid_mask_bytes(n, self.levels, self.features, experts=self.experts, expert_params=self.expert_params)
 
     def backward(self, coords, offsets, upstream, gradient=None, accumulate=False):
         return grid_backward(coords, upstream, self.levels, self.features, offsets=offsets, experts=self.experts,
@@ -195,19 +202,31 @@ class ExpertGrid:
             gradient.data_ptr(), 0 if accumulate else 1, _lib.stream_of(coords)))
         return gradient
 
-    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0):
+    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0, masks=None):
         """backward_adam with the fp16 upstream given as Decoder.train_planes writes it (planes
-        int32 [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same update, bit for bit."""
+        int32 [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same update, bit for bit.
+        With masks (written by forward(masks=...) on the same coords and offsets, no tuning change
+        in between) the backward reads the slice masks instead of forming them."""
         from .encoding import _offsets_arg
         self._check_planes(coords, planes, blockmax)
         n = coords.shape[0]
         if optimizer.master.numel() != self.experts * self.expert_params:
             raise ValueError('the optimizer must own this table\'s fp32 master')
         offsets = _offsets_arg(offsets, self.experts, n)
+        if masks is not None and (masks.dtype != torch.uint8 or not masks.is_cuda or not masks.is_contiguous()):
+            raise ValueError('masks must be a contiguous CUDA uint8 tensor')
         optimizer.step_count += 1
-        _lib.check(_lib.library().odie_grid_backward_adam_planes(
+        if masks is None:
+            _lib.check(_lib.library().odie_grid_backward_adam_planes(
+                coords.data_ptr(), n, _lib.ptr(offsets), self.experts, planes.data_ptr(), blockmax.data_ptr(),
+                self.expert_params, self.levels, len(self.levels), self.features, optimizer.master.data_ptr(),
+                _lib.ptr(optimizer.half_copy), optimizer.m.data_ptr(), optimizer.v.data_ptr(),
+                _lib.ptr(optimizer.steps), optimizer.variant_code, optimizer.step_count, optimizer.lr,
+                optimizer.betas[0], optimizer.betas[1], optimizer.eps, float(loss_scale), _lib.stream_of(coords)))
+            return
+        _lib.check(_lib.library().odie_grid_backward_adam_planes_masks(
             coords.data_ptr(), n, _lib.ptr(offsets), self.experts, planes.data_ptr(), blockmax.data_ptr(),
             self.expert_params, self.levels, len(self.levels), self.features, optimizer.master.data_ptr(),
             _lib.ptr(optimizer.half_copy), optimizer.m.data_ptr(), optimizer.v.data_ptr(), _lib.ptr(optimizer.steps),
             optimizer.variant_code, optimizer.step_count, optimizer.lr, optimizer.betas[0], optimizer.betas[1],
-            optimizer.eps, float(loss_scale), _lib.stream_of(coords)))
+            optimizer.eps, float(loss_scale), masks.data_ptr(), masks.numel(), _lib.stream_of(coords)))

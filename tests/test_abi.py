@@ -55,6 +55,25 @@ def test_grid_forward_rejects_bad_arguments(native, change, message):
     assert message in native.odie_error().decode()
 
 
+def test_grid_mask_bytes_follows_the_owner_plan(native):
+    """odie_grid_mask_bytes plans on the host: whole planes of n rounded up to 256 bytes for a
+    grid whose hashed levels the owner cuts into masked blocks (64 experts of 2^16-entry levels),
+    none for tables that fit one slice; and a forward given fewer bytes refuses before launching."""
+    levels, entries = grid_levels(dict(n_levels=16, base_resolution=16, log2_hashmap_size=16, per_level_scale=1.38))
+    n = (1 << 22) - 5
+    stride = (n + 255) // 256 * 256
+    size = native.odie_grid_mask_bytes(n, 64, entries * 2, levels, 16, 2)
+    assert size > 0 and size % stride == 0 and size // stride <= 16
+    assert native.odie_grid_mask_bytes(0, 64, entries * 2, levels, 16, 2) == 0
+    small, small_entries = _levels()
+    assert native.odie_grid_mask_bytes(4096, 1, small_entries * 2, small, 4, 2) == 0
+    assert native.odie_grid_mask_bytes(16, 1, small_entries * 2, small, 4, 3) == -1
+    assert 'features per level' in native.odie_error().decode()
+    code = native.odie_grid_forward_masks(8, n, 8, 64, 8, entries * 2, 1, levels, 16, 2, 16, 32, 8, size - 1, 0)
+    assert code == -1
+    assert 'shorter than odie_grid_mask_bytes' in native.odie_error().decode()
+
+
 def test_levels_must_be_contiguous(native):
     levels, entries = _levels()
     levels[2].offset += 8
