@@ -16,6 +16,9 @@ namespace odie {
 namespace {
 
 constexpr int kBlock = 256;
+// Word 3 of a raw buffer resource on CDNA (gfx9 layout): DATA_FORMAT 32 in bits 15..18 (a zero
+// data format would make untyped buffer loads return zero), the rest (swizzle, index stride) 0.
+constexpr int kRawBufferWord3 = 0x00020000;
 
 struct GridArgs {
     const float* coords;
@@ -105,7 +108,8 @@ __device__ inline uint32_t pick4(const uint4& v, uint32_t j) {
 
 template <int F, bool HALF, int LMAX>
 __device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, const int32_t* mask_info,
-                                  const Elem<HALF>* table, const uint32_t* staged, int64_t i) {
+                                  const Elem<HALF>* table, __amdgpu_buffer_rsrc_t entries_rsrc,
+                                  const uint32_t* staged, int64_t i) {
     using T = Elem<HALF>;
     const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
     T vals[LMAX * F];
@@ -139,6 +143,25 @@ __device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, con
                     // coarse level staged in LDS by the block
 #pragma unroll
                     for (int k = 0; k < 4; ++k) g[k] = staged[lv.offset + idx[k]];
+                } else if (!lv.hashed) {
+                    // dense: corners (x, y) and (x+1, y) are adjacent entries (but where the index
+                    // wraps at the level's end), so one 8-byte load fetches both: two vector
+                    // memory instructions per level instead of four.  A raw buffer load over the
+                    // expert's table takes the 4-byte aligned offset as one dwordx2 (a global
+                    // load at that alignment is split in two).
+                    const uint32_t* entries = reinterpret_cast<const uint32_t*>(t);
+#pragma unroll
+                    for (int k = 0; k < 4; k += 2) {
+                        if (idx[k + 1] == idx[k] + 1u) {
+                            const auto two =
+                                __builtin_amdgcn_raw_buffer_load_b64(entries_rsrc, (lv.offset + idx[k]) * 4u, 0, 0);
+                            g[k] = two[0];
+                            g[k + 1] = two[1];
+                        } else {
+                            g[k] = entries[idx[k]];
+                            g[k + 1] = entries[idx[k + 1]];
+                        }
+                    }
                 } else if (a.paired) {
                     const uint32_t* entries = reinterpret_cast<const uint32_t*>(table);
 #pragma unroll
@@ -258,6 +281,17 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
         const int e = expert_at(a, begin);
         const int64_t stop = segment_end(a, e, begin, end);
         const Elem<HALF>* table = reinterpret_cast<const Elem<HALF>*>(a.params) + static_cast<size_t>(e) * a.expert_params;
+        // the expert's table as a raw buffer (scalar registers; out-of-range offsets read 0).
+        // readfirstlane returns an int: each half goes back through uint32_t, so that the low
+        // half is not sign-extended over the high one when bit 31 of the address is set.
+        const uint64_t at = reinterpret_cast<uint64_t>(table);
+        const uint32_t at_hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(at >> 32)));
+        const uint32_t at_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(at)));
+        const uint64_t base = (static_cast<uint64_t>(at_hi) << 32) | at_lo;
+        const uint64_t bytes = static_cast<uint64_t>(a.expert_params) * sizeof(Elem<HALF>);
+        const __amdgpu_buffer_rsrc_t entries_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(base), 0, static_cast<int>(bytes < 0xffffffffull ? bytes : 0xffffffffull),
+            kRawBufferWord3);
         if (a.stage_levels > 0) {
             // Stage the expert's coarse levels (fp16 x2 entries as dwords) in LDS.
             __syncthreads();
@@ -266,7 +300,7 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
             __syncthreads();
         }
         for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock)
-            encode_row<F, HALF, LMAX>(a, levels, mask_info, table, staged, i);
+            encode_row<F, HALF, LMAX>(a, levels, mask_info, table, entries_rsrc, staged, i);
         begin = stop;
     }
 }
