@@ -311,11 +311,14 @@ def single_expert_steps(steps):
     """The single-expert workload: one 16-level x 2-feature fp16 hash grid (2^19-entry tables,
     base 16, scale 1.38, 5,487,024 parameters), 2^22 coordinates uniform in [0,1)^2 (seed 0), an
     upstream [2^22, 32] of N(0,1) rounded to fp16; forward encode and the backward scatter into
-    a zeroed fp32 gradient, timed with events on the stream they run on."""
+    a zeroed fp32 gradient, timed with events on the stream they run on.  The pair goes through
+    the forward-to-backward handoff (odie_grid_forward_handoff / odie_grid_backward_handoff): the
+    forward builds the owner's band lists and walks the coordinates in band order, and the
+    backward reads the lists instead of building them."""
     import torch
     from odie_amd import synth
     from odie_amd.config import grid_levels
-    from odie_amd.encoding import grid_backward, grid_forward
+    from odie_amd.encoding import grid_backward, grid_forward, grid_handoff_bytes
     levels, entries = grid_levels(C2_ENCODING)
     n = N_COORDS
     table = torch.from_numpy(synth.table(0, 2 * entries)).cuda().half()
@@ -323,17 +326,19 @@ def single_expert_steps(steps):
     upstream = torch.from_numpy(synth.upstream(0, n, 32)).cuda()
     out = torch.empty((n, 32), dtype=torch.float16, device='cuda')
     gradient = torch.empty(2 * entries, dtype=torch.float32, device='cuda')
+    size = grid_handoff_bytes(n, levels, 2, expert_params=2 * entries)
+    handoff = torch.empty(max(size, 1), dtype=torch.uint8, device='cuda') if size > 0 else None
     stream = torch.cuda.current_stream()
     for _ in range(3):
-        grid_forward(xy, table, levels, 2, out=out)
-        grid_backward(xy, upstream, levels, 2, expert_params=2 * entries, gradient=gradient)
+        grid_forward(xy, table, levels, 2, out=out, handoff=handoff)
+        grid_backward(xy, upstream, levels, 2, expert_params=2 * entries, gradient=gradient, handoff=handoff)
     marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     for a, b, c in marks:
         a.record(stream)
-        grid_forward(xy, table, levels, 2, out=out)
+        grid_forward(xy, table, levels, 2, out=out, handoff=handoff)
         b.record(stream)
-        grid_backward(xy, upstream, levels, 2, expert_params=2 * entries, gradient=gradient)
+        grid_backward(xy, upstream, levels, 2, expert_params=2 * entries, gradient=gradient, handoff=handoff)
         c.record(stream)
     torch.cuda.synchronize()
     forward = sum(a.elapsed_time(b) for a, b, _ in marks) / steps

@@ -116,34 +116,41 @@ int odie_grid_backward_adam_planes(const float* coords, int64_t n, const int32_t
                                    int64_t step, float lr, float beta1, float beta2, float eps, float loss_scale,
                                    uint64_t stream);
 
-/* Slice masks carried from the encode forward to the encode backward.  No counterpart in the
- * reference: a split of this library's owner backward, for training steps that run
- * odie_grid_forward and then odie_grid_backward_adam_planes on the same coordinates.  The
- * backward's unbanded hashed slices walk only the coordinates whose corners reach them; it
- * forms a byte per (coordinate, such level) itself in a pass over the coordinates, which the
- * forward can write instead, since it forms every corner index already.
+/* A handoff from the encode forward to the encode backward of the same batch.  No counterpart
+ * in the reference: a split of this library's owner backward, for steps that run the encode
+ * forward and then the backward on the same coordinates.  From its own plan for the batch the
+ * backward would form, in passes over the coordinates, either the slice masks its unbanded hashed
+ * slices walk by (a byte per coordinate and such level) or the band lists its banded passes walk
+ * (the coordinates sorted into 2047 y-bands per expert).  The forward can form them instead: it
+ * writes the masks as it forms every corner index, or builds the lists first and then walks the
+ * coordinates in band order itself, reading the tables with locality (its rows still land at
+ * their own indices).  Either way the backward skips that work.
  *
- * odie_grid_mask_bytes: the bytes of that mask buffer for this batch and grid under the
- * current tuning (0 when the backward would use no masks; -1 on invalid arguments).
- * odie_grid_forward_masks: odie_grid_forward that also writes the masks (mask_bytes at least
- * odie_grid_mask_bytes; masks may be null when that is 0).
- * odie_grid_backward_adam_planes_masks: odie_grid_backward_adam_planes that reads those masks
- * instead of forming them: the same update, bit for bit, when they were written by
- * odie_grid_forward_masks for the same coords, n, offsets, experts and levels, with no
- * odie_set_tuning call in between. */
-int64_t odie_grid_mask_bytes(int64_t n, int experts, int64_t expert_params, const odie_grid_level* levels,
-                             int n_levels, int features);
-int odie_grid_forward_masks(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                            const void* params, int64_t expert_params, int param_dtype,
-                            const odie_grid_level* levels, int n_levels, int features, void* out, int out_width,
-                            uint8_t* masks, int64_t mask_bytes, uint64_t stream);
-int odie_grid_backward_adam_planes_masks(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                                         const uint32_t* planes, const float* blockmax, int64_t expert_params,
-                                         const odie_grid_level* levels, int n_levels, int features, float* master,
-                                         uint16_t* half_copy, float* m, float* v, uint32_t* steps, int variant,
-                                         int64_t step, float lr, float beta1, float beta2, float eps,
-                                         float loss_scale, const uint8_t* masks, int64_t mask_bytes,
-                                         uint64_t stream);
+ * odie_grid_handoff_bytes: the handoff buffer's bytes for this batch and grid under the current
+ * tuning (0 when the backward would take nothing; -1 on invalid arguments).
+ * odie_grid_forward_handoff: odie_grid_forward that also fills the handoff (handoff_bytes at
+ * least odie_grid_handoff_bytes; handoff may be null when that is 0).  Same features, bit for bit.
+ * odie_grid_backward_handoff / odie_grid_backward_adam_planes_handoff: odie_grid_backward /
+ * odie_grid_backward_adam_planes reading that handoff instead of forming it: the same gradient
+ * or update, bit for bit, when it was filled by odie_grid_forward_handoff for the same coords,
+ * n, offsets, experts and levels, with no odie_set_tuning call in between. */
+int64_t odie_grid_handoff_bytes(int64_t n, int experts, int64_t expert_params, const odie_grid_level* levels,
+                                int n_levels, int features);
+int odie_grid_forward_handoff(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                              const void* params, int64_t expert_params, int param_dtype,
+                              const odie_grid_level* levels, int n_levels, int features, void* out, int out_width,
+                              void* handoff, int64_t handoff_bytes, uint64_t stream);
+int odie_grid_backward_handoff(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                               const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                               const odie_grid_level* levels, int n_levels, int features, float* gradient,
+                               int zero_first, const void* handoff, int64_t handoff_bytes, uint64_t stream);
+int odie_grid_backward_adam_planes_handoff(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                           const uint32_t* planes, const float* blockmax, int64_t expert_params,
+                                           const odie_grid_level* levels, int n_levels, int features,
+                                           float* master, uint16_t* half_copy, float* m, float* v, uint32_t* steps,
+                                           int variant, int64_t step, float lr, float beta1, float beta2, float eps,
+                                           float loss_scale, const void* handoff, int64_t handoff_bytes,
+                                           uint64_t stream);
 
 /* Launch-shape knobs of the encode kernels, for measurement sweeps; no counterpart in the
  * reference.  Keys: "forward_chunk", "backward_chunk" (coordinates per block, multiples of

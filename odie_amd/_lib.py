@@ -32,11 +32,12 @@ SIGNATURES = {
     'odie_grid_backward_planes': ([_P, _I64, _P, _I, _P, _P, _I64, _P, _I, _I, _P, _I, _U64], _I),
     'odie_set_tuning': ([C.c_char_p, _I], _I),
     'odie_grid_forward': ([_P, _I64, _P, _I, _P, _I64, _I, _P, _I, _I, _P, _I, _U64], _I),
-    'odie_grid_mask_bytes': ([_I64, _I, _I64, _P, _I, _I], _I64),
-    'odie_grid_forward_masks': ([_P, _I64, _P, _I, _P, _I64, _I, _P, _I, _I, _P, _I, _P, _I64, _U64], _I),
-    'odie_grid_backward_adam_planes_masks': ([_P, _I64, _P, _I, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _I,
-                                              _I64, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float, _P, _I64,
-                                              _U64], _I),
+    'odie_grid_handoff_bytes': ([_I64, _I, _I64, _P, _I, _I], _I64),
+    'odie_grid_forward_handoff': ([_P, _I64, _P, _I, _P, _I64, _I, _P, _I, _I, _P, _I, _P, _I64, _U64], _I),
+    'odie_grid_backward_handoff': ([_P, _I64, _P, _I, _P, _I, _I, _I64, _P, _I, _I, _P, _I, _P, _I64, _U64], _I),
+    'odie_grid_backward_adam_planes_handoff': ([_P, _I64, _P, _I, _P, _P, _I64, _P, _I, _I, _P, _P, _P, _P, _P,
+                                                _I, _I64, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float,
+                                                _P, _I64, _U64], _I),
     'odie_grid_backward': ([_P, _I64, _P, _I, _P, _I, _I, _I64, _P, _I, _I, _P, _I, _U64], _I),
     'odie_packed_forward': ([_P, _I64, _P, _I64, _P, _I, _P, _P, _P, _I, _P, _P, _U64], _I),
     'odie_packed_backward': ([_P, _I64, _P, _I, _P, _I, _P, _P, _P, _P, _I64, _U64], _I),

@@ -1467,6 +1467,34 @@ double band_coverage(const DevLevel& lv, int64_t entries, int64_t slices, int ro
 
 }  // namespace
 
+// The band lists of every expert's coordinates (count, per-slot scan, starts, place) on in.stream.
+int build_band_lists(const OwnerLaunch& in, int parts, int32_t* counts, int32_t* start, int32_t* list, float2* sorted,
+                     int32_t* ordered) {
+    BandArgs b{};
+    b.coords = in.coords;
+    b.offsets = in.offsets;
+    b.n = in.n;
+    b.experts = in.experts;
+    b.parts = parts;
+    b.counts = counts;
+    b.start = start;
+    b.list = list;
+    b.sorted = sorted;
+    b.ordered = ordered;
+    const uint32_t blocks = round_up(static_cast<uint32_t>(in.experts) * parts, kXcds);
+    int group = 1;
+    while (group < parts && group < 64) group <<= 1;
+    const int per = (parts + group - 1) / group;
+    const int64_t column_waves = static_cast<int64_t>(in.experts) * kBandSlots / (64 / group);
+    const uint32_t column_blocks = static_cast<uint32_t>((column_waves + kWaves - 1) / kWaves);
+    hipStream_t s = in.stream;
+    band_kernel<false><<<blocks, kBandBlock, 0, s>>>(b);
+    band_columns_kernel<<<column_blocks, kBandBlock, 0, s>>>(b, group, per);
+    band_start_kernel<<<static_cast<uint32_t>(in.experts), kBandBlock, 0, s>>>(b);
+    band_kernel<true><<<blocks, kBandBlock, 0, s>>>(b);
+    return check_launch("owner band lists");
+}
+
 int launch_owner_backward(const OwnerLaunch& in) {
     const int F = in.features;
     const int L = in.n_levels;
@@ -1558,21 +1586,6 @@ int launch_owner_backward(const OwnerLaunch& in) {
         }
     }
     const int64_t mask_stride = (in.n + 255) / 256 * 256;
-    if (in.plan_out) {
-        MaskPlan& plan = *in.plan_out;
-        plan = MaskPlan{};
-        plan.planes = mask_args.planes;
-        plan.stride = mask_stride;
-        for (int l = 0; l < L; ++l)
-            if (o.mask_plane[l] >= 0) {
-                plan.level[o.mask_plane[l]] = l;
-                plan.bits[o.mask_plane[l]] = mask_args.bits[o.mask_plane[l]];
-            }
-        return 0;
-    }
-    const bool given_masks = in.given_masks && mask_args.planes > 0;
-    if (given_masks && in.given_mask_bytes < mask_stride * mask_args.planes)
-        return fail("odie_grid_backward: the given slice masks are shorter than the plan's planes");
     o.ring_at = static_cast<int>(shmem - kRingBytes);
     int passes = group > 0 ? 1 : 0;
     for (int l = 0; l < L; ++l) {
@@ -1687,9 +1700,38 @@ int launch_owner_backward(const OwnerLaunch& in) {
     const size_t start_bytes = lists ? align(static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4 + 4) : 0;
     const size_t list_bytes = lists ? align(static_cast<size_t>(in.n) * 4) : 0;
     const size_t sorted_bytes = lists ? align(static_cast<size_t>(in.n) * 8) : 0;
+    // the handoff a forward can fill for this pass: the band lists (starts and the ordered word,
+    // list, sorted), or the slice masks (masks are planned only for unbanded passes)
+    const int64_t list_at = static_cast<int64_t>(start_bytes);
+    const int64_t sorted_at = list_at + static_cast<int64_t>(list_bytes);
+    const int64_t handoff_bytes = lists ? sorted_at + static_cast<int64_t>(sorted_bytes) : mask_stride * mask_args.planes;
+    if (in.plan_out) {
+        HandoffPlan& plan = *in.plan_out;
+        plan = HandoffPlan{};
+        plan.planes = mask_args.planes;
+        plan.stride = mask_stride;
+        for (int l = 0; l < L; ++l)
+            if (o.mask_plane[l] >= 0) {
+                plan.level[o.mask_plane[l]] = l;
+                plan.bits[o.mask_plane[l]] = mask_args.bits[o.mask_plane[l]];
+            }
+        plan.lists = lists ? 1 : 0;
+        plan.parts = parts;
+        plan.ordered_at = static_cast<int64_t>(in.experts) * (kBandSlots + 1) * 4;
+        plan.list_at = list_at;
+        plan.sorted_at = sorted_at;
+        plan.bytes = handoff_bytes;
+        return 0;
+    }
+    const bool handed = in.handoff != nullptr && handoff_bytes > 0;
+    if (handed && in.handoff_bytes < handoff_bytes)
+        return fail("odie_grid_backward: the handoff buffer is shorter than the plan's (odie_grid_handoff_bytes)");
+    const bool given_masks = handed && !lists;
+    const bool given_lists = handed && lists;
     const size_t mask_bytes = given_masks ? 0 : static_cast<size_t>(mask_stride) * mask_args.planes;
     const size_t sizes[] = {planes_bytes, max_bytes, partial_bytes, partial64_bytes, peak_bytes,
-                            count_bytes, start_bytes, list_bytes, sorted_bytes, mask_bytes};
+                            given_lists ? 0 : count_bytes, given_lists ? 0 : start_bytes,
+                            given_lists ? 0 : list_bytes, given_lists ? 0 : sorted_bytes, mask_bytes};
     constexpr int kParts = sizeof(sizes) / sizeof(sizes[0]);
     size_t at[kParts], sum = 0;
     for (int k = 0; k < kParts; ++k) {
@@ -1707,39 +1749,21 @@ int launch_owner_backward(const OwnerLaunch& in) {
     o.partial_floats = split_floats;
     uint32_t* peaks = reinterpret_cast<uint32_t*>(space + at[4]);
     o.peaks = peaks;
-    o.band_start = reinterpret_cast<const int32_t*>(space + at[6]);
-    o.band_list = reinterpret_cast<const int32_t*>(space + at[7]);
-    o.band_sorted = reinterpret_cast<const float2*>(space + at[8]);
-    o.ordered = reinterpret_cast<const int32_t*>(space + at[6] + static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4);
-    o.masks = !mask_args.planes ? nullptr : given_masks ? in.given_masks : reinterpret_cast<const uint8_t*>(space + at[9]);
+    const char* lists_at = given_lists ? reinterpret_cast<const char*>(in.handoff) : space + at[6];
+    o.band_start = reinterpret_cast<const int32_t*>(lists_at);
+    o.band_list = reinterpret_cast<const int32_t*>(given_lists ? lists_at + list_at : space + at[7]);
+    o.band_sorted = reinterpret_cast<const float2*>(given_lists ? lists_at + sorted_at : space + at[8]);
+    o.ordered = reinterpret_cast<const int32_t*>(lists_at + static_cast<size_t>(in.experts) * (kBandSlots + 1) * 4);
+    o.masks = !mask_args.planes ? nullptr : given_masks ? in.handoff : reinterpret_cast<const uint8_t*>(space + at[9]);
     o.mask_stride = mask_stride;
     o.grad = in.grad;
     hipStream_t s = in.stream;
 
-    if (lists) {
-        BandArgs b{};
-        b.coords = in.coords;
-        b.offsets = in.offsets;
-        b.n = in.n;
-        b.experts = in.experts;
-        b.parts = parts;
-        b.counts = reinterpret_cast<int32_t*>(space + at[5]);
-        b.start = reinterpret_cast<int32_t*>(space + at[6]);
-        b.list = reinterpret_cast<int32_t*>(space + at[7]);
-        b.sorted = reinterpret_cast<float2*>(space + at[8]);
-        b.ordered = const_cast<int32_t*>(o.ordered);
-        const uint32_t blocks = round_up(static_cast<uint32_t>(in.experts) * parts, kXcds);
-        int group = 1;
-        while (group < parts && group < 64) group <<= 1;
-        const int per = (parts + group - 1) / group;
-        const int64_t column_waves = static_cast<int64_t>(in.experts) * kBandSlots / (64 / group);
-        const uint32_t column_blocks = static_cast<uint32_t>((column_waves + kWaves - 1) / kWaves);
-        band_kernel<false><<<blocks, kBandBlock, 0, s>>>(b);
-        band_columns_kernel<<<column_blocks, kBandBlock, 0, s>>>(b, group, per);
-        band_start_kernel<<<static_cast<uint32_t>(in.experts), kBandBlock, 0, s>>>(b);
-        band_kernel<true><<<blocks, kBandBlock, 0, s>>>(b);
-        if (check_launch("owner band lists")) return -1;
-    }
+    if (lists && !given_lists &&
+        build_band_lists(in, parts, reinterpret_cast<int32_t*>(space + at[5]), reinterpret_cast<int32_t*>(space + at[6]),
+                         reinterpret_cast<int32_t*>(space + at[7]), reinterpret_cast<float2*>(space + at[8]),
+                         const_cast<int32_t*>(o.ordered)))
+        return -1;
 
     // the backward's own transpose writes the planes in band-list order (read in order by every
     // pass) for a single expert; planes the caller hands over stay in index order, and so do
@@ -1827,6 +1851,17 @@ int launch_owner_backward(const OwnerLaunch& in) {
                                                                           in.expert_params, prefix);
     }
     return check_launch("odie_grid_backward");
+}
+
+int launch_band_lists(const OwnerLaunch& in, const HandoffPlan& plan, uint8_t* handoff) {
+    if (!plan.lists) return 0;
+    const size_t count_bytes = (static_cast<size_t>(in.experts) * plan.parts * kBandSlots * 4 + 255) / 256 * 256;
+    int32_t* counts = static_cast<int32_t*>(workspace(count_bytes, in.stream));
+    if (!counts) return -1;
+    return build_band_lists(in, plan.parts, counts, reinterpret_cast<int32_t*>(handoff),
+                            reinterpret_cast<int32_t*>(handoff + plan.list_at),
+                            reinterpret_cast<float2*>(handoff + plan.sorted_at),
+                            reinterpret_cast<int32_t*>(handoff + plan.ordered_at));
 }
 
 int launch_packed_owner(const float* coords, int64_t n, const uint16_t* upstream, int width, const int32_t* desc,

@@ -40,8 +40,11 @@ struct GridArgs {
     int paired;      // forward, fp16 F=2: 16-byte group loads (table 16-byte aligned, entries % 4 == 0)
     int stage_levels;   // forward, fp16 F=2: coarse levels read from an LDS copy of the expert's table
     int stage_entries;  // entries staged (multiple of 4)
-    uint8_t* masks;     // forward: the owner backward's slice masks written on the way (MaskPlan), or null
+    uint8_t* masks;     // forward: the owner backward's slice masks written on the way (HandoffPlan), or null
     int64_t mask_stride;
+    const int32_t* list;     // forward: walk the owner's band lists (list position j: coordinate list[j]
+    const float2* sorted;    // at sorted[j]; its row is written at list[j]) when *ordered, or null
+    const int32_t* ordered;
     int32_t mask_info[ODIE_MAX_LEVELS];   // level l: its mask plane | bits << 8, or -1
     DevLevel level[ODIE_MAX_LEVELS];
 };
@@ -106,12 +109,13 @@ __device__ inline uint32_t pick4(const uint4& v, uint32_t j) {
     return (j & 2u) ? high : low;
 }
 
+// Row `row` of the output from coordinate p (slot i of the walk: row i, or list[i] in band order;
+// the masks, written only in slot order, at i).
 template <int F, bool HALF, int LMAX>
 __device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, const int32_t* mask_info,
                                   const Elem<HALF>* table, __amdgpu_buffer_rsrc_t entries_rsrc,
-                                  const uint32_t* staged, int64_t i) {
+                                  const uint32_t* staged, int64_t i, float2 p, int64_t row_at) {
     using T = Elem<HALF>;
-    const float2 p = reinterpret_cast<const float2*>(a.coords)[i];
     T vals[LMAX * F];
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) {
@@ -218,7 +222,7 @@ __device__ inline void encode_row(const GridArgs& a, const DevLevel* levels, con
             for (int c = 0; c < F; ++c) vals[l * F + c] = T(0.0f);
         }
     }
-    T* row = reinterpret_cast<T*>(a.out) + static_cast<size_t>(i) * a.width;
+    T* row = reinterpret_cast<T*>(a.out) + static_cast<size_t>(row_at) * a.width;
     const int used = a.n_levels * F;
     if (a.vec_rows && (used * static_cast<int>(sizeof(T))) % 16 == 0) {
         constexpr int kPer = 16 / sizeof(T);
@@ -268,6 +272,10 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
     if (begin >= a.n) return;
     int64_t end = begin + a.chunk < a.n ? begin + a.chunk : a.n;
     extern __shared__ uint32_t staged[];
+    // band order when the lists are exact and cover every owned position: expert ranges in order
+    // from position 0 (each expert's list positions are then its own range, so a position's
+    // expert is the same either way)
+    const bool by_list = a.list && *a.ordered && (!a.offsets || a.offsets[0] <= 0);
     const int64_t owned = owned_end(a);
     for (int64_t i = (begin > owned ? begin : owned) + threadIdx.x; i < end; i += kBlock) {
         Elem<HALF>* row = reinterpret_cast<Elem<HALF>*>(a.out) + static_cast<size_t>(i) * a.width;
@@ -299,8 +307,12 @@ __global__ __launch_bounds__(kBlock) void grid_forward_kernel(GridArgs a) {
             for (int j = threadIdx.x; j < a.stage_entries / 4; j += kBlock) reinterpret_cast<uint4*>(staged)[j] = src[j];
             __syncthreads();
         }
-        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock)
-            encode_row<F, HALF, LMAX>(a, levels, mask_info, table, entries_rsrc, staged, i);
+        for (int64_t i = begin + threadIdx.x; i < stop; i += kBlock) {
+            const float2 p = by_list ? a.sorted[i] : reinterpret_cast<const float2*>(a.coords)[i];
+            const int64_t row_at = by_list ? static_cast<int64_t>(a.list[i]) : i;
+            if (row_at < 0 || row_at >= a.n) continue;   // (a list entry is always a coordinate index)
+            encode_row<F, HALF, LMAX>(a, levels, mask_info, table, entries_rsrc, staged, i, p, row_at);
+        }
         begin = stop;
     }
 }
@@ -748,12 +760,15 @@ using namespace odie;
 
 namespace {
 
-// The slice-mask plan that odie_grid_backward_adam_planes forms for this grid and batch under
-// the current tuning (the owner backward's own planning, asked for the plan alone).
-int mask_plan(int64_t n, int experts, int64_t expert_params, const GridArgs& a, int n_levels, int features,
-              MaskPlan& plan) {
+// The owner backward's launch for this grid and batch under the current tuning, as far as its
+// planning reads it.
+OwnerLaunch planning_launch(const float* coords, int64_t n, const int32_t* offsets, int experts, int64_t expert_params,
+                            const GridArgs& a, int n_levels, int features, hipStream_t stream) {
     const Tuning& t = tuning();
     OwnerLaunch o{};
+    o.coords = coords;
+    o.offsets = offsets;
+    o.stream = stream;
     o.n = n;
     o.experts = experts;
     o.expert_params = expert_params;
@@ -767,27 +782,36 @@ int mask_plan(int64_t n, int experts, int64_t expert_params, const GridArgs& a, 
     o.split_target = t.split_target;
     o.up_half = 1;
     o.up_width = n_levels * features;
+    return o;
+}
+
+// The handoff plan of the owner backward for this grid and batch (its own planning, asked for
+// the plan alone).
+int handoff_plan(int64_t n, int experts, int64_t expert_params, const GridArgs& a, int n_levels, int features,
+                 HandoffPlan& plan) {
+    OwnerLaunch o = planning_launch(nullptr, n, nullptr, experts, expert_params, a, n_levels, features, nullptr);
     o.plan_out = &plan;
     return launch_owner_backward(o);
 }
 
-// odie_grid_forward, writing the owner backward's slice masks on the way when `masks` is
-// non-null (mask_bytes long, at least odie_grid_mask_bytes).
+// odie_grid_forward, filling the owner backward's handoff on the way when `handoff` is non-null
+// (handoff_bytes long, at least odie_grid_handoff_bytes): the slice masks, written by the
+// forward kernel, or the band lists, built first and then walked by the forward kernel.
 int grid_forward(const char* who, const float* coords, int64_t n, const int32_t* offsets, int experts,
                  const void* params, int64_t expert_params, int param_dtype, const odie_grid_level* levels,
-                 int n_levels, int features, void* out, int out_width, uint8_t* masks, int64_t mask_bytes,
+                 int n_levels, int features, void* out, int out_width, uint8_t* handoff, int64_t handoff_bytes,
                  uint64_t stream) {
     GridArgs a{};
     if (validate_grid(who, coords, n, offsets, experts, expert_params, levels, n_levels, features, a))
         return -1;
     for (int l = 0; l < ODIE_MAX_LEVELS; ++l) a.mask_info[l] = -1;
-    if (masks && n > 0) {
-        MaskPlan plan;
-        if (mask_plan(n, experts, expert_params, a, n_levels, features, plan)) return -1;
+    HandoffPlan plan{};
+    if (handoff && n > 0) {
+        if (handoff_plan(n, experts, expert_params, a, n_levels, features, plan)) return -1;
+        if (plan.bytes > 0 && handoff_bytes < plan.bytes)
+            return fail(std::string(who) + ": handoff is shorter than odie_grid_handoff_bytes");
         if (plan.planes > 0) {
-            if (mask_bytes < plan.stride * plan.planes)
-                return fail(std::string(who) + ": masks is shorter than odie_grid_mask_bytes");
-            a.masks = masks;
+            a.masks = handoff;
             a.mask_stride = plan.stride;
             for (int p = 0; p < plan.planes; ++p) a.mask_info[plan.level[p]] = p | (plan.bits[p] << 8);
         }
@@ -839,6 +863,13 @@ int grid_forward(const char* who, const float* coords, int64_t n, const int32_t*
     if (reinterpret_cast<uintptr_t>(coords) % 8) return fail(w + ": coords must be 8-byte aligned");
     const uint32_t blocks = grid_blocks(n, a.chunk);
     const hipStream_t s = as_stream(stream);
+    if (plan.lists) {
+        const OwnerLaunch o = planning_launch(coords, n, a.offsets, experts, expert_params, a, n_levels, features, s);
+        if (launch_band_lists(o, plan, handoff)) return -1;
+        a.list = reinterpret_cast<const int32_t*>(handoff + plan.list_at);
+        a.sorted = reinterpret_cast<const float2*>(handoff + plan.sorted_at);
+        a.ordered = reinterpret_cast<const int32_t*>(handoff + plan.ordered_at);
+    }
     ODIE_GRID_DISPATCH(grid_forward_kernel, features, half, n_levels, blocks,
                        static_cast<size_t>(a.stage_entries) * 4, s, a);
     return check_launch(who);
@@ -854,9 +885,9 @@ ODIE_API int odie_grid_forward(const float* coords, int64_t n, const int32_t* of
                         n_levels, features, out, out_width, nullptr, 0, stream);
 }
 
-ODIE_API int64_t odie_grid_mask_bytes(int64_t n, int experts, int64_t expert_params,
-                                      const odie_grid_level* levels, int n_levels, int features) {
-    const std::string w("odie_grid_mask_bytes");
+ODIE_API int64_t odie_grid_handoff_bytes(int64_t n, int experts, int64_t expert_params,
+                                         const odie_grid_level* levels, int n_levels, int features) {
+    const std::string w("odie_grid_handoff_bytes");
     if (n < 0 || n > (int64_t{1} << 31) - 1) return fail(w + ": n must be within [0, 2^31-1]");
     if (experts < 1) return fail(w + ": experts must be >= 1");
     if (!levels) return fail(w + ": levels is null");
@@ -865,28 +896,32 @@ ODIE_API int64_t odie_grid_mask_bytes(int64_t n, int experts, int64_t expert_par
         return fail(w + ": features per level must be 1, 2, 4 or 8");
     GridArgs a{};
     uint64_t entries = 0;
-    if (make_dev_levels("odie_grid_mask_bytes", levels, n_levels, a.level, entries)) return -1;
+    if (make_dev_levels("odie_grid_handoff_bytes", levels, n_levels, a.level, entries)) return -1;
     if (expert_params < static_cast<int64_t>(entries) * features)
         return fail(w + ": expert_params is smaller than the levels' table");
     if (n == 0) return 0;
-    MaskPlan plan;
-    if (mask_plan(n, experts, expert_params, a, n_levels, features, plan)) return -1;
-    return plan.stride * plan.planes;
+    HandoffPlan plan;
+    if (handoff_plan(n, experts, expert_params, a, n_levels, features, plan)) return -1;
+    return plan.bytes;
 }
 
-ODIE_API int odie_grid_forward_masks(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                                     const void* params, int64_t expert_params, int param_dtype,
-                                     const odie_grid_level* levels, int n_levels, int features, void* out,
-                                     int out_width, uint8_t* masks, int64_t mask_bytes, uint64_t stream) {
-    if (n > 0 && !masks && mask_bytes > 0) return fail("odie_grid_forward_masks: masks is null");
-    return grid_forward("odie_grid_forward_masks", coords, n, offsets, experts, params, expert_params, param_dtype,
-                        levels, n_levels, features, out, out_width, masks, mask_bytes, stream);
+ODIE_API int odie_grid_forward_handoff(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                       const void* params, int64_t expert_params, int param_dtype,
+                                       const odie_grid_level* levels, int n_levels, int features, void* out,
+                                       int out_width, void* handoff, int64_t handoff_bytes, uint64_t stream) {
+    if (n > 0 && !handoff && handoff_bytes > 0) return fail("odie_grid_forward_handoff: handoff is null");
+    return grid_forward("odie_grid_forward_handoff", coords, n, offsets, experts, params, expert_params, param_dtype,
+                        levels, n_levels, features, out, out_width, static_cast<uint8_t*>(handoff), handoff_bytes,
+                        stream);
 }
 
-ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, int experts,
-                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
-                                const odie_grid_level* levels, int n_levels, int features,
-                                float* gradient, int zero_first, uint64_t stream) {
+namespace {
+
+// odie_grid_backward, reading the forward's handoff (odie_grid_forward_handoff) when non-null.
+int grid_backward(const float* coords, int64_t n, const int32_t* offsets, int experts, const void* upstream,
+                  int up_dtype, int up_width, int64_t expert_params, const odie_grid_level* levels, int n_levels,
+                  int features, float* gradient, int zero_first, const uint8_t* handoff, int64_t handoff_bytes,
+                  uint64_t stream) {
     GridArgs a{};
     if (validate_grid("odie_grid_backward", coords, n, offsets, experts, expert_params, levels, n_levels, features, a))
         return -1;
@@ -927,6 +962,8 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
         o.masks = t.owner_masks;
         o.split_target = t.split_target;
         o.stream = s;
+        o.handoff = handoff;
+        o.handoff_bytes = handoff_bytes;
         return launch_owner_backward(o);
     }
     if (zero_first && launch_fill_zero(gradient, total, s)) return -1;
@@ -957,6 +994,16 @@ ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* o
     return check_launch("odie_grid_backward");
 }
 
+}  // namespace
+
+ODIE_API int odie_grid_backward(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                const odie_grid_level* levels, int n_levels, int features,
+                                float* gradient, int zero_first, uint64_t stream) {
+    return grid_backward(coords, n, offsets, experts, upstream, up_dtype, up_width, expert_params, levels, n_levels,
+                         features, gradient, zero_first, nullptr, 0, stream);
+}
+
 // Encode backward fused with the optimizer step: every parameter's gradient is formed in
 // LDS by the owner-computes backward and the Adam update (adam.h) is applied where it is
 // flushed, so the gradient never reaches HBM.  Same result as odie_grid_backward followed
@@ -973,7 +1020,7 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
                   const void* upstream, int up_dtype, int up_width, const uint32_t* planes, const float* blockmax,
                   int64_t expert_params, const odie_grid_level* levels, int n_levels, int features,
                   const AdamStep* adam, float* gradient, int zero_first, hipStream_t s,
-                  const uint8_t* masks = nullptr, int64_t mask_bytes = 0) {
+                  const uint8_t* handoff = nullptr, int64_t handoff_bytes = 0) {
     GridArgs a{};
     if (validate_grid(name, coords, n, offsets, experts, expert_params, levels, n_levels, features, a)) return -1;
     if (planes || blockmax) {
@@ -1022,8 +1069,8 @@ int backward_adam(const char* name, const float* coords, int64_t n, const int32_
     o.split_target = t.split_target;
     o.stream = s;
     o.adam = adam;
-    o.given_masks = masks;
-    o.given_mask_bytes = mask_bytes;
+    o.handoff = handoff;
+    o.handoff_bytes = handoff_bytes;
     return launch_owner_backward(o);
 }
 
@@ -1074,21 +1121,32 @@ ODIE_API int odie_grid_backward_adam_planes(const float* coords, int64_t n, cons
                                               n_levels, features, adam, as_stream(stream));
 }
 
-ODIE_API int odie_grid_backward_adam_planes_masks(const float* coords, int64_t n, const int32_t* offsets,
-                                                  int experts, const uint32_t* planes, const float* blockmax,
-                                                  int64_t expert_params, const odie_grid_level* levels, int n_levels,
-                                                  int features, float* master, uint16_t* half_copy, float* m, float* v,
-                                                  uint32_t* steps, int variant, int64_t step, float lr, float beta1,
-                                                  float beta2, float eps, float loss_scale, const uint8_t* masks,
-                                                  int64_t mask_bytes, uint64_t stream) {
+ODIE_API int odie_grid_backward_adam_planes_handoff(const float* coords, int64_t n, const int32_t* offsets,
+                                                    int experts, const uint32_t* planes, const float* blockmax,
+                                                    int64_t expert_params, const odie_grid_level* levels,
+                                                    int n_levels, int features, float* master, uint16_t* half_copy,
+                                                    float* m, float* v, uint32_t* steps, int variant, int64_t step,
+                                                    float lr, float beta1, float beta2, float eps, float loss_scale,
+                                                    const void* handoff, int64_t handoff_bytes, uint64_t stream) {
     AdamStep adam;
-    if (make_adam_step("odie_grid_backward_adam_planes_masks", master, half_copy, m, v, steps, variant, step, lr,
+    if (make_adam_step("odie_grid_backward_adam_planes_handoff", master, half_copy, m, v, steps, variant, step, lr,
                        beta1, beta2, eps, loss_scale, true, adam))
         return -1;
-    if (n > 0 && !masks && mask_bytes > 0) return fail("odie_grid_backward_adam_planes_masks: masks is null");
-    return backward_adam("odie_grid_backward_adam_planes_masks", coords, n, offsets, experts, nullptr, ODIE_F16, 0,
+    if (n > 0 && !handoff && handoff_bytes > 0) return fail("odie_grid_backward_adam_planes_handoff: handoff is null");
+    return backward_adam("odie_grid_backward_adam_planes_handoff", coords, n, offsets, experts, nullptr, ODIE_F16, 0,
                          planes, blockmax, expert_params, levels, n_levels, features, &adam, nullptr, 0,
-                         as_stream(stream), masks, mask_bytes);
+                         as_stream(stream), static_cast<const uint8_t*>(handoff), handoff_bytes);
+}
+
+ODIE_API int odie_grid_backward_handoff(const float* coords, int64_t n, const int32_t* offsets, int experts,
+                                        const void* upstream, int up_dtype, int up_width, int64_t expert_params,
+                                        const odie_grid_level* levels, int n_levels, int features, float* gradient,
+                                        int zero_first, const void* handoff, int64_t handoff_bytes,
+                                        uint64_t stream) {
+    if (n > 0 && !handoff && handoff_bytes > 0) return fail("odie_grid_backward_handoff: handoff is null");
+    // (with the atomics backward, tuning key backward_mode 0, the handoff goes unread)
+    return grid_backward(coords, n, offsets, experts, upstream, up_dtype, up_width, expert_params, levels, n_levels,
+                         features, gradient, zero_first, static_cast<const uint8_t*>(handoff), handoff_bytes, stream);
 }
 
 ODIE_API int odie_grid_backward_planes(const float* coords, int64_t n, const int32_t* offsets, int experts,

@@ -179,15 +179,24 @@ inline int make_dev_levels(const char* what, const odie_grid_level* levels, int 
 // Host-side description of one owner-computes backward launch (backward.hip).
 struct AdamStep;
 
-// The owner backward's slice masks: plane p (`stride` bytes, stride >= n) belongs to level
-// level[p], and its byte i has bit s set when a corner of coordinate i lands in the aligned block
-// s of 2^bits[p] entries of that level.
+// What the encode forward can hand the owner backward of the same batch (the handoff buffer),
+// from the owner's own plan: its slice masks when its passes are unbanded, or its band lists
+// when they are banded (else nothing, bytes 0).
+//   masks: plane p (`stride` bytes, stride >= n) belongs to level level[p]; its byte i has bit s
+//     set when a corner of coordinate i lands in the aligned block s of 2^bits[p] entries;
+//   lists: at byte 0 each expert's slot starts [experts][kBandSlots + 1] and the `ordered` word,
+//     at list_at the coordinate index of every list position [n] (int32), at sorted_at that
+//     coordinate's (x, y) [n] (float2); the band kernels' counts go to the library's workspace.
 constexpr int kMaxMaskPlanes = 16;
-struct MaskPlan {
+struct HandoffPlan {
     int planes;
     int level[kMaxMaskPlanes];
     int bits[kMaxMaskPlanes];
     int64_t stride;
+    int lists;        // 1: band lists (and no masks)
+    int parts;        // band counting parts per expert
+    int64_t ordered_at, list_at, sorted_at;
+    int64_t bytes;    // the handoff buffer's length
 };
 
 struct OwnerLaunch {
@@ -213,12 +222,15 @@ struct OwnerLaunch {
     const AdamStep* adam;   // non-null: apply this optimizer step instead of writing grad
     const void* planes;       // non-null: upstream already level-major [n_levels][n][features]
     const float* blockmax;    // with planes: max |upstream| per 128-row record and level
-    MaskPlan* plan_out;       // non-null: only fill in the slice-mask plan (no launch, no workspace)
-    const uint8_t* given_masks;   // non-null: the slice masks, already written (by the forward) per
-                                  // the plan, given_mask_bytes long; else the backward forms them
-    int64_t given_mask_bytes;
+    HandoffPlan* plan_out;    // non-null: only fill in the handoff plan (no launch, no workspace)
+    const uint8_t* handoff;   // non-null: the handoff buffer, already filled (by the forward) per the
+                              // plan, handoff_bytes long; else the backward forms masks or lists itself
+    int64_t handoff_bytes;
 };
 int launch_owner_backward(const OwnerLaunch& launch);
+// The band lists of a banded plan into `handoff` (plan.lists), for the forward to walk and the
+// backward to reuse: the owner's own band kernels on in.coords / in.offsets.
+int launch_band_lists(const OwnerLaunch& in, const HandoffPlan& plan, uint8_t* handoff);
 
 // Owner-computes backward of packed xy planes (backward.hip): gradient [params] fp32, every
 // value written once.  upstream fp16 [n][width]; descriptors device [levels][8].

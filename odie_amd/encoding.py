@@ -29,20 +29,20 @@ def _offsets_arg(offsets, experts, n):
     return offsets
 
 
-def grid_mask_bytes(n, levels, features, *, experts=1, expert_params):
-    """Bytes of the slice masks that grid_forward(masks=...) writes for the encode backward
-    (odie_grid_mask_bytes; 0 when the backward would use none)."""
-    size = _lib.library().odie_grid_mask_bytes(n, experts, expert_params, levels, len(levels), features)
+def grid_handoff_bytes(n, levels, features, *, experts=1, expert_params):
+    """Bytes of the handoff that grid_forward(handoff=...) fills for the encode backward of the
+    same batch (odie_grid_handoff_bytes; 0 when the backward would take nothing)."""
+    size = _lib.library().odie_grid_handoff_bytes(n, experts, expert_params, levels, len(levels), features)
     if size < 0:
         _lib.check(-1)
     return size
 
 
 def grid_forward(coords, table, levels, features, *, offsets=None, experts=1, expert_params=None,
-                 width=None, out=None, masks=None):
-    """Encode coords [N,2] into [N, width] features of the table's dtype.  With masks (uint8,
-    at least grid_mask_bytes long) the forward also writes the encode backward's slice masks
-    (odie_grid_forward_masks)."""
+                 width=None, out=None, handoff=None):
+    """Encode coords [N,2] into [N, width] features of the table's dtype.  With handoff (uint8,
+    at least grid_handoff_bytes long) the forward also fills the encode backward's handoff
+    (odie_grid_forward_handoff: the slice masks or the band lists, by the backward's plan)."""
     _check_coords(coords)
     if table.dtype not in _DTYPES or not table.is_cuda or not table.is_contiguous():
         raise ValueError('table must be a contiguous CUDA fp32 or fp16 tensor')
@@ -56,24 +56,25 @@ def grid_forward(coords, table, levels, features, *, offsets=None, experts=1, ex
         out = torch.empty((n, width), dtype=table.dtype, device=coords.device)
     elif out.dtype != table.dtype or out.shape != (n, width) or not out.is_contiguous():
         raise ValueError('out must be a contiguous [N, width] tensor of the table dtype')
-    if masks is None:
+    if handoff is None:
         _lib.check(_lib.library().odie_grid_forward(
             coords.data_ptr(), n, _lib.ptr(offsets), experts, table.data_ptr(), expert_params,
             _DTYPES[table.dtype], levels, len(levels), features, out.data_ptr(), width,
             _lib.stream_of(coords)))
         return out
-    if masks.dtype != torch.uint8 or not masks.is_cuda or not masks.is_contiguous():
-        raise ValueError('masks must be a contiguous CUDA uint8 tensor')
-    _lib.check(_lib.library().odie_grid_forward_masks(
+    _check_handoff(handoff)
+    _lib.check(_lib.library().odie_grid_forward_handoff(
         coords.data_ptr(), n, _lib.ptr(offsets), experts, table.data_ptr(), expert_params,
         _DTYPES[table.dtype], levels, len(levels), features, out.data_ptr(), width,
-        _lib.ptr(masks), masks.numel(), _lib.stream_of(coords)))
+        handoff.data_ptr(), handoff.numel(), _lib.stream_of(coords)))
     return out
 
 
 def grid_backward(coords, upstream, levels, features, *, offsets=None, experts=1, expert_params,
-                  gradient=None, accumulate=False):
-    """Scatter upstream [N, width] into an fp32 gradient of experts*expert_params values."""
+                  gradient=None, accumulate=False, handoff=None):
+    """Scatter upstream [N, width] into an fp32 gradient of experts*expert_params values.  With
+    handoff (filled by grid_forward(handoff=...) on the same coords and offsets, no tuning change
+    in between) the backward reads it instead of forming it (odie_grid_backward_handoff)."""
     _check_coords(coords)
     if upstream.dtype not in _DTYPES or upstream.ndim != 2 or upstream.shape[0] != coords.shape[0]:
         raise ValueError('upstream must be fp32 or fp16 [N, width]')
@@ -85,11 +86,23 @@ def grid_backward(coords, upstream, levels, features, *, offsets=None, experts=1
         accumulate = False
     elif gradient.dtype != torch.float32 or gradient.numel() < total or not gradient.is_contiguous():
         raise ValueError('gradient must be a contiguous fp32 tensor of experts*expert_params values')
-    _lib.check(_lib.library().odie_grid_backward(
+    if handoff is None:
+        _lib.check(_lib.library().odie_grid_backward(
+            coords.data_ptr(), coords.shape[0], _lib.ptr(offsets), experts, upstream.data_ptr(),
+            _DTYPES[upstream.dtype], upstream.shape[1], expert_params, levels, len(levels), features,
+            gradient.data_ptr(), 0 if accumulate else 1, _lib.stream_of(coords)))
+        return gradient
+    _check_handoff(handoff)
+    _lib.check(_lib.library().odie_grid_backward_handoff(
         coords.data_ptr(), coords.shape[0], _lib.ptr(offsets), experts, upstream.data_ptr(),
         _DTYPES[upstream.dtype], upstream.shape[1], expert_params, levels, len(levels), features,
-        gradient.data_ptr(), 0 if accumulate else 1, _lib.stream_of(coords)))
+        gradient.data_ptr(), 0 if accumulate else 1, handoff.data_ptr(), handoff.numel(), _lib.stream_of(coords)))
     return gradient
+
+
+def _check_handoff(handoff):
+    if handoff.dtype != torch.uint8 or not handoff.is_cuda or not handoff.is_contiguous():
+        raise ValueError('handoff must be a contiguous CUDA uint8 tensor')
 
 
 class _GridEncode(torch.autograd.Function):

@@ -9,7 +9,7 @@ import torch
 
 from . import _lib
 from .config import grid_levels
-from .encoding import grid_backward, grid_forward, grid_mask_bytes
+from .encoding import grid_backward, grid_forward, grid_handoff_bytes
 
 
 def tile_bounds(size, regions):
@@ -137,20 +137,22 @@ class ExpertGrid:
         self.width = len(self.levels) * self.features
         self.table = torch.zeros(experts * self.expert_params, dtype=dtype, device=device)
 
-    def forward(self, coords, offsets, out=None, masks=None):
-        """Features [N, width]; with masks (uint8, at least mask_bytes(N)) also the encode
-        backward's slice masks, for backward_adam_planes(masks=...)."""
+    def forward(self, coords, offsets, out=None, handoff=None):
+        """Features [N, width]; with handoff (uint8, at least handoff_bytes(N)) also the encode
+        backward's handoff, for backward(handoff=...) or backward_adam_planes(handoff=...)."""
         return grid_forward(coords, self.table, self.levels, self.features, offsets=offsets,
                             experts=self.experts, expert_params=self.expert_params, width=self.width, out=out,
-                            masks=masks)
+                            handoff=handoff)
 
-    def mask_bytes(self, n):
-        """Bytes of the slice masks forward(masks=...) writes for a batch of n coordinates."""
-        return grid_mask_bytes(n, self.levels, self.features, experts=self.experts, expert_params=self.expert_params)
+    def handoff_bytes(self, n):
+        """Bytes of the handoff forward(handoff=...) fills for a batch of n coordinates."""
+        return grid_handoff_bytes(n, self.levels, self.features, experts=self.experts,
+                                  expert_params=self.expert_params)
 
-    def backward(self, coords, offsets, upstream, gradient=None, accumulate=False):
+    def backward(self, coords, offsets, upstream, gradient=None, accumulate=False, handoff=None):
         return grid_backward(coords, upstream, self.levels, self.features, offsets=offsets, experts=self.experts,
-                             expert_params=self.expert_params, gradient=gradient, accumulate=accumulate)
+                             expert_params=self.expert_params, gradient=gradient, accumulate=accumulate,
+                             handoff=handoff)
 
     def backward_adam(self, coords, offsets, upstream, optimizer, loss_scale=1.0):
         """Encode backward fused with optimizer.step (a FusedAdam over this table's fp32 master,
@@ -202,21 +204,21 @@ class ExpertGrid:
             gradient.data_ptr(), 0 if accumulate else 1, _lib.stream_of(coords)))
         return gradient
 
-    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0, masks=None):
+    def backward_adam_planes(self, coords, offsets, planes, blockmax, optimizer, loss_scale=1.0, handoff=None):
         """backward_adam with the fp16 upstream given as Decoder.train_planes writes it (planes
         int32 [levels, N], blockmax fp32 [ceil(N/128), 2 levels]): the same update, bit for bit.
-        With masks (written by forward(masks=...) on the same coords and offsets, no tuning change
-        in between) the backward reads the slice masks instead of forming them."""
+        With handoff (filled by forward(handoff=...) on the same coords and offsets, no tuning change
+        in between) the backward reads it instead of forming it."""
         from .encoding import _offsets_arg
         self._check_planes(coords, planes, blockmax)
         n = coords.shape[0]
         if optimizer.master.numel() != self.experts * self.expert_params:
             raise ValueError('the optimizer must own this table\'s fp32 master')
         offsets = _offsets_arg(offsets, self.experts, n)
-        if masks is not None and (masks.dtype != torch.uint8 or not masks.is_cuda or not masks.is_contiguous()):
-            raise ValueError('masks must be a contiguous CUDA uint8 tensor')
+        if handoff is not None and (handoff.dtype != torch.uint8 or not handoff.is_cuda or not handoff.is_contiguous()):
+            raise ValueError('handoff must be a contiguous CUDA uint8 tensor')
         optimizer.step_count += 1
-        if masks is None:
+        if handoff is None:
             _lib.check(_lib.library().odie_grid_backward_adam_planes(
                 coords.data_ptr(), n, _lib.ptr(offsets), self.experts, planes.data_ptr(), blockmax.data_ptr(),
                 self.expert_params, self.levels, len(self.levels), self.features, optimizer.master.data_ptr(),
@@ -224,9 +226,9 @@ class ExpertGrid:
                 _lib.ptr(optimizer.steps), optimizer.variant_code, optimizer.step_count, optimizer.lr,
                 optimizer.betas[0], optimizer.betas[1], optimizer.eps, float(loss_scale), _lib.stream_of(coords)))
             return
-        _lib.check(_lib.library().odie_grid_backward_adam_planes_masks(
+        _lib.check(_lib.library().odie_grid_backward_adam_planes_handoff(
             coords.data_ptr(), n, _lib.ptr(offsets), self.experts, planes.data_ptr(), blockmax.data_ptr(),
             self.expert_params, self.levels, len(self.levels), self.features, optimizer.master.data_ptr(),
             _lib.ptr(optimizer.half_copy), optimizer.m.data_ptr(), optimizer.v.data_ptr(), _lib.ptr(optimizer.steps),
             optimizer.variant_code, optimizer.step_count, optimizer.lr, optimizer.betas[0], optimizer.betas[1],
-            optimizer.eps, float(loss_scale), masks.data_ptr(), masks.numel(), _lib.stream_of(coords)))
+            optimizer.eps, float(loss_scale), handoff.data_ptr(), handoff.numel(), _lib.stream_of(coords)))

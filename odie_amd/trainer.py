@@ -18,10 +18,9 @@ With fused=True (the default) the grid's Adam step runs inside the encode backwa
 Without the router, planes=True (the default) has the decoder write the grid's upstream in the
 encode backward's own level-major layout with its 128-row maxima (odie_mlp_train_planes,
 odie_grid_backward_adam_planes), so the backward does not transpose it; the result is the same,
-bit for bit.  With it, masks=True (the default) has the encode forward also write the slice masks
-that the backward's hashed slices walk by (odie_grid_forward_masks,
-odie_grid_backward_adam_planes_masks), so the backward does not form them in a pass of its own;
-again bit for bit.
+bit for bit.  With it, handoff=True (the default) has the encode forward also fill what the
+backward would otherwise form in passes of its own (its slice masks, or its band lists:
+odie_grid_forward_handoff, odie_grid_backward_adam_planes_handoff); again bit for bit.
 
 With slots (int32 [regions_y * regions_x], tile -> expert, -1: none; allocate_tiles forms it
 from a predicate and a parameter budget) only `experts` tables exist: ids of tiles without an
@@ -46,7 +45,7 @@ GRID_SCALE, HEAD_SCALE = 128.0, 16384.0   # loss scales (odie/native/runtime.cu:
 class ExpertTrainer:
     def __init__(self, image, encoding, regions_x, regions_y, batch, *, grid_lr=1e-2, decoder_lr=1e-3, seed=0,
                  device='cuda', fused=True, router=False, gate_lr=1e-3, coarse_levels=0, activation='sigmoid',
-                 planes=True, slots=None, experts=None, masks=True):
+                 planes=True, slots=None, experts=None, handoff=True):
         if isinstance(image, torch.Tensor):    # already on the device (gigapixel images)
             if image.dtype != torch.uint8 or image.ndim != 3 or image.shape[2] != 3:
                 raise ValueError('image must be uint8 [height, width, 3]')
@@ -102,12 +101,12 @@ class ExpertTrainer:
         self.gradient = None if fused else torch.empty(total, dtype=torch.float32, device=device)
         self.squares = torch.empty(batch, dtype=torch.float32, device=device)
         self.planes = planes and fused and not router
-        self.masks = masks and self.planes
+        self.handoff = handoff and self.planes
         if self.planes:
             self.plane_buffer = torch.empty(16 * batch, dtype=torch.int32, device=device)
             self.max_buffer = torch.empty(32 * ((batch + 127) // 128), dtype=torch.float32, device=device)
-        if self.masks:
-            self.mask_buffer = torch.empty(max(self.grid.mask_bytes(batch), 1), dtype=torch.uint8, device=device)
+        if self.handoff:
+            self.handoff_buffer = torch.empty(max(self.grid.handoff_bytes(batch), 1), dtype=torch.uint8, device=device)
         if self.grid.width != 32:
             raise ValueError('the decoder takes 32 input features (16 levels x 2)')
 
@@ -127,15 +126,15 @@ class ExpertTrainer:
         route(ids, self.width, self.height, *self.regions, out=view, workspace=self.workspace, pixels=True,
               uniforms=uniforms, slots=self.slots, experts=self.experts if self.slots is not None else None)
         mark('route')
-        # with the planes path the forward also writes the backward's slice masks (sized per call:
-        # the backward's plan follows the tuning)
-        masks = None
-        if self.masks and update:
-            need = self.grid.mask_bytes(n)
-            if need > self.mask_buffer.numel():
-                self.mask_buffer = torch.empty(need, dtype=torch.uint8, device=self.mask_buffer.device)
-            masks = self.mask_buffer[:need] if need > 0 else None
-        raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n], masks=masks)
+        # with the planes path the forward also fills the backward's handoff (sized per call: the
+        # backward's plan follows the tuning)
+        handoff = None
+        if self.handoff and update:
+            need = self.grid.handoff_bytes(n)
+            if need > self.handoff_buffer.numel():
+                self.handoff_buffer = torch.empty(need, dtype=torch.uint8, device=self.handoff_buffer.device)
+            handoff = self.handoff_buffer[:need] if need > 0 else None
+        raw = self.grid.forward(view.coords, view.offsets, out=self.raw[:n], handoff=handoff)
         mark('encode_forward')
         features = raw
         if self.gate is not None:
@@ -147,7 +146,7 @@ class ExpertTrainer:
                 blockmax=self.max_buffer[:32 * ((n + 127) // 128)].view(-1, 32))
             mark('decoder')
             self.grid.backward_adam_planes(view.coords, view.offsets, planes, blockmax, self.grid_optimizer,
-                                           loss_scale=GRID_SCALE, masks=masks)
+                                           loss_scale=GRID_SCALE, handoff=handoff)
             mark('encode_backward')
             mark('grid_adam')
             self.decoder_optimizer.step(self.decoder.grad, loss_scale=HEAD_SCALE)

@@ -55,23 +55,28 @@ def test_grid_forward_rejects_bad_arguments(native, change, message):
     assert message in native.odie_error().decode()
 
 
-def test_grid_mask_bytes_follows_the_owner_plan(native):
-    """odie_grid_mask_bytes plans on the host: whole planes of n rounded up to 256 bytes for a
-    grid whose hashed levels the owner cuts into masked blocks (64 experts of 2^16-entry levels),
-    none for tables that fit one slice; and a forward given fewer bytes refuses before launching."""
+def test_grid_handoff_bytes_follows_the_owner_plan(native):
+    """odie_grid_handoff_bytes plans on the host.  Slice masks (whole planes of n rounded up to 256
+    bytes) for 64 experts of 2^16-entry levels, whose hashed levels the owner cuts into masked
+    blocks; band lists (starts, then a 4-byte index and an 8-byte (x, y) per coordinate) for one
+    expert of 2^19-entry levels, whose passes the owner bands; nothing for tables that fit one
+    slice.  A forward given fewer bytes refuses before launching."""
     levels, entries = grid_levels(dict(n_levels=16, base_resolution=16, log2_hashmap_size=16, per_level_scale=1.38))
     n = (1 << 22) - 5
     stride = (n + 255) // 256 * 256
-    size = native.odie_grid_mask_bytes(n, 64, entries * 2, levels, 16, 2)
+    size = native.odie_grid_handoff_bytes(n, 64, entries * 2, levels, 16, 2)
     assert size > 0 and size % stride == 0 and size // stride <= 16
-    assert native.odie_grid_mask_bytes(0, 64, entries * 2, levels, 16, 2) == 0
+    assert native.odie_grid_handoff_bytes(0, 64, entries * 2, levels, 16, 2) == 0
+    big, big_entries = grid_levels(dict(n_levels=16, base_resolution=16, log2_hashmap_size=19, per_level_scale=1.38))
+    lists = native.odie_grid_handoff_bytes(n, 1, big_entries * 2, big, 16, 2)
+    assert 12 * n <= lists < 12 * n + 64 * 1024
     small, small_entries = _levels()
-    assert native.odie_grid_mask_bytes(4096, 1, small_entries * 2, small, 4, 2) == 0
-    assert native.odie_grid_mask_bytes(16, 1, small_entries * 2, small, 4, 3) == -1
+    assert native.odie_grid_handoff_bytes(4096, 1, small_entries * 2, small, 4, 2) == 0
+    assert native.odie_grid_handoff_bytes(16, 1, small_entries * 2, small, 4, 3) == -1
     assert 'features per level' in native.odie_error().decode()
-    code = native.odie_grid_forward_masks(8, n, 8, 64, 8, entries * 2, 1, levels, 16, 2, 16, 32, 8, size - 1, 0)
+    code = native.odie_grid_forward_handoff(8, n, 8, 64, 8, entries * 2, 1, levels, 16, 2, 16, 32, 8, size - 1, 0)
     assert code == -1
-    assert 'shorter than odie_grid_mask_bytes' in native.odie_error().decode()
+    assert 'shorter than odie_grid_handoff_bytes' in native.odie_error().decode()
 
 
 def test_levels_must_be_contiguous(native):

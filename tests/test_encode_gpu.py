@@ -81,6 +81,32 @@ def test_forward_corner_pairs_bit_exact(mode, log2):
     assert not mismatch.any(), 'mismatches at %s' % (np.argwhere(mismatch)[:5],)
 
 
+@pytest.mark.parametrize('experts', [1, 3])
+def test_handoff_band_lists_bit_identical(experts):
+    """The forward filling the handoff with the owner's band lists (2^19-entry levels, whose
+    passes the owner bands) and walking the coordinates in band order, and the backward reading
+    them: features and gradient bit-identical to the plain pair, one expert and three."""
+    from odie_amd.encoding import grid_handoff_bytes
+    enc = encoding(log2=19)
+    levels, entries = grid_levels(enc)
+    n = (1 << 17) + 333
+    params = entries * 2
+    xy = torch.from_numpy(synth.coordinates(5, n)).cuda()
+    table = torch.from_numpy(synth.table(5, experts * params).astype(np.float16)).cuda()
+    upstream = torch.from_numpy(synth.upstream(5, n, 32)).cuda().half()
+    offsets = torch.tensor([k * n // experts for k in range(experts + 1)], dtype=torch.int32).cuda()
+    size = grid_handoff_bytes(n, levels, 2, experts=experts, expert_params=params)
+    assert size >= 12 * n   # band lists: a 4-byte index and an 8-byte (x, y) per coordinate
+    handoff = torch.empty(size, dtype=torch.uint8, device='cuda')
+    kw = dict(offsets=offsets, experts=experts, expert_params=params)
+    plain = grid_forward(xy, table, levels, 2, **kw)
+    walked = grid_forward(xy, table, levels, 2, handoff=handoff, **kw)
+    assert np.array_equal(walked.cpu().numpy().view(np.uint16), plain.cpu().numpy().view(np.uint16))
+    formed = grid_backward(xy, upstream, levels, 2, **kw)
+    read = grid_backward(xy, upstream, levels, 2, handoff=handoff, **kw)
+    assert np.array_equal(read.cpu().numpy().view(np.uint32), formed.cpu().numpy().view(np.uint32))
+
+
 @pytest.fixture(params=[(1, 1), (1, 0), (0, 0)], ids=['owner-banded', 'owner', 'atomics'])
 def backward_mode(request):
     mode, banded = request.param

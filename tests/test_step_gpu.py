@@ -164,19 +164,19 @@ def test_planes_layout_step_is_bit_identical():
     assert np.array_equal(planes.decoder.params.cpu().numpy(), rows.decoder.params.cpu().numpy())
 
 
-def test_forward_masks_step_is_bit_identical():
-    """The encode forward writing the backward's slice masks (the default with the planes path)
-    trains exactly as the backward forming them itself.  2^15-entry hashed levels: each is cut
-    into masked blocks, so the masks are in play."""
+def test_forward_handoff_step_is_bit_identical():
+    """The encode forward filling the backward's handoff (the default with the planes path; here
+    its slice masks) trains exactly as the backward forming them itself.  2^15-entry hashed
+    levels: each is cut into masked blocks, so the masks are in play."""
     encoding = dict(n_levels=16, n_features_per_level=2, log2_hashmap_size=15, base_resolution=16,
                     per_level_scale=1.38)
     width, height = 256, 200
     image = synth.image(11, width, height)
     batch = 1 << 16
     given = ExpertTrainer(image, encoding, 2, 2, batch, seed=11)
-    formed = ExpertTrainer(image, encoding, 2, 2, batch, seed=11, masks=False)
-    assert given.masks and not formed.masks
-    assert given.grid.mask_bytes(batch) > 0
+    formed = ExpertTrainer(image, encoding, 2, 2, batch, seed=11, handoff=False)
+    assert given.handoff and not formed.handoff
+    assert given.grid.handoff_bytes(batch) > 0
     for step in range(3):
         ids = torch.from_numpy(synth.integers(step, 'mask_ids', batch - 13 * step, width * height)).cuda()
         a = given.step(ids).cpu().numpy()
