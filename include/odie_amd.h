@@ -164,7 +164,9 @@ int odie_grid_backward_adam_planes_handoff(const float* coords, int64_t n, const
  * 2 (default) when one expert's fp16 table is larger than 4 MB), "forward_lds_bytes", "packed_owner" (1: the packed-plane
  * backward computes each slice of the gradient in one workgroup, 0 (default): global atomics),
  * "packed_splits" (0 = automatic), "route_part" (the routes' smallest sub-chunk of ids, a power
- * of two within 64..65536, default 512; size route workspaces after setting it).  Results do
+ * of two within 64..65536, default 512; size route workspaces after setting it),
+ * "route_one_scan" (1, the default: the routes scan their counts in one launch when they have at
+ * most 1024 segments of 1024 counts; 0: the reduce and apply launches).  Results do
  * not depend on them beyond fp32 summation order and the owner's fixed-point scale. */
 int odie_set_tuning(const char* key, int value);
 

@@ -48,6 +48,8 @@ struct RouteArgs {
     uint32_t* colors;       // packed r | g << 8 | b << 16 of each slot's pixel, or null
     int32_t* counts;   // [experts * parts]
     int32_t* block_sums;  // [ceil(experts * parts / kScanSegment)]
+    uint32_t* scan_ticket; // with the one-launch scan: block_sums + its segments (block_sums hold sum + 1)
+    int scan_segments;     // with the one-launch scan: its blocks
     const int32_t* slots; // tile -> expert, or null (expert = tile); with slots, bucket `owned` holds
                           // the ids of tiles without an expert (slot outside [0, owned))
     int owned;            // experts owning tiles (with slots; experts = owned + 1 buckets)
@@ -106,7 +108,7 @@ __device__ inline void pixel_ids(const RouteArgs& a, int64_t first, int64_t stri
     }
 }
 
-__device__ inline void locate_id(const RouteArgs& a, const Bounds& b, uint32_t id, int& expert, uint32_t& x,
+__device__ inline void locate_id(const RouteArgs& a, uint32_t id, int& expert, uint32_t& x,
                                  uint32_t& y, int& rx, int& ry) {
     y = divide(id, a.by_width);
     x = id - y * a.width;
@@ -141,30 +143,37 @@ __device__ inline void load_bounds(const RouteArgs& a, Bounds& b) {
 template <bool GROUPED>
 __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
     extern __shared__ int32_t hist[];  // [experts][kWaves] counts of the block's sub-chunks, or [experts]
-    __shared__ Bounds bounds;
-    load_bounds(a, bounds);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     constexpr int kSlots = GROUPED ? 1 : kWaves;
     const int first = static_cast<int>(blockIdx.x) * (GROUPED ? a.per_column : kWaves);
     const int members = GROUPED ? a.per_column : kWaves;
-    for (int j = threadIdx.x; j < a.experts * kSlots; j += kRouteBlock) hist[j] = 0;
-    __syncthreads();
+    if (a.scan_ticket)   // the one-launch scan's published sums (0: not yet) and its ticket
+        for (int j = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); j <= a.scan_segments;
+             j += static_cast<int>(gridDim.x * blockDim.x))
+            a.block_sums[j] = 0;
     if constexpr (GROUPED) {
         // the group's ids as 16-byte pairs (ids 16-byte aligned: checked by the host), every
-        // pair of a round of kPairs per thread loaded before any is used
+        // pair of a round of kPairs per thread loaded before any is used; the first round is
+        // issued before the histogram is cleared, so its loads fly over the clear and the barrier
         constexpr int kPairs = 8;
         const int64_t begin = static_cast<int64_t>(first) * a.part;
         const int64_t group_end = begin + static_cast<int64_t>(members) * a.part;
         const int64_t end = group_end < a.n ? group_end : a.n;
         const int4* pairs = reinterpret_cast<const int4*>(a.ids + begin);
         const int64_t count = end - begin, npairs = count / 2;   // whole pairs; an odd last id alone
-        for (int64_t round = 0; round < npairs; round += kRouteBlock * kPairs) {
-            int4 two[kPairs];
+        int4 two[kPairs];
+        auto fetch = [&](int64_t round) {
 #pragma unroll
             for (int k = 0; k < kPairs; ++k) {
                 const int64_t q = round + k * kRouteBlock + threadIdx.x;
                 two[k] = pairs[q < npairs ? q : npairs - 1];
             }
+        };
+        if (npairs > 0) fetch(0);
+        for (int j = threadIdx.x; j < a.experts; j += kRouteBlock) hist[j] = 0;
+        __syncthreads();
+        for (int64_t round = 0; round < npairs; round += kRouteBlock * kPairs) {
+            if (round > 0) fetch(round);
 #pragma unroll
             for (int k = 0; k < kPairs; ++k) {
                 const int64_t q = round + k * kRouteBlock + threadIdx.x;
@@ -172,7 +181,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
                 for (int h = 0; h < 2; ++h) {
                     int expert, rx, ry;
                     uint32_t x, y;
-                    locate_id(a, bounds, static_cast<uint32_t>(h ? two[k].z : two[k].x), expert, x, y, rx, ry);
+                    locate_id(a, static_cast<uint32_t>(h ? two[k].z : two[k].x), expert, x, y, rx, ry);
                     if (q < npairs) atomicAdd(hist + expert, 1);
                 }
             }
@@ -180,9 +189,13 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
         if ((count & 1) && threadIdx.x == 0) {
             int expert, rx, ry;
             uint32_t x, y;
-            locate_id(a, bounds, static_cast<uint32_t>(a.ids[end - 1]), expert, x, y, rx, ry);
+            locate_id(a, static_cast<uint32_t>(a.ids[end - 1]), expert, x, y, rx, ry);
             atomicAdd(hist + expert, 1);
         }
+    }
+    if constexpr (!GROUPED) {
+        for (int j = threadIdx.x; j < a.experts * kSlots; j += kRouteBlock) hist[j] = 0;
+        __syncthreads();
     }
     for (int k = wave; !GROUPED && k < members && first + k < a.parts; k += kWaves) {
         const int64_t begin = static_cast<int64_t>(first + k) * a.part;
@@ -195,7 +208,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
             for (int j = 0; j < kAhead; ++j) {
                 int expert, rx, ry;
                 uint32_t x, y;
-                locate_id(a, bounds, id[j], expert, x, y, rx, ry);
+                locate_id(a, id[j], expert, x, y, rx, ry);
                 if (g + j * 64 + lane < end) atomicAdd(counter + expert * kSlots, 1);
             }
         }
@@ -303,6 +316,56 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
     }
 }
 
+// The two scan launches in one, when there are few segments: each block draws a ticket (its
+// segment), sums the segment, publishes the sum + 1 with a device-coherent store, then adds the
+// sums its predecessors published.  A block waits only for segments of lower tickets, whose
+// blocks started before it and publish before they wait, so every wait ends.
+constexpr int kScanSpinLimit = 1 << 22;
+
+__global__ __launch_bounds__(kScanBlock) void route_scan_kernel(RouteArgs a) {
+    __shared__ int32_t shared[kScanBlock];
+    __shared__ uint32_t drawn;
+    if (threadIdx.x == 0) drawn = atomicAdd(a.scan_ticket, 1u);
+    __syncthreads();
+    const uint32_t segment = drawn;
+    const int64_t total = static_cast<int64_t>(a.experts) * a.columns;
+    constexpr int kPer = kScanSegment / kScanBlock;
+    const int64_t begin = static_cast<int64_t>(segment) * kScanSegment + threadIdx.x * kPer;
+    int32_t values[kPer];
+    int32_t sum = 0;
+    for (int j = 0; j < kPer; ++j) {
+        values[j] = begin + j < total ? a.counts[begin + j] : 0;
+        sum += values[j];
+    }
+    int32_t block_total;
+    const int32_t inside = block_exclusive_scan(sum, shared, block_total);
+    uint32_t* sums = reinterpret_cast<uint32_t*>(a.block_sums);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(sums + segment, static_cast<uint32_t>(block_total) + 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    int32_t before = 0;
+    for (uint32_t q = threadIdx.x; q < segment; q += kScanBlock) {
+        uint32_t v = __hip_atomic_load(sums + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int spins = 0; v == 0u && spins < kScanSpinLimit; ++spins) {
+            __builtin_amdgcn_s_sleep(2);
+            v = __hip_atomic_load(sums + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        before += static_cast<int32_t>(v - 1u);
+    }
+    int32_t offset;
+    block_exclusive_scan(before, shared, offset);
+    int32_t running = offset + inside;
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t k = begin + j;
+        if (k < total) {
+            a.counts[k] = running;
+            if (k % a.columns == 0) a.offsets[k / a.columns] = running;
+        }
+        running += values[j];
+    }
+    if (segment == 0 && threadIdx.x == 0 && !a.slots) a.offsets[a.experts] = static_cast<int32_t>(a.n);
+}
+
 __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a) {
     extern __shared__ int32_t running[];  // [kWaves][experts]
     __shared__ Bounds bounds;
@@ -326,7 +389,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
             const bool valid = i < end;
             int expert = -1, rx = 0, ry = 0;
             uint32_t x = 0, y = 0;
-            if (valid) locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
+            if (valid) locate_id(a, ids[k], expert, x, y, rx, ry);
             // Lanes holding the same expert: the AND over the id's bits of ballot(bit) or its
             // complement (one ballot per bit, whatever the number of distinct experts).  Every
             // lane reads the running count of its expert, then the lowest lane of each expert
@@ -424,11 +487,19 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
     extern __shared__ int32_t lds[];
     __shared__ Bounds bounds;
     __shared__ int32_t wave_sums[W];
-    load_bounds(a, bounds);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int tid = static_cast<int>(threadIdx.x);
     const int first = static_cast<int>(xcd_major(blockIdx.x, gridDim.x)) * group;   // the group's first sub-chunk
     if (first >= a.parts) return;
+    // the tile bounds (used at the write-out) loaded beside the counts and ids, not ahead of them
+    // behind a barrier of their own
+    static_assert(64 * W > kMaxRegions, "one bound per thread");
+    const bool bounder = tid <= kMaxRegions;
+    int32_t bound_x = 0, bound_y = 0;
+    if (bounder) {
+        bound_x = a.x0[tid];
+        bound_y = a.y0[tid];
+    }
     const int members = a.parts - first < group ? a.parts - first : group;
     const int64_t group_begin = static_cast<int64_t>(first) * a.part;
     const int64_t group_end = group_begin + static_cast<int64_t>(members) * a.part;
@@ -460,6 +531,10 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
             if (j < count) held[j] = ids[k];
         }
     }
+    if (bounder) {
+        bounds.x0[tid] = bound_x;
+        bounds.y0[tid] = bound_y;
+    }
     __syncthreads();
     // slices of whole groups of 64 ids
     const int32_t slice = ((count + W - 1) / W + 63) / 64 * 64;
@@ -478,7 +553,7 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
         for (int k = 0; k < kAhead; ++k) {
             int rx, ry;
             uint32_t x, y;
-            locate_id(a, bounds, ids[k], tags[k], x, y, rx, ry);
+            locate_id(a, ids[k], tags[k], x, y, rx, ry);
         }
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
@@ -583,7 +658,7 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
             const int32_t j = j0 + k * 64 * W + tid;
             int expert, rx, ry;
             uint32_t x, y;
-            locate_id(a, bounds, ids[k], expert, x, y, rx, ry);
+            locate_id(a, ids[k], expert, x, y, rx, ry);
             if (j < count) {
                 const int64_t slot = static_cast<int64_t>(base[expert]) + j;
                 a.perm[slot] = static_cast<int32_t>(group_begin + at[k]);
@@ -637,6 +712,11 @@ int launch_staged(const RouteArgs& a, int group, hipStream_t s) {
     return 0;
 }
 
+int& route_one_scan() {
+    static int enabled = 1;
+    return enabled;
+}
+
 int& route_min_part() {
     static int part = 512;
     return part;
@@ -659,6 +739,7 @@ int route_plan(int64_t n, int experts, int& part, int& parts) {
 int set_route_tuning(const std::string& key, int value) {
     // the workspace size follows the part, so a caller sizes it after the setting
     if (key == "route_part" && value >= 64 && value <= (1 << 16) && (value & (value - 1)) == 0) route_min_part() = value;
+    else if (key == "route_one_scan" && (value == 0 || value == 1)) route_one_scan() = value;
     else return fail("odie_set_tuning: unknown key or value out of range: " + key);
     return 0;
 }
@@ -769,12 +850,20 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
     if (n == 0) return launch_fill_zero(reinterpret_cast<float*>(offsets), slots ? owned + 1 : experts + 1, s);
     const int sblocks = static_cast<int>((static_cast<int64_t>(experts) * a.columns + kScanSegment - 1) / kScanSegment);
     if (sblocks > kScanBlock * 64) return fail("odie_route: too many counts to scan");
+    // one scan launch when its segments' sums and ticket fit the workspace's block sums
+    if (route_one_scan() && sblocks <= kScanBlock * 4 && sblocks + 1 <= scan_blocks(n, experts)) {
+        a.scan_segments = sblocks;
+        a.scan_ticket = reinterpret_cast<uint32_t*>(a.block_sums + sblocks);
+    }
     if (staged) route_count_kernel<true><<<a.columns, kRouteBlock, static_cast<size_t>(experts) * 4, s>>>(a);
     else route_count_kernel<false><<<blocks, kRouteBlock, shmem, s>>>(a);
-    route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
-    if (sblocks <= kScanBlock * 4) {
+    if (a.scan_ticket) {
+        route_scan_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
+    } else if (sblocks <= kScanBlock * 4) {
+        route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
         route_scan_apply_kernel<false><<<sblocks, kScanBlock, 0, s>>>(a);
     } else {
+        route_scan_reduce_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
         route_scan_top_kernel<<<1, kScanBlock, 0, s>>>(a, sblocks);
         route_scan_apply_kernel<true><<<sblocks, kScanBlock, 0, s>>>(a);
     }

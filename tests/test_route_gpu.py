@@ -11,6 +11,16 @@ from odie_amd.experts import route
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=[1, 0], ids=['one_scan_launch', 'two_scan_launches'])
+def scan_form(request):
+    """Both scans of the counts: one launch (each segment adds the sums its predecessors publish;
+    the default when there are at most 1024 segments) and the reduce and apply launches."""
+    from odie_amd import _lib
+    _lib.set_tuning('route_one_scan', request.param)
+    yield request.param
+    _lib.set_tuning('route_one_scan', 1)
+
+
 @pytest.mark.parametrize('width,height,rx,ry,n', [
     (2048, 1365, 8, 8, 1 << 20),        # 64 experts over the 2048x1365 image
     (32768, 32768, 32, 32, 1 << 20),    # 1024 tile experts of the gigapixel image
@@ -18,8 +28,9 @@ pytestmark = pytest.mark.gpu
     (64, 64, 1, 1, 777),                # a single expert
     (7, 5, 2, 2, 1),
     (4096, 4096, 60, 60, 1 << 23),      # 3600 experts: too many for the staged scatter's LDS
+    (2048, 1365, 8, 8, 1 << 22),        # the training step's batch
 ])
-def test_route_matches_oracle(width, height, rx, ry, n):
+def test_route_matches_oracle(width, height, rx, ry, n, scan_form):
     ids = synth.integers(17, 'ids', n, width * height)
     result = route(torch.from_numpy(ids).cuda(), width, height, rx, ry, with_expert=True)
     expert, perm, local, offsets = oracle.route(ids, width, height, rx, ry)
@@ -71,7 +82,7 @@ def test_route_splits_ids_at_every_kind_of_row_bound(width, height, rx, ry):
 
 @pytest.mark.parametrize('width,height,rx,ry,n,offset', [(2048, 1365, 8, 8, 1 << 18, 0), (100, 37, 3, 5, 4099, 0),
                                                           (100, 37, 3, 5, 4099, 1)])
-def test_route_gathers_slot_colors(width, height, rx, ry, n, offset):
+def test_route_gathers_slot_colors(width, height, rx, ry, n, offset, scan_form):
     """Colors are read in 8-byte windows from a 4-byte aligned image, byte by byte at its last
     pixels and from an image that starts off a 4-byte boundary (offset 1)."""
     ids = synth.integers(23, 'ids', n, width * height)
@@ -96,7 +107,7 @@ def test_route_gathers_slot_colors(width, height, rx, ry, n, offset):
     assert np.array_equal(indexes.perm.cpu().numpy(), perm)
 
 
-def test_route_clustered_ids_and_empty_experts():
+def test_route_clustered_ids_and_empty_experts(scan_form):
     # all ids inside one tile: every other expert is empty
     width, height = 2048, 1365
     xs = synth.integers(19, 'x', 50000, 256)
@@ -119,7 +130,7 @@ def test_route_empty_batch():
     (32768, 32768, 32, 32, 1 << 20),    # the gigapixel image's 1024 tiles
     (100, 37, 3, 5, 64),                # ragged tiles, strata larger than pixels
 ])
-def test_route_stratified_fuses_the_draw(width, height, rx, ry, n):
+def test_route_stratified_fuses_the_draw(width, height, rx, ry, n, scan_form):
     """odie_route_stratified (the stratified draw computed inside the route) equals the route of
     odie_stratified_ids' ids bit for bit: experts, perm, local coordinates, offsets, colours;
     the oracle's stratified ids and route pin both."""
@@ -159,7 +170,7 @@ def _slot_map(seed, tiles, experts):
     (100, 37, 3, 5, 1, 4099),               # one expert, ragged tiles
     (4096, 4096, 60, 60, 3000, 1 << 21),    # too many buckets for the staged scatter's LDS
 ])
-def test_route_allocated_matches_oracle(width, height, rx, ry, experts, n):
+def test_route_allocated_matches_oracle(width, height, rx, ry, experts, n, scan_form):
     """odie_route_allocated: ids grouped by their tile's expert, the ids of tiles without one
     after all experts in input order; experts (-1 for those), perm, local coordinates, offsets
     [experts + 1] and colours bit-exact against the oracle's route with the same slot map, for
