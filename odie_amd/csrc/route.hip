@@ -321,9 +321,34 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
 // sums its predecessors published.  A block waits only for segments of lower tickets, whose
 // blocks started before it and publish before they wait, so every wait ends.
 constexpr int kScanSpinLimit = 1 << 22;
+constexpr int kScanWaves = kScanBlock / 64;
+
+// Exclusive scan of one value per thread over the block with wave shuffles and one barrier;
+// `totals` ([2][kScanWaves], alternated by `round` so that consecutive scans need no barrier
+// between them) receives the waves' sums, `total` the block's.
+__device__ inline int32_t block_scan_shuffled(int32_t value, int32_t* totals, int round, int32_t& total) {
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    int32_t inclusive = value;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t other = __shfl_up(inclusive, d);
+        if (lane >= d) inclusive += other;
+    }
+    int32_t* mine = totals + (round & 1) * kScanWaves;
+    if (lane == 63) mine[wave] = inclusive;
+    __syncthreads();
+    int32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kScanWaves; ++w) {
+        const int32_t t = mine[w];
+        if (w < wave) before += t;
+        total += t;
+    }
+    return before + inclusive - value;
+}
 
 __global__ __launch_bounds__(kScanBlock) void route_scan_kernel(RouteArgs a) {
-    __shared__ int32_t shared[kScanBlock];
+    __shared__ int32_t totals[2 * kScanWaves];
     __shared__ uint32_t drawn;
     if (threadIdx.x == 0) drawn = atomicAdd(a.scan_ticket, 1u);
     __syncthreads();
@@ -338,7 +363,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_kernel(RouteArgs a) {
         sum += values[j];
     }
     int32_t block_total;
-    const int32_t inside = block_exclusive_scan(sum, shared, block_total);
+    const int32_t inside = block_scan_shuffled(sum, totals, 0, block_total);
     uint32_t* sums = reinterpret_cast<uint32_t*>(a.block_sums);
     if (threadIdx.x == 0)
         __hip_atomic_store(sums + segment, static_cast<uint32_t>(block_total) + 1u, __ATOMIC_RELAXED,
@@ -353,7 +378,7 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_kernel(RouteArgs a) {
         before += static_cast<int32_t>(v - 1u);
     }
     int32_t offset;
-    block_exclusive_scan(before, shared, offset);
+    block_scan_shuffled(before, totals, 1, offset);
     int32_t running = offset + inside;
     for (int j = 0; j < kPer; ++j) {
         const int64_t k = begin + j;
