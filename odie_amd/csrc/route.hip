@@ -320,6 +320,8 @@ __global__ __launch_bounds__(kScanBlock) void route_scan_apply_kernel(RouteArgs 
 // segment), sums the segment, publishes the sum + 1 with a device-coherent store, then adds the
 // sums its predecessors published.  A block waits only for segments of lower tickets, whose
 // blocks started before it and publish before they wait, so every wait ends.
+// (The wait is bounded so that the kernel always ends; the scatters store only slots inside
+// [0, n), so even counts scanned after an expired wait cannot send a store outside the outputs.)
 constexpr int kScanSpinLimit = 1 << 22;
 constexpr int kScanWaves = kScanBlock / 64;
 
@@ -433,8 +435,9 @@ __global__ __launch_bounds__(kRouteBlock) void route_scatter_kernel(RouteArgs a)
             __builtin_amdgcn_wave_barrier();
             if (valid && rank == 0) mine[expert] = base + __popcll(same);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (valid) {
-                const int64_t slot = static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.columns + part]) + base + rank;
+            const int64_t slot =
+                valid ? static_cast<int64_t>(a.counts[static_cast<int64_t>(expert) * a.columns + part]) + base + rank : 0;
+            if (valid && slot >= 0 && slot < a.n) {
                 a.perm[slot] = static_cast<int32_t>(i);
                 const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
                 const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
@@ -684,8 +687,8 @@ __global__ __launch_bounds__(64 * W) void route_scatter_staged_kernel(RouteArgs 
             int expert, rx, ry;
             uint32_t x, y;
             locate_id(a, ids[k], expert, x, y, rx, ry);
-            if (j < count) {
-                const int64_t slot = static_cast<int64_t>(base[expert]) + j;
+            const int64_t slot = static_cast<int64_t>(base[expert]) + j;
+            if (j < count && slot >= 0 && slot < a.n) {
                 a.perm[slot] = static_cast<int32_t>(group_begin + at[k]);
                 const float u = static_cast<float>(x - static_cast<uint32_t>(bounds.x0[rx])) * a.rx[rx];
                 const float v = static_cast<float>(y - static_cast<uint32_t>(bounds.y0[ry])) * a.ry[ry];
