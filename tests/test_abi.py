@@ -98,6 +98,18 @@ def test_tuning_rejects_unknown_keys(native):
     assert native.odie_set_tuning(b'lds_bytes', 10 ** 9) == -1
 
 
+def test_route_tuning_keys_take_their_ranges(native):
+    """The routes' keys (no GPU work: a setting only changes how later calls launch)."""
+    for value in (0, 1):
+        assert native.odie_set_tuning(b'route_one_scan', value) == 0
+    assert native.odie_set_tuning(b'route_one_scan', 2) == -1
+    assert native.odie_set_tuning(b'route_part', 512) == 0
+    assert native.odie_set_tuning(b'route_part', 500) == -1      # not a power of two
+    assert native.odie_set_tuning(b'route_part', 1 << 17) == -1  # past 65536
+    assert 'route_part' in native.odie_error().decode()
+    assert native.odie_set_tuning(b'route_one_scan', 1) == 0
+
+
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, 'LIBRARY', tmp_path / 'libodie_amd.so')
     monkeypatch.setattr(_lib, '_handle', None)
