@@ -32,6 +32,7 @@ namespace {
 
 constexpr int kRouteBlock = 256;
 constexpr int kWaves = kRouteBlock / 64;
+constexpr int kCountThreads = 512;   // the grouped count pass's workgroup (2048 id pairs per round either way)
 constexpr int kMaxRegions = kMaxTiles;
 constexpr int kMaxExperts = kMaxRegions * kMaxRegions;
 
@@ -140,8 +141,8 @@ __device__ inline void load_bounds(const RouteArgs& a, Bounds& b) {
 // written as one run), or of every group of per_column consecutive sub-chunks (GROUPED: a block
 // per group, its waves taking the group's sub-chunks in turn; the staged scatter needs no finer
 // offsets, and the scans then run over per_column times fewer counts).
-template <bool GROUPED>
-__global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
+template <bool GROUPED, int T = kRouteBlock>
+__global__ __launch_bounds__(T) void route_count_kernel(RouteArgs a) {
     extern __shared__ int32_t hist[];  // [experts][kWaves] counts of the block's sub-chunks, or [experts]
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     constexpr int kSlots = GROUPED ? 1 : kWaves;
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
         // the group's ids as 16-byte pairs (ids 16-byte aligned: checked by the host), every
         // pair of a round of kPairs per thread loaded before any is used; the first round is
         // issued before the histogram is cleared, so its loads fly over the clear and the barrier
-        constexpr int kPairs = 8;
+        constexpr int kPairs = 2048 / T;
         const int64_t begin = static_cast<int64_t>(first) * a.part;
         const int64_t group_end = begin + static_cast<int64_t>(members) * a.part;
         const int64_t end = group_end < a.n ? group_end : a.n;
@@ -165,18 +166,18 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
         auto fetch = [&](int64_t round) {
 #pragma unroll
             for (int k = 0; k < kPairs; ++k) {
-                const int64_t q = round + k * kRouteBlock + threadIdx.x;
+                const int64_t q = round + k * T + threadIdx.x;
                 two[k] = pairs[q < npairs ? q : npairs - 1];
             }
         };
         if (npairs > 0) fetch(0);
-        for (int j = threadIdx.x; j < a.experts; j += kRouteBlock) hist[j] = 0;
+        for (int j = threadIdx.x; j < a.experts; j += T) hist[j] = 0;
         __syncthreads();
-        for (int64_t round = 0; round < npairs; round += kRouteBlock * kPairs) {
+        for (int64_t round = 0; round < npairs; round += T * kPairs) {
             if (round > 0) fetch(round);
 #pragma unroll
             for (int k = 0; k < kPairs; ++k) {
-                const int64_t q = round + k * kRouteBlock + threadIdx.x;
+                const int64_t q = round + k * T + threadIdx.x;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     int expert, rx, ry;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kRouteBlock) void route_count_kernel(RouteArgs a) {
     }
     __syncthreads();
     if constexpr (GROUPED) {
-        for (int e = threadIdx.x; e < a.experts; e += kRouteBlock)
+        for (int e = threadIdx.x; e < a.experts; e += T)
             a.counts[static_cast<int64_t>(e) * a.columns + blockIdx.x] = hist[e];
     } else {
         for (int j = threadIdx.x; j < a.experts * kWaves; j += kRouteBlock) {
@@ -883,7 +884,7 @@ int route_launch(const int64_t* ids, int64_t n, int width, int height, int regio
         a.scan_segments = sblocks;
         a.scan_ticket = reinterpret_cast<uint32_t*>(a.block_sums + sblocks);
     }
-    if (staged) route_count_kernel<true><<<a.columns, kRouteBlock, static_cast<size_t>(experts) * 4, s>>>(a);
+    if (staged) route_count_kernel<true, kCountThreads><<<a.columns, kCountThreads, static_cast<size_t>(experts) * 4, s>>>(a);
     else route_count_kernel<false><<<blocks, kRouteBlock, shmem, s>>>(a);
     if (a.scan_ticket) {
         route_scan_kernel<<<sblocks, kScanBlock, 0, s>>>(a);
