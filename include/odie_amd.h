@@ -161,7 +161,7 @@ int odie_grid_backward_adam_planes_handoff(const float* coords, int64_t n, const
  * 2 (default) when the lists cut the estimated visits at least four times),
  * "split_target" (banded: coordinate-level visits per owner work item, 0 = automatic),
  * "owner_lds_bytes", "paired_loads" (the forward's 16-byte corner-pair loads: 0 off, 1 on,
- * 2 (default) when one expert's fp16 table is larger than 4 MB), "forward_lds_bytes", "packed_owner" (1: the packed-plane
+ * 2 (default) when one expert's fp16 table is larger than 1 MB), "forward_lds_bytes", "packed_owner" (1: the packed-plane
  * backward computes each slice of the gradient in one workgroup, 0 (default): global atomics),
  * "packed_splits" (0 = automatic), "route_part" (the routes' smallest sub-chunk of ids, a power
  * of two within 64..65536, default 512; size route workspaces after setting it),

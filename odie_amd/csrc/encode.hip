@@ -66,7 +66,7 @@ struct Tuning {
     int packed_splits = 0;          // packed owner: coordinate splits per slice (0: automatic)
     int packed_lds = 1;             // packed backward with atomics: coarse levels accumulated in LDS
     int packed_blocks = 256;        // packed backward with LDS: most blocks (each flushes its partials once)
-    int paired_loads = 2;           // forward: 16-byte corner-pair loads (0 off, 1 on, 2: tables past one L2)
+    int paired_loads = 2;           // forward: 16-byte corner-pair loads (0 off, 1 on, 2: expert tables past 1 MB)
     int forward_lds_bytes = 28672;  // forward: LDS budget for staged coarse levels (0: off)
     int owner_lds_bytes = 162816;   // 160 KiB minus the owner kernel's static 1 KiB (its Adam rate table)
 };
@@ -830,13 +830,13 @@ int grid_forward(const char* who, const float* coords, int64_t n, const int32_t*
     a.remap = tuning().xcd_remap;
     {
         const uint64_t entries = static_cast<uint64_t>(levels[n_levels - 1].offset) + levels[n_levels - 1].size;
-        // Corner pairs from one 16-byte group load pay where an expert's table is larger than one
-        // XCD's L2 (4 MB) and the gathers miss it: one request for corners (x, y) and (x+1, y)
-        // instead of two (measured, one expert of 2^19-entry levels, 11 MB: 0.611 -> 0.581 ms).
-        // With the table in L2 the gathers hit and the pair's selects cost more than the second
-        // request (64 experts of 2^16-entry levels, 2.2 MB each: 0.453 -> 0.458 ms).
+        // Corner pairs from one 16-byte group load: one request for corners (x, y) and (x+1, y)
+        // instead of two.  Measured: one expert of 2^19-entry levels (11 MB) 0.611 -> 0.581 ms;
+        // 64 experts of 2^16-entry levels (2.2 MB each) 0.462 -> 0.453 ms; 1024 experts of
+        // 32 KB tables 3.49 -> 3.52 ms per stratified gigapixel step (small tables: mostly dense
+        // levels, which fetch their pairs with 8-byte loads either way).  So pairs from 1 MB up.
         const int mode = tuning().paired_loads;
-        const bool past_l2 = expert_params * 2 > (int64_t{4} << 20);
+        const bool past_l2 = expert_params * 2 > (int64_t{1} << 20);
         a.paired = (mode == 1 || (mode == 2 && past_l2)) && half && features == 2 &&
                    reinterpret_cast<uintptr_t>(params) % 16 == 0 && entries % 4 == 0 && (expert_params * 2) % 16 == 0;
         // Stage the longest prefix of levels that fits the budget (entries of 4 bytes).
